@@ -1,0 +1,130 @@
+"""GGUF Q4_K / Q8_0 oracle -- TEST INFRASTRUCTURE ONLY.
+
+Block formats and decode follow the reference's GGUF decoder
+(snowllm/checkpoint/gguf/dequant.py:20-32 `_scales_min_k4`, :31-32 `_q8_0`, :82-92 `_q4_k`;
+block sizes snowllm/checkpoint/gguf/__init__.py:45,49):
+
+  Q4_K, 144 bytes per 256 weights: d fp16 @0, dmin fp16 @2, 12 bytes of 6-bit scales/mins @4,
+  128 bytes of nibbles @16. Group g (0..3) of 32 bytes holds sub-block 2g in the low nibbles
+  and sub-block 2g+1 in the high nibbles. w = d * sc_j * q - dmin * m_j.
+  Q8_0, 34 bytes per 32 weights: d fp16 @0, 32 int8 @2. w = d * q.
+
+The GEMV reference is x.float() @ W.float().T in float64 (tests/test_mixed_gguf.py:57-67
+uses the same form in fp32).
+"""
+import numpy as np
+import torch
+
+QK_K = 256
+Q4_K_BYTES = 144
+Q8_0_BYTES = 34
+
+
+def scales_min_k4(s: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """6-bit (scale, min) unpack of the 12 scale bytes (dequant.py:20-28)."""
+    s = s.astype(np.int32)
+    sc = np.empty((s.shape[0], 8), dtype=np.int32)
+    mn = np.empty_like(sc)
+    sc[:, :4] = s[:, 0:4] & 63
+    mn[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)
+    mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    return sc, mn
+
+
+def pack_scales_min_k4(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
+    """Inverse of scales_min_k4 for values 0..63: [nb, 8] x2 -> [nb, 12] bytes."""
+    sc = sc.astype(np.int32)
+    mn = mn.astype(np.int32)
+    s = np.zeros((sc.shape[0], 12), dtype=np.int32)
+    s[:, 0:4] = (sc[:, :4] & 63) | ((sc[:, 4:] >> 4) << 6)
+    s[:, 4:8] = (mn[:, :4] & 63) | ((mn[:, 4:] >> 4) << 6)
+    s[:, 8:12] = (sc[:, 4:] & 0xF) | ((mn[:, 4:] & 0xF) << 4)
+    return s.astype(np.uint8)
+
+
+def _f16(b: np.ndarray, off: int) -> np.ndarray:
+    return np.ascontiguousarray(b[:, off:off + 2]).view(np.float16).astype(np.float32)[:, 0]
+
+
+def dequant_q4_k(raw: np.ndarray, n: int, k: int) -> np.ndarray:
+    """[n*k/256*144] bytes -> float32 [n, k] (dequant.py:82-92, in fp32 like the reference)."""
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, Q4_K_BYTES)
+    nb = b.shape[0]
+    d, dmin = _f16(b, 0), _f16(b, 2)
+    sc, mn = scales_min_k4(b[:, 4:16])
+    q = b[:, 16:144].astype(np.int32).reshape(nb, 4, 32)
+    d1 = (d[:, None] * sc[:, 0::2].astype(np.float32)).astype(np.float32)
+    m1 = (dmin[:, None] * mn[:, 0::2].astype(np.float32)).astype(np.float32)
+    d2 = (d[:, None] * sc[:, 1::2].astype(np.float32)).astype(np.float32)
+    m2 = (dmin[:, None] * mn[:, 1::2].astype(np.float32)).astype(np.float32)
+    out = np.empty((nb, 4, 64), dtype=np.float32)
+    out[:, :, :32] = d1[..., None] * (q & 0xF).astype(np.float32) - m1[..., None]
+    out[:, :, 32:] = d2[..., None] * (q >> 4).astype(np.float32) - m2[..., None]
+    return out.reshape(n, k)
+
+
+def dequant_q8_0(raw: np.ndarray, n: int, k: int) -> np.ndarray:
+    """[n*k/32*34] bytes -> float32 [n, k] (dequant.py:31-32)."""
+    b = np.asarray(raw, dtype=np.uint8).reshape(-1, Q8_0_BYTES)
+    d = _f16(b, 0)
+    q = np.ascontiguousarray(b[:, 2:34]).view(np.int8).astype(np.float32)
+    return (d[:, None] * q).reshape(n, k)
+
+
+def make_q4_k(n: int, k: int, seed: int, d_std: float = 1e-3) -> np.ndarray:
+    """Synthetic Q4_K weight: 6-bit scales/mins uniform 0..63,
+    d, dmin = fp16(|N(0, d_std^2)|), nibbles uniform 0..15. Returns uint8 [n*k/256*144]."""
+    assert k % QK_K == 0
+    g = torch.Generator().manual_seed(seed)
+    nb = n * k // QK_K
+    sc = torch.randint(0, 64, (nb, 8), generator=g).numpy()
+    mn = torch.randint(0, 64, (nb, 8), generator=g).numpy()
+    dd = (torch.randn(nb, 2, generator=g) * d_std).abs().half().numpy()
+    qs = torch.randint(0, 256, (nb, 128), generator=g, dtype=torch.int32).numpy().astype(np.uint8)
+    blk = np.empty((nb, Q4_K_BYTES), dtype=np.uint8)
+    blk[:, 0:4] = dd.view(np.uint8).reshape(nb, 4)
+    blk[:, 4:16] = pack_scales_min_k4(sc, mn)
+    blk[:, 16:] = qs
+    return blk.reshape(-1)
+
+
+def make_q8_0(n: int, k: int, seed: int, d_std: float = 1e-2) -> np.ndarray:
+    """Synthetic Q8_0 weight: d = fp16(|N(0, d_std^2)|), int8 uniform
+    -127..127. Returns uint8 [n*k/32*34]."""
+    assert k % 32 == 0
+    g = torch.Generator().manual_seed(seed)
+    nb = n * k // 32
+    d = (torch.randn(nb, generator=g) * d_std).abs().half().numpy()
+    q = torch.randint(-127, 128, (nb, 32), generator=g, dtype=torch.int32).numpy().astype(np.int8)
+    blk = np.empty((nb, Q8_0_BYTES), dtype=np.uint8)
+    blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    blk[:, 2:] = q.view(np.uint8)
+    return blk.reshape(-1)
+
+
+def make_activations(m: int, k: int, seed: int) -> torch.Tensor:
+    """bf16 ~N(0,1) activations [m, k]."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(m, k, generator=g).bfloat16()
+
+
+def gemv_reference(x_bf16: torch.Tensor, w: np.ndarray) -> np.ndarray:
+    """x.float() @ W.T in float64: [m, n]."""
+    x = x_bf16.float().double().numpy()
+    return x @ w.astype(np.float64).T
+
+
+def dequant(raw: np.ndarray, fmt: int, n: int, k: int) -> np.ndarray:
+    if fmt == 4:
+        return dequant_q4_k(raw, n, k)
+    if fmt == 8:
+        return dequant_q8_0(raw, n, k)
+    raise ValueError(fmt)
+
+
+def rel_l2(got: np.ndarray, want: np.ndarray) -> float:
+    """Relative L2 error, the reference harness's `rel` (tests/_harness.py:71-74)."""
+    g = np.asarray(got, dtype=np.float64)
+    w = np.asarray(want, dtype=np.float64)
+    return float(np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-9))

@@ -1,0 +1,126 @@
+"""ctypes binding of libsnowverify.so, the gfx950 verify-step kernel library.
+
+Mirrors the loading pattern of the reference's binding (snowllm/_capi.py:144-194, 821-855):
+torch's HIP runtime is loaded first so the kernel library binds to the same libamdhip64,
+an ABI version is checked, every entry point gets an explicit signature, a nonzero status
+becomes SnowLLMError, and the torch stream is always the last argument.
+
+The library exports only the hot-path subset of the reference's C ABI under the same
+symbol names and argument orders; it never poses as libsnowllm.so.
+"""
+import ctypes
+import os
+import pathlib
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_void_p
+
+from .errors import SnowLLMError
+
+__all__ = ["lib", "check", "synchronize", "assert_single_hip_runtime", "LIB_PATH", "ABI_VERSION"]
+
+LIB_PATH = pathlib.Path(os.environ.get("SNOWVERIFY_LIB",
+                                       pathlib.Path(__file__).resolve().parent / "libsnowverify.so"))
+ABI_VERSION = 1
+
+
+def _preload_hip_runtime() -> None:
+    # Importing torch maps its bundled libamdhip64.so.7; the kernel library links the same
+    # soname, so the dynamic linker reuses that runtime instead of /opt/rocm's copy.
+    import torch  # noqa: F401
+    lib_dir = pathlib.Path(torch.__file__).resolve().parent / "lib"
+    hip = lib_dir / "libamdhip64.so"
+    if hip.exists():
+        ctypes.CDLL(str(hip), mode=ctypes.RTLD_GLOBAL)
+
+
+def _load():
+    if not LIB_PATH.exists():
+        raise SnowLLMError(
+            f"the kernel library {LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; "
+            f"g.build()'` (or `python snowllm_amd/build.py`) first")
+    _preload_hip_runtime()
+    try:
+        return ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+    except OSError as exc:
+        raise SnowLLMError(f"cannot load kernel library {LIB_PATH}: {exc}") from exc
+
+
+lib = _load()
+
+lib.snowllm_abi_version.restype = c_int
+_got = lib.snowllm_abi_version()
+if _got != ABI_VERSION:
+    raise SnowLLMError(f"ABI mismatch: snowllm_amd expects {ABI_VERSION}, {LIB_PATH} provides {_got}. "
+                       f"Rebuild the library.")
+
+
+class Stream:
+    pass
+
+
+P, S = c_void_p, Stream
+_SIGS = [
+    ("snowllm_abi_version", c_int, []),
+    ("snowllm_error_string", c_char_p, [c_int]),
+    ("snowllm_synchronize", c_int, [S]),
+    # acceptance
+    ("snowllm_sampling_max_k", c_int64, []),
+    ("snowllm_sampling_argmax", c_int, [P, P, c_int64, c_int64, S]),
+    ("snowllm_spec_accept", c_int, [P] * 3 + [c_int64] * 4 + [S]),
+    ("snowllm_sampling_workspace_bytes", c_int64, [c_int64] * 3),
+    ("snowllm_sampling_softmax", c_int, [P, P, c_int64, c_int64, P, S]),
+    ("snowllm_sampling_topk_topp", c_int, [P, P, P, c_int64, c_int64, c_int64, P, P, S]),
+    ("snowllm_sampling_sample", c_int, [P] * 7 + [c_int64] * 4 + [S]),
+    ("snowllm_draft_reject", c_int, [P] * 10 + [c_int64] * 4 + [S]),
+    # GGUF k-quant GEMV
+    ("snowllm_kquant_gguf_bytes", c_int64, [c_int, c_int64, c_int64]),
+    ("snowllm_kquant_quant_bytes", c_int64, [c_int, c_int64, c_int64]),
+    ("snowllm_kquant_meta_bytes", c_int64, [c_int, c_int64, c_int64]),
+    ("snowllm_kquant_supported", c_int, [c_int]),
+    ("snowllm_gemm_kquant_shuffle_b", c_int, [c_int, P, P, P, c_int64, c_int64, S]),
+    ("snowllm_gemm_kquant_a_ws_bytes", c_int64, [c_int64, c_int64]),
+    ("snowllm_gemm_kquant_a", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
+    ("snowllm_gemm_kquant_prepare_a", c_int, [P, c_int64, c_int64, P, S]),
+    ("snowllm_gemm_kquant_a_prepared", c_int, [c_int, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
+]
+
+_missing = []
+for _name, _res, _args in _SIGS:
+    try:
+        _fn = getattr(lib, _name)
+    except AttributeError:
+        _missing.append(_name)
+        continue
+    _fn.restype = _res
+    _fn.argtypes = [c_void_p if _a is S else _a for _a in _args]
+if _missing:
+    raise SnowLLMError(f"{LIB_PATH} is missing {len(_missing)} entry points this binding needs:\n  "
+                       + "\n  ".join(_missing))
+
+SYMBOLS = tuple(n for n, _, _ in _SIGS)
+LAUNCHES = frozenset(n for n, _, a in _SIGS if a and S in a)
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib.snowllm_error_string(status).decode()
+        raise SnowLLMError(f"{what}: hip status {status}: {msg}")
+
+
+def synchronize(stream: int = 0) -> None:
+    check(lib.snowllm_synchronize(stream), "synchronize")
+
+
+def hip_runtimes() -> set[str]:
+    try:
+        lines = pathlib.Path("/proc/self/maps").read_text().splitlines()
+    except OSError:
+        return set()
+    return {os.path.realpath(line.rsplit(" ", 1)[-1].strip())
+            for line in lines if "libamdhip64.so" in line}
+
+
+def assert_single_hip_runtime() -> None:
+    paths = hip_runtimes()
+    if len(paths) > 1:
+        raise SnowLLMError("two HIP runtimes are loaded in this process -- torch's device pointers "
+                           "are not valid in the kernels:\n  " + "\n  ".join(sorted(paths)))

@@ -1,0 +1,230 @@
+// Shared device helpers for the gfx950 verify-step kernels.
+//
+// Everything here is wave64 / CDNA4 specific: reductions use 64-lane butterflies, bf16 and
+// fp16 are handled as raw 16-bit patterns, and the canonical arithmetic used by the
+// acceptance kernels (exp, fixed-point sums) is written with explicit IEEE operations so
+// that a plain C restatement on the host reproduces it bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SV_API extern "C" __attribute__((visibility("default")))
+
+// Status codes are HIP statuses so that snowllm_error_string can defer to the runtime.
+#define SV_OK 0
+#define SV_EINVAL ((int)hipErrorInvalidValue)
+#define SV_ENOTSUP ((int)hipErrorNotSupported)
+
+#define SV_CHECK_LAUNCH()                                   \
+  do {                                                      \
+    hipError_t _e = hipGetLastError();                      \
+    if (_e != hipSuccess) return (int)_e;                   \
+  } while (0)
+
+static constexpr int WAVE = 64;
+
+// ---------------------------------------------------------------------------------------
+// 16-bit float patterns
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return (float)v;
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  _Float16 v = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+// ---------------------------------------------------------------------------------------
+// Wave64 reductions (butterfly; every lane ends with the result)
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    T o = __shfl_xor(v, s, WAVE);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) v += __shfl_xor(v, s, WAVE);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int s) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = __shfl_xor(lo, s, WAVE);
+  hi = __shfl_xor(hi, s, WAVE);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) v += shfl_xor_u64(v, s);
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int s = 32; s > 0; s >>= 1) {
+    uint64_t o = shfl_xor_u64(v, s);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Block-wide reductions for blockDim.x == NT (a multiple of 64). `red` must hold NT/64 slots.
+template <int NT>
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* red) {
+  v = wave_sum_u64(v);
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int i = 0; i < NT / WAVE; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+template <int NT>
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
+  v = wave_max_u64(v);
+  const int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int i = 0; i < NT / WAVE; ++i) t = red[i] > t ? red[i] : t;
+  __syncthreads();
+  return t;
+}
+
+// ---------------------------------------------------------------------------------------
+// Ordered float keys. NaN is treated as -inf (the argmax and top-k rules of the reference
+// sampler). ord(a) > ord(b) <=> a > b for non-NaN floats, and -0.0 == +0.0.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ord_key(float f) {
+  if (f != f) f = -__builtin_huge_valf();
+  if (f == 0.0f) f = 0.0f;  // fold -0 into +0 so that ties compare equal
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float ord_key_to_float(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
+// (value, index) packed so that the maximum key is the largest value with the lowest index.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+  return ((uint64_t)ord_key(v) << 32) | (uint64_t)(0xffffffffu - idx);
+}
+__device__ __forceinline__ uint32_t argmax_key_index(uint64_t k) {
+  return 0xffffffffu - (uint32_t)(k & 0xffffffffu);
+}
+
+// ---------------------------------------------------------------------------------------
+// Canonical arithmetic shared (by restatement) with the host oracle.
+//
+// canon_exp: e^x for x <= 0 by Cody & Waite argument reduction (x = n ln2 + r, ln2 split
+// into a high part with trailing zero bits and a low correction) followed by the degree-7
+// Taylor polynomial of e^r evaluated by Horner's rule with fused multiply-adds, then
+// scaled by 2^n. Inputs below -86 return 0 so that no subnormal result is ever produced.
+// Every step is a single IEEE-754 binary32 operation, so the result is reproducible on any
+// IEEE host with a correctly rounded fmaf.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float canon_exp(float x) {
+#pragma clang fp contract(off)
+  if (!(x >= -86.0f)) return 0.0f;  // also maps NaN and -inf to 0
+  const float kLog2e = 1.44269502162933349609375f;   // log2(e) rounded to binary32
+  const float kLn2Hi = 0.693145751953125f;           // ln 2 high part (12 trailing zero bits)
+  const float kLn2Lo = 1.428606765330187045037746429443359375e-06f;  // ln 2 - kLn2Hi
+  float t = __fmul_rn(x, kLog2e);
+  float n = __builtin_rintf(t);
+  float r = __builtin_fmaf(-n, kLn2Hi, x);
+  r = __builtin_fmaf(-n, kLn2Lo, r);
+  float p = 1.98412698412698412698e-4f;              // 1/7!
+  p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f);  // 1/6!
+  p = __builtin_fmaf(p, r, 8.33333333333333333333e-3f);  // 1/5!
+  p = __builtin_fmaf(p, r, 4.16666666666666666667e-2f);  // 1/4!
+  p = __builtin_fmaf(p, r, 1.66666666666666666667e-1f);  // 1/3!
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
+}
+
+// Probabilities below the smallest normal binary32 are flushed to zero explicitly, so the
+// result never depends on a device's denormal mode.
+__device__ __forceinline__ float canon_div(float a, float b) {
+#pragma clang fp contract(off)
+  float q = __fdiv_rn(a, b);
+  return (__builtin_fabsf(q) < 1.17549435082228750797e-38f) ? 0.0f : q;
+}
+
+// Fixed-point weight: floor(w * 2^44) for w in [0, 1]. Sums of up to 2^19 such terms fit in
+// 63 bits exactly, so any reduction order gives the same integer.
+#define SV_FIX_BITS 44
+__device__ __forceinline__ uint64_t canon_fix(float w) {
+#pragma clang fp contract(off)
+  if (!(w > 0.0f)) return 0;
+  float s = __builtin_ldexpf(w, SV_FIX_BITS);
+  return (uint64_t)__builtin_floorf(s);
+}
+
+// Round-to-nearest-even conversion of an unsigned 64-bit integer to binary32, written out
+// with integer operations so that host and device agree without relying on library code.
+__device__ __forceinline__ float canon_u64_to_f32(uint64_t v) {
+  if (v == 0) return 0.0f;
+  int lz = __builtin_clzll(v);
+  int msb = 63 - lz;
+  if (msb <= 23) return (float)(uint32_t)v;  // exact
+  int shift = msb - 23;
+  uint64_t mant = v >> shift;
+  uint64_t rem = v & ((1ull << shift) - 1);
+  uint64_t half = 1ull << (shift - 1);
+  if (rem > half || (rem == half && (mant & 1))) {
+    mant += 1;
+    if (mant == (1ull << 24)) { mant >>= 1; shift += 1; }
+  }
+  return __builtin_ldexpf((float)(uint32_t)mant, shift);
+}
+
+// Sum of fixed-point weights back to a binary32 value: round(v) * 2^-44.
+__device__ __forceinline__ float canon_unfix(uint64_t v) {
+#pragma clang fp contract(off)
+  return __builtin_ldexpf(canon_u64_to_f32(v), -SV_FIX_BITS);
+}
+
+// floor(u * R) for u in [0, 1) a binary32 value and R a 63-bit integer, exactly.
+__device__ __forceinline__ uint64_t canon_scale_floor(float u, uint64_t R) {
+  if (!(u > 0.0f)) return 0;
+  uint32_t bits = __float_as_uint(u);
+  int e = (int)((bits >> 23) & 0xff);
+  uint64_t m = (e == 0) ? (bits & 0x7fffffu) : ((bits & 0x7fffffu) | 0x800000u);
+  int exp2 = (e == 0 ? 1 : e) - 127 - 23;  // u = m * 2^exp2, exp2 <= -24 for u < 1
+  unsigned __int128 prod = (unsigned __int128)m * (unsigned __int128)R;
+  int sh = -exp2;
+  if (sh >= 128) return 0;
+  return (uint64_t)(prod >> sh);
+}

@@ -1,0 +1,864 @@
+// Acceptance-side kernels of the verify step: argmax, greedy prefix acceptance, temperature
+// softmax, top-k/top-p candidate lists, rejection sampling with residual resample, and
+// ordinary top-k/top-p sampling.
+//
+// Vocabulary-wide work is split into 4096-element chunks so that a handful of rows still
+// spreads over hundreds of workgroups. Every sum that feeds a sampling decision is taken in
+// 44-bit fixed point (canon_fix), which makes the result independent of how the chunks and
+// lanes are combined; maxima are exact in any order. The host oracle restates exactly this
+// arithmetic, so accept lengths, emitted ids and probabilities agree bit for bit.
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int CHUNK = 4096;
+constexpr int NT = 256;                // threads per chunk workgroup
+constexpr int RUN = CHUNK / NT;        // contiguous elements per thread in scan kernels
+constexpr int ROWS_MAX = 2048;         // rows per argmax / reject launch
+constexpr int CHUNKS_MAX = 128;        // vocab < 2^19 (fixed-point headroom)
+constexpr int64_t VOCAB_MAX = (int64_t)CHUNK * CHUNKS_MAX;
+
+// Library-owned scratch for the entry points whose reference signature carries no
+// workspace (argmax, draft_reject). Calls on one device must be stream-ordered.
+__device__ uint64_t g_chunk_keys[ROWS_MAX * CHUNKS_MAX];
+__device__ uint64_t g_chunk_sums[ROWS_MAX * CHUNKS_MAX * 2];
+__device__ int32_t g_first[ROWS_MAX];
+
+inline int chunks_of(int64_t n) { return (int)((n + CHUNK - 1) / CHUNK); }
+
+// ---------------------------------------------------------------------------------------
+// argmax
+// ---------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(NT) argmax_chunks(const float* __restrict__ logits,
+                                                    int64_t V, int C) {
+  __shared__ uint64_t red[NT / WAVE];
+  const int c = blockIdx.x, row = blockIdx.y;
+  const float* x = logits + (int64_t)row * V;
+  const int64_t base = (int64_t)c * CHUNK;
+  uint64_t best = 0;
+#pragma unroll 4
+  for (int k = 0; k < RUN; ++k) {
+    int64_t i = base + threadIdx.x + (int64_t)k * NT;
+    if (i < V) {
+      uint64_t key = argmax_key(x[i], (uint32_t)i);
+      best = key > best ? key : best;
+    }
+  }
+  best = block_max_u64<NT>(best, red);
+  if (threadIdx.x == 0) g_chunk_keys[row * CHUNKS_MAX + c] = best;
+}
+
+__global__ void __launch_bounds__(WAVE) argmax_final(int64_t* __restrict__ out, int C) {
+  const int row = blockIdx.x;
+  uint64_t best = 0;
+  for (int c = threadIdx.x; c < C; c += WAVE) {
+    uint64_t k = g_chunk_keys[row * CHUNKS_MAX + c];
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  if (threadIdx.x == 0) out[row] = (int64_t)argmax_key_index(best);
+}
+
+// ---------------------------------------------------------------------------------------
+// greedy acceptance: accepted = 1 + number of leading positions where the verified token
+// equals the draft token.
+// ---------------------------------------------------------------------------------------
+__global__ void spec_accept_kernel(const int64_t* __restrict__ tokens,
+                                   const int64_t* __restrict__ drafts, int64_t* __restrict__ acc,
+                                   int64_t b, int64_t t, int64_t ts, int64_t ds) {
+  int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= b) return;
+  int64_t a = 1;
+  for (int64_t j = 0; j + 1 < t; ++j) {
+    if (tokens[r * ts + j] != drafts[r * ds + j]) break;
+    ++a;
+  }
+  acc[r] = a;
+}
+
+// ---------------------------------------------------------------------------------------
+// temperature softmax into a dense [rows, vocab] buffer. Row statistics live in the tail of
+// the sampling workspace: per-chunk maxima (u32 keys) and per-chunk fixed-point sums.
+// ---------------------------------------------------------------------------------------
+struct SoftmaxTail {
+  uint32_t* max_keys;  // [rows, C]
+  uint64_t* sums;      // [rows, C]
+};
+
+__device__ __forceinline__ float row_temperature(const float* temperature, int row) {
+  float t = temperature ? temperature[row] : 1.0f;
+  return (t > 0.0f) ? t : 1.0f;
+}
+
+__global__ void __launch_bounds__(NT) softmax_max(const float* __restrict__ logits, int64_t V,
+                                                  const float* __restrict__ temperature,
+                                                  SoftmaxTail tail, int C) {
+  __shared__ uint64_t red[NT / WAVE];
+  const int c = blockIdx.x, row = blockIdx.y;
+  const float* x = logits + (int64_t)row * V;
+  const float T = row_temperature(temperature, row);
+  uint64_t best = 0;
+  for (int k = 0; k < RUN; ++k) {
+    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    if (i < V) {
+      uint32_t key = ord_key(__fdiv_rn(x[i], T));
+      best = key > best ? key : best;
+    }
+  }
+  best = block_max_u64<NT>(best, red);
+  if (threadIdx.x == 0) tail.max_keys[row * C + c] = (uint32_t)best;
+}
+
+__device__ __forceinline__ float row_max_from_keys(const uint32_t* keys, int C) {
+  uint32_t m = 0;
+  for (int c = 0; c < C; ++c) m = keys[c] > m ? keys[c] : m;
+  return ord_key_to_float(m);
+}
+
+__global__ void __launch_bounds__(NT) softmax_exp(const float* __restrict__ logits, int64_t V,
+                                                  const float* __restrict__ temperature,
+                                                  float* __restrict__ dense, SoftmaxTail tail,
+                                                  int C) {
+  __shared__ uint64_t red[NT / WAVE];
+  __shared__ float s_max;
+  const int c = blockIdx.x, row = blockIdx.y;
+  if (threadIdx.x == 0) s_max = row_max_from_keys(tail.max_keys + row * C, C);
+  __syncthreads();
+  const float M = s_max;
+  const float* x = logits + (int64_t)row * V;
+  float* e = dense + (int64_t)row * V;
+  const float T = row_temperature(temperature, row);
+  uint64_t sum = 0;
+  for (int k = 0; k < RUN; ++k) {
+    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    if (i < V) {
+      float v = canon_exp(__fsub_rn(__fdiv_rn(x[i], T), M));
+      e[i] = v;
+      sum += canon_fix(v);
+    }
+  }
+  sum = block_sum_u64<NT>(sum, red);
+  if (threadIdx.x == 0) tail.sums[row * C + c] = sum;
+}
+
+__global__ void __launch_bounds__(NT) softmax_norm(float* __restrict__ dense, int64_t V,
+                                                   SoftmaxTail tail, int C) {
+  __shared__ float s_z;
+  const int c = blockIdx.x, row = blockIdx.y;
+  if (threadIdx.x == 0) {
+    uint64_t z = 0;
+    for (int i = 0; i < C; ++i) z += tail.sums[row * C + i];
+    s_z = canon_unfix(z);
+  }
+  __syncthreads();
+  const float Z = s_z;
+  float* e = dense + (int64_t)row * V;
+  for (int k = 0; k < RUN; ++k) {
+    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    if (i < V) e[i] = (Z > 0.0f) ? canon_div(e[i], Z) : 0.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// top-k / top-p candidate lists.
+//
+// Rows that keep the whole vocabulary without nucleus truncation are written in vocabulary
+// order (ids 0..V-1) with the dense probabilities unchanged. Rows with k <= TOPK_MAX are
+// selected by a four-pass radix select on the ordered probability keys (ties resolved to the
+// lower vocabulary index), sorted by (probability desc, index asc), renormalised over the
+// k survivors, truncated by top-p on the exclusive fixed-point prefix, and renormalised
+// again. Unused slots of the width are (0, -1).
+// ---------------------------------------------------------------------------------------
+constexpr int TOPK_NT = 1024;
+constexpr int TOPK_MAX = 1024;
+
+struct TopkShared {
+  uint32_t hist[256];
+  uint64_t red[TOPK_NT / WAVE];
+  uint64_t sel_key[TOPK_MAX];  // (ord key << 32) | ~index : descending order == wanted order
+  uint64_t fix[TOPK_MAX];
+  int32_t n_sel;
+};
+
+// Radix select: returns the ordered key tau of the k-th largest element of x[0..n) and the
+// number of elements strictly above it.
+__device__ void radix_threshold(const float* x, int64_t n, int k, TopkShared& sh,
+                                uint32_t* tau_out, int* above_out) {
+  uint32_t prefix = 0, mask = 0;
+  int remaining = k;  // rank still to find among elements matching the prefix
+  int above = 0;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = threadIdx.x; i < 256; i += TOPK_NT) sh.hist[i] = 0;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < n; i += TOPK_NT) {
+      uint32_t key = ord_key(x[i]);
+      if ((key & mask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 0xff], 1u);
+    }
+    __syncthreads();
+    // walk the digits from the top until the remaining rank falls inside one bucket
+    __shared__ uint32_t s_digit;
+    __shared__ int s_before;
+    if (threadIdx.x == 0) {
+      int acc = 0;
+      int d = 255;
+      for (; d >= 0; --d) {
+        int h = (int)sh.hist[d];
+        if (acc + h >= remaining) break;
+        acc += h;
+      }
+      if (d < 0) d = 0;
+      s_digit = (uint32_t)d;
+      s_before = acc;
+    }
+    __syncthreads();
+    above += s_before;
+    remaining -= s_before;
+    prefix |= s_digit << shift;
+    mask |= 0xffu << shift;
+    __syncthreads();
+  }
+  *tau_out = prefix;
+  *above_out = above;
+}
+
+__global__ void __launch_bounds__(TOPK_NT) topk_topp_rows(
+    const float* __restrict__ dense, float* __restrict__ values, int64_t* __restrict__ ids,
+    int64_t V, int64_t width, const int32_t* __restrict__ top_k,
+    const float* __restrict__ top_p) {
+  __shared__ TopkShared sh;
+  const int row = blockIdx.x;
+  const float* p = dense + (int64_t)row * V;
+  float* out_v = values + (int64_t)row * width;
+  int64_t* out_i = ids + (int64_t)row * width;
+  int64_t k64 = top_k ? (int64_t)top_k[row] : V;
+  if (k64 <= 0 || k64 > V) k64 = V;
+  const float tp = top_p ? top_p[row] : 1.0f;
+  const bool nucleus = tp < 1.0f;
+
+  if (k64 >= V && !nucleus) {
+    for (int64_t i = threadIdx.x; i < width; i += TOPK_NT) {
+      bool in = i < V;
+      out_v[i] = in ? p[i] : 0.0f;
+      out_i[i] = in ? i : -1;
+    }
+    return;
+  }
+  if (k64 > TOPK_MAX || k64 > width) {
+    // Unsupported list shape: the row is marked with id -2 and NaN values.
+    for (int64_t i = threadIdx.x; i < width; i += TOPK_NT) {
+      out_v[i] = __builtin_nanf("");
+      out_i[i] = -2;
+    }
+    return;
+  }
+  const int k = (int)k64;
+  uint32_t tau;
+  int above;
+  radix_threshold(p, V, k, sh, &tau, &above);
+  const int ties_needed = k - above;
+
+  // Compaction in vocabulary order: thread t owns a contiguous run so that the exclusive scan
+  // of tie counts yields the lowest-index ties.
+  const int64_t run = (V + TOPK_NT - 1) / TOPK_NT;
+  const int64_t lo = (int64_t)threadIdx.x * run;
+  const int64_t hi = lo + run < V ? lo + run : V;
+  uint32_t my_gt = 0, my_eq = 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    uint32_t key = ord_key(p[i]);
+    my_gt += key > tau;
+    my_eq += key == tau;
+  }
+  // exclusive scans of (gt, eq) counts over threads
+  __shared__ uint32_t sgt[TOPK_NT];
+  __shared__ uint32_t seq[TOPK_NT];
+  sgt[threadIdx.x] = my_gt;
+  seq[threadIdx.x] = my_eq;
+  __syncthreads();
+  for (int off = 1; off < TOPK_NT; off <<= 1) {
+    uint32_t a = threadIdx.x >= (unsigned)off ? sgt[threadIdx.x - off] : 0;
+    uint32_t b = threadIdx.x >= (unsigned)off ? seq[threadIdx.x - off] : 0;
+    __syncthreads();
+    sgt[threadIdx.x] += a;
+    seq[threadIdx.x] += b;
+    __syncthreads();
+  }
+  uint32_t gt_before = sgt[threadIdx.x] - my_gt;
+  uint32_t eq_before = seq[threadIdx.x] - my_eq;
+  uint32_t slot = gt_before + (eq_before < (uint32_t)ties_needed ? eq_before : ties_needed);
+  uint32_t eq_seen = eq_before;
+  for (int64_t i = lo; i < hi; ++i) {
+    uint32_t key = ord_key(p[i]);
+    bool take = key > tau;
+    if (key == tau) {
+      take = eq_seen < (uint32_t)ties_needed;
+      ++eq_seen;
+    }
+    if (take) {
+      sh.sel_key[slot] = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+      ++slot;
+    }
+  }
+  __syncthreads();
+  // bitonic sort (descending) over the next power of two
+  int n2 = 1;
+  while (n2 < k) n2 <<= 1;
+  for (int i = k + threadIdx.x; i < n2; i += TOPK_NT) sh.sel_key[i] = 0;
+  __syncthreads();
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < n2; i += TOPK_NT) {
+        int j = i ^ stride;
+        if (j > i) {
+          bool desc = (i & size) == 0;
+          uint64_t a = sh.sel_key[i], b = sh.sel_key[j];
+          if (desc ? (a < b) : (a > b)) {
+            sh.sel_key[i] = b;
+            sh.sel_key[j] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // renormalise over the k survivors
+  uint64_t part = 0;
+  for (int i = threadIdx.x; i < k; i += TOPK_NT)
+    part += canon_fix(p[0xffffffffu - (uint32_t)(sh.sel_key[i] & 0xffffffffu)]);
+  uint64_t S = block_sum_u64<TOPK_NT>(part, sh.red);
+  const float Sf = canon_unfix(S);
+  for (int i = threadIdx.x; i < k; i += TOPK_NT) {
+    uint32_t idx = 0xffffffffu - (uint32_t)(sh.sel_key[i] & 0xffffffffu);
+    float v = Sf > 0.0f ? canon_div(p[idx], Sf) : 0.0f;
+    out_v[i] = v;
+    out_i[i] = idx;
+    sh.fix[i] = canon_fix(v);
+  }
+  for (int64_t i = k + threadIdx.x; i < width; i += TOPK_NT) {
+    out_v[i] = 0.0f;
+    out_i[i] = -1;
+  }
+  if (!nucleus) return;
+  __syncthreads();
+  // nucleus: keep i iff the exclusive prefix (sorted order) is below top_p
+  __shared__ uint64_t s_kept;
+  if (threadIdx.x == 0) {
+    const double limit = (double)tp * (double)(1ull << SV_FIX_BITS);
+    uint64_t pre = 0, kept = 0;
+    for (int i = 0; i < k; ++i) {
+      bool keep = (double)pre < limit;
+      pre += sh.fix[i];
+      if (keep) kept += sh.fix[i]; else sh.fix[i] = ~0ull;  // mark dropped
+    }
+    s_kept = kept;
+  }
+  __syncthreads();
+  const float Kf = canon_unfix(s_kept);
+  for (int i = threadIdx.x; i < k; i += TOPK_NT) {
+    float v = out_v[i];
+    out_v[i] = (sh.fix[i] == ~0ull || !(Kf > 0.0f)) ? 0.0f : canon_div(v, Kf);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Picking an index from non-negative weights: pick = #{k : prefix_incl(k) <= floor(u * R)}
+// with prefix sums and R taken in fixed point, clamped to n - 1.
+// ---------------------------------------------------------------------------------------
+
+// Weight sources
+struct ValuesRow {  // plain probabilities row
+  const float* v;
+  __device__ float operator()(int64_t k) const { return v[k]; }
+};
+
+// Exclusive block scan of u64 run sums for blockDim == NT; returns the exclusive prefix.
+template <int N>
+__device__ uint64_t block_exclusive_scan_u64(uint64_t v, uint64_t* buf) {
+  buf[threadIdx.x] = v;
+  __syncthreads();
+  for (int off = 1; off < N; off <<= 1) {
+    uint64_t a = threadIdx.x >= (unsigned)off ? buf[threadIdx.x - off] : 0;
+    __syncthreads();
+    buf[threadIdx.x] += a;
+    __syncthreads();
+  }
+  uint64_t incl = buf[threadIdx.x];
+  __syncthreads();
+  return incl - v;
+}
+
+// Count, within chunk c of a weight row of length n, the elements whose inclusive fixed-point
+// prefix (starting from `base`) does not exceed `target`.
+template <typename W>
+__device__ uint32_t count_in_chunk(const W& w, int64_t n, int c, uint64_t base, uint64_t target,
+                                   uint64_t* buf, uint64_t* red) {
+  const int64_t lo = (int64_t)c * CHUNK + (int64_t)threadIdx.x * RUN;
+  uint64_t run_sum = 0;
+  for (int j = 0; j < RUN; ++j) {
+    int64_t k = lo + j;
+    if (k < n) run_sum += canon_fix(w(k));
+  }
+  uint64_t pre = base + block_exclusive_scan_u64<NT>(run_sum, buf);
+  uint32_t cnt = 0;
+  for (int j = 0; j < RUN; ++j) {
+    int64_t k = lo + j;
+    if (k < n) {
+      pre += canon_fix(w(k));
+      cnt += pre <= target;
+    }
+  }
+  return (uint32_t)block_sum_u64<NT>(cnt, red);
+}
+
+// ---------------------------------------------------------------------------------------
+// Rejection sampling (DFlash verify).
+// ---------------------------------------------------------------------------------------
+struct RejectArgs {
+  const float* p;
+  const int64_t* ids;
+  const int64_t* drafts;
+  const int64_t* cand;
+  const float* q;
+  const int32_t* slots;
+  const int32_t* valid;
+  const float* uniform;
+  int64_t* out;
+  int64_t* accepted;
+  int64_t b, width, p_width, q_width;
+};
+
+// Probability assigned to `token` by a candidate row (sum over matching ids; ids are unique
+// in lists produced by topk_topp and the selector, so the direct slot is tried first).
+__device__ float row_prob_block(const float* probs, const int64_t* ids, int64_t n,
+                                int64_t token, float* red_f) {
+  __shared__ int s_direct;
+  if (threadIdx.x == 0) s_direct = (token >= 0 && token < n && ids[token] == token);
+  __syncthreads();
+  if (s_direct) {
+    float r = probs[token];
+    __syncthreads();
+    return r;
+  }
+  // general case: block-parallel search, matches summed in index order
+  __shared__ int s_count;
+  __shared__ int64_t s_first;
+  if (threadIdx.x == 0) { s_count = 0; s_first = -1; }
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+    if (ids[i] == token) {
+      atomicAdd(&s_count, 1);
+      s_first = i;  // unique case: the only writer
+    }
+  }
+  __syncthreads();
+  float r = 0.0f;
+  if (s_count == 1) {
+    r = probs[s_first];
+  } else if (s_count > 1) {
+    if (threadIdx.x == 0) {
+      float acc = 0.0f;
+      for (int64_t i = 0; i < n; ++i)
+        if (ids[i] == token) acc = __fadd_rn(acc, probs[i]);
+      red_f[0] = acc;
+    }
+    __syncthreads();
+    r = red_f[0];
+  }
+  __syncthreads();
+  return r;
+}
+
+// Per-thread lookup used inside the residual (q rows are short, or the identity layout).
+__device__ __forceinline__ float row_prob_thread(const float* probs, const int64_t* ids, int64_t n,
+                                                 int64_t token) {
+  if (token >= 0 && token < n && ids[token] == token) return probs[token];
+  float acc = 0.0f;
+  for (int64_t i = 0; i < n; ++i)
+    if (ids[i] == token) acc = __fadd_rn(acc, probs[i]);
+  return acc;
+}
+
+__global__ void __launch_bounds__(NT) reject_scan(RejectArgs a) {
+  __shared__ float red_f[4];
+  const int r = blockIdx.x;
+  const int64_t length = a.width - 1;
+  const int slot = a.slots[r];
+  const bool valid = a.valid[r] != 0;
+  int64_t first = length;
+  for (int64_t j = 0; j < length; ++j) {
+    const int64_t token = a.drafts[r * length + j];
+    const int64_t prow = r * a.width + j;
+    float pt = row_prob_block(a.p + prow * a.p_width, a.ids + prow * a.p_width, a.p_width, token,
+                              red_f);
+    float qt = 1.0f;
+    if (valid) {
+      const int64_t qrow = ((int64_t)slot * length + j) * a.q_width;
+      qt = row_prob_block(a.q + qrow, a.cand + qrow, a.q_width, token, red_f);
+    }
+    if (__fmul_rn(a.uniform[r * a.width + j], qt) >= pt) {
+      first = j;
+      break;
+    }
+  }
+  if (threadIdx.x == 0) g_first[r] = (int32_t)first;
+  for (int64_t j = threadIdx.x; j < a.width; j += NT)
+    a.out[r * a.width + j] = j < first ? a.drafts[r * length + j] : -1;
+}
+
+struct ResidualRow {
+  const float* p;       // p row at position `first`
+  const int64_t* ids;   // ids row at position `first`
+  const float* q;       // q row (or null when the proposal is not valid)
+  const int64_t* cand;
+  int64_t q_width;
+  int64_t draft;        // draft token at `first` (used when q is null)
+  bool subtract;        // false for the bonus position
+  __device__ float operator()(int64_t k) const {
+    float pk = p[k];
+    if (!subtract) return pk;
+    float qk;
+    if (q) qk = row_prob_thread(q, cand, q_width, ids[k]);
+    else qk = (ids[k] == draft) ? 1.0f : 0.0f;
+    float d = __fsub_rn(pk, qk);
+    return d > 0.0f ? d : 0.0f;
+  }
+};
+
+__device__ ResidualRow residual_row(const RejectArgs& a, int r, int64_t first) {
+  const int64_t length = a.width - 1;
+  const int64_t prow = r * a.width + first;
+  ResidualRow w;
+  w.p = a.p + prow * a.p_width;
+  w.ids = a.ids + prow * a.p_width;
+  w.subtract = first < length;
+  const bool valid = a.valid[r] != 0;
+  const int slot = a.slots[r];
+  if (w.subtract && valid) {
+    const int64_t qrow = ((int64_t)slot * length + first) * a.q_width;
+    w.q = a.q + qrow;
+    w.cand = a.cand + qrow;
+  } else {
+    w.q = nullptr;
+    w.cand = nullptr;
+  }
+  w.q_width = a.q_width;
+  w.draft = w.subtract ? a.drafts[r * length + first] : -1;
+  return w;
+}
+
+__global__ void __launch_bounds__(NT) reject_chunks(RejectArgs a, int C) {
+  __shared__ uint64_t red[NT / WAVE];
+  const int c = blockIdx.x, r = blockIdx.y;
+  const int64_t first = g_first[r];
+  ResidualRow w = residual_row(a, r, first);
+  uint64_t rs = 0, ps = 0;
+  for (int k = 0; k < RUN; ++k) {
+    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    if (i < a.p_width) {
+      rs += canon_fix(w(i));
+      ps += canon_fix(w.p[i]);
+    }
+  }
+  rs = block_sum_u64<NT>(rs, red);
+  ps = block_sum_u64<NT>(ps, red);
+  if (threadIdx.x == 0) {
+    g_chunk_sums[(r * CHUNKS_MAX + c) * 2 + 0] = rs;
+    g_chunk_sums[(r * CHUNKS_MAX + c) * 2 + 1] = ps;
+  }
+}
+
+__global__ void __launch_bounds__(NT) reject_pick(RejectArgs a, int C) {
+  __shared__ uint64_t buf[NT];
+  __shared__ uint64_t red[NT / WAVE];
+  __shared__ int s_chunk;
+  __shared__ uint64_t s_base, s_target;
+  __shared__ int s_use_p;
+  const int r = blockIdx.x;
+  const int64_t first = g_first[r];
+  if (threadIdx.x == 0) {
+    uint64_t R = 0;
+    for (int c = 0; c < C; ++c) R += g_chunk_sums[(r * CHUNKS_MAX + c) * 2 + 0];
+    int use_p = 0;
+    if (R == 0) {
+      use_p = 1;
+      for (int c = 0; c < C; ++c) R += g_chunk_sums[(r * CHUNKS_MAX + c) * 2 + 1];
+    }
+    const uint64_t target = canon_scale_floor(a.uniform[r * a.width + a.width - 1], R);
+    uint64_t pre = 0;
+    int c = 0;
+    for (; c < C; ++c) {
+      uint64_t s = g_chunk_sums[(r * CHUNKS_MAX + c) * 2 + use_p];
+      if (pre + s > target) break;
+      pre += s;
+    }
+    s_chunk = c;
+    s_base = pre;
+    s_target = target;
+    s_use_p = use_p;
+  }
+  __syncthreads();
+  int64_t pick;
+  if (s_chunk >= C) {
+    pick = a.p_width - 1;
+  } else {
+    ResidualRow w = residual_row(a, r, first);
+    if (s_use_p) w.subtract = false;
+    uint32_t cnt = count_in_chunk(w, a.p_width, s_chunk, s_base, s_target, buf, red);
+    pick = (int64_t)s_chunk * CHUNK + cnt;
+    if (pick > a.p_width - 1) pick = a.p_width - 1;
+  }
+  if (threadIdx.x == 0) {
+    const int64_t prow = r * a.width + first;
+    a.out[r * a.width + first] = a.ids[prow * a.p_width + pick];
+    a.accepted[r] = first + 1;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Sampling from candidate lists: pick = #(u >= cumsum(values)), clamped to the last slot.
+// ---------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(NT) sample_chunks(const float* __restrict__ values,
+                                                    int64_t width, uint64_t* __restrict__ sums,
+                                                    int C) {
+  __shared__ uint64_t red[NT / WAVE];
+  const int c = blockIdx.x, row = blockIdx.y;
+  const float* v = values + (int64_t)row * width;
+  uint64_t s = 0;
+  for (int k = 0; k < RUN; ++k) {
+    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    if (i < width) s += canon_fix(v[i]);
+  }
+  s = block_sum_u64<NT>(s, red);
+  if (threadIdx.x == 0) sums[row * C + c] = s;
+}
+
+__global__ void __launch_bounds__(NT) sample_pick(const float* __restrict__ values,
+                                                  const int64_t* __restrict__ ids, int64_t width,
+                                                  const uint64_t* __restrict__ sums,
+                                                  const float* __restrict__ uniform,
+                                                  int64_t* __restrict__ out, int C) {
+  __shared__ uint64_t buf[NT];
+  __shared__ uint64_t red[NT / WAVE];
+  __shared__ int s_chunk;
+  __shared__ uint64_t s_base, s_target;
+  const int row = blockIdx.x;
+  if (threadIdx.x == 0) {
+    // u >= prefix  <=>  floor(u * 2^44) >= prefix for integer prefixes
+    const float u = uniform[row];
+    const uint64_t target = u > 0.0f ? (uint64_t)__builtin_floorf(__builtin_ldexpf(u, SV_FIX_BITS)) : 0;
+    uint64_t pre = 0;
+    int c = 0;
+    for (; c < C; ++c) {
+      uint64_t s = sums[row * C + c];
+      if (pre + s > target) break;
+      pre += s;
+    }
+    s_chunk = c;
+    s_base = pre;
+    s_target = target;
+  }
+  __syncthreads();
+  int64_t pick;
+  if (s_chunk >= C) {
+    pick = width - 1;
+  } else {
+    ValuesRow w{values + (int64_t)row * width};
+    uint32_t cnt = count_in_chunk(w, width, s_chunk, s_base, s_target, buf, red);
+    pick = (int64_t)s_chunk * CHUNK + cnt;
+    if (pick > width - 1) pick = width - 1;
+  }
+  if (threadIdx.x == 0) {
+    // never land on an unused (-1) slot: step back to the last real candidate
+    int64_t id = ids[(int64_t)row * width + pick];
+    while (id < 0 && pick > 0) id = ids[(int64_t)row * width + (--pick)];
+    out[row] = id;
+  }
+}
+
+inline hipStream_t S(void* s) { return (hipStream_t)s; }
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+
+// =======================================================================================
+// C ABI
+// =======================================================================================
+
+SV_API int64_t snowllm_sampling_max_k(void) { return VOCAB_MAX; }
+
+SV_API int snowllm_sampling_argmax(const float* logits, int64_t* out, int64_t B, int64_t V,
+                                   void* stream) {
+  if (B < 0 || V <= 0 || V > VOCAB_MAX) return B == 0 ? SV_OK : SV_EINVAL;
+  if (B == 0) return SV_OK;
+  const int C = chunks_of(V);
+  for (int64_t r0 = 0; r0 < B; r0 += ROWS_MAX) {
+    const int rows = (int)((B - r0) < ROWS_MAX ? (B - r0) : ROWS_MAX);
+    hipLaunchKernelGGL(argmax_chunks, dim3(C, rows), dim3(NT), 0, S(stream), logits + r0 * V, V,
+                       C);
+    SV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(argmax_final, dim3(rows), dim3(WAVE), 0, S(stream), out + r0, C);
+    SV_CHECK_LAUNCH();
+  }
+  return SV_OK;
+}
+
+SV_API int snowllm_spec_accept(const int64_t* tokens, const int64_t* drafts, int64_t* acc,
+                               int64_t b, int64_t t, int64_t tokens_stride,
+                               int64_t drafts_stride, void* stream) {
+  if (b < 0 || t < 1) return SV_EINVAL;
+  if (b == 0) return SV_OK;
+  const int nt = 64;
+  hipLaunchKernelGGL(spec_accept_kernel, dim3((unsigned)((b + nt - 1) / nt)), dim3(nt), 0,
+                     S(stream), tokens, drafts, acc, b, t, tokens_stride, drafts_stride);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Workspace: dense probabilities [batch, vocab] f32, then the softmax row statistics, then
+// the candidate lists used by snowllm_sampling_sample (values f32 and ids i64 [batch, width])
+// and their chunk sums.
+SV_API int64_t snowllm_sampling_workspace_bytes(int64_t batch, int64_t vocab, int64_t width) {
+  if (batch < 0 || vocab <= 0) return 0;
+  const int64_t C = chunks_of(vocab);
+  const int64_t Cw = chunks_of(width > 0 ? width : 1);
+  size_t bytes = align256((size_t)batch * vocab * 4);
+  bytes += align256((size_t)batch * C * 4);
+  bytes += align256((size_t)batch * C * 8);
+  bytes += align256((size_t)batch * width * 4);
+  bytes += align256((size_t)batch * width * 8);
+  bytes += align256((size_t)batch * Cw * 8);
+  return (int64_t)bytes;
+}
+
+namespace {
+SoftmaxTail softmax_tail(void* dense, int64_t rows, int64_t vocab) {
+  const int64_t C = chunks_of(vocab);
+  char* base = (char*)dense + align256((size_t)rows * vocab * 4);
+  SoftmaxTail t;
+  t.max_keys = (uint32_t*)base;
+  t.sums = (uint64_t*)(base + align256((size_t)rows * C * 4));
+  return t;
+}
+
+int launch_softmax(const float* logits, float* dense, int64_t rows, int64_t vocab,
+                   const float* temperature, hipStream_t s) {
+  const int C = chunks_of(vocab);
+  SoftmaxTail tail = softmax_tail(dense, rows, vocab);
+  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+    const int n = (int)((rows - r0) < 65535 ? (rows - r0) : 65535);
+    SoftmaxTail t = tail;
+    t.max_keys += r0 * C;
+    t.sums += r0 * C;
+    const float* tr = temperature ? temperature + r0 : nullptr;
+    hipLaunchKernelGGL(softmax_max, dim3(C, n), dim3(NT), 0, s, logits + r0 * vocab, vocab, tr,
+                       t, C);
+    SV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(softmax_exp, dim3(C, n), dim3(NT), 0, s, logits + r0 * vocab, vocab, tr,
+                       dense + r0 * vocab, t, C);
+    SV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(softmax_norm, dim3(C, n), dim3(NT), 0, s, dense + r0 * vocab, vocab, t, C);
+    SV_CHECK_LAUNCH();
+  }
+  return SV_OK;
+}
+
+int launch_topk_topp(const float* dense, float* values, int64_t* ids, int64_t rows,
+                     int64_t vocab, int64_t width, const int32_t* top_k, const float* top_p,
+                     hipStream_t s) {
+  hipLaunchKernelGGL(topk_topp_rows, dim3((unsigned)rows), dim3(TOPK_NT), 0, s, dense, values,
+                     ids, vocab, width, top_k, top_p);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+}  // namespace
+
+SV_API int snowllm_sampling_softmax(const float* logits, float* dense, int64_t rows,
+                                    int64_t vocab, const float* temperature, void* stream) {
+  if (rows < 0 || vocab <= 0 || vocab > VOCAB_MAX) return SV_EINVAL;
+  if (rows == 0) return SV_OK;
+  return launch_softmax(logits, dense, rows, vocab, temperature, S(stream));
+}
+
+// Rows whose top-k exceeds 1024 without keeping the whole vocabulary (or with top-p below 1
+// over the whole vocabulary) are not supported: they are written as (NaN, -2).
+SV_API int snowllm_sampling_topk_topp(const float* dense, float* values, int64_t* ids,
+                                      int64_t rows, int64_t vocab, int64_t width,
+                                      const int32_t* top_k, const float* top_p, void* stream) {
+  if (rows < 0 || vocab <= 0 || vocab > VOCAB_MAX || width <= 0) return SV_EINVAL;
+  if (rows == 0) return SV_OK;
+  return launch_topk_topp(dense, values, ids, rows, vocab, width, top_k, top_p, S(stream));
+}
+
+SV_API int snowllm_sampling_sample(const float* logits, const int32_t* top_k, const float* top_p,
+                                   const float* temperature, const float* uniform, int64_t* out,
+                                   void* ws, int64_t ws_bytes, int64_t B, int64_t V,
+                                   int64_t width, void* stream) {
+  if (B < 0 || V <= 0 || V > VOCAB_MAX || width <= 0) return SV_EINVAL;
+  if (B == 0) return SV_OK;
+  if (ws_bytes < snowllm_sampling_workspace_bytes(B, V, width)) return SV_EINVAL;
+  const int64_t C = chunks_of(V);
+  const int Cw = chunks_of(width);
+  float* dense = (float*)ws;
+  char* p = (char*)ws + align256((size_t)B * V * 4) + align256((size_t)B * C * 4) +
+            align256((size_t)B * C * 8);
+  float* values = (float*)p;
+  p += align256((size_t)B * width * 4);
+  int64_t* ids = (int64_t*)p;
+  p += align256((size_t)B * width * 8);
+  uint64_t* sums = (uint64_t*)p;
+  hipStream_t s = S(stream);
+  int rc = launch_softmax(logits, dense, B, V, temperature, s);
+  if (rc) return rc;
+  rc = launch_topk_topp(dense, values, ids, B, V, width, top_k, top_p, s);
+  if (rc) return rc;
+  for (int64_t r0 = 0; r0 < B; r0 += 65535) {
+    const int n = (int)((B - r0) < 65535 ? (B - r0) : 65535);
+    hipLaunchKernelGGL(sample_chunks, dim3(Cw, n), dim3(NT), 0, s, values + r0 * width, width,
+                       sums + r0 * Cw, Cw);
+    SV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(sample_pick, dim3(n), dim3(NT), 0, s, values + r0 * width,
+                       ids + r0 * width, width, sums + r0 * Cw, uniform + r0, out + r0, Cw);
+    SV_CHECK_LAUNCH();
+  }
+  return SV_OK;
+}
+
+SV_API int snowllm_draft_reject(const float* p, const int64_t* ids, const int64_t* drafts,
+                                const int64_t* cand, const float* q, const int32_t* slots,
+                                const int32_t* valid, const float* uniform, int64_t* out,
+                                int64_t* accepted, int64_t b, int64_t width, int64_t p_width,
+                                int64_t q_width, void* stream) {
+  if (b < 0 || width < 1 || p_width <= 0 || p_width > VOCAB_MAX || q_width < 0)
+    return SV_EINVAL;
+  if (b == 0) return SV_OK;
+  const int C = chunks_of(p_width);
+  hipStream_t s = S(stream);
+  for (int64_t r0 = 0; r0 < b; r0 += ROWS_MAX) {
+    const int n = (int)((b - r0) < ROWS_MAX ? (b - r0) : ROWS_MAX);
+    RejectArgs a;
+    a.p = p + r0 * width * p_width;
+    a.ids = ids + r0 * width * p_width;
+    a.drafts = drafts + r0 * (width - 1);
+    a.cand = cand;
+    a.q = q;
+    a.slots = slots + r0;
+    a.valid = valid + r0;
+    a.uniform = uniform + r0 * width;
+    a.out = out + r0 * width;
+    a.accepted = accepted + r0;
+    a.b = n;
+    a.width = width;
+    a.p_width = p_width;
+    a.q_width = q_width;
+    hipLaunchKernelGGL(reject_scan, dim3(n), dim3(NT), 0, s, a);
+    SV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(reject_chunks, dim3(C, n), dim3(NT), 0, s, a, C);
+    SV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(reject_pick, dim3(n), dim3(NT), 0, s, a, C);
+    SV_CHECK_LAUNCH();
+  }
+  return SV_OK;
+}

@@ -1,0 +1,65 @@
+"""GGUF k-quant GEMM operators (snowllm/ops/gemm.py:130-163).
+
+Format ids follow the reference (ops/moe.py:189-190): 4 = Q4_K, 8 = Q8_0.
+"""
+import torch
+
+from ._capi import SnowLLMError, check, lib
+from ._common import _chk, _p, _stream, empty_bytes
+
+Q4_K, Q8_0 = 4, 8
+
+
+def kquant_bytes(fmt: int, N: int, K: int) -> tuple[int, int, int]:
+    return (lib.snowllm_kquant_quant_bytes(fmt, N, K), lib.snowllm_kquant_meta_bytes(fmt, N, K),
+            lib.snowllm_kquant_gguf_bytes(fmt, N, K))
+
+
+def gemm_kquant_shuffle_b(fmt: int, b_gguf: torch.Tensor, N: int,
+                          K: int) -> tuple[torch.Tensor, torch.Tensor]:
+    quant_bytes, meta_bytes, gguf_bytes = kquant_bytes(fmt, N, K)
+    if quant_bytes < 0 or meta_bytes < 0:
+        raise SnowLLMError(f"gemm_kquant_shuffle_b: format {fmt} with N={N}, K={K} is not supported "
+                           f"(N must be a multiple of 16 and K of 256)")
+    _chk(b_gguf, "b_gguf", torch.uint8)
+    if b_gguf.numel() != gguf_bytes:
+        raise SnowLLMError(f"gemm_kquant_shuffle_b: expected {gguf_bytes} bytes of GGUF blocks for "
+                           f"a [{N}, {K}] weight at format {fmt}, got {b_gguf.numel()}")
+    quant, meta = empty_bytes(quant_bytes), empty_bytes(meta_bytes)
+    check(lib.snowllm_gemm_kquant_shuffle_b(fmt, _p(b_gguf), _p(quant), _p(meta), N, K, _stream()),
+          "gemm_kquant_shuffle_b")
+    return quant, meta
+
+
+def gemm_kquant_a_ws_bytes(M: int, K: int) -> int:
+    return int(lib.snowllm_gemm_kquant_a_ws_bytes(int(M), int(K)))
+
+
+def gemm_kquant_a(fmt: int, a: torch.Tensor, quant: torch.Tensor, meta: torch.Tensor,
+                  c: torch.Tensor, M: int, N: int, K: int, ws: torch.Tensor) -> None:
+    """C[M, N] = A[M, K] @ W[N, K]^T with W dequantised on the fly (fp32 accumulate)."""
+    _chk(a, "a", torch.bfloat16, M, K)
+    _chk(ws, "ws", torch.uint8, gemm_kquant_a_ws_bytes(M, K))
+    bf16 = c.dtype is torch.bfloat16
+    _chk(c, "c", torch.bfloat16 if bf16 else torch.float32, M, N)
+    check(lib.snowllm_gemm_kquant_a(fmt, _p(a), _p(quant), _p(meta), _p(c), M, N, K, bf16, _p(ws),
+                                    _stream()), "gemm_kquant_a")
+
+
+def gemm_kquant_prepare_a(a: torch.Tensor, ws: torch.Tensor) -> None:
+    """Convert activations into the operand workspace once (extension; no reference
+    counterpart): lets several weights sharing one input skip the conversion."""
+    M, K = a.shape
+    _chk(a, "a", torch.bfloat16, M, K)
+    _chk(ws, "ws", torch.uint8, gemm_kquant_a_ws_bytes(M, K))
+    check(lib.snowllm_gemm_kquant_prepare_a(_p(a), M, K, _p(ws), _stream()), "gemm_kquant_prepare_a")
+
+
+def gemm_kquant_a_prepared(fmt: int, quant: torch.Tensor, meta: torch.Tensor, c: torch.Tensor,
+                           M: int, N: int, K: int, ws: torch.Tensor) -> None:
+    """gemm_kquant_a on a workspace filled by gemm_kquant_prepare_a (extension)."""
+    _chk(ws, "ws", torch.uint8, gemm_kquant_a_ws_bytes(M, K))
+    bf16 = c.dtype is torch.bfloat16
+    _chk(c, "c", torch.bfloat16 if bf16 else torch.float32, M, N)
+    check(lib.snowllm_gemm_kquant_a_prepared(fmt, _p(quant), _p(meta), _p(c), M, N, K, bf16, _p(ws),
+                                             _stream()), "gemm_kquant_a_prepared")
