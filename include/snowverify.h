@@ -114,6 +114,10 @@ int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, const ui
                           void* c, int64_t M, int64_t N, int64_t K, int c_is_bf16, void* ws,
                           void* stream);
 
+/* Extension (tuning knob), no counterpart in the reference: force a GEMV tile shape,
+ * 0 = automatic. Process-global. */
+void snowverify_gemv_variant(int v);
+
 /* Extension, no counterpart in the reference: fill the gemm_kquant_a operand workspace from
  * bf16 activations A[M, K] once, so that several weights sharing one input reuse it. */
 int snowllm_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws, void* stream);
@@ -122,6 +126,28 @@ int snowllm_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws,
 int snowllm_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta, void* c,
                                    int64_t M, int64_t N, int64_t K, int c_is_bf16,
                                    const void* ws, void* stream);
+
+/* ---- paged attention --------------------------------------------------------------- */
+
+/* Scratch bytes of snowverify_paged_attention (split-KV partials). */
+int64_t snowverify_paged_attention_scratch_bytes(int64_t batch, int64_t tokens, int64_t num_heads,
+                                                 int64_t num_kv_heads, int64_t head_size);
+
+/* GQA attention of `tokens` query rows per request against the paged bf16 KV cache, with the
+ * shapes passed explicitly (the reference's snowllm_paged_attention, snowllm/_capi.py:220 and
+ * snowllm/ops/attention_full.py:120-177, reads them from its compiled-in geometry).
+ * q/out bf16 [batch*tokens, num_heads, head_size]; pools in the reference layouts
+ * K [blocks, Hkv, d/16, page, 16], V [blocks, Hkv, page/4, d, 4] (tests/test_lfm2_dspark_
+ * reference.py:30-36); table i32 [batch, table_stride]; lens i32 [batch] = context + tokens.
+ * Row t sees the context and, of the block, the rows whose bits are set in tree[b*tokens + t]
+ * (u64), or rows 0..t when tree is null (causal, tests/test_lfm2_long_attention.py:40-44).
+ * head_size 128 or 256, page_size 16, tokens <= 64. */
+int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_pool, void* out,
+                               const int32_t* table, const int32_t* lens, const uint64_t* tree,
+                               int64_t batch, int64_t tokens, int64_t num_heads,
+                               int64_t num_kv_heads, int64_t head_size, int64_t page_size,
+                               int64_t table_stride, float scale, void* scratch,
+                               int64_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -81,6 +81,10 @@ _SIGS = [
     ("snowllm_gemm_kquant_a", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
     ("snowllm_gemm_kquant_prepare_a", c_int, [P, c_int64, c_int64, P, S]),
     ("snowllm_gemm_kquant_a_prepared", c_int, [c_int, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
+    ("snowverify_gemv_variant", None, [c_int]),
+    # paged attention
+    ("snowverify_paged_attention_scratch_bytes", c_int64, [c_int64] * 5),
+    ("snowverify_paged_attention", c_int, [P] * 7 + [c_int64] * 7 + [c_float, P, c_int64, S]),
 ]
 
 _missing = []

@@ -27,17 +27,19 @@ constexpr int QK = 256;          // weights per superblock
 constexpr int TILE_N = 16;       // columns per MFMA tile
 constexpr int TILE_M = 16;       // rows per MFMA tile
 
-// Activation workspace for one 16-row tile and S superblocks.
+// Activation workspace for one 16-row tile and S superblocks. Each (row, superblock) has its
+// own power-of-two scale so that the fp16 operands are exact for any bf16 input.
 struct XPrepView {
-  u32x4* xop;   // [S][8][64] fp16 A operands (8 halves per lane)
-  float* sxop;  // [S][2][64] negated sub-block sums, f32 MFMA A operand
-  int* exps;    // [16] per-row power-of-two scale
+  u32x4* xop;     // [S][8][64] fp16 A operands (8 halves per lane)
+  float* sxop;    // [S][2][64] negated sub-block sums, f32 MFMA A operand
+  float* scale;   // [S][16] 2^e per (superblock, row): undoes the operand scaling
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 inline size_t xprep_tile_bytes(int64_t S) {
-  return align256((size_t)S * 8 * 64 * 16) + align256((size_t)S * 2 * 64 * 4) + 256;
+  return align256((size_t)S * 8 * 64 * 16) + align256((size_t)S * 2 * 64 * 4) +
+         align256((size_t)S * 16 * 4);
 }
 
 __host__ __device__ inline XPrepView xprep_view(void* base, int64_t S) {
@@ -47,99 +49,87 @@ __host__ __device__ inline XPrepView xprep_view(void* base, int64_t S) {
   p += ((size_t)S * 8 * 64 * 16 + 255) & ~(size_t)255;
   v.sxop = (float*)p;
   p += ((size_t)S * 2 * 64 * 4 + 255) & ~(size_t)255;
-  v.exps = (int*)p;
+  v.scale = (float*)p;
   return v;
 }
 
-// Slot e of a lane's 8 fp16 operand values holds k-offset kperm[e] within its 8-wide k range.
-// This is the order in which the nibble/byte decoders below emit weights.
-__constant__ int kperm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+// Slot e of a lane's 8 fp16 operand values holds k-offset kperm(e) within its 8-wide k range:
+// 0, 2, 1, 3, 4, 6, 5, 7 -- the order in which the nibble/byte decoders below emit weights.
+__host__ __device__ constexpr int kperm_c(int e) { return (e & 4) | ((e & 1) << 1) | ((e >> 1) & 1); }
 
 // ---------------------------------------------------------------------------------------
-// Activation prep: bf16 [rows, K] -> fp16 MFMA operands with a per-row exponent.
+// Activation prep: bf16 [rows, K] -> fp16 MFMA operands. One wave per (row tile, superblock);
+// lane (row = lane & 15, kq = lane >> 4) owns k = 32 j + 8 kq + 0..7 of every sub-block j.
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) xprep_kernel(const uint16_t* __restrict__ a, int64_t M,
-                                                    int64_t K, void* ws, size_t tile_bytes) {
-  __shared__ float s_max[TILE_M];
-  const int tile = blockIdx.x;
+__global__ void __launch_bounds__(64) xprep_kernel(const uint16_t* __restrict__ a, int64_t M,
+                                                   int64_t K, void* ws, size_t tile_bytes) {
+  const int s = blockIdx.x, tile = blockIdx.y;
+  const int lane = threadIdx.x, r = lane & 15, kq = lane >> 4;
   const int64_t S = K / QK;
   XPrepView v = xprep_view((char*)ws + tile * tile_bytes, S);
-  const int64_t r0 = (int64_t)tile * TILE_M;
-  const int rows = (int)((M - r0) < TILE_M ? (M - r0) : TILE_M);
-  // per-row max |x|
-  for (int r = 0; r < TILE_M; ++r) {
-    float m = 0.0f;
-    if (r < rows) {
-      const uint16_t* x = a + (r0 + r) * K;
-      for (int64_t i = threadIdx.x; i < K; i += 256) {
-        float f = __builtin_fabsf(bf16_to_f32(x[i]));
-        m = f > m ? f : m;
-      }
-    }
-    m = wave_max(m);
-    __shared__ float wm[4];
-    if ((threadIdx.x & 63) == 0) wm[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float t = wm[0];
-      for (int i = 1; i < 4; ++i) t = wm[i] > t ? wm[i] : t;
-      s_max[r] = t;
-    }
-    __syncthreads();
+  const int64_t row = (int64_t)tile * TILE_M + r;
+  const bool live = row < M;
+  // raw bf16 (8 sub-blocks x 8 values)
+  u32x4 raw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    raw[j] = live ? *(const u32x4*)(a + row * K + (int64_t)s * QK + j * 32 + kq * 8)
+                  : u32x4{0u, 0u, 0u, 0u};
   }
-  if (threadIdx.x < TILE_M) {
-    float m = s_max[threadIdx.x];
-    int e = 0;
-    if (m > 0.0f && m <= 3.40282346638528859812e38f) {
-      int E = (int)((__float_as_uint(m) >> 23) & 0xff) - 127;
-      if (E < -126) E = -126;
-      e = E - 14;  // scaled row maximum lands in [2^14, 2^15)
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mx = fmaxf(mx, __builtin_fabsf(__uint_as_float(w4[i] << 16)));
+      mx = fmaxf(mx, __builtin_fabsf(__uint_as_float(w4[i] & 0xffff0000u)));
     }
-    v.exps[threadIdx.x] = e;
   }
-  __syncthreads();
-  // fp16 operands
-  const int64_t n_ops = S * 8 * 64;
-  for (int64_t idx = threadIdx.x; idx < n_ops; idx += 256) {
-    const int lane = (int)(idx & 63);
-    const int64_t sj = idx >> 6;  // s * 8 + j
-    const int r = lane & 15, kq = lane >> 4;
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.40282346638528859812e38f) {
+    int E = (int)((__float_as_uint(mx) >> 23) & 0xff) - 127;
+    if (E < -126) E = -126;
+    e = E - 14;  // scaled maximum lands in [2^14, 2^15)
+  }
+  float part[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w4[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w4[i] & 0xffff0000u);
+    }
     uint16_t h[8];
-    if (r < rows) {
-      const int e = v.exps[r];
-      const uint16_t* x = a + (r0 + r) * K + sj * 32 + kq * 8;
+    float sum = 0.0f;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) h[t] = f32_to_f16(__builtin_ldexpf(bf16_to_f32(x[kperm[t]]), -e));
-    } else {
-#pragma unroll
-      for (int t = 0; t < 8; ++t) h[t] = 0;
+    for (int t = 0; t < 8; ++t) {
+      _Float16 hv = (_Float16)__builtin_ldexpf(f[kperm_c(t)], -e);
+      h[t] = __builtin_bit_cast(uint16_t, hv);
+      sum += (float)hv;
     }
+    part[j] = sum;
     u32x4 o;
     o.x = h[0] | ((uint32_t)h[1] << 16);
     o.y = h[2] | ((uint32_t)h[3] << 16);
     o.z = h[4] | ((uint32_t)h[5] << 16);
     o.w = h[6] | ((uint32_t)h[7] << 16);
-    v.xop[idx] = o;
+    v.xop[((int64_t)s * 8 + j) * 64 + lane] = o;
   }
-  // negated sub-block sums in the f32 MFMA A layout: lane -> (row lane&15, k = lane>>4)
-  const int64_t n_sx = S * 2 * 64;
-  for (int64_t idx = threadIdx.x; idx < n_sx; idx += 256) {
-    const int lane = (int)(idx & 63);
-    const int64_t sh = idx >> 6;  // s * 2 + half
-    const int64_t s = sh >> 1;
-    const int j = (int)(sh & 1) * 4 + (lane >> 4);
-    const int r = lane & 15;
-    float sum = 0.0f;
-    if (r < rows) {
-      const int e = v.exps[r];
-      const uint16_t* x = a + (r0 + r) * K + s * QK + j * 32;
-      for (int i = 0; i < 32; ++i) {
-        _Float16 hx = (_Float16)__builtin_ldexpf(bf16_to_f32(x[i]), -e);
-        sum += (float)hx;
-      }
-    }
-    v.sxop[idx] = -sum;
+  // full sub-block sums: add the four kq lanes of the row (fixed order)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    part[j] += __shfl_xor(part[j], 16, 64);
+    part[j] += __shfl_xor(part[j], 32, 64);
   }
+  // f32 MFMA A layout: lane -> (row lane & 15, k = lane >> 4): half hh holds sub-block 4 hh + kq
+  v.sxop[((int64_t)s * 2 + 0) * 64 + lane] = -part[kq];
+  v.sxop[((int64_t)s * 2 + 1) * 64 + lane] = -part[4 + kq];
+  if (kq == 0) v.scale[(int64_t)s * 16 + r] = __builtin_ldexpf(1.0f, e);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -174,14 +164,16 @@ __device__ __forceinline__ float byte_f(uint32_t w, int i) {
   return (float)((w >> (8 * i)) & 0xffu);
 }
 
-// One 16-column x 256-weight tile, accumulated into acc (C layout: column lane&15, rows
-// 4*(lane>>4)+i). xa: A operands of the 8 sub-blocks, sx: negated sub-block sums.
+// One 16-column x 256-weight tile. Returns the superblock's contribution in the C layout
+// (column lane & 15, rows 4*(lane >> 4) + i), still in units of the operand scaling.
+// xa: A operands of the 8 sub-blocks, sx0/sx1: negated sub-block sums (f32 MFMA A operand).
 template <int FMT>
-__device__ __forceinline__ void tile_superblock(const u32x4* qv, u32x4 meta, const half8* xa,
-                                                float sx0, float sx1, int kq, floatx4& acc) {
+__device__ __forceinline__ floatx4 tile_superblock(const u32x4* qv, u32x4 meta, const half8* xa,
+                                                   float sx0, float sx1, int kq) {
   const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+  floatx4 acc = zero;
   float a[8];
-  float beta_lo, beta_hi;  // beta for sub-blocks kq and kq+4
+  float beta_lo, beta_hi;  // beta for sub-blocks kq and kq + 4
   if constexpr (FMT == FMT_Q4_K) {
     const float d = f16_to_f32((uint16_t)(meta.x & 0xffff));
     const float dmin = f16_to_f32((uint16_t)(meta.x >> 16));
@@ -197,10 +189,10 @@ __device__ __forceinline__ void tile_superblock(const u32x4* qv, u32x4 meta, con
     }
     const float m_lo = dmin * byte_f(m03, kq);
     const float m_hi = dmin * byte_f(m47, kq);
-    // even sub-blocks carry the 1024 offset, odd ones 1024/16 after the 1/16 fold
-    const float off_lo = (kq & 1) ? 64.0f : 1024.0f;
-    beta_lo = __builtin_fmaf(off_lo, a[kq], m_lo);
-    beta_hi = __builtin_fmaf(off_lo, a[4 + kq], m_hi);
+    // even sub-blocks carry the 1024 offset; odd ones read 1024 + 16 q, i.e. 64 after the 1/16
+    const float off = (kq & 1) ? 64.0f : 1024.0f;
+    beta_lo = __builtin_fmaf(off, a[kq], m_lo);
+    beta_hi = __builtin_fmaf(off, a[4 + kq], m_hi);
     const u32x4 q0 = qv[0], q1 = qv[1];
     half8 lo, hi;
     floatx4 c;
@@ -243,9 +235,10 @@ __device__ __forceinline__ void tile_superblock(const u32x4* qv, u32x4 meta, con
       acc += a[2 * jp + 1] * c;
     }
   }
-  // offset/min term: acc += (-Sx) * beta over the 8 sub-blocks (k = lane>>4 within each half)
+  // offset/min term: acc += (-Sx) * beta over the 8 sub-blocks (k = lane >> 4 in each half)
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sx0, beta_lo, acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sx1, beta_hi, acc, 0, 0, 0);
+  return acc;
 }
 
 template <int FMT>
@@ -253,14 +246,48 @@ struct QLayout {
   static constexpr int kQuantVecs = FMT == FMT_Q4_K ? 2 : 4;  // u32x4 per lane per superblock
 };
 
-// NW waves split the superblocks of NTILE column tiles; partial sums meet in LDS.
+// Per-wave operands of one superblock for NTILE column tiles.
+template <int FMT, int NTILE>
+struct SbOperands {
+  u32x4 x[8];
+  float sx0, sx1;
+  floatx4 scale;
+  u32x4 q[NTILE][QLayout<FMT>::kQuantVecs];
+  u32x4 m[NTILE];
+};
+
+template <int FMT, int NTILE>
+__device__ __forceinline__ void load_sb(SbOperands<FMT, NTILE>& o, const XPrepView& xv,
+                                        const u32x4* __restrict__ quant,
+                                        const u32x4* __restrict__ meta, int s, int S, int tile0,
+                                        int tiles, int lane, bool live) {
+  constexpr int QV = QLayout<FMT>::kQuantVecs;
+  const int r = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    o.x[j] = live ? xv.xop[((int64_t)s * 8 + j) * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
+  o.sx0 = xv.sxop[((int64_t)s * 2 + 0) * 64 + lane];
+  o.sx1 = xv.sxop[((int64_t)s * 2 + 1) * 64 + lane];
+  o.scale = *(const floatx4*)(xv.scale + (int64_t)s * 16 + 4 * kq);
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) {
+    const int tile = tile0 + t < tiles ? tile0 + t : tiles - 1;
+    const int64_t ts = (int64_t)tile * S + s;
+#pragma unroll
+    for (int i = 0; i < QV; ++i) o.q[t][i] = quant[(ts * QV + i) * 64 + lane];
+    o.m[t] = meta[ts * 16 + r];
+  }
+}
+
+// NW waves split the superblocks of NTILE column tiles (wave w takes s = w, w + NW, ...) with
+// the next superblock's operands in flight while the current one is multiplied; the waves'
+// partial sums meet in LDS and are added in a fixed order.
 template <int FMT, int NTILE, int NW>
 __global__ void __launch_bounds__(NW * 64) kquant_gemv(const u32x4* __restrict__ quant,
                                                        const u32x4* __restrict__ meta,
                                                        const void* __restrict__ ws,
                                                        void* __restrict__ c, int M, int N, int S,
                                                        int c_bf16) {
-  constexpr int QV = QLayout<FMT>::kQuantVecs;
   __shared__ floatx4 part[NW][NTILE][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int kq = lane >> 4, r = lane & 15;
@@ -272,27 +299,22 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv(const u32x4* __restrict__
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  for (int s = w; s < S; s += NW) {
-    half8 xa[8];
+  if (w < S) {
+    SbOperands<FMT, NTILE> cur, nxt;
+    load_sb<FMT, NTILE>(cur, xv, quant, meta, w, S, tile0, tiles, lane, live);
+    for (int s = w; s < S; s += NW) {
+      const bool more = s + NW < S;
+      if (more) load_sb<FMT, NTILE>(nxt, xv, quant, meta, s + NW, S, tile0, tiles, lane, live);
+      half8 xa[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x4 v = live ? xv.xop[((int64_t)s * 8 + j) * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
-      xa[j] = __builtin_bit_cast(half8, v);
+      for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, cur.x[j]);
+#pragma unroll
+      for (int t = 0; t < NTILE; ++t) {
+        floatx4 sb = tile_superblock<FMT>(cur.q[t], cur.m[t], xa, cur.sx0, cur.sx1, kq);
+        acc[t] += sb * cur.scale;
+      }
+      if (more) cur = nxt;
     }
-    const float sx0 = xv.sxop[((int64_t)s * 2 + 0) * 64 + lane];
-    const float sx1 = xv.sxop[((int64_t)s * 2 + 1) * 64 + lane];
-    u32x4 qv[NTILE][QV];
-    u32x4 mv[NTILE];
-#pragma unroll
-    for (int t = 0; t < NTILE; ++t) {
-      const int tile = tile0 + t < tiles ? tile0 + t : tiles - 1;
-      const int64_t ts = (int64_t)tile * S + s;
-#pragma unroll
-      for (int i = 0; i < QV; ++i) qv[t][i] = quant[(ts * QV + i) * 64 + lane];
-      mv[t] = meta[ts * 16 + r];
-    }
-#pragma unroll
-    for (int t = 0; t < NTILE; ++t) tile_superblock<FMT>(qv[t], mv[t], xa, sx0, sx1, kq, acc[t]);
   }
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) part[w][t][lane] = acc[t];
@@ -311,9 +333,8 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv(const u32x4* __restrict__
     for (int i = 0; i < 4; ++i) {
       const int row = rb + i;
       if (row >= M) break;
-      const float y = __builtin_ldexpf(v[i], xv.exps[row]);
-      if (c_bf16) ((uint16_t*)c)[(int64_t)row * N + n] = f32_to_bf16(y);
-      else ((float*)c)[(int64_t)row * N + n] = y;
+      if (c_bf16) ((uint16_t*)c)[(int64_t)row * N + n] = f32_to_bf16(v[i]);
+      else ((float*)c)[(int64_t)row * N + n] = v[i];
     }
   }
 }
@@ -379,12 +400,27 @@ int launch_gemv(const void* quant, const void* meta, const void* ws, void* c, in
   return SV_OK;
 }
 
+int g_gemv_variant = 0;  // 0 = automatic; see snowverify_gemv_variant
+
 template <int FMT>
 int dispatch_gemv(const void* quant, const void* meta, const void* ws, void* c, int M, int N,
                   int S, int c_bf16, hipStream_t s) {
+  switch (g_gemv_variant) {
+    case 1: return launch_gemv<FMT, 1, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 2: return launch_gemv<FMT, 2, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 3: return launch_gemv<FMT, 4, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 4: return launch_gemv<FMT, 1, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 5: return launch_gemv<FMT, 2, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 6: return launch_gemv<FMT, 1, 16>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 7: return launch_gemv<FMT, 2, 16>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 8: return launch_gemv<FMT, 4, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    default: break;
+  }
   const int tiles = N / TILE_N;
-  // Keep at least one workgroup per CU (256 on MI355X) where the shape allows it.
-  if (tiles >= 4 * 256) return launch_gemv<FMT, 4, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
+  if (S >= 16) {
+    if (tiles >= 2 * 256) return launch_gemv<FMT, 2, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    return launch_gemv<FMT, 1, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
+  }
   if (tiles >= 2 * 256) return launch_gemv<FMT, 2, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
   return launch_gemv<FMT, 1, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
 }
@@ -413,6 +449,10 @@ SV_API int64_t snowllm_kquant_meta_bytes(int fmt, int64_t N, int64_t K) {
 }
 
 SV_API int snowllm_kquant_supported(int fmt) { return fmt_ok(fmt) ? 1 : 0; }
+
+// Extension (tuning knob, no counterpart in the reference): force a GEMV tile shape
+// (0 = automatic, 1..8 = fixed (tiles per workgroup, waves) pairs). Process-global.
+SV_API void snowverify_gemv_variant(int v) { g_gemv_variant = v; }
 
 SV_API int snowllm_gemm_kquant_shuffle_b(int fmt, const uint8_t* gguf, uint8_t* quant,
                                          uint8_t* meta, int64_t N, int64_t K, void* stream) {
@@ -445,8 +485,8 @@ SV_API int snowllm_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, vo
   if (M == 0) return SV_OK;
   const int64_t S = K / 256;
   const int64_t mt = (M + TILE_M - 1) / TILE_M;
-  hipLaunchKernelGGL(xprep_kernel, dim3((unsigned)mt), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)a, M, K, ws, xprep_tile_bytes(S));
+  hipLaunchKernelGGL(xprep_kernel, dim3((unsigned)S, (unsigned)mt), dim3(64), 0,
+                     (hipStream_t)stream, (const uint16_t*)a, M, K, ws, xprep_tile_bytes(S));
   SV_CHECK_LAUNCH();
   return SV_OK;
 }

@@ -7,3 +7,5 @@ from . import dflash  # noqa: F401
 from .gemm import (Q4_K, Q8_0, gemm_kquant_a, gemm_kquant_a_ws_bytes,  # noqa: F401
                    gemm_kquant_shuffle_b, kquant_bytes,
                    gemm_kquant_prepare_a, gemm_kquant_a_prepared)
+from .attention import (kv_pool_bytes, paged_attention_explicit,  # noqa: F401
+                        paged_attention_scratch_bytes)

@@ -10,7 +10,7 @@ ROOT = pathlib.Path(__file__).resolve().parents[1]
 
 def declared_symbols():
     text = (ROOT / "include" / "snowverify.h").read_text()
-    return sorted(set(re.findall(r"\b(snowllm_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b((?:snowllm|snowverify)_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
