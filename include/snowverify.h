@@ -149,6 +149,97 @@ int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_
                                int64_t table_stride, float scale, void* scratch,
                                int64_t scratch_bytes, void* stream);
 
+/* ---- geometry ------------------------------------------------------------------------ */
+/* The reference compiles its shapes in (snowllm/_capi.py:44-113); here they are run-time
+ * data. BuildGeometry has the reference's 37 int64 fields in the same order. */
+typedef struct BuildGeometry BuildGeometry;
+
+/* Current geometry (snowllm/_capi.py:50-53). */
+void snowllm_model_config(BuildGeometry* out);
+/* Select a geometry: 0 = Qwen3.6-35B-A3B shape (BASELINE configs 4/5), 100 = dense 8B shape
+ * (snowllm/_capi.py:94-103). */
+int snowllm_select_geometry(int geo);
+int snowllm_active_geometry(void);                                     /* _capi.py:106-107 */
+int64_t snowllm_geometry_name(int geo, char* buf, int64_t n);          /* _capi.py:110-113 */
+/* Extension, no counterpart in the reference: install arbitrary shapes (geometry id 1000). */
+int snowverify_define_geometry(const BuildGeometry* g);
+
+/* ---- layer plumbing --------------------------------------------------------------------- */
+/* Embedding gather (snowllm/_capi.py:375; snowllm/ops/embedding.py:18-25): bf16 table of the
+ * current geometry. The extension takes an fp16 (table_f16 = 1) or bf16 table [V, H]. */
+int snowllm_gather_embedding(const int64_t* ids, const void* table, void* out, int64_t M,
+                             void* stream);
+int snowverify_gather_embedding(const int64_t* ids, const void* table, void* out, int64_t M,
+                                int64_t V, int64_t H, int table_f16, void* stream);
+
+/* RMSNorm y = x rsqrt(mean(x^2) + eps) gamma (snowllm/_capi.py:376, 381; ops/norm.py:66-97);
+ * the residual form first sets residual = x + residual. */
+int snowllm_rmsnorm(const void* x, const void* gamma, void* out, int64_t M, float eps,
+                    void* stream);
+int snowllm_rmsnorm_residual(const void* x, void* residual, const void* gamma, void* out,
+                             int64_t M, float eps, void* stream);
+int snowverify_rmsnorm(const void* x, void* residual, const void* gamma, void* out, int64_t M,
+                       int64_t H, float eps, void* stream);
+
+/* RoPE tables cos/sin [M, half] of pos * inv_freq (snowllm/ops/rope.py:11-24 computes them
+ * inside snowllm_rope_cos_sin; this form takes the table width explicitly). */
+int snowverify_rope_cos_sin(const int64_t* pos, const float* inv_freq, float* cos_out,
+                            float* sin_out, int64_t M, int64_t half, void* stream);
+
+/* QK-norm + RoPE + paged KV write (snowllm/_capi.py:397-399; ops/attention_full.py:736-784)
+ * with explicit shapes: proj [M, stride] = q|k|v bf16 -> q_out [M, Hq, D]; k, v into the pools
+ * at slots[m] (negative: skipped). D <= 256. */
+int snowverify_qk_norm_rope_cache(const void* proj, int64_t stride, const void* q_gamma,
+                                  const void* k_gamma, const float* cos_in, const float* sin_in,
+                                  void* q_out, void* k_pool, void* v_pool, const int32_t* slots,
+                                  int64_t M, int64_t Hq, int64_t Hkv, int64_t D, int64_t half,
+                                  int64_t page, float eps, void* stream);
+
+/* slot = table[seq, pos / page] * page + pos % page (snowllm/_capi.py:361; ops/cache.py:40-53;
+ * spec_decode.py:183). */
+int snowllm_resolve_slots(const int32_t* table, int64_t stride, const int32_t* seq,
+                          const int32_t* pos, int32_t* out, int64_t M, int64_t page, void* stream);
+
+/* K/V pool bytes for num_blocks pages of the current geometry (snowllm/_capi.py:359). */
+void snowllm_kv_pool_bytes(int64_t num_blocks, int64_t block_size, int kv_int8, int64_t* k,
+                           int64_t* v);
+
+/* Extensions: SwiGLU over a [M, 2F] gate|up block, bf16 add, and MoE routing (softmax over E
+ * routed logits, top-k, renormalised; sigmoid of column E as the shared-expert gate). */
+int snowverify_swiglu(const void* gate_up, int64_t stride, void* out, int64_t M, int64_t F,
+                      void* stream);
+int snowverify_add_bf16(const void* a, const void* b, void* out, int64_t n, void* stream);
+int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, int64_t E, int64_t topk,
+                         float* weights, int32_t* ids, float* shared_w, void* stream);
+
+/* ---- feed-forward (extensions; the reference reaches these through snowllm_inference_*,
+ * snowllm/_capi.py:687-692, whose weight descriptors and workspaces are internal) ------------ */
+/* res_out = x + res_in; y = RMSNorm(res_out) * gamma into the k-quant operand workspace ws (and
+ * y_out if given). res_out must not alias x or res_in. */
+int snowverify_norm_prep(const void* x, const void* res_in, void* res_out, const void* gamma,
+                         void* y_out, void* ws, int64_t M, int64_t H, float eps, void* stream);
+/* 16-bit weight GEMV: repack size, repack (wt 1 = fp16, 2 = bf16), and C = A W^T (fp16 weights
+ * take the operand workspace, bf16 weights bf16 activations). M <= 16. */
+int64_t snowverify_dense_bytes(int64_t N, int64_t K);
+int snowverify_dense_shuffle(const void* src, void* dst, int64_t N, int64_t K, int wt,
+                             void* stream);
+int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c, int64_t M, int64_t N,
+                          int64_t K, int c_is_bf16, void* stream);
+/* act[M, F] = silu(x Wg^T) * (x Wu^T), gate_up the packed [2F, K] k-quant weight. */
+int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* meta, const void* ws,
+                              void* act, int64_t M, int64_t F, int64_t K, void* stream);
+/* MoE: plan of the experts the block touches (device side), then the experts of one layer. */
+int64_t snowverify_moe_plan_bytes(void);
+int snowverify_moe_plan(const int32_t* ids, int64_t M, int64_t topk, int64_t E, int shared,
+                        void* plan, void* stream);
+int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_meta,
+                           const void* dn_quant, const void* dn_meta, const void* sh_gu_quant,
+                           const void* sh_gu_meta, const void* sh_dn_quant,
+                           const void* sh_dn_meta, const void* plan, const void* ws,
+                           const float* weights, const float* shared_w, void* act, float* pairs,
+                           float* shared_out, void* out, int64_t M, int64_t topk, int64_t E,
+                           int64_t H, int64_t F, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,152 @@
+"""CPU reference of one verify-step layer -- TEST INFRASTRUCTURE ONLY.
+
+torch fp32 arithmetic with bf16 rounding at the tensor boundaries of the reference's Qwen3.5
+layer (snowllm/models/qwen3_5/qwen3_5.py:32-78, layers.py:75-228):
+  residual update, RMSNorm (x * rsqrt(mean(x^2) + eps) * gamma; gamma stored as 1 + w,
+  snowllm/models/qwen3_5/qwen3_5_weights.py:39-40), QKV projection, per-head QK RMSNorm and
+  rotate-half RoPE rounded once (tests/test_lfm2_dspark_reference.py:16-27), masked softmax
+  attention (tests/test_lfm2_long_attention.py:36-44), O projection, and either a SwiGLU MLP
+  or the Qwen-Next MoE (softmax over routed experts in fp32, top-k, renormalised, plus the
+  sigmoid-gated shared expert: transformers models/qwen3_next/modeling_qwen3_next.py).
+Weights are dequantized with oracle.quant from the raw GGUF bytes the GPU model was built from.
+"""
+import numpy as np
+import torch
+
+from oracle import quant as Q
+
+
+def bf(x):
+    return x.to(torch.bfloat16).float()
+
+
+def rmsnorm(x, gamma, eps):
+    return bf(x * torch.rsqrt(x.square().mean(-1, keepdim=True) + eps) * gamma.float())
+
+
+def rope(x, cos, sin, half):
+    """x [T, heads, D] fp32; rotates dims [0, 2*half) in (i, i + half) pairs."""
+    out = x.clone()
+    a, b = x[..., :half], x[..., half:2 * half]
+    c, s = cos[:, None, :], sin[:, None, :]
+    out[..., :half] = a * c - b * s
+    out[..., half:2 * half] = b * c + a * s
+    return out
+
+
+def dequant_raw(raw, fmt, n, k):
+    return torch.from_numpy(Q.dequant(raw.cpu().numpy(), fmt, n, k))
+
+
+def linear(x, w):
+    """bf16 output of x [T, K] @ w[N, K]^T computed in float64."""
+    return bf((x.double() @ w.double().T).float())
+
+
+class LayerRef:
+    """Dequantized weights of one layer (CPU)."""
+
+    def __init__(self, cfg, lw):
+        c = cfg
+        H = c.hidden
+        self.cfg = c
+        self.in_norm = lw.in_norm.cpu().float()
+        self.post_norm = lw.post_norm.cpu().float()
+        self.q_norm = lw.q_norm.cpu().float()
+        self.k_norm = lw.k_norm.cpu().float()
+        self.qkv = dequant_raw(lw.qkv[2], c.attn_fmt, c.qkv_n, H)
+        self.o = dequant_raw(lw.o[2], c.attn_fmt, H, c.heads * c.head_dim)
+        if c.moe:
+            E, F = c.experts, c.expert_ffn
+            self.router = lw.raw["router"].cpu().float()
+            self.gu = dequant_raw(lw.gu[2], c.ffn_fmt, E * 2 * F, H).view(E, 2 * F, H)
+            self.dn = dequant_raw(lw.dn[2], c.ffn_fmt, E * H, F).view(E, H, F)
+            self.sh_gu = dequant_raw(lw.sh_gu[2], c.ffn_fmt, 2 * F, H)
+            self.sh_dn = dequant_raw(lw.sh_dn[2], c.ffn_fmt, H, F)
+        else:
+            self.gu = dequant_raw(lw.gu[2], c.ffn_fmt, 2 * c.ffn, H)
+            self.dn = dequant_raw(lw.dn[2], c.ffn_fmt, H, c.ffn)
+
+
+def swiglu_ffn(x, gu, dn, F):
+    g = linear(x, gu[:F])
+    u = linear(x, gu[F:])
+    act = bf(g / (1 + torch.exp(-g)) * u)
+    return linear(act, dn)
+
+
+def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
+    """One layer. x: block input [T, H] (bf16 values), res: residual stream or None,
+    k_ctx/v_ctx: context keys/values [ctx, Hkv, D]; masks: per-row visibility bits over the
+    block. Returns (ffn output x', residual after the FFN update, attention output, routing)."""
+    c = ref.cfg
+    T = x.shape[0]
+    D, Hq, Hkv = c.head_dim, c.heads, c.kv_heads
+    r1 = x if res is None else bf(x + res)
+    h = rmsnorm(r1, ref.in_norm, c.eps)
+    proj = linear(h, ref.qkv)
+    q = proj[:, :Hq * D].view(T, Hq, D)
+    k = proj[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D)
+    v = proj[:, (Hq + Hkv) * D:].view(T, Hkv, D)
+
+    def head_norm(t, g):
+        return t * torch.rsqrt(t.square().mean(-1, keepdim=True) + c.eps) * g
+
+    q = bf(rope(head_norm(q, ref.q_norm), cos, sin, c.rot_half))
+    k = bf(rope(head_norm(k, ref.k_norm), cos, sin, c.rot_half))
+    keys = torch.cat([k_ctx.float(), k])
+    vals = torch.cat([v_ctx.float(), v])
+    ctx = k_ctx.shape[0]
+    L = ctx + T
+    vis = torch.zeros(T, L, dtype=torch.bool)
+    vis[:, :ctx] = True
+    for t in range(T):
+        for j in range(T):
+            if (masks[t] >> j) & 1:
+                vis[t, ctx + j] = True
+    G = Hq // Hkv
+    attn = torch.empty(T, Hq, D)
+    for hk in range(Hkv):
+        qs = q[:, hk * G:(hk + 1) * G].double()
+        s = torch.einsum("tgd,ld->tgl", qs, keys[:, hk].double()) * D ** -0.5
+        s = s.masked_fill(~vis[:, None, :], float("-inf"))
+        attn[:, hk * G:(hk + 1) * G] = torch.einsum("tgl,ld->tgd", s.softmax(-1), vals[:, hk].double()).float()
+    attn = bf(attn)
+    o = linear(attn.view(T, -1), ref.o)
+    r2 = bf(o + r1)
+    h2 = rmsnorm(r2, ref.post_norm, c.eps)
+    routing = None
+    if c.moe:
+        E, F, K = c.experts, c.expert_ffn, c.topk
+        logits = (h2.double() @ ref.router.double().T).float()
+        probs = torch.softmax(logits[:, :E], -1)
+        w, ids = torch.topk(probs, K, dim=-1)
+        w = w / w.sum(-1, keepdim=True)
+        out = torch.zeros(T, c.hidden)
+        for t in range(T):
+            acc = torch.zeros(c.hidden)
+            for kk in range(K):
+                e = int(ids[t, kk])
+                y = swiglu_ffn(h2[t:t + 1], ref.gu[e], ref.dn[e], F)[0]
+                acc += y * w[t, kk]
+            sh = swiglu_ffn(h2[t:t + 1], ref.sh_gu, ref.sh_dn, F)[0]
+            acc += sh * torch.sigmoid(logits[t, E])
+            out[t] = acc
+        x2 = bf(out)
+        routing = ids
+    else:
+        x2 = swiglu_ffn(h2, ref.gu, ref.dn, c.ffn)
+    return x2, r2, attn, routing
+
+
+def rope_tables(positions, inv_freq):
+    """cos/sin of pos * inv_freq with the angle rounded to fp32 (as the tables are built)."""
+    ang = positions.float()[:, None] * inv_freq.float()[None, :]
+    return torch.cos(ang.double()).float(), torch.sin(ang.double()).float()
+
+
+def head_reference(x, res, final_norm, lm_head, eps):
+    """Final norm + fp16 LM head -> f32 logits [T, V]."""
+    r = bf(x + res)
+    h = rmsnorm(r, final_norm.float(), eps)
+    return (h.double() @ lm_head.double().T).float()

@@ -85,6 +85,34 @@ _SIGS = [
     # paged attention
     ("snowverify_paged_attention_scratch_bytes", c_int64, [c_int64] * 5),
     ("snowverify_paged_attention", c_int, [P] * 7 + [c_int64] * 7 + [c_float, P, c_int64, S]),
+    # geometry and layer plumbing
+    ("snowllm_model_config", None, [P]),
+    ("snowllm_select_geometry", c_int, [c_int]),
+    ("snowllm_active_geometry", c_int, []),
+    ("snowllm_geometry_name", c_int64, [c_int, c_char_p, c_int64]),
+    ("snowverify_define_geometry", c_int, [P]),
+    ("snowverify_gather_embedding", c_int, [P, P, P, c_int64, c_int64, c_int64, c_int, S]),
+    ("snowllm_gather_embedding", c_int, [P, P, P, c_int64, S]),
+    ("snowverify_rmsnorm", c_int, [P, P, P, P, c_int64, c_int64, c_float, S]),
+    ("snowllm_rmsnorm", c_int, [P, P, P, c_int64, c_float, S]),
+    ("snowllm_rmsnorm_residual", c_int, [P, P, P, P, c_int64, c_float, S]),
+    ("snowverify_rope_cos_sin", c_int, [P, P, P, P, c_int64, c_int64, S]),
+    ("snowverify_qk_norm_rope_cache", c_int, [P, c_int64, P, P, P, P, P, P, P, P] + [c_int64] * 6
+     + [c_float, S]),
+    ("snowllm_resolve_slots", c_int, [P, c_int64, P, P, P, c_int64, c_int64, S]),
+    ("snowllm_kv_pool_bytes", None, [c_int64, c_int64, c_int, P, P]),
+    ("snowverify_swiglu", c_int, [P, c_int64, P, c_int64, c_int64, S]),
+    ("snowverify_add_bf16", c_int, [P, P, P, c_int64, S]),
+    ("snowverify_moe_route", c_int, [P, c_int64, c_int64, c_int64, c_int64, P, P, P, S]),
+    # feed-forward
+    ("snowverify_norm_prep", c_int, [P, P, P, P, P, P, c_int64, c_int64, c_float, S]),
+    ("snowverify_dense_bytes", c_int64, [c_int64, c_int64]),
+    ("snowverify_dense_shuffle", c_int, [P, P, c_int64, c_int64, c_int, S]),
+    ("snowverify_dense_gemv", c_int, [c_int, P, P, P, c_int64, c_int64, c_int64, c_int, S]),
+    ("snowverify_gate_up_swiglu", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, S]),
+    ("snowverify_moe_plan_bytes", c_int64, []),
+    ("snowverify_moe_plan", c_int, [P, c_int64, c_int64, c_int64, c_int, P, S]),
+    ("snowverify_moe_experts", c_int, [c_int] + [P] * 16 + [c_int64] * 5 + [S]),
 ]
 
 _missing = []

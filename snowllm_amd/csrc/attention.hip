@@ -167,10 +167,17 @@ __global__ void __launch_bounds__(64) attn_split_kernel(AttnArgs a) {
     m = m_new;
 #pragma unroll
     for (int i = 0; i < DT; ++i) o[i] *= alpha;
-    // P^T operand: slots 0..3 page 0 keys 4kq+i, slots 4..7 page 1 keys 4kq+i
+    // P^T operand: slots 0..3 page 0 keys 4kq+i, slots 4..7 page 1 keys 4kq+i. P is carried
+    // as a bf16 pair (hi + lo residual), which keeps ~16 significant bits through the MFMA.
+    float plo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) plo[i] = p[i] - bf16_to_f32(f32_to_bf16(p[i]));
     u32x4 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                 pack_bf16x2(p[6], p[7])};
+    u32x4 pwl = {pack_bf16x2(plo[0], plo[1]), pack_bf16x2(plo[2], plo[3]),
+                 pack_bf16x2(plo[4], plo[5]), pack_bf16x2(plo[6], plo[7])};
     const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+    const bf16x8 pbl = __builtin_bit_cast(bf16x8, pwl);
     // O^T += V^T P^T ; V layout [4 key groups][D][4 keys]: keys 4kq..4kq+3 of d -> 8 bytes
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -180,8 +187,9 @@ __global__ void __launch_bounds__(64) attn_split_kernel(AttnArgs a) {
       u32x2 vb = *(const u32x2*)(v1 + off);
       if (!has2) vb = u32x2{0u, 0u};
       u32x4 vv = {va.x, va.y, vb.x, vb.y};
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb, o[dt],
-                                                      0, 0, 0);
+      const bf16x8 vt = __builtin_bit_cast(bf16x8, vv);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pb, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pbl, o[dt], 0, 0, 0);
     }
   }
   // partial results: O^T lane holds row col, d = dt*16 + 4*kq + i

@@ -1,0 +1,377 @@
+// Shared device code of the k-quant GEMV family (plain GEMV, fused gate/up + SwiGLU, MoE
+// experts): operand workspace layout, activation conversion, nibble/byte decoders, the
+// per-superblock MFMA tile and the double-buffered superblock loop.
+//
+// Arithmetic (per 32-weight sub-block j, column n, row r):
+//   y[r,n] = sum_j  a_j * sum_i q_i x_ri  - mn_j * sum_i x_ri
+// Quants are turned into exact fp16 values with the 1024-offset trick (0x6400 | q == 1024+q;
+// a high nibble left in bits 4..7 reads as 1024+16q), multiplied against fp16 activations on
+// v_mfma_f32_16x16x32_f16 (K = 32 = one sub-block), and the sub-block result is scaled by
+// a_j in fp32. The offset and min terms are one rank-8 product per superblock, done on
+// v_mfma_f32_16x16x4_f32 with the sub-block sums of the activations. Activations are
+// converted to fp16 with a power-of-two scale per (row, superblock): exact for bf16 input.
+#pragma once
+#include "common.h"
+
+namespace kq {
+
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int FMT_Q4_K = 4;
+constexpr int FMT_Q8_0 = 8;
+constexpr int QK = 256;          // weights per superblock
+constexpr int TILE_N = 16;       // columns per MFMA tile
+constexpr int TILE_M = 16;       // rows per MFMA tile
+
+// Activation workspace (ws) for one 16-row tile and S superblocks. Each (row, superblock) has its
+// own power-of-two scale so that the fp16 operands are exact for any bf16 input.
+struct XPrepView {
+  u32x4* xop;     // [S][8][64] fp16 A operands (8 halves per lane)
+  float* sxop;    // [S][2][64] negated sub-block sums, f32 MFMA A operand
+  float* scale;   // [S][16] 2^e per (superblock, row): undoes the operand scaling
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+inline size_t xprep_tile_bytes(int64_t S) {
+  return align256((size_t)S * 8 * 64 * 16) + align256((size_t)S * 2 * 64 * 4) +
+         align256((size_t)S * 16 * 4);
+}
+
+__host__ __device__ inline XPrepView xprep_view(void* base, int64_t S) {
+  XPrepView v;
+  char* p = (char*)base;
+  v.xop = (u32x4*)p;
+  p += ((size_t)S * 8 * 64 * 16 + 255) & ~(size_t)255;
+  v.sxop = (float*)p;
+  p += ((size_t)S * 2 * 64 * 4 + 255) & ~(size_t)255;
+  v.scale = (float*)p;
+  return v;
+}
+
+// Slot e of a lane's 8 fp16 operand values holds k-offset kperm(e) within its 8-wide k range:
+// 0, 2, 1, 3, 4, 6, 5, 7 -- the order in which the nibble/byte decoders below emit weights.
+__host__ __device__ constexpr int kperm_c(int e) { return (e & 4) | ((e & 1) << 1) | ((e >> 1) & 1); }
+
+// ---------------------------------------------------------------------------------------
+// Activation conversion for one (16-row tile, superblock): lane (row = lane & 15,
+// kq = lane >> 4) owns k = 32 j + 8 kq + kperm(0..7) of every sub-block j. `src` points at
+// the tile's first row; rows >= rows_valid read as zero.
+// ---------------------------------------------------------------------------------------
+struct XOperands {
+  u32x4 x[8];      // fp16 A operands of the 8 sub-blocks
+  float sx0, sx1;  // negated sub-block sums (f32 MFMA A operand: row lane&15, k = lane>>4)
+  float scale;     // 2^e of this lane's row
+};
+
+__device__ __forceinline__ void convert_superblock(const uint16_t* __restrict__ src,
+                                                   int64_t row_stride, int rows_valid, int s,
+                                                   int lane, XOperands& o) {
+  const int r = lane & 15, kq = lane >> 4;
+  const bool live = r < rows_valid;
+  u32x4 raw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    raw[j] = live ? *(const u32x4*)(src + r * row_stride + (int64_t)s * QK + j * 32 + kq * 8)
+                  : u32x4{0u, 0u, 0u, 0u};
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mx = fmaxf(mx, __builtin_fabsf(__uint_as_float(w4[i] << 16)));
+      mx = fmaxf(mx, __builtin_fabsf(__uint_as_float(w4[i] & 0xffff0000u)));
+    }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.40282346638528859812e38f) {
+    int E = (int)((__float_as_uint(mx) >> 23) & 0xff) - 127;
+    if (E < -126) E = -126;
+    e = E - 14;  // scaled maximum lands in [2^14, 2^15)
+  }
+  float part[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(w4[i] << 16);
+      f[2 * i + 1] = __uint_as_float(w4[i] & 0xffff0000u);
+    }
+    uint16_t h[8];
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      _Float16 hv = (_Float16)__builtin_ldexpf(f[kperm_c(t)], -e);
+      h[t] = __builtin_bit_cast(uint16_t, hv);
+      sum += (float)hv;
+    }
+    part[j] = sum;
+    o.x[j] = u32x4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                   h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
+  }
+  // full sub-block sums: add the four kq lanes of the row (fixed order)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    part[j] += __shfl_xor(part[j], 16, 64);
+    part[j] += __shfl_xor(part[j], 32, 64);
+  }
+  o.sx0 = -part[kq];
+  o.sx1 = -part[4 + kq];
+  o.scale = __builtin_ldexpf(1.0f, e);
+}
+
+// ---------------------------------------------------------------------------------------
+// Decoders: packed words -> fp16 MFMA B operands (slot order kperm).
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ half8 as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  u32x4 v = {a, b, c, d};
+  return __builtin_bit_cast(half8, v);
+}
+
+// (w & mask) | orv in one VALU op. GFX9 VOP3 may read one scalar register, so the OR constant
+// is passed in a vector register (materialised once, outside the loops).
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t orv) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(orv));
+  return r;
+}
+
+// Q4_K group (two dwords = 8 bytes of one 32-byte nibble group): low nibbles -> sub-block 2g
+// as 1024+q, high nibbles -> sub-block 2g+1 as 1024+16q. 10 VALU ops for 16 weights.
+__device__ __forceinline__ void q4_group(uint32_t wa, uint32_t wb, uint32_t M, half8& lo,
+                                         half8& hi) {
+  const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+  lo = as_half8(and_or(wa, 0x000f000fu, M), and_or(wa8, 0x000f000fu, M),
+                and_or(wb, 0x000f000fu, M), and_or(wb8, 0x000f000fu, M));
+  hi = as_half8(and_or(wa, 0x00f000f0u, M), and_or(wa8, 0x00f000f0u, M),
+                and_or(wb, 0x00f000f0u, M), and_or(wb8, 0x00f000f0u, M));
+}
+
+// Q8_0 sub-block (two dwords = 8 int8): 1024 + (q + 128), byte-permuted next to the 0x64
+// exponent byte (v_perm_b32: result bytes (w.b0, 0x64, w.b2, 0x64) and (w.b1, .., w.b3, ..)).
+__device__ __forceinline__ half8 q8_sub(uint32_t wa, uint32_t wb, uint32_t M8) {
+  wa ^= 0x80808080u;
+  wb ^= 0x80808080u;
+  return as_half8(__builtin_amdgcn_perm(M8, wa, 0x04020400u), __builtin_amdgcn_perm(M8, wa, 0x04030401u),
+                  __builtin_amdgcn_perm(M8, wb, 0x04020400u), __builtin_amdgcn_perm(M8, wb, 0x04030401u));
+}
+
+__device__ __forceinline__ float byte_f(uint32_t w, int i) {
+  return (float)((w >> (8 * i)) & 0xffu);
+}
+
+// One 16-column x 256-weight tile. Returns the superblock's contribution in the C layout
+// (column lane & 15, rows 4*(lane >> 4) + i), still in units of the operand scaling.
+// xa: A operands of the 8 sub-blocks, sx0/sx1: negated sub-block sums (f32 MFMA A operand).
+template <int FMT>
+__device__ __forceinline__ floatx4 tile_superblock(const u32x4* qv, u32x4 meta, const half8* xa,
+                                                   float sx0, float sx1, int kq, uint32_t M) {
+  const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+  floatx4 acc = zero;
+  float a[8];
+  float beta_lo, beta_hi;  // beta for sub-blocks kq and kq + 4
+  if constexpr (FMT == FMT_Q4_K) {
+    const float d = f16_to_f32((uint16_t)(meta.x & 0xffff));
+    const float dmin = f16_to_f32((uint16_t)(meta.x >> 16));
+    const uint32_t s0 = meta.y, s1 = meta.z, s2 = meta.w;
+    const uint32_t sc03 = s0 & 0x3f3f3f3fu;
+    const uint32_t m03 = s1 & 0x3f3f3f3fu;
+    const uint32_t sc47 = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t m47 = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = d * byte_f(sc03, i);
+      a[4 + i] = d * byte_f(sc47, i);
+    }
+    const float m_lo = dmin * byte_f(m03, kq);
+    const float m_hi = dmin * byte_f(m47, kq);
+    // even sub-blocks carry the 1024 offset; odd ones read 1024 + 16 q, i.e. 64 after the 1/16
+    const float off = (kq & 1) ? 64.0f : 1024.0f;
+    beta_lo = __builtin_fmaf(off, d * byte_f(sc03, kq), m_lo);  // a[kq] without a select chain
+    beta_hi = __builtin_fmaf(off, d * byte_f(sc47, kq), m_hi);
+    const u32x4 q0 = qv[0], q1 = qv[1];
+    half8 lo, hi;
+    floatx4 c;
+    q4_group(q0.x, q0.y, M, lo, hi);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0], lo, zero, 0, 0, 0);
+    acc += a[0] * c;
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1], hi, zero, 0, 0, 0);
+    acc += (a[1] * 0.0625f) * c;
+    q4_group(q0.z, q0.w, M, lo, hi);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2], lo, zero, 0, 0, 0);
+    acc += a[2] * c;
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[3], hi, zero, 0, 0, 0);
+    acc += (a[3] * 0.0625f) * c;
+    q4_group(q1.x, q1.y, M, lo, hi);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[4], lo, zero, 0, 0, 0);
+    acc += a[4] * c;
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[5], hi, zero, 0, 0, 0);
+    acc += (a[5] * 0.0625f) * c;
+    q4_group(q1.z, q1.w, M, lo, hi);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[6], lo, zero, 0, 0, 0);
+    acc += a[6] * c;
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[7], hi, zero, 0, 0, 0);
+    acc += (a[7] * 0.0625f) * c;
+  } else {
+    const uint32_t dw[4] = {meta.x, meta.y, meta.z, meta.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[2 * i] = f16_to_f32((uint16_t)(dw[i] & 0xffff));
+      a[2 * i + 1] = f16_to_f32((uint16_t)(dw[i] >> 16));
+    }
+    // a[kq], a[4 + kq] read straight from the packed scales (no select chain on kq)
+    beta_lo = 1152.0f * f16_to_f32((uint16_t)(((kq & 1) ? (dw[kq >> 1] >> 16) : dw[kq >> 1]) & 0xffff));
+    beta_hi = 1152.0f * f16_to_f32((uint16_t)(((kq & 1) ? (dw[2 + (kq >> 1)] >> 16) : dw[2 + (kq >> 1)]) & 0xffff));
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {
+      const u32x4 q = qv[jp];
+      floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * jp], q8_sub(q.x, q.y, M), zero, 0,
+                                                          0, 0);
+      acc += a[2 * jp] * c;
+      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2 * jp + 1], q8_sub(q.z, q.w, M), zero, 0, 0, 0);
+      acc += a[2 * jp + 1] * c;
+    }
+  }
+  // offset/min term: acc += (-Sx) * beta over the 8 sub-blocks (k = lane >> 4 in each half)
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sx0, beta_lo, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sx1, beta_hi, acc, 0, 0, 0);
+  return acc;
+}
+
+template <int FMT>
+struct QLayout {
+  static constexpr int kQuantVecs = FMT == FMT_Q4_K ? 2 : 4;  // u32x4 per lane per superblock
+};
+
+// Per-wave operands of one superblock for NTILE column tiles.
+template <int FMT, int NTILE>
+struct SbOperands {
+  u32x4 x[8];
+  float sx0, sx1;
+  floatx4 scale;  // 2^e of rows 4*(lane>>4) + 0..3
+  u32x4 q[NTILE][QLayout<FMT>::kQuantVecs];
+  u32x4 m[NTILE];
+};
+
+__device__ __forceinline__ u32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ float bload1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+// Buffer resources and per-lane byte offsets of the streams one wave reads.
+struct GemvStreams {
+  __amdgpu_buffer_rsrc_t quant, meta, xop, sxop, scale;
+  uint32_t v_quant, v_meta, v_xop, v_sx, v_scale;  // per-lane byte offsets
+};
+
+// Load the weights of superblock s for tiles tile0 + t * tstride (t < NTILE) and, when
+// WITH_X, its activation operands from the workspace.
+template <int FMT, int NTILE, bool WITH_X = true>
+__device__ __forceinline__ void load_sb(SbOperands<FMT, NTILE>& o, const GemvStreams& st, int s,
+                                        int S, int tile0, int tstride = 1) {
+  constexpr int QV = QLayout<FMT>::kQuantVecs;
+  if constexpr (WITH_X) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o.x[j] = bload4(st.xop, st.v_xop, (uint32_t)((s * 8 + j) * 64 * 16));
+    o.sx0 = bload1(st.sxop, st.v_sx, (uint32_t)((s * 2 + 0) * 64 * 4));
+    o.sx1 = bload1(st.sxop, st.v_sx, (uint32_t)((s * 2 + 1) * 64 * 4));
+    o.scale = __builtin_bit_cast(floatx4, bload4(st.scale, st.v_scale, (uint32_t)(s * 16 * 4)));
+  }
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) {
+    const uint32_t ts = (uint32_t)((tile0 + t * tstride) * S + s);
+#pragma unroll
+    for (int i = 0; i < QV; ++i) o.q[t][i] = bload4(st.quant, st.v_quant, (ts * QV + i) * 64 * 16);
+    o.m[t] = bload4(st.meta, st.v_meta, ts * 16 * 16);
+  }
+}
+
+// Multiply one superblock's operands into acc.
+template <int FMT, int NTILE>
+__device__ __forceinline__ void gemv_superblock(const SbOperands<FMT, NTILE>& o, floatx4* acc,
+                                                int kq, uint32_t Mv) {
+  half8 xa[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, o.x[j]);
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) {
+    floatx4 sb = tile_superblock<FMT>(o.q[t], o.m[t], xa, o.sx0, o.sx1, kq, Mv);
+    acc[t] += sb * o.scale;
+  }
+}
+
+
+// Streams of a k-quant weight (`tiles` column tiles x S superblocks) and of the activation
+// workspace. Lanes whose row is >= rows read activations at an out-of-range offset: the buffer
+// unit returns zeros without touching memory.
+template <int FMT>
+__device__ __forceinline__ GemvStreams make_streams(const void* quant, const void* meta,
+                                                    const void* ws, int tiles, int S, int lane,
+                                                    int rows) {
+  constexpr int QV = QLayout<FMT>::kQuantVecs;
+  const int kq = lane >> 4, r = lane & 15;
+  XPrepView xv = xprep_view((void*)ws, S);
+  GemvStreams st;
+  st.quant = __builtin_amdgcn_make_buffer_rsrc((void*)quant, 0, tiles * S * QV * 64 * 16, 0x00020000);
+  st.meta = __builtin_amdgcn_make_buffer_rsrc((void*)meta, 0, tiles * S * 16 * 16, 0x00020000);
+  st.xop = __builtin_amdgcn_make_buffer_rsrc((void*)xv.xop, 0, S * 8 * 64 * 16, 0x00020000);
+  st.sxop = __builtin_amdgcn_make_buffer_rsrc((void*)xv.sxop, 0, S * 2 * 64 * 4, 0x00020000);
+  st.scale = __builtin_amdgcn_make_buffer_rsrc((void*)xv.scale, 0, S * 16 * 4, 0x00020000);
+  st.v_quant = lane * 16;
+  st.v_meta = r * 16;
+  st.v_xop = r < rows ? lane * 16 : 0x80000000u;
+  st.v_sx = lane * 4;
+  st.v_scale = kq * 16;
+  return st;
+}
+
+// The decoders' 0x6400 exponent pattern, kept in a vector register.
+template <int FMT>
+__device__ __forceinline__ uint32_t decode_magic() {
+  const uint32_t Mc = __builtin_amdgcn_readfirstlane(FMT == FMT_Q4_K ? 0x64006400u : 0x64646464u);
+  uint32_t Mv;
+  asm("v_mov_b32 %0, %1" : "=v"(Mv) : "s"(Mc));
+  return Mv;
+}
+
+// Wave w of NW walks superblocks s = w, w + NW, ... of the tiles tile0 + t * tstride, with the
+// next superblock's operands in flight while the current one is multiplied.
+template <int FMT, int NTILE, int NW>
+__device__ __forceinline__ void gemv_loop(const GemvStreams& st, int w, int S, int tile0,
+                                          int tstride, int kq, uint32_t Mv, floatx4* acc) {
+  if (w >= S) return;
+  SbOperands<FMT, NTILE> bufA, bufB;
+  load_sb<FMT, NTILE>(bufA, st, w, S, tile0, tstride);
+  for (int s = w;;) {
+    if (s + NW < S) load_sb<FMT, NTILE>(bufB, st, s + NW, S, tile0, tstride);
+    gemv_superblock<FMT, NTILE>(bufA, acc, kq, Mv);
+    s += NW;
+    if (s >= S) break;
+    if (s + NW < S) load_sb<FMT, NTILE>(bufA, st, s + NW, S, tile0, tstride);
+    gemv_superblock<FMT, NTILE>(bufB, acc, kq, Mv);
+    s += NW;
+    if (s >= S) break;
+  }
+}
+
+// Sum the NW waves' accumulators in a fixed order; threads < NTILE*64 get tile t = idx >> 6,
+// lane l = idx & 63 (C layout: column l & 15, rows 4*(l >> 4) + i).
+template <int NTILE, int NW>
+__device__ __forceinline__ void combine_waves(floatx4 (*part)[NTILE][64], const floatx4* acc,
+                                              int w, int lane) {
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) part[w][t][lane] = acc[t];
+  __syncthreads();
+}
+
+}  // namespace kq

@@ -1,0 +1,470 @@
+// Per-layer plumbing of the verify step around the GEMVs and attention: model geometry,
+// embedding gather, RMSNorm (+ residual), RoPE tables, QK-norm + RoPE + paged KV write, slot
+// resolution, SwiGLU, MoE routing and residual adds.
+//
+// The reference compiles its model shapes into the library and selects one with
+// snowllm_select_geometry (snowllm/_capi.py:44-113). Here shapes are run-time data: the same
+// selection call works for the shapes this build is measured on, and snowverify_define_geometry
+// installs any other. Entry points with the reference's signatures read the current geometry;
+// the snowverify_* forms take every shape explicitly.
+#include "common.h"
+
+#include <string.h>
+
+// Field order of the reference's BuildGeometry (snowllm/_capi.py:44-64).
+struct BuildGeometry {
+  int64_t hidden, num_heads, num_kv_heads, head_size, block_size, vocab_size;
+  int64_t qkv_proj_n, qkv_q_head_stride, qkv_off_scale, qkv_off_k, qkv_off_v;
+  int64_t lin_num_k_heads, lin_num_v_heads, lin_head_k, lin_head_v, lin_key_dim;
+  int64_t lin_value_dim, lin_conv_dim, lin_conv_k, lin_conv_state, lin_in_proj_n;
+  int64_t lin_in_proj_n_pad;
+  int64_t lin_in_proj_ba_n_pad, lin_off_qkv, lin_off_z, lin_off_b, lin_off_a;
+  int64_t moe_num_experts, moe_shared_expert, moe_num_slabs, moe_topk, moe_topk_all;
+  int64_t moe_inter, sampling_max_k, lm_head_decode_max_m, mlp_inter;
+  int64_t mlp_gate_up_n;
+};
+static_assert(sizeof(BuildGeometry) == 37 * 8, "BuildGeometry layout");
+
+namespace {
+
+constexpr int GEO_QWEN36_35B_A3B = 0;  // reference id; BASELINE configs 4 and 5
+constexpr int GEO_DENSE_8B = 100;      // this build's id for BASELINE config 3
+constexpr int GEO_CUSTOM = 1000;       // installed by snowverify_define_geometry
+
+BuildGeometry make_moe_35b() {
+  BuildGeometry g;
+  memset(&g, 0, sizeof g);
+  g.hidden = 2048; g.num_heads = 16; g.num_kv_heads = 2; g.head_size = 256; g.block_size = 16;
+  g.vocab_size = 151936;
+  g.qkv_proj_n = (16 + 2 + 2) * 256; g.qkv_q_head_stride = 256;
+  g.qkv_off_k = 16 * 256; g.qkv_off_v = 18 * 256;
+  g.moe_num_experts = 256; g.moe_shared_expert = 1; g.moe_topk = 8; g.moe_topk_all = 9;
+  g.moe_inter = 512; g.sampling_max_k = 1 << 19; g.lm_head_decode_max_m = 256;
+  return g;
+}
+
+BuildGeometry make_dense_8b() {
+  BuildGeometry g;
+  memset(&g, 0, sizeof g);
+  g.hidden = 4096; g.num_heads = 32; g.num_kv_heads = 8; g.head_size = 128; g.block_size = 16;
+  g.vocab_size = 151936;
+  g.qkv_proj_n = (32 + 8 + 8) * 128; g.qkv_q_head_stride = 128;
+  g.qkv_off_k = 32 * 128; g.qkv_off_v = 40 * 128;
+  g.sampling_max_k = 1 << 19; g.lm_head_decode_max_m = 256;
+  g.mlp_inter = 14336; g.mlp_gate_up_n = 2 * 14336;
+  return g;
+}
+
+BuildGeometry g_geo = make_moe_35b();
+int g_geo_id = GEO_QWEN36_35B_A3B;
+
+inline hipStream_t S(void* s) { return (hipStream_t)s; }
+
+// ---------------------------------------------------------------------------------------
+// embedding gather: out[m, :] = table[ids[m], :] (fp16 or bf16 table) -> bf16
+// ---------------------------------------------------------------------------------------
+__global__ void gather_embedding_kernel(const int64_t* __restrict__ ids,
+                                        const uint16_t* __restrict__ table,
+                                        uint16_t* __restrict__ out, int64_t V, int64_t H,
+                                        int table_f16) {
+  const int64_t m = blockIdx.x;
+  int64_t id = ids[m];
+  if (id < 0 || id >= V) id = 0;
+  const uint16_t* row = table + id * H;
+  for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
+    const uint16_t v = row[i];
+    out[m * H + i] = table_f16 ? f32_to_bf16(f16_to_f32(v)) : v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// RMSNorm: y = x * rsqrt(mean(x^2) + eps) * gamma, fp32 math, bf16 out. With a residual,
+// the residual stream is updated first (residual = x + residual, rounded to bf16) and
+// normalised. One 256-thread block per row.
+// ---------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      uint16_t* __restrict__ residual,
+                                                      const uint16_t* __restrict__ gamma,
+                                                      uint16_t* __restrict__ out, int64_t H,
+                                                      float eps) {
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  const uint16_t* xr = x + m * H;
+  uint16_t* rr = residual ? residual + m * H : nullptr;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < H; i += 256) {
+    float v = bf16_to_f32(xr[i]);
+    if (rr) {
+      v = bf16_to_f32(f32_to_bf16(v + bf16_to_f32(rr[i])));
+      rr[i] = f32_to_bf16(v);
+    }
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = __frsqrt_rn(tot / (float)H + eps);
+  const uint16_t* src = rr ? rr : xr;
+  for (int64_t i = threadIdx.x; i < H; i += 256)
+    out[m * H + i] = f32_to_bf16(bf16_to_f32(src[i]) * inv * bf16_to_f32(gamma[i]));
+}
+
+// ---------------------------------------------------------------------------------------
+// RoPE tables: cos/sin[m, i] = cos/sin(pos[m] * inv_freq[i]), i < half (f32)
+// ---------------------------------------------------------------------------------------
+__global__ void rope_cos_sin_kernel(const int64_t* __restrict__ pos,
+                                    const float* __restrict__ inv_freq, float* __restrict__ c,
+                                    float* __restrict__ s, int64_t M, int half) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * half) return;
+  const int64_t m = idx / half;
+  const int i = (int)(idx % half);
+  const float a = (float)pos[m] * inv_freq[i];
+  c[idx] = cosf(a);
+  s[idx] = sinf(a);
+}
+
+// ---------------------------------------------------------------------------------------
+// QK-norm + RoPE + paged KV write. proj row m = [q heads | k heads | v heads] (bf16, head
+// size D, row stride `stride`). Per head: RMSNorm over D with its gamma (fp32), rotate the first
+// 2*half dims (pairs (i, i + half)), round once to bf16 (tests/test_lfm2_dspark_reference.py:
+// 22-27 order). q goes to q_out [M, Hq, D]; k and v go to the pools at slots[m] in the layouts
+// K [blocks, Hkv, D/16, page, 16] and V [blocks, Hkv, page/4, D, 4].
+// One wave per (row, head); heads >= Hq + Hkv copy v.
+// ---------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(64) qk_norm_rope_cache_kernel(
+    const uint16_t* __restrict__ proj, int64_t stride, const uint16_t* __restrict__ q_gamma,
+    const uint16_t* __restrict__ k_gamma, const float* __restrict__ cosv,
+    const float* __restrict__ sinv, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool,
+    uint16_t* __restrict__ v_pool, const int32_t* __restrict__ slots, int Hq, int Hkv, int D,
+    int half, int page, float eps) {
+  const int64_t m = blockIdx.y;
+  const int head = blockIdx.x;
+  const int lane = threadIdx.x;
+  const uint16_t* src = proj + m * stride + (int64_t)head * D;
+  const int slot = slots[m];
+  const int blk = slot / page, off = slot % page;
+  if (head >= Hq + Hkv) {  // v
+    const int h = head - Hq - Hkv;
+    for (int d = lane; d < D; d += 64) {
+      if (slot < 0) break;
+      // V [blocks, Hkv, page/4, D, 4]
+      const int64_t idx = ((((int64_t)blk * Hkv + h) * (page / 4) + off / 4) * D + d) * 4 + off % 4;
+      v_pool[idx] = src[d];
+    }
+    return;
+  }
+  const bool is_q = head < Hq;
+  const uint16_t* gamma = is_q ? q_gamma : k_gamma;
+  // D <= 256: each lane holds up to 4 values
+  float v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int d = lane + 64 * j;
+    v[j] = d < D ? bf16_to_f32(src[d]) : 0.f;
+    ss = __builtin_fmaf(v[j], v[j], ss);
+  }
+  ss = wave_sum(ss);
+  const float inv = __frsqrt_rn(ss / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) v[j] = v[j] * inv * bf16_to_f32(gamma[d]);
+  }
+  // rotate: partner of d < half is d + half and vice versa. Exchange through LDS.
+  __shared__ float buf[256];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) buf[d] = v[j];
+  }
+  __syncthreads();
+  const float* cr = cosv + m * half;
+  const float* sr = sinv + m * half;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int d = lane + 64 * j;
+    if (d >= D) continue;
+    float y = v[j];
+    if (d < half) y = v[j] * cr[d] - buf[d + half] * sr[d];
+    else if (d < 2 * half) y = v[j] * cr[d - half] + buf[d - half] * sr[d - half];
+    const uint16_t o = f32_to_bf16(y);
+    if (is_q) {
+      q_out[(m * Hq + head) * D + d] = o;
+    } else if (slot >= 0) {
+      const int h = head - Hq;
+      // K [blocks, Hkv, D/16, page, 16]
+      const int64_t idx = ((((int64_t)blk * Hkv + h) * (D / 16) + d / 16) * page + off) * 16 + d % 16;
+      k_pool[idx] = o;
+    }
+  }
+}
+
+// slot = table[row_seq, pos / page] * page + pos % page (snowllm/engine/spec_decode.py:183)
+__global__ void resolve_slots_kernel(const int32_t* __restrict__ table, int64_t stride,
+                                     const int32_t* __restrict__ seq, const int32_t* __restrict__ pos,
+                                     int32_t* __restrict__ out, int64_t M, int64_t page) {
+  const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (m >= M) return;
+  const int32_t p = pos[m];
+  const int64_t col = p / page;
+  out[m] = (col < stride) ? (int32_t)(table[seq[m] * stride + col] * page + p % page) : -1;
+}
+
+// SwiGLU: out[m, i] = silu(gu[m, i]) * gu[m, F + i] (bf16)
+__global__ void swiglu_kernel(const uint16_t* __restrict__ gu, int64_t stride,
+                              uint16_t* __restrict__ out, int64_t M, int64_t F) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * F) return;
+  const int64_t m = idx / F, i = idx % F;
+  const float g = bf16_to_f32(gu[m * stride + i]);
+  const float u = bf16_to_f32(gu[m * stride + F + i]);
+  const float s = g / (1.0f + __expf(-g));
+  out[idx] = f32_to_bf16(s * u);
+}
+
+// out = a + b (bf16, fp32 add, one rounding)
+__global__ void add_bf16_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                                uint16_t* __restrict__ out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = f32_to_bf16(bf16_to_f32(a[i]) + bf16_to_f32(b[i]));
+}
+
+// ---------------------------------------------------------------------------------------
+// MoE routing (transformers qwen3_next semantics): softmax over the E routed logits in fp32,
+// top-k (ties to the lower expert id), renormalised; the logit in column E is the shared
+// expert's gate, applied as sigmoid. One wave per row.
+// ---------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(64) moe_route_kernel(const float* __restrict__ logits,
+                                                       int64_t stride, int E, int topk,
+                                                       float* __restrict__ weights,
+                                                       int32_t* __restrict__ ids,
+                                                       float* __restrict__ shared_w) {
+  const int64_t m = blockIdx.x;
+  const float* l = logits + m * stride;
+  const int lane = threadIdx.x;
+  // softmax statistics
+  float mx = -__builtin_huge_valf();
+  for (int e = lane; e < E; e += 64) mx = fmaxf(mx, l[e]);
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int e = lane; e < E; e += 64) sum += __expf(l[e] - mx);
+  sum = wave_sum(sum);
+  // top-k by repeated arg-max over (value, lower id)
+  float chosen_p[16];
+  int chosen_id[16];
+  uint64_t taken_lo = 0, taken_hi = 0, taken2 = 0, taken3 = 0;  // up to 256 experts
+  float ksum = 0.f;
+  for (int k = 0; k < topk; ++k) {
+    uint64_t best = 0;
+    for (int e = lane; e < E; e += 64) {
+      const int w = e >> 6;
+      const uint64_t tk = w == 0 ? taken_lo : w == 1 ? taken_hi : w == 2 ? taken2 : taken3;
+      if ((tk >> (e & 63)) & 1ull) continue;
+      const uint64_t key = argmax_key(l[e], (uint32_t)e);
+      best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    const int e = (int)argmax_key_index(best);
+    const int w = e >> 6;
+    if (w == 0) taken_lo |= 1ull << (e & 63);
+    else if (w == 1) taken_hi |= 1ull << (e & 63);
+    else if (w == 2) taken2 |= 1ull << (e & 63);
+    else taken3 |= 1ull << (e & 63);
+    const float p = __expf(l[e] - mx) / sum;
+    chosen_p[k] = p;
+    chosen_id[k] = e;
+    ksum += p;
+  }
+  if (lane == 0) {
+    for (int k = 0; k < topk; ++k) {
+      weights[m * topk + k] = chosen_p[k] / ksum;
+      ids[m * topk + k] = chosen_id[k];
+    }
+    if (shared_w) shared_w[m] = 1.0f / (1.0f + __expf(-l[E]));
+  }
+}
+
+}  // namespace
+
+// =======================================================================================
+// geometry
+// =======================================================================================
+
+SV_API void snowllm_model_config(BuildGeometry* out) {
+  if (out) *out = g_geo;
+}
+
+SV_API int snowllm_select_geometry(int geo) {
+  if (geo == GEO_QWEN36_35B_A3B) g_geo = make_moe_35b();
+  else if (geo == GEO_DENSE_8B) g_geo = make_dense_8b();
+  else return SV_EINVAL;
+  g_geo_id = geo;
+  return SV_OK;
+}
+
+SV_API int snowllm_active_geometry(void) { return g_geo_id; }
+
+SV_API int64_t snowllm_geometry_name(int geo, char* buf, int64_t n) {
+  const char* name = geo == GEO_QWEN36_35B_A3B ? "qwen3.6-35b-a3b"
+                     : geo == GEO_DENSE_8B     ? "dense-8b"
+                     : geo == GEO_CUSTOM       ? "custom"
+                                               : "";
+  const int64_t len = (int64_t)strlen(name);
+  if (buf && n > 0) {
+    const int64_t c = len < n - 1 ? len : n - 1;
+    memcpy(buf, name, (size_t)c);
+    buf[c] = 0;
+  }
+  return len;
+}
+
+// Extension: install arbitrary shapes as the current geometry (id 1000).
+SV_API int snowverify_define_geometry(const BuildGeometry* g) {
+  if (!g || g->hidden <= 0 || g->num_heads <= 0 || g->num_kv_heads <= 0 ||
+      g->num_heads % g->num_kv_heads || g->head_size <= 0)
+    return SV_EINVAL;
+  g_geo = *g;
+  g_geo_id = GEO_CUSTOM;
+  return SV_OK;
+}
+
+// =======================================================================================
+// layer ops
+// =======================================================================================
+
+// Extension: embedding gather from an fp16 (table_f16 = 1) or bf16 table [V, H] -> bf16.
+SV_API int snowverify_gather_embedding(const int64_t* ids, const void* table, void* out, int64_t M,
+                                       int64_t V, int64_t H, int table_f16, void* stream) {
+  if (M < 0 || V <= 0 || H <= 0) return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  hipLaunchKernelGGL(gather_embedding_kernel, dim3((unsigned)M), dim3(256), 0, S(stream), ids,
+                     (const uint16_t*)table, (uint16_t*)out, V, H, table_f16);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Reference signature (snowllm/_capi.py:375; snowllm/ops/embedding.py:18-25): bf16 table
+// [vocab, hidden] of the current geometry.
+SV_API int snowllm_gather_embedding(const int64_t* ids, const void* table, void* out, int64_t M,
+                                    void* stream) {
+  return snowverify_gather_embedding(ids, table, out, M, g_geo.vocab_size, g_geo.hidden, 0, stream);
+}
+
+// Extension: RMSNorm with explicit width; residual may be null.
+SV_API int snowverify_rmsnorm(const void* x, void* residual, const void* gamma, void* out,
+                              int64_t M, int64_t H, float eps, void* stream) {
+  if (M < 0 || H <= 0) return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)M), dim3(256), 0, S(stream),
+                     (const uint16_t*)x, (uint16_t*)residual, (const uint16_t*)gamma,
+                     (uint16_t*)out, H, eps);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Reference signatures (snowllm/_capi.py:376, 381; snowllm/ops/norm.py:66-97).
+SV_API int snowllm_rmsnorm(const void* x, const void* gamma, void* out, int64_t M, float eps,
+                           void* stream) {
+  return snowverify_rmsnorm(x, nullptr, gamma, out, M, g_geo.hidden, eps, stream);
+}
+
+SV_API int snowllm_rmsnorm_residual(const void* x, void* residual, const void* gamma, void* out,
+                                    int64_t M, float eps, void* stream) {
+  return snowverify_rmsnorm(x, residual, gamma, out, M, g_geo.hidden, eps, stream);
+}
+
+// Extension: RoPE tables [M, half] for positions and inverse frequencies.
+SV_API int snowverify_rope_cos_sin(const int64_t* pos, const float* inv_freq, float* cosv,
+                                   float* sinv, int64_t M, int64_t half, void* stream) {
+  if (M < 0 || half <= 0) return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  const int64_t n = M * half;
+  hipLaunchKernelGGL(rope_cos_sin_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     S(stream), pos, inv_freq, cosv, sinv, M, (int)half);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Extension: QK-norm + RoPE + paged KV write with explicit shapes (the reference's
+// snowllm_qk_norm_rope_cache, snowllm/_capi.py:397-399 and ops/attention_full.py:736-784,
+// takes them from the geometry). proj [M, stride] bf16 = [q | k | v]; q_out [M, Hq, D];
+// cos/sin [M, half]; slots [M] (negative: do not cache). D <= 256, D % 16 == 0.
+SV_API int snowverify_qk_norm_rope_cache(const void* proj, int64_t stride, const void* q_gamma,
+                                         const void* k_gamma, const float* cosv, const float* sinv,
+                                         void* q_out, void* k_pool, void* v_pool,
+                                         const int32_t* slots, int64_t M, int64_t Hq, int64_t Hkv,
+                                         int64_t D, int64_t half, int64_t page, float eps,
+                                         void* stream) {
+  if (M < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || D > 256 || D % 16 || 2 * half > D || half < 0 ||
+      page != 16)
+    return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  hipLaunchKernelGGL(qk_norm_rope_cache_kernel, dim3((unsigned)(Hq + 2 * Hkv), (unsigned)M),
+                     dim3(64), 0, S(stream), (const uint16_t*)proj, stride,
+                     (const uint16_t*)q_gamma, (const uint16_t*)k_gamma, cosv, sinv,
+                     (uint16_t*)q_out, (uint16_t*)k_pool, (uint16_t*)v_pool, slots, (int)Hq,
+                     (int)Hkv, (int)D, (int)half, (int)page, eps);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Reference signature (snowllm/_capi.py:361; snowllm/ops/cache.py:40-53).
+SV_API int snowllm_resolve_slots(const int32_t* table, int64_t stride, const int32_t* seq,
+                                 const int32_t* pos, int32_t* out, int64_t M, int64_t page,
+                                 void* stream) {
+  if (M < 0 || stride <= 0 || page <= 0) return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  hipLaunchKernelGGL(resolve_slots_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0,
+                     S(stream), table, stride, seq, pos, out, M, page);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Reference signature (snowllm/_capi.py:359; snowllm/ops/attention_full.py:521-528): bytes of
+// the K and V pools for num_blocks pages of the current geometry (bf16 only).
+SV_API void snowllm_kv_pool_bytes(int64_t num_blocks, int64_t block_size, int kv_int8, int64_t* k,
+                                  int64_t* v) {
+  const int64_t n = kv_int8 ? 0 : num_blocks * block_size * g_geo.num_kv_heads * g_geo.head_size * 2;
+  if (k) *k = n;
+  if (v) *v = n;
+}
+
+// Extension: SwiGLU over a [M, 2F] gate|up block (row stride in elements) -> [M, F].
+SV_API int snowverify_swiglu(const void* gate_up, int64_t stride, void* out, int64_t M, int64_t F,
+                             void* stream) {
+  if (M < 0 || F <= 0 || stride < 2 * F) return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  const int64_t n = M * F;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, S(stream),
+                     (const uint16_t*)gate_up, stride, (uint16_t*)out, M, F);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Extension: out = a + b over n bf16 values.
+SV_API int snowverify_add_bf16(const void* a, const void* b, void* out, int64_t n, void* stream) {
+  if (n < 0) return SV_EINVAL;
+  if (n == 0) return SV_OK;
+  hipLaunchKernelGGL(add_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, S(stream),
+                     (const uint16_t*)a, (const uint16_t*)b, (uint16_t*)out, n);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Extension: MoE routing from router logits [M, stride] f32 (E routed columns, then the shared
+// expert's gate in column E when shared_w is given): weights/ids [M, topk], shared_w [M].
+SV_API int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, int64_t E,
+                                int64_t topk, float* weights, int32_t* ids, float* shared_w,
+                                void* stream) {
+  if (M < 0 || E <= 0 || E > 256 || topk <= 0 || topk > 16 || topk > E ||
+      stride < E + (shared_w ? 1 : 0))
+    return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)M), dim3(64), 0, S(stream), logits, stride,
+                     (int)E, (int)topk, weights, ids, shared_w);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}

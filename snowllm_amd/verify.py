@@ -1,0 +1,367 @@
+"""The speculative-decoding verify step on one MI355X.
+
+One verify step runs the target model over a block of T = k+1 rows (the last accepted token
+plus k draft tokens) against the paged KV cache and then accepts a prefix of the drafts:
+
+  embed -> [norm -> QKV -> QK-norm/RoPE/KV write -> paged attention -> O] ->
+           [norm -> MoE (router, top-k, experts, shared expert) | SwiGLU MLP]  x L
+  -> final norm -> LM head -> target probabilities -> rejection sampling (or argmax + prefix)
+
+Layer order and fusions follow the reference's Qwen3.5 model (snowllm/models/qwen3_5/
+qwen3_5.py:32-78, layers.py:75-228) and its verify drivers (snowllm/engine/spec_decode.py:
+263-309, 527-581). Every launch goes to torch's current stream and nothing allocates or
+synchronises inside step(), so the step can be captured in one HIP graph.
+
+Weights are random-initialised on the GPU from seeded generators (no checkpoint), in the
+formats of the BASELINE configs: Q4_K/Q8_0 GGUF blocks repacked with
+snowllm_gemm_kquant_shuffle_b, fp16 embedding and LM head, bf16 router and norms.
+"""
+from dataclasses import dataclass, field, replace
+import math
+
+import torch
+
+from . import layers as Lops
+from . import ops
+from ._capi import SnowLLMError
+
+Q4_K, Q8_0 = 4, 8
+
+
+@dataclass
+class VerifyConfig:
+    name: str
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rot_half: int            # rotated pairs per head (rotary dims / 2)
+    rope_theta: float
+    vocab: int
+    context: int             # prior tokens in the KV cache
+    block: int               # T = k + 1 query rows
+    ffn: int = 0             # dense SwiGLU width (0 for MoE)
+    experts: int = 0
+    expert_ffn: int = 0
+    topk: int = 0
+    shared_expert: bool = True
+    attn_fmt: int = Q4_K
+    ffn_fmt: int = Q4_K
+    tree_parents: tuple = ()  # non-empty: tree block (ancestor mask) instead of a chain
+    eps: float = 1e-6
+    page: int = 16
+    qk_norm: bool = True
+
+    @property
+    def moe(self):
+        return self.experts > 0
+
+    @property
+    def qkv_n(self):
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+
+# BASELINE.json configs. RoPE: config 3 rotates the full head (theta 1e6); the 35B-A3B shape
+# rotates 64 of 256 dims (partial_rotary_factor 0.25, as the reference's Qwen3.5 loader
+# requires at snowllm/models/qwen3_5/qwen3_5_weights.py:443-445) with theta 1e7.
+CONFIG3 = VerifyConfig("config3_dense8b", layers=36, hidden=4096, heads=32, kv_heads=8,
+                       head_dim=128, rot_half=64, rope_theta=1e6, vocab=151936, context=8192,
+                       block=9, ffn=14336)
+CONFIG4 = VerifyConfig("config4_moe35b_a3b", layers=40, hidden=2048, heads=16, kv_heads=2,
+                       head_dim=256, rot_half=32, rope_theta=1e7, vocab=151936, context=8192,
+                       block=9, experts=256, expert_ffn=512, topk=8)
+CONFIG5 = replace(CONFIG4, name="config5_moe35b_a3b_220k_tree", context=220000, block=11,
+                  attn_fmt=Q8_0, tree_parents=(-1, 0, 1, 2, 3, 4, 0, 6, 7, 8, 9))
+CONFIGS = {"config3": CONFIG3, "config4": CONFIG4, "config5": CONFIG5}
+
+
+def tree_masks(parents):
+    masks = []
+    for i, p in enumerate(parents):
+        masks.append((1 << i) | (masks[p] if p >= 0 else 0))
+    return masks
+
+
+def tree_depths(parents):
+    d = []
+    for p in parents:
+        d.append(0 if p < 0 else d[p] + 1)
+    return d
+
+
+# ---------------------------------------------------------------------------------------
+# random-init weights (GPU)
+# ---------------------------------------------------------------------------------------
+def gguf_random(fmt, n, k, seed, device="cuda"):
+    """Seeded random GGUF blocks for an [n, k] weight: Q4_K with 6-bit scales/mins and nibbles
+    uniform and d, dmin = fp16(|N(0, 1e-3^2)|); Q8_0 with int8 uniform in
+    -127..127 and d = fp16(|N(0, 1e-2^2)|)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    if fmt == Q4_K:
+        nb = n * k // 256
+        raw = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device=device, generator=g)
+        dd = (torch.randn(nb, 2, device=device, generator=g) * 1e-3).abs().half()
+        raw[:, 0:4] = dd.view(torch.uint8).view(nb, 4)
+        return raw.view(-1)
+    if fmt == Q8_0:
+        nb = n * k // 32
+        raw = torch.empty(nb, 34, dtype=torch.uint8, device=device)
+        q = torch.randint(-127, 128, (nb, 32), dtype=torch.int8, device=device, generator=g)
+        d = (torch.randn(nb, device=device, generator=g) * 1e-2).abs().half()
+        raw[:, 0:2] = d.view(torch.uint8).view(nb, 2)
+        raw[:, 2:] = q.view(torch.uint8)
+        return raw.view(-1)
+    raise SnowLLMError(f"unknown format {fmt}")
+
+
+def packed_random(fmt, n, k, seed, keep_raw=False):
+    raw = gguf_random(fmt, n, k, seed)
+    quant, meta = ops.gemm_kquant_shuffle_b(fmt, raw, n, k)
+    return (quant, meta, raw if keep_raw else None)
+
+
+@dataclass
+class LayerWeights:
+    in_norm: torch.Tensor
+    post_norm: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    qkv: tuple
+    o: tuple
+    router: torch.Tensor = None      # shuffled bf16 [E+1, H]
+    gu: tuple = None                 # stacked experts (MoE) or the dense MLP gate/up
+    dn: tuple = None
+    sh_gu: tuple = None
+    sh_dn: tuple = None
+    raw: dict = field(default_factory=dict)  # unshuffled copies kept for parity checks
+
+
+class VerifyModel:
+    """Weights, KV pools and step buffers of one verify-step configuration."""
+
+    def __init__(self, cfg: VerifyConfig, seed: int = 0, keep_raw: bool = False,
+                 kv_std: float = 1.0):
+        self.cfg = c = cfg
+        self.keep_raw = keep_raw
+        dev = "cuda"
+        torch.cuda.synchronize()
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        H, V = c.hidden, c.vocab
+
+        def gamma(n):
+            return (1.0 + 0.02 * torch.randn(n, device=dev, generator=gen)).bfloat16()
+
+        def sub(i, j):
+            return seed * 100003 + i * 101 + j
+
+        self.layers = []
+        for i in range(c.layers):
+            lw = LayerWeights(in_norm=gamma(H), post_norm=gamma(H), q_norm=gamma(c.head_dim),
+                              k_norm=gamma(c.head_dim),
+                              qkv=packed_random(c.attn_fmt, c.qkv_n, H, sub(i, 0), keep_raw),
+                              o=packed_random(c.attn_fmt, H, c.heads * c.head_dim, sub(i, 1), keep_raw))
+            if c.moe:
+                E, F = c.experts, c.expert_ffn
+                router = (torch.randn(E + 1, H, device=dev, generator=gen) / math.sqrt(H)).bfloat16()
+                lw.router = Lops.dense_shuffle(router)
+                lw.gu = packed_random(c.ffn_fmt, E * 2 * F, H, sub(i, 2), keep_raw)
+                lw.dn = packed_random(c.ffn_fmt, E * H, F, sub(i, 3), keep_raw)
+                lw.sh_gu = packed_random(c.ffn_fmt, 2 * F, H, sub(i, 4), keep_raw)
+                lw.sh_dn = packed_random(c.ffn_fmt, H, F, sub(i, 5), keep_raw)
+                if keep_raw:
+                    lw.raw["router"] = router
+            else:
+                lw.gu = packed_random(c.ffn_fmt, 2 * c.ffn, H, sub(i, 2), keep_raw)
+                lw.dn = packed_random(c.ffn_fmt, H, c.ffn, sub(i, 3), keep_raw)
+            self.layers.append(lw)
+        self.embed = (0.02 * torch.randn(V, H, device=dev, generator=gen)).half()
+        head = (0.02 * torch.randn(V, H, device=dev, generator=gen)).half()
+        self.lm_head = Lops.dense_shuffle(head)
+        self.lm_head_raw = head if keep_raw else None
+        self.final_norm = gamma(H)
+        self.inv_freq = (1.0 / (c.rope_theta ** (torch.arange(c.rot_half, device=dev,
+                                                             dtype=torch.float32) / c.rot_half)))
+        # KV cache: context + block pages, random page table (prior tokens ~ N(0, kv_std^2))
+        T = c.block
+        self.pages = (c.context + T + c.page - 1) // c.page
+        self.blocks = self.pages + 8
+        kvg = torch.Generator(device=dev).manual_seed(seed + 7)
+        shape_k = (self.blocks, c.kv_heads, c.head_dim // 16, c.page, 16)
+        shape_v = (self.blocks, c.kv_heads, c.page // 4, c.head_dim, 4)
+        self.k_pools, self.v_pools = [], []
+        for _ in range(c.layers):
+            k = torch.empty(shape_k, dtype=torch.bfloat16, device=dev)
+            v = torch.empty(shape_v, dtype=torch.bfloat16, device=dev)
+            k.normal_(0, kv_std, generator=kvg)
+            v.normal_(0, kv_std, generator=kvg)
+            self.k_pools.append(k)
+            self.v_pools.append(v)
+        perm = torch.randperm(self.blocks, device=dev, generator=kvg)[:self.pages]
+        self.table = perm.int().view(1, -1).contiguous()
+        self._alloc_step_buffers()
+
+    # -----------------------------------------------------------------------------------
+    def _alloc_step_buffers(self):
+        c, T, dev = self.cfg, self.cfg.block, "cuda"
+        H = c.hidden
+        bf = torch.bfloat16
+        self.ids = torch.zeros(T, dtype=torch.int64, device=dev)
+        self.positions = torch.zeros(T, dtype=torch.int64, device=dev)
+        self.slots = torch.zeros(T, dtype=torch.int32, device=dev)
+        self.lens = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.tree = None
+        if c.tree_parents:
+            self.tree = torch.tensor([m - (1 << 64) if m >= 1 << 63 else m
+                                      for m in tree_masks(c.tree_parents)],
+                                     dtype=torch.int64, device=dev)
+        self.cos = torch.empty(T, c.rot_half, dtype=torch.float32, device=dev)
+        self.sin = torch.empty_like(self.cos)
+        self.x = torch.empty(T, H, dtype=bf, device=dev)         # layer input (block output)
+        self.res = [torch.empty(T, H, dtype=bf, device=dev) for _ in range(2)]
+        self.proj = torch.empty(T, c.qkv_n, dtype=bf, device=dev)
+        self.q = torch.empty(T, c.heads, c.head_dim, dtype=bf, device=dev)
+        self.attn = torch.empty(T, c.heads, c.head_dim, dtype=bf, device=dev)
+        self.o = torch.empty(T, H, dtype=bf, device=dev)
+        self.h2 = torch.empty(T, H, dtype=bf, device=dev)
+        wsH = ops.gemm_kquant_a_ws_bytes(T, H)
+        self.ws_h = torch.empty(wsH, dtype=torch.uint8, device=dev)
+        self.ws_h2 = torch.empty(wsH, dtype=torch.uint8, device=dev)
+        self.ws_a = torch.empty(ops.gemm_kquant_a_ws_bytes(T, c.heads * c.head_dim),
+                                dtype=torch.uint8, device=dev)
+        self.attn_scratch = torch.empty(
+            ops.paged_attention_scratch_bytes(1, T, c.heads, c.kv_heads, c.head_dim),
+            dtype=torch.uint8, device=dev)
+        if c.moe:
+            E, F, K = c.experts, c.expert_ffn, c.topk
+            self.router_logits = torch.empty(T, E + 1, dtype=torch.float32, device=dev)
+            self.route_w = torch.empty(T, K, dtype=torch.float32, device=dev)
+            self.route_ids = torch.empty(T, K, dtype=torch.int32, device=dev)
+            self.shared_w = torch.empty(T, dtype=torch.float32, device=dev)
+            self.plan = torch.empty(Lops.MOE_PLAN_BYTES, dtype=torch.uint8, device=dev)
+            self.moe_act = torch.empty(T * K + 1, 16, F, dtype=bf, device=dev)
+            self.pairs = torch.empty(T * K, H, dtype=torch.float32, device=dev)
+            self.shared_out = torch.empty(T, H, dtype=torch.float32, device=dev)
+        else:
+            self.act = torch.empty(T, c.ffn, dtype=bf, device=dev)
+            self.ws_act = torch.empty(ops.gemm_kquant_a_ws_bytes(T, c.ffn), dtype=torch.uint8,
+                                      device=dev)
+        self.ws_f = torch.empty(wsH, dtype=torch.uint8, device=dev)
+        self.logits = torch.empty(T, c.vocab, dtype=torch.float32, device=dev)
+
+    def set_block(self, ids, context=None):
+        """Stage one block: ids [T] (last token + drafts) at positions context..context+T-1
+        (tree blocks: context + depth). Host-side, outside the timed/captured step."""
+        c, T = self.cfg, self.cfg.block
+        ctx = c.context if context is None else context
+        dev = "cuda"
+        depth = tree_depths(c.tree_parents) if c.tree_parents else list(range(T))
+        self.ids.copy_(torch.as_tensor(ids, dtype=torch.int64, device=dev))
+        self.positions.copy_(torch.tensor([ctx + d for d in depth], dtype=torch.int64, device=dev))
+        rows = torch.arange(ctx, ctx + T, dtype=torch.int64)
+        tbl = self.table.view(-1).cpu().long()
+        self.slots.copy_((tbl[rows // c.page] * c.page + rows % c.page).int().to(dev))
+        self.lens.fill_(ctx + T)
+
+    # -----------------------------------------------------------------------------------
+    def forward(self, *, upto_layer=None):
+        """Target model over the staged block -> self.logits [T, V] f32."""
+        c, T = self.cfg, self.cfg.block
+        H = c.hidden
+        Lops.gather_embedding(self.ids, self.embed, self.x)
+        Lops.rope_cos_sin(self.positions, self.inv_freq, self.cos, self.sin)
+        res_in, res_out = None, self.res[0]
+        n_layers = c.layers if upto_layer is None else upto_layer
+        for i in range(n_layers):
+            lw = self.layers[i]
+            # attention block: residual update + input norm fused with the QKV operand prep
+            Lops.norm_prep(self.x, lw.in_norm, self.ws_h, c.eps, res_in=res_in, res_out=res_out)
+            ops.gemm_kquant_a_prepared(c.attn_fmt, lw.qkv[0], lw.qkv[1], self.proj, T, c.qkv_n, H,
+                                       self.ws_h)
+            Lops.qk_norm_rope_cache(self.proj, lw.q_norm, lw.k_norm, self.cos, self.sin, self.q,
+                                    self.k_pools[i], self.v_pools[i], self.slots, c.eps)
+            ops.paged_attention_explicit(self.q, self.k_pools[i], self.v_pools[i], self.attn,
+                                         self.table, self.lens, c.head_dim ** -0.5,
+                                         self.attn_scratch, tree=self.tree)
+            ops.gemm_kquant_a(c.attn_fmt, self.attn.view(T, -1), lw.o[0], lw.o[1], self.o, T, H,
+                              c.heads * c.head_dim, self.ws_a)
+            # feed-forward block
+            res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
+            if c.moe:
+                Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,
+                               res_out=res_out, y_out=self.h2)
+                Lops.dense_gemv(Lops.WT_BF16, lw.router, self.h2, self.router_logits, T,
+                                c.experts + 1, H)
+                Lops.moe_route(self.router_logits, c.experts, c.topk, self.route_w,
+                               self.route_ids, self.shared_w)
+                Lops.moe_plan(self.route_ids, c.experts, self.plan, shared=True)
+                Lops.moe_experts(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, self.plan,
+                                 self.ws_h2, self.route_w, self.shared_w, self.moe_act,
+                                 self.pairs, self.shared_out, self.x, T, c.topk, c.experts, H,
+                                 c.expert_ffn)
+            else:
+                Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,
+                               res_out=res_out)
+                Lops.gate_up_swiglu(c.ffn_fmt, lw.gu[0], lw.gu[1], self.ws_h2, self.act, T,
+                                    c.ffn, H)
+                ops.gemm_kquant_a(c.ffn_fmt, self.act, lw.dn[0], lw.dn[1], self.x, T, H, c.ffn,
+                                  self.ws_act)
+            res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
+        self.layer_residual = res_in  # residual stream entering the next layer (with self.x)
+        # final norm + LM head (fp16 weights, f32 logits)
+        Lops.norm_prep(self.x, self.final_norm, self.ws_f, c.eps, res_in=res_in, res_out=res_out)
+        self.final_residual = res_out
+        Lops.dense_gemv(Lops.WT_F16, self.lm_head, self.ws_f, self.logits, T, c.vocab, H)
+        return self.logits
+
+
+class Acceptance:
+    """Rejection-sampling acceptance of the block against draft probabilities q (the draft
+    side's proposal): target probabilities over the full vocabulary (ops.sampling.
+    probabilities), then ops.dflash.reject (snowllm/engine/dflash_sampling.py:52-69).
+    For a tree block the chain rows[0..k] is accepted."""
+
+    def __init__(self, vocab, chain_rows):
+        dev = "cuda"
+        self.rows = list(chain_rows)
+        T = len(self.rows)
+        k = T - 1
+        self.V, self.T = vocab, T
+        self.top_k = torch.full((T,), ops.SAMPLING_MAX_K, dtype=torch.int32, device=dev)
+        self.top_p = torch.ones(T, device=dev)
+        self.temp = torch.ones(T, device=dev)
+        self.p = torch.empty(T, vocab, device=dev)
+        self.pid = torch.empty(T, vocab, dtype=torch.int64, device=dev)
+        self.ws = torch.empty(ops.sample_workspace_bytes(T, vocab, vocab), dtype=torch.uint8, device=dev)
+        self.q = torch.empty(1, k, vocab, device=dev)
+        self.qid = torch.arange(vocab, dtype=torch.int64, device=dev).repeat(1, k, 1).contiguous()
+        self.drafts = torch.zeros(1, k, dtype=torch.int64, device=dev)
+        self.uniform = torch.zeros(1, T, device=dev)
+        self.slot = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.valid = torch.ones(1, dtype=torch.int32, device=dev)
+        self.out = torch.empty(1, T, dtype=torch.int64, device=dev)
+        self.accepted = torch.empty(1, dtype=torch.int64, device=dev)
+        self.chain_logits = None
+        if self.rows != list(range(T)):
+            self.chain_logits = torch.empty(T, vocab, device=dev)
+            self.chain_index = torch.tensor(self.rows, dtype=torch.int64, device=dev)
+
+    def set_draft(self, draft_logits, drafts, uniform):
+        """Draft side (outside the step): q = softmax(draft logits) over the vocabulary."""
+        k = self.T - 1
+        ones = torch.ones(k, device="cuda")
+        qid = torch.empty(k, self.V, dtype=torch.int64, device="cuda")
+        q = self.q.view(k, self.V)
+        ops.probabilities(draft_logits, self.top_k[:k], ones, ones, self.V, q, qid, self.ws)
+        self.drafts.copy_(drafts.view(1, k))
+        self.uniform.copy_(uniform.view(1, self.T))
+
+    def __call__(self, logits):
+        src = logits
+        if self.chain_logits is not None:
+            torch.index_select(logits, 0, self.chain_index, out=self.chain_logits)
+            src = self.chain_logits
+        ops.probabilities(src, self.top_k, self.top_p, self.temp, self.V, self.p, self.pid, self.ws)
+        ops.dflash.reject(self.p, self.pid, self.drafts, self.qid, self.q, self.slot, self.valid,
+                          self.uniform, self.out, self.accepted)
+        return self.out, self.accepted

@@ -87,3 +87,26 @@ def test_gemv_graph_replay(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert Q.rel_l2(c.cpu().numpy(), Q.gemv_reference(x.cpu(), w)) < TOL
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+def test_every_gemv_variant(gpu, fmt):
+    """Each fixed tile shape (the tuning knob) agrees with the oracle, incl. K with S > waves."""
+    from snowllm_amd import ops
+    from snowllm_amd._capi import lib
+    for n, k in [(1024, 14336), (768, 2048)]:
+        raw = Q.make_q4_k(n, k, seed=n) if fmt == 4 else Q.make_q8_0(n, k, seed=n)
+        x = Q.make_activations(9, k, seed=k)
+        want = Q.gemv_reference(x, Q.dequant(raw, fmt, n, k))
+        quant, meta = ops.gemm_kquant_shuffle_b(fmt, torch.from_numpy(raw).cuda(), n, k)
+        ws = torch.empty(ops.gemm_kquant_a_ws_bytes(9, k), dtype=torch.uint8, device="cuda")
+        c = torch.empty(9, n, device="cuda")
+        try:
+            for v in range(7):
+                print(f"variant {v} fmt={fmt} N={n} K={k}", flush=True)
+                lib.snowverify_gemv_variant(v)
+                c.zero_()
+                ops.gemm_kquant_a(fmt, x.cuda(), quant, meta, c, 9, n, k, ws)
+                assert Q.rel_l2(c.cpu().numpy(), want) < TOL, v
+        finally:
+            lib.snowverify_gemv_variant(0)

@@ -1,0 +1,110 @@
+"""End-to-end verify step on the GPU against the CPU layer reference (oracle/model.py).
+
+Each layer is checked with teacher forcing: the CPU reference gets the GPU's input to that
+layer, so every comparison measures one layer's error. Then the LM head, and the acceptance
+on the GPU's own logits (bit-exact against the C oracle)."""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as A
+from oracle import model as RM
+from tests.kvcache import cache_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny(kind):
+    from snowllm_amd.verify import VerifyConfig
+    base = dict(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, rot_half=32,
+                rope_theta=1e4, vocab=2048, context=300, block=9)
+    if kind == "moe":
+        return VerifyConfig("tiny_moe", experts=16, expert_ffn=256, topk=4, **base)
+    if kind == "dense":
+        return VerifyConfig("tiny_dense", ffn=512, **dict(base, kv_heads=1, rot_half=64))
+    if kind == "tree":
+        return VerifyConfig("tiny_tree", experts=16, expert_ffn=256, topk=4, attn_fmt=8,
+                            tree_parents=(-1, 0, 1, 0, 3), **dict(base, block=5))
+    raise ValueError(kind)
+
+
+def rel(a, b):
+    a, b = a.double(), b.double()
+    return ((a - b).norm() / b.norm().clamp_min(1e-12)).item()
+
+
+@pytest.mark.parametrize("kind", ["dense", "moe", "tree"])
+def test_layers_and_head_match_cpu_reference(gpu, kind):
+    from snowllm_amd.verify import VerifyModel, tree_masks, Acceptance
+    cfg = tiny(kind)
+    print(f"verify step {cfg.name}", flush=True)
+    m = VerifyModel(cfg, seed=3, keep_raw=True)
+    T = cfg.block
+    ids = torch.randint(0, cfg.vocab, (T,), generator=torch.Generator().manual_seed(5))
+    m.set_block(ids)
+    masks = tree_masks(cfg.tree_parents) if cfg.tree_parents else [(2 << t) - 1 for t in range(T)]
+    cos, sin = RM.rope_tables(m.positions.cpu(), m.inv_freq.cpu())
+    pages = m.table.view(-1).long().cpu()
+    for layer in range(cfg.layers):
+        m.forward(upto_layer=layer)
+        torch.cuda.synchronize()
+        x_in = m.x.float().cpu()
+        res_in = None if layer == 0 else m.layer_residual.float().cpu()
+        kctx = cache_rows(m.k_pools[layer].cpu(), pages, cfg.kv_heads, cfg.head_dim, 16, key=True)[:cfg.context]
+        vctx = cache_rows(m.v_pools[layer].cpu(), pages, cfg.kv_heads, cfg.head_dim, 16, key=False)[:cfg.context]
+        ref = RM.LayerRef(cfg, m.layers[layer])
+        x2, r2, attn, routing = RM.layer_forward(ref, x_in, res_in, cos, sin, kctx, vctx, masks)
+        m.forward(upto_layer=layer + 1)
+        torch.cuda.synchronize()
+        e_attn = rel(m.attn.float().cpu(), attn)
+        e_x = rel(m.x.float().cpu(), x2)
+        e_r = rel(m.layer_residual.float().cpu(), r2)
+        print(f"  layer {layer}: attn {e_attn:.2e}  ffn out {e_x:.2e}  residual {e_r:.2e}", flush=True)
+        assert e_attn < 1e-2 and e_r < 1e-2 and e_x < 2e-2
+        if routing is not None:
+            got = m.route_ids.cpu().long()
+            assert torch.equal(got.sort(-1).values, routing.sort(-1).values)
+    logits = m.forward().clone()
+    torch.cuda.synchronize()
+    want = RM.head_reference(m.x.float().cpu(), m.layer_residual.float().cpu(), m.final_norm.cpu(),
+                             m.lm_head_raw.cpu(), cfg.eps)
+    e_l = rel(logits.cpu(), want)
+    print(f"  logits rel L2 {e_l:.2e}", flush=True)
+    assert e_l < 1e-2
+    # acceptance over the chain rows on the GPU's own logits: bit-exact vs the C oracle
+    rows = list(range(T)) if not cfg.tree_parents else [0, 1, 2]
+    acc = Acceptance(cfg.vocab, rows)
+    k = len(rows) - 1
+    g = torch.Generator(device="cuda").manual_seed(9)
+    draft_logits = torch.randn(k, cfg.vocab, device="cuda", generator=g) * 2
+    drafts = torch.multinomial(draft_logits.softmax(-1), 1, generator=g).view(1, k)
+    u = torch.rand(1, k + 1, device="cuda", generator=g)
+    acc.set_draft(draft_logits, drafts, u)
+    out, accepted = acc(logits)
+    torch.cuda.synchronize()
+    chain = logits.cpu()[rows].numpy()
+    p = A.softmax(chain)
+    q = A.softmax(draft_logits.cpu().numpy())
+    ident = np.tile(np.arange(cfg.vocab), (k + 1, 1))
+    want_out, want_acc = A.reject(p, ident, drafts.cpu().numpy(), ident[:k][None], q[None],
+                                  np.zeros(1, np.int32), np.ones(1, np.int32), u.cpu().numpy())
+    assert np.array_equal(out.cpu().numpy(), want_out) and np.array_equal(accepted.cpu().numpy(), want_acc)
+
+
+def test_step_graph_replay_matches_eager(gpu):
+    from snowllm_amd.verify import VerifyModel
+    cfg = tiny("moe")
+    m = VerifyModel(cfg, seed=4)
+    m.set_block(torch.arange(cfg.block) * 7)
+    eager = m.forward().clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        m.forward()
+    for _ in range(3):
+        m.logits.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m.logits, eager)
