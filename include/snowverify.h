@@ -149,6 +149,10 @@ int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_
                                int64_t table_stride, float scale, void* scratch,
                                int64_t scratch_bytes, void* stream);
 
+/* Extension, no counterpart in the reference (a tuning knob): pages per context split of
+ * snowverify_paged_attention; 0 = automatic. Returns the previous value. */
+int snowverify_attention_pages_per_split(int pages);
+
 /* ---- geometry ------------------------------------------------------------------------ */
 /* The reference compiles its shapes in (snowllm/_capi.py:44-113); here they are run-time
  * data. BuildGeometry has the reference's 37 int64 fields in the same order. */
@@ -232,6 +236,10 @@ int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* meta, cons
 int64_t snowverify_moe_plan_bytes(void);
 int snowverify_moe_plan(const int32_t* ids, int64_t M, int64_t topk, int64_t E, int shared,
                         void* plan, void* stream);
+/* snowverify_moe_route and snowverify_moe_plan in one launch (shared slot iff shared_w). */
+int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_t M, int64_t E,
+                              int64_t topk, float* weights, int32_t* ids, float* shared_w,
+                              void* plan, void* stream);
 int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_meta,
                            const void* dn_quant, const void* dn_meta, const void* sh_gu_quant,
                            const void* sh_gu_meta, const void* sh_dn_quant,

@@ -85,6 +85,7 @@ _SIGS = [
     # paged attention
     ("snowverify_paged_attention_scratch_bytes", c_int64, [c_int64] * 5),
     ("snowverify_paged_attention", c_int, [P] * 7 + [c_int64] * 7 + [c_float, P, c_int64, S]),
+    ("snowverify_attention_pages_per_split", c_int, [c_int]),
     # geometry and layer plumbing
     ("snowllm_model_config", None, [P]),
     ("snowllm_select_geometry", c_int, [c_int]),
@@ -112,6 +113,7 @@ _SIGS = [
     ("snowverify_gate_up_swiglu", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, S]),
     ("snowverify_moe_plan_bytes", c_int64, []),
     ("snowverify_moe_plan", c_int, [P, c_int64, c_int64, c_int64, c_int, P, S]),
+    ("snowverify_moe_route_plan", c_int, [P, c_int64, c_int64, c_int64, c_int64, P, P, P, P, S]),
     ("snowverify_moe_experts", c_int, [c_int] + [P] * 16 + [c_int64] * 5 + [S]),
 ]
 

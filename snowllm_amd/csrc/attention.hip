@@ -3,13 +3,20 @@
 //
 // KV pool layouts are the reference's (tests/test_lfm2_dspark_reference.py:30-36):
 //   K: [blocks, Hkv, d/16, page, 16]   V: [blocks, Hkv, page/4, d, 4]   (bf16, page = 16)
-// so one (page, kv head) is a contiguous 2*d*16-byte run of each.
+// so one (page, kv head) is a contiguous 32*d-byte run of each.
 //
-// MFMA mapping (v_mfma_f32_16x16x32_bf16), per wave = one 16-row tile of query rows of one kv
-// head, over 32-key chunks (two pages):
-//   S^T[key, row] = K[key, :] . Q[row, :]      A = K (16 keys x 32 d, 16-byte lane loads)
+// One workgroup per (request, kv head, context split), one wave per 16-row tile of the
+// head's query rows. The pages of the split stream through an LDS ring with direct
+// global->LDS loads (global_load_lds_dwordx4, 1 KiB per wave instruction), RING - 1 pages
+// ahead of the MFMAs, so K and V leave HBM once per workgroup whatever the number of tiles.
+// Each wave waits for its own loads of a page (vmcnt) and a barrier publishes the page.
+//
+// MFMA mapping, per wave and page:
+//   S^T[key, row] = K[key, :] . Q[row, :]      v_mfma_f32_16x16x32_bf16 over d:
+//                                              A = K (16 keys x 32 d, ds_read_b128)
 //                                              B = Q^T (held in registers)
-//   O^T[d, row]  += V^T[d, key] . P^T[key, row] A = V^T (two 8-byte lane loads per page)
+//   O^T[d, row]  += V^T[d, key] . P^T[key, row] v_mfma_f32_16x16x16_bf16 over the 16 keys:
+//                                              A = V^T (ds_read_b64 per d tile)
 //                                              B = P^T, straight from the S^T registers
 // Putting keys on the M side makes the C layout of S^T (row = lane & 15, key = 4*(lane>>4)+i)
 // exactly the B layout P^T needs, so the softmax never leaves registers.
@@ -25,10 +32,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short short4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(4))) const int32_t cint32;
 
 constexpr int PAGE = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int SPLITS_MAX = 512;
+constexpr int MAX_TILES = 8;  // row tiles (waves) per workgroup: T * G <= 128
 
 struct AttnArgs {
   const uint16_t* q;        // [batch*T, Hq, D]
@@ -43,39 +54,148 @@ struct AttnArgs {
   float qk_scale;           // softmax scale * log2(e)
 };
 
+// LDS image of one (page, kv head): K as in HBM, then V with its four key groups padded apart
+// (VPAD bytes) so the four lane groups of a V^T read fall on different banks.
+template <int D>
+struct SlotGeo {
+  static constexpr int KBYTES = PAGE * D * 2;           // K (and V) bytes of one page
+  static constexpr int CHUNKS = 2 * KBYTES / 1024;      // 1 KiB load chunks per page, K then V
+  static constexpr int VGROUP = D * 8;                  // bytes of one V key group (4 keys x D)
+  static constexpr int VPAD = 128;
+  static constexpr int BYTES = KBYTES + 4 * (VGROUP + VPAD);
+};
+
 __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
   u32x4 v = *(const u32x4*)p;
   return __builtin_bit_cast(bf16x8, v);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+// s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
+// expcnt 7 and lgkmcnt 15 = no wait on those).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int D>
-__global__ void __launch_bounds__(64) attn_split_kernel(AttnArgs a) {
-  constexpr int DS = D / 32;  // MFMA k-steps over the head dimension
-  constexpr int DT = D / 16;  // 16-wide d tiles of the output
-  const int lane = threadIdx.x;
-  const int kq = lane >> 4, col = lane & 15;
+// Workgroup barrier that the compiler may not move memory accesses across, without the
+// release fence of __syncthreads (which would wait for every load in flight).
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
-  // XCD-aware block mapping: consecutive block ids land on different XCDs (id % 8), so the
-  // NRT row tiles of one (request, kv head, split) are given ids that share id % 8.
-  const int nblk = gridDim.x;
-  const int id = blockIdx.x;
-  int lin;
-  {
-    const int per_x = nblk / 8, rem = nblk % 8;
-    const int xcd = id % 8, local = id / 8;
-    lin = (xcd < rem) ? xcd * (per_x + 1) + local : rem * (per_x + 1) + (xcd - rem) * per_x + local;
-    if (nblk < 8) lin = id;
+// Issue wave w's CPW chunk loads of one (page, head) into an LDS slot. Chunk ids past the
+// page wrap around (an identical second copy), so every wave issues exactly CPW loads and the
+// vmcnt bookkeeping is the same for all waves.
+template <int D, int CPW>
+__device__ __forceinline__ void dma_page(const uint8_t* __restrict__ kp,
+                                         const uint8_t* __restrict__ vp, uint8_t* slot, int w,
+                                         int NW, int lane) {
+  using G = SlotGeo<D>;
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    int c = w + i * NW;
+    if (c >= G::CHUNKS) c -= G::CHUNKS;
+    const uint8_t* src;
+    uint8_t* dst;
+    if (c < G::CHUNKS / 2) {
+      src = kp + c * 1024;
+      dst = slot + c * 1024;
+    } else {
+      const int off = (c - G::CHUNKS / 2) * 1024;
+      src = vp + off;
+      dst = slot + G::KBYTES + (off / G::VGROUP) * (G::VGROUP + G::VPAD) + off % G::VGROUP;
+    }
+    __builtin_amdgcn_global_load_lds((const void*)(src + lane * 16), (lds_void*)dst, 16, 0, 0);
   }
-  const int tile = lin % a.NRT;
-  int rest = lin / a.NRT;
-  const int split = rest % a.S;
-  rest /= a.S;
-  const int h = rest % a.Hkv;
-  const int b = rest / a.Hkv;
+}
+
+// Online-softmax state of one wave (16 query rows = lanes' columns).
+template <int D>
+struct AttnState {
+  floatx4 o[D / 16];
+  float m, l;
+};
+
+// One page from its LDS slot: S^T = K Q^T, masked online softmax, O^T += V^T P^T.
+template <int D>
+__device__ __forceinline__ void attend_page(AttnState<D>& st, const uint8_t* slot,
+                                            const bf16x8 (&qb)[D / 32], int pg, int L, int ctx,
+                                            uint64_t anc, float qk_scale, int kq, int col) {
+  using G = SlotGeo<D>;
+  constexpr int DS = D / 32, DT = D / 16;
+  u32x4 kr[DS];
+  u32x2 vr[DT];
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds)  // K [D/16][16 keys][16 d]: chunk 2*ds + kq/2, offset 8*(kq&1)
+    kr[ds] = *(const u32x4*)(slot + ((2 * ds + (kq >> 1)) * PAGE + col) * 32 + (kq & 1) * 16);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)  // V group kq: keys 4kq..4kq+3 of d = dt*16 + col
+    vr[dt] = *(const u32x2*)(slot + G::KBYTES + kq * (G::VGROUP + G::VPAD) + (dt * 16 + col) * 8);
+  floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds)
+    sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[ds]), qb[ds], sacc,
+                                                   0, 0, 0);
+  // mask + online softmax (row = col; keys 4*kq + i)
+  float sv[4];
+  float cmax = -__builtin_huge_valf();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pos = pg * PAGE + 4 * kq + i;
+    bool vis = pos < L;
+    if (vis && pos >= ctx) vis = (anc >> (pos - ctx)) & 1ull;
+    sv[i] = vis ? sacc[i] * qk_scale : -__builtin_huge_valf();
+    cmax = sv[i] > cmax ? sv[i] : cmax;
+  }
+  cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+  cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+  const float m_new = fmaxf(st.m, cmax);
+  const float msafe = (m_new == -__builtin_huge_valf()) ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(st.m - msafe);  // exp2(-inf) = 0
+  float p[4];
+  float psum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    p[i] = __builtin_amdgcn_exp2f(sv[i] - msafe);
+    psum += p[i];
+  }
+  psum += __shfl_xor(psum, 16, 64);
+  psum += __shfl_xor(psum, 32, 64);
+  st.l = st.l * alpha + psum;
+  st.m = m_new;
+  // P^T operand (keys 4kq + i of row col), carried as a bf16 pair (hi + lo residual), which
+  // keeps ~16 significant bits through the MFMA.
+  float plo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) plo[i] = p[i] - bf16_to_f32(f32_to_bf16(p[i]));
+  const u32x2 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+  const u32x2 pwl = {pack_bf16x2(plo[0], plo[1]), pack_bf16x2(plo[2], plo[3])};
+  const short4 pb = __builtin_bit_cast(short4, pw);
+  const short4 pbl = __builtin_bit_cast(short4, pwl);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const short4 vt = __builtin_bit_cast(short4, vr[dt]);
+    floatx4 o = st.o[dt] * alpha;
+    o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, pb, o, 0, 0, 0);
+    st.o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, pbl, o, 0, 0, 0);
+  }
+}
+
+template <int D, int CPW, int RING>
+__global__ void __launch_bounds__(MAX_TILES * 64) attn_split_kernel(AttnArgs a) {
+  using G = SlotGeo<D>;
+  constexpr int DS = D / 32, DT = D / 16;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING * G::BYTES];
+  const int NW = (int)(blockDim.x >> 6);  // == NRT
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row tile
+  const int kq = lane >> 4, col = lane & 15;
+  const int split = blockIdx.x % a.S;
+  const int h = (blockIdx.x / a.S) % a.Hkv;
+  const int b = blockIdx.x / (a.S * a.Hkv);
 
   int L = a.lens[b];
   if (L > a.table_stride * PAGE) L = a.table_stride * PAGE;  // never read past the table row
@@ -86,7 +206,7 @@ __global__ void __launch_bounds__(64) attn_split_kernel(AttnArgs a) {
   if (p1 > n_pages) p1 = n_pages;
 
   // this lane's query row (column of S^T / O^T)
-  const int r = tile * 16 + col;
+  const int r = w * 16 + col;
   const bool row_live = r < a.T * a.G;
   const int t = row_live ? r / a.G : 0;
   const int g = row_live ? r % a.G : 0;
@@ -94,164 +214,167 @@ __global__ void __launch_bounds__(64) attn_split_kernel(AttnArgs a) {
   uint64_t anc;
   if (a.tree) anc = row_live ? a.tree[(int64_t)b * a.T + t] : 1ull;
   else anc = (t >= 63) ? ~0ull : ((2ull << t) - 1ull);
-  // Q^T operand: 8 consecutive d per k-step
-  bf16x8 qb[DS];
-  {
-    const uint16_t* qrow = a.q + (((int64_t)b * a.T + t) * a.Hq + hq) * D;
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      if (row_live) qb[ds] = load_bf16x8(qrow + ds * 32 + kq * 8);
-      else qb[ds] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
-    }
-  }
 
-  floatx4 o[DT];
+  AttnState<D> st;
 #pragma unroll
-  for (int i = 0; i < DT; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m = -__builtin_huge_valf();  // running max (log2 domain)
-  float l = 0.f;
+  for (int i = 0; i < DT; ++i) st.o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  st.m = -__builtin_huge_valf();
+  st.l = 0.f;
 
-  const int64_t page_elems = (int64_t)PAGE * D;          // one (page, head) of K or V
-  const int64_t block_elems = page_elems * a.Hkv;
-  const int32_t* trow = a.table + (int64_t)b * a.table_stride;
-
-  for (int pg = p0; pg < p1; pg += 2) {
-    const bool has2 = pg + 1 < p1;
-    const int blk0 = trow[pg];
-    const int blk1 = has2 ? trow[pg + 1] : blk0;
-    const uint16_t* k0 = a.k_pool + blk0 * block_elems + h * page_elems;
-    const uint16_t* k1 = a.k_pool + blk1 * block_elems + h * page_elems;
-    const uint16_t* v0 = a.v_pool + blk0 * block_elems + h * page_elems;
-    const uint16_t* v1 = a.v_pool + blk1 * block_elems + h * page_elems;
-    // S^T for the two pages
-    floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  if (p0 < p1) {  // uniform over the workgroup
+    // Q^T operand (8 consecutive d per k-step), loaded before the page loads are queued
+    bf16x8 qb[DS];
+    {
+      const uint16_t* qrow = a.q + (((int64_t)b * a.T + t) * a.Hq + hq) * D;
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      // K layout [D/16][16 keys][16 d]: d = ds*32 + kq*8 .. +7 -> chunk 2*ds + kq/2, offset 8*(kq&1)
-      const int chunk = 2 * ds + (kq >> 1);
-      const int off = (chunk * PAGE + col) * 16 + 8 * (kq & 1);
-      bf16x8 ka = load_bf16x8(k0 + off);
-      bf16x8 kb = load_bf16x8(k1 + off);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[ds], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qb[ds], s1, 0, 0, 0);
+      for (int ds = 0; ds < DS; ++ds) {
+        if (row_live) qb[ds] = load_bf16x8(qrow + ds * 32 + kq * 8);
+        else qb[ds] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+      }
     }
-    // mask + online softmax (row = col; keys 4*kq+i of each page)
-    float sv[8];
-    float cmax = -__builtin_huge_valf();
+    const int64_t page_bytes = (int64_t)G::KBYTES;
+    const int64_t block_bytes = page_bytes * a.Hkv;
+    const uint8_t* kbase = (const uint8_t*)a.k_pool + h * page_bytes;
+    const uint8_t* vbase = (const uint8_t*)a.v_pool + h * page_bytes;
+    // block table through the constant address space: scalar loads, which count on lgkmcnt
+    // and so never wait for the page loads in flight on vmcnt
+    const cint32* trow = (const cint32*)(a.table + (int64_t)b * a.table_stride);
+    // pages past the split reload page p0 into a free slot (keeps the load count uniform)
+    auto issue = [&](int pg, int slot_idx) {
+      const int64_t blk = trow[pg < p1 ? pg : p0];
+      dma_page<D, CPW>(kbase + blk * block_bytes, vbase + blk * block_bytes,
+                       ring + slot_idx * G::BYTES, w, NW, lane);
+    };
+    wait_vmcnt<0>();  // Q has landed: the loop below then waits on page loads only
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int page = pg + (i >> 2);
-      const int key = 4 * kq + (i & 3);
-      const int pos = page * PAGE + key;
-      bool vis = pos < L && (i < 4 || has2);
-      if (vis && pos >= ctx) vis = (anc >> (pos - ctx)) & 1ull;
-      const float s = (i < 4 ? s0[i & 3] : s1[i & 3]) * a.qk_scale;
-      sv[i] = vis ? s : -__builtin_huge_valf();
-      cmax = sv[i] > cmax ? sv[i] : cmax;
+    for (int i = 0; i < RING - 1; ++i) issue(p0 + i, i);
+    int slot = 0;
+    for (int pg = p0; pg < p1; ++pg) {
+      wait_vmcnt<(RING - 2) * CPW>();  // this wave's loads of page pg have landed
+      block_barrier();                 // ... and every wave's; page pg - 1 is free
+      issue(pg + RING - 1, slot == 0 ? RING - 1 : slot - 1);
+      attend_page<D>(st, ring + slot * G::BYTES, qb, pg, L, ctx, anc, a.qk_scale, kq, col);
+      slot = slot == RING - 1 ? 0 : slot + 1;
     }
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-    const float m_new = fmaxf(m, cmax);
-    const float msafe = (m_new == -__builtin_huge_valf()) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - msafe);  // exp2(-inf) = 0
-    float psum = 0.f;
-    float p[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      p[i] = __builtin_amdgcn_exp2f(sv[i] - msafe);
-      psum += p[i];
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l = l * alpha + psum;
-    m = m_new;
-#pragma unroll
-    for (int i = 0; i < DT; ++i) o[i] *= alpha;
-    // P^T operand: slots 0..3 page 0 keys 4kq+i, slots 4..7 page 1 keys 4kq+i. P is carried
-    // as a bf16 pair (hi + lo residual), which keeps ~16 significant bits through the MFMA.
-    float plo[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) plo[i] = p[i] - bf16_to_f32(f32_to_bf16(p[i]));
-    u32x4 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                pack_bf16x2(p[6], p[7])};
-    u32x4 pwl = {pack_bf16x2(plo[0], plo[1]), pack_bf16x2(plo[2], plo[3]),
-                 pack_bf16x2(plo[4], plo[5]), pack_bf16x2(plo[6], plo[7])};
-    const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
-    const bf16x8 pbl = __builtin_bit_cast(bf16x8, pwl);
-    // O^T += V^T P^T ; V layout [4 key groups][D][4 keys]: keys 4kq..4kq+3 of d -> 8 bytes
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int d = dt * 16 + col;
-      const int off = (kq * D + d) * 4;
-      u32x2 va = *(const u32x2*)(v0 + off);
-      u32x2 vb = *(const u32x2*)(v1 + off);
-      if (!has2) vb = u32x2{0u, 0u};
-      u32x4 vv = {va.x, va.y, vb.x, vb.y};
-      const bf16x8 vt = __builtin_bit_cast(bf16x8, vv);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pb, o[dt], 0, 0, 0);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pbl, o[dt], 0, 0, 0);
-    }
+    wait_vmcnt<0>();  // no load may still target LDS when the workgroup retires
   }
   // partial results: O^T lane holds row col, d = dt*16 + 4*kq + i
-  const int64_t pidx = ((((int64_t)b * a.Hkv + h) * a.NRT + tile) * a.S + split);
+  const int64_t pidx = ((((int64_t)b * a.Hkv + h) * a.NRT + w) * a.S + split);
   float* po = a.part_o + pidx * 16 * D + (int64_t)col * D;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) *(floatx4*)(po + dt * 16 + 4 * kq) = o[dt];
+  for (int dt = 0; dt < DT; ++dt) *(floatx4*)(po + dt * 16 + 4 * kq) = st.o[dt];
   if (kq == 0) {
     float* pml = a.part_ml + (pidx * 16 + col) * 2;
-    pml[0] = m;
-    pml[1] = l;
+    pml[0] = st.m;
+    pml[1] = st.l;
   }
 }
 
-// Merge the splits of one (request, kv head, row tile): out = sum_s 2^(m_s-M) O_s / sum_s 2^(m_s-M) l_s
+// Merge the splits: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s. A block covers
+// MERGE_ROWS rows x MERGE_D columns of one (request, kv head, row tile); wave j computes the
+// split weights of row j, then thread (group sg, row, 4 columns) sums the splits s = sg mod
+// MERGE_SG, and the MERGE_SG partial sums are added in a fixed order.
+constexpr int MERGE_ROWS = 4, MERGE_D = 64, MERGE_SG = 4;
+constexpr int MERGE_THREADS = MERGE_ROWS * (MERGE_D / 4) * MERGE_SG;  // 256
+
 template <int D>
-__global__ void __launch_bounds__(256) attn_merge_kernel(AttnArgs a, uint16_t* __restrict__ out) {
-  __shared__ float w[16][SPLITS_MAX];  // per-row split weights
-  __shared__ float inv_l[16];
-  const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+__global__ void __launch_bounds__(MERGE_THREADS) attn_merge_kernel(AttnArgs a,
+                                                                  uint16_t* __restrict__ out) {
+  __shared__ float w[MERGE_ROWS][SPLITS_MAX];
+  __shared__ float inv_l[MERGE_ROWS];
+  __shared__ floatx4 red[MERGE_SG][MERGE_ROWS][MERGE_D / 4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int prog = blockIdx.x;  // (b, h, tile)
+  const int row0 = blockIdx.y * MERGE_ROWS;
+  const int d0 = blockIdx.z * MERGE_D;
+  const int tile = prog % a.NRT, h = (prog / a.NRT) % a.Hkv, b = prog / (a.NRT * a.Hkv);
   const int64_t pbase = (((int64_t)b * a.Hkv + h) * a.NRT + tile) * a.S;
-  if (threadIdx.x < 16) {
-    const int row = threadIdx.x;
+  {
+    const int row = row0 + wv;
     float M = -__builtin_huge_valf();
-    for (int s = 0; s < a.S; ++s) M = fmaxf(M, a.part_ml[((pbase + s) * 16 + row) * 2]);
+    for (int s = lane; s < a.S; s += 64) M = fmaxf(M, a.part_ml[((pbase + s) * 16 + row) * 2]);
+    M = wave_max(M);
     const float Ms = (M == -__builtin_huge_valf()) ? 0.f : M;
     float lsum = 0.f;
-    for (int s = 0; s < a.S; ++s) {
-      const float ms = a.part_ml[((pbase + s) * 16 + row) * 2];
-      const float ls = a.part_ml[((pbase + s) * 16 + row) * 2 + 1];
-      const float ws = __builtin_amdgcn_exp2f(ms - Ms);
-      w[row][s] = ws;
-      lsum += ws * ls;
+    for (int s = lane; s < a.S; s += 64) {
+      const float* ml = a.part_ml + ((pbase + s) * 16 + row) * 2;
+      const float ws = __builtin_amdgcn_exp2f(ml[0] - Ms);
+      w[wv][s] = ws;
+      lsum += ws * ml[1];
     }
-    inv_l[row] = lsum > 0.f ? 1.0f / lsum : 0.f;
+    lsum = wave_sum(lsum);
+    if (lane == 0) inv_l[wv] = lsum > 0.f ? 1.0f / lsum : 0.f;
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * D; idx += 256) {
-    const int row = idx / D, d = idx % D;
-    const int r = tile * 16 + row;
-    if (r >= a.T * a.G) continue;
-    float acc = 0.f;
-    for (int s = 0; s < a.S; ++s) acc += w[row][s] * a.part_o[((pbase + s) * 16 + row) * D + d];
-    const int t = r / a.G, g = r % a.G;
-    out[(((int64_t)b * a.T + t) * a.Hq + h * a.G + g) * D + d] = f32_to_bf16(acc * inv_l[row]);
+  const int sg = wv, rr = lane >> 4, d4 = lane & 15;
+  const int row = row0 + rr;
+  const float* po = a.part_o + (pbase * 16 + row) * D + d0 + 4 * d4;
+  const int64_t sstride = (int64_t)16 * D * MERGE_SG;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  int s = sg;
+  po += (int64_t)sg * 16 * D;
+  for (; s + 3 * MERGE_SG < a.S; s += 4 * MERGE_SG, po += 4 * sstride) {
+    const floatx4 x0 = *(const floatx4*)(po);
+    const floatx4 x1 = *(const floatx4*)(po + sstride);
+    const floatx4 x2 = *(const floatx4*)(po + 2 * sstride);
+    const floatx4 x3 = *(const floatx4*)(po + 3 * sstride);
+    acc += w[rr][s] * x0;
+    acc += w[rr][s + MERGE_SG] * x1;
+    acc += w[rr][s + 2 * MERGE_SG] * x2;
+    acc += w[rr][s + 3 * MERGE_SG] * x3;
   }
+  for (; s < a.S; s += MERGE_SG, po += sstride) acc += w[rr][s] * *(const floatx4*)po;
+  red[sg][rr][d4] = acc;
+  __syncthreads();
+  if (sg != 0) return;
+  floatx4 v = red[0][rr][d4];
+#pragma unroll
+  for (int j = 1; j < MERGE_SG; ++j) v += red[j][rr][d4];
+  const int rg = tile * 16 + row;
+  if (rg >= a.T * a.G) return;
+  const float il = inv_l[rr];
+  const int t = rg / a.G, g = rg % a.G;
+  uint16_t* dst = out + (((int64_t)b * a.T + t) * a.Hq + h * a.G + g) * D + d0 + 4 * d4;
+  *(u32x2*)dst = u32x2{pack_bf16x2(v[0] * il, v[1] * il), pack_bf16x2(v[2] * il, v[3] * il)};
 }
 
 inline int n_row_tiles(int T, int G) { return (T * G + 15) / 16; }
 
-int choose_splits(int64_t batch, int Hkv, int NRT, int64_t pages) {
-  // aim for ~2 waves of row-tile programs per CU, at least two pages per split
-  const int64_t programs = batch * Hkv * NRT;
-  int64_t s = (2 * 256 * 4 + programs - 1) / programs;
-  const int64_t max_by_pages = (pages + 1) / 2;
-  if (s > max_by_pages) s = max_by_pages;
-  if (s < 1) s = 1;
-  if (s > SPLITS_MAX) s = SPLITS_MAX;
-  return (int)s;
+int g_pages_per_split = 0;  // 0: automatic
+
+// Pages per split: about 128 workgroups over the launch (each keeps RING - 1 pages in flight),
+// at least two pages, at most SPLITS_MAX splits.
+int choose_pages_per_split(int64_t batch, int Hkv, int64_t pages) {
+  int64_t pps = g_pages_per_split;
+  if (pps <= 0) {
+    const int64_t heads = batch * Hkv;
+    const int64_t target = (128 + heads - 1) / heads;
+    pps = (pages + target - 1) / target;
+    if (pps < 2) pps = 2;
+  }
+  while ((pages + pps - 1) / pps > SPLITS_MAX) ++pps;
+  return (int)pps;
 }
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Loads per wave per page: the page's chunks over the NRT waves, rounded up to a power of two.
+template <int D>
+int launch_split(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
+  constexpr int CH = SlotGeo<D>::CHUNKS;
+  int cpw = 1;
+  while (cpw * a.NRT < CH) cpw *= 2;
+  const dim3 grid((unsigned)nblocks), block((unsigned)(64 * a.NRT));
+  switch (cpw) {
+    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1, 8>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2, 8>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4, 8>), grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((attn_split_kernel<D, 8, 8>), grid, block, 0, s, a); break;
+    case 16: hipLaunchKernelGGL((attn_split_kernel<D, 16, 4>), grid, block, 0, s, a); break;
+    default: return SV_ENOTSUP;
+  }
+  return SV_OK;
+}
 
 }  // namespace
 
@@ -276,10 +399,11 @@ SV_API int snowverify_paged_attention(const void* q, const void* k_pool, const v
                                       int64_t num_heads, int64_t num_kv_heads, int64_t head_size,
                                       int64_t page_size, int64_t table_stride, float scale,
                                       void* scratch, int64_t scratch_bytes, void* stream) {
-  if (batch <= 0 || tokens <= 0 || tokens > 64 || num_kv_heads <= 0 ||
-      num_heads % num_kv_heads || page_size != PAGE || table_stride <= 0)
+  if (batch <= 0 || tokens <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
+      page_size != PAGE || table_stride <= 0)
     return SV_EINVAL;
   if (head_size != 128 && head_size != 256) return SV_ENOTSUP;
+  if (n_row_tiles((int)tokens, (int)(num_heads / num_kv_heads)) > MAX_TILES) return SV_ENOTSUP;
   if (scratch_bytes < snowverify_paged_attention_scratch_bytes(batch, tokens, num_heads,
                                                               num_kv_heads, head_size))
     return SV_EINVAL;
@@ -296,27 +420,35 @@ SV_API int snowverify_paged_attention(const void* q, const void* k_pool, const v
   a.G = (int)(num_heads / num_kv_heads);
   a.NRT = n_row_tiles(a.T, a.G);
   a.table_stride = (int)table_stride;
-  a.S = choose_splits(batch, a.Hkv, a.NRT, table_stride);
-  a.pages_per_split = (int)((table_stride + a.S - 1) / a.S);
-  if (a.pages_per_split & 1) a.pages_per_split += 1;
+  a.pages_per_split = choose_pages_per_split(batch, a.Hkv, table_stride);
   a.S = (int)((table_stride + a.pages_per_split - 1) / a.pages_per_split);
   a.qk_scale = scale * kLog2e;
   const size_t parts = (size_t)batch * a.Hkv * a.NRT * SPLITS_MAX * 16;
   a.part_o = (float*)scratch;
   a.part_ml = (float*)((char*)scratch + align256(parts * head_size * 4));
   hipStream_t s = (hipStream_t)stream;
-  const int64_t nprog = batch * a.Hkv * a.NRT * a.S;
+  const int64_t nblocks = batch * a.Hkv * a.S;
+  const dim3 mgrid((unsigned)(batch * a.Hkv * a.NRT), 16 / MERGE_ROWS, (unsigned)(head_size / MERGE_D));
+  int rc;
   if (head_size == 128) {
-    hipLaunchKernelGGL(attn_split_kernel<128>, dim3((unsigned)nprog), dim3(64), 0, s, a);
+    rc = launch_split<128>(a, nblocks, s);
+    if (rc != SV_OK) return rc;
     SV_CHECK_LAUNCH();
-    hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(a.NRT, a.Hkv, (unsigned)batch), dim3(256), 0,
-                       s, a, (uint16_t*)out);
+    hipLaunchKernelGGL(attn_merge_kernel<128>, mgrid, dim3(MERGE_THREADS), 0, s, a, (uint16_t*)out);
   } else {
-    hipLaunchKernelGGL(attn_split_kernel<256>, dim3((unsigned)nprog), dim3(64), 0, s, a);
+    rc = launch_split<256>(a, nblocks, s);
+    if (rc != SV_OK) return rc;
     SV_CHECK_LAUNCH();
-    hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(a.NRT, a.Hkv, (unsigned)batch), dim3(256), 0,
-                       s, a, (uint16_t*)out);
+    hipLaunchKernelGGL(attn_merge_kernel<256>, mgrid, dim3(MERGE_THREADS), 0, s, a, (uint16_t*)out);
   }
   SV_CHECK_LAUNCH();
   return SV_OK;
+}
+
+// Tuning knob (extension, no reference counterpart): pages per split of the attention's
+// context split (0 restores the automatic choice). Returns the previous value.
+SV_API int snowverify_attention_pages_per_split(int pages) {
+  const int prev = g_pages_per_split;
+  g_pages_per_split = pages < 0 ? 0 : pages;
+  return prev;
 }

@@ -32,12 +32,16 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 }
 
 // Round-to-nearest-even float -> bf16 (NaN kept quiet).
+// Round to nearest even (NaN stays NaN): the gfx950 v_cvt_pk_bf16_f32 conversion.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
-  uint32_t lsb = (u >> 16) & 1u;
-  u += 0x7fffu + lsb;
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// Two floats -> packed bf16 pair (a in the low half), one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){a, b}, b2_t));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {

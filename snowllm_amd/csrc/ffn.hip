@@ -17,37 +17,63 @@ using namespace kq;
 inline hipStream_t Sx(void* s) { return (hipStream_t)s; }
 
 // ---------------------------------------------------------------------------------------
-// residual + RMSNorm + operand conversion. One wave per (row tile, superblock): every wave
-// computes the row statistics over the full row (a few KiB from L2) and converts its own
-// superblock. v = bf16(x + res_in) (v = x without res_in) is written to res_out by the wave
-// owning those columns (res_out must not alias x or res_in: other waves still read them),
-// y = bf16(v * inv * gamma), optional bf16 copy of y, fp16 operands of y into the workspace.
+// residual + RMSNorm + operand conversion. One block per 16-row tile, one wave per superblock
+// (waves loop when H > 16 superblocks), so x and the residual are read from HBM once:
+//   v = bf16(x + res_in) (v = x without res_in) -> res_out
+//   y = bf16(v * rsqrt(mean(v^2) + eps) * gamma) -> y_out (optional), fp16 operands -> ws
+// The row sums of squares meet in LDS and are added over the waves in a fixed order. Lane
+// (r = lane & 15, kq = lane >> 4) owns k = 32 j + 8 kq .. + 7 of each sub-block j, the layout
+// the operand conversion consumes, so y never leaves registers.
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(64) norm_prep_kernel(
+constexpr int NORM_MAX_WAVES = 16;
+
+__device__ __forceinline__ void residual_words(const uint16_t* __restrict__ x,
+                                               const uint16_t* __restrict__ residual, int64_t off,
+                                               u32x4& v) {
+  const u32x4 xv = *(const u32x4*)(x + off);
+  if (!residual) {
+    v = xv;
+    return;
+  }
+  const u32x4 rv = *(const u32x4*)(residual + off);
+  const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, rw[4] = {rv.x, rv.y, rv.z, rv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = __uint_as_float(xw[i] << 16) + __uint_as_float(rw[i] << 16);
+    const float b = __uint_as_float(xw[i] & 0xffff0000u) + __uint_as_float(rw[i] & 0xffff0000u);
+    o[i] = pack_bf16x2(a, b);
+  }
+  v = u32x4{o[0], o[1], o[2], o[3]};
+}
+
+__global__ void __launch_bounds__(NORM_MAX_WAVES * 64) norm_prep_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
     uint16_t* __restrict__ res_out, const uint16_t* __restrict__ gamma,
     uint16_t* __restrict__ y_out, void* __restrict__ ws, size_t tile_bytes, int64_t M, int64_t H,
     float eps) {
-  const int s = blockIdx.x, tile = blockIdx.y;
-  const int lane = threadIdx.x, r = lane & 15, kq = lane >> 4;
-  const int64_t S = H / QK;
+  __shared__ float part[NORM_MAX_WAVES][16];
+  const int tile = blockIdx.x;
+  const int NW = (int)(blockDim.x >> 6);
+  const int lane = threadIdx.x & 63, r = lane & 15, kq = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int S = (int)(H / QK);
   const int64_t row = (int64_t)tile * TILE_M + r;
   const bool live = row < M;
-  // 1) sum of squares of v = bf16(x + residual) over the row (this lane: k = 8 (4 i + kq) ..)
+  const int64_t base = row * H + kq * 8;
+  // 1) v for this wave's first superblock (kept), sum of squares over all of its superblocks
+  u32x4 v0[8];
   float ss = 0.f;
-  if (live) {
-    for (int64_t k0 = kq * 8; k0 < H; k0 += 32) {
-      const u32x4 xv = *(const u32x4*)(x + row * H + k0);
-      u32x4 rv = {0u, 0u, 0u, 0u};
-      if (residual) rv = *(const u32x4*)(residual + row * H + k0);
-      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, rw[4] = {rv.x, rv.y, rv.z, rv.w};
+  for (int s = w; s < S; s += NW) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (live) residual_words(x, residual, base + (int64_t)s * QK + j * 32, v);
+      if (s == w) v0[j] = v;
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float a = __uint_as_float(xw[i] << 16), b = __uint_as_float(xw[i] & 0xffff0000u);
-        if (residual) {
-          a = bf16_to_f32(f32_to_bf16(a + __uint_as_float(rw[i] << 16)));
-          b = bf16_to_f32(f32_to_bf16(b + __uint_as_float(rw[i] & 0xffff0000u)));
-        }
+        const float a = __uint_as_float(vw[i] << 16), b = __uint_as_float(vw[i] & 0xffff0000u);
         ss = __builtin_fmaf(a, a, ss);
         ss = __builtin_fmaf(b, b, ss);
       }
@@ -55,51 +81,39 @@ __global__ void __launch_bounds__(64) norm_prep_kernel(
   }
   ss += __shfl_xor(ss, 16, 64);
   ss += __shfl_xor(ss, 32, 64);
-  const float inv = __frsqrt_rn(ss / (float)H + eps);
-  // 2) this superblock: update residual, normalise, stage bf16 y in LDS for the conversion
-  __shared__ uint16_t ybuf[16][QK];
-  if (live) {
+  if (kq == 0) part[w][r] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (int ww = 0; ww < NW; ++ww) tot += part[ww][r];
+  const float inv = __frsqrt_rn(tot / (float)H + eps);
+  // 2) residual out, y, operands
+  XPrepView view = xprep_view((char*)ws + tile * tile_bytes, S);
+  for (int s = w; s < S; s += NW) {
+    u32x4 yw[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int64_t k0 = (int64_t)s * QK + j * 32 + kq * 8;
-      const u32x4 xv = *(const u32x4*)(x + row * H + k0);
-      u32x4 rv = {0u, 0u, 0u, 0u};
-      if (residual) rv = *(const u32x4*)(residual + row * H + k0);
+      u32x4 v = v0[j];
+      if (s != w && live) residual_words(x, residual, base + (int64_t)s * QK + j * 32, v);
       const u32x4 gv = *(const u32x4*)(gamma + k0);
-      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, rw[4] = {rv.x, rv.y, rv.z, rv.w};
-      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
-      uint32_t nres[4], yw[4];
+      const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+      uint32_t o[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float a = __uint_as_float(xw[i] << 16), b = __uint_as_float(xw[i] & 0xffff0000u);
-        if (residual) {
-          a = bf16_to_f32(f32_to_bf16(a + __uint_as_float(rw[i] << 16)));
-          b = bf16_to_f32(f32_to_bf16(b + __uint_as_float(rw[i] & 0xffff0000u)));
-        }
-        nres[i] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-        const uint16_t ya = f32_to_bf16(a * inv * __uint_as_float(gw[i] << 16));
-        const uint16_t yb = f32_to_bf16(b * inv * __uint_as_float(gw[i] & 0xffff0000u));
-        yw[i] = (uint32_t)ya | ((uint32_t)yb << 16);
+        o[i] = pack_bf16x2(__uint_as_float(vw[i] << 16) * inv * __uint_as_float(gw[i] << 16),
+                           __uint_as_float(vw[i] & 0xffff0000u) * inv *
+                               __uint_as_float(gw[i] & 0xffff0000u));
       }
-      if (res_out) *(u32x4*)(res_out + row * H + k0) = u32x4{nres[0], nres[1], nres[2], nres[3]};
-      const u32x4 yv = {yw[0], yw[1], yw[2], yw[3]};
-      if (y_out) *(u32x4*)(y_out + row * H + k0) = yv;
-      *(u32x4*)&ybuf[r][j * 32 + kq * 8] = yv;
+      yw[j] = live ? u32x4{o[0], o[1], o[2], o[3]} : u32x4{0u, 0u, 0u, 0u};
+      if (live) {
+        if (res_out) *(u32x4*)(res_out + row * H + k0) = v;
+        if (y_out) *(u32x4*)(y_out + row * H + k0) = yw[j];
+      }
     }
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *(u32x4*)&ybuf[r][j * 32 + kq * 8] = u32x4{0u, 0u, 0u, 0u};
+    XOperands op;
+    convert_words(yw, lane, op);
+    store_operands(view, s, lane, op);
   }
-  __syncthreads();
-  // 3) fp16 operands of this superblock (src = ybuf, superblock 0 of a 256-wide row)
-  XPrepView v = xprep_view((char*)ws + tile * tile_bytes, S);
-  XOperands o;
-  convert_superblock(&ybuf[0][0], QK, 16, 0, lane, o);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v.xop[((int64_t)s * 8 + j) * 64 + lane] = o.x[j];
-  v.sxop[((int64_t)s * 2 + 0) * 64 + lane] = o.sx0;
-  v.sxop[((int64_t)s * 2 + 1) * 64 + lane] = o.sx1;
-  if (kq == 0) v.scale[(int64_t)s * 16 + r] = o.scale;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -274,39 +288,140 @@ __global__ void __launch_bounds__(NW * 64) gate_up_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
-// MoE plan: unique experts touched by the block (ascending id), the (row, k) pair of each
-// row routed to each, then the shared expert as the last slot. One block.
+// MoE routing (transformers qwen3_next semantics): softmax over the E routed logits in fp32,
+// top-k (ties to the lower expert id), renormalised; the logit in column E is the shared
+// expert's gate, applied as sigmoid. Wave m routes row m with the row's logits in registers
+// (expert e = lane + 64 i), k rounds of a wave arg-max.
+//
+// MoE plan: the unique experts the block touches in ascending id (a ballot prefix count over
+// the 256 expert flags), the (row, k) pair of each row routed to each, then the shared expert
+// as the last slot. Routing and plan run in one block so the ids never leave LDS.
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t* __restrict__ ids, int M,
-                                                       int topk, int E, int shared,
-                                                       MoePlan* __restrict__ plan) {
-  __shared__ uint32_t mask[256];
-  __shared__ int32_t slot_of[256];
-  const int t = threadIdx.x;
-  for (int e = t; e < 256; e += 256) mask[e] = 0;
-  __syncthreads();
-  for (int p = t; p < M * topk; p += 256) {
-    const int e = ids[p];
+constexpr int ROUTE_THREADS = 1024;  // 16 waves: one per row (M <= 16), four for the plan
+
+__device__ __forceinline__ void route_row(const float* __restrict__ l, int E, int topk, int lane,
+                                          float& my_p, int& my_id, float& ksum) {
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? l[e] : -__builtin_huge_valf();
+  }
+  float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (lane + 64 * i < E) sum += __expf(v[i] - mx);
+  sum = wave_sum(sum);
+  uint32_t taken = 0;
+  my_p = 0.f;
+  my_id = -1;
+  for (int k = 0; k < topk; ++k) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && !((taken >> i) & 1u)) {
+        const uint64_t key = argmax_key(v[i], (uint32_t)e);
+        best = key > best ? key : best;
+      }
+    }
+    best = wave_max_u64(best);
+    const int e = (int)argmax_key_index(best);
+    const int ei = e >> 6;  // wave-uniform
+    if ((e & 63) == lane) taken |= 1u << ei;
+    const float mine = ei == 0 ? v[0] : ei == 1 ? v[1] : ei == 2 ? v[2] : v[3];
+    const float p = __expf(__shfl(mine, e & 63, 64) - mx) / sum;
+    if (lane == k) {
+      my_p = p;
+      my_id = e;
+    }
+  }
+  ksum = 0.f;
+  for (int k = 0; k < topk; ++k) ksum += __shfl(my_p, k, 64);
+}
+
+// Plan from ids_s[M * topk] in LDS; all ROUTE_THREADS threads call it.
+__device__ __forceinline__ void build_plan(const int32_t* ids_s, int M, int topk, int E, int shared,
+                                          uint32_t* mask, int32_t* slot_of, int32_t* wave_cnt,
+                                          MoePlan* __restrict__ plan) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  for (int p = t; p < M * topk; p += blockDim.x) {
+    const int e = ids_s[p];
     if (e >= 0 && e < E) atomicOr(&mask[e], 1u << (p / topk));
   }
   __syncthreads();
-  if (t == 0) {
-    int n = 0;
-    for (int e = 0; e < E; ++e) {
-      slot_of[e] = mask[e] ? n : -1;
-      if (mask[e]) plan->slot_expert[n++] = e;
+  bool used = false;
+  int before = 0;
+  if (w < 4) {
+    used = t < E && mask[t] != 0u;
+    const uint64_t bal = __ballot(used);
+    before = __popcll(bal & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_cnt[w] = __popcll(bal);
+  }
+  for (int i = t; i < 136 * 16; i += blockDim.x) plan->pair_of[i / 16][i % 16] = -1;
+  __syncthreads();
+  if (w < 4) {
+    int off = 0;
+    for (int ww = 0; ww < w; ++ww) off += wave_cnt[ww];
+    slot_of[t] = used ? off + before : -1;
+    if (used) plan->slot_expert[off + before] = t;
+    if (t == 0) {
+      const int n = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+      plan->n_routed = n;
+      if (shared) plan->slot_expert[n] = E;
+      plan->n_slots = n + (shared ? 1 : 0);
     }
-    plan->n_routed = n;
-    if (shared) plan->slot_expert[n++] = E;
-    plan->n_slots = n;
   }
   __syncthreads();
-  for (int i = t; i < 136 * 16; i += 256) plan->pair_of[i / 16][i % 16] = -1;
-  __syncthreads();
-  for (int p = t; p < M * topk; p += 256) {
-    const int e = ids[p];
+  for (int p = t; p < M * topk; p += blockDim.x) {
+    const int e = ids_s[p];
     if (e >= 0 && e < E) plan->pair_of[slot_of[e]][p / topk] = p;
   }
+}
+
+__global__ void __launch_bounds__(ROUTE_THREADS) moe_route_plan_kernel(
+    const float* __restrict__ logits, int64_t stride, int M, int E, int topk,
+    float* __restrict__ weights, int32_t* __restrict__ ids, float* __restrict__ shared_w,
+    MoePlan* __restrict__ plan) {
+  __shared__ int32_t ids_s[16 * 16];
+  __shared__ uint32_t mask[256];
+  __shared__ int32_t slot_of[256];
+  __shared__ int32_t wave_cnt[4];
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  if (t < 256) mask[t] = 0u;
+  if (w < M) {
+    const float* l = logits + (int64_t)w * stride;
+    const float gate = shared_w ? l[E] : 0.f;
+    float my_p, ksum;
+    int my_id;
+    route_row(l, E, topk, lane, my_p, my_id, ksum);
+    if (lane < topk) {
+      weights[w * topk + lane] = my_p / ksum;
+      ids[w * topk + lane] = my_id;
+      ids_s[w * topk + lane] = my_id;
+    }
+    if (lane == 0 && shared_w) shared_w[w] = 1.0f / (1.0f + __expf(-gate));
+  }
+  if (!plan) return;
+  __syncthreads();
+  build_plan(ids_s, M, topk, E, shared_w != nullptr, mask, slot_of, wave_cnt, plan);
+}
+
+__global__ void __launch_bounds__(ROUTE_THREADS) moe_plan_kernel(const int32_t* __restrict__ ids,
+                                                                int M, int topk, int E, int shared,
+                                                                MoePlan* __restrict__ plan) {
+  __shared__ int32_t ids_s[16 * 16];
+  __shared__ uint32_t mask[256];
+  __shared__ int32_t slot_of[256];
+  __shared__ int32_t wave_cnt[4];
+  const int t = threadIdx.x;
+  if (t < 256) mask[t] = 0u;
+  if (t < M * topk) ids_s[t] = ids[t];
+  __syncthreads();
+  build_plan(ids_s, M, topk, E, shared, mask, slot_of, wave_cnt, plan);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -418,7 +533,8 @@ SV_API int snowverify_norm_prep(const void* x, const void* res_in, void* res_out
   if (M <= 0 || H <= 0 || H % 256) return SV_EINVAL;
   if (res_out && (res_out == x || res_out == res_in)) return SV_EINVAL;
   const int64_t S = H / 256, mt = (M + 15) / 16;
-  hipLaunchKernelGGL(norm_prep_kernel, dim3((unsigned)S, (unsigned)mt), dim3(64), 0, Sx(stream),
+  const int nw = (int)(S < NORM_MAX_WAVES ? S : NORM_MAX_WAVES);
+  hipLaunchKernelGGL(norm_prep_kernel, dim3((unsigned)mt), dim3(64 * nw), 0, Sx(stream),
                      (const uint16_t*)x, (const uint16_t*)res_in, (uint16_t*)res_out,
                      (const uint16_t*)gamma, (uint16_t*)y_out, ws, xprep_tile_bytes(S), M, H, eps);
   SV_CHECK_LAUNCH();
@@ -486,8 +602,36 @@ SV_API int64_t snowverify_moe_plan_bytes(void) { return (int64_t)sizeof(MoePlan)
 SV_API int snowverify_moe_plan(const int32_t* ids, int64_t M, int64_t topk, int64_t E, int shared,
                                void* plan, void* stream) {
   if (M <= 0 || M > 16 || topk <= 0 || M * topk > 135 || E <= 0 || E > 256) return SV_EINVAL;
-  hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, Sx(stream), ids, (int)M, (int)topk,
-                     (int)E, shared, (MoePlan*)plan);
+  hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(ROUTE_THREADS), 0, Sx(stream), ids, (int)M,
+                     (int)topk, (int)E, shared, (MoePlan*)plan);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// MoE routing from router logits [M, stride] f32 (E routed columns, then the shared expert's
+// gate in column E when shared_w is given): weights/ids [M, topk], shared_w [M].
+SV_API int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, int64_t E,
+                                int64_t topk, float* weights, int32_t* ids, float* shared_w,
+                                void* stream) {
+  if (M < 0 || M > 16 || E <= 0 || E > 256 || topk <= 0 || topk > 16 || topk > E ||
+      stride < E + (shared_w ? 1 : 0))
+    return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(ROUTE_THREADS), 0, Sx(stream), logits,
+                     stride, (int)M, (int)E, (int)topk, weights, ids, shared_w, nullptr);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Routing and plan in one launch (the plan's shared slot exists when shared_w is given).
+SV_API int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_t M, int64_t E,
+                                     int64_t topk, float* weights, int32_t* ids, float* shared_w,
+                                     void* plan, void* stream) {
+  if (M <= 0 || M > 16 || E <= 0 || E > 256 || topk <= 0 || topk > 16 || topk > E ||
+      M * topk > 135 || stride < E + (shared_w ? 1 : 0) || !plan)
+    return SV_EINVAL;
+  hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(ROUTE_THREADS), 0, Sx(stream), logits,
+                     stride, (int)M, (int)E, (int)topk, weights, ids, shared_w, (MoePlan*)plan);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }

@@ -26,17 +26,13 @@ using namespace kq;
 __global__ void __launch_bounds__(64) xprep_kernel(const uint16_t* __restrict__ a, int64_t M,
                                                    int64_t K, void* ws, size_t tile_bytes) {
   const int s = blockIdx.x, tile = blockIdx.y;
-  const int lane = threadIdx.x, r = lane & 15, kq = lane >> 4;
+  const int lane = threadIdx.x;
   const int64_t S = K / QK;
   XPrepView v = xprep_view((char*)ws + tile * tile_bytes, S);
   const int64_t r0 = (int64_t)tile * TILE_M;
   XOperands o;
   convert_superblock(a + r0 * K, K, (int)(M - r0 < TILE_M ? M - r0 : TILE_M), s, lane, o);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v.xop[((int64_t)s * 8 + j) * 64 + lane] = o.x[j];
-  v.sxop[((int64_t)s * 2 + 0) * 64 + lane] = o.sx0;
-  v.sxop[((int64_t)s * 2 + 1) * 64 + lane] = o.sx1;
-  if (kq == 0) v.scale[(int64_t)s * 16 + r] = o.scale;
+  store_operands(v, s, lane, o);
 }
 
 // NW waves split the superblocks of NTILE column tiles; the waves' partial sums meet in LDS

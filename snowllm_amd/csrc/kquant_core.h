@@ -67,16 +67,10 @@ struct XOperands {
   float scale;     // 2^e of this lane's row
 };
 
-__device__ __forceinline__ void convert_superblock(const uint16_t* __restrict__ src,
-                                                   int64_t row_stride, int rows_valid, int s,
-                                                   int lane, XOperands& o) {
-  const int r = lane & 15, kq = lane >> 4;
-  const bool live = r < rows_valid;
-  u32x4 raw[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    raw[j] = live ? *(const u32x4*)(src + r * row_stride + (int64_t)s * QK + j * 32 + kq * 8)
-                  : u32x4{0u, 0u, 0u, 0u};
+// Conversion of one lane's 64 bf16 values: raw[j] holds k = 32 j + 8 kq .. + 7 of sub-block
+// j in natural order (two bf16 per dword, low half first).
+__device__ __forceinline__ void convert_words(const u32x4 (&raw)[8], int lane, XOperands& o) {
+  const int kq = lane >> 4;
   float mx = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -128,6 +122,29 @@ __device__ __forceinline__ void convert_superblock(const uint16_t* __restrict__ 
   o.scale = __builtin_ldexpf(1.0f, e);
 }
 
+__device__ __forceinline__ void convert_superblock(const uint16_t* __restrict__ src,
+                                                   int64_t row_stride, int rows_valid, int s,
+                                                   int lane, XOperands& o) {
+  const int r = lane & 15, kq = lane >> 4;
+  const bool live = r < rows_valid;
+  u32x4 raw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    raw[j] = live ? *(const u32x4*)(src + r * row_stride + (int64_t)s * QK + j * 32 + kq * 8)
+                  : u32x4{0u, 0u, 0u, 0u};
+  convert_words(raw, lane, o);
+}
+
+// Store one superblock's operands into the workspace view.
+__device__ __forceinline__ void store_operands(const XPrepView& v, int64_t s, int lane,
+                                               const XOperands& o) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v.xop[(s * 8 + j) * 64 + lane] = o.x[j];
+  v.sxop[(s * 2 + 0) * 64 + lane] = o.sx0;
+  v.sxop[(s * 2 + 1) * 64 + lane] = o.sx1;
+  if ((lane >> 4) == 0) v.scale[s * 16 + (lane & 15)] = o.scale;
+}
+
 // ---------------------------------------------------------------------------------------
 // Decoders: packed words -> fp16 MFMA B operands (slot order kperm).
 // ---------------------------------------------------------------------------------------
@@ -136,12 +153,10 @@ __device__ __forceinline__ half8 as_half8(uint32_t a, uint32_t b, uint32_t c, ui
   return __builtin_bit_cast(half8, v);
 }
 
-// (w & mask) | orv in one VALU op. GFX9 VOP3 may read one scalar register, so the OR constant
-// is passed in a vector register (materialised once, outside the loops).
+// (w & mask) | orv: written in plain C so that the compiler, which tracks the wait states
+// between VALU writes and in-flight MFMA reads, emits and schedules the v_and_or_b32 itself.
 __device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t orv) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(orv));
-  return r;
+  return (w & mask) | orv;
 }
 
 // Q4_K group (two dwords = 8 bytes of one 32-byte nibble group): low nibbles -> sub-block 2g
@@ -335,13 +350,13 @@ __device__ __forceinline__ GemvStreams make_streams(const void* quant, const voi
   return st;
 }
 
-// The decoders' 0x6400 exponent pattern, kept in a vector register.
+// The decoders' 0x6400 exponent pattern, held in a vector register: a VOP3 v_and_or_b32 may
+// read one scalar operand, the mask. The identity DPP move makes the value opaque to constant
+// folding while remaining an ordinary instruction for the compiler's hazard tracking.
 template <int FMT>
 __device__ __forceinline__ uint32_t decode_magic() {
-  const uint32_t Mc = __builtin_amdgcn_readfirstlane(FMT == FMT_Q4_K ? 0x64006400u : 0x64646464u);
-  uint32_t Mv;
-  asm("v_mov_b32 %0, %1" : "=v"(Mv) : "s"(Mc));
-  return Mv;
+  constexpr int M = FMT == FMT_Q4_K ? 0x64006400 : 0x64646464;
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, M, 0xE4, 0xF, 0xF, false);
 }
 
 // Wave w of NW walks superblocks s = w, w + NW, ... of the tiles tile0 + t * tstride, with the

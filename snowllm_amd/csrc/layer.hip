@@ -232,61 +232,6 @@ __global__ void add_bf16_kernel(const uint16_t* __restrict__ a, const uint16_t* 
   if (i < n) out[i] = f32_to_bf16(bf16_to_f32(a[i]) + bf16_to_f32(b[i]));
 }
 
-// ---------------------------------------------------------------------------------------
-// MoE routing (transformers qwen3_next semantics): softmax over the E routed logits in fp32,
-// top-k (ties to the lower expert id), renormalised; the logit in column E is the shared
-// expert's gate, applied as sigmoid. One wave per row.
-// ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(64) moe_route_kernel(const float* __restrict__ logits,
-                                                       int64_t stride, int E, int topk,
-                                                       float* __restrict__ weights,
-                                                       int32_t* __restrict__ ids,
-                                                       float* __restrict__ shared_w) {
-  const int64_t m = blockIdx.x;
-  const float* l = logits + m * stride;
-  const int lane = threadIdx.x;
-  // softmax statistics
-  float mx = -__builtin_huge_valf();
-  for (int e = lane; e < E; e += 64) mx = fmaxf(mx, l[e]);
-  mx = wave_max(mx);
-  float sum = 0.f;
-  for (int e = lane; e < E; e += 64) sum += __expf(l[e] - mx);
-  sum = wave_sum(sum);
-  // top-k by repeated arg-max over (value, lower id)
-  float chosen_p[16];
-  int chosen_id[16];
-  uint64_t taken_lo = 0, taken_hi = 0, taken2 = 0, taken3 = 0;  // up to 256 experts
-  float ksum = 0.f;
-  for (int k = 0; k < topk; ++k) {
-    uint64_t best = 0;
-    for (int e = lane; e < E; e += 64) {
-      const int w = e >> 6;
-      const uint64_t tk = w == 0 ? taken_lo : w == 1 ? taken_hi : w == 2 ? taken2 : taken3;
-      if ((tk >> (e & 63)) & 1ull) continue;
-      const uint64_t key = argmax_key(l[e], (uint32_t)e);
-      best = key > best ? key : best;
-    }
-    best = wave_max_u64(best);
-    const int e = (int)argmax_key_index(best);
-    const int w = e >> 6;
-    if (w == 0) taken_lo |= 1ull << (e & 63);
-    else if (w == 1) taken_hi |= 1ull << (e & 63);
-    else if (w == 2) taken2 |= 1ull << (e & 63);
-    else taken3 |= 1ull << (e & 63);
-    const float p = __expf(l[e] - mx) / sum;
-    chosen_p[k] = p;
-    chosen_id[k] = e;
-    ksum += p;
-  }
-  if (lane == 0) {
-    for (int k = 0; k < topk; ++k) {
-      weights[m * topk + k] = chosen_p[k] / ksum;
-      ids[m * topk + k] = chosen_id[k];
-    }
-    if (shared_w) shared_w[m] = 1.0f / (1.0f + __expf(-l[E]));
-  }
-}
-
 }  // namespace
 
 // =======================================================================================
@@ -454,17 +399,3 @@ SV_API int snowverify_add_bf16(const void* a, const void* b, void* out, int64_t 
   return SV_OK;
 }
 
-// Extension: MoE routing from router logits [M, stride] f32 (E routed columns, then the shared
-// expert's gate in column E when shared_w is given): weights/ids [M, topk], shared_w [M].
-SV_API int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, int64_t E,
-                                int64_t topk, float* weights, int32_t* ids, float* shared_w,
-                                void* stream) {
-  if (M < 0 || E <= 0 || E > 256 || topk <= 0 || topk > 16 || topk > E ||
-      stride < E + (shared_w ? 1 : 0))
-    return SV_EINVAL;
-  if (M == 0) return SV_OK;
-  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)M), dim3(64), 0, S(stream), logits, stride,
-                     (int)E, (int)topk, weights, ids, shared_w);
-  SV_CHECK_LAUNCH();
-  return SV_OK;
-}

@@ -129,6 +129,16 @@ def moe_plan(ids, E, plan, shared=True):
     check(lib.snowverify_moe_plan(_p(ids), M, topk, E, int(shared), _p(plan), _stream()), "moe_plan")
 
 
+def moe_route_plan(logits, E, topk, weights, ids, shared_w, plan):
+    """moe_route + moe_plan in one launch (shared-expert slot iff shared_w is given)."""
+    M = logits.shape[0]
+    _chk(weights, "routing weights", torch.float32, M, topk)
+    _chk(ids, "routing ids", torch.int32, M, topk)
+    check(lib.snowverify_moe_route_plan(_p(logits), logits.stride(0), M, E, topk, _p(weights),
+                                        _p(ids), _p(shared_w), _p(plan), _stream()),
+          "moe_route_plan")
+
+
 def moe_experts(fmt, gu, dn, sh_gu, sh_dn, plan, ws, weights, shared_w, act, pairs, shared_out,
                 out, M, topk, E, H, F):
     """gu/dn/sh_gu/sh_dn: (quant, meta) pairs of the stacked expert weights."""

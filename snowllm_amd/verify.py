@@ -93,16 +93,33 @@ def tree_depths(parents):
 # ---------------------------------------------------------------------------------------
 # random-init weights (GPU)
 # ---------------------------------------------------------------------------------------
-def gguf_random(fmt, n, k, seed, device="cuda"):
+def gguf_random(fmt, n, k, seed, device="cuda", centered=False):
     """Seeded random GGUF blocks for an [n, k] weight: Q4_K with 6-bit scales/mins and nibbles
     uniform and d, dmin = fp16(|N(0, 1e-3^2)|); Q8_0 with int8 uniform in
-    -127..127 and d = fp16(|N(0, 1e-2^2)|)."""
+    -127..127 and d = fp16(|N(0, 1e-2^2)|).
+
+    centered (model weights): Q4_K blocks whose dequantised values are zero-mean, as GGUF
+    blocks quantised from a trained matrix are (the min offsets one sub-block's range):
+    d = fp16(|N(0, (2e-4)^2)|), dmin = fp16(8 d), m_j = round(0.9375 sc_j), so that
+    w = d sc_j q - dmin m_j ~ d sc_j (q - 7.5). Uniform raw mins put a common-mode component
+    into every projection, which makes all rows of a block route to the same experts."""
     g = torch.Generator(device=device).manual_seed(seed)
     if fmt == Q4_K:
         nb = n * k // 256
         raw = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, device=device, generator=g)
-        dd = (torch.randn(nb, 2, device=device, generator=g) * 1e-3).abs().half()
+        if not centered:
+            dd = (torch.randn(nb, 2, device=device, generator=g) * 1e-3).abs().half()
+            raw[:, 0:4] = dd.view(torch.uint8).view(nb, 4)
+            return raw.view(-1)
+        d = (torch.randn(nb, device=device, generator=g) * 2e-4).abs()
+        dd = torch.stack([d, 8 * d], 1).half()
         raw[:, 0:4] = dd.view(torch.uint8).view(nb, 4)
+        sc = torch.randint(0, 64, (nb, 8), dtype=torch.int32, device=device, generator=g)
+        mn = torch.round(sc.float() * 0.9375).int().clamp_(0, 63)
+        lo = (sc[:, :4] & 63) | ((sc[:, 4:] >> 4) << 6)
+        mid = (mn[:, :4] & 63) | ((mn[:, 4:] >> 4) << 6)
+        hi = (sc[:, 4:] & 15) | ((mn[:, 4:] & 15) << 4)
+        raw[:, 4:16] = torch.cat([lo, mid, hi], 1).to(torch.uint8)
         return raw.view(-1)
     if fmt == Q8_0:
         nb = n * k // 32
@@ -116,7 +133,7 @@ def gguf_random(fmt, n, k, seed, device="cuda"):
 
 
 def packed_random(fmt, n, k, seed, keep_raw=False):
-    raw = gguf_random(fmt, n, k, seed)
+    raw = gguf_random(fmt, n, k, seed, centered=True)
     quant, meta = ops.gemm_kquant_shuffle_b(fmt, raw, n, k)
     return (quant, meta, raw if keep_raw else None)
 
@@ -292,9 +309,8 @@ class VerifyModel:
                                res_out=res_out, y_out=self.h2)
                 Lops.dense_gemv(Lops.WT_BF16, lw.router, self.h2, self.router_logits, T,
                                 c.experts + 1, H)
-                Lops.moe_route(self.router_logits, c.experts, c.topk, self.route_w,
-                               self.route_ids, self.shared_w)
-                Lops.moe_plan(self.route_ids, c.experts, self.plan, shared=True)
+                Lops.moe_route_plan(self.router_logits, c.experts, c.topk, self.route_w,
+                                    self.route_ids, self.shared_w, self.plan)
                 Lops.moe_experts(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, self.plan,
                                  self.ws_h2, self.route_w, self.shared_w, self.moe_act,
                                  self.pairs, self.shared_out, self.x, T, c.topk, c.experts, H,
@@ -361,6 +377,8 @@ class Acceptance:
         if self.chain_logits is not None:
             torch.index_select(logits, 0, self.chain_index, out=self.chain_logits)
             src = self.chain_logits
+        elif logits.shape[0] != self.T:
+            src = logits[:self.T]  # chain = leading rows of the block (contiguous view)
         ops.probabilities(src, self.top_k, self.top_p, self.temp, self.V, self.p, self.pid, self.ws)
         ops.dflash.reject(self.p, self.pid, self.drafts, self.qid, self.q, self.slot, self.valid,
                           self.uniform, self.out, self.accepted)
