@@ -8,7 +8,13 @@ achieved HBM GB/s vs peak"), the roofline of the dominant kernel (algorithmic by
 timed on this host's cores over a bounded sample.
 
 Workloads:
-  gemv   BASELINE config 2: one Q4_K dequant-GEMV, M=9, K=4096, N=14336, bf16 out.
+  config4  (default) BASELINE config 4: the MoE 35B-A3B-shaped verify step, 40 layers, block
+           k=8 (9 rows), 8192-token paged KV cache, Q4_K weights, full-vocabulary rejection
+           sampling. One step = embed -> 40 layers -> LM head -> probabilities -> acceptance,
+           replayed as one HIP graph with every input already in HBM.
+  config3  BASELINE config 3: the dense 8B-shaped step (36 layers, Q4_K, SwiGLU 14336).
+  config5  BASELINE config 5: the MoE shape at 220000 tokens of context, tree block of 11 rows.
+  gemv     BASELINE config 2: one Q4_K dequant-GEMV, M=9, K=4096, N=14336, bf16 out.
 """
 import argparse
 import json
@@ -151,15 +157,273 @@ def bench_gemv(args):
     }
 
 
-WORKLOADS = {"gemv": bench_gemv}
+# ---------------------------------------------------------------------------------------
+# configs 3-5: the full verify step
+# ---------------------------------------------------------------------------------------
+def q4k_bytes(n, k):
+    return n * k // 256 * 144
+
+
+def q80_bytes(n, k):
+    return n * k // 32 * 34
+
+
+def step_bytes(cfg, slots):
+    """Algorithmic HBM bytes of one verify step: every weight byte the step must read once
+    (the touched experts only), the KV cache of the context plus the block's new rows, the
+    LM head, and the logits/probabilities of the acceptance."""
+    H, T, V = cfg.hidden, cfg.block, cfg.vocab
+    wb = q4k_bytes if cfg.attn_fmt == 4 else q80_bytes
+    attn_w = wb(cfg.qkv_n, H) + wb(H, cfg.heads * cfg.head_dim)
+    kv = (cfg.context + T) * cfg.kv_heads * cfg.head_dim * 2 * 2
+    total = 0
+    for i in range(cfg.layers):
+        total += attn_w + kv + 2 * 2 * H * 2  # + norm weights (bf16), negligible
+        if cfg.moe:
+            F = cfg.expert_ffn
+            total += (cfg.experts + 1) * H * 2 + int(slots[i]) * (q4k_bytes(2 * F, H) + q4k_bytes(H, F))
+        else:
+            total += q4k_bytes(2 * cfg.ffn, H) + q4k_bytes(H, cfg.ffn)
+    total += V * H * 2 + T * H * 2  # LM head (fp16), embedding rows
+    total += 3 * T * V * 4          # logits write, probabilities read + write
+    return total
+
+
+def timed_graph(fn, reps, stream):
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    return time_events(lambda: g.replay(), reps, stream)
+
+
+def bench_step(args, name):
+    import numpy as np
+    import torch
+    from snowllm_amd import layers as Lops, ops
+    from snowllm_amd.verify import CONFIGS, VerifyModel, Acceptance
+
+    cfg = CONFIGS[name]
+    T, V, k = cfg.block, cfg.vocab, None
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    m = VerifyModel(cfg, seed=0, keep_raw=1)  # raw GGUF bytes of layer 0 for the CPU baseline
+    torch.cuda.synchronize()
+    init_s = time.perf_counter() - t0
+    ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(7))
+    m.set_block(ids)
+    rows = list(range(T)) if not cfg.tree_parents else chain_rows(cfg.tree_parents)
+    k = len(rows) - 1
+    acc = Acceptance(V, rows)
+    # draft side (BASELINE config 1 generators): draft logits ~N(0, 2^2), drafts sampled from
+    # the draft softmax with seed 0, acceptance uniforms U(0, 1) with seed 1
+    g0, g1 = torch.Generator().manual_seed(0), torch.Generator().manual_seed(1)
+    draft_logits = torch.randn(k, V, generator=g0) * 2
+    drafts = torch.multinomial(draft_logits.softmax(-1), 1, generator=g0).view(1, k)
+    uniform = torch.rand(1, k + 1, generator=g1)
+    acc.set_draft(draft_logits.cuda(), drafts.cuda(), uniform.cuda())
+
+    def step():
+        m.forward()
+        acc(m.logits)
+
+    stream = torch.cuda.current_stream()
+    # byte accounting: an eager pass that records each layer's plan size
+    slots = torch.zeros(cfg.layers, dtype=torch.int32, device="cuda")
+    m.forward(record_slots=slots if cfg.moe else None)
+    acc(m.logits)
+    torch.cuda.synchronize()
+    slots_np = slots.cpu().numpy()
+    alg = step_bytes(cfg, slots_np)
+    # the timed region: K graph replays of the whole step, inputs resident in HBM
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(max(1, args.warmup)):
+        g.replay()
+    torch.cuda.synchronize()
+    ms = time_events(lambda: g.replay(), args.steps, stream)
+    emitted = int(acc.accepted[0])  # accepted drafts + the correction/bonus token
+    out_tokens = acc.out[0, :emitted].tolist()
+    step_gbs = alg / (ms * 1e-3) / 1e9
+
+    # per-kernel launch times (HIP events, launch stream), each rotated over the layers so the
+    # weights stream from HBM as they do inside the step
+    c, H = cfg, cfg.hidden
+    Lw = m.layers
+    kern = {}
+
+    def per_launch(label, fn_layer, alg_bytes, launches=1):
+        def run():
+            for i in range(len(Lw)):
+                fn_layer(i)
+        ms_all = timed_graph(run, 3, stream)
+        us = ms_all * 1e3 / len(Lw) / launches
+        kern[label] = {"us": round(us, 3), "alg_bytes": int(alg_bytes),
+                       "gbs": round(alg_bytes / (us * 1e-6) / 1e9, 1)}
+
+    last_slots = int(slots_np[-1]) if cfg.moe else 0
+    wb = q4k_bytes if cfg.attn_fmt == 4 else q80_bytes
+    per_launch("kquant_gemv qkv", lambda i: ops.gemm_kquant_a_prepared(
+        c.attn_fmt, Lw[i].qkv[0], Lw[i].qkv[1], m.proj, T, c.qkv_n, H, m.ws_h), wb(c.qkv_n, H))
+    per_launch("paged_attention (split + merge)", lambda i: ops.paged_attention_explicit(
+        m.q, m.k_pools[i], m.v_pools[i], m.attn, m.table, m.lens, c.head_dim ** -0.5,
+        m.attn_scratch, tree=m.tree), (c.context + T) * c.kv_heads * c.head_dim * 4)
+    if cfg.moe:
+        F = c.expert_ffn
+        ns = T * c.topk + 1
+        per_launch("moe_gate_up", lambda i: Lops.moe_gate_up(
+            c.ffn_fmt, Lw[i].gu, Lw[i].sh_gu, m.plan, m.ws_h2, m.moe_act, T, ns, c.experts, H, F),
+            last_slots * q4k_bytes(2 * F, H))
+        per_launch("moe_down", lambda i: Lops.moe_down(
+            c.ffn_fmt, Lw[i].dn, Lw[i].sh_dn, m.plan, m.moe_act, m.route_w, m.shared_w, m.pairs,
+            m.shared_out, ns, c.experts, H, F), last_slots * q4k_bytes(H, F))
+    else:
+        per_launch("gate_up_swiglu", lambda i: Lops.gate_up_swiglu(
+            c.ffn_fmt, Lw[i].gu[0], Lw[i].gu[1], m.ws_h2, m.act, T, c.ffn, H),
+            q4k_bytes(2 * c.ffn, H))
+    # dominant single kernel per step (launch time x launches per step)
+    single = {kk: v for kk, v in kern.items() if "+" not in kk}
+    dom = max(single, key=lambda kk: single[kk]["us"])
+    d = kern[dom]
+    traffic = read_traffic(dom)
+
+    # reference CPU path (oracle, torch CPU) on a bounded sample: layer 0 x layers + head +
+    # acceptance
+    cpu = cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform)
+    cpu_value = emitted / (cpu["step_s"])
+    return {
+        "metric": METRIC, "value": round(emitted / (ms * 1e-3), 2), "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_k weights x bf16 activations (fp16/bf16 MFMA, fp32 accumulate)",
+        "data": "synthetic, random-init weights (seeded), BASELINE generators",
+        "config": {"workload": cfg.name, "layers": cfg.layers, "hidden": cfg.hidden,
+                   "block_rows": T, "context": cfg.context, "vocab": V,
+                   "experts": cfg.experts, "topk": cfg.topk,
+                   "attn_fmt": "q4_k" if cfg.attn_fmt == 4 else "q8_0",
+                   "tree": bool(cfg.tree_parents)},
+        "verify_step_us": round(ms * 1e3, 1),
+        "accepted_per_step": emitted, "accepted_drafts": emitted - 1,
+        "emitted_tokens": out_tokens,
+        "step_hbm": {"alg_bytes": int(alg), "achieved": round(step_gbs, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(step_gbs / PEAK_HBM_GBS, 4),
+                     "unique_experts_per_layer": float(np.mean(slots_np) - 1) if cfg.moe else None},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": d["gbs"], "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(d["gbs"] / PEAK_HBM_GBS, 4),
+                     "traffic": traffic, "alg_bytes_per_launch": d["alg_bytes"],
+                     "kernel_us": d["us"]},
+        "kernels": kern,
+        "init_s": round(init_s, 1),
+        "cpu_baseline": {"value": round(cpu_value, 4), "unit": "tok/s", "cores": cpu["cores"],
+                         "kind": "port", "cpu": cpu_model(), "sample": cpu["sample"],
+                         "step_s": round(cpu["step_s"], 3)},
+    }
+
+
+def chain_rows(parents):
+    """Rows of the first root-to-leaf chain of a tree block (the chain the acceptance runs)."""
+    rows = [0]
+    while True:
+        kids = [i for i, p in enumerate(parents) if p == rows[-1]]
+        if not kids:
+            return rows
+        rows.append(kids[0])
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (profiles/traffic.txt: 'kernel | fetch_bytes | write_bytes' rows, already scaled by the
+    copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.txt")
+    try:
+        for line in open(path):
+            parts = [x.strip() for x in line.split("|")]
+            if len(parts) >= 3 and parts[0] == kernel:
+                return int(float(parts[1]) + float(parts[2]))
+    except OSError:
+        pass
+    return None
+
+
+def cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform):
+    """The oracle's CPU restatement of the verify step, timed on this host: layer 0 (GGUF
+    dequantization of the weights it touches + fp64/fp32 compute) extrapolated to every layer,
+    the final norm + LM head, and the acceptance (probabilities + rejection sampling)."""
+    import numpy as np
+    import torch
+    from oracle import accept as A
+    from oracle import model as RM
+    from snowllm_amd.verify import tree_masks
+
+    cores = cpu_cores()
+    torch.set_num_threads(cores)
+    T = cfg.block
+    masks = tree_masks(cfg.tree_parents) if cfg.tree_parents else [(2 << t) - 1 for t in range(T)]
+    x = m.embed[m.ids].cpu().float()
+    cos, sin = RM.rope_tables(m.positions.cpu(), m.inv_freq.cpu())
+    pages = m.table.view(-1).long().cpu()
+    kctx = RM.cache_rows(m.k_pools[0].cpu(), pages, cfg.kv_heads, cfg.head_dim, 16, key=True)[:cfg.context]
+    vctx = RM.cache_rows(m.v_pools[0].cpu(), pages, cfg.kv_heads, cfg.head_dim, 16, key=False)[:cfg.context]
+    lw0 = m.layers[0]
+    t0 = time.perf_counter()
+    ref = RM.LayerRef(cfg, lw0)
+    x2, r2, _, _ = RM.layer_forward(ref, RM.bf(x), None, cos, sin, kctx, vctx, masks)
+    layer_s = time.perf_counter() - t0
+    head = m.lm_head_raw.cpu() if m.lm_head_raw is not None else None
+    t1 = time.perf_counter()
+    if head is not None:
+        logits = RM.head_reference(x2, r2, m.final_norm.cpu(), head, cfg.eps)
+    else:
+        logits = torch.randn(T, cfg.vocab)
+    chain = logits[rows].numpy().astype(np.float32)
+    p = A.softmax(chain)
+    q = A.softmax(draft_logits.numpy())
+    ident = np.tile(np.arange(cfg.vocab), (len(rows), 1))
+    k = len(rows) - 1
+    A.reject(p, ident, drafts.numpy(), ident[:k][None], q[None], np.zeros(1, np.int32),
+             np.ones(1, np.int32), uniform.numpy())
+    tail_s = time.perf_counter() - t1
+    step_s = layer_s * cfg.layers + tail_s
+    return {"step_s": step_s, "cores": cores,
+            "sample": f"layer 0 of {cfg.layers} ({layer_s:.2f} s: GGUF dequantize of the "
+                      f"weights it touches + compute, oracle/model.py) x{cfg.layers} + final "
+                      f"norm, LM head and acceptance ({tail_s:.2f} s); torch CPU, {cores} threads"}
+
+
+def bench_copy(args):
+    """A plain device copy of known size: the calibration for rocprofv3's FETCH_SIZE and
+    WRITE_SIZE counters (bytes read and written per launch are both exactly `nbytes`)."""
+    import torch
+    nbytes = 512 << 20
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(args.warmup):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    ms = time_events(lambda: b.copy_(a), args.steps, torch.cuda.current_stream())
+    gbs = 2 * nbytes / (ms * 1e-3) / 1e9
+    return {"metric": "device copy GB/s (counter calibration)", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u8", "data": "synthetic",
+            "config": {"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes}}
+
+
+WORKLOADS = {"gemv": bench_gemv, "copy": bench_copy, "config3": lambda a: bench_step(a, "config3"),
+             "config4": lambda a: bench_step(a, "config4"),
+             "config5": lambda a: bench_step(a, "config5")}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="gemv", choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="config4", choices=sorted(WORKLOADS))
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only (one-GPU boxes); "

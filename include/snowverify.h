@@ -240,6 +240,20 @@ int snowverify_moe_plan(const int32_t* ids, int64_t M, int64_t topk, int64_t E, 
 int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_t M, int64_t E,
                               int64_t topk, float* weights, int32_t* ids, float* shared_w,
                               void* plan, void* stream);
+/* The three stages of snowverify_moe_experts, for callers that schedule them separately:
+ * gate/up + SwiGLU over max_slots plan slots (compact activation rows), the down GEMV into
+ * pre-weighted pairs / shared rows, and the fixed-order combine. */
+int snowverify_moe_gate_up(int fmt, const void* gu_quant, const void* gu_meta,
+                           const void* sh_gu_quant, const void* sh_gu_meta, const void* plan,
+                           const void* ws, void* act, int64_t M, int64_t max_slots, int64_t E,
+                           int64_t H, int64_t F, void* stream);
+int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_meta,
+                        const void* sh_dn_quant, const void* sh_dn_meta, const void* plan,
+                        const void* act, const float* weights, const float* shared_w,
+                        float* pairs, float* shared_out, int64_t max_slots, int64_t E, int64_t H,
+                        int64_t F, void* stream);
+int snowverify_moe_combine(const float* pairs, const float* shared_out, void* out, int64_t M,
+                           int64_t topk, int64_t H, void* stream);
 int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_meta,
                            const void* dn_quant, const void* dn_meta, const void* sh_gu_quant,
                            const void* sh_gu_meta, const void* sh_dn_quant,

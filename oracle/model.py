@@ -43,8 +43,20 @@ def linear(x, w):
     return bf((x.double() @ w.double().T).float())
 
 
+def cache_rows(pool, pages, heads, dim, page, *, key):
+    """Paged pool -> dense rows [len, heads, dim] (tests/test_lfm2_dspark_reference.py:30-36:
+    K [blocks, Hkv, d/16, page, 16], V [blocks, Hkv, page/4, d, 4])."""
+    x = pool.view(torch.bfloat16)
+    if key:
+        x = x.view(-1, heads, dim // 16, page, 16)[pages].permute(0, 3, 1, 2, 4)
+    else:
+        x = x.view(-1, heads, page // 4, dim, 4)[pages].permute(0, 2, 4, 1, 3)
+    return x.reshape(-1, heads, dim)
+
+
 class LayerRef:
-    """Dequantized weights of one layer (CPU)."""
+    """Dequantized weights of one layer (CPU). Routed experts are dequantized when first
+    used (the reference's CPU path only touches the experts a block routes to)."""
 
     def __init__(self, cfg, lw):
         c = cfg
@@ -57,15 +69,28 @@ class LayerRef:
         self.qkv = dequant_raw(lw.qkv[2], c.attn_fmt, c.qkv_n, H)
         self.o = dequant_raw(lw.o[2], c.attn_fmt, H, c.heads * c.head_dim)
         if c.moe:
-            E, F = c.experts, c.expert_ffn
+            F = c.expert_ffn
             self.router = lw.raw["router"].cpu().float()
-            self.gu = dequant_raw(lw.gu[2], c.ffn_fmt, E * 2 * F, H).view(E, 2 * F, H)
-            self.dn = dequant_raw(lw.dn[2], c.ffn_fmt, E * H, F).view(E, H, F)
+            self._gu_raw = lw.gu[2].cpu()
+            self._dn_raw = lw.dn[2].cpu()
+            self._experts = {}
             self.sh_gu = dequant_raw(lw.sh_gu[2], c.ffn_fmt, 2 * F, H)
             self.sh_dn = dequant_raw(lw.sh_dn[2], c.ffn_fmt, H, F)
         else:
             self.gu = dequant_raw(lw.gu[2], c.ffn_fmt, 2 * c.ffn, H)
             self.dn = dequant_raw(lw.dn[2], c.ffn_fmt, H, c.ffn)
+
+    def expert(self, e):
+        """(gate_up [2F, H], down [H, F]) of routed expert e."""
+        if e not in self._experts:
+            c = self.cfg
+            H, F = c.hidden, c.expert_ffn
+            gb = self._gu_raw.numel() // c.experts
+            db = self._dn_raw.numel() // c.experts
+            gu = dequant_raw(self._gu_raw[e * gb:(e + 1) * gb], c.ffn_fmt, 2 * F, H)
+            dn = dequant_raw(self._dn_raw[e * db:(e + 1) * db], c.ffn_fmt, H, F)
+            self._experts[e] = (gu, dn)
+        return self._experts[e]
 
 
 def swiglu_ffn(x, gu, dn, F):
@@ -126,8 +151,8 @@ def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
         for t in range(T):
             acc = torch.zeros(c.hidden)
             for kk in range(K):
-                e = int(ids[t, kk])
-                y = swiglu_ffn(h2[t:t + 1], ref.gu[e], ref.dn[e], F)[0]
+                gu, dn = ref.expert(int(ids[t, kk]))
+                y = swiglu_ffn(h2[t:t + 1], gu, dn, F)[0]
                 acc += y * w[t, kk]
             sh = swiglu_ffn(h2[t:t + 1], ref.sh_gu, ref.sh_dn, F)[0]
             acc += sh * torch.sigmoid(logits[t, E])

@@ -20,8 +20,12 @@ ARCH = os.environ.get("SNOWVERIFY_ARCH", "gfx950")
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable", "-Wno-unused-parameter",
-    # packed FP32 instructions are disabled on purpose
+    # no packed FP32 instructions (v_pk_fma_f32 and kin): some of their forms have given
+    # wrong results on these boxes
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the k-quant kernels rescale every sub-block product in VALU, and
+    # AGPR results would cost a v_accvgpr_read per element first
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-munsafe-fp-atomics",
 ]
 

@@ -232,58 +232,101 @@ __global__ void dense_shuffle_kernel(const uint16_t* __restrict__ src, uint16_t*
 // `plan` selects the expert per grid.y slot (MoE) or is null (dense MLP, one weight).
 // act_out: [slots, 16, F] bf16 (MoE; rows >= M zero) or [M, F] (dense).
 // ---------------------------------------------------------------------------------------
+// MoE plan: per slot (a routed expert the block touches, then the shared expert) the rows
+// routed to it in ascending order, compacted, and each row's (row * topk + k) pair index.
+// ---------------------------------------------------------------------------------------
+constexpr int MOE_MAX_SLOTS = 136;
 struct MoePlan {
-  int32_t n_slots;             // routed unique experts + shared expert
+  int32_t n_slots;                         // routed unique experts + shared expert
   int32_t n_routed;
-  int32_t slot_expert[136];    // expert id per slot (E = shared)
-  int32_t pair_of[136][16];    // (row * topk + k) routed to the slot's expert, or -1
+  int32_t slot_expert[MOE_MAX_SLOTS];      // expert id per slot (E = shared)
+  int32_t slot_rows[MOE_MAX_SLOTS];        // rows routed to the slot
+  int32_t row_of[MOE_MAX_SLOTS][16];       // compact position -> block row
+  int32_t pair_of[MOE_MAX_SLOTS][16];      // compact position -> pair index (-1: shared)
 };
 
-template <int FMT, int NW>
-__global__ void __launch_bounds__(NW * 64) gate_up_kernel(
+// Row gather for one wave: compact row r = lane & 15 of the slot reads block row row_of[r]
+// from the operand workspace; rows past the slot's count read zeros (out-of-range offsets).
+__device__ __forceinline__ void gather_rows(GemvStreams& st, const int32_t* rows, int n_rows,
+                                            int lane) {
+  const int r = lane & 15, kq = lane >> 4;
+  const int R = r < n_rows ? rows[r] : -1;
+  st.v_xop = R >= 0 ? (uint32_t)((R + 16 * kq) * 16) : 0x80000000u;
+  st.v_sx = R >= 0 ? (uint32_t)((R + 16 * kq) * 4) : 0x80000000u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ci = 4 * kq + i;
+    st.v_scale_g[i] = ci < n_rows ? (uint32_t)(rows[ci] * 4) : 0x80000000u;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Gate/up GEMV with SwiGLU in the epilogue: act[r, n] = silu(x Wg^T)[r, n] * (x Wu^T)[r, n],
+// gate_up the packed [2F, K] k-quant weight (gate rows first). Block = PPB pairs (a gate tile
+// and its up tile) x WS waves splitting the superblocks; blockIdx.y = MoE slot (plan mode:
+// the slot's expert, rows gathered, act written compact at act_out + slot * 16 * F) or the
+// whole block (plan == null: rows 0..M-1 of x, act [M, F]).
+// ---------------------------------------------------------------------------------------
+template <int FMT, int WS, int PPB>
+__global__ void __launch_bounds__(WS * PPB * 64) gate_up_kernel(
     const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t gu_qbytes,
     int64_t gu_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
     const MoePlan* __restrict__ plan, int E, const void* __restrict__ ws,
     uint16_t* __restrict__ act_out, int M, int F, int S) {
-  __shared__ floatx4 part[NW][2][64];
+  __shared__ floatx4 part[PPB][WS][2][64];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pl = wv / WS, sw = wv % WS;
   const int kq = lane >> 4;
-  const int pair = blockIdx.x, slot = blockIdx.y;
+  const int slot = blockIdx.y;
+  const int half_tiles = F / TILE_N;
+  const int pair = blockIdx.x * PPB + pl;
   const uint8_t* q = quant;
   const uint8_t* m = meta;
+  int n_rows = M;
   if (plan) {
     if (slot >= plan->n_slots) return;
     const int e = plan->slot_expert[slot];
     if (e >= E) { q = sh_quant; m = sh_meta; }
     else { q = quant + e * gu_qbytes; m = meta + e * gu_mbytes; }
+    n_rows = plan->slot_rows[slot];
   }
-  const int half_tiles = F / TILE_N;
-  const GemvStreams st = make_streams<FMT>(q, m, ws, 2 * half_tiles, S, lane, M);
+  GemvStreams st = make_streams<FMT>(q, m, ws, 2 * half_tiles, S, lane, M);
   const uint32_t Mv = decode_magic<FMT>();
   floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-  gemv_loop<FMT, 2, NW>(st, wv, S, pair, half_tiles, kq, Mv, acc);
-  combine_waves<2, NW>(part, acc, wv, lane);
-  if (threadIdx.x < 64) {
-    const int l = threadIdx.x;
-    floatx4 g = part[0][0][l], u = part[0][1][l];
-#pragma unroll
-    for (int ww = 1; ww < NW; ++ww) {
-      g += part[ww][0][l];
-      u += part[ww][1][l];
+  if (pair < half_tiles) {
+    if (plan) {
+      gather_rows(st, plan->row_of[slot], n_rows, lane);
+      gemv_loop<FMT, 2, WS, true>(st, sw, S, pair, half_tiles, kq, Mv, acc);
+    } else {
+      gemv_loop<FMT, 2, WS>(st, sw, S, pair, half_tiles, kq, Mv, acc);
     }
-    const int n = pair * TILE_N + (l & 15);
-    const int rb = 4 * (l >> 4);
-    uint16_t* out = plan ? act_out + (int64_t)slot * 16 * F : act_out;
+  }
+  floatx4 g = acc[0], u = acc[1];
+  if constexpr (WS > 1) {
+    part[pl][sw][0][lane] = acc[0];
+    part[pl][sw][1][lane] = acc[1];
+    __syncthreads();
+    if (sw != 0) return;
+    g = part[pl][0][0][lane];
+    u = part[pl][0][1][lane];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = rb + i;
-      if (!plan && row >= M) break;
-      const float gg = bf16_to_f32(f32_to_bf16(g[i]));  // projections are bf16 tensors
-      const float uu = bf16_to_f32(f32_to_bf16(u[i]));
-      const float a = (row < M) ? gg / (1.0f + __expf(-gg)) * uu : 0.f;
-      out[(int64_t)row * F + n] = f32_to_bf16(a);
+    for (int j = 1; j < WS; ++j) {
+      g += part[pl][j][0][lane];
+      u += part[pl][j][1][lane];
     }
+  }
+  if (pair >= half_tiles) return;
+  const int n = pair * TILE_N + (lane & 15);
+  const int rb = 4 * (lane >> 4);
+  uint16_t* out = plan ? act_out + (int64_t)slot * 16 * F : act_out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = rb + i;
+    if (row >= n_rows) break;
+    const float gg = bf16_to_f32(f32_to_bf16(g[i]));  // projections are bf16 tensors
+    const float uu = bf16_to_f32(f32_to_bf16(u[i]));
+    out[(int64_t)row * F + n] = f32_to_bf16(gg / (1.0f + __expf(-gg)) * uu);
   }
 }
 
@@ -360,25 +403,41 @@ __device__ __forceinline__ void build_plan(const int32_t* ids_s, int M, int topk
     before = __popcll(bal & ((1ull << lane) - 1ull));
     if (lane == 0) wave_cnt[w] = __popcll(bal);
   }
-  for (int i = t; i < 136 * 16; i += blockDim.x) plan->pair_of[i / 16][i % 16] = -1;
   __syncthreads();
+  const int n_routed = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
   if (w < 4) {
     int off = 0;
     for (int ww = 0; ww < w; ++ww) off += wave_cnt[ww];
     slot_of[t] = used ? off + before : -1;
-    if (used) plan->slot_expert[off + before] = t;
+    if (used) {
+      plan->slot_expert[off + before] = t;
+      plan->slot_rows[off + before] = __popc(mask[t]);
+    }
     if (t == 0) {
-      const int n = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
-      plan->n_routed = n;
-      if (shared) plan->slot_expert[n] = E;
-      plan->n_slots = n + (shared ? 1 : 0);
+      plan->n_routed = n_routed;
+      if (shared) {
+        plan->slot_expert[n_routed] = E;
+        plan->slot_rows[n_routed] = M;
+      }
+      plan->n_slots = n_routed + (shared ? 1 : 0);
     }
   }
   __syncthreads();
+  // compact row lists: a row's position in its slot = routed rows of the expert before it
   for (int p = t; p < M * topk; p += blockDim.x) {
     const int e = ids_s[p];
-    if (e >= 0 && e < E) plan->pair_of[slot_of[e]][p / topk] = p;
+    if (e >= 0 && e < E) {
+      const int r = p / topk, sl = slot_of[e];
+      const int pos = __popc(mask[e] & ((1u << r) - 1u));
+      plan->row_of[sl][pos] = r;
+      plan->pair_of[sl][pos] = p;
+    }
   }
+  if (shared)
+    for (int r = t; r < M; r += blockDim.x) {
+      plan->row_of[n_routed][r] = r;
+      plan->pair_of[n_routed][r] = -1;
+    }
 }
 
 __global__ void __launch_bounds__(ROUTE_THREADS) moe_route_plan_kernel(
@@ -425,69 +484,106 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_plan_kernel(const int32_t* 
 }
 
 // ---------------------------------------------------------------------------------------
-// MoE down: per (tile group, slot): converts the slot's activations [16, F] in-kernel, runs the
-// down GEMV of that expert and writes routed rows, pre-weighted, into pairs [M*topk, H] f32
-// (or the shared expert's rows, weighted by sigmoid(gate), into shared_out [M, H]).
+// MoE down: per (tile group, slot) the down GEMV of the slot's expert over its compact
+// activation rows [n_rows, F] (converted to fp16 operands in-kernel), with the weights of the
+// next superblock in flight during the current one. Routed rows are written pre-weighted into
+// pairs [M*topk, H] f32 at their pair index; the shared expert's rows, weighted by
+// sigmoid(gate), into shared_out [M, H].
 // ---------------------------------------------------------------------------------------
-template <int FMT, int NTILE, int NW>
-__global__ void __launch_bounds__(NW * 64) moe_down_kernel(
+template <int FMT, int NTILE>
+__device__ __forceinline__ void act_operands(SbOperands<FMT, NTILE>& o, const uint16_t* a, int F,
+                                             int n_rows, int s, int lane) {
+  XOperands xo;
+  convert_superblock(a, F, n_rows, s, lane, xo);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o.x[j] = xo.x[j];
+  o.sx0 = xo.sx0;
+  o.sx1 = xo.sx1;
+  // per-row scales of rows 4 kq .. 4 kq + 3 live in lanes 4 kq + i (kq = 0 row group)
+  const int kq = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o.scale[i] = __shfl(xo.scale, 4 * kq + i, 64);
+}
+
+template <int FMT, int NTILE, int WS>
+__device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t* a, int F,
+                                          int n_rows, int w, int S, int tile0, int lane,
+                                          uint32_t Mv, floatx4* acc) {
+  if (w >= S) return;
+  const int kq = lane >> 4;
+  SbOperands<FMT, NTILE> bufA, bufB;
+  load_sb<FMT, NTILE, false>(bufA, st, w, S, tile0, 1);
+  for (int s = w;;) {
+    if (s + WS < S) load_sb<FMT, NTILE, false>(bufB, st, s + WS, S, tile0, 1);
+    act_operands<FMT, NTILE>(bufA, a, F, n_rows, s, lane);
+    gemv_superblock<FMT, NTILE>(bufA, acc, kq, Mv);
+    s += WS;
+    if (s >= S) break;
+    if (s + WS < S) load_sb<FMT, NTILE, false>(bufA, st, s + WS, S, tile0, 1);
+    act_operands<FMT, NTILE>(bufB, a, F, n_rows, s, lane);
+    gemv_superblock<FMT, NTILE>(bufB, acc, kq, Mv);
+    s += WS;
+    if (s >= S) break;
+  }
+}
+
+template <int FMT, int NTILE, int WS, int GPB>
+__global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
     const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t dn_qbytes,
     int64_t dn_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
     const MoePlan* __restrict__ plan, int E, const uint16_t* __restrict__ act,
     const float* __restrict__ weights, const float* __restrict__ shared_w,
-    float* __restrict__ pairs, float* __restrict__ shared_out, int M, int H, int F) {
-  __shared__ floatx4 part[NW][NTILE][64];
+    float* __restrict__ pairs, float* __restrict__ shared_out, int H, int F) {
+  __shared__ floatx4 part[GPB][WS][NTILE][64];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kq = lane >> 4;
+  const int gl = wv / WS, sw = wv % WS;
   const int slot = blockIdx.y;
   if (slot >= plan->n_slots) return;
   const int e = plan->slot_expert[slot];
+  const int n_rows = plan->slot_rows[slot];
   const uint8_t* q = e >= E ? sh_quant : quant + e * dn_qbytes;
   const uint8_t* m = e >= E ? sh_meta : meta + e * dn_mbytes;
   const int S = F / QK;
   const int tiles = H / TILE_N;
-  const int tile0 = blockIdx.x * NTILE;
-  GemvStreams st = make_streams<FMT>(q, m, nullptr, tiles, S, lane, M);
+  const int tile0 = (blockIdx.x * GPB + gl) * NTILE;
+  const GemvStreams st = make_streams<FMT>(q, m, nullptr, tiles, S, lane, 16);
   const uint32_t Mv = decode_magic<FMT>();
   floatx4 acc[NTILE];
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const uint16_t* a = act + (int64_t)slot * 16 * F;
-  for (int s = wv; s < S; s += NW) {
-    SbOperands<FMT, NTILE> o;
-    load_sb<FMT, NTILE, false>(o, st, s, S, tile0, 1);
-    XOperands xo;
-    convert_superblock(a, F, 16, s, lane, xo);
+  if (tile0 < tiles)
+    down_loop<FMT, NTILE, WS>(st, act + (int64_t)slot * 16 * F, F, n_rows, sw, S, tile0, lane, Mv,
+                              acc);
+  if constexpr (WS > 1) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o.x[j] = xo.x[j];
-    o.sx0 = xo.sx0;
-    o.sx1 = xo.sx1;
-    // per-row scales of rows 4 kq .. 4 kq + 3 live in lanes 4 kq + i (kq = 0 row group)
+    for (int t = 0; t < NTILE; ++t) part[gl][sw][t][lane] = acc[t];
+    __syncthreads();
+    if (sw != 0) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o.scale[i] = __shfl(xo.scale, 4 * kq + i, 64);
-    gemv_superblock<FMT, NTILE>(o, acc, kq, Mv);
+    for (int t = 0; t < NTILE; ++t) {
+      acc[t] = part[gl][0][t][lane];
+#pragma unroll
+      for (int j = 1; j < WS; ++j) acc[t] += part[gl][j][t][lane];
+    }
   }
-  combine_waves<NTILE, NW>(part, acc, wv, lane);
-  for (int idx = threadIdx.x; idx < NTILE * 64; idx += NW * 64) {
-    const int t = idx >> 6, l = idx & 63;
-    const int tile = tile0 + t;
-    if (tile >= tiles) continue;
-    floatx4 v = part[0][t][l];
+  const int rb = 4 * (lane >> 4);
 #pragma unroll
-    for (int ww = 1; ww < NW; ++ww) v += part[ww][t][l];
-    const int n = tile * TILE_N + (l & 15);
-    const int rb = 4 * (l >> 4);
+  for (int t = 0; t < NTILE; ++t) {
+    const int tile = tile0 + t;
+    if (tile >= tiles) break;
+    const int n = tile * TILE_N + (lane & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = rb + i;
-      if (row >= M) break;
-      const float y = bf16_to_f32(f32_to_bf16(v[i]));  // expert outputs are bf16 tensors
+      const int ci = rb + i;  // compact row
+      if (ci >= n_rows) break;
+      const float y = bf16_to_f32(f32_to_bf16(acc[t][i]));  // expert outputs are bf16 tensors
       if (e >= E) {
+        const int row = plan->row_of[slot][ci];
         shared_out[(int64_t)row * H + n] = y * shared_w[row];
       } else {
-        const int p = plan->pair_of[slot][row];
-        if (p >= 0) pairs[(int64_t)p * H + n] = y * weights[p];
+        const int p = plan->pair_of[slot][ci];
+        pairs[(int64_t)p * H + n] = y * weights[p];
       }
     }
   }
@@ -584,14 +680,15 @@ SV_API int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* met
   if ((fmt != 4 && fmt != 8) || M <= 0 || M > 16 || F <= 0 || F % 16 || K % 256) return SV_EINVAL;
   const int S = (int)(K / 256);
   hipStream_t s = Sx(stream);
+  const dim3 grid((unsigned)(F / 16), 1);
   if (fmt == 4)
-    hipLaunchKernelGGL((gate_up_kernel<4, 8>), dim3((unsigned)(F / 16), 1), dim3(512), 0, s,
-                       (const uint8_t*)quant, (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr,
-                       0, ws, (uint16_t*)act, (int)M, (int)F, S);
+    hipLaunchKernelGGL((gate_up_kernel<4, 4, 1>), grid, dim3(256), 0, s, (const uint8_t*)quant,
+                       (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr, 0, ws, (uint16_t*)act,
+                       (int)M, (int)F, S);
   else
-    hipLaunchKernelGGL((gate_up_kernel<8, 8>), dim3((unsigned)(F / 16), 1), dim3(512), 0, s,
-                       (const uint8_t*)quant, (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr,
-                       0, ws, (uint16_t*)act, (int)M, (int)F, S);
+    hipLaunchKernelGGL((gate_up_kernel<8, 4, 1>), grid, dim3(256), 0, s, (const uint8_t*)quant,
+                       (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr, 0, ws, (uint16_t*)act,
+                       (int)M, (int)F, S);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -636,9 +733,65 @@ SV_API int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_
   return SV_OK;
 }
 
-// MoE experts of one layer (Q4_K). ws: prepared operands of the normalised hidden [M, H];
-// act scratch [M*topk + 1, 16, F] bf16; pairs [M*topk, H] f32; shared_out [M, H] f32;
-// out [M, H] bf16 = sum_k w_k expert_k(x) + sigmoid(g) shared(x).
+// MoE expert stages (Q4_K). act scratch [M*topk + 1, 16, F] bf16 (compact rows per slot).
+constexpr int MOE_GU_PPB = 4;                          // gate/up: pairs per block, one wave each
+constexpr int MOE_DN_NTILE = 4, MOE_DN_GPB = 4;         // down: tiles per wave, waves per block
+
+// Gate/up + SwiGLU of every slot of the plan; ws: prepared operands of the normalised hidden.
+SV_API int snowverify_moe_gate_up(int fmt, const void* gu_quant, const void* gu_meta,
+                                  const void* sh_gu_quant, const void* sh_gu_meta,
+                                  const void* plan, const void* ws, void* act, int64_t M,
+                                  int64_t max_slots, int64_t E, int64_t H, int64_t F,
+                                  void* stream) {
+  if (fmt != 4 || M <= 0 || M > 16 || max_slots <= 0 || max_slots > MOE_MAX_SLOTS || H % 256 ||
+      F % 256)
+    return SV_EINVAL;
+  const int64_t gu_q = 2 * F * H / 2, gu_m = 2 * F * (H / 256) * 16;
+  const dim3 grid((unsigned)((F / 16 + MOE_GU_PPB - 1) / MOE_GU_PPB), (unsigned)max_slots);
+  hipLaunchKernelGGL((gate_up_kernel<4, 1, MOE_GU_PPB>), grid, dim3(64 * MOE_GU_PPB), 0,
+                     Sx(stream), (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
+                     (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
+                     (const MoePlan*)plan, (int)E, ws, (uint16_t*)act, (int)M, (int)F,
+                     (int)(H / 256));
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Down GEMV of every slot: routed rows pre-weighted into pairs [M*topk, H] f32, shared rows
+// into shared_out [M, H] f32.
+SV_API int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_meta,
+                               const void* sh_dn_quant, const void* sh_dn_meta, const void* plan,
+                               const void* act, const float* weights, const float* shared_w,
+                               float* pairs, float* shared_out, int64_t max_slots, int64_t E,
+                               int64_t H, int64_t F, void* stream) {
+  if (fmt != 4 || max_slots <= 0 || max_slots > MOE_MAX_SLOTS || H % 256 || F % 256)
+    return SV_EINVAL;
+  const int64_t dn_q = H * F / 2, dn_m = H * (F / 256) * 16;
+  const int groups = (int)(H / 16 / MOE_DN_NTILE);
+  const dim3 grid((unsigned)((groups + MOE_DN_GPB - 1) / MOE_DN_GPB), (unsigned)max_slots);
+  hipLaunchKernelGGL((moe_down_kernel<4, MOE_DN_NTILE, 1, MOE_DN_GPB>), grid,
+                     dim3(64 * MOE_DN_GPB), 0, Sx(stream), (const uint8_t*)dn_quant,
+                     (const uint8_t*)dn_meta, dn_q, dn_m, (const uint8_t*)sh_dn_quant,
+                     (const uint8_t*)sh_dn_meta, (const MoePlan*)plan, (int)E,
+                     (const uint16_t*)act, weights, shared_w, pairs, shared_out, (int)H, (int)F);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// out [M, H] bf16 = sum_k pairs[r * topk + k] (+ shared_out[r]) in a fixed order.
+SV_API int snowverify_moe_combine(const float* pairs, const float* shared_out, void* out,
+                                  int64_t M, int64_t topk, int64_t H, void* stream) {
+  if (M <= 0 || topk <= 0 || H <= 0) return SV_EINVAL;
+  const int64_t n = M * H;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     Sx(stream), pairs, shared_out, (uint16_t*)out, (int)M, (int)H, (int)topk);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// MoE experts of one layer (Q4_K): gate/up, down and combine. ws: prepared operands of the
+// normalised hidden [M, H]; act scratch [M*topk + 1, 16, F] bf16; pairs [M*topk, H] f32;
+// shared_out [M, H] f32; out [M, H] bf16 = sum_k w_k expert_k(x) + sigmoid(g) shared(x).
 SV_API int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_meta,
                                   const void* dn_quant, const void* dn_meta, const void* sh_gu_quant,
                                   const void* sh_gu_meta, const void* sh_dn_quant,
@@ -646,25 +799,13 @@ SV_API int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_
                                   const float* weights, const float* shared_w, void* act,
                                   float* pairs, float* shared_out, void* out, int64_t M,
                                   int64_t topk, int64_t E, int64_t H, int64_t F, void* stream) {
-  if (fmt != 4 || M <= 0 || M > 16 || M * topk > 135 || H % 256 || F % 256) return SV_EINVAL;
-  hipStream_t s = Sx(stream);
-  const int64_t gu_q = 2 * F * H / 2, gu_m = 2 * F * (H / 256) * 16;
-  const int64_t dn_q = H * F / 2, dn_m = H * (F / 256) * 16;
-  const int slots = (int)(M * topk + (sh_gu_quant ? 1 : 0));
-  hipLaunchKernelGGL((gate_up_kernel<4, 8>), dim3((unsigned)(F / 16), (unsigned)slots), dim3(512),
-                     0, s, (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
-                     (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta, (const MoePlan*)plan,
-                     (int)E, ws, (uint16_t*)act, (int)M, (int)F, (int)(H / 256));
-  SV_CHECK_LAUNCH();
-  hipLaunchKernelGGL((moe_down_kernel<4, 4, 2>), dim3((unsigned)(H / 16 / 4), (unsigned)slots),
-                     dim3(128), 0, s, (const uint8_t*)dn_quant, (const uint8_t*)dn_meta, dn_q, dn_m,
-                     (const uint8_t*)sh_dn_quant, (const uint8_t*)sh_dn_meta, (const MoePlan*)plan,
-                     (int)E, (const uint16_t*)act, weights, shared_w, pairs, shared_out, (int)M,
-                     (int)H, (int)F);
-  SV_CHECK_LAUNCH();
-  const int64_t n = M * H;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, pairs,
-                     sh_gu_quant ? shared_out : nullptr, (uint16_t*)out, (int)M, (int)H, (int)topk);
-  SV_CHECK_LAUNCH();
-  return SV_OK;
+  if (M * topk > MOE_MAX_SLOTS - 1) return SV_EINVAL;
+  const int64_t slots = M * topk + (sh_gu_quant ? 1 : 0);
+  int rc = snowverify_moe_gate_up(fmt, gu_quant, gu_meta, sh_gu_quant, sh_gu_meta, plan, ws, act,
+                                  M, slots, E, H, F, stream);
+  if (rc != SV_OK) return rc;
+  rc = snowverify_moe_down(fmt, dn_quant, dn_meta, sh_dn_quant, sh_dn_meta, plan, act, weights,
+                           shared_w, pairs, shared_out, slots, E, H, F, stream);
+  if (rc != SV_OK) return rc;
+  return snowverify_moe_combine(pairs, sh_gu_quant ? shared_out : nullptr, out, M, topk, H, stream);
 }

@@ -155,7 +155,9 @@ int dispatch_gemv(const void* quant, const void* meta, const void* ws, void* c, 
   // measured on MI355X (M = 9): wide outputs want 4 tiles x 8 waves, K >= 4096 narrow outputs
   // 1 x 8, K = 2048 2 x 8 when there are >= 2 tiles per CU
   if (S >= 8) {
-    if (tiles >= 4 * 192) return launch_gemv<FMT, 4, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    // (Q8_0 keeps two tiles: four tiles of int8 quants exceed the register file)
+    if (tiles >= 4 * 192 && FMT == FMT_Q4_K)
+      return launch_gemv<FMT, 4, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
     if (tiles >= 2 * 128 && S <= 8) return launch_gemv<FMT, 2, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
     return launch_gemv<FMT, 1, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
   }

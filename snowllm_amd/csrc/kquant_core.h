@@ -287,11 +287,12 @@ __device__ __forceinline__ float bload1(__amdgpu_buffer_rsrc_t r, uint32_t voff,
 struct GemvStreams {
   __amdgpu_buffer_rsrc_t quant, meta, xop, sxop, scale;
   uint32_t v_quant, v_meta, v_xop, v_sx, v_scale;  // per-lane byte offsets
+  uint32_t v_scale_g[4];  // row-gathered streams: offsets of the scales of rows 4*kq + i
 };
 
 // Load the weights of superblock s for tiles tile0 + t * tstride (t < NTILE) and, when
 // WITH_X, its activation operands from the workspace.
-template <int FMT, int NTILE, bool WITH_X = true>
+template <int FMT, int NTILE, bool WITH_X = true, bool GATHER = false>
 __device__ __forceinline__ void load_sb(SbOperands<FMT, NTILE>& o, const GemvStreams& st, int s,
                                         int S, int tile0, int tstride = 1) {
   constexpr int QV = QLayout<FMT>::kQuantVecs;
@@ -300,7 +301,12 @@ __device__ __forceinline__ void load_sb(SbOperands<FMT, NTILE>& o, const GemvStr
     for (int j = 0; j < 8; ++j) o.x[j] = bload4(st.xop, st.v_xop, (uint32_t)((s * 8 + j) * 64 * 16));
     o.sx0 = bload1(st.sxop, st.v_sx, (uint32_t)((s * 2 + 0) * 64 * 4));
     o.sx1 = bload1(st.sxop, st.v_sx, (uint32_t)((s * 2 + 1) * 64 * 4));
-    o.scale = __builtin_bit_cast(floatx4, bload4(st.scale, st.v_scale, (uint32_t)(s * 16 * 4)));
+    if constexpr (GATHER) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o.scale[i] = bload1(st.scale, st.v_scale_g[i], (uint32_t)(s * 16 * 4));
+    } else {
+      o.scale = __builtin_bit_cast(floatx4, bload4(st.scale, st.v_scale, (uint32_t)(s * 16 * 4)));
+    }
   }
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) {
@@ -361,18 +367,18 @@ __device__ __forceinline__ uint32_t decode_magic() {
 
 // Wave w of NW walks superblocks s = w, w + NW, ... of the tiles tile0 + t * tstride, with the
 // next superblock's operands in flight while the current one is multiplied.
-template <int FMT, int NTILE, int NW>
+template <int FMT, int NTILE, int NW, bool GATHER = false>
 __device__ __forceinline__ void gemv_loop(const GemvStreams& st, int w, int S, int tile0,
                                           int tstride, int kq, uint32_t Mv, floatx4* acc) {
   if (w >= S) return;
   SbOperands<FMT, NTILE> bufA, bufB;
-  load_sb<FMT, NTILE>(bufA, st, w, S, tile0, tstride);
+  load_sb<FMT, NTILE, true, GATHER>(bufA, st, w, S, tile0, tstride);
   for (int s = w;;) {
-    if (s + NW < S) load_sb<FMT, NTILE>(bufB, st, s + NW, S, tile0, tstride);
+    if (s + NW < S) load_sb<FMT, NTILE, true, GATHER>(bufB, st, s + NW, S, tile0, tstride);
     gemv_superblock<FMT, NTILE>(bufA, acc, kq, Mv);
     s += NW;
     if (s >= S) break;
-    if (s + NW < S) load_sb<FMT, NTILE>(bufA, st, s + NW, S, tile0, tstride);
+    if (s + NW < S) load_sb<FMT, NTILE, true, GATHER>(bufA, st, s + NW, S, tile0, tstride);
     gemv_superblock<FMT, NTILE>(bufB, acc, kq, Mv);
     s += NW;
     if (s >= S) break;

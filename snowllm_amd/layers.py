@@ -147,3 +147,39 @@ def moe_experts(fmt, gu, dn, sh_gu, sh_dn, plan, ws, weights, shared_w, act, pai
                                      _p(plan), _p(ws), _p(weights), _p(shared_w), _p(act),
                                      _p(pairs), _p(shared_out), _p(out), M, topk, E, H, F,
                                      _stream()), "moe_experts")
+
+
+def moe_gate_up(fmt, gu, sh_gu, plan, ws, act, M, max_slots, E, H, F):
+    check(lib.snowverify_moe_gate_up(fmt, _p(gu[0]), _p(gu[1]), _p(sh_gu[0]), _p(sh_gu[1]), _p(plan),
+                                     _p(ws), _p(act), M, max_slots, E, H, F, _stream()),
+          "moe_gate_up")
+
+
+def moe_down(fmt, dn, sh_dn, plan, act, weights, shared_w, pairs, shared_out, max_slots, E, H, F):
+    check(lib.snowverify_moe_down(fmt, _p(dn[0]), _p(dn[1]), _p(sh_dn[0]), _p(sh_dn[1]), _p(plan),
+                                  _p(act), _p(weights), _p(shared_w), _p(pairs), _p(shared_out),
+                                  max_slots, E, H, F, _stream()), "moe_down")
+
+
+def moe_combine(pairs, shared_out, out, M, topk, H):
+    check(lib.snowverify_moe_combine(_p(pairs), _p(shared_out), _p(out), M, topk, H, _stream()),
+          "moe_combine")
+
+
+def parse_plan(plan):
+    """Host view of a MoE plan buffer (tests and accounting): dict of numpy arrays."""
+    import numpy as np
+    a = plan.view(torch.int32).cpu().numpy()
+    S = MOE_MAX_SLOTS
+    n = int(a[0])
+    o = 2
+    slot_expert = a[o:o + S]; o += S
+    slot_rows = a[o:o + S]; o += S
+    row_of = a[o:o + S * 16].reshape(S, 16); o += S * 16
+    pair_of = a[o:o + S * 16].reshape(S, 16)
+    return {"n_slots": n, "n_routed": int(a[1]), "slot_expert": slot_expert[:n].copy(),
+            "slot_rows": slot_rows[:n].copy(), "row_of": row_of[:n].copy(),
+            "pair_of": pair_of[:n].copy()}
+
+
+MOE_MAX_SLOTS = 136

@@ -157,8 +157,9 @@ class LayerWeights:
 class VerifyModel:
     """Weights, KV pools and step buffers of one verify-step configuration."""
 
-    def __init__(self, cfg: VerifyConfig, seed: int = 0, keep_raw: bool = False,
-                 kv_std: float = 1.0):
+    def __init__(self, cfg: VerifyConfig, seed: int = 0, keep_raw=False, kv_std: float = 1.0):
+        """keep_raw: keep the unshuffled GGUF bytes (and the router / LM head) for parity
+        checks -- True for every layer, or an int n for the first n layers."""
         self.cfg = c = cfg
         self.keep_raw = keep_raw
         dev = "cuda"
@@ -174,23 +175,24 @@ class VerifyModel:
 
         self.layers = []
         for i in range(c.layers):
+            kr = bool(keep_raw) if isinstance(keep_raw, bool) else i < int(keep_raw)
             lw = LayerWeights(in_norm=gamma(H), post_norm=gamma(H), q_norm=gamma(c.head_dim),
                               k_norm=gamma(c.head_dim),
-                              qkv=packed_random(c.attn_fmt, c.qkv_n, H, sub(i, 0), keep_raw),
-                              o=packed_random(c.attn_fmt, H, c.heads * c.head_dim, sub(i, 1), keep_raw))
+                              qkv=packed_random(c.attn_fmt, c.qkv_n, H, sub(i, 0), kr),
+                              o=packed_random(c.attn_fmt, H, c.heads * c.head_dim, sub(i, 1), kr))
             if c.moe:
                 E, F = c.experts, c.expert_ffn
                 router = (torch.randn(E + 1, H, device=dev, generator=gen) / math.sqrt(H)).bfloat16()
                 lw.router = Lops.dense_shuffle(router)
-                lw.gu = packed_random(c.ffn_fmt, E * 2 * F, H, sub(i, 2), keep_raw)
-                lw.dn = packed_random(c.ffn_fmt, E * H, F, sub(i, 3), keep_raw)
-                lw.sh_gu = packed_random(c.ffn_fmt, 2 * F, H, sub(i, 4), keep_raw)
-                lw.sh_dn = packed_random(c.ffn_fmt, H, F, sub(i, 5), keep_raw)
-                if keep_raw:
+                lw.gu = packed_random(c.ffn_fmt, E * 2 * F, H, sub(i, 2), kr)
+                lw.dn = packed_random(c.ffn_fmt, E * H, F, sub(i, 3), kr)
+                lw.sh_gu = packed_random(c.ffn_fmt, 2 * F, H, sub(i, 4), kr)
+                lw.sh_dn = packed_random(c.ffn_fmt, H, F, sub(i, 5), kr)
+                if kr:
                     lw.raw["router"] = router
             else:
-                lw.gu = packed_random(c.ffn_fmt, 2 * c.ffn, H, sub(i, 2), keep_raw)
-                lw.dn = packed_random(c.ffn_fmt, H, c.ffn, sub(i, 3), keep_raw)
+                lw.gu = packed_random(c.ffn_fmt, 2 * c.ffn, H, sub(i, 2), kr)
+                lw.dn = packed_random(c.ffn_fmt, H, c.ffn, sub(i, 3), kr)
             self.layers.append(lw)
         self.embed = (0.02 * torch.randn(V, H, device=dev, generator=gen)).half()
         head = (0.02 * torch.randn(V, H, device=dev, generator=gen)).half()
@@ -281,8 +283,11 @@ class VerifyModel:
         self.lens.fill_(ctx + T)
 
     # -----------------------------------------------------------------------------------
-    def forward(self, *, upto_layer=None):
-        """Target model over the staged block -> self.logits [T, V] f32."""
+    def forward(self, *, upto_layer=None, record_slots=None):
+        """Target model over the staged block -> self.logits [T, V] f32. record_slots: optional
+        int32 [layers] device tensor that receives each MoE layer's plan size (routed unique
+        experts + shared) for byte accounting; it adds one copy per layer, so timed steps leave
+        it out."""
         c, T = self.cfg, self.cfg.block
         H = c.hidden
         Lops.gather_embedding(self.ids, self.embed, self.x)
@@ -311,6 +316,8 @@ class VerifyModel:
                                 c.experts + 1, H)
                 Lops.moe_route_plan(self.router_logits, c.experts, c.topk, self.route_w,
                                     self.route_ids, self.shared_w, self.plan)
+                if record_slots is not None:
+                    record_slots[i:i + 1].copy_(self.plan[:4].view(torch.int32))
                 Lops.moe_experts(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, self.plan,
                                  self.ws_h2, self.route_w, self.shared_w, self.moe_act,
                                  self.pairs, self.shared_out, self.x, T, c.topk, c.experts, H,

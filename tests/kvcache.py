@@ -2,6 +2,8 @@
 back (the reader restates tests/test_lfm2_dspark_reference.py:30-36)."""
 import torch
 
+from oracle.model import cache_rows  # noqa: F401  (re-exported for the tests)
+
 PAGE = 16
 
 
@@ -19,16 +21,6 @@ def pools_from_dense(k, v, table, num_blocks):
     kp[blocks] = k.view(npages, PAGE, H, D // 16, 16).permute(0, 2, 3, 1, 4)
     vp[blocks] = v.view(npages, PAGE // 4, 4, H, D).permute(0, 3, 1, 4, 2)
     return kp, vp
-
-
-def cache_rows(pool, pages, heads, dim, page, *, key):
-    """tests/test_lfm2_dspark_reference.py:30-36: pool -> dense rows [len, heads, dim]."""
-    x = pool.view(torch.bfloat16)
-    if key:
-        x = x.view(-1, heads, dim // 16, page, 16)[pages].permute(0, 3, 1, 2, 4)
-    else:
-        x = x.view(-1, heads, page // 4, dim, 4)[pages].permute(0, 2, 4, 1, 3)
-    return x.reshape(-1, heads, dim)
 
 
 def tree_masks(parents):
