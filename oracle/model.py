@@ -100,6 +100,40 @@ def swiglu_ffn(x, gu, dn, F):
     return linear(act, dn)
 
 
+def visibility(ctx, masks):
+    """[T, ctx + T] bool: row t sees the context and block row j iff bit j of masks[t]."""
+    T = len(masks)
+    vis = torch.zeros(T, ctx + T, dtype=torch.bool)
+    vis[:, :ctx] = True
+    for t in range(T):
+        for j in range(T):
+            if (masks[t] >> j) & 1:
+                vis[t, ctx + j] = True
+    return vis
+
+
+def masked_attention(q, keys, vals, vis, scale):
+    """GQA softmax attention in float64: q [T, Hq, D], keys/vals [L, Hkv, D], vis [T, L]."""
+    T, Hq, D = q.shape
+    Hkv = keys.shape[1]
+    G = Hq // Hkv
+    attn = torch.empty(T, Hq, D)
+    for hk in range(Hkv):
+        qs = q[:, hk * G:(hk + 1) * G].double()
+        s = torch.einsum("tgd,ld->tgl", qs, keys[:, hk].double()) * scale
+        s = s.masked_fill(~vis[:, None, :], float("-inf"))
+        attn[:, hk * G:(hk + 1) * G] = torch.einsum("tgl,ld->tgd", s.softmax(-1), vals[:, hk].double()).float()
+    return attn
+
+
+def route(logits, E, K):
+    """Qwen-Next routing: softmax over the E routed logits, top-K, renormalised; sigmoid of
+    column E is the shared expert's gate."""
+    probs = torch.softmax(logits[:, :E], -1)
+    w, ids = torch.topk(probs, K, dim=-1)
+    return ids, w / w.sum(-1, keepdim=True), torch.sigmoid(logits[:, E])
+
+
 def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
     """One layer. x: block input [T, H] (bf16 values), res: residual stream or None,
     k_ctx/v_ctx: context keys/values [ctx, Hkv, D]; masks: per-row visibility bits over the
@@ -121,22 +155,7 @@ def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
     k = bf(rope(head_norm(k, ref.k_norm), cos, sin, c.rot_half))
     keys = torch.cat([k_ctx.float(), k])
     vals = torch.cat([v_ctx.float(), v])
-    ctx = k_ctx.shape[0]
-    L = ctx + T
-    vis = torch.zeros(T, L, dtype=torch.bool)
-    vis[:, :ctx] = True
-    for t in range(T):
-        for j in range(T):
-            if (masks[t] >> j) & 1:
-                vis[t, ctx + j] = True
-    G = Hq // Hkv
-    attn = torch.empty(T, Hq, D)
-    for hk in range(Hkv):
-        qs = q[:, hk * G:(hk + 1) * G].double()
-        s = torch.einsum("tgd,ld->tgl", qs, keys[:, hk].double()) * D ** -0.5
-        s = s.masked_fill(~vis[:, None, :], float("-inf"))
-        attn[:, hk * G:(hk + 1) * G] = torch.einsum("tgl,ld->tgd", s.softmax(-1), vals[:, hk].double()).float()
-    attn = bf(attn)
+    attn = bf(masked_attention(q, keys, vals, visibility(k_ctx.shape[0], masks), D ** -0.5))
     o = linear(attn.view(T, -1), ref.o)
     r2 = bf(o + r1)
     h2 = rmsnorm(r2, ref.post_norm, c.eps)
@@ -144,9 +163,7 @@ def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
     if c.moe:
         E, F, K = c.experts, c.expert_ffn, c.topk
         logits = (h2.double() @ ref.router.double().T).float()
-        probs = torch.softmax(logits[:, :E], -1)
-        w, ids = torch.topk(probs, K, dim=-1)
-        w = w / w.sum(-1, keepdim=True)
+        ids, w, gate = route(logits, E, K)
         out = torch.zeros(T, c.hidden)
         for t in range(T):
             acc = torch.zeros(c.hidden)
@@ -155,7 +172,7 @@ def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
                 y = swiglu_ffn(h2[t:t + 1], gu, dn, F)[0]
                 acc += y * w[t, kk]
             sh = swiglu_ffn(h2[t:t + 1], ref.sh_gu, ref.sh_dn, F)[0]
-            acc += sh * torch.sigmoid(logits[t, E])
+            acc += sh * gate[t]
             out[t] = acc
         x2 = bf(out)
         routing = ids
