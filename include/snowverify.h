@@ -152,6 +152,13 @@ int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_
 /* Extension, no counterpart in the reference (a tuning knob): pages per context split of
  * snowverify_paged_attention; 0 = automatic. Returns the previous value. */
 int snowverify_attention_pages_per_split(int pages);
+/* Extension, no counterpart in the reference (a tuning knob): waves per 16-row tile of the
+ * attention's split kernel, 1 or 2 (two split the head's output columns); 0 = automatic.
+ * Returns the previous value. */
+int snowverify_attention_d_split(int dh);
+/* Extension, no counterpart in the reference (a tuning knob): pages in the attention split
+ * kernel's LDS ring, 4 or 8; 0 = automatic. Returns the previous value. */
+int snowverify_attention_ring(int pages);
 
 /* ---- geometry ------------------------------------------------------------------------ */
 /* The reference compiles its shapes in (snowllm/_capi.py:44-113); here they are run-time

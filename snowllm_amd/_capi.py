@@ -86,6 +86,8 @@ _SIGS = [
     ("snowverify_paged_attention_scratch_bytes", c_int64, [c_int64] * 5),
     ("snowverify_paged_attention", c_int, [P] * 7 + [c_int64] * 7 + [c_float, P, c_int64, S]),
     ("snowverify_attention_pages_per_split", c_int, [c_int]),
+    ("snowverify_attention_d_split", c_int, [c_int]),
+    ("snowverify_attention_ring", c_int, [c_int]),
     # geometry and layer plumbing
     ("snowllm_model_config", None, [P]),
     ("snowllm_select_geometry", c_int, [c_int]),

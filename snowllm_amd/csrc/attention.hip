@@ -11,12 +11,12 @@
 // ahead of the MFMAs, so K and V leave HBM once per workgroup whatever the number of tiles.
 // Each wave waits for its own loads of a page (vmcnt) and a barrier publishes the page.
 //
-// MFMA mapping, per wave and page:
-//   S^T[key, row] = K[key, :] . Q[row, :]      v_mfma_f32_16x16x32_bf16 over d:
+// MFMA mapping, per wave and 32-key chunk (two pages):
+//   S^T[key, row] = K[key, :] . Q[row, :]      v_mfma_f32_16x16x32_bf16 over d, per page:
 //                                              A = K (16 keys x 32 d, ds_read_b128)
 //                                              B = Q^T (held in registers)
-//   O^T[d, row]  += V^T[d, key] . P^T[key, row] v_mfma_f32_16x16x16_bf16 over the 16 keys:
-//                                              A = V^T (ds_read_b64 per d tile)
+//   O^T[d, row]  += V^T[d, key] . P^T[key, row] v_mfma_f32_16x16x32_bf16 over the 32 keys:
+//                                              A = V^T (two ds_read_b64 per d tile)
 //                                              B = P^T, straight from the S^T registers
 // Putting keys on the M side makes the C layout of S^T (row = lane & 15, key = 4*(lane>>4)+i)
 // exactly the B layout P^T needs, so the softmax never leaves registers.
@@ -39,7 +39,8 @@ typedef __attribute__((address_space(4))) const int32_t cint32;
 constexpr int PAGE = 16;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int SPLITS_MAX = 512;
-constexpr int MAX_TILES = 8;  // row tiles (waves) per workgroup: T * G <= 128
+constexpr int MAX_TILES = 8;     // row tiles per workgroup: T * G <= 128
+constexpr int MAX_TILES_DH = 4;  // up to 4 tiles, each tile's output columns split over 2 waves
 
 struct AttnArgs {
   const uint16_t* q;        // [batch*T, Hq, D]
@@ -112,86 +113,113 @@ __device__ __forceinline__ void dma_page(const uint8_t* __restrict__ kp,
   }
 }
 
-// Online-softmax state of one wave (16 query rows = lanes' columns).
-template <int D>
+// Online-softmax state of one wave (16 query rows = lanes' columns, D / DH output columns):
+// O^T, the row's reference maximum m (log2 domain) and this lane's part of the row sum l.
+template <int D, int DH>
 struct AttnState {
-  floatx4 o[D / 16];
+  floatx4 o[D / 16 / DH];
   float m, l;
 };
+constexpr float RESCALE = 8.0f;  // p = 2^(s - m) stays <= 2^8 between rescales
 
-// One page from its LDS slot: S^T = K Q^T, masked online softmax, O^T += V^T P^T.
-template <int D>
-__device__ __forceinline__ void attend_page(AttnState<D>& st, const uint8_t* slot,
-                                            const bf16x8 (&qb)[D / 32], int pg, int L, int ctx,
-                                            uint64_t anc, float qk_scale, int kq, int col) {
+// Two pages (32 keys) from their LDS slots: the two S^T products are independent MFMA
+// chains; P^T of both pages forms one 16x16x32 B operand (slots 0..3 = page A keys 4kq + i,
+// slots 4..7 = page B keys 4kq + i) and V^T reads the same keys of both pages, so O^T += V^T P^T
+// takes half the MFMA cycles of two 16x16x16 steps. Keys of page B are masked when !has_b.
+template <int D, int DH>
+__device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t* sa,
+                                             const uint8_t* sb, bool has_b,
+                                             const bf16x8 (&qb)[D / 32], int pg, int L, int ctx,
+                                             uint64_t anc, float qk_scale, int kq, int col,
+                                             int dhalf) {
   using G = SlotGeo<D>;
-  constexpr int DS = D / 32, DT = D / 16;
-  u32x4 kr[DS];
-  u32x2 vr[DT];
+  constexpr int DS = D / 32, DT = D / 16 / DH;
+  // every LDS read of the chunk is issued before the first MFMA (V's latency then hides behind
+  // the S products and the softmax)
+  u32x4 ka[DS], kb[DS];
+  u32x2 va[DT], vb[DT];
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds)  // K [D/16][16 keys][16 d]: chunk 2*ds + kq/2, offset 8*(kq&1)
-    kr[ds] = *(const u32x4*)(slot + ((2 * ds + (kq >> 1)) * PAGE + col) * 32 + (kq & 1) * 16);
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)  // V group kq: keys 4kq..4kq+3 of d = dt*16 + col
-    vr[dt] = *(const u32x2*)(slot + G::KBYTES + kq * (G::VGROUP + G::VPAD) + (dt * 16 + col) * 8);
-  floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ds = 0; ds < DS; ++ds)
-    sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[ds]), qb[ds], sacc,
-                                                   0, 0, 0);
-  // mask + online softmax (row = col; keys 4*kq + i)
-  float sv[4];
-  float cmax = -__builtin_huge_valf();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int pos = pg * PAGE + 4 * kq + i;
-    bool vis = pos < L;
-    if (vis && pos >= ctx) vis = (anc >> (pos - ctx)) & 1ull;
-    sv[i] = vis ? sacc[i] * qk_scale : -__builtin_huge_valf();
-    cmax = sv[i] > cmax ? sv[i] : cmax;
+  for (int ds = 0; ds < DS; ++ds) {
+    const int off = ((2 * ds + (kq >> 1)) * PAGE + col) * 32 + (kq & 1) * 16;
+    ka[ds] = *(const u32x4*)(sa + off);
+    kb[ds] = *(const u32x4*)(sb + off);
   }
-  cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-  cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-  const float m_new = fmaxf(st.m, cmax);
-  const float msafe = (m_new == -__builtin_huge_valf()) ? 0.f : m_new;
-  const float alpha = __builtin_amdgcn_exp2f(st.m - msafe);  // exp2(-inf) = 0
-  float p[4];
-  float psum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    p[i] = __builtin_amdgcn_exp2f(sv[i] - msafe);
-    psum += p[i];
-  }
-  psum += __shfl_xor(psum, 16, 64);
-  psum += __shfl_xor(psum, 32, 64);
-  st.l = st.l * alpha + psum;
-  st.m = m_new;
-  // P^T operand (keys 4kq + i of row col), carried as a bf16 pair (hi + lo residual), which
-  // keeps ~16 significant bits through the MFMA.
-  float plo[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) plo[i] = p[i] - bf16_to_f32(f32_to_bf16(p[i]));
-  const u32x2 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
-  const u32x2 pwl = {pack_bf16x2(plo[0], plo[1]), pack_bf16x2(plo[2], plo[3])};
-  const short4 pb = __builtin_bit_cast(short4, pw);
-  const short4 pbl = __builtin_bit_cast(short4, pwl);
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
-    const short4 vt = __builtin_bit_cast(short4, vr[dt]);
-    floatx4 o = st.o[dt] * alpha;
-    o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, pb, o, 0, 0, 0);
-    st.o[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, pbl, o, 0, 0, 0);
+    const int off = G::KBYTES + kq * (G::VGROUP + G::VPAD) + ((dhalf * DT + dt) * 16 + col) * 8;
+    va[dt] = *(const u32x2*)(sa + off);
+    vb[dt] = *(const u32x2*)(sb + off);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds) {
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[ds]), qb[ds], s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kb[ds]), qb[ds], s1, 0, 0, 0);
+  }
+  float sv[8];
+  float cmax = -__builtin_huge_valf();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int pos = (pg + (i >> 2)) * PAGE + 4 * kq + (i & 3);
+    bool vis = pos < L && (i < 4 || has_b);
+    if (vis && pos >= ctx) vis = (anc >> (pos - ctx)) & 1ull;
+    const float x = (i < 4 ? s0[i & 3] : s1[i & 3]) * qk_scale;
+    sv[i] = vis ? x : -__builtin_huge_valf();
+    cmax = sv[i] > cmax ? sv[i] : cmax;
+  }
+  // Lazy rescaling: the row maximum (shared by the four lanes of a row, which hold different
+  // keys of one P^T column) moves only when some score exceeds it by more than 2^RESCALE in
+  // the exp2 domain; otherwise p <= 2^RESCALE and nothing is rescaled. The decision is
+  // wave-uniform, so every lane of a row keeps the same reference. Row sums stay per lane
+  // until the end of the split.
+  if (__builtin_amdgcn_ballot_w64(cmax > st.m + RESCALE) != 0) {
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+    const float m_new = fmaxf(st.m, cmax);
+    // 0 when the row had no visible key yet; 1 for a row that still has none
+    const float alpha =
+        m_new == -__builtin_huge_valf() ? 1.0f : __builtin_amdgcn_exp2f(st.m - m_new);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.o[dt] *= alpha;
+    st.l *= alpha;
+    st.m = m_new;
+  }
+  const float msafe = (st.m == -__builtin_huge_valf()) ? 0.f : st.m;
+  float p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    p[i] = __builtin_amdgcn_exp2f(sv[i] - msafe);
+    st.l += p[i];
+  }
+  // P^T as a bf16 pair (hi + lo residual): ~16 significant bits through the MFMA
+  float plo[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) plo[i] = p[i] - bf16_to_f32(f32_to_bf16(p[i]));
+  const u32x4 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                    pack_bf16x2(p[6], p[7])};
+  const u32x4 pwl = {pack_bf16x2(plo[0], plo[1]), pack_bf16x2(plo[2], plo[3]),
+                     pack_bf16x2(plo[4], plo[5]), pack_bf16x2(plo[6], plo[7])};
+  const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+  const bf16x8 pbl = __builtin_bit_cast(bf16x8, pwl);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const bf16x8 vt = __builtin_bit_cast(bf16x8, u32x4{va[dt].x, va[dt].y, vb[dt].x, vb[dt].y});
+    floatx4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pb, st.o[dt], 0, 0, 0);
+    st.o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pbl, o, 0, 0, 0);
   }
 }
 
-template <int D, int CPW, int RING>
-__global__ void __launch_bounds__(MAX_TILES * 64) attn_split_kernel(AttnArgs a) {
+template <int D, int CPW, int RING, int DH>
+__global__ void __launch_bounds__(DH == 1 ? MAX_TILES * 64 : MAX_TILES_DH * 2 * 64)
+attn_split_kernel(AttnArgs a) {
   using G = SlotGeo<D>;
-  constexpr int DS = D / 32, DT = D / 16;
+  constexpr int DS = D / 32, DT = D / 16 / DH;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING * G::BYTES];
-  const int NW = (int)(blockDim.x >> 6);  // == NRT
+  const int NW = (int)(blockDim.x >> 6);  // NRT * DH
   const int lane = threadIdx.x & 63;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // row tile
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = wv / DH, dhalf = wv % DH;  // row tile, output-column part
   const int kq = lane >> 4, col = lane & 15;
   const int split = blockIdx.x % a.S;
   const int h = (blockIdx.x / a.S) % a.Hkv;
@@ -215,7 +243,7 @@ __global__ void __launch_bounds__(MAX_TILES * 64) attn_split_kernel(AttnArgs a) 
   if (a.tree) anc = row_live ? a.tree[(int64_t)b * a.T + t] : 1ull;
   else anc = (t >= 63) ? ~0ull : ((2ull << t) - 1ull);
 
-  AttnState<D> st;
+  AttnState<D, DH> st;
 #pragma unroll
   for (int i = 0; i < DT; ++i) st.o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   st.m = -__builtin_huge_valf();
@@ -243,18 +271,22 @@ __global__ void __launch_bounds__(MAX_TILES * 64) attn_split_kernel(AttnArgs a) 
     auto issue = [&](int pg, int slot_idx) {
       const int64_t blk = trow[pg < p1 ? pg : p0];
       dma_page<D, CPW>(kbase + blk * block_bytes, vbase + blk * block_bytes,
-                       ring + slot_idx * G::BYTES, w, NW, lane);
+                       ring + slot_idx * G::BYTES, wv, NW, lane);
     };
     wait_vmcnt<0>();  // Q has landed: the loop below then waits on page loads only
+    // pages go two per step (one 32-key chunk); RING - 2 pages are queued ahead of a step
 #pragma unroll
-    for (int i = 0; i < RING - 1; ++i) issue(p0 + i, i);
-    int slot = 0;
-    for (int pg = p0; pg < p1; ++pg) {
-      wait_vmcnt<(RING - 2) * CPW>();  // this wave's loads of page pg have landed
-      block_barrier();                 // ... and every wave's; page pg - 1 is free
-      issue(pg + RING - 1, slot == 0 ? RING - 1 : slot - 1);
-      attend_page<D>(st, ring + slot * G::BYTES, qb, pg, L, ctx, anc, a.qk_scale, kq, col);
-      slot = slot == RING - 1 ? 0 : slot + 1;
+    for (int i = 0; i < RING - 2; ++i) issue(p0 + i, i);
+    int slot = 0;  // first ring slot of the current chunk (even)
+    for (int pg = p0; pg < p1; pg += 2) {
+      wait_vmcnt<(RING - 4) * CPW>();  // this wave's loads of pages pg, pg + 1 have landed
+      block_barrier();                 // ... and every wave's; the previous chunk is free
+      const int prev = slot == 0 ? RING - 2 : slot - 2;
+      issue(pg + RING - 2, prev);
+      issue(pg + RING - 1, prev + 1);
+      attend_chunk<D, DH>(st, ring + slot * G::BYTES, ring + (slot + 1) * G::BYTES, pg + 1 < p1,
+                          qb, pg, L, ctx, anc, a.qk_scale, kq, col, dhalf);
+      slot = slot == RING - 2 ? 0 : slot + 2;
     }
     wait_vmcnt<0>();  // no load may still target LDS when the workgroup retires
   }
@@ -262,11 +294,14 @@ __global__ void __launch_bounds__(MAX_TILES * 64) attn_split_kernel(AttnArgs a) 
   const int64_t pidx = ((((int64_t)b * a.Hkv + h) * a.NRT + w) * a.S + split);
   float* po = a.part_o + pidx * 16 * D + (int64_t)col * D;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) *(floatx4*)(po + dt * 16 + 4 * kq) = st.o[dt];
-  if (kq == 0) {
+  for (int dt = 0; dt < DT; ++dt) *(floatx4*)(po + (dhalf * DT + dt) * 16 + 4 * kq) = st.o[dt];
+  // row sums: add the four lanes of each row in a fixed order
+  float l = st.l + __shfl_xor(st.l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (kq == 0 && dhalf == 0) {
     float* pml = a.part_ml + (pidx * 16 + col) * 2;
     pml[0] = st.m;
-    pml[1] = st.l;
+    pml[1] = l;
   }
 }
 
@@ -342,15 +377,20 @@ inline int n_row_tiles(int T, int G) { return (T * G + 15) / 16; }
 
 int g_pages_per_split = 0;  // 0: automatic
 
-// Pages per split: about 128 workgroups over the launch (each keeps RING - 1 pages in flight),
-// at least two pages, at most SPLITS_MAX splits.
+// Pages per split (measured on MI355X): short contexts want ~384 workgroups of at least six
+// pages (more splits cost more partials than they gain); long contexts ~216 workgroups, one
+// per CU, since the partials are then negligible and longer splits pipeline better.
 int choose_pages_per_split(int64_t batch, int Hkv, int64_t pages) {
   int64_t pps = g_pages_per_split;
   if (pps <= 0) {
     const int64_t heads = batch * Hkv;
-    const int64_t target = (128 + heads - 1) / heads;
+    int64_t target = (384 + heads - 1) / heads;
     pps = (pages + target - 1) / target;
-    if (pps < 2) pps = 2;
+    if (pps >= 48) {
+      target = (216 + heads - 1) / heads;
+      pps = (pages + target - 1) / target;
+    }
+    if (pps < 6) pps = 6;
   }
   while ((pages + pps - 1) / pps > SPLITS_MAX) ++pps;
   return (int)pps;
@@ -358,22 +398,43 @@ int choose_pages_per_split(int64_t batch, int Hkv, int64_t pages) {
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Loads per wave per page: the page's chunks over the NRT waves, rounded up to a power of two.
-template <int D>
-int launch_split(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
+// Waves per row tile: two (each computing S for the full head and O for half of its columns)
+// when the tiles fit, so that a workgroup keeps more waves per SIMD; loads per wave per page:
+// the page's chunks over the waves, rounded up to a power of two.
+int g_ring = 0;  // LDS ring pages: 0 automatic, 4 or 8
+
+template <int D, int DH, int RING>
+int launch_split_ring(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   constexpr int CH = SlotGeo<D>::CHUNKS;
+  const int nw = a.NRT * DH;
   int cpw = 1;
-  while (cpw * a.NRT < CH) cpw *= 2;
-  const dim3 grid((unsigned)nblocks), block((unsigned)(64 * a.NRT));
+  while (cpw * nw < CH) cpw *= 2;
+  if (RING == 8 && cpw == 16) return launch_split_ring<D, DH, 4>(a, nblocks, s);  // vmcnt range
+  const dim3 grid((unsigned)nblocks), block((unsigned)(64 * nw));
   switch (cpw) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1, 8>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2, 8>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4, 8>), grid, block, 0, s, a); break;
-    case 8: hipLaunchKernelGGL((attn_split_kernel<D, 8, 8>), grid, block, 0, s, a); break;
-    case 16: hipLaunchKernelGGL((attn_split_kernel<D, 16, 4>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1, RING, DH>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2, RING, DH>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4, RING, DH>), grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((attn_split_kernel<D, 8, RING, DH>), grid, block, 0, s, a); break;
+    case 16: hipLaunchKernelGGL((attn_split_kernel<D, 16, 4, DH>), grid, block, 0, s, a); break;
     default: return SV_ENOTSUP;
   }
   return SV_OK;
+}
+
+template <int D, int DH>
+int launch_split_dh(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
+  if (g_ring == 8) return launch_split_ring<D, DH, 8>(a, nblocks, s);
+  return launch_split_ring<D, DH, 4>(a, nblocks, s);  // measured: as fast, half the LDS
+}
+
+int g_d_split = 0;  // 0: automatic, 1 or 2 forced
+
+template <int D>
+int launch_split(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
+  const int dh = g_d_split ? g_d_split : (a.NRT <= MAX_TILES_DH ? 2 : 1);
+  if (dh == 2 && a.NRT <= MAX_TILES_DH) return launch_split_dh<D, 2>(a, nblocks, s);
+  return launch_split_dh<D, 1>(a, nblocks, s);
 }
 
 }  // namespace
@@ -450,5 +511,21 @@ SV_API int snowverify_paged_attention(const void* q, const void* k_pool, const v
 SV_API int snowverify_attention_pages_per_split(int pages) {
   const int prev = g_pages_per_split;
   g_pages_per_split = pages < 0 ? 0 : pages;
+  return prev;
+}
+
+// Tuning knob (extension, no reference counterpart): waves per row tile of the attention's
+// split kernel (1 or 2; 0 restores the automatic choice). Returns the previous value.
+SV_API int snowverify_attention_d_split(int dh) {
+  const int prev = g_d_split;
+  g_d_split = (dh == 1 || dh == 2) ? dh : 0;
+  return prev;
+}
+
+// Tuning knob (extension, no reference counterpart): pages in the attention's LDS ring, 4 or 8
+// (0 restores the automatic choice). Returns the previous value.
+SV_API int snowverify_attention_ring(int pages) {
+  const int prev = g_ring;
+  g_ring = (pages == 4 || pages == 8) ? pages : 0;
   return prev;
 }
