@@ -124,7 +124,13 @@ __global__ void __launch_bounds__(NT) softmax_exp(const float* __restrict__ logi
   __shared__ uint64_t red[NT / WAVE];
   __shared__ float s_max;
   const int c = blockIdx.x, row = blockIdx.y;
-  if (threadIdx.x == 0) s_max = row_max_from_keys(tail.max_keys + row * C, C);
+  if (threadIdx.x < WAVE) {  // chunk maxima, one wave (exact in any order)
+    const uint32_t* keys = tail.max_keys + row * C;
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < C; i += WAVE) m = keys[i] > m ? keys[i] : m;
+    m = wave_max(m);
+    if (threadIdx.x == 0) s_max = ord_key_to_float(m);
+  }
   __syncthreads();
   const float M = s_max;
   const float* x = logits + (int64_t)row * V;
@@ -147,10 +153,11 @@ __global__ void __launch_bounds__(NT) softmax_norm(float* __restrict__ dense, in
                                                    SoftmaxTail tail, int C) {
   __shared__ float s_z;
   const int c = blockIdx.x, row = blockIdx.y;
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < WAVE) {  // fixed-point chunk sums, one wave (exact in any order)
     uint64_t z = 0;
-    for (int i = 0; i < C; ++i) z += tail.sums[row * C + i];
-    s_z = canon_unfix(z);
+    for (int i = threadIdx.x; i < C; i += WAVE) z += tail.sums[row * C + i];
+    z = wave_sum_u64(z);
+    if (threadIdx.x == 0) s_z = canon_unfix(z);
   }
   __syncthreads();
   const float Z = s_z;
@@ -230,6 +237,7 @@ __global__ void __launch_bounds__(TOPK_NT) topk_topp_rows(
     const float* __restrict__ top_p) {
   __shared__ TopkShared sh;
   const int row = blockIdx.x;
+  const int chunk = blockIdx.y;  // identity rows are copied chunk by chunk; selection uses chunk 0
   const float* p = dense + (int64_t)row * V;
   float* out_v = values + (int64_t)row * width;
   int64_t* out_i = ids + (int64_t)row * width;
@@ -239,13 +247,15 @@ __global__ void __launch_bounds__(TOPK_NT) topk_topp_rows(
   const bool nucleus = tp < 1.0f;
 
   if (k64 >= V && !nucleus) {
-    for (int64_t i = threadIdx.x; i < width; i += TOPK_NT) {
+    const int64_t end = ((int64_t)chunk + 1) * CHUNK < width ? ((int64_t)chunk + 1) * CHUNK : width;
+    for (int64_t i = (int64_t)chunk * CHUNK + threadIdx.x; i < end; i += TOPK_NT) {
       bool in = i < V;
       out_v[i] = in ? p[i] : 0.0f;
       out_i[i] = in ? i : -1;
     }
     return;
   }
+  if (chunk != 0) return;
   if (k64 > TOPK_MAX || k64 > width) {
     // Unsupported list shape: the row is marked with id -2 and NaN values.
     for (int64_t i = threadIdx.x; i < width; i += TOPK_NT) {
@@ -518,9 +528,17 @@ struct ResidualRow {
   __device__ float operator()(int64_t k) const {
     float pk = p[k];
     if (!subtract) return pk;
+    const int64_t id = ids[k];
     float qk;
-    if (q) qk = row_prob_thread(q, cand, q_width, ids[k]);
-    else qk = (ids[k] == draft) ? 1.0f : 0.0f;
+    if (q) {
+      // identity layouts (ids[k] == k, cand[k] == k) resolve with loads independent of id
+      const bool in_q = k < q_width;
+      const float qd = in_q ? q[k] : 0.0f;
+      const int64_t cd = in_q ? cand[k] : -1;
+      qk = (id == k && cd == k) ? qd : row_prob_thread(q, cand, q_width, id);
+    } else {
+      qk = (id == draft) ? 1.0f : 0.0f;
+    }
     float d = __fsub_rn(pk, qk);
     return d > 0.0f ? d : 0.0f;
   }
@@ -575,21 +593,25 @@ __global__ void __launch_bounds__(NT) reject_pick(RejectArgs a, int C) {
   __shared__ int s_chunk;
   __shared__ uint64_t s_base, s_target;
   __shared__ int s_use_p;
+  __shared__ uint64_t s_sums[CHUNKS_MAX][2];
   const int r = blockIdx.x;
   const int64_t first = g_first[r];
+  for (int i = threadIdx.x; i < 2 * C; i += NT)
+    s_sums[i >> 1][i & 1] = g_chunk_sums[(r * CHUNKS_MAX + (i >> 1)) * 2 + (i & 1)];
+  __syncthreads();
   if (threadIdx.x == 0) {
     uint64_t R = 0;
-    for (int c = 0; c < C; ++c) R += g_chunk_sums[(r * CHUNKS_MAX + c) * 2 + 0];
+    for (int c = 0; c < C; ++c) R += s_sums[c][0];
     int use_p = 0;
     if (R == 0) {
       use_p = 1;
-      for (int c = 0; c < C; ++c) R += g_chunk_sums[(r * CHUNKS_MAX + c) * 2 + 1];
+      for (int c = 0; c < C; ++c) R += s_sums[c][1];
     }
     const uint64_t target = canon_scale_floor(a.uniform[r * a.width + a.width - 1], R);
     uint64_t pre = 0;
     int c = 0;
     for (; c < C; ++c) {
-      uint64_t s = g_chunk_sums[(r * CHUNKS_MAX + c) * 2 + use_p];
+      uint64_t s = s_sums[c][use_p];
       if (pre + s > target) break;
       pre += s;
     }
@@ -768,8 +790,8 @@ int launch_softmax(const float* logits, float* dense, int64_t rows, int64_t voca
 int launch_topk_topp(const float* dense, float* values, int64_t* ids, int64_t rows,
                      int64_t vocab, int64_t width, const int32_t* top_k, const float* top_p,
                      hipStream_t s) {
-  hipLaunchKernelGGL(topk_topp_rows, dim3((unsigned)rows), dim3(TOPK_NT), 0, s, dense, values,
-                     ids, vocab, width, top_k, top_p);
+  hipLaunchKernelGGL(topk_topp_rows, dim3((unsigned)rows, (unsigned)chunks_of(width)),
+                     dim3(TOPK_NT), 0, s, dense, values, ids, vocab, width, top_k, top_p);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
