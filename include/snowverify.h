@@ -226,7 +226,7 @@ int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, int64_t
 /* ---- feed-forward (extensions; the reference reaches these through snowllm_inference_*,
  * snowllm/_capi.py:687-692, whose weight descriptors and workspaces are internal) ------------ */
 /* res_out = x + res_in; y = RMSNorm(res_out) * gamma into the k-quant operand workspace ws (and
- * y_out if given). res_out must not alias x or res_in. */
+ * y_out if given). H <= 8192; res_out and y_out must not alias x or res_in. */
 int snowverify_norm_prep(const void* x, const void* res_in, void* res_out, const void* gamma,
                          void* y_out, void* ws, int64_t M, int64_t H, float eps, void* stream);
 /* 16-bit weight GEMV: repack size, repack (wt 1 = fp16, 2 = bf16), and C = A W^T (fp16 weights

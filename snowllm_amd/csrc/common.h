@@ -96,6 +96,43 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
+// Cross-lane moves on the VALU (DPP) instead of the LDS crossbar: quad xor 1 / xor 2, then
+// mirrors within 8 and 16 lanes leave every lane of a 16-lane row with the row's result; the
+// four rows meet through readlane. Each step is symmetric, so all lanes end with one value.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141,
+              DPP_MIRROR = 0x140;
+
+__device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
+  uint32_t o;
+  o = dpp_u32<DPP_QUAD_XOR1>(v); v = o > v ? o : v;
+  o = dpp_u32<DPP_QUAD_XOR2>(v); v = o > v ? o : v;
+  o = dpp_u32<DPP_HALF_MIRROR>(v); v = o > v ? o : v;
+  o = dpp_u32<DPP_MIRROR>(v); v = o > v ? o : v;
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+  return ab > cd ? ab : cd;
+}
+
+// Sum in a fixed order (pairs, quads, 8s, 16s, then rows 0 + 1 + 2 + 3).
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<DPP_QUAD_XOR2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<DPP_HALF_MIRROR>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<DPP_MIRROR>(__float_as_uint(v)));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (a + b) + (c + d);
+}
+
 // Block-wide reductions for blockDim.x == NT (a multiple of 64). `red` must hold NT/64 slots.
 template <int NT>
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* red) {

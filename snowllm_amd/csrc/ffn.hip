@@ -17,25 +17,19 @@ using namespace kq;
 inline hipStream_t Sx(void* s) { return (hipStream_t)s; }
 
 // ---------------------------------------------------------------------------------------
-// residual + RMSNorm + operand conversion. One block per 16-row tile, one wave per superblock
-// (waves loop when H > 16 superblocks), so x and the residual are read from HBM once:
+// residual + RMSNorm + operand conversion. One workgroup per row, one thread per 16-byte word
+// of the row (thread t holds k = 8 t .. 8 t + 7), so the row is read with one load per thread:
 //   v = bf16(x + res_in) (v = x without res_in) -> res_out
 //   y = bf16(v * rsqrt(mean(v^2) + eps) * gamma) -> y_out (optional), fp16 operands -> ws
-// The row sums of squares meet in LDS and are added over the waves in a fixed order. Lane
-// (r = lane & 15, kq = lane >> 4) owns k = 32 j + 8 kq .. + 7 of each sub-block j, the layout
-// the operand conversion consumes, so y never leaves registers.
+// The sum of squares meets over the waves in LDS in a fixed order. Word t is (superblock
+// t / 32, sub-block (t / 4) % 8, k-group t % 4), so a superblock's 32 words lie in one half
+// wave and a sub-block's 4 words in one quad: the conversion's per-(row, superblock) maximum
+// and sub-block sums are cross-lane moves within the wave. The tile's rows past M write zero
+// operands, as the conversion of a zero row would.
 // ---------------------------------------------------------------------------------------
-constexpr int NORM_MAX_WAVES = 16;
+constexpr int NORM_MAX_THREADS = 1024;
 
-__device__ __forceinline__ void residual_words(const uint16_t* __restrict__ x,
-                                               const uint16_t* __restrict__ residual, int64_t off,
-                                               u32x4& v) {
-  const u32x4 xv = *(const u32x4*)(x + off);
-  if (!residual) {
-    v = xv;
-    return;
-  }
-  const u32x4 rv = *(const u32x4*)(residual + off);
+__device__ __forceinline__ u32x4 add_bf16_words(const u32x4& xv, const u32x4& rv) {
   const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, rw[4] = {rv.x, rv.y, rv.z, rv.w};
   uint32_t o[4];
 #pragma unroll
@@ -44,76 +38,91 @@ __device__ __forceinline__ void residual_words(const uint16_t* __restrict__ x,
     const float b = __uint_as_float(xw[i] & 0xffff0000u) + __uint_as_float(rw[i] & 0xffff0000u);
     o[i] = pack_bf16x2(a, b);
   }
-  v = u32x4{o[0], o[1], o[2], o[3]};
+  return u32x4{o[0], o[1], o[2], o[3]};
 }
 
-__global__ void __launch_bounds__(NORM_MAX_WAVES * 64) norm_prep_kernel(
+__global__ void __launch_bounds__(NORM_MAX_THREADS) norm_prep_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
     uint16_t* __restrict__ res_out, const uint16_t* __restrict__ gamma,
     uint16_t* __restrict__ y_out, void* __restrict__ ws, size_t tile_bytes, int64_t M, int64_t H,
     float eps) {
-  __shared__ float part[NORM_MAX_WAVES][16];
-  const int tile = blockIdx.x;
-  const int NW = (int)(blockDim.x >> 6);
-  const int lane = threadIdx.x & 63, r = lane & 15, kq = lane >> 4;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int S = (int)(H / QK);
-  const int64_t row = (int64_t)tile * TILE_M + r;
-  const bool live = row < M;
-  const int64_t base = row * H + kq * 8;
-  // 1) v for this wave's first superblock (kept), sum of squares over all of its superblocks
-  u32x4 v0[8];
-  float ss = 0.f;
-  for (int s = w; s < S; s += NW) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (live) residual_words(x, residual, base + (int64_t)s * QK + j * 32, v);
-      if (s == w) v0[j] = v;
-      const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = __uint_as_float(vw[i] << 16), b = __uint_as_float(vw[i] & 0xffff0000u);
-        ss = __builtin_fmaf(a, a, ss);
-        ss = __builtin_fmaf(b, b, ss);
-      }
-    }
+  __shared__ float part[NORM_MAX_THREADS / 64];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int nwaves = (int)(blockDim.x >> 6);
+  const int wpr = (int)(H >> 3);
+  const bool act = t < wpr, live = act && row < M;
+  const int64_t off = row * H + (int64_t)t * 8;
+  u32x4 v = {0u, 0u, 0u, 0u}, gv = {0u, 0u, 0u, 0u};
+  if (act) gv = *(const u32x4*)(gamma + (int64_t)t * 8);
+  if (live) {
+    v = *(const u32x4*)(x + off);
+    if (residual) v = add_bf16_words(v, *(const u32x4*)(residual + off));
   }
-  ss += __shfl_xor(ss, 16, 64);
-  ss += __shfl_xor(ss, 32, 64);
-  if (kq == 0) part[w][r] = ss;
+  const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = __uint_as_float(vw[i] << 16), b = __uint_as_float(vw[i] & 0xffff0000u);
+    ss = __builtin_fmaf(a, a, ss);
+    ss = __builtin_fmaf(b, b, ss);
+  }
+  ss = wave_sum_dpp(ss);
+  if (lane == 0) part[wv] = ss;
   __syncthreads();
   float tot = 0.f;
-  for (int ww = 0; ww < NW; ++ww) tot += part[ww][r];
+  for (int w = 0; w < nwaves; ++w) tot += part[w];
   const float inv = __frsqrt_rn(tot / (float)H + eps);
-  // 2) residual out, y, operands
-  XPrepView view = xprep_view((char*)ws + tile * tile_bytes, S);
-  for (int s = w; s < S; s += NW) {
-    u32x4 yw[8];
+  float y[8];
+  uint32_t yo[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t k0 = (int64_t)s * QK + j * 32 + kq * 8;
-      u32x4 v = v0[j];
-      if (s != w && live) residual_words(x, residual, base + (int64_t)s * QK + j * 32, v);
-      const u32x4 gv = *(const u32x4*)(gamma + k0);
-      const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        o[i] = pack_bf16x2(__uint_as_float(vw[i] << 16) * inv * __uint_as_float(gw[i] << 16),
-                           __uint_as_float(vw[i] & 0xffff0000u) * inv *
-                               __uint_as_float(gw[i] & 0xffff0000u));
-      }
-      yw[j] = live ? u32x4{o[0], o[1], o[2], o[3]} : u32x4{0u, 0u, 0u, 0u};
-      if (live) {
-        if (res_out) *(u32x4*)(res_out + row * H + k0) = v;
-        if (y_out) *(u32x4*)(y_out + row * H + k0) = yw[j];
-      }
-    }
-    XOperands op;
-    convert_words(yw, lane, op);
-    store_operands(view, s, lane, op);
+  for (int i = 0; i < 4; ++i) {
+    yo[i] = pack_bf16x2(__uint_as_float(vw[i] << 16) * inv * __uint_as_float(gw[i] << 16),
+                        __uint_as_float(vw[i] & 0xffff0000u) * inv *
+                            __uint_as_float(gw[i] & 0xffff0000u));
+    y[2 * i] = __uint_as_float(yo[i] << 16);
+    y[2 * i + 1] = __uint_as_float(yo[i] & 0xffff0000u);
   }
+  if (live) {
+    if (res_out) *(u32x4*)(res_out + off) = v;
+    if (y_out) *(u32x4*)(y_out + off) = u32x4{yo[0], yo[1], yo[2], yo[3]};
+  }
+  // operand conversion of (row, superblock t / 32): power-of-two scale from the maximum
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, __builtin_fabsf(y[i]));
+  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(mx))));
+  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_QUAD_XOR2>(__float_as_uint(mx))));
+  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_HALF_MIRROR>(__float_as_uint(mx))));
+  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_MIRROR>(__float_as_uint(mx))));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.40282346638528859812e38f) {
+    int E = (int)((__float_as_uint(mx) >> 23) & 0xff) - 127;
+    if (E < -126) E = -126;
+    e = E - 14;  // scaled maximum lands in [2^14, 2^15)
+  }
+  uint16_t h[8];
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const _Float16 hv = (_Float16)__builtin_ldexpf(y[kperm_c(i)], -e);
+    h[i] = __builtin_bit_cast(uint16_t, hv);
+    sum += (float)hv;
+  }
+  // sub-block sum over its four k-groups: (g0 + g1) + (g2 + g3)
+  sum += __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(sum)));
+  sum += __uint_as_float(dpp_u32<DPP_QUAD_XOR2>(__float_as_uint(sum)));
+  if (!act) return;
+  const int sb = t >> 5, j = (t >> 2) & 7, kq = t & 3;
+  const int tile = (int)(row / TILE_M), r = (int)(row % TILE_M);
+  XPrepView view = xprep_view((char*)ws + tile * tile_bytes, H / QK);
+  view.xop[((int64_t)sb * 8 + j) * 64 + r + 16 * kq] =
+      u32x4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+            h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
+  if (kq == 0) view.sxop[((int64_t)sb * 2 + (j >> 2)) * 64 + r + 16 * (j & 3)] = -sum;
+  if ((t & 31) == 0) view.scale[sb * 16 + r] = __builtin_ldexpf(1.0f, e);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -345,44 +354,54 @@ constexpr int ROUTE_THREADS = 1024;  // 16 waves: one per row (M <= 16), four fo
 __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, int topk, int lane,
                                           float& my_p, int& my_id, float& ksum) {
   float v[4];
+  uint32_t key[4];  // ordered keys of the candidates left; 0 = taken or past E
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = l[lane + 64 * i < E ? lane + 64 * i : 0];  // all in flight
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    v[i] = e < E ? l[e] : -__builtin_huge_valf();
+    v[i] = e < E ? v[i] : -__builtin_huge_valf();
+    key[i] = e < E ? ord_key(v[i]) : 0u;
   }
-  float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-  mx = wave_max(mx);
+  uint32_t km = key[0] > key[1] ? key[0] : key[1];
+  km = key[2] > km ? key[2] : km;
+  km = key[3] > km ? key[3] : km;
+  const float mx = ord_key_to_float(wave_max_u32_dpp(km));
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     if (lane + 64 * i < E) sum += __expf(v[i] - mx);
-  sum = wave_sum(sum);
-  uint32_t taken = 0;
+  sum = wave_sum_dpp(sum);
   my_p = 0.f;
   my_id = -1;
   for (int k = 0; k < topk; ++k) {
-    uint64_t best = 0;
+    // largest key left, then the lowest expert id holding it (e = lane + 64 i: lowest i first)
+    uint32_t b = key[0] > key[1] ? key[0] : key[1];
+    b = key[2] > b ? key[2] : b;
+    b = key[3] > b ? key[3] : b;
+    b = wave_max_u32_dpp(b);
+    int e = -1;
+    float ve = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E && !((taken >> i) & 1u)) {
-        const uint64_t key = argmax_key(v[i], (uint32_t)e);
-        best = key > best ? key : best;
+      const uint64_t hit = __ballot(key[i] == b);
+      if (e < 0 && hit) {
+        e = 64 * i + (int)__builtin_ctzll(hit);
+        ve = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), e & 63));
       }
     }
-    best = wave_max_u64(best);
-    const int e = (int)argmax_key_index(best);
-    const int ei = e >> 6;  // wave-uniform
-    if ((e & 63) == lane) taken |= 1u << ei;
-    const float mine = ei == 0 ? v[0] : ei == 1 ? v[1] : ei == 2 ? v[2] : v[3];
-    const float p = __expf(__shfl(mine, e & 63, 64) - mx) / sum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if ((e >> 6) == i && (e & 63) == lane) key[i] = 0u;
+    const float p = __expf(ve - mx) / sum;
     if (lane == k) {
       my_p = p;
       my_id = e;
     }
   }
   ksum = 0.f;
-  for (int k = 0; k < topk; ++k) ksum += __shfl(my_p, k, 64);
+  for (int k = 0; k < topk; ++k)
+    ksum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), k));
 }
 
 // Plan from ids_s[M * topk] in LDS; all ROUTE_THREADS threads call it.
@@ -620,19 +639,22 @@ int launch_dense(const void* w, const void* act, void* c, int M, int N, int S, i
 // =======================================================================================
 
 // Residual update + RMSNorm + operand conversion for the k-quant GEMVs: res_out = x + res_in
-// (x alone when res_in is null), y = RMSNorm(res_out) * gamma. All bf16 [M, H]; res_in,
-// res_out and y_out may be null; res_out must not alias x or res_in. ws as for
-// snowllm_gemm_kquant_a.
+// (x alone when res_in is null), y = RMSNorm(res_out) * gamma. All bf16 [M, H], H <= 8192;
+// res_in, res_out and y_out may be null; res_out and y_out must not alias x or res_in. ws as
+// for snowllm_gemm_kquant_a.
 SV_API int snowverify_norm_prep(const void* x, const void* res_in, void* res_out,
                                 const void* gamma, void* y_out, void* ws, int64_t M, int64_t H,
                                 float eps, void* stream) {
   if (M <= 0 || H <= 0 || H % 256) return SV_EINVAL;
   if (res_out && (res_out == x || res_out == res_in)) return SV_EINVAL;
+  if (y_out && (y_out == x || y_out == res_in)) return SV_EINVAL;
+  if (H > 8 * NORM_MAX_THREADS) return SV_EINVAL;
   const int64_t S = H / 256, mt = (M + 15) / 16;
-  const int nw = (int)(S < NORM_MAX_WAVES ? S : NORM_MAX_WAVES);
-  hipLaunchKernelGGL(norm_prep_kernel, dim3((unsigned)mt), dim3(64 * nw), 0, Sx(stream),
+  const int threads = (int)((H / 8 + 63) / 64 * 64);
+  hipLaunchKernelGGL(norm_prep_kernel, dim3((unsigned)(mt * 16)), dim3(threads), 0, Sx(stream),
                      (const uint16_t*)x, (const uint16_t*)res_in, (uint16_t*)res_out,
-                     (const uint16_t*)gamma, (uint16_t*)y_out, ws, xprep_tile_bytes(S), M, H, eps);
+                     (const uint16_t*)gamma,
+                     (uint16_t*)y_out, ws, xprep_tile_bytes(S), M, H, eps);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }

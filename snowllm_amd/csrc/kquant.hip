@@ -38,7 +38,9 @@ __global__ void __launch_bounds__(64) xprep_kernel(const uint16_t* __restrict__ 
 // NW waves split the superblocks of NTILE column tiles; the waves' partial sums meet in LDS
 // and are added in a fixed order. Reads past the end of a buffer return zero (buffer range
 // checking), so the last partial tile group needs no clamping.
-template <int FMT, int NTILE, int NW>
+// RAW: ws is the bf16 activation matrix [M, S*256] itself, converted in-kernel (one launch
+// for the whole operator instead of a prep pass + GEMV).
+template <int FMT, int NTILE, int NW, bool RAW = false>
 __global__ void __launch_bounds__(NW * 64) kquant_gemv(const u32x4* __restrict__ quant,
                                                        const u32x4* __restrict__ meta,
                                                        const void* __restrict__ ws,
@@ -55,7 +57,12 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv(const u32x4* __restrict__
   floatx4 acc[NTILE];
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-  gemv_loop<FMT, NTILE, NW>(st, w, S, tile0, 1, kq, Mv, acc);
+  if constexpr (RAW) {
+    const RawX rx = make_raw_x(ws, M, S * QK, lane);
+    gemv_loop_raw<FMT, NTILE, NW>(st, rx, w, S, tile0, 1, lane, Mv, acc);
+  } else {
+    gemv_loop<FMT, NTILE, NW>(st, w, S, tile0, 1, kq, Mv, acc);
+  }
   combine_waves<NTILE, NW>(part, acc, w, lane);
   for (int idx = threadIdx.x; idx < NTILE * 64; idx += NW * 64) {
     const int t = idx >> 6, l = idx & 63;
@@ -126,12 +133,12 @@ __global__ void shuffle_q80(const uint8_t* __restrict__ gguf, uint8_t* __restric
 
 bool fmt_ok(int fmt) { return fmt == FMT_Q4_K || fmt == FMT_Q8_0; }
 
-template <int FMT, int NTILE, int NW>
+template <int FMT, int NTILE, int NW, bool RAW = false>
 int launch_gemv(const void* quant, const void* meta, const void* ws, void* c, int M, int N, int S,
                 int c_bf16, hipStream_t s) {
   const int tiles = N / TILE_N;
   const int grid = (tiles + NTILE - 1) / NTILE;
-  hipLaunchKernelGGL((kquant_gemv<FMT, NTILE, NW>), dim3(grid), dim3(NW * 64), 0, s,
+  hipLaunchKernelGGL((kquant_gemv<FMT, NTILE, NW, RAW>), dim3(grid), dim3(NW * 64), 0, s,
                      (const u32x4*)quant, (const u32x4*)meta, ws, c, M, N, S, c_bf16);
   SV_CHECK_LAUNCH();
   return SV_OK;
@@ -139,16 +146,16 @@ int launch_gemv(const void* quant, const void* meta, const void* ws, void* c, in
 
 int g_gemv_variant = 0;  // 0 = automatic; see snowverify_gemv_variant
 
-template <int FMT>
+template <int FMT, bool RAW = false>
 int dispatch_gemv(const void* quant, const void* meta, const void* ws, void* c, int M, int N,
                   int S, int c_bf16, hipStream_t s) {
   switch (g_gemv_variant) {
-    case 1: return launch_gemv<FMT, 1, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 2: return launch_gemv<FMT, 2, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 3: return launch_gemv<FMT, 4, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 4: return launch_gemv<FMT, 1, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 5: return launch_gemv<FMT, 2, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 6: return launch_gemv<FMT, 4, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 1: return launch_gemv<FMT, 1, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 2: return launch_gemv<FMT, 2, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 3: return launch_gemv<FMT, 4, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 4: return launch_gemv<FMT, 1, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 5: return launch_gemv<FMT, 2, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 6: return launch_gemv<FMT, 4, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
     default: break;
   }
   const int tiles = N / TILE_N;
@@ -157,12 +164,12 @@ int dispatch_gemv(const void* quant, const void* meta, const void* ws, void* c, 
   if (S >= 8) {
     // (Q8_0 keeps two tiles: four tiles of int8 quants exceed the register file)
     if (tiles >= 4 * 192 && FMT == FMT_Q4_K)
-      return launch_gemv<FMT, 4, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    if (tiles >= 2 * 128 && S <= 8) return launch_gemv<FMT, 2, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    return launch_gemv<FMT, 1, 8>(quant, meta, ws, c, M, N, S, c_bf16, s);
+      return launch_gemv<FMT, 4, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    if (tiles >= 2 * 128 && S <= 8) return launch_gemv<FMT, 2, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    return launch_gemv<FMT, 1, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
   }
-  if (tiles >= 2 * 256) return launch_gemv<FMT, 2, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
-  return launch_gemv<FMT, 1, 4>(quant, meta, ws, c, M, N, S, c_bf16, s);
+  if (tiles >= 2 * 256) return launch_gemv<FMT, 2, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+  return launch_gemv<FMT, 1, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
 }
 
 }  // namespace
@@ -258,6 +265,15 @@ SV_API int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, c
                                  void* c, int64_t M, int64_t N, int64_t K, int c_is_bf16, void* ws,
                                  void* stream) {
   if (!fmt_ok(fmt) || M < 0 || N <= 0 || K <= 0 || K % 256 || N % TILE_N) return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  if (M <= TILE_M && M * K * 2 <= INT32_MAX) {
+    // one launch: the GEMV converts the bf16 activations itself (same operands as the
+    // prepared path, so the same results); ws is not touched
+    hipStream_t s = (hipStream_t)stream;
+    return fmt == FMT_Q4_K
+               ? dispatch_gemv<FMT_Q4_K, true>(quant, meta, a, c, (int)M, (int)N, (int)(K / 256), c_is_bf16, s)
+               : dispatch_gemv<FMT_Q8_0, true>(quant, meta, a, c, (int)M, (int)N, (int)(K / 256), c_is_bf16, s);
+  }
   int rc = snowllm_gemm_kquant_prepare_a(a, M, K, ws, stream);
   if (rc) return rc;
   return snowllm_gemm_kquant_a_prepared(fmt, quant, meta, c, M, N, K, c_is_bf16, ws, stream);

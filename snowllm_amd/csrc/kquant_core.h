@@ -385,6 +385,66 @@ __device__ __forceinline__ void gemv_loop(const GemvStreams& st, int w, int S, i
   }
 }
 
+// Variant for bf16 activations read straight from [M, K] (no operand workspace): the raw words
+// of superblock s are loaded with the weights and converted at multiply time (the same
+// per-(row, superblock) power-of-two conversion as the workspace path, so results match it).
+struct RawX {
+  __amdgpu_buffer_rsrc_t act;
+  uint32_t v_act;  // byte offset of this lane's row + 8 kq, or out of range for rows >= M
+};
+
+__device__ __forceinline__ RawX make_raw_x(const void* act, int M, int K, int lane) {
+  RawX rx;
+  const int r = lane & 15, kq = lane >> 4;
+  rx.act = __builtin_amdgcn_make_buffer_rsrc((void*)act, 0, M * K * 2, 0x00020000);
+  rx.v_act = r < M ? (uint32_t)((r * K + kq * 8) * 2) : 0x80000000u;
+  return rx;
+}
+
+template <int FMT, int NTILE>
+__device__ __forceinline__ void load_sb_raw(SbOperands<FMT, NTILE>& o, const GemvStreams& st,
+                                            const RawX& rx, int s, int S, int tile0,
+                                            int tstride) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o.x[j] = bload4(rx.act, rx.v_act, (uint32_t)((s * QK + j * 32) * 2));
+  load_sb<FMT, NTILE, false>(o, st, s, S, tile0, tstride);
+}
+
+template <int FMT, int NTILE>
+__device__ __forceinline__ void gemv_superblock_raw(SbOperands<FMT, NTILE>& o, floatx4* acc,
+                                                    int lane, uint32_t Mv) {
+  XOperands xo;
+  convert_words(o.x, lane, xo);
+  const int kq = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o.x[j] = xo.x[j];
+  o.sx0 = xo.sx0;
+  o.sx1 = xo.sx1;
+  // per-row scales of rows 4 kq .. 4 kq + 3 live in lanes 4 kq + i (kq = 0 row group)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o.scale[i] = __shfl(xo.scale, 4 * kq + i, 64);
+  gemv_superblock<FMT, NTILE>(o, acc, kq, Mv);
+}
+
+template <int FMT, int NTILE, int NW>
+__device__ __forceinline__ void gemv_loop_raw(const GemvStreams& st, const RawX& rx, int w, int S,
+                                              int tile0, int tstride, int lane, uint32_t Mv,
+                                              floatx4* acc) {
+  if (w >= S) return;
+  SbOperands<FMT, NTILE> bufA, bufB;
+  load_sb_raw<FMT, NTILE>(bufA, st, rx, w, S, tile0, tstride);
+  for (int s = w;;) {
+    if (s + NW < S) load_sb_raw<FMT, NTILE>(bufB, st, rx, s + NW, S, tile0, tstride);
+    gemv_superblock_raw<FMT, NTILE>(bufA, acc, lane, Mv);
+    s += NW;
+    if (s >= S) break;
+    if (s + NW < S) load_sb_raw<FMT, NTILE>(bufA, st, rx, s + NW, S, tile0, tstride);
+    gemv_superblock_raw<FMT, NTILE>(bufB, acc, lane, Mv);
+    s += NW;
+    if (s >= S) break;
+  }
+}
+
 // Sum the NW waves' accumulators in a fixed order; threads < NTILE*64 get tile t = idx >> 6,
 // lane l = idx & 63 (C layout: column l & 15, rows 4*(l >> 4) + i).
 template <int NTILE, int NW>

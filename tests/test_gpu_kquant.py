@@ -101,6 +101,7 @@ def test_every_gemv_variant(gpu, fmt):
         quant, meta = ops.gemm_kquant_shuffle_b(fmt, torch.from_numpy(raw).cuda(), n, k)
         ws = torch.empty(ops.gemm_kquant_a_ws_bytes(9, k), dtype=torch.uint8, device="cuda")
         c = torch.empty(9, n, device="cuda")
+        c2 = torch.empty(9, n, device="cuda")
         try:
             for v in range(7):
                 print(f"variant {v} fmt={fmt} N={n} K={k}", flush=True)
@@ -108,5 +109,10 @@ def test_every_gemv_variant(gpu, fmt):
                 c.zero_()
                 ops.gemm_kquant_a(fmt, x.cuda(), quant, meta, c, 9, n, k, ws)
                 assert Q.rel_l2(c.cpu().numpy(), want) < TOL, v
+                # the one-launch path (in-kernel conversion) and the prepared workspace path
+                # build the same operands: identical results
+                ops.gemm_kquant_prepare_a(x.cuda(), ws)
+                ops.gemm_kquant_a_prepared(fmt, quant, meta, c2, 9, n, k, ws)
+                assert torch.equal(c, c2), v
         finally:
             lib.snowverify_gemv_variant(0)
