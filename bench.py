@@ -168,10 +168,21 @@ def q80_bytes(n, k):
     return n * k // 32 * 34
 
 
-def step_bytes(cfg, slots):
+SEL_RANK = 256
+
+
+def use_selector(cfg):
+    """BASELINE config 4 runs the fused selector + acceptance; the others take the draft
+    proposal from outside the step."""
+    return cfg.moe and not cfg.tree_parents
+
+
+def step_bytes(cfg, slots, selector=False):
     """Algorithmic HBM bytes of one verify step: every weight byte the step must read once
     (the touched experts only), the KV cache of the context plus the block's new rows, the
-    LM head, and the logits/probabilities of the acceptance."""
+    LM head, the logits/probabilities of the acceptance, and (with the selector) the draft
+    logits plus the codebook rows the selector gathers (16 candidates and 16 previous
+    tokens per position)."""
     H, T, V = cfg.hidden, cfg.block, cfg.vocab
     wb = q4k_bytes if cfg.attn_fmt == 4 else q80_bytes
     attn_w = wb(cfg.qkv_n, H) + wb(H, cfg.heads * cfg.head_dim)
@@ -186,6 +197,9 @@ def step_bytes(cfg, slots):
             total += q4k_bytes(2 * cfg.ffn, H) + q4k_bytes(H, cfg.ffn)
     total += V * H * 2 + T * H * 2  # LM head (fp16), embedding rows
     total += 3 * T * V * 4          # logits write, probabilities read + write
+    if selector:
+        k = T - 1
+        total += k * V * 4 + k * (2 * 16 + 1) * SEL_RANK * 2
     return total
 
 
@@ -223,20 +237,39 @@ def bench_step(args, name):
     draft_logits = torch.randn(k, V, generator=g0) * 2
     drafts = torch.multinomial(draft_logits.softmax(-1), 1, generator=g0).view(1, k)
     uniform = torch.rand(1, k + 1, generator=g1)
-    acc.set_draft(draft_logits.cuda(), drafts.cuda(), uniform.cuda())
+    # config 4 is quoted with the DFlash 2 selector in the step: it walks the draft logits
+    # (codebook rank 256, seeded synthetic codebooks and selector projection) at T = 1.0,
+    # proposes the drafts and hands its 16-candidate lists to the rejection step
+    sel = None
+    if use_selector(cfg):
+        g2 = torch.Generator().manual_seed(2)
+        hp = (torch.randn(k, SEL_RANK, generator=g2) * .2).bfloat16()
+        pred = (torch.randn(V, SEL_RANK, generator=g2) * .2).bfloat16()
+        succ = (torch.randn(V, SEL_RANK, generator=g2) * .2).bfloat16()
+        sel_u = torch.rand(1, k, generator=g2)
+        sel = dict(hp=hp, pred=pred, succ=succ, anchor=ids[:1].clone(), temp=torch.ones(1),
+                   u=sel_u)
+        acc.set_selector(hp.cuda(), draft_logits.cuda(), pred.cuda(), succ.cuda(),
+                         sel["anchor"].cuda(), sel["temp"].cuda(), sel_u.cuda(), uniform.cuda())
+    else:
+        acc.set_draft(draft_logits.cuda(), drafts.cuda(), uniform.cuda())
 
     def step():
+        if sel is not None:
+            acc.propose(m.ids)
         m.forward()
         acc(m.logits)
 
     stream = torch.cuda.current_stream()
     # byte accounting: an eager pass that records each layer's plan size
     slots = torch.zeros(cfg.layers, dtype=torch.int32, device="cuda")
+    if sel is not None:
+        acc.propose(m.ids)
     m.forward(record_slots=slots if cfg.moe else None)
     acc(m.logits)
     torch.cuda.synchronize()
     slots_np = slots.cpu().numpy()
-    alg = step_bytes(cfg, slots_np)
+    alg = step_bytes(cfg, slots_np, selector=sel is not None)
     # the timed region: K graph replays of the whole step, inputs resident in HBM
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
@@ -284,6 +317,11 @@ def bench_step(args, name):
         per_launch("gate_up_swiglu", lambda i: Lops.gate_up_swiglu(
             c.ffn_fmt, Lw[i].gu[0], Lw[i].gu[1], m.ws_h2, m.act, T, c.ffn, H),
             q4k_bytes(2 * c.ffn, H))
+    if sel is not None:
+        us = timed_graph(lambda: acc.propose(), 5, stream) * 1e3
+        sb = k * V * 4 + k * (2 * 16 + 1) * SEL_RANK * 2
+        kern["draft_select (chunks + table + walk)"] = {
+            "us": round(us, 3), "alg_bytes": int(sb), "gbs": round(sb / (us * 1e-6) / 1e9, 1)}
     # dominant single kernel per step (launch time x launches per step)
     single = {kk: v for kk, v in kern.items() if "+" not in kk}
     dom = max(single, key=lambda kk: single[kk]["us"])
@@ -292,7 +330,7 @@ def bench_step(args, name):
 
     # reference CPU path (oracle, torch CPU) on a bounded sample: layer 0 x layers + head +
     # acceptance
-    cpu = cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform)
+    cpu = cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform, sel)
     cpu_value = emitted / (cpu["step_s"])
     return {
         "metric": METRIC, "value": round(emitted / (ms * 1e-3), 2), "unit": "tok/s",
@@ -304,7 +342,7 @@ def bench_step(args, name):
                    "block_rows": T, "context": cfg.context, "vocab": V,
                    "experts": cfg.experts, "topk": cfg.topk,
                    "attn_fmt": "q4_k" if cfg.attn_fmt == 4 else "q8_0",
-                   "tree": bool(cfg.tree_parents)},
+                   "tree": bool(cfg.tree_parents), "selector": sel is not None},
         "verify_step_us": round(ms * 1e3, 1),
         "accepted_per_step": emitted, "accepted_drafts": emitted - 1,
         "emitted_tokens": out_tokens,
@@ -349,10 +387,11 @@ def read_traffic(kernel):
     return None
 
 
-def cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform):
+def cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform, sel=None):
     """The oracle's CPU restatement of the verify step, timed on this host: layer 0 (GGUF
     dequantization of the weights it touches + fp64/fp32 compute) extrapolated to every layer,
-    the final norm + LM head, and the acceptance (probabilities + rejection sampling)."""
+    the final norm + LM head, and the acceptance (the selector walk when the step has one,
+    probabilities + rejection sampling)."""
     import numpy as np
     import torch
     from oracle import accept as A
@@ -381,11 +420,18 @@ def cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform):
         logits = torch.randn(T, cfg.vocab)
     chain = logits[rows].numpy().astype(np.float32)
     p = A.softmax(chain)
-    q = A.softmax(draft_logits.numpy())
     ident = np.tile(np.arange(cfg.vocab), (len(rows), 1))
     k = len(rows) - 1
-    A.reject(p, ident, drafts.numpy(), ident[:k][None], q[None], np.zeros(1, np.int32),
-             np.ones(1, np.int32), uniform.numpy())
+    if sel is not None:
+        path, cand, q = A.select(sel["hp"], draft_logits.numpy(), sel["pred"], sel["succ"],
+                                 sel["anchor"].numpy(), sel["temp"].numpy(), sel["u"].numpy(),
+                                 np.zeros(1, np.int32), 1)
+        A.reject(p, ident, path, cand, q, np.zeros(1, np.int32), np.ones(1, np.int32),
+                 uniform.numpy())
+    else:
+        q = A.softmax(draft_logits.numpy())
+        A.reject(p, ident, drafts.numpy(), ident[:k][None], q[None], np.zeros(1, np.int32),
+                 np.ones(1, np.int32), uniform.numpy())
     tail_s = time.perf_counter() - t1
     step_s = layer_s * cfg.layers + tail_s
     return {"step_s": step_s, "cores": cores,

@@ -87,6 +87,34 @@ int snowllm_draft_reject(const float* p, const int64_t* ids, const int64_t* draf
                          int64_t* accepted, int64_t b, int64_t width, int64_t p_width,
                          int64_t q_width, void* stream);
 
+/* ---- DFlash 2 candidate selector (snowllm/ops/dflash.py:164-198; semantics
+ * tests/test_dflash_sampling.py:44-75, tests/test_dflash_selector_topk.py:42-61) ------------
+ * Per position: the 16 largest logits (stable descending, NaN as -inf), scores = values +
+ * the codebook correction pred[prev] . hp[row] . succ[cand], then the first argmax (greedy)
+ * or a pick from softmax(scores / T) with uniform[b, j]; prev = the pick. hp bf16
+ * [b*ell, 256], logits f32 [b*ell, v] (16 <= v <= 262144), pred/succ bf16 [v, 256], anchor
+ * i64 [b], path i64 [b, ell] (ell <= 32). */
+/* Scratch bytes for n = b * ell rows (snowllm/_capi.py:285). */
+int64_t snowllm_draft_select_scratch_bytes(int64_t n);
+/* Greedy walk, path only (snowllm/_capi.py:286-287). */
+int snowllm_draft_select(const void* hp, const float* logits, const void* pred, const void* succ,
+                         const int64_t* anchor, int64_t* path, void* scratch, int64_t b,
+                         int64_t ell, int64_t v, void* stream);
+/* Per-row greedy (temperature <= 0) or sampling walk; writes candidate_ids i64 and
+ * probabilities f32 [S, ell, 16] at row slots[b] (snowllm/_capi.py:288). top_k must be 16. */
+int snowllm_draft_sample(const void* hp, const float* logits, const void* pred, const void* succ,
+                         const int64_t* anchor, const float* temperature, const float* uniform,
+                         const int32_t* slots, int64_t* path, int64_t* candidate_ids,
+                         float* probabilities, void* scratch, int64_t b, int64_t ell, int64_t v,
+                         int64_t top_k, void* stream);
+/* Extension, no counterpart in the reference: the selector at codebook rank `rank` (64, 128,
+ * 256 or 512); temperature == NULL is snowllm_draft_select. */
+int snowverify_draft_select(const void* hp, const float* logits, const void* pred,
+                            const void* succ, const int64_t* anchor, const float* temperature,
+                            const float* uniform, const int32_t* slots, int64_t* path,
+                            int64_t* candidate_ids, float* probabilities, void* scratch,
+                            int64_t b, int64_t ell, int64_t v, int64_t rank, void* stream);
+
 /* ---- GGUF k-quant GEMV ----------------------------------------------------------------- */
 /* Format ids as in the reference (snowllm/ops/moe.py:189-190): 4 = Q4_K, 8 = Q8_0. */
 

@@ -327,3 +327,106 @@ void oc_reject(const float* p, const int64_t* ids, const int64_t* drafts, const 
     free(res);
   }
 }
+
+/* ---- DFlash 2 selector: snowllm/ops/dflash.py:164-198; tests/test_dflash_sampling.py:44-75,
+ * tests/test_dflash_selector_topk.py:42-61 -----------------------------------------------------
+ * Per batch row b and position j (row = b * ell + j, prev = the previous pick, anchor[b] at
+ * j = 0): the 16 largest logits in stable descending order (NaN as -inf, -0 == +0), scores =
+ * value + correction, then the first argmax (greedy: no temperature or T <= 0) or a pick from
+ * softmax(scores / T). The correction is the device's canonical sum: the products
+ * pred * hp * succ are exact in binary32 (sampling rows round pred * hp to bf16 first, as
+ * torch's bf16 product does); lane l of 64 sums r = l E .. l E + E - 1 (E = R / 64) in order,
+ * and the 64 lane sums meet in a balanced binary tree in lane order; sampling rows round the
+ * sum to bf16. The softmax and the pick use the canonical exp / fixed-point arithmetic. */
+#define SEL_K 16
+
+static float bf16f(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+static float round_bf16(float f) {
+  if (f != f) return f;
+  uint32_t u = f2u(f);
+  u += 0x7fffu + ((u >> 16) & 1u);  /* round to nearest even on the dropped 16 bits */
+  return u2f(u & 0xffff0000u);
+}
+
+float oc_round_bf16(float f) { return round_bf16(f); }
+
+float oc_select_dot(const uint16_t* pred_row, const uint16_t* hp_row, const uint16_t* succ_row,
+                    int64_t R, int sampling) {
+  const int64_t E = R / 64;
+  float lanes[64];
+  for (int l = 0; l < 64; ++l) {
+    float part = 0.0f;
+    for (int64_t i = 0; i < E; ++i) {
+      const int64_t r = l * E + i;
+      float prod = bf16f(pred_row[r]) * bf16f(hp_row[r]);
+      if (sampling) prod = round_bf16(prod);
+      part = part + prod * bf16f(succ_row[r]);
+    }
+    lanes[l] = part;
+  }
+  for (int step = 1; step < 64; step *= 2)
+    for (int l = 0; l < 64; l += 2 * step) lanes[l] = lanes[l] + lanes[l + step];
+  return sampling ? round_bf16(lanes[0]) : lanes[0];
+}
+
+void oc_select(const uint16_t* hp, const float* logits, const uint16_t* pred,
+               const uint16_t* succ, const int64_t* anchor, const float* temperature,
+               const float* uniform, const int32_t* slots, int64_t* path, int64_t* cand,
+               float* q, int64_t b, int64_t ell, int64_t V, int64_t R) {
+  KeyIdx* buf = (KeyIdx*)malloc(sizeof(KeyIdx) * (size_t)V);
+  for (int64_t bi = 0; bi < b; ++bi) {
+    int64_t prev = anchor[bi];
+    const float T = temperature ? temperature[bi] : 0.0f;
+    const int sampling = T > 0.0f;
+    for (int64_t j = 0; j < ell; ++j) {
+      const int64_t row = bi * ell + j;
+      const float* x = logits + row * V;
+      for (int64_t i = 0; i < V; ++i) { buf[i].key = oc_ord_key(x[i]); buf[i].idx = (uint32_t)i; }
+      qsort(buf, (size_t)V, sizeof(KeyIdx), cmp_desc);
+      int64_t id[SEL_K];
+      float score[SEL_K], qv[SEL_K];
+      for (int c = 0; c < SEL_K; ++c) {
+        id[c] = buf[c].idx;
+        const float corr = oc_select_dot(pred + prev * R, hp + row * R, succ + id[c] * R, R,
+                                         sampling);
+        score[c] = ord_key_to_float(buf[c].key) + corr;
+      }
+      int pick = 0;
+      if (!sampling) {
+        uint32_t best = oc_ord_key(score[0]);
+        for (int c = 1; c < SEL_K; ++c) {
+          const uint32_t k = oc_ord_key(score[c]);
+          if (k > best) { best = k; pick = c; }
+        }
+        for (int c = 0; c < SEL_K; ++c) qv[c] = c == pick ? 1.0f : 0.0f;
+      } else {
+        float xs[SEL_K], e[SEL_K];
+        uint32_t mk = 0;
+        for (int c = 0; c < SEL_K; ++c) {
+          xs[c] = score[c] / T;
+          const uint32_t k = oc_ord_key(xs[c]);
+          if (k > mk) mk = k;
+        }
+        const float M = ord_key_to_float(mk);
+        uint64_t Z = 0;
+        for (int c = 0; c < SEL_K; ++c) { e[c] = oc_exp(xs[c] - M); Z += oc_fix(e[c]); }
+        const float Zf = oc_unfix(Z);
+        for (int c = 0; c < SEL_K; ++c) qv[c] = Zf > 0.0f ? oc_div(e[c], Zf) : 0.0f;
+        const float u = uniform[row];
+        const uint64_t target = u > 0.0f ? (uint64_t)floorf(ldexpf(u, FIX_BITS)) : 0;
+        uint64_t pre = 0;
+        int n = 0;
+        for (int c = 0; c < SEL_K; ++c) { pre += oc_fix(qv[c]); n += pre <= target; }
+        pick = n < SEL_K - 1 ? n : SEL_K - 1;
+      }
+      path[row] = id[pick];
+      if (cand) {
+        const int64_t base = ((int64_t)slots[bi] * ell + j) * SEL_K;
+        for (int c = 0; c < SEL_K; ++c) { cand[base + c] = id[c]; q[base + c] = qv[c]; }
+      }
+      prev = id[pick];
+    }
+  }
+  free(buf);
+}

@@ -38,6 +38,9 @@ for name, res, args in [
     ("oc_topk_topp", ctypes.c_int, [_P, _P, _P, _I, _I, _I, _P, _P]),
     ("oc_pick_rows", None, [_P, _P, _I, _I, _P, _P]),
     ("oc_reject", None, [_P] * 10 + [_I] * 4),
+    ("oc_round_bf16", ctypes.c_float, [ctypes.c_float]),
+    ("oc_select_dot", ctypes.c_float, [_P, _P, _P, _I, ctypes.c_int]),
+    ("oc_select", None, [_P] * 11 + [_I] * 4),
 ]:
     fn = getattr(_lib, name)
     fn.restype = res
@@ -138,3 +141,47 @@ def reject(p, ids, drafts, cand, q, slots, valid, uniform):
     _lib.oc_reject(_ptr(p), _ptr(ids), _ptr(drafts), _ptr(cand), _ptr(q), _ptr(slots),
                    _ptr(valid), _ptr(uniform), _ptr(out), _ptr(acc), b, width, p_width, q_width)
     return out, acc
+
+
+def _bf16_bits(a) -> np.ndarray:
+    """bf16 data as uint16 words (accepts a torch bf16 tensor or uint16 words)."""
+    if hasattr(a, "view") and str(getattr(a, "dtype", "")) == "torch.bfloat16":
+        import torch
+        return a.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    return _c(a, np.uint16)
+
+
+def round_bf16(x: float) -> float:
+    return float(_lib.oc_round_bf16(ctypes.c_float(x)))
+
+
+def select_dot(pred_row, hp_row, succ_row, sampling: bool) -> float:
+    p, h, s = _bf16_bits(pred_row), _bf16_bits(hp_row), _bf16_bits(succ_row)
+    return float(_lib.oc_select_dot(_ptr(p), _ptr(h), _ptr(s), p.shape[-1], int(sampling)))
+
+
+def select(hp, logits, pred, succ, anchor, temperature=None, uniform=None, slots=None,
+           n_slots=None):
+    """The DFlash 2 candidate walk (accept.c: oc_select). Returns path [b, ell] and, when a
+    temperature is given, candidate ids and probabilities [n_slots, ell, 16] (zero-filled
+    outside the written slots)."""
+    h = _bf16_bits(hp)
+    x = _c(logits, np.float32)
+    pr, sc = _bf16_bits(pred), _bf16_bits(succ)
+    a = _c(anchor, np.int64)
+    b = a.shape[0]
+    n, V = x.shape
+    ell = n // b
+    R = h.shape[-1]
+    path = np.empty((b, ell), dtype=np.int64)
+    t = u = s = cand = q = None
+    if temperature is not None:
+        t = _c(temperature, np.float32)
+        u = _c(uniform, np.float32)
+        s = _c(slots, np.int32)
+        S = int(n_slots if n_slots is not None else s.max() + 1)
+        cand = np.zeros((S, ell, 16), dtype=np.int64)
+        q = np.zeros((S, ell, 16), dtype=np.float32)
+    _lib.oc_select(_ptr(h), _ptr(x), _ptr(pr), _ptr(sc), _ptr(a), _ptr(t), _ptr(u), _ptr(s),
+                   _ptr(path), _ptr(cand), _ptr(q), b, ell, V, R)
+    return path, cand, q

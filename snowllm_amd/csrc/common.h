@@ -133,6 +133,25 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return (a + b) + (c + d);
 }
 
+__device__ __forceinline__ uint32_t wave_sum_u32_dpp(uint32_t v) {
+  v += dpp_u32<DPP_QUAD_XOR1>(v);
+  v += dpp_u32<DPP_QUAD_XOR2>(v);
+  v += dpp_u32<DPP_HALF_MIRROR>(v);
+  v += dpp_u32<DPP_MIRROR>(v);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 0) + (uint32_t)__builtin_amdgcn_readlane((int)v, 16) +
+         (uint32_t)__builtin_amdgcn_readlane((int)v, 32) + (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+}
+
+// Inclusive prefix sum within each 16-lane row (row_shr by 1, 2, 4, 8; lanes shifted in
+// from outside the row read 0).
+__device__ __forceinline__ uint32_t row_scan_u32_dpp(uint32_t v) {
+  v += dpp_u32<0x111>(v);
+  v += dpp_u32<0x112>(v);
+  v += dpp_u32<0x114>(v);
+  v += dpp_u32<0x118>(v);
+  return v;
+}
+
 // Block-wide reductions for blockDim.x == NT (a multiple of 64). `red` must hold NT/64 slots.
 template <int NT>
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* red) {

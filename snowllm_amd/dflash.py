@@ -1,8 +1,72 @@
-"""DFlash acceptance: rejection sampling of a draft prefix (snowllm/ops/dflash.py:201-219)."""
+"""DFlash 2 selector and acceptance (snowllm/ops/dflash.py:159-219): the candidate walk that
+proposes a draft path, and rejection sampling of a draft prefix."""
 import torch
 
 from ._capi import check, lib
 from ._common import _chk, _p, _stream
+from .errors import SnowLLMError
+
+# The DFlash 2 draft geometry's selector (tests/test_dflash_sampling.py:24): codebook rank and
+# candidates per position. Ranks 64, 128 and 512 use the extension entry.
+SELECTOR_RANK = 256
+SELECTOR_TOP_K = 16
+
+
+def select_scratch_bytes(n: int) -> int:
+    """Scratch of select_path for n = b * ell logit rows (snowllm/ops/dflash.py:159-161)."""
+    return lib.snowllm_draft_select_scratch_bytes(int(n))
+
+
+def select_path(hp: torch.Tensor, logits: torch.Tensor, pred_cb: torch.Tensor,
+                succ_cb: torch.Tensor, anchor: torch.Tensor, path: torch.Tensor,
+                scratch: torch.Tensor, *, temperature=None, uniform=None, slots=None,
+                candidate_ids=None, probabilities=None) -> None:
+    """The candidate walk that replaces argmax on a DFlash 2 draft's logits
+    (snowllm/ops/dflash.py:164-198): without temperature a greedy walk writing path only;
+    with it, per-row greedy or sampling walks that also store the 16 candidates and their
+    probabilities at each request's stable slot."""
+    b, ell = path.shape
+    n, v = logits.shape
+    if n != b * ell:
+        raise SnowLLMError(f"the selector was given {n} logit rows for {b}x{ell} positions")
+    rank = hp.shape[1] if hp.dim() == 2 else -1
+    _chk(hp, "hp", torch.bfloat16, n, rank)
+    _chk(logits, "logits", torch.float32, n, v)
+    _chk(pred_cb, "pred_cb", torch.bfloat16, v, rank)
+    _chk(succ_cb, "succ_cb", torch.bfloat16, v, rank)
+    _chk(anchor, "anchor", torch.int64, b)
+    _chk(path, "path", torch.int64, b, ell)
+    _chk(scratch, "scratch", torch.uint8)
+    if scratch.numel() < select_scratch_bytes(n):
+        raise SnowLLMError("selector scratch is too small")
+    if temperature is None:
+        if rank == SELECTOR_RANK:
+            check(lib.snowllm_draft_select(_p(hp), _p(logits), _p(pred_cb), _p(succ_cb),
+                                           _p(anchor), _p(path), _p(scratch), b, ell, v,
+                                           _stream()), "draft_select")
+        else:
+            check(lib.snowverify_draft_select(_p(hp), _p(logits), _p(pred_cb), _p(succ_cb),
+                                              _p(anchor), None, None, None, _p(path), None, None,
+                                              _p(scratch), b, ell, v, rank, _stream()),
+                  "draft_select")
+        return
+    _chk(temperature, "temperature", torch.float32, b)
+    _chk(uniform, "uniform", torch.float32, b, ell)
+    _chk(slots, "slots", torch.int32, b)
+    _chk(candidate_ids, "candidate_ids", torch.int64)
+    _chk(probabilities, "probabilities", torch.float32, *candidate_ids.shape)
+    if tuple(candidate_ids.shape[1:]) != (ell, SELECTOR_TOP_K):
+        raise SnowLLMError("selector probability pool has the wrong block or candidate count")
+    if rank == SELECTOR_RANK:
+        check(lib.snowllm_draft_sample(
+            _p(hp), _p(logits), _p(pred_cb), _p(succ_cb), _p(anchor), _p(temperature),
+            _p(uniform), _p(slots), _p(path), _p(candidate_ids), _p(probabilities), _p(scratch),
+            b, ell, v, SELECTOR_TOP_K, _stream()), "draft_sample")
+    else:
+        check(lib.snowverify_draft_select(
+            _p(hp), _p(logits), _p(pred_cb), _p(succ_cb), _p(anchor), _p(temperature),
+            _p(uniform), _p(slots), _p(path), _p(candidate_ids), _p(probabilities), _p(scratch),
+            b, ell, v, rank, _stream()), "draft_sample")
 
 
 def reject(probabilities, indices, drafts, candidate_ids, q, slots, valid, uniform, out, accepted):

@@ -379,6 +379,36 @@ class Acceptance:
         self.drafts.copy_(drafts.view(1, k))
         self.uniform.copy_(uniform.view(1, self.T))
 
+    def set_selector(self, hp, draft_logits, pred, succ, anchor, temperature, select_uniform,
+                     uniform):
+        """Draft side inside the step: the DFlash 2 selector walks the draft logits and
+        proposes the drafts with their 16-candidate probabilities (snowllm/engine/
+        dflash_sampling.py:44-48); the rejection step then reads those candidate lists by
+        request slot. hp [k, rank], draft_logits [k, V], codebooks [V, rank], anchor [1],
+        temperature [1], select_uniform [1, k], uniform [1, k + 1]."""
+        k = self.T - 1
+        dev = "cuda"
+        self.sel = dict(hp=hp, logits=draft_logits, pred=pred, succ=succ,
+                        anchor=anchor.view(1), temperature=temperature.view(1),
+                        uniform=select_uniform.view(1, k))
+        self.q = torch.empty(1, k, 16, device=dev)
+        self.qid = torch.empty(1, k, 16, dtype=torch.int64, device=dev)
+        self.sel_scratch = torch.empty(ops.dflash.select_scratch_bytes(k), dtype=torch.uint8,
+                                       device=dev)
+        self.uniform.copy_(uniform.view(1, self.T))
+
+    def propose(self, block_ids=None):
+        """Run the selector: drafts, candidate ids and q for this step; block_ids [k + 1], if
+        given, receives anchor + drafts (the verify block's input ids)."""
+        s = self.sel
+        ops.dflash.select_path(s["hp"], s["logits"], s["pred"], s["succ"], s["anchor"],
+                               self.drafts, self.sel_scratch, temperature=s["temperature"],
+                               uniform=s["uniform"], slots=self.slot, candidate_ids=self.qid,
+                               probabilities=self.q)
+        if block_ids is not None:
+            block_ids[1:].copy_(self.drafts.view(-1))
+        return self.drafts
+
     def __call__(self, logits):
         src = logits
         if self.chain_logits is not None:

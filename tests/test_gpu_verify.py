@@ -108,3 +108,59 @@ def test_step_graph_replay_matches_eager(gpu):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(m.logits, eager)
+
+
+def test_selector_driven_step(gpu):
+    """The config-4 step shape at small size: the DFlash 2 selector proposes the drafts inside
+    the step (path and candidate probabilities bit-exact against the oracle walk), the block
+    runs on them, and the rejection step reads the selector's 16-candidate lists (bit-exact
+    against the oracle); the captured step replays to the eager result."""
+    from snowllm_amd.verify import VerifyModel, Acceptance
+    cfg = tiny("moe")
+    m = VerifyModel(cfg, seed=6)
+    T, k, V = cfg.block, cfg.block - 1, cfg.vocab
+    m.set_block(torch.arange(T) * 5)
+    g = torch.Generator().manual_seed(11)
+    hp = (torch.randn(k, 256, generator=g) * .3).bfloat16()
+    draft_logits = torch.randn(k, V, generator=g) * 2
+    pred = (torch.randn(V, 256, generator=g) * .3).bfloat16()
+    succ = (torch.randn(V, 256, generator=g) * .3).bfloat16()
+    anchor = torch.tensor([123])
+    temp = torch.ones(1)
+    su = torch.rand(1, k, generator=g)
+    u = torch.rand(1, T, generator=g)
+    acc = Acceptance(V, list(range(T)))
+    acc.set_selector(hp.cuda(), draft_logits.cuda(), pred.cuda(), succ.cuda(), anchor.cuda(),
+                     temp.cuda(), su.cuda(), u.cuda())
+    m.ids[0] = int(anchor)
+
+    def step():
+        acc.propose(m.ids)
+        m.forward()
+        return acc(m.logits)
+
+    out, accepted = step()
+    torch.cuda.synchronize()
+    want_path, want_cand, want_q = A.select(hp, draft_logits.numpy(), pred, succ, anchor.numpy(),
+                                            temp.numpy(), su.numpy(), np.zeros(1, np.int32), 1)
+    assert np.array_equal(acc.drafts.cpu().numpy(), want_path)
+    assert np.array_equal(m.ids[1:].cpu().numpy(), want_path[0])
+    assert np.array_equal(acc.qid.cpu().numpy(), want_cand)
+    assert np.array_equal(acc.q.cpu().numpy(), want_q)
+    logits = m.logits.cpu().numpy()
+    p = A.softmax(logits)
+    ident = np.tile(np.arange(V), (T, 1))
+    want_out, want_acc = A.reject(p, ident, want_path, want_cand, want_q, np.zeros(1, np.int32),
+                                  np.ones(1, np.int32), u.numpy())
+    assert np.array_equal(out.cpu().numpy(), want_out)
+    assert np.array_equal(accepted.cpu().numpy(), want_acc)
+    eager_out, eager_logits = out.clone(), m.logits.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(3):
+        m.logits.zero_()
+        acc.out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(m.logits, eager_logits) and torch.equal(acc.out, eager_out)
