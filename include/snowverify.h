@@ -257,6 +257,13 @@ int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, int64_t
  * y_out if given). H <= 8192; res_out and y_out must not alias x or res_in. */
 int snowverify_norm_prep(const void* x, const void* res_in, void* res_out, const void* gamma,
                          void* y_out, void* ws, int64_t M, int64_t H, float eps, void* stream);
+/* snowverify_norm_prep on the MoE layer's output, combined in the same launch: x = bf16(sum_k
+ * pairs[r*topk + k] + shared_out[r]) (snowverify_moe_combine's order), written to x_out if
+ * given. pairs [M*topk, H] f32, shared_out [M, H] f32 or NULL. */
+int snowverify_norm_prep_moe(const float* pairs, const float* shared_out, int64_t topk,
+                             void* x_out, const void* res_in, void* res_out, const void* gamma,
+                             void* y_out, void* ws, int64_t M, int64_t H, float eps,
+                             void* stream);
 /* 16-bit weight GEMV: repack size, repack (wt 1 = fp16, 2 = bf16), and C = A W^T (fp16 weights
  * take the operand workspace, bf16 weights bf16 activations). M <= 16. */
 int64_t snowverify_dense_bytes(int64_t N, int64_t K);

@@ -114,6 +114,7 @@ _SIGS = [
     ("snowverify_moe_route", c_int, [P, c_int64, c_int64, c_int64, c_int64, P, P, P, S]),
     # feed-forward
     ("snowverify_norm_prep", c_int, [P, P, P, P, P, P, c_int64, c_int64, c_float, S]),
+    ("snowverify_norm_prep_moe", c_int, [P, P, c_int64] + [P] * 6 + [c_int64, c_int64, c_float, S]),
     ("snowverify_dense_bytes", c_int64, [c_int64, c_int64]),
     ("snowverify_dense_shuffle", c_int, [P, P, c_int64, c_int64, c_int, S]),
     ("snowverify_dense_gemv", c_int, [c_int, P, P, P, c_int64, c_int64, c_int64, c_int, S]),

@@ -41,8 +41,37 @@ __device__ __forceinline__ u32x4 add_bf16_words(const u32x4& xv, const u32x4& rv
   return u32x4{o[0], o[1], o[2], o[3]};
 }
 
+// The MoE layer's output as the norm's input: x[r] = bf16(sum_k pairs[r * topk + k] +
+// shared[r]) in that order (the combine of the experts' pre-weighted rows), optionally
+// written to x_out.
+struct MoeSource {
+  const float* pairs;   // [M * topk, H] f32, or null: x is read as bf16
+  const float* shared;  // [M, H] f32 or null
+  uint16_t* x_out;      // [M, H] bf16 or null
+  int topk;
+};
+
+__device__ __forceinline__ u32x4 moe_words(const MoeSource& ms, int64_t row, int64_t H,
+                                           int64_t col) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < ms.topk; ++k) {
+    const float4* src = (const float4*)(ms.pairs + (row * ms.topk + k) * H + col);
+    const float4 a = src[0], b = src[1];
+    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+  }
+  if (ms.shared) {
+    const float4* src = (const float4*)(ms.shared + row * H + col);
+    const float4 a = src[0], b = src[1];
+    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+  }
+  return u32x4{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+               pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7])};
+}
+
 __global__ void __launch_bounds__(NORM_MAX_THREADS) norm_prep_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
+    const uint16_t* __restrict__ x, MoeSource ms, const uint16_t* __restrict__ residual,
     uint16_t* __restrict__ res_out, const uint16_t* __restrict__ gamma,
     uint16_t* __restrict__ y_out, void* __restrict__ ws, size_t tile_bytes, int64_t M, int64_t H,
     float eps) {
@@ -57,7 +86,12 @@ __global__ void __launch_bounds__(NORM_MAX_THREADS) norm_prep_kernel(
   u32x4 v = {0u, 0u, 0u, 0u}, gv = {0u, 0u, 0u, 0u};
   if (act) gv = *(const u32x4*)(gamma + (int64_t)t * 8);
   if (live) {
-    v = *(const u32x4*)(x + off);
+    if (ms.pairs) {
+      v = moe_words(ms, row, H, (int64_t)t * 8);
+      if (ms.x_out) *(u32x4*)(ms.x_out + off) = v;
+    } else {
+      v = *(const u32x4*)(x + off);
+    }
     if (residual) v = add_bf16_words(v, *(const u32x4*)(residual + off));
   }
   const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
@@ -621,6 +655,19 @@ __global__ void moe_combine_kernel(const float* __restrict__ pairs,
   out[i] = f32_to_bf16(acc);
 }
 
+int launch_norm_prep(const void* x, MoeSource ms, const void* res_in, void* res_out,
+                     const void* gamma, void* y_out, void* ws, int64_t M, int64_t H, float eps,
+                     hipStream_t s) {
+  const int64_t S = H / 256, mt = (M + 15) / 16;
+  const int threads = (int)((H / 8 + 63) / 64 * 64);
+  hipLaunchKernelGGL(norm_prep_kernel, dim3((unsigned)(mt * 16)), dim3(threads), 0, s,
+                     (const uint16_t*)x, ms, (const uint16_t*)res_in, (uint16_t*)res_out,
+                     (const uint16_t*)gamma, (uint16_t*)y_out, ws, xprep_tile_bytes(S), M, H,
+                     eps);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
 template <int WT, int NTILE, int NW>
 int launch_dense(const void* w, const void* act, void* c, int M, int N, int S, int c_bf16,
                  hipStream_t s) {
@@ -649,14 +696,24 @@ SV_API int snowverify_norm_prep(const void* x, const void* res_in, void* res_out
   if (res_out && (res_out == x || res_out == res_in)) return SV_EINVAL;
   if (y_out && (y_out == x || y_out == res_in)) return SV_EINVAL;
   if (H > 8 * NORM_MAX_THREADS) return SV_EINVAL;
-  const int64_t S = H / 256, mt = (M + 15) / 16;
-  const int threads = (int)((H / 8 + 63) / 64 * 64);
-  hipLaunchKernelGGL(norm_prep_kernel, dim3((unsigned)(mt * 16)), dim3(threads), 0, Sx(stream),
-                     (const uint16_t*)x, (const uint16_t*)res_in, (uint16_t*)res_out,
-                     (const uint16_t*)gamma,
-                     (uint16_t*)y_out, ws, xprep_tile_bytes(S), M, H, eps);
-  SV_CHECK_LAUNCH();
-  return SV_OK;
+  return launch_norm_prep(x, MoeSource{nullptr, nullptr, nullptr, 0}, res_in, res_out, gamma,
+                          y_out, ws, M, H, eps, Sx(stream));
+}
+
+// snowverify_norm_prep on the MoE layer's output without materialising it first: x =
+// bf16(sum_k pairs[r * topk + k] + shared_out[r]) (as snowverify_moe_combine), written to
+// x_out if given. pairs [M*topk, H] f32, shared_out [M, H] f32 or null.
+SV_API int snowverify_norm_prep_moe(const float* pairs, const float* shared_out, int64_t topk,
+                                    void* x_out, const void* res_in, void* res_out,
+                                    const void* gamma, void* y_out, void* ws, int64_t M,
+                                    int64_t H, float eps, void* stream) {
+  if (!pairs || topk <= 0 || M <= 0 || H <= 0 || H % 256 || H > 8 * NORM_MAX_THREADS)
+    return SV_EINVAL;
+  if (res_out && res_out == res_in) return SV_EINVAL;
+  if (y_out && y_out == res_in) return SV_EINVAL;
+  if (x_out && (x_out == res_in || x_out == res_out || x_out == y_out)) return SV_EINVAL;
+  return launch_norm_prep(nullptr, MoeSource{pairs, shared_out, (uint16_t*)x_out, (int)topk},
+                          res_in, res_out, gamma, y_out, ws, M, H, eps, Sx(stream));
 }
 
 // Bytes of a repacked 16-bit weight [N, K] (N padded to a multiple of 16).

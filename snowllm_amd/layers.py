@@ -45,6 +45,23 @@ def norm_prep(x, gamma, ws, eps, *, res_in=None, res_out=None, y_out=None):
                                    M, H, eps, _stream()), "norm_prep")
 
 
+def norm_prep_moe(pairs, shared_out, topk, gamma, ws, eps, *, x_out=None, res_in=None,
+                  res_out=None, y_out=None):
+    """norm_prep on the MoE layer's output, combined in the same launch: x = bf16(sum_k
+    pairs[r * topk + k] + shared_out[r]) (-> x_out if given), then as norm_prep."""
+    M, H = pairs.shape[0] // topk, pairs.shape[1]
+    _chk(pairs, "pairs", torch.float32, M * topk, H)
+    if shared_out is not None:
+        _chk(shared_out, "shared_out", torch.float32, M, H)
+    _chk(gamma, "gamma", torch.bfloat16, H)
+    for t, n in ((x_out, "x_out"), (res_in, "res_in"), (res_out, "res_out"), (y_out, "y_out")):
+        if t is not None:
+            _chk(t, n, torch.bfloat16, M, H)
+    check(lib.snowverify_norm_prep_moe(_p(pairs), _p(shared_out), topk, _p(x_out), _p(res_in),
+                                       _p(res_out), _p(gamma), _p(y_out), _p(ws), M, H, eps,
+                                       _stream()), "norm_prep_moe")
+
+
 def rope_cos_sin(positions, inv_freq, cos, sin):
     M, half = cos.shape
     _chk(positions, "positions", torch.int64, M)

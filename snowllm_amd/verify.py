@@ -294,10 +294,21 @@ class VerifyModel:
         Lops.rope_cos_sin(self.positions, self.inv_freq, self.cos, self.sin)
         res_in, res_out = None, self.res[0]
         n_layers = c.layers if upto_layer is None else upto_layer
+        moe_out = False  # the previous layer's MoE output is still in (pairs, shared_out)
+
+        def norm(gamma, ws):
+            # residual update + norm fused with the GEMV operand prep; after a MoE layer the
+            # experts' combine is fused in too (self.x still receives the layer output)
+            if moe_out:
+                Lops.norm_prep_moe(self.pairs, self.shared_out, c.topk, gamma, ws, c.eps,
+                                   x_out=self.x, res_in=res_in, res_out=res_out)
+            else:
+                Lops.norm_prep(self.x, gamma, ws, c.eps, res_in=res_in, res_out=res_out)
+
         for i in range(n_layers):
             lw = self.layers[i]
-            # attention block: residual update + input norm fused with the QKV operand prep
-            Lops.norm_prep(self.x, lw.in_norm, self.ws_h, c.eps, res_in=res_in, res_out=res_out)
+            # attention block
+            norm(lw.in_norm, self.ws_h)
             ops.gemm_kquant_a_prepared(c.attn_fmt, lw.qkv[0], lw.qkv[1], self.proj, T, c.qkv_n, H,
                                        self.ws_h)
             Lops.qk_norm_rope_cache(self.proj, lw.q_norm, lw.k_norm, self.cos, self.sin, self.q,
@@ -318,10 +329,13 @@ class VerifyModel:
                                     self.route_ids, self.shared_w, self.plan)
                 if record_slots is not None:
                     record_slots[i:i + 1].copy_(self.plan[:4].view(torch.int32))
-                Lops.moe_experts(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, self.plan,
-                                 self.ws_h2, self.route_w, self.shared_w, self.moe_act,
-                                 self.pairs, self.shared_out, self.x, T, c.topk, c.experts, H,
-                                 c.expert_ffn)
+                ns = T * c.topk + 1
+                Lops.moe_gate_up(c.ffn_fmt, lw.gu, lw.sh_gu, self.plan, self.ws_h2, self.moe_act,
+                                 T, ns, c.experts, H, c.expert_ffn)
+                Lops.moe_down(c.ffn_fmt, lw.dn, lw.sh_dn, self.plan, self.moe_act, self.route_w,
+                              self.shared_w, self.pairs, self.shared_out, ns, c.experts, H,
+                              c.expert_ffn)
+                moe_out = True
             else:
                 Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,
                                res_out=res_out)
@@ -332,7 +346,7 @@ class VerifyModel:
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
         self.layer_residual = res_in  # residual stream entering the next layer (with self.x)
         # final norm + LM head (fp16 weights, f32 logits)
-        Lops.norm_prep(self.x, self.final_norm, self.ws_f, c.eps, res_in=res_in, res_out=res_out)
+        norm(self.final_norm, self.ws_f)
         self.final_residual = res_out
         Lops.dense_gemv(Lops.WT_F16, self.lm_head, self.ws_f, self.logits, T, c.vocab, H)
         return self.logits

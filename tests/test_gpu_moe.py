@@ -117,3 +117,33 @@ def test_experts_match_dequantized_reference(gpu, M):
     err = ((out.cpu().double() - want).norm() / want.norm()).item()
     print(f"  experts rel L2 {err:.2e} ({len(cache)} experts touched)", flush=True)
     assert err < 5e-3
+
+
+@pytest.mark.parametrize("M,shared", [(9, True), (16, False), (3, True)])
+def test_norm_prep_moe_equals_combine_then_norm(gpu, M, shared):
+    """The norm fused with the experts' combine gives the same bits as combine + norm."""
+    from snowllm_amd import layers as L
+    from snowllm_amd import ops
+    print(f"norm_prep_moe M={M} shared={shared}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(40 + M)
+    pairs = torch.randn(M * K, H, device="cuda", generator=g) * .1
+    sh = torch.randn(M, H, device="cuda", generator=g) * .1 if shared else None
+    res_in = torch.randn(M, H, device="cuda", generator=g).bfloat16()
+    gamma = (torch.rand(H, device="cuda", generator=g) + .5).bfloat16()
+    wsb = ops.gemm_kquant_a_ws_bytes(M, H)
+    outs = []
+    for fused in (False, True):
+        x = torch.empty(M, H, dtype=torch.bfloat16, device="cuda")
+        res_out = torch.empty_like(x)
+        y = torch.empty_like(x)
+        ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
+        if fused:
+            L.norm_prep_moe(pairs, sh, K, gamma, ws, 1e-6, x_out=x, res_in=res_in,
+                            res_out=res_out, y_out=y)
+        else:
+            L.moe_combine(pairs, sh, x, M, K, H)
+            L.norm_prep(x, gamma, ws, 1e-6, res_in=res_in, res_out=res_out, y_out=y)
+        torch.cuda.synchronize()
+        outs.append((x, res_out, y, ws))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
