@@ -188,6 +188,77 @@ int snowverify_attention_d_split(int dh);
  * kernel's LDS ring, 4 or 8; 0 = automatic. Returns the previous value. */
 int snowverify_attention_ring(int pages);
 
+/* ---- geometry-driven operator entry points (reference signatures) ---------------------
+ * Shapes from the active geometry (see below); weights in the reference's _Weight descriptor
+ * (snowllm/ops/inference.py:10-22) holding this library's repacked layouts: k-quant (quant,
+ * meta) from snowllm_gemm_kquant_shuffle_b as kind 2 (kind 3: an expert stack, the experts'
+ * packed matrices back to back), 16-bit dense matrices (router, LM head) repacked by
+ * snowverify_dense_shuffle as kind 0. Features the verify path of this build does not carry
+ * (int8 KV, gated attention output, split Q/KV weights, fp8 dense scales, the DSA indexer,
+ * hashed routing, varlen prefill) return hipErrorNotSupported. */
+typedef struct SnowllmWeight {
+  void* data[3];
+  void* scale;
+  int kind; /* -1 absent, 0 dense, 1 dense + scale, 2 k-quant, 3 k-quant expert stack */
+  int fmt;  /* 4 = Q4_K, 8 = Q8_0 */
+} SnowllmWeight;
+
+/* snowllm/ops/attention_full.py:120-123. inputs: q, k_pool, v_pool, k_scale, v_scale,
+ * cu_seqlens, table, lens, qmap, gate; outputs: out, plan, workspace. */
+typedef struct PagedAttentionStep {
+  void* inputs[10];
+  void* outputs[3];
+  int64_t batch, pages, q_blocks, slots, tokens, page_size, gate_stride, gate_row0;
+  float scale;
+  int varlen; /* bit 0 varlen, bit 1 host lengths, bit 2 prepared metadata */
+} PagedAttentionStep;
+
+/* QKV projection with the input norm fused (snowllm/_capi.py:688; ops/inference.py:34-43):
+ * out [M, qkv_proj_n] bf16 = RMSNorm(residual += x) * gamma . W^T (no residual: RMSNorm(x);
+ * no gamma: x). w[3]: the QKV k-quant weight, then split V / KV (absent). */
+int64_t snowllm_qkv_proj_scratch_bytes(int64_t M);                     /* _capi.py:251 */
+int snowllm_inference_qkv(const SnowllmWeight* w, const void* x, void* residual,
+                          const void* gamma, float eps, void* scratch, void* out, int64_t M,
+                          int path, const void* index_w, void* index_out, void* stream);
+/* Attention output projection (snowllm/_capi.py:223-225; ops/attention_full.py:54-117):
+ * plan -> {elements of the attention output, scratch bytes}; the gate is NULL (no output gate
+ * in these geometries); out [m, hidden] bf16 = a [m, heads * head_size] . Wo^T (k-quant). */
+int snowllm_attn_output_plan(int64_t m, int prefill, int kv_int8, int64_t* out);
+void* snowllm_attn_output_gate(const void* proj, int prefill, int kv_int8);
+int snowllm_attn_output_project(const void* a, const void* proj, int64_t proj_stride,
+                                const void* dense, const void* quant, const void* meta,
+                                const void* scale, int fmt, void* scratch, void* out, int64_t m,
+                                int prefill, int kv_int8, void* stream);
+/* Paged attention through the step descriptor (snowllm/_capi.py:218-220; ops/attention_full.py:
+ * 126-177): the decode/verify form (tokens query rows per request, causal in the block). */
+int64_t snowllm_paged_attention_scratch_bytes(int64_t batch, int64_t tokens, int varlen);
+int snowllm_paged_attention_varlen(int prefill, int64_t tokens, int chunk_decode);
+int snowllm_paged_attention(const PagedAttentionStep* step, void* scratch, int64_t bytes,
+                            void* stream);
+/* MoE block (snowllm/_capi.py:315, 690-691, 805-807; ops/inference.py:54-95): w[4] = experts'
+ * gate/up stack, experts' down stack, shared gate/up, shared down; router: repacked bf16
+ * [E+1, hidden], the shared expert's gate last. The _norm form first sets residual += x and
+ * hidden_row = RMSNorm(residual) * gamma. x and out may alias. M <= 16. */
+int64_t snowllm_moe_workspace_bytes(int64_t rows);
+int64_t snowllm_inference_moe_workspace_bytes(int64_t rows, int64_t flags);
+int snowllm_inference_moe(const SnowllmWeight* w, const void* x, const void* router,
+                          const int64_t* token_ids, const int32_t* tid2eid, void* out,
+                          void* scratch, int64_t capacity, int64_t M, int flags, void* stream);
+int snowllm_inference_moe_norm(const SnowllmWeight* w, const void* x, void* residual,
+                               const void* gamma, float eps, void* hidden_row,
+                               const void* router, void* out, void* scratch, int64_t capacity,
+                               int64_t M, void* stream);
+/* Dense SwiGLU MLP (snowllm/_capi.py:599, 689; ops/inference.py:46-51): w[3] = packed [2F, H]
+ * gate/up (gate rows first), separate up (absent), down. M <= 16. */
+int64_t snowllm_fused_mlp_workspace_bytes(int64_t M);
+int snowllm_inference_mlp(const SnowllmWeight* w, const void* x, void* out, void* scratch,
+                          int64_t M, int decode, void* stream);
+/* LM head (snowllm/_capi.py:355, 692; ops/inference.py:98-104): logits [M, vocab] f32 for the
+ * normalised rows x; w: the repacked fp16 [vocab, hidden] head (kind 0). */
+int64_t snowllm_lm_head_scratch_bytes(int64_t M);
+int snowllm_inference_head(const SnowllmWeight* w, const void* x, float* out, void* scratch,
+                           int64_t M, void* stream);
+
 /* ---- geometry ------------------------------------------------------------------------ */
 /* The reference compiles its shapes in (snowllm/_capi.py:44-113); here they are run-time
  * data. BuildGeometry has the reference's 37 int64 fields in the same order. */
@@ -220,14 +291,26 @@ int snowllm_rmsnorm_residual(const void* x, void* residual, const void* gamma, v
 int snowverify_rmsnorm(const void* x, void* residual, const void* gamma, void* out, int64_t M,
                        int64_t H, float eps, void* stream);
 
-/* RoPE tables cos/sin [M, half] of pos * inv_freq (snowllm/ops/rope.py:11-24 computes them
- * inside snowllm_rope_cos_sin; this form takes the table width explicitly). */
+/* RoPE tables cos/sin [M, 64] of pos * inv_freq[32] (snowllm/ops/rope.py:11-24, the plain
+ * form): the reference's rotary dimension 64, the 32 values repeated in columns 32..63. */
+int snowllm_rope_cos_sin(const int64_t* pos, const float* inv_freq, float* cos_out,
+                         float* sin_out, int64_t M, void* stream);
+/* Extension: RoPE tables cos/sin [M, half] of pos * inv_freq (any rotary width). */
 int snowverify_rope_cos_sin(const int64_t* pos, const float* inv_freq, float* cos_out,
                             float* sin_out, int64_t M, int64_t half, void* stream);
 
-/* QK-norm + RoPE + paged KV write (snowllm/_capi.py:397-399; ops/attention_full.py:736-784)
- * with explicit shapes: proj [M, stride] = q|k|v bf16 -> q_out [M, Hq, D]; k, v into the pools
- * at slots[m] (negative: skipped). D <= 256. */
+/* QK-norm + RoPE + paged KV write (snowllm/_capi.py:397-399; ops/attention_full.py:736-784),
+ * shapes from the active geometry: q heads of proj [m, n] at the geometry's q head stride, K
+ * rows at kp (stride ks), V rows at v (stride vs); cos/sin [m, 64]; q [m, Hq, D]; K/V into the
+ * bf16 pools at slots[m] (negative: skipped). k_scale and v_scale must be NULL (no int8 KV). */
+int snowllm_qk_norm_rope_cache(const void* proj, int64_t n, const void* kp, int64_t ks,
+                               const void* v, int64_t vs, const void* q_gamma,
+                               const void* k_gamma, const float* cos_in, const float* sin_in,
+                               void* q, void* k_cache, void* v_cache, const void* k_scale,
+                               const void* v_scale, const int32_t* slots, int64_t m, float eps,
+                               int64_t block_size, void* stream);
+/* Extension: the same with explicit shapes: proj [M, stride] = q|k|v bf16 -> q_out [M, Hq, D];
+ * cos/sin [M, half]. D <= 256. */
 int snowverify_qk_norm_rope_cache(const void* proj, int64_t stride, const void* q_gamma,
                                   const void* k_gamma, const float* cos_in, const float* sin_in,
                                   void* q_out, void* k_pool, void* v_pool, const int32_t* slots,
@@ -254,7 +337,7 @@ int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, int64_t
 /* ---- feed-forward (extensions; the reference reaches these through snowllm_inference_*,
  * snowllm/_capi.py:687-692, whose weight descriptors and workspaces are internal) ------------ */
 /* res_out = x + res_in; y = RMSNorm(res_out) * gamma into the k-quant operand workspace ws (and
- * y_out if given). H <= 8192; res_out and y_out must not alias x or res_in. */
+ * y_out if given). H <= 8192; res_out and y_out may alias x or res_in (in place). */
 int snowverify_norm_prep(const void* x, const void* res_in, void* res_out, const void* gamma,
                          void* y_out, void* ws, int64_t M, int64_t H, float eps, void* stream);
 /* snowverify_norm_prep on the MoE layer's output, combined in the same launch: x = bf16(sum_k

@@ -93,6 +93,25 @@ _SIGS = [
     ("snowverify_attention_pages_per_split", c_int, [c_int]),
     ("snowverify_attention_d_split", c_int, [c_int]),
     ("snowverify_attention_ring", c_int, [c_int]),
+    # geometry-driven operator entry points (reference signatures)
+    ("snowllm_qkv_proj_scratch_bytes", c_int64, [c_int64]),
+    ("snowllm_inference_qkv", c_int, [P, P, P, P, c_float, P, P, c_int64, c_int, P, P, S]),
+    ("snowllm_attn_output_plan", c_int, [c_int64, c_int, c_int, P]),
+    ("snowllm_attn_output_gate", P, [P, c_int, c_int]),
+    ("snowllm_attn_output_project", c_int, [P, P, c_int64, P, P, P, P, c_int, P, P, c_int64, c_int, c_int, S]),
+    ("snowllm_paged_attention_scratch_bytes", c_int64, [c_int64, c_int64, c_int]),
+    ("snowllm_paged_attention_varlen", c_int, [c_int, c_int64, c_int]),
+    ("snowllm_paged_attention", c_int, [P, P, c_int64, S]),
+    ("snowllm_moe_workspace_bytes", c_int64, [c_int64]),
+    ("snowllm_inference_moe_workspace_bytes", c_int64, [c_int64, c_int64]),
+    ("snowllm_inference_moe", c_int, [P] * 7 + [c_int64, c_int64, c_int, S]),
+    ("snowllm_inference_moe_norm", c_int, [P, P, P, P, c_float, P, P, P, P, c_int64, c_int64, S]),
+    ("snowllm_fused_mlp_workspace_bytes", c_int64, [c_int64]),
+    ("snowllm_inference_mlp", c_int, [P, P, P, P, c_int64, c_int, S]),
+    ("snowllm_lm_head_scratch_bytes", c_int64, [c_int64]),
+    ("snowllm_inference_head", c_int, [P, P, P, P, c_int64, S]),
+    ("snowllm_rope_cos_sin", c_int, [P, P, P, P, c_int64, S]),
+    ("snowllm_qk_norm_rope_cache", c_int, [P, c_int64, P, c_int64, P, c_int64] + [P] * 10 + [c_int64, c_float, c_int64, S]),
     # geometry and layer plumbing
     ("snowllm_model_config", None, [P]),
     ("snowllm_select_geometry", c_int, [c_int]),

@@ -687,15 +687,13 @@ int launch_dense(const void* w, const void* act, void* c, int M, int N, int S, i
 
 // Residual update + RMSNorm + operand conversion for the k-quant GEMVs: res_out = x + res_in
 // (x alone when res_in is null), y = RMSNorm(res_out) * gamma. All bf16 [M, H], H <= 8192;
-// res_in, res_out and y_out may be null; res_out and y_out must not alias x or res_in. ws as
-// for snowllm_gemm_kquant_a.
+// res_in, res_out and y_out may be null. Each element is read and written by one thread, so
+// res_out and y_out may alias x or res_in (in-place residual update). ws as for
+// snowllm_gemm_kquant_a.
 SV_API int snowverify_norm_prep(const void* x, const void* res_in, void* res_out,
                                 const void* gamma, void* y_out, void* ws, int64_t M, int64_t H,
                                 float eps, void* stream) {
-  if (M <= 0 || H <= 0 || H % 256) return SV_EINVAL;
-  if (res_out && (res_out == x || res_out == res_in)) return SV_EINVAL;
-  if (y_out && (y_out == x || y_out == res_in)) return SV_EINVAL;
-  if (H > 8 * NORM_MAX_THREADS) return SV_EINVAL;
+  if (M <= 0 || H <= 0 || H % 256 || H > 8 * NORM_MAX_THREADS) return SV_EINVAL;
   return launch_norm_prep(x, MoeSource{nullptr, nullptr, nullptr, 0}, res_in, res_out, gamma,
                           y_out, ws, M, H, eps, Sx(stream));
 }
@@ -709,9 +707,7 @@ SV_API int snowverify_norm_prep_moe(const float* pairs, const float* shared_out,
                                     int64_t H, float eps, void* stream) {
   if (!pairs || topk <= 0 || M <= 0 || H <= 0 || H % 256 || H > 8 * NORM_MAX_THREADS)
     return SV_EINVAL;
-  if (res_out && res_out == res_in) return SV_EINVAL;
-  if (y_out && y_out == res_in) return SV_EINVAL;
-  if (x_out && (x_out == res_in || x_out == res_out || x_out == y_out)) return SV_EINVAL;
+  if (x_out && (x_out == res_out || x_out == y_out)) return SV_EINVAL;
   return launch_norm_prep(nullptr, MoeSource{pairs, shared_out, (uint16_t*)x_out, (int)topk},
                           res_in, res_out, gamma, y_out, ws, M, H, eps, Sx(stream));
 }

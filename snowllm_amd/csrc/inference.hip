@@ -1,0 +1,387 @@
+// The reference's geometry-driven operator entry points for the verify path, composed from this
+// library's kernels: fused-norm QKV projection, attention output projection, paged attention
+// through its step descriptor, the MoE block (with and without the fused post-attention norm),
+// the dense MLP and the LM head (snowllm/_capi.py:218-225, 251, 315, 355, 599, 687-692, 805-807;
+// wrappers snowllm/ops/inference.py:10-104, snowllm/ops/attention_full.py:54-177).
+//
+// Shapes come from the active geometry, as in the reference. Weights arrive in the reference's
+// _Weight descriptor (snowllm/ops/inference.py:10-22), holding this library's repacked layouts:
+// k-quant matrices as (quant, meta) from snowllm_gemm_kquant_shuffle_b (kind 2, or kind 3 for an
+// expert stack: the experts' packed matrices back to back), 16-bit dense matrices (router, LM
+// head) as repacked by snowverify_dense_shuffle (kind 0). Features of the reference that the
+// verify path of this build does not carry -- int8 KV, gated attention output, split Q/KV
+// weights, fp8 dense scales, the DSA indexer, hashed routing, varlen prefill -- return
+// hipErrorNotSupported instead of computing something else.
+//
+// Workspaces are carved from the caller's scratch with 256-byte alignment; the *_bytes queries
+// return the totals. No entry point allocates or synchronises.
+#include "common.h"
+#include "geometry.h"
+
+namespace {
+
+struct Weight {  // snowllm/ops/inference.py:10-12
+  void* data[3];
+  void* scale;
+  int kind;  // -1 absent, 0 dense, 1 dense + scale, 2 k-quant, 3 k-quant expert stack
+  int fmt;
+};
+
+struct PagedAttentionStep {  // snowllm/ops/attention_full.py:120-123
+  void* inputs[10];  // q, k_pool, v_pool, k_scale, v_scale, cu_seqlens, table, lens, qmap, gate
+  void* outputs[3];  // out, plan, workspace
+  int64_t batch, pages, q_blocks, slots, tokens, page_size, gate_stride, gate_row0;
+  float scale;
+  int varlen;  // bit 0: varlen, bit 1: host lengths, bit 2: prepared metadata
+};
+
+constexpr int WT_F16 = 1, WT_BF16 = 2;  // snowverify_dense_gemv weight types
+constexpr int MAX_ROWS = 16;            // rows per MoE / dense-GEMV call (one 16-row tile)
+
+inline size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+bool kquant(const Weight* w) { return w && (w->kind == 2 || w->kind == 3) && w->data[0] && w->data[1]; }
+bool absent(const Weight* w) { return !w || w->kind < 0; }
+
+// Carves consecutive 256-byte aligned regions out of a scratch buffer.
+struct Carve {
+  char* p;
+  size_t used = 0;
+  explicit Carve(void* base) : p((char*)base) {}
+  void* take(size_t n) {
+    void* r = p ? p + used : nullptr;
+    used += a256(n);
+    return r;
+  }
+};
+
+}  // namespace
+
+extern "C" {
+int64_t snowllm_gemm_kquant_a_ws_bytes(int64_t M, int64_t K);
+int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, const uint8_t* meta,
+                          void* c, int64_t M, int64_t N, int64_t K, int c_is_bf16, void* ws,
+                          void* stream);
+int snowllm_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws, void* stream);
+int snowllm_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta, void* c,
+                                   int64_t M, int64_t N, int64_t K, int c_is_bf16,
+                                   const void* ws, void* stream);
+int snowverify_norm_prep(const void* x, const void* res_in, void* res_out, const void* gamma,
+                         void* y_out, void* ws, int64_t M, int64_t H, float eps, void* stream);
+int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c, int64_t M, int64_t N,
+                          int64_t K, int c_is_bf16, void* stream);
+int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* meta, const void* ws,
+                              void* act, int64_t M, int64_t F, int64_t K, void* stream);
+int64_t snowverify_moe_plan_bytes(void);
+int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_t M, int64_t E,
+                              int64_t topk, float* weights, int32_t* ids, float* shared_w,
+                              void* plan, void* stream);
+int snowverify_moe_gate_up(int fmt, const void* gu_quant, const void* gu_meta,
+                           const void* sh_gu_quant, const void* sh_gu_meta, const void* plan,
+                           const void* ws, void* act, int64_t M, int64_t max_slots, int64_t E,
+                           int64_t H, int64_t F, void* stream);
+int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_meta,
+                        const void* sh_dn_quant, const void* sh_dn_meta, const void* plan,
+                        const void* act, const float* weights, const float* shared_w,
+                        float* pairs, float* shared_out, int64_t max_slots, int64_t E, int64_t H,
+                        int64_t F, void* stream);
+int snowverify_moe_combine(const float* pairs, const float* shared_out, void* out, int64_t M,
+                           int64_t topk, int64_t H, void* stream);
+int64_t snowverify_paged_attention_scratch_bytes(int64_t batch, int64_t tokens,
+                                                 int64_t num_heads, int64_t num_kv_heads,
+                                                 int64_t head_size);
+int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_pool, void* out,
+                               const int32_t* table, const int32_t* lens, const uint64_t* tree,
+                               int64_t batch, int64_t tokens, int64_t num_heads,
+                               int64_t num_kv_heads, int64_t head_size, int64_t page_size,
+                               int64_t table_stride, float scale, void* scratch,
+                               int64_t scratch_bytes, void* stream);
+}
+
+namespace {
+
+// ---- MoE workspace: operands | logits | routing | plan | activations | pairs | shared rows --
+struct MoeWs {
+  void* ws;
+  float* logits;
+  float* weights;
+  int32_t* ids;
+  float* shared_w;
+  void* plan;
+  void* act;
+  float* pairs;
+  float* shared_out;
+  size_t bytes;
+};
+
+MoeWs moe_ws(void* base, int64_t M) {
+  const BuildGeometry& g = active_geometry();
+  const int64_t E = g.moe_num_experts, K = g.moe_topk, H = g.hidden, F = g.moe_inter;
+  Carve c(base);
+  MoeWs w;
+  w.ws = c.take((size_t)snowllm_gemm_kquant_a_ws_bytes(M, H));
+  w.logits = (float*)c.take((size_t)M * (E + 1) * 4);
+  w.weights = (float*)c.take((size_t)M * K * 4);
+  w.ids = (int32_t*)c.take((size_t)M * K * 4);
+  w.shared_w = (float*)c.take((size_t)M * 4);
+  w.plan = c.take((size_t)snowverify_moe_plan_bytes());
+  w.act = c.take((size_t)(M * K + 1) * 16 * F * 2);
+  w.pairs = (float*)c.take((size_t)M * K * H * 4);
+  w.shared_out = (float*)c.take((size_t)M * H * 4);
+  w.bytes = c.used;
+  return w;
+}
+
+bool moe_geometry_ok() {
+  const BuildGeometry& g = active_geometry();
+  return g.moe_num_experts > 0 && g.moe_topk > 0 && g.moe_inter > 0;
+}
+
+// Router GEMV, routing + plan, experts, combine: out = sum_k w_k expert_k(y) + sigmoid(g) shared(y)
+// for the normalised rows y (bf16 `hidden`, operands already in ws.ws).
+int moe_body(const Weight* w, const void* hidden, const void* router, void* out, const MoeWs& ws,
+             int64_t M, void* s) {
+  const BuildGeometry& g = active_geometry();
+  const int64_t E = g.moe_num_experts, K = g.moe_topk, H = g.hidden, F = g.moe_inter;
+  const bool shared = !absent(&w[2]);
+  if (!kquant(&w[0]) || !kquant(&w[1]) || w[0].fmt != 4 || w[1].fmt != 4) return SV_ENOTSUP;
+  if (shared && (!kquant(&w[2]) || !kquant(&w[3]) || w[2].fmt != 4 || w[3].fmt != 4))
+    return SV_ENOTSUP;
+  if (shared != (g.moe_shared_expert != 0)) return SV_EINVAL;
+  int rc = snowverify_dense_gemv(WT_BF16, router, hidden, ws.logits, M, E + 1, H, 0, s);
+  if (rc) return rc;
+  rc = snowverify_moe_route_plan(ws.logits, E + 1, M, E, K, ws.weights, ws.ids,
+                                 shared ? ws.shared_w : nullptr, ws.plan, s);
+  if (rc) return rc;
+  const int64_t slots = M * K + (shared ? 1 : 0);
+  rc = snowverify_moe_gate_up(4, w[0].data[0], w[0].data[1], shared ? w[2].data[0] : nullptr,
+                              shared ? w[2].data[1] : nullptr, ws.plan, ws.ws, ws.act, M, slots,
+                              E, H, F, s);
+  if (rc) return rc;
+  rc = snowverify_moe_down(4, w[1].data[0], w[1].data[1], shared ? w[3].data[0] : nullptr,
+                           shared ? w[3].data[1] : nullptr, ws.plan, ws.act, ws.weights,
+                           ws.shared_w, ws.pairs, ws.shared_out, slots, E, H, F, s);
+  if (rc) return rc;
+  return snowverify_moe_combine(ws.pairs, shared ? ws.shared_out : nullptr, out, M, K, H, s);
+}
+
+// ---- dense MLP workspace: x operands | activations | activation operands -----------------
+struct MlpWs {
+  void* ws_x;
+  void* act;
+  void* ws_act;
+  size_t bytes;
+};
+
+MlpWs mlp_ws(void* base, int64_t M) {
+  const BuildGeometry& g = active_geometry();
+  Carve c(base);
+  MlpWs w;
+  w.ws_x = c.take((size_t)snowllm_gemm_kquant_a_ws_bytes(M, g.hidden));
+  w.act = c.take((size_t)M * g.mlp_inter * 2);
+  w.ws_act = c.take((size_t)snowllm_gemm_kquant_a_ws_bytes(M, g.mlp_inter));
+  w.bytes = c.used;
+  return w;
+}
+
+}  // namespace
+
+// =======================================================================================
+// C ABI
+// =======================================================================================
+
+// snowllm/_capi.py:251 -- scratch of snowllm_inference_qkv: the operand workspace of M rows.
+SV_API int64_t snowllm_qkv_proj_scratch_bytes(int64_t M) {
+  return M <= 0 ? 0 : snowllm_gemm_kquant_a_ws_bytes(M, active_geometry().hidden);
+}
+
+// snowllm/_capi.py:688 (ops/inference.py:34-43; QKVProj, models/qwen3_5/layers.py:33-50):
+// out [M, qkv_proj_n] bf16 = y W^T with y = RMSNorm(residual += x) * gamma when gamma is given
+// (y = RMSNorm(x) * gamma without a residual; y = x without gamma). w[0]: the QKV k-quant
+// weight; w[1], w[2] (split V / KV) must be absent, as must the indexer.
+SV_API int snowllm_inference_qkv(const Weight* w, const void* x, void* residual,
+                                 const void* gamma, float eps, void* scratch, void* out,
+                                 int64_t M, int path, const void* index_w, void* index_out,
+                                 void* stream) {
+  (void)path;  // the reference's execution-path hint; one path here
+  const BuildGeometry& g = active_geometry();
+  if (!w || !kquant(&w[0]) || !absent(&w[1]) || !absent(&w[2]) || index_w || index_out)
+    return SV_ENOTSUP;
+  if (M <= 0 || !x || !out || !scratch) return SV_EINVAL;
+  const auto* q = (const uint8_t*)w[0].data[0];
+  const auto* m = (const uint8_t*)w[0].data[1];
+  if (!gamma)
+    return snowllm_gemm_kquant_a(w[0].fmt, x, q, m, out, M, g.qkv_proj_n, g.hidden, 1, scratch,
+                                 stream);
+  int rc = snowverify_norm_prep(x, residual, residual, gamma, nullptr, scratch, M, g.hidden, eps,
+                                stream);
+  if (rc) return rc;
+  return snowllm_gemm_kquant_a_prepared(w[0].fmt, q, m, out, M, g.qkv_proj_n, g.hidden, 1,
+                                        scratch, stream);
+}
+
+// snowllm/_capi.py:223 (ops/attention_full.py:54-64): elements of the attention output and the
+// scratch bytes of snowllm_attn_output_project for m rows.
+SV_API int snowllm_attn_output_plan(int64_t m, int prefill, int kv_int8, int64_t* out) {
+  (void)prefill;
+  if (kv_int8) return SV_ENOTSUP;
+  if (m < 0 || !out) return SV_EINVAL;
+  const BuildGeometry& g = active_geometry();
+  out[0] = m * g.num_heads * g.head_size;
+  out[1] = m > 16 ? snowllm_gemm_kquant_a_ws_bytes(m, g.num_heads * g.head_size) : 0;
+  return SV_OK;
+}
+
+// snowllm/_capi.py:224 (ops/attention_full.py:67-70): the attention output gate inside the
+// projection rows. The geometries of this build carry no output gate.
+SV_API void* snowllm_attn_output_gate(const void* proj, int prefill, int kv_int8) {
+  (void)proj;
+  (void)prefill;
+  (void)kv_int8;
+  return nullptr;
+}
+
+// snowllm/_capi.py:225 (ops/attention_full.py:98-117; OProj, models/qwen3_5/layers.py:53-64):
+// out [m, hidden] bf16 = a [m, heads * head_size] Wo^T with the k-quant (quant, meta) weight.
+SV_API int snowllm_attn_output_project(const void* a, const void* proj, int64_t proj_stride,
+                                       const void* dense, const void* quant, const void* meta,
+                                       const void* scale, int fmt, void* scratch, void* out,
+                                       int64_t m, int prefill, int kv_int8, void* stream) {
+  (void)proj;
+  (void)proj_stride;
+  (void)prefill;
+  if (dense || scale || kv_int8 || active_geometry().qkv_off_scale) return SV_ENOTSUP;
+  if (!quant || !meta || !a || !out || m < 0) return SV_EINVAL;
+  if (m == 0) return SV_OK;
+  const BuildGeometry& g = active_geometry();
+  return snowllm_gemm_kquant_a(fmt, a, (const uint8_t*)quant, (const uint8_t*)meta, out, m,
+                               g.hidden, g.num_heads * g.head_size, 1, scratch, stream);
+}
+
+// snowllm/_capi.py:218-219 (ops/attention_full.py:126-134).
+SV_API int64_t snowllm_paged_attention_scratch_bytes(int64_t batch, int64_t tokens, int varlen) {
+  if (varlen || batch <= 0 || tokens <= 0) return 0;
+  const BuildGeometry& g = active_geometry();
+  return snowverify_paged_attention_scratch_bytes(batch, tokens, g.num_heads, g.num_kv_heads,
+                                                  g.head_size);
+}
+
+// Whether a step runs the varlen (prefill) form. Decode and verify steps -- equal token counts
+// per request -- do not; prefill, which this build does not carry, would.
+SV_API int snowllm_paged_attention_varlen(int prefill, int64_t tokens, int chunk_decode) {
+  (void)tokens;
+  (void)chunk_decode;
+  return prefill ? 1 : 0;
+}
+
+// snowllm/_capi.py:220 (ops/attention_full.py:152-177): the step descriptor's decode/verify
+// form -- `tokens` query rows per request, causal within the block, bf16 pools, no gate.
+SV_API int snowllm_paged_attention(const PagedAttentionStep* st, void* scratch, int64_t bytes,
+                                   void* stream) {
+  if (!st) return SV_EINVAL;
+  if ((st->varlen & 5) || st->inputs[3] || st->inputs[4] || st->inputs[9]) return SV_ENOTSUP;
+  const BuildGeometry& g = active_geometry();
+  return snowverify_paged_attention(st->inputs[0], st->inputs[1], st->inputs[2], st->outputs[0],
+                                    (const int32_t*)st->inputs[6], (const int32_t*)st->inputs[7],
+                                    nullptr, st->batch, st->tokens, g.num_heads, g.num_kv_heads,
+                                    g.head_size, st->page_size, st->pages, st->scale, scratch,
+                                    bytes, stream);
+}
+
+// snowllm/_capi.py:315 and 690 -- scratch of the MoE block for `rows` rows (flags must be 0).
+SV_API int64_t snowllm_moe_workspace_bytes(int64_t rows) {
+  if (rows <= 0 || !moe_geometry_ok()) return 0;
+  return (int64_t)moe_ws(nullptr, rows).bytes;
+}
+
+SV_API int64_t snowllm_inference_moe_workspace_bytes(int64_t rows, int64_t flags) {
+  return flags ? 0 : snowllm_moe_workspace_bytes(rows);
+}
+
+// snowllm/_capi.py:691 (ops/inference.py:60-76): out [M, hidden] = MoE(x) for normalised x.
+// w: experts' gate/up stack, experts' down stack, shared gate/up, shared down (absent when the
+// geometry has no shared expert); router: the repacked bf16 [E + 1, hidden] router with the
+// shared expert's gate last. x and out may be the same buffer. M <= 16.
+SV_API int snowllm_inference_moe(const Weight* w, const void* x, const void* router,
+                                 const int64_t* token_ids, const int32_t* tid2eid, void* out,
+                                 void* scratch, int64_t capacity, int64_t M, int flags,
+                                 void* stream) {
+  if (token_ids || tid2eid || flags) return SV_ENOTSUP;
+  if (!w || !x || !router || !out || !scratch || M <= 0 || M > MAX_ROWS || !moe_geometry_ok())
+    return SV_EINVAL;
+  const MoeWs ws = moe_ws(scratch, M);
+  if (capacity < (int64_t)ws.bytes) return SV_EINVAL;
+  int rc = snowllm_gemm_kquant_prepare_a(x, M, active_geometry().hidden, ws.ws, stream);
+  if (rc) return rc;
+  return moe_body(w, x, router, out, ws, M, stream);
+}
+
+// snowllm/_capi.py:805-807 (ops/inference.py:82-95; FusedMoE with the post-attention norm,
+// models/qwen3_5/qwen3_5.py:38-41): residual += x; hidden_row = RMSNorm(residual) * gamma;
+// out = MoE(hidden_row). x and out may be the same buffer. M <= 16.
+SV_API int snowllm_inference_moe_norm(const Weight* w, const void* x, void* residual,
+                                      const void* gamma, float eps, void* hidden_row,
+                                      const void* router, void* out, void* scratch,
+                                      int64_t capacity, int64_t M, void* stream) {
+  if (!w || !x || !residual || !gamma || !hidden_row || !router || !out || !scratch || M <= 0 ||
+      M > MAX_ROWS || !moe_geometry_ok())
+    return SV_EINVAL;
+  const MoeWs ws = moe_ws(scratch, M);
+  if (capacity < (int64_t)ws.bytes) return SV_EINVAL;
+  int rc = snowverify_norm_prep(x, residual, residual, gamma, hidden_row, ws.ws, M,
+                                active_geometry().hidden, eps, stream);
+  if (rc) return rc;
+  return moe_body(w, hidden_row, router, out, ws, M, stream);
+}
+
+// snowllm/_capi.py:599 -- scratch of snowllm_inference_mlp for M rows.
+SV_API int64_t snowllm_fused_mlp_workspace_bytes(int64_t M) {
+  if (M <= 0 || active_geometry().mlp_inter <= 0) return 0;
+  return (int64_t)mlp_ws(nullptr, M).bytes;
+}
+
+// snowllm/_capi.py:689 (ops/inference.py:46-51; DenseMLP, models/qwen3_5/layers.py:192-205):
+// out [M, hidden] = (silu(x Wg^T) * (x Wu^T)) Wd^T with w[0] the packed [2F, hidden] gate/up
+// k-quant weight (gate rows first), w[1] (separate up) absent, w[2] the down weight. M <= 16.
+SV_API int snowllm_inference_mlp(const Weight* w, const void* x, void* out, void* scratch,
+                                 int64_t M, int decode, void* stream) {
+  (void)decode;
+  if (!w || !kquant(&w[0]) || !absent(&w[1]) || !kquant(&w[2]) || w[0].fmt != w[2].fmt)
+    return SV_ENOTSUP;
+  const BuildGeometry& g = active_geometry();
+  if (!x || !out || !scratch || M <= 0 || M > MAX_ROWS || g.mlp_inter <= 0) return SV_EINVAL;
+  const MlpWs ws = mlp_ws(scratch, M);
+  int rc = snowllm_gemm_kquant_prepare_a(x, M, g.hidden, ws.ws_x, stream);
+  if (rc) return rc;
+  rc = snowverify_gate_up_swiglu(w[0].fmt, w[0].data[0], w[0].data[1], ws.ws_x, ws.act, M,
+                                 g.mlp_inter, g.hidden, stream);
+  if (rc) return rc;
+  return snowllm_gemm_kquant_a(w[2].fmt, ws.act, (const uint8_t*)w[2].data[0],
+                               (const uint8_t*)w[2].data[1], out, M, g.hidden, g.mlp_inter, 1,
+                               ws.ws_act, stream);
+}
+
+// snowllm/_capi.py:355 -- scratch of snowllm_inference_head for M rows.
+SV_API int64_t snowllm_lm_head_scratch_bytes(int64_t M) {
+  return M <= 0 ? 0 : snowllm_gemm_kquant_a_ws_bytes(M, active_geometry().hidden);
+}
+
+// snowllm/_capi.py:692 (ops/inference.py:98-104; LMHead, models/qwen3_5/layers.py:209-228):
+// logits [M, vocab] f32 = x W^T for the normalised rows x, W the fp16 [vocab, hidden] head
+// repacked by snowverify_dense_shuffle (kind 0). Rows go in 16-row tiles.
+SV_API int snowllm_inference_head(const Weight* w, const void* x, float* out, void* scratch,
+                                  int64_t M, void* stream) {
+  if (!w || w->kind != 0 || !w->data[0]) return SV_ENOTSUP;
+  const BuildGeometry& g = active_geometry();
+  if (!x || !out || !scratch || M <= 0) return SV_EINVAL;
+  int rc = snowllm_gemm_kquant_prepare_a(x, M, g.hidden, scratch, stream);
+  if (rc) return rc;
+  const int64_t tile_bytes = snowllm_gemm_kquant_a_ws_bytes(16, g.hidden);
+  for (int64_t r0 = 0; r0 < M; r0 += 16) {
+    const int64_t rows = M - r0 < 16 ? M - r0 : 16;
+    rc = snowverify_dense_gemv(WT_F16, w->data[0], (const char*)scratch + (r0 / 16) * tile_bytes,
+                               out + r0 * g.vocab_size, rows, g.vocab_size, g.hidden, 0, stream);
+    if (rc) return rc;
+  }
+  return SV_OK;
+}

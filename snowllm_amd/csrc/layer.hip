@@ -11,19 +11,7 @@
 
 #include <string.h>
 
-// Field order of the reference's BuildGeometry (snowllm/_capi.py:44-64).
-struct BuildGeometry {
-  int64_t hidden, num_heads, num_kv_heads, head_size, block_size, vocab_size;
-  int64_t qkv_proj_n, qkv_q_head_stride, qkv_off_scale, qkv_off_k, qkv_off_v;
-  int64_t lin_num_k_heads, lin_num_v_heads, lin_head_k, lin_head_v, lin_key_dim;
-  int64_t lin_value_dim, lin_conv_dim, lin_conv_k, lin_conv_state, lin_in_proj_n;
-  int64_t lin_in_proj_n_pad;
-  int64_t lin_in_proj_ba_n_pad, lin_off_qkv, lin_off_z, lin_off_b, lin_off_a;
-  int64_t moe_num_experts, moe_shared_expert, moe_num_slabs, moe_topk, moe_topk_all;
-  int64_t moe_inter, sampling_max_k, lm_head_decode_max_m, mlp_inter;
-  int64_t mlp_gate_up_n;
-};
-static_assert(sizeof(BuildGeometry) == 37 * 8, "BuildGeometry layout");
+#include "geometry.h"
 
 namespace {
 
@@ -113,16 +101,22 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict
 // ---------------------------------------------------------------------------------------
 // RoPE tables: cos/sin[m, i] = cos/sin(pos[m] * inv_freq[i]), i < half (f32)
 // ---------------------------------------------------------------------------------------
+// Rows are `width` apart; width = 2 half repeats the half in columns half .. 2 half - 1.
 __global__ void rope_cos_sin_kernel(const int64_t* __restrict__ pos,
                                     const float* __restrict__ inv_freq, float* __restrict__ c,
-                                    float* __restrict__ s, int64_t M, int half) {
+                                    float* __restrict__ s, int64_t M, int half, int width) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= M * half) return;
   const int64_t m = idx / half;
   const int i = (int)(idx % half);
   const float a = (float)pos[m] * inv_freq[i];
-  c[idx] = cosf(a);
-  s[idx] = sinf(a);
+  const float cv = cosf(a), sv = sinf(a);
+  c[m * width + i] = cv;
+  s[m * width + i] = sv;
+  if (width >= 2 * half) {
+    c[m * width + half + i] = cv;
+    s[m * width + half + i] = sv;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -133,16 +127,28 @@ __global__ void rope_cos_sin_kernel(const int64_t* __restrict__ pos,
 // K [blocks, Hkv, D/16, page, 16] and V [blocks, Hkv, page/4, D, 4].
 // One wave per (row, head); heads >= Hq + Hkv copy v.
 // ---------------------------------------------------------------------------------------
+// Sources of one row's heads: q head h at q + m * q_stride + h * q_head_stride, k head h at
+// k + m * k_stride + h * D, v head h at v + m * v_stride + h * D; cos/sin rows cs_stride apart
+// (the first `half` entries of a row are used).
+struct QkvSources {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t q_stride, q_head_stride, k_stride, v_stride, cs_stride;
+};
+
 __global__ void __launch_bounds__(64) qk_norm_rope_cache_kernel(
-    const uint16_t* __restrict__ proj, int64_t stride, const uint16_t* __restrict__ q_gamma,
-    const uint16_t* __restrict__ k_gamma, const float* __restrict__ cosv,
-    const float* __restrict__ sinv, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool,
-    uint16_t* __restrict__ v_pool, const int32_t* __restrict__ slots, int Hq, int Hkv, int D,
-    int half, int page, float eps) {
+    QkvSources src_, const uint16_t* __restrict__ q_gamma, const uint16_t* __restrict__ k_gamma,
+    const float* __restrict__ cosv, const float* __restrict__ sinv, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
+    const int32_t* __restrict__ slots, int Hq, int Hkv, int D, int half, int page, float eps) {
   const int64_t m = blockIdx.y;
   const int head = blockIdx.x;
   const int lane = threadIdx.x;
-  const uint16_t* src = proj + m * stride + (int64_t)head * D;
+  const uint16_t* src =
+      head < Hq ? src_.q + m * src_.q_stride + (int64_t)head * src_.q_head_stride
+      : head < Hq + Hkv ? src_.k + m * src_.k_stride + (int64_t)(head - Hq) * D
+                        : src_.v + m * src_.v_stride + (int64_t)(head - Hq - Hkv) * D;
   const int slot = slots[m];
   const int blk = slot / page, off = slot % page;
   if (head >= Hq + Hkv) {  // v
@@ -181,8 +187,8 @@ __global__ void __launch_bounds__(64) qk_norm_rope_cache_kernel(
     if (d < D) buf[d] = v[j];
   }
   __syncthreads();
-  const float* cr = cosv + m * half;
-  const float* sr = sinv + m * half;
+  const float* cr = cosv + m * src_.cs_stride;
+  const float* sr = sinv + m * src_.cs_stride;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int d = lane + 64 * j;
@@ -200,6 +206,23 @@ __global__ void __launch_bounds__(64) qk_norm_rope_cache_kernel(
       k_pool[idx] = o;
     }
   }
+}
+
+// The reference's rotary geometry: rotary dimension 64 (head_size x partial_rotary_factor,
+// checked at snowllm/models/qwen3_5/qwen3_5_weights.py:444), so 32 frequencies.
+constexpr int REF_ROPE_HALF = 32;
+
+int launch_qk_norm_rope_cache(const QkvSources& src, const void* q_gamma, const void* k_gamma,
+                              const float* cosv, const float* sinv, void* q_out, void* k_pool,
+                              void* v_pool, const int32_t* slots, int64_t M, int64_t Hq,
+                              int64_t Hkv, int64_t D, int64_t half, int64_t page, float eps,
+                              hipStream_t s) {
+  hipLaunchKernelGGL(qk_norm_rope_cache_kernel, dim3((unsigned)(Hq + 2 * Hkv), (unsigned)M),
+                     dim3(64), 0, s, src, (const uint16_t*)q_gamma, (const uint16_t*)k_gamma,
+                     cosv, sinv, (uint16_t*)q_out, (uint16_t*)k_pool, (uint16_t*)v_pool, slots,
+                     (int)Hq, (int)Hkv, (int)D, (int)half, (int)page, eps);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
 }
 
 // slot = table[row_seq, pos / page] * page + pos % page (snowllm/engine/spec_decode.py:183)
@@ -328,7 +351,21 @@ SV_API int snowverify_rope_cos_sin(const int64_t* pos, const float* inv_freq, fl
   if (M == 0) return SV_OK;
   const int64_t n = M * half;
   hipLaunchKernelGGL(rope_cos_sin_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     S(stream), pos, inv_freq, cosv, sinv, M, (int)half);
+                     S(stream), pos, inv_freq, cosv, sinv, M, (int)half, (int)half);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Reference signature (snowllm/_capi.py; wrapper snowllm/ops/rope.py:11-24, the plain form):
+// cos/sin [M, 64] f32 for the reference's rotary dimension 64, the 32 frequencies' values in
+// columns 0..31 repeated in 32..63 (the rotate-half convention); inv_freq f32 [32].
+SV_API int snowllm_rope_cos_sin(const int64_t* pos, const float* inv_freq, float* cosv,
+                                float* sinv, int64_t M, void* stream) {
+  if (M < 0) return SV_EINVAL;
+  if (M == 0) return SV_OK;
+  const int64_t n = M * REF_ROPE_HALF;
+  hipLaunchKernelGGL(rope_cos_sin_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     S(stream), pos, inv_freq, cosv, sinv, M, REF_ROPE_HALF, 2 * REF_ROPE_HALF);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -347,13 +384,33 @@ SV_API int snowverify_qk_norm_rope_cache(const void* proj, int64_t stride, const
       page != 16)
     return SV_EINVAL;
   if (M == 0) return SV_OK;
-  hipLaunchKernelGGL(qk_norm_rope_cache_kernel, dim3((unsigned)(Hq + 2 * Hkv), (unsigned)M),
-                     dim3(64), 0, S(stream), (const uint16_t*)proj, stride,
-                     (const uint16_t*)q_gamma, (const uint16_t*)k_gamma, cosv, sinv,
-                     (uint16_t*)q_out, (uint16_t*)k_pool, (uint16_t*)v_pool, slots, (int)Hq,
-                     (int)Hkv, (int)D, (int)half, (int)page, eps);
-  SV_CHECK_LAUNCH();
-  return SV_OK;
+  const uint16_t* p = (const uint16_t*)proj;
+  const QkvSources src{p, p + Hq * D, p + (Hq + Hkv) * D, stride, D, stride, stride, half};
+  return launch_qk_norm_rope_cache(src, q_gamma, k_gamma, cosv, sinv, q_out, k_pool, v_pool,
+                                   slots, M, Hq, Hkv, D, half, page, eps, S(stream));
+}
+
+// Reference signature (snowllm/_capi.py:397-399; wrapper snowllm/ops/attention_full.py:736-
+// 784): shapes from the active geometry (num_heads, num_kv_heads, head_size, q head stride),
+// K and V read from their own rows (kp/ks, v/vs), cos/sin [m, 64] (rotary dim 64: the first 32
+// columns hold the frequencies' cos and sin, as rope_cos_sin writes them). bf16 KV pools only:
+// k_scale and v_scale must be null (the int8 KV variant is not part of this build).
+SV_API int snowllm_qk_norm_rope_cache(const void* proj, int64_t n, const void* kp, int64_t ks,
+                                      const void* v, int64_t vs, const void* q_gamma,
+                                      const void* k_gamma, const float* cosv, const float* sinv,
+                                      void* q, void* k_cache, void* v_cache, const void* k_scale,
+                                      const void* v_scale, const int32_t* slots, int64_t m,
+                                      float eps, int64_t block_size, void* stream) {
+  if (k_scale || v_scale) return SV_ENOTSUP;
+  const BuildGeometry& g = g_geo;
+  if (block_size != g.block_size) return SV_EINVAL;
+  const int64_t D = g.head_size, Hq = g.num_heads, Hkv = g.num_kv_heads;
+  if (m < 0 || D <= 0 || D > 256 || D % 16 || block_size != 16) return SV_EINVAL;
+  if (m == 0) return SV_OK;
+  const QkvSources src{(const uint16_t*)proj, (const uint16_t*)kp, (const uint16_t*)v, n,
+                       g.qkv_q_head_stride, ks, vs, 2 * REF_ROPE_HALF};
+  return launch_qk_norm_rope_cache(src, q_gamma, k_gamma, cosv, sinv, q, k_cache, v_cache, slots,
+                                   m, Hq, Hkv, D, REF_ROPE_HALF, block_size, eps, S(stream));
 }
 
 // Reference signature (snowllm/_capi.py:361; snowllm/ops/cache.py:40-53).
@@ -399,3 +456,4 @@ SV_API int snowverify_add_bf16(const void* a, const void* b, void* out, int64_t 
   return SV_OK;
 }
 
+const BuildGeometry& active_geometry() { return g_geo; }

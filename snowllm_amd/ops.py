@@ -8,4 +8,13 @@ from .gemm import (Q4_K, Q8_0, gemm_kquant_a, gemm_kquant_a_ws_bytes,  # noqa: F
                    gemm_kquant_shuffle_b, kquant_bytes,
                    gemm_kquant_prepare_a, gemm_kquant_a_prepared)
 from .attention import (kv_pool_bytes, paged_attention_explicit,  # noqa: F401
-                        paged_attention_scratch_bytes)
+                        paged_attention_explicit_scratch_bytes, paged_attention,
+                        paged_attention_scratch_bytes, paged_attention_varlen, attn_output_plan,
+                        attn_output_shape, attn_output_gating, attn_output_project, rope_cos_sin,
+                        qk_norm_rope_cache)
+from .inference import (KQuantProjWeight, KQuantExpertWeight, inference_qkv,  # noqa: F401
+                        qkv_proj_scratch_bytes, inference_mlp, mlp_workspace_bytes,
+                        inference_moe, inference_moe_norm, inference_moe_workspace_bytes,
+                        moe_workspace_bytes, inference_head, lm_head_scratch_bytes)
+from .geometry import (build_geometry, select_geometry, active_geometry,  # noqa: F401
+                       define_geometry)

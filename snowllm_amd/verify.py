@@ -249,7 +249,7 @@ class VerifyModel:
         self.ws_a = torch.empty(ops.gemm_kquant_a_ws_bytes(T, c.heads * c.head_dim),
                                 dtype=torch.uint8, device=dev)
         self.attn_scratch = torch.empty(
-            ops.paged_attention_scratch_bytes(1, T, c.heads, c.kv_heads, c.head_dim),
+            ops.paged_attention_explicit_scratch_bytes(1, T, c.heads, c.kv_heads, c.head_dim),
             dtype=torch.uint8, device=dev)
         if c.moe:
             E, F, K = c.experts, c.expert_ffn, c.topk

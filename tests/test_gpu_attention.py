@@ -54,7 +54,7 @@ def _case(lengths, T, Hq, Hkv, D, seed, tree_parents=None, extra_blocks=7):
     scale = D ** -0.5
     out = torch.empty_like(q).cuda()
     lens = torch.tensor(lengths, dtype=torch.int32)
-    scratch = torch.empty(ops.paged_attention_scratch_bytes(batch, T, Hq, Hkv, D), dtype=torch.uint8, device="cuda")
+    scratch = torch.empty(ops.paged_attention_explicit_scratch_bytes(batch, T, Hq, Hkv, D), dtype=torch.uint8, device="cuda")
     print(f"attention lengths={lengths} T={T} Hq={Hq} Hkv={Hkv} D={D} tree={bool(tree_parents)}", flush=True)
     ops.paged_attention_explicit(q.cuda(), kp.cuda(), vp.cuda(), out, table.cuda(), lens.cuda(), scale,
                                  scratch, tree=None if tree is None else tree.cuda())

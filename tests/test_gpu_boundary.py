@@ -1,0 +1,182 @@
+"""The reference-signature entry points (geometry-driven, _Weight descriptors, the paged-attention
+step descriptor) against this build's explicit-shape path: one decoder layer run in the
+reference's own dataflow (snowllm/models/qwen3_5/qwen3_5.py:32-43, layers.py:86-117, 166-188)
+must give the same bits as VerifyModel's layer, and each operator matches its explicit form."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def tiny(kind):
+    from snowllm_amd.verify import VerifyConfig
+    base = dict(layers=2, hidden=512, heads=4, kv_heads=2, head_dim=128, rot_half=32,
+                rope_theta=1e4, vocab=2048, context=300, block=9)
+    if kind == "moe":
+        return VerifyConfig("tiny_moe", experts=16, expert_ffn=256, topk=4, **base)
+    return VerifyConfig("tiny_dense", ffn=512, **base)
+
+
+@pytest.fixture
+def geometry_of():
+    """Install the geometry of a VerifyConfig for the reference-signature entry points; the
+    default geometry comes back afterwards."""
+    from snowllm_amd import ops
+
+    def install(cfg):
+        d = cfg.head_dim
+        ops.define_geometry(
+            hidden=cfg.hidden, num_heads=cfg.heads, num_kv_heads=cfg.kv_heads, head_size=d,
+            block_size=16, vocab_size=cfg.vocab, qkv_proj_n=cfg.qkv_n, qkv_q_head_stride=d,
+            qkv_off_k=cfg.heads * d, qkv_off_v=(cfg.heads + cfg.kv_heads) * d,
+            moe_num_experts=cfg.experts if cfg.moe else 0, moe_shared_expert=int(cfg.moe),
+            moe_topk=cfg.topk if cfg.moe else 0, moe_topk_all=cfg.topk + 1 if cfg.moe else 0,
+            moe_inter=cfg.expert_ffn if cfg.moe else 0, sampling_max_k=1 << 19,
+            lm_head_decode_max_m=256, mlp_inter=0 if cfg.moe else cfg.ffn,
+            mlp_gate_up_n=0 if cfg.moe else 2 * cfg.ffn)
+    yield install
+    ops.select_geometry(0)
+
+
+def test_reference_dataflow_layer_matches_verify_model(gpu, geometry_of):
+    from snowllm_amd import ops
+    from snowllm_amd.verify import VerifyModel
+    cfg = tiny("moe")
+    geometry_of(cfg)
+    print("reference-signature layer, tiny moe", flush=True)
+    m = VerifyModel(cfg, seed=8)
+    T, H, d = cfg.block, cfg.hidden, cfg.head_dim
+    m.set_block(torch.arange(T) * 11)
+    m.forward(upto_layer=0)
+    torch.cuda.synchronize()
+    x0 = m.x.clone()  # the embeddings: the residual stream entering layer 0
+    lw = m.layers[0]
+    k_pool, v_pool = m.k_pools[0].clone(), m.v_pools[0].clone()
+    # -- the reference's layer 0, entry point by entry point --------------------------------
+    residual = x0.clone()
+    bf = torch.bfloat16
+    proj = torch.empty(T, cfg.qkv_n, dtype=bf, device="cuda")
+    scratch = torch.empty(ops.qkv_proj_scratch_bytes(T), dtype=torch.uint8, device="cuda")
+    w_qkv = ops.KQuantProjWeight(lw.qkv[0], lw.qkv[1], cfg.attn_fmt)
+    ops.inference_qkv(residual, w_qkv, None, None, None, scratch, proj, 0, None, lw.in_norm,
+                      cfg.eps)
+    cos = torch.empty(T, 64, device="cuda")
+    sin = torch.empty_like(cos)
+    ops.rope_cos_sin(m.positions, m.inv_freq, cos, sin)
+    q = torch.empty(T, cfg.heads, d, dtype=bf, device="cuda")
+    v = proj[:, (cfg.heads + cfg.kv_heads) * d:]
+    ops.qk_norm_rope_cache(proj, lw.q_norm, lw.k_norm, cos, sin, q, v, k_pool, v_pool, m.slots,
+                           cfg.eps, 16)
+    attn = torch.empty(*ops.attn_output_shape(T, False, False), dtype=bf, device="cuda")
+    ascratch = torch.empty(ops.paged_attention_scratch_bytes(1, T, False), dtype=torch.uint8,
+                           device="cuda")
+    ops.paged_attention(q, (k_pool, v_pool), attn, None, m.table, m.lens, None, 0, None, None,
+                        0, T, 16, d ** -0.5, False, ascratch,
+                        ops.attn_output_gating(proj, False, False))
+    blk = torch.empty(T, H, dtype=bf, device="cuda")
+    _, need = ops.attn_output_plan(T, False, False)
+    w_o = ops.KQuantProjWeight(lw.o[0], lw.o[1], cfg.attn_fmt)
+    ops.attn_output_project(attn, proj, w_o, None,
+                            torch.empty(max(need, 1), dtype=torch.uint8, device="cuda"), blk,
+                            False, False)
+    hidden = torch.empty(T, H, dtype=bf, device="cuda")
+    mws = torch.empty(ops.moe_workspace_bytes(T), dtype=torch.uint8, device="cuda")
+    gate = ops.KQuantExpertWeight(lw.gu[0], lw.gu[1], None, cfg.ffn_fmt)
+    down = ops.KQuantExpertWeight(lw.dn[0], lw.dn[1], None, cfg.ffn_fmt)
+    sh_gate = ops.KQuantProjWeight(lw.sh_gu[0], lw.sh_gu[1], cfg.ffn_fmt)
+    sh_down = ops.KQuantProjWeight(lw.sh_dn[0], lw.sh_dn[1], cfg.ffn_fmt)
+    ops.inference_moe_norm(blk, residual, lw.post_norm, cfg.eps, hidden, lw.router, gate, down,
+                           sh_gate, sh_down, blk, mws)
+    torch.cuda.synchronize()
+    # -- VerifyModel's layer 0 ------------------------------------------------------------
+    m.forward(upto_layer=1)
+    torch.cuda.synchronize()
+    assert torch.equal(proj, m.proj) and torch.equal(q, m.q)
+    assert torch.equal(k_pool, m.k_pools[0]) and torch.equal(v_pool, m.v_pools[0])
+    assert torch.equal(attn, m.attn)
+    assert torch.equal(hidden, m.h2)
+    assert torch.equal(residual, m.layer_residual)
+    assert torch.equal(blk, m.x)
+
+
+def test_moe_without_norm_and_head(gpu, geometry_of):
+    from snowllm_amd import layers as L
+    from snowllm_amd import ops
+    from snowllm_amd.verify import VerifyModel
+    cfg = tiny("moe")
+    geometry_of(cfg)
+    print("reference-signature MoE / head, tiny moe", flush=True)
+    m = VerifyModel(cfg, seed=9)
+    T, H = cfg.block, cfg.hidden
+    m.set_block(torch.arange(T) * 3)
+    m.forward()
+    torch.cuda.synchronize()
+    lw = m.layers[1]
+    y = m.h2.clone()  # a normalised hidden of the last layer
+    out = torch.empty(T, H, dtype=torch.bfloat16, device="cuda")
+    mws = torch.empty(ops.inference_moe_workspace_bytes(T), dtype=torch.uint8, device="cuda")
+    gate = ops.KQuantExpertWeight(lw.gu[0], lw.gu[1], None, cfg.ffn_fmt)
+    down = ops.KQuantExpertWeight(lw.dn[0], lw.dn[1], None, cfg.ffn_fmt)
+    sh_gate = ops.KQuantProjWeight(lw.sh_gu[0], lw.sh_gu[1], cfg.ffn_fmt)
+    sh_down = ops.KQuantProjWeight(lw.sh_dn[0], lw.sh_dn[1], cfg.ffn_fmt)
+    ops.inference_moe(y, lw.router, gate, down, sh_gate, sh_down, out, mws)
+    # explicit path on the same rows
+    ws = torch.empty(ops.gemm_kquant_a_ws_bytes(T, H), dtype=torch.uint8, device="cuda")
+    ops.gemm_kquant_prepare_a(y, ws)
+    L.dense_gemv(L.WT_BF16, lw.router, y, m.router_logits, T, cfg.experts + 1, H)
+    L.moe_route_plan(m.router_logits, cfg.experts, cfg.topk, m.route_w, m.route_ids, m.shared_w,
+                     m.plan)
+    want = torch.empty_like(out)
+    L.moe_experts(cfg.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, m.plan, ws, m.route_w,
+                  m.shared_w, m.moe_act, m.pairs, m.shared_out, want, T, cfg.topk, cfg.experts, H,
+                  cfg.expert_ffn)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    # LM head on normalised rows
+    hs = torch.empty(ops.lm_head_scratch_bytes(T), dtype=torch.uint8, device="cuda")
+    logits = torch.empty(T, cfg.vocab, device="cuda")
+    ops.inference_head(y, m.lm_head, logits, hs)
+    ops.gemm_kquant_prepare_a(y, ws)
+    want_l = torch.empty_like(logits)
+    L.dense_gemv(L.WT_F16, m.lm_head, ws, want_l, T, cfg.vocab, H)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, want_l)
+
+
+def test_dense_mlp(gpu, geometry_of):
+    from snowllm_amd import layers as L
+    from snowllm_amd import ops
+    from snowllm_amd.verify import VerifyModel
+    cfg = tiny("dense")
+    geometry_of(cfg)
+    print("reference-signature MLP, tiny dense", flush=True)
+    m = VerifyModel(cfg, seed=10)
+    T, H, F = cfg.block, cfg.hidden, cfg.ffn
+    lw = m.layers[0]
+    x = (torch.randn(T, H, device="cuda") * .5).bfloat16()
+    out = torch.empty(T, H, dtype=torch.bfloat16, device="cuda")
+    scratch = torch.empty(ops.mlp_workspace_bytes(T), dtype=torch.uint8, device="cuda")
+    ops.inference_mlp(x, ops.KQuantProjWeight(lw.gu[0], lw.gu[1], cfg.ffn_fmt),
+                      ops.KQuantProjWeight(lw.dn[0], lw.dn[1], cfg.ffn_fmt), out, scratch, True)
+    ws = torch.empty(ops.gemm_kquant_a_ws_bytes(T, H), dtype=torch.uint8, device="cuda")
+    ops.gemm_kquant_prepare_a(x, ws)
+    act = torch.empty(T, F, dtype=torch.bfloat16, device="cuda")
+    L.gate_up_swiglu(cfg.ffn_fmt, lw.gu[0], lw.gu[1], ws, act, T, F, H)
+    want = torch.empty_like(out)
+    ws2 = torch.empty(ops.gemm_kquant_a_ws_bytes(T, F), dtype=torch.uint8, device="cuda")
+    ops.gemm_kquant_a(cfg.ffn_fmt, act, lw.dn[0], lw.dn[1], want, T, H, F, ws2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+
+
+def test_unsupported_features_are_refused(gpu, geometry_of):
+    """Features outside the verify path return hipErrorNotSupported, not a wrong answer."""
+    from snowllm_amd import ops
+    from snowllm_amd._capi import SnowLLMError
+    cfg = tiny("moe")
+    geometry_of(cfg)
+    with pytest.raises(SnowLLMError):
+        ops.attn_output_plan(9, False, True)  # int8 KV
+    assert ops.attn_output_gating(torch.empty(9, 8, dtype=torch.bfloat16, device="cuda"),
+                                  False, False)[0] == 0
+    assert ops.paged_attention_varlen(True, 9, False) and not ops.paged_attention_varlen(False, 9, False)
