@@ -380,17 +380,31 @@ int g_pages_per_split = 0;  // 0: automatic
 // Pages per split (measured on MI355X): short contexts want ~384 workgroups of at least six
 // pages (more splits cost more partials than they gain); long contexts ~216 workgroups, one
 // per CU, since the partials are then negligible and longer splits pipeline better.
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+                   ? n : 256;
+  }
+  return cus[dev];
+}
+
+// A workgroup's time grows with its pages (measured on MI355X: about 1.2 us per page at
+// head_size 256), and one workgroup per CU runs best, so the splits are sized for one round of
+// workgroups over the CUs: the fewest pages per split that keep batch * Hkv * splits <= CUs.
+// Very short contexts keep at least 5 pages per split (more splits only add merge work).
 int choose_pages_per_split(int64_t batch, int Hkv, int64_t pages) {
   int64_t pps = g_pages_per_split;
   if (pps <= 0) {
     const int64_t heads = batch * Hkv;
-    int64_t target = (384 + heads - 1) / heads;
-    pps = (pages + target - 1) / target;
-    if (pps >= 48) {
-      target = (216 + heads - 1) / heads;
-      pps = (pages + target - 1) / target;
-    }
-    if (pps < 6) pps = 6;
+    const int64_t cus = device_cus();
+    const int64_t splits = heads < cus ? cus / heads : 1;
+    pps = (pages + splits - 1) / splits;
+    if (pps < 5) pps = 5;
   }
   while ((pages + pps - 1) / pps > SPLITS_MAX) ++pps;
   return (int)pps;
