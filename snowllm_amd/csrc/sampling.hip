@@ -405,17 +405,26 @@ template <typename W>
 __device__ uint32_t count_in_chunk(const W& w, int64_t n, int c, uint64_t base, uint64_t target,
                                    uint64_t* buf, uint64_t* red) {
   const int64_t lo = (int64_t)c * CHUNK + (int64_t)threadIdx.x * RUN;
-  uint64_t run_sum = 0;
+  // every weight of the run first (clamped indices keep the loads unconditional, so they are
+  // all in flight together), then the two passes over registers
+  uint64_t f[RUN];
+#pragma unroll
   for (int j = 0; j < RUN; ++j) {
-    int64_t k = lo + j;
-    if (k < n) run_sum += canon_fix(w(k));
+    const int64_t k = lo + j;
+    f[j] = canon_fix(w(k < n ? k : n - 1));
+  }
+  uint64_t run_sum = 0;
+#pragma unroll
+  for (int j = 0; j < RUN; ++j) {
+    if (lo + j >= n) f[j] = 0;
+    run_sum += f[j];
   }
   uint64_t pre = base + block_exclusive_scan_u64<NT>(run_sum, buf);
   uint32_t cnt = 0;
+#pragma unroll
   for (int j = 0; j < RUN; ++j) {
-    int64_t k = lo + j;
-    if (k < n) {
-      pre += canon_fix(w(k));
+    if (lo + j < n) {
+      pre += f[j];
       cnt += pre <= target;
     }
   }
@@ -525,12 +534,17 @@ struct ResidualRow {
   int64_t q_width;
   int64_t draft;        // draft token at `first` (used when q is null)
   bool subtract;        // false for the bonus position
+  const uint32_t* bits = nullptr;  // staged rows: bit (id mod 2^16) set for every candidate id
   __device__ float operator()(int64_t k) const {
     float pk = p[k];
     if (!subtract) return pk;
     const int64_t id = ids[k];
     float qk;
-    if (q) {
+    if (bits) {
+      // q(id) = 0 unless id may be a candidate; candidates are then searched exactly
+      const uint32_t h = (uint32_t)id & 0xffffu;
+      qk = ((bits[h >> 5] >> (h & 31)) & 1u) ? row_prob_thread(q, cand, q_width, id) : 0.0f;
+    } else if (q) {
       // identity layouts (ids[k] == k, cand[k] == k) resolve with loads independent of id
       const bool in_q = k < q_width;
       const float qd = in_q ? q[k] : 0.0f;
@@ -566,17 +580,55 @@ __device__ ResidualRow residual_row(const RejectArgs& a, int r, int64_t first) {
   return w;
 }
 
+// Short candidate rows (the selector's 16) are staged in LDS, so the per-element lookup of the
+// residual reads LDS instead of global memory. All threads call it.
+// They also get a 2^16-bit membership filter of their ids (id mod 2^16), so an element whose
+// id is not a candidate skips the search: q(id) = 0 and the residual is p.
+constexpr int Q_STAGE = 64;
+constexpr int Q_BITS_WORDS = 65536 / 32;
+__device__ __forceinline__ void stage_q(ResidualRow& w, int64_t* s_cand, float* s_q,
+                                        uint32_t* s_bits) {
+  const bool stage = w.subtract && w.q && w.q_width <= Q_STAGE;
+  if (stage) {
+    for (int i = threadIdx.x; i < Q_BITS_WORDS; i += blockDim.x) s_bits[i] = 0u;
+    for (int i = threadIdx.x; i < w.q_width; i += blockDim.x) {
+      s_cand[i] = w.cand[i];
+      s_q[i] = w.q[i];
+    }
+  }
+  __syncthreads();
+  if (stage) {
+    for (int i = threadIdx.x; i < w.q_width; i += blockDim.x) {
+      const uint32_t h = (uint32_t)s_cand[i] & 0xffffu;
+      atomicOr(&s_bits[h >> 5], 1u << (h & 31));
+    }
+  }
+  __syncthreads();
+  if (stage) {
+    w.cand = s_cand;
+    w.q = s_q;
+    w.bits = s_bits;
+  }
+}
+
 __global__ void __launch_bounds__(NT) reject_chunks(RejectArgs a, int C) {
   __shared__ uint64_t red[NT / WAVE];
+  __shared__ int64_t s_cand[Q_STAGE];
+  __shared__ float s_q[Q_STAGE];
+  __shared__ uint32_t s_bits[Q_BITS_WORDS];
   const int c = blockIdx.x, r = blockIdx.y;
   const int64_t first = g_first[r];
   ResidualRow w = residual_row(a, r, first);
+  stage_q(w, s_cand, s_q, s_bits);
   uint64_t rs = 0, ps = 0;
+#pragma unroll
   for (int k = 0; k < RUN; ++k) {
-    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    const int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    const int64_t ii = i < a.p_width ? i : a.p_width - 1;  // loads stay unconditional
+    const uint64_t r1 = canon_fix(w(ii)), p1 = canon_fix(w.p[ii]);
     if (i < a.p_width) {
-      rs += canon_fix(w(i));
-      ps += canon_fix(w.p[i]);
+      rs += r1;
+      ps += p1;
     }
   }
   rs = block_sum_u64<NT>(rs, red);
@@ -594,6 +646,9 @@ __global__ void __launch_bounds__(NT) reject_pick(RejectArgs a, int C) {
   __shared__ uint64_t s_base, s_target;
   __shared__ int s_use_p;
   __shared__ uint64_t s_sums[CHUNKS_MAX][2];
+  __shared__ int64_t s_cand[Q_STAGE];
+  __shared__ float s_q[Q_STAGE];
+  __shared__ uint32_t s_bits[Q_BITS_WORDS];
   const int r = blockIdx.x;
   const int64_t first = g_first[r];
   for (int i = threadIdx.x; i < 2 * C; i += NT)
@@ -627,6 +682,7 @@ __global__ void __launch_bounds__(NT) reject_pick(RejectArgs a, int C) {
   } else {
     ResidualRow w = residual_row(a, r, first);
     if (s_use_p) w.subtract = false;
+    stage_q(w, s_cand, s_q, s_bits);
     uint32_t cnt = count_in_chunk(w, a.p_width, s_chunk, s_base, s_target, buf, red);
     pick = (int64_t)s_chunk * CHUNK + cnt;
     if (pick > a.p_width - 1) pick = a.p_width - 1;
