@@ -177,6 +177,25 @@ int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_
                                int64_t table_stride, float scale, void* scratch,
                                int64_t scratch_bytes, void* stream);
 
+/* Extension, no counterpart in the reference (which runs snowllm_qk_norm_rope_cache, then
+ * snowllm_paged_attention): both in the attention's launches. Its workgroups normalise and
+ * rotate their query rows from the raw projection rows, and the workgroup whose split holds a
+ * block row's cache position writes that row's K (normalised, rotated) and V into the pools
+ * first -- the same bits as the separate writer. proj [batch*tokens, proj_stride] bf16 (q head
+ * hq at hq * q_head_stride, k / v head h at k_off / v_off + h * head_size); cos/sin rows
+ * cs_stride apart (first `half` used, half a multiple of 32); slots [batch*tokens] the cache
+ * slot of each block row (position lens[b] - tokens + t); q_out [batch*tokens, Hq, D] or NULL. */
+int snowverify_paged_attention_qk(const void* proj, int64_t proj_stride, int64_t q_head_stride,
+                                  int64_t k_off, int64_t v_off, const void* q_gamma,
+                                  const void* k_gamma, const float* cos_in, const float* sin_in,
+                                  int64_t cs_stride, int64_t half, float eps,
+                                  const int32_t* slots, void* q_out, void* k_pool, void* v_pool,
+                                  void* out, const int32_t* table, const int32_t* lens,
+                                  const uint64_t* tree, int64_t batch, int64_t tokens,
+                                  int64_t num_heads, int64_t num_kv_heads, int64_t head_size,
+                                  int64_t page_size, int64_t table_stride, float scale,
+                                  void* scratch, int64_t scratch_bytes, void* stream);
+
 /* Extension, no counterpart in the reference (a tuning knob): pages per context split of
  * snowverify_paged_attention; 0 = automatic. Returns the previous value. */
 int snowverify_attention_pages_per_split(int pages);
@@ -310,7 +329,7 @@ int snowllm_qk_norm_rope_cache(const void* proj, int64_t n, const void* kp, int6
                                const void* v_scale, const int32_t* slots, int64_t m, float eps,
                                int64_t block_size, void* stream);
 /* Extension: the same with explicit shapes: proj [M, stride] = q|k|v bf16 -> q_out [M, Hq, D];
- * cos/sin [M, half]. D <= 256. */
+ * cos/sin [M, half]. D in {64, 128, 256}; half a multiple of 32 with 2 half <= D. */
 int snowverify_qk_norm_rope_cache(const void* proj, int64_t stride, const void* q_gamma,
                                   const void* k_gamma, const float* cos_in, const float* sin_in,
                                   void* q_out, void* k_pool, void* v_pool, const int32_t* slots,

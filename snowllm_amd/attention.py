@@ -58,6 +58,43 @@ def paged_attention_explicit(q, k_pool, v_pool, out, table, lens, scale, scratch
                                          _stream()), "paged_attention")
 
 
+# Widest rotation (pairs per head) the fused QK-norm attention takes; wider ones run the
+# standalone writer first (the kernel refuses them with hipErrorNotSupported).
+FUSED_QK_MAX_HALF = 64
+
+
+def paged_attention_qk(proj, q_gamma, k_gamma, cos, sin, eps, slots, k_pool, v_pool, out, table,
+                       lens, scale, scratch, *, num_heads, num_kv_heads, tree=None, q_out=None):
+    """QK-norm + RoPE + the block's K/V write fused into the attention (extension): proj
+    [batch*T, n] bf16 = [q heads | k heads | v heads] (head size d); cos/sin [batch*T, half]
+    f32; slots int32 [batch*T]. Same bits as qk_norm_rope_cache followed by
+    paged_attention_explicit; q_out receives the rotated q if given. half <= FUSED_QK_MAX_HALF."""
+    batch = lens.numel()
+    M, n = proj.shape
+    D = out.shape[2]
+    T = M // batch
+    _chk(proj, "projection", torch.bfloat16, M, n)
+    _chk(out, "attention output", torch.bfloat16, M, num_heads, D)
+    _chk(cos, "cos", torch.float32, M, cos.shape[1])
+    _chk(sin, "sin", torch.float32, M, cos.shape[1])
+    _chk(slots, "slot mapping", torch.int32, M)
+    _chk(table, "attention block table", torch.int32, batch, table.shape[1])
+    _chk(lens, "attention sequence lengths", torch.int32, batch)
+    if q_out is not None:
+        _chk(q_out, "q", torch.bfloat16, M, num_heads, D)
+    if tree is not None:
+        _chk(tree, "tree masks", torch.int64, M)
+    need = paged_attention_explicit_scratch_bytes(batch, T, num_heads, num_kv_heads, D)
+    if scratch is None or scratch.nbytes < need:
+        raise SnowLLMError(f"paged attention needs {need} scratch bytes")
+    check(lib.snowverify_paged_attention_qk(
+        _p(proj), n, D, num_heads * D, (num_heads + num_kv_heads) * D, _p(q_gamma), _p(k_gamma),
+        _p(cos), _p(sin), cos.shape[1], cos.shape[1], eps, _p(slots), _p(q_out), _p(k_pool),
+        _p(v_pool), _p(out), _p(table), _p(lens), _p(tree), batch, T, num_heads, num_kv_heads, D,
+        PAGE, table.shape[1], float(scale), _p(scratch), scratch.nbytes, _stream()),
+        "paged_attention_qk")
+
+
 # ---------------------------------------------------------------------------------------
 # Geometry-driven forms with the reference's signatures (snowllm/ops/attention_full.py)
 # ---------------------------------------------------------------------------------------

@@ -25,6 +25,7 @@
 // group); rows >= T*G are padding. Row t of request b sees context keys [0, L - T) and block
 // key j (position L - T + j) iff bit j of its ancestor mask is set (causal: j <= t).
 #include "common.h"
+#include "qknorm.h"
 
 namespace {
 
@@ -41,6 +42,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int SPLITS_MAX = 512;
 constexpr int MAX_TILES = 8;     // row tiles per workgroup: T * G <= 128
 constexpr int MAX_TILES_DH = 4;  // up to 4 tiles, each tile's output columns split over 2 waves
+// The fused QK-norm form rotates at most 128 dims of a head (half <= 64): wider rotations of a
+// 256-wide head would not fit the kernel's registers, and the entry point refuses them.
+constexpr int FUSED_MAX_HS = 2;
 
 struct AttnArgs {
   const uint16_t* q;        // [batch*T, Hq, D]
@@ -53,6 +57,21 @@ struct AttnArgs {
   float* part_ml;           // [batch, Hkv, NRT, S, 16, 2]
   int T, Hq, Hkv, G, NRT, S, pages_per_split, table_stride;
   float qk_scale;           // softmax scale * log2(e)
+  // QK-norm + RoPE + the block's K/V write done here (proj != null): q head hq of block row m
+  // at proj + m * proj_stride + hq * q_head_stride, k / v head h at k_off / v_off + h * D;
+  // cos/sin rows cs_stride apart; slots [batch*T] the rows' cache slots; q_out optional.
+  const uint16_t* proj;
+  int64_t proj_stride, q_head_stride, k_off, v_off, cs_stride;
+  const uint16_t* q_gamma;
+  const uint16_t* k_gamma;
+  const float* cosv;
+  const float* sinv;
+  const int32_t* slots;
+  uint16_t* q_out;
+  uint16_t* k_pool_w;
+  uint16_t* v_pool_w;
+  int rot_half;
+  float eps;
 };
 
 // LDS image of one (page, kv head): K as in HBM, then V with its four key groups padded apart
@@ -244,21 +263,56 @@ attn_split_kernel(AttnArgs a) {
   else anc = (t >= 63) ? ~0ull : ((2ull << t) - 1ull);
 
   AttnState<D, DH> st;
+  // set just before the first chunk, so the accumulators are not live across the prologue
+  auto init_state = [&]() {
 #pragma unroll
-  for (int i = 0; i < DT; ++i) st.o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-  st.m = -__builtin_huge_valf();
-  st.l = 0.f;
+    for (int i = 0; i < DT; ++i) st.o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    st.m = -__builtin_huge_valf();
+    st.l = 0.f;
+  };
 
   if (p0 < p1) {  // uniform over the workgroup
-    // Q^T operand (8 consecutive d per k-step), loaded before the page loads are queued
+    // Q^T operand (8 consecutive d per k-step), loaded before the page loads are queued; the
+    // fused form fetches the raw projection row and its norm operands here and normalises the
+    // row once the first pages are on their way
     bf16x8 qb[DS];
-    {
-      const uint16_t* qrow = a.q + (((int64_t)b * a.T + t) * a.Hq + hq) * D;
+    QkRaw<D> qraw;
+    QkAux<D> qaux;
+    const int64_t m_row = (int64_t)b * a.T + t;
+    if (a.proj) {
+      // the block rows whose cache position falls in this split: K normalised and rotated,
+      // K and V into the pools (wave 0, 16 rows per pass)
+      const int t_lo = p0 * PAGE - ctx > 0 ? p0 * PAGE - ctx : 0;
+      const int t_hi = p1 * PAGE - ctx < a.T ? p1 * PAGE - ctx : a.T;
+      if (t_lo < t_hi) {  // uniform: this split holds block rows
+        if (wv == 0)
+          for (int t0 = t_lo; t0 < t_hi; t0 += 16) {
+            const int tr = t0 + col;
+            const bool live = tr < t_hi;
+            const int64_t m = (int64_t)b * a.T + (live ? tr : t_lo);
+            uint4 kr[DS];
+            qk_load_norm_rope<D, FUSED_MAX_HS>(a.proj + m * a.proj_stride + a.k_off + (int64_t)h * D, live,
+                                 a.k_gamma, a.cosv + m * a.cs_stride, a.sinv + m * a.cs_stride,
+                                 a.rot_half, a.eps, kq, kr);
+            if (live)
+              qk_store_kv<D>(kr, a.proj + m * a.proj_stride + a.v_off + (int64_t)h * D,
+                             a.k_pool_w, a.v_pool_w, a.slots[m], h, a.Hkv, PAGE, kq);
+          }
+        wait_vmcnt<0>();  // the block's K/V stores are done ...
+        block_barrier();  // ... before any wave queues a page load
+      }
+      qk_fetch<D>(qraw, a.proj + m_row * a.proj_stride + (int64_t)hq * a.q_head_stride, kq,
+                  row_live);
+      qk_fetch_aux<D>(qaux, a.q_gamma, a.cosv + m_row * a.cs_stride, a.sinv + m_row * a.cs_stride,
+                      a.rot_half, kq);
+    } else {
+      const uint16_t* qrow = a.q + (m_row * a.Hq + hq) * D;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
         if (row_live) qb[ds] = load_bf16x8(qrow + ds * 32 + kq * 8);
         else qb[ds] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
       }
+      wait_vmcnt<0>();  // Q has landed: the loop below then waits on page loads only
     }
     const int64_t page_bytes = (int64_t)G::KBYTES;
     const int64_t block_bytes = page_bytes * a.Hkv;
@@ -273,10 +327,25 @@ attn_split_kernel(AttnArgs a) {
       dma_page<D, CPW>(kbase + blk * block_bytes, vbase + blk * block_bytes,
                        ring + slot_idx * G::BYTES, wv, NW, lane);
     };
-    wait_vmcnt<0>();  // Q has landed: the loop below then waits on page loads only
     // pages go two per step (one 32-key chunk); RING - 2 pages are queued ahead of a step
 #pragma unroll
     for (int i = 0; i < RING - 2; ++i) issue(p0 + i, i);
+    if (a.proj) {
+      // this lane's query row, normalised and rotated while the first pages load (angles of
+      // sub-blocks past the first, when half > 32, load here behind the pages)
+      uint4 qo[DS];
+      qk_norm_rope<D, FUSED_MAX_HS>(qraw, qaux, a.cosv + m_row * a.cs_stride, a.sinv + m_row * a.cs_stride,
+                      a.rot_half, a.eps, kq, qo);
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const uint4 o = qo[ds];
+        qb[ds] = row_live ? __builtin_bit_cast(bf16x8, u32x4{o.x, o.y, o.z, o.w})
+                          : __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+        if (a.q_out && split == 0 && dhalf == 0 && row_live)
+          *(uint4*)(a.q_out + (m_row * a.Hq + hq) * D + ds * 32 + kq * 8) = o;
+      }
+    }
+    init_state();
     int slot = 0;  // first ring slot of the current chunk (even)
     for (int pg = p0; pg < p1; pg += 2) {
       wait_vmcnt<(RING - 4) * CPW>();  // this wave's loads of pages pg, pg + 1 have landed
@@ -289,6 +358,8 @@ attn_split_kernel(AttnArgs a) {
       slot = slot == RING - 2 ? 0 : slot + 2;
     }
     wait_vmcnt<0>();  // no load may still target LDS when the workgroup retires
+  } else {
+    init_state();
   }
   // partial results: O^T lane holds row col, d = dt*16 + 4*kq + i
   const int64_t pidx = ((((int64_t)b * a.Hkv + h) * a.NRT + w) * a.S + split);
@@ -377,9 +448,6 @@ inline int n_row_tiles(int T, int G) { return (T * G + 15) / 16; }
 
 int g_pages_per_split = 0;  // 0: automatic
 
-// Pages per split (measured on MI355X): short contexts want ~384 workgroups of at least six
-// pages (more splits cost more partials than they gain); long contexts ~216 workgroups, one
-// per CU, since the partials are then negligible and longer splits pipeline better.
 // Compute units of the current device (queried once per device).
 int device_cus() {
   static int cus[64] = {0};
@@ -468,12 +536,14 @@ SV_API int64_t snowverify_paged_attention_scratch_bytes(int64_t batch, int64_t t
 // takes shapes at run time). q [batch*tokens, Hq, D] bf16; out same; table [batch, stride]
 // i32; lens [batch] i32 = context + tokens; tree [batch*tokens] u64 ancestor masks or null for
 // causal. The block's K/V must already be in the pools.
-SV_API int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_pool,
-                                      void* out, const int32_t* table, const int32_t* lens,
-                                      const uint64_t* tree, int64_t batch, int64_t tokens,
-                                      int64_t num_heads, int64_t num_kv_heads, int64_t head_size,
-                                      int64_t page_size, int64_t table_stride, float scale,
-                                      void* scratch, int64_t scratch_bytes, void* stream) {
+namespace {
+
+int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const void* v_pool,
+                         void* out, const int32_t* table, const int32_t* lens,
+                         const uint64_t* tree, int64_t batch, int64_t tokens, int64_t num_heads,
+                         int64_t num_kv_heads, int64_t head_size, int64_t page_size,
+                         int64_t table_stride, float scale, void* scratch, int64_t scratch_bytes,
+                         void* stream) {
   if (batch <= 0 || tokens <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
       page_size != PAGE || table_stride <= 0)
     return SV_EINVAL;
@@ -482,7 +552,6 @@ SV_API int snowverify_paged_attention(const void* q, const void* k_pool, const v
   if (scratch_bytes < snowverify_paged_attention_scratch_bytes(batch, tokens, num_heads,
                                                               num_kv_heads, head_size))
     return SV_EINVAL;
-  AttnArgs a;
   a.q = (const uint16_t*)q;
   a.k_pool = (const uint16_t*)k_pool;
   a.v_pool = (const uint16_t*)v_pool;
@@ -518,6 +587,65 @@ SV_API int snowverify_paged_attention(const void* q, const void* k_pool, const v
   }
   SV_CHECK_LAUNCH();
   return SV_OK;
+}
+
+}  // namespace
+
+SV_API int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_pool,
+                                      void* out, const int32_t* table, const int32_t* lens,
+                                      const uint64_t* tree, int64_t batch, int64_t tokens,
+                                      int64_t num_heads, int64_t num_kv_heads, int64_t head_size,
+                                      int64_t page_size, int64_t table_stride, float scale,
+                                      void* scratch, int64_t scratch_bytes, void* stream) {
+  AttnArgs a = {};
+  return paged_attention_impl(a, q, k_pool, v_pool, out, table, lens, tree, batch, tokens,
+                              num_heads, num_kv_heads, head_size, page_size, table_stride, scale,
+                              scratch, scratch_bytes, stream);
+}
+
+// Extension (no counterpart in the reference, which runs snowllm_qk_norm_rope_cache and then
+// snowllm_paged_attention): the two in one pair of launches. The attention's workgroups
+// normalise and rotate their own query rows from the raw projection rows, and the workgroup
+// whose split holds a block row's cache position writes that row's K (normalised, rotated) and
+// V into the pools before loading its pages -- the same bits as the separate writer
+// (qknorm.h). proj [batch*tokens, proj_stride] bf16 with q head hq at hq * q_head_stride, k / v
+// head h at k_off / v_off + h * head_size; cos/sin [batch*tokens, cs_stride] f32 (first `half`
+// used; half a multiple of 32, at most 64: wider rotations return hipErrorNotSupported);
+// slots [batch*tokens] the cache slot of each block row (position lens[b] - tokens + t, as
+// snowllm_resolve_slots gives it); q_out [batch*tokens, Hq, D] or NULL. Other arguments as
+// snowverify_paged_attention.
+SV_API int snowverify_paged_attention_qk(
+    const void* proj, int64_t proj_stride, int64_t q_head_stride, int64_t k_off, int64_t v_off,
+    const void* q_gamma, const void* k_gamma, const float* cos_in, const float* sin_in,
+    int64_t cs_stride, int64_t half, float eps, const int32_t* slots, void* q_out, void* k_pool,
+    void* v_pool, void* out, const int32_t* table, const int32_t* lens, const uint64_t* tree,
+    int64_t batch, int64_t tokens, int64_t num_heads, int64_t num_kv_heads, int64_t head_size,
+    int64_t page_size, int64_t table_stride, float scale, void* scratch, int64_t scratch_bytes,
+    void* stream) {
+  if (!proj || !q_gamma || !k_gamma || !cos_in || !sin_in || !slots || half < 0 || half % 32 ||
+      2 * half > head_size || proj_stride % 8 || q_head_stride % 8 || k_off % 8 || v_off % 8)
+    return SV_EINVAL;
+  if (half > 32 * FUSED_MAX_HS) return SV_ENOTSUP;
+  AttnArgs a = {};
+  a.proj = (const uint16_t*)proj;
+  a.proj_stride = proj_stride;
+  a.q_head_stride = q_head_stride;
+  a.k_off = k_off;
+  a.v_off = v_off;
+  a.cs_stride = cs_stride;
+  a.q_gamma = (const uint16_t*)q_gamma;
+  a.k_gamma = (const uint16_t*)k_gamma;
+  a.cosv = cos_in;
+  a.sinv = sin_in;
+  a.slots = slots;
+  a.q_out = (uint16_t*)q_out;
+  a.k_pool_w = (uint16_t*)k_pool;
+  a.v_pool_w = (uint16_t*)v_pool;
+  a.rot_half = (int)half;
+  a.eps = eps;
+  return paged_attention_impl(a, nullptr, k_pool, v_pool, out, table, lens, tree, batch, tokens,
+                              num_heads, num_kv_heads, head_size, page_size, table_stride, scale,
+                              scratch, scratch_bytes, stream);
 }
 
 // Tuning knob (extension, no reference counterpart): pages per split of the attention's

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include "geometry.h"
+#include "qknorm.h"
 
 namespace {
 
@@ -120,12 +121,11 @@ __global__ void rope_cos_sin_kernel(const int64_t* __restrict__ pos,
 }
 
 // ---------------------------------------------------------------------------------------
-// QK-norm + RoPE + paged KV write. proj row m = [q heads | k heads | v heads] (bf16, head
-// size D, row stride `stride`). Per head: RMSNorm over D with its gamma (fp32), rotate the first
-// 2*half dims (pairs (i, i + half)), round once to bf16 (tests/test_lfm2_dspark_reference.py:
-// 22-27 order). q goes to q_out [M, Hq, D]; k and v go to the pools at slots[m] in the layouts
-// K [blocks, Hkv, D/16, page, 16] and V [blocks, Hkv, page/4, D, 4].
-// One wave per (row, head); heads >= Hq + Hkv copy v.
+// QK-norm + RoPE + paged KV write. Per head: RMSNorm over D with its gamma (fp32), rotate the
+// first 2*half dims (pairs (i, i + half)), round once to bf16 (qknorm.h). q goes to q_out
+// [M, Hq, D]; k and v go to the pools at slots[m] in the layouts K [blocks, Hkv, D/16, page, 16]
+// and V [blocks, Hkv, page/4, D, 4]. One wave per (16 rows, head); a kv head's wave writes both
+// its K and V rows.
 // ---------------------------------------------------------------------------------------
 // Sources of one row's heads: q head h at q + m * q_stride + h * q_head_stride, k head h at
 // k + m * k_stride + h * D, v head h at v + m * v_stride + h * D; cos/sin rows cs_stride apart
@@ -137,75 +137,35 @@ struct QkvSources {
   int64_t q_stride, q_head_stride, k_stride, v_stride, cs_stride;
 };
 
+template <int D>
 __global__ void __launch_bounds__(64) qk_norm_rope_cache_kernel(
-    QkvSources src_, const uint16_t* __restrict__ q_gamma, const uint16_t* __restrict__ k_gamma,
+    QkvSources src, const uint16_t* __restrict__ q_gamma, const uint16_t* __restrict__ k_gamma,
     const float* __restrict__ cosv, const float* __restrict__ sinv, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
-    const int32_t* __restrict__ slots, int Hq, int Hkv, int D, int half, int page, float eps) {
-  const int64_t m = blockIdx.y;
+    const int32_t* __restrict__ slots, int64_t M, int Hq, int Hkv, int half, int page, float eps) {
   const int head = blockIdx.x;
-  const int lane = threadIdx.x;
-  const uint16_t* src =
-      head < Hq ? src_.q + m * src_.q_stride + (int64_t)head * src_.q_head_stride
-      : head < Hq + Hkv ? src_.k + m * src_.k_stride + (int64_t)(head - Hq) * D
-                        : src_.v + m * src_.v_stride + (int64_t)(head - Hq - Hkv) * D;
-  const int slot = slots[m];
-  const int blk = slot / page, off = slot % page;
-  if (head >= Hq + Hkv) {  // v
-    const int h = head - Hq - Hkv;
-    for (int d = lane; d < D; d += 64) {
-      if (slot < 0) break;
-      // V [blocks, Hkv, page/4, D, 4]
-      const int64_t idx = ((((int64_t)blk * Hkv + h) * (page / 4) + off / 4) * D + d) * 4 + off % 4;
-      v_pool[idx] = src[d];
-    }
+  const int lane = threadIdx.x, col = lane & 15, kq = lane >> 4;
+  const int64_t m = (int64_t)blockIdx.y * 16 + col;
+  const bool live = m < M;
+  const int64_t mr = live ? m : 0;
+  const float* cr = cosv + mr * src.cs_stride;
+  const float* sr = sinv + mr * src.cs_stride;
+  uint4 o[D / 32];
+  if (head < Hq) {
+    qk_load_norm_rope<D>(src.q + mr * src.q_stride + (int64_t)head * src.q_head_stride, live,
+                         q_gamma, cr, sr, half, eps, kq, o);
+    if (live)
+#pragma unroll
+      for (int ds = 0; ds < D / 32; ++ds)
+        *(uint4*)(q_out + (m * Hq + head) * D + ds * 32 + kq * 8) = o[ds];
     return;
   }
-  const bool is_q = head < Hq;
-  const uint16_t* gamma = is_q ? q_gamma : k_gamma;
-  // D <= 256: each lane holds up to 4 values
-  float v[4];
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int d = lane + 64 * j;
-    v[j] = d < D ? bf16_to_f32(src[d]) : 0.f;
-    ss = __builtin_fmaf(v[j], v[j], ss);
-  }
-  ss = wave_sum(ss);
-  const float inv = __frsqrt_rn(ss / (float)D + eps);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int d = lane + 64 * j;
-    if (d < D) v[j] = v[j] * inv * bf16_to_f32(gamma[d]);
-  }
-  // rotate: partner of d < half is d + half and vice versa. Exchange through LDS.
-  __shared__ float buf[256];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int d = lane + 64 * j;
-    if (d < D) buf[d] = v[j];
-  }
-  __syncthreads();
-  const float* cr = cosv + m * src_.cs_stride;
-  const float* sr = sinv + m * src_.cs_stride;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int d = lane + 64 * j;
-    if (d >= D) continue;
-    float y = v[j];
-    if (d < half) y = v[j] * cr[d] - buf[d + half] * sr[d];
-    else if (d < 2 * half) y = v[j] * cr[d - half] + buf[d - half] * sr[d - half];
-    const uint16_t o = f32_to_bf16(y);
-    if (is_q) {
-      q_out[(m * Hq + head) * D + d] = o;
-    } else if (slot >= 0) {
-      const int h = head - Hq;
-      // K [blocks, Hkv, D/16, page, 16]
-      const int64_t idx = ((((int64_t)blk * Hkv + h) * (D / 16) + d / 16) * page + off) * 16 + d % 16;
-      k_pool[idx] = o;
-    }
-  }
+  const int h = head - Hq;
+  qk_load_norm_rope<D>(src.k + mr * src.k_stride + (int64_t)h * D, live, k_gamma, cr, sr, half,
+                       eps, kq, o);
+  if (live)
+    qk_store_kv<D>(o, src.v + m * src.v_stride + (int64_t)h * D, k_pool, v_pool, slots[m], h, Hkv,
+                   page, kq);
 }
 
 // The reference's rotary geometry: rotary dimension 64 (head_size x partial_rotary_factor,
@@ -217,10 +177,14 @@ int launch_qk_norm_rope_cache(const QkvSources& src, const void* q_gamma, const 
                               void* v_pool, const int32_t* slots, int64_t M, int64_t Hq,
                               int64_t Hkv, int64_t D, int64_t half, int64_t page, float eps,
                               hipStream_t s) {
-  hipLaunchKernelGGL(qk_norm_rope_cache_kernel, dim3((unsigned)(Hq + 2 * Hkv), (unsigned)M),
-                     dim3(64), 0, s, src, (const uint16_t*)q_gamma, (const uint16_t*)k_gamma,
-                     cosv, sinv, (uint16_t*)q_out, (uint16_t*)k_pool, (uint16_t*)v_pool, slots,
-                     (int)Hq, (int)Hkv, (int)D, (int)half, (int)page, eps);
+  if (half < 0 || half % 32 || 2 * half > D) return SV_EINVAL;
+  const dim3 grid((unsigned)(Hq + Hkv), (unsigned)((M + 15) / 16));
+  auto kern = D == 64 ? qk_norm_rope_cache_kernel<64>
+            : D == 128 ? qk_norm_rope_cache_kernel<128> : qk_norm_rope_cache_kernel<256>;
+  if (D != 64 && D != 128 && D != 256) return SV_EINVAL;
+  hipLaunchKernelGGL(kern, grid, dim3(64), 0, s, src, (const uint16_t*)q_gamma,
+                     (const uint16_t*)k_gamma, cosv, sinv, (uint16_t*)q_out, (uint16_t*)k_pool,
+                     (uint16_t*)v_pool, slots, M, (int)Hq, (int)Hkv, (int)half, (int)page, eps);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -373,15 +337,16 @@ SV_API int snowllm_rope_cos_sin(const int64_t* pos, const float* inv_freq, float
 // Extension: QK-norm + RoPE + paged KV write with explicit shapes (the reference's
 // snowllm_qk_norm_rope_cache, snowllm/_capi.py:397-399 and ops/attention_full.py:736-784,
 // takes them from the geometry). proj [M, stride] bf16 = [q | k | v]; q_out [M, Hq, D];
-// cos/sin [M, half]; slots [M] (negative: do not cache). D <= 256, D % 16 == 0.
+// cos/sin [M, half]; slots [M] (negative: do not cache). D in {64, 128, 256}; half a multiple
+// of 32 with 2 half <= D.
 SV_API int snowverify_qk_norm_rope_cache(const void* proj, int64_t stride, const void* q_gamma,
                                          const void* k_gamma, const float* cosv, const float* sinv,
                                          void* q_out, void* k_pool, void* v_pool,
                                          const int32_t* slots, int64_t M, int64_t Hq, int64_t Hkv,
                                          int64_t D, int64_t half, int64_t page, float eps,
                                          void* stream) {
-  if (M < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || D > 256 || D % 16 || 2 * half > D || half < 0 ||
-      page != 16)
+  if (M < 0 || Hq <= 0 || Hkv <= 0 || (D != 64 && D != 128 && D != 256) || half % 32 ||
+      2 * half > D || half < 0 || page != 16)
     return SV_EINVAL;
   if (M == 0) return SV_OK;
   const uint16_t* p = (const uint16_t*)proj;
@@ -405,7 +370,7 @@ SV_API int snowllm_qk_norm_rope_cache(const void* proj, int64_t n, const void* k
   const BuildGeometry& g = g_geo;
   if (block_size != g.block_size) return SV_EINVAL;
   const int64_t D = g.head_size, Hq = g.num_heads, Hkv = g.num_kv_heads;
-  if (m < 0 || D <= 0 || D > 256 || D % 16 || block_size != 16) return SV_EINVAL;
+  if (m < 0 || (D != 64 && D != 128 && D != 256) || block_size != 16) return SV_EINVAL;
   if (m == 0) return SV_OK;
   const QkvSources src{(const uint16_t*)proj, (const uint16_t*)kp, (const uint16_t*)v, n,
                        g.qkv_q_head_stride, ks, vs, 2 * REF_ROPE_HALF};

@@ -8,7 +8,8 @@ from .gemm import (Q4_K, Q8_0, gemm_kquant_a, gemm_kquant_a_ws_bytes,  # noqa: F
                    gemm_kquant_shuffle_b, kquant_bytes,
                    gemm_kquant_prepare_a, gemm_kquant_a_prepared)
 from .attention import (kv_pool_bytes, paged_attention_explicit,  # noqa: F401
-                        paged_attention_explicit_scratch_bytes, paged_attention,
+                        paged_attention_explicit_scratch_bytes, paged_attention, paged_attention_qk,
+                        FUSED_QK_MAX_HALF,
                         paged_attention_scratch_bytes, paged_attention_varlen, attn_output_plan,
                         attn_output_shape, attn_output_gating, attn_output_project, rope_cos_sin,
                         qk_norm_rope_cache)

@@ -311,11 +311,20 @@ class VerifyModel:
             norm(lw.in_norm, self.ws_h)
             ops.gemm_kquant_a_prepared(c.attn_fmt, lw.qkv[0], lw.qkv[1], self.proj, T, c.qkv_n, H,
                                        self.ws_h)
-            Lops.qk_norm_rope_cache(self.proj, lw.q_norm, lw.k_norm, self.cos, self.sin, self.q,
-                                    self.k_pools[i], self.v_pools[i], self.slots, c.eps)
-            ops.paged_attention_explicit(self.q, self.k_pools[i], self.v_pools[i], self.attn,
-                                         self.table, self.lens, c.head_dim ** -0.5,
-                                         self.attn_scratch, tree=self.tree)
+            if c.rot_half <= ops.FUSED_QK_MAX_HALF:
+                # QK-norm + RoPE + the block's K/V cache write inside the attention's launches
+                ops.paged_attention_qk(self.proj, lw.q_norm, lw.k_norm, self.cos, self.sin,
+                                       c.eps, self.slots, self.k_pools[i], self.v_pools[i],
+                                       self.attn, self.table, self.lens, c.head_dim ** -0.5,
+                                       self.attn_scratch, num_heads=c.heads,
+                                       num_kv_heads=c.kv_heads, tree=self.tree, q_out=self.q)
+            else:
+                Lops.qk_norm_rope_cache(self.proj, lw.q_norm, lw.k_norm, self.cos, self.sin,
+                                        self.q, self.k_pools[i], self.v_pools[i], self.slots,
+                                        c.eps)
+                ops.paged_attention_explicit(self.q, self.k_pools[i], self.v_pools[i], self.attn,
+                                             self.table, self.lens, c.head_dim ** -0.5,
+                                             self.attn_scratch, tree=self.tree)
             ops.gemm_kquant_a(c.attn_fmt, self.attn.view(T, -1), lw.o[0], lw.o[1], self.o, T, H,
                               c.heads * c.head_dim, self.ws_a)
             # feed-forward block

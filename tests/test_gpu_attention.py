@@ -87,3 +87,87 @@ def test_ragged_batches(lengths, T):
 
 def test_single_kv_head_d256_tree_batch():
     _case([300, 1201], 3, 4, 1, 256, seed=9, tree_parents=[-1, 0, 0])
+
+
+@pytest.mark.parametrize("lengths,T,Hq,Hkv,D,half,pps,tree", [
+    ([8192 + 9], 9, 16, 2, 256, 32, 0, False),      # config 4 shape
+    ([8190 + 9, 301 + 9], 9, 32, 8, 128, 64, 0, False),  # block rows over two pages
+    ([100 + 11], 11, 16, 2, 256, 32, 5, True),     # tree; splits of 5 pages
+    ([77 + 9], 9, 4, 2, 128, 32, 1, False),        # one page per split: rows over two splits
+    ([500 + 9], 9, 8, 2, 256, 64, 0, False),       # widest rotation the fused form takes
+])
+def test_fused_qk_attention_equals_separate_kernels(lengths, T, Hq, Hkv, D, half, pps, tree):
+    """QK-norm + RoPE + the block's K/V write inside the attention gives the same q, pools and
+    output bits as qk_norm_rope_cache followed by paged_attention_explicit."""
+    from snowllm_amd import layers as L, ops
+    from snowllm_amd._capi import lib
+    print(f"fused qk attention lengths={lengths} T={T} D={D} pps={pps} tree={tree}", flush=True)
+    g = torch.Generator().manual_seed(len(lengths) * 100 + D + pps)
+    batch = len(lengths)
+    pages = [(n + 15) // 16 for n in lengths]
+    total = sum(pages) + 5
+    perm = torch.randperm(total, generator=g).int()
+    width = max(pages)
+    table = torch.zeros(batch, width, dtype=torch.int32)
+    off = 0
+    for b in range(batch):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    kp0 = torch.randn(total, Hkv, D // 16, 16, 16, generator=g).bfloat16()
+    vp0 = torch.randn(total, Hkv, 4, D, 4, generator=g).bfloat16()
+    n = (Hq + 2 * Hkv) * D
+    proj = torch.randn(batch * T, n, generator=g).bfloat16()
+    qg = (torch.rand(D, generator=g) + .5).bfloat16()
+    kg = (torch.rand(D, generator=g) + .5).bfloat16()
+    pos = torch.cat([torch.arange(n - T, n) for n in lengths])
+    inv = 1.0 / (1e4 ** (torch.arange(half).float() / half))
+    ang = pos[:, None].float() * inv[None]
+    cos, sin = ang.cos(), ang.sin()
+    slots = torch.cat([(table[b, (torch.arange(n - T, n) // 16)] * 16 + torch.arange(n - T, n) % 16)
+                       for b, n in enumerate(lengths)]).int()
+    masks = tree_masks([-1, 0, 1, 2, 3, 4, 0, 6, 7, 8, 9]) if tree else None
+    tr = torch.tensor(to_i64(masks) * batch, dtype=torch.int64).cuda() if tree else None
+    lens = torch.tensor(lengths, dtype=torch.int32).cuda()
+    scratch = torch.empty(ops.paged_attention_explicit_scratch_bytes(batch, T, Hq, Hkv, D),
+                          dtype=torch.uint8, device="cuda")
+    dev = lambda x: x.cuda()
+    prev = lib.snowverify_attention_pages_per_split(pps)
+    try:
+        res = []
+        for fused in (False, True):
+            kp, vp = kp0.clone().cuda(), vp0.clone().cuda()
+            q = torch.zeros(batch * T, Hq, D, dtype=torch.bfloat16, device="cuda")
+            out = torch.empty_like(q)
+            if fused:
+                ops.paged_attention_qk(dev(proj), dev(qg), dev(kg), dev(cos), dev(sin), 1e-6,
+                                       dev(slots), kp, vp, out, dev(table), lens, D ** -0.5,
+                                       scratch, num_heads=Hq, num_kv_heads=Hkv, tree=tr, q_out=q)
+            else:
+                L.qk_norm_rope_cache(dev(proj), dev(qg), dev(kg), dev(cos), dev(sin), q, kp, vp,
+                                     dev(slots), 1e-6)
+                ops.paged_attention_explicit(q, kp, vp, out, dev(table), lens, D ** -0.5,
+                                             scratch, tree=tr)
+            torch.cuda.synchronize()
+            res.append((q, kp, vp, out))
+        for a, b in zip(*res):
+            assert torch.equal(a, b)
+    finally:
+        lib.snowverify_attention_pages_per_split(prev)
+
+
+def test_fused_qk_attention_refuses_wide_rotation():
+    """Rotations wider than FUSED_QK_MAX_HALF pairs are refused before any launch."""
+    from snowllm_amd import ops
+    from snowllm_amd._capi import SnowLLMError
+    T, Hq, Hkv, D, half = 9, 8, 2, 256, 96
+    assert half > ops.FUSED_QK_MAX_HALF
+    c = lambda *s, dt=torch.bfloat16: torch.zeros(*s, dtype=dt, device="cuda")
+    scratch = torch.empty(ops.paged_attention_explicit_scratch_bytes(1, T, Hq, Hkv, D),
+                          dtype=torch.uint8, device="cuda")
+    with pytest.raises(SnowLLMError):
+        ops.paged_attention_qk(c(T, (Hq + 2 * Hkv) * D), c(D), c(D), c(T, half, dt=torch.float32),
+                               c(T, half, dt=torch.float32), 1e-6, c(T, dt=torch.int32),
+                               c(2, Hkv, D // 16, 16, 16), c(2, Hkv, 4, D, 4), c(T, Hq, D),
+                               c(1, 2, dt=torch.int32),
+                               torch.tensor([T + 7], dtype=torch.int32, device="cuda"), D ** -0.5,
+                               scratch, num_heads=Hq, num_kv_heads=Hkv)
