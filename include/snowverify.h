@@ -183,7 +183,8 @@ int snowverify_paged_attention(const void* q, const void* k_pool, const void* v_
  * block row's cache position writes that row's K (normalised, rotated) and V into the pools
  * first -- the same bits as the separate writer. proj [batch*tokens, proj_stride] bf16 (q head
  * hq at hq * q_head_stride, k / v head h at k_off / v_off + h * head_size); cos/sin rows
- * cs_stride apart (first `half` used, half a multiple of 32); slots [batch*tokens] the cache
+ * cs_stride apart (first `half` used, half a multiple of 32 and at most 64, wider returns
+ * hipErrorNotSupported); slots [batch*tokens] the cache
  * slot of each block row (position lens[b] - tokens + t); q_out [batch*tokens, Hq, D] or NULL. */
 int snowverify_paged_attention_qk(const void* proj, int64_t proj_stride, int64_t q_head_stride,
                                   int64_t k_off, int64_t v_off, const void* q_gamma,
