@@ -23,7 +23,7 @@ def _mask(ctx, T, masks):
     return m
 
 
-def _case(lengths, T, Hq, Hkv, D, seed, tree_parents=None, extra_blocks=7):
+def _case(lengths, T, Hq, Hkv, D, seed, tree_parents=None, extra_blocks=7, v_scale=1.0):
     from snowllm_amd import ops
     g = torch.Generator().manual_seed(seed)
     batch = len(lengths)
@@ -40,7 +40,7 @@ def _case(lengths, T, Hq, Hkv, D, seed, tree_parents=None, extra_blocks=7):
         table[b, :pages[b]] = perm[off:off + pages[b]]
         off += pages[b]
         k = torch.randn(L, Hkv, D, generator=g).bfloat16()
-        v = torch.randn(L, Hkv, D, generator=g).bfloat16()
+        v = (torch.randn(L, Hkv, D, generator=g) * v_scale).bfloat16()
         kb, vb = pools_from_dense(k, v, table[b], total_blocks)
         used = table[b, :pages[b]].long()
         kp[used] = kb[used]
@@ -73,6 +73,13 @@ def test_config3_shape():
 
 def test_config4_shape():
     _case([8192 + 9], 9, 16, 2, 256, seed=5)
+
+
+@pytest.mark.parametrize("v_scale", [3e6, 1e-12])
+def test_value_magnitudes_outside_fp16(v_scale):
+    """The split partials are fp16 with a power-of-two scale per row: values far outside fp16's
+    range merge without overflow or flush."""
+    _case([2000 + 9], 9, 16, 2, 256, seed=7, v_scale=v_scale)
 
 
 def test_config5_tree_long_context():
