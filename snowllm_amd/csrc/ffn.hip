@@ -385,10 +385,37 @@ __global__ void __launch_bounds__(WS * PPB * 64) gate_up_kernel(
 // ---------------------------------------------------------------------------------------
 constexpr int ROUTE_THREADS = 1024;  // 16 waves: one per row (M <= 16), four for the plan
 
+// 64-bit maximum over the wave on the VALU: DPP within each 16-lane row, row broadcasts 15 and
+// 31 across rows, then lane 63 holds the result. No scalar round trips, no branches.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_u64_step(uint64_t v) {
+  const uint32_t h = (uint32_t)(v >> 32), l = (uint32_t)v;
+  const uint32_t nh = (uint32_t)__builtin_amdgcn_update_dpp((int)h, (int)h, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t nl = (uint32_t)__builtin_amdgcn_update_dpp((int)l, (int)l, CTRL, ROW_MASK, 0xF, false);
+  const uint64_t n = ((uint64_t)nh << 32) | nl;
+  return n > v ? n : v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
+  v = dpp_max_u64_step<DPP_QUAD_XOR1, 0xF>(v);
+  v = dpp_max_u64_step<DPP_QUAD_XOR2, 0xF>(v);
+  v = dpp_max_u64_step<DPP_HALF_MIRROR, 0xF>(v);
+  v = dpp_max_u64_step<DPP_MIRROR, 0xF>(v);
+  v = dpp_max_u64_step<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_max_u64_step<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  const uint32_t h = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  const uint32_t l = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  return ((uint64_t)h << 32) | l;
+}
+
+// Softmax over E <= 256 logits (expert e = lane + 64 i), then the top-k in descending order
+// with ties to the lower expert id: lane k ends with the k-th pick's probability and id. Each
+// lane sorts its four candidates once; a round takes the wave maximum of the lanes' heads as
+// (ordered key, ~expert id) and the winning lane drops its head.
 __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, int topk, int lane,
                                           float& my_p, int& my_id, float& ksum) {
   float v[4];
-  uint32_t key[4];  // ordered keys of the candidates left; 0 = taken or past E
+  uint32_t key[4];  // ordered keys; 0 = past E
+  uint32_t id[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = l[lane + 64 * i < E ? lane + 64 * i : 0];  // all in flight
 #pragma unroll
@@ -396,6 +423,7 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
     const int e = lane + 64 * i;
     v[i] = e < E ? v[i] : -__builtin_huge_valf();
     key[i] = e < E ? ord_key(v[i]) : 0u;
+    id[i] = (uint32_t)e;
   }
   uint32_t km = key[0] > key[1] ? key[0] : key[1];
   km = key[2] > km ? key[2] : km;
@@ -406,32 +434,34 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
   for (int i = 0; i < 4; ++i)
     if (lane + 64 * i < E) sum += __expf(v[i] - mx);
   sum = wave_sum_dpp(sum);
+  // sort the lane's candidates: key descending, then id ascending (a five-comparator network
+  // under that total order)
+  auto cswap = [&](int a, int b) {
+    const bool sw = key[b] > key[a] || (key[b] == key[a] && id[b] < id[a]);
+    const uint32_t ka = key[a], ia = id[a];
+    key[a] = sw ? key[b] : key[a];
+    id[a] = sw ? id[b] : id[a];
+    key[b] = sw ? ka : key[b];
+    id[b] = sw ? ia : id[b];
+  };
+  cswap(0, 1); cswap(2, 3); cswap(0, 2); cswap(1, 3); cswap(1, 2);
   my_p = 0.f;
   my_id = -1;
   for (int k = 0; k < topk; ++k) {
-    // largest key left, then the lowest expert id holding it (e = lane + 64 i: lowest i first)
-    uint32_t b = key[0] > key[1] ? key[0] : key[1];
-    b = key[2] > b ? key[2] : b;
-    b = key[3] > b ? key[3] : b;
-    b = wave_max_u32_dpp(b);
-    int e = -1;
-    float ve = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint64_t hit = __ballot(key[i] == b);
-      if (e < 0 && hit) {
-        e = 64 * i + (int)__builtin_ctzll(hit);
-        ve = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), e & 63));
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if ((e >> 6) == i && (e & 63) == lane) key[i] = 0u;
+    const uint64_t best = wave_max_u64_dpp(((uint64_t)key[0] << 32) | (0xffffffffu - id[0]));
+    const int e = (int)(0xffffffffu - (uint32_t)best);
+    const float ve = ord_key_to_float((uint32_t)(best >> 32));
+    const bool pop = lane == (e & 63);
+    key[0] = pop ? key[1] : key[0];
+    id[0] = pop ? id[1] : id[0];
+    key[1] = pop ? key[2] : key[1];
+    id[1] = pop ? id[2] : id[1];
+    key[2] = pop ? key[3] : key[2];
+    id[2] = pop ? id[3] : id[2];
+    key[3] = pop ? 0u : key[3];
     const float p = __expf(ve - mx) / sum;
-    if (lane == k) {
-      my_p = p;
-      my_id = e;
-    }
+    my_p = lane == k ? p : my_p;
+    my_id = lane == k ? e : my_id;
   }
   ksum = 0.f;
   for (int k = 0; k < topk; ++k)
