@@ -307,12 +307,11 @@ def bench_step(args, name):
     if cfg.moe:
         F = c.expert_ffn
         ns = T * c.topk + 1
-        per_launch("moe_gate_up", lambda i: Lops.moe_gate_up(
-            c.ffn_fmt, Lw[i].gu, Lw[i].sh_gu, m.plan, m.ws_h2, m.moe_act, T, ns, c.experts, H, F),
-            last_slots * q4k_bytes(2 * F, H))
-        per_launch("moe_down", lambda i: Lops.moe_down(
-            c.ffn_fmt, Lw[i].dn, Lw[i].sh_dn, m.plan, m.moe_act, m.route_w, m.shared_w, m.pairs,
-            m.shared_out, ns, c.experts, H, F), last_slots * q4k_bytes(H, F))
+        # the expert gate/up and down GEMVs: one launch (moe_experts_kernel)
+        per_launch("moe_experts", lambda i: Lops.moe_gate_up_down(
+            c.ffn_fmt, Lw[i].gu, Lw[i].dn, Lw[i].sh_gu, Lw[i].sh_dn, m.plan, m.ws_h2, m.route_w,
+            m.shared_w, m.moe_act, m.pairs, m.shared_out, T, ns, c.experts, H, F),
+            last_slots * (q4k_bytes(2 * F, H) + q4k_bytes(H, F)))
     else:
         per_launch("gate_up_swiglu", lambda i: Lops.gate_up_swiglu(
             c.ffn_fmt, Lw[i].gu[0], Lw[i].gu[1], m.ws_h2, m.act, T, c.ffn, H),

@@ -397,6 +397,20 @@ int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_meta,
                         const void* act, const float* weights, const float* shared_w,
                         float* pairs, float* shared_out, int64_t max_slots, int64_t E, int64_t H,
                         int64_t F, void* stream);
+/* Extension, no counterpart in the reference (whose expert stages are internal to
+ * snowllm_inference_moe): snowverify_moe_gate_up then snowverify_moe_down in one launch, same
+ * outputs and bits; a down item starts as soon as its slot's gate/up items are done. Uses
+ * library-owned counters, so calls on one device must be stream-ordered. */
+int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void* gu_meta,
+                                const void* dn_quant, const void* dn_meta,
+                                const void* sh_gu_quant, const void* sh_gu_meta,
+                                const void* sh_dn_quant, const void* sh_dn_meta, const void* plan,
+                                const void* ws, const float* weights, const float* shared_w,
+                                void* act, float* pairs, float* shared_out, int64_t M,
+                                int64_t max_slots, int64_t E, int64_t H, int64_t F, void* stream);
+/* Non-zero once a snowverify_moe_gate_up_down launch has timed out waiting for its own
+ * activations (never expected; reading it synchronises the device). */
+int snowverify_moe_sync_error(void);
 int snowverify_moe_combine(const float* pairs, const float* shared_out, void* out, int64_t M,
                            int64_t topk, int64_t H, void* stream);
 int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_meta,

@@ -145,6 +145,8 @@ _SIGS = [
     ("snowverify_moe_route_plan", c_int, [P, c_int64, c_int64, c_int64, c_int64, P, P, P, P, S]),
     ("snowverify_moe_gate_up", c_int, [c_int] + [P] * 7 + [c_int64] * 5 + [S]),
     ("snowverify_moe_down", c_int, [c_int] + [P] * 10 + [c_int64] * 4 + [S]),
+    ("snowverify_moe_gate_up_down", c_int, [c_int] + [P] * 15 + [c_int64] * 5 + [S]),
+    ("snowverify_moe_sync_error", c_int, []),
     ("snowverify_moe_combine", c_int, [P, P, P, c_int64, c_int64, c_int64, S]),
     ("snowverify_moe_experts", c_int, [c_int] + [P] * 16 + [c_int64] * 5 + [S]),
 ]

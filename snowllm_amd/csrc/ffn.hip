@@ -310,20 +310,22 @@ __device__ __forceinline__ void gather_rows(GemvStreams& st, const int32_t* rows
 // the slot's expert, rows gathered, act written compact at act_out + slot * 16 * F) or the
 // whole block (plan == null: rows 0..M-1 of x, act [M, F]).
 // ---------------------------------------------------------------------------------------
-template <int FMT, int WS, int PPB>
-__global__ void __launch_bounds__(WS * PPB * 64) gate_up_kernel(
-    const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t gu_qbytes,
-    int64_t gu_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
-    const MoePlan* __restrict__ plan, int E, const void* __restrict__ ws,
-    uint16_t* __restrict__ act_out, int M, int F, int S) {
+// bx: the block's pair group; slot: the plan slot (plan mode) or 0. DEVICE_SCOPE: the
+// activations are stored with device-scope stores (visible to other workgroups of the same
+// launch once the stores complete).
+template <int FMT, int WS, int PPB, bool DEVICE_SCOPE>
+__device__ __forceinline__ void gate_up_body(
+    int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
+    int64_t gu_qbytes, int64_t gu_mbytes, const uint8_t* __restrict__ sh_quant,
+    const uint8_t* __restrict__ sh_meta, const MoePlan* __restrict__ plan, int E,
+    const void* __restrict__ ws, uint16_t* __restrict__ act_out, int M, int F, int S) {
   __shared__ floatx4 part[PPB][WS][2][64];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int pl = wv / WS, sw = wv % WS;
   const int kq = lane >> 4;
-  const int slot = blockIdx.y;
   const int half_tiles = F / TILE_N;
-  const int pair = blockIdx.x * PPB + pl;
+  const int pair = bx * PPB + pl;
   const uint8_t* q = quant;
   const uint8_t* m = meta;
   int n_rows = M;
@@ -369,8 +371,22 @@ __global__ void __launch_bounds__(WS * PPB * 64) gate_up_kernel(
     if (row >= n_rows) break;
     const float gg = bf16_to_f32(f32_to_bf16(g[i]));  // projections are bf16 tensors
     const float uu = bf16_to_f32(f32_to_bf16(u[i]));
-    out[(int64_t)row * F + n] = f32_to_bf16(gg / (1.0f + __expf(-gg)) * uu);
+    const uint16_t a = f32_to_bf16(gg / (1.0f + __expf(-gg)) * uu);
+    if constexpr (DEVICE_SCOPE)
+      __hip_atomic_store(out + (int64_t)row * F + n, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      out[(int64_t)row * F + n] = a;
   }
+}
+
+template <int FMT, int WS, int PPB>
+__global__ void __launch_bounds__(WS * PPB * 64) gate_up_kernel(
+    const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t gu_qbytes,
+    int64_t gu_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
+    const MoePlan* __restrict__ plan, int E, const void* __restrict__ ws,
+    uint16_t* __restrict__ act_out, int M, int F, int S) {
+  gate_up_body<FMT, WS, PPB, false>(blockIdx.x, blockIdx.y, quant, meta, gu_qbytes, gu_mbytes,
+                                    sh_quant, sh_meta, plan, E, ws, act_out, M, F, S);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -573,11 +589,26 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_plan_kernel(const int32_t* 
 // pairs [M*topk, H] f32 at their pair index; the shared expert's rows, weighted by
 // sigmoid(gate), into shared_out [M, H].
 // ---------------------------------------------------------------------------------------
-template <int FMT, int NTILE>
+template <int FMT, int NTILE, bool DEVICE_SCOPE>
 __device__ __forceinline__ void act_operands(SbOperands<FMT, NTILE>& o, const uint16_t* a, int F,
                                              int n_rows, int s, int lane) {
   XOperands xo;
-  convert_superblock(a, F, n_rows, s, lane, xo);
+  if constexpr (DEVICE_SCOPE) {
+    // device-scope loads (sc1): rows another workgroup of this launch has just published
+    const int r = lane & 15, kq = lane >> 4;
+    const __amdgpu_buffer_rsrc_t ar =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a, 0, 16 * F * 2, 0x00020000);
+    const uint32_t vo = r < n_rows ? (uint32_t)((r * F + kq * 8) * 2) : 0x80000000u;
+    u32x4 raw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      raw[j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, vo, (uint32_t)((s * QK + j * 32) * 2),
+                                                       16 /* sc1 */));
+    convert_words(raw, lane, xo);
+  } else {
+    convert_superblock(a, F, n_rows, s, lane, xo);
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) o.x[j] = xo.x[j];
   o.sx0 = xo.sx0;
@@ -588,7 +619,7 @@ __device__ __forceinline__ void act_operands(SbOperands<FMT, NTILE>& o, const ui
   for (int i = 0; i < 4; ++i) o.scale[i] = __shfl(xo.scale, 4 * kq + i, 64);
 }
 
-template <int FMT, int NTILE, int WS>
+template <int FMT, int NTILE, int WS, bool DEVICE_SCOPE>
 __device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t* a, int F,
                                           int n_rows, int w, int S, int tile0, int lane,
                                           uint32_t Mv, floatx4* acc) {
@@ -598,30 +629,32 @@ __device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t*
   load_sb<FMT, NTILE, false>(bufA, st, w, S, tile0, 1);
   for (int s = w;;) {
     if (s + WS < S) load_sb<FMT, NTILE, false>(bufB, st, s + WS, S, tile0, 1);
-    act_operands<FMT, NTILE>(bufA, a, F, n_rows, s, lane);
+    act_operands<FMT, NTILE, DEVICE_SCOPE>(bufA, a, F, n_rows, s, lane);
     gemv_superblock<FMT, NTILE>(bufA, acc, kq, Mv);
     s += WS;
     if (s >= S) break;
     if (s + WS < S) load_sb<FMT, NTILE, false>(bufA, st, s + WS, S, tile0, 1);
-    act_operands<FMT, NTILE>(bufB, a, F, n_rows, s, lane);
+    act_operands<FMT, NTILE, DEVICE_SCOPE>(bufB, a, F, n_rows, s, lane);
     gemv_superblock<FMT, NTILE>(bufB, acc, kq, Mv);
     s += WS;
     if (s >= S) break;
   }
 }
 
-template <int FMT, int NTILE, int WS, int GPB>
-__global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
-    const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t dn_qbytes,
-    int64_t dn_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
-    const MoePlan* __restrict__ plan, int E, const uint16_t* __restrict__ act,
-    const float* __restrict__ weights, const float* __restrict__ shared_w,
-    float* __restrict__ pairs, float* __restrict__ shared_out, int H, int F) {
+// bx: the block's tile-group index; slot: the plan slot. DEVICE_SCOPE: the activations are read
+// with device-scope loads.
+template <int FMT, int NTILE, int WS, int GPB, bool DEVICE_SCOPE>
+__device__ __forceinline__ void moe_down_body(
+    int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
+    int64_t dn_qbytes, int64_t dn_mbytes, const uint8_t* __restrict__ sh_quant,
+    const uint8_t* __restrict__ sh_meta, const MoePlan* __restrict__ plan, int E,
+    const uint16_t* __restrict__ act, const float* __restrict__ weights,
+    const float* __restrict__ shared_w, float* __restrict__ pairs,
+    float* __restrict__ shared_out, int H, int F) {
   __shared__ floatx4 part[GPB][WS][NTILE][64];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int gl = wv / WS, sw = wv % WS;
-  const int slot = blockIdx.y;
   if (slot >= plan->n_slots) return;
   const int e = plan->slot_expert[slot];
   const int n_rows = plan->slot_rows[slot];
@@ -629,15 +662,15 @@ __global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
   const uint8_t* m = e >= E ? sh_meta : meta + e * dn_mbytes;
   const int S = F / QK;
   const int tiles = H / TILE_N;
-  const int tile0 = (blockIdx.x * GPB + gl) * NTILE;
+  const int tile0 = (bx * GPB + gl) * NTILE;
   const GemvStreams st = make_streams<FMT>(q, m, nullptr, tiles, S, lane, 16);
   const uint32_t Mv = decode_magic<FMT>();
   floatx4 acc[NTILE];
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
   if (tile0 < tiles)
-    down_loop<FMT, NTILE, WS>(st, act + (int64_t)slot * 16 * F, F, n_rows, sw, S, tile0, lane, Mv,
-                              acc);
+    down_loop<FMT, NTILE, WS, DEVICE_SCOPE>(st, act + (int64_t)slot * 16 * F, F, n_rows, sw, S,
+                                            tile0, lane, Mv, acc);
   if constexpr (WS > 1) {
 #pragma unroll
     for (int t = 0; t < NTILE; ++t) part[gl][sw][t][lane] = acc[t];
@@ -668,6 +701,96 @@ __global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
         const int p = plan->pair_of[slot][ci];
         pairs[(int64_t)p * H + n] = y * weights[p];
       }
+    }
+  }
+}
+
+template <int FMT, int NTILE, int WS, int GPB>
+__global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
+    const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t dn_qbytes,
+    int64_t dn_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
+    const MoePlan* __restrict__ plan, int E, const uint16_t* __restrict__ act,
+    const float* __restrict__ weights, const float* __restrict__ shared_w,
+    float* __restrict__ pairs, float* __restrict__ shared_out, int H, int F) {
+  moe_down_body<FMT, NTILE, WS, GPB, false>(blockIdx.x, blockIdx.y, quant, meta, dn_qbytes,
+                                            dn_mbytes, sh_quant, sh_meta, plan, E, act, weights,
+                                            shared_w, pairs, shared_out, H, F);
+}
+
+// ---------------------------------------------------------------------------------------
+// Gate/up and down of every slot in one launch. Workgroups 0 .. GU-1 run gate/up items
+// (slot-major), the rest down items (slot-major). A gate/up item stores its activations with
+// device-scope stores and, once every wave's stores have completed, counts itself done for its
+// slot; a down item waits until all of its slot's gate/up items are counted, then reads the
+// activations with device-scope loads, and the slot's last down item clears the slot's two
+// counters for the next launch (one counter pair per slot, so the atomics spread over the
+// slots). Workgroups start in index order on each XCD, so a waiting item only waits for items
+// that have started and wait for nothing; the wait is bounded all the same, and a time-out is
+// recorded in g_moe_sync[MOE_SYNC_ERROR]. The counters are library-owned: launches of this
+// kernel on one device must be stream-ordered.
+// ---------------------------------------------------------------------------------------
+constexpr int MOE_SYNC_ERROR = 0, MOE_SYNC_UP = 1, MOE_SYNC_DOWN = 1 + MOE_MAX_SLOTS;
+__device__ uint32_t g_moe_sync[1 + 2 * MOE_MAX_SLOTS];
+constexpr uint32_t MOE_WAIT_POLLS = 1u << 20;  // ~0.1 s: far beyond any gate/up item
+
+template <int FMT, int GU_WS, int GU_PPB, int DN_NTILE, int DN_WS, int DN_GPB>
+__global__ void __launch_bounds__(256) moe_experts_kernel(
+    const uint8_t* __restrict__ gu_quant, const uint8_t* __restrict__ gu_meta, int64_t gu_qbytes,
+    int64_t gu_mbytes, const uint8_t* __restrict__ sh_gu_quant,
+    const uint8_t* __restrict__ sh_gu_meta, const uint8_t* __restrict__ dn_quant,
+    const uint8_t* __restrict__ dn_meta, int64_t dn_qbytes, int64_t dn_mbytes,
+    const uint8_t* __restrict__ sh_dn_quant, const uint8_t* __restrict__ sh_dn_meta,
+    const MoePlan* __restrict__ plan, int E, const void* __restrict__ ws,
+    uint16_t* __restrict__ act, const float* __restrict__ weights,
+    const float* __restrict__ shared_w, float* __restrict__ pairs,
+    float* __restrict__ shared_out, int M, int H, int F, int gu_per_slot, int dn_per_slot,
+    int max_slots) {
+  static_assert(GU_WS * GU_PPB * 64 == 256 && DN_WS * DN_GPB * 64 == 256, "256-thread items");
+  const int item = blockIdx.x;
+  const int n_gu = gu_per_slot * max_slots;
+  const int n_slots = plan->n_slots;
+  if (item < n_gu) {
+    const int slot = item / gu_per_slot;
+    if (slot >= n_slots) return;
+    gate_up_body<FMT, GU_WS, GU_PPB, true>(item % gu_per_slot, slot, gu_quant, gu_meta,
+                                           gu_qbytes, gu_mbytes, sh_gu_quant, sh_gu_meta, plan,
+                                           E, ws, act, M, F, H / QK);
+    // every wave waits for its own activation stores to complete (the barrier alone does not
+    // wait for stores), then one count publishes the item
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_add(&g_moe_sync[MOE_SYNC_UP + slot], 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int d = item - n_gu;
+  const int slot = d / dn_per_slot;
+  if (slot >= n_slots) return;
+  if (threadIdx.x == 0) {
+    uint32_t polls = 0;
+    while (__hip_atomic_load(&g_moe_sync[MOE_SYNC_UP + slot], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)gu_per_slot) {
+      if (++polls == MOE_WAIT_POLLS) {
+        __hip_atomic_store(&g_moe_sync[MOE_SYNC_ERROR], 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
+  moe_down_body<FMT, DN_NTILE, DN_WS, DN_GPB, true>(
+      d % dn_per_slot, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
+      plan, E, act, weights, shared_w, pairs, shared_out, H, F);
+  if (threadIdx.x == 0) {
+    const uint32_t done = __hip_atomic_fetch_add(&g_moe_sync[MOE_SYNC_DOWN + slot], 1u,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == (uint32_t)dn_per_slot - 1) {  // the slot's last down item: nothing reads them now
+      __hip_atomic_store(&g_moe_sync[MOE_SYNC_UP + slot], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&g_moe_sync[MOE_SYNC_DOWN + slot], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -887,6 +1010,48 @@ SV_API int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_met
                      (const uint16_t*)act, weights, shared_w, pairs, shared_out, (int)H, (int)F);
   SV_CHECK_LAUNCH();
   return SV_OK;
+}
+
+// snowverify_moe_gate_up followed by snowverify_moe_down in one launch, with the same outputs
+// and bits (max_slots = M * topk + shared). Uses library-owned counters: calls on one device
+// must be stream-ordered.
+SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void* gu_meta,
+                                       const void* dn_quant, const void* dn_meta,
+                                       const void* sh_gu_quant, const void* sh_gu_meta,
+                                       const void* sh_dn_quant, const void* sh_dn_meta,
+                                       const void* plan, const void* ws, const float* weights,
+                                       const float* shared_w, void* act, float* pairs,
+                                       float* shared_out, int64_t M, int64_t max_slots,
+                                       int64_t E, int64_t H, int64_t F, void* stream) {
+  if (fmt != 4 || M <= 0 || M > 16 || max_slots <= 0 || max_slots > MOE_MAX_SLOTS || H % 256 ||
+      F % 256 || (F / 16) % MOE_GU_PPB || (H / 16 / MOE_DN_NTILE) % MOE_DN_GPB)
+    return SV_EINVAL;
+  const int64_t gu_q = 2 * F * H / 2, gu_m = 2 * F * (H / 256) * 16;
+  const int64_t dn_q = H * F / 2, dn_m = H * (F / 256) * 16;
+  const int gu_per_slot = (int)(F / 16 / MOE_GU_PPB);
+  const int dn_per_slot = (int)(H / 16 / MOE_DN_NTILE / MOE_DN_GPB);
+  const int64_t blocks = (int64_t)(gu_per_slot + dn_per_slot) * max_slots;
+  hipLaunchKernelGGL((moe_experts_kernel<4, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS,
+                                         MOE_DN_GPB>),
+                     dim3((unsigned)blocks), dim3(256), 0, Sx(stream), (const uint8_t*)gu_quant,
+                     (const uint8_t*)gu_meta, gu_q, gu_m, (const uint8_t*)sh_gu_quant,
+                     (const uint8_t*)sh_gu_meta, (const uint8_t*)dn_quant,
+                     (const uint8_t*)dn_meta, dn_q, dn_m, (const uint8_t*)sh_dn_quant,
+                     (const uint8_t*)sh_dn_meta, (const MoePlan*)plan, (int)E, ws,
+                     (uint16_t*)act, weights, shared_w, pairs, shared_out, (int)M, (int)H,
+                     (int)F, gu_per_slot, dn_per_slot, (int)max_slots);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Non-zero if a launch of snowverify_moe_gate_up_down ever timed out waiting for its
+// activations (a bug, never expected); reading it blocks on the device.
+SV_API int snowverify_moe_sync_error(void) {
+  uint32_t v = 0;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_moe_sync), sizeof(v),
+                          MOE_SYNC_ERROR * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess)
+    return -1;
+  return (int)v;
 }
 
 // out [M, H] bf16 = sum_k pairs[r * topk + k] (+ shared_out[r]) in a fixed order.

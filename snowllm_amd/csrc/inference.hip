@@ -76,6 +76,13 @@ int64_t snowverify_moe_plan_bytes(void);
 int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_t M, int64_t E,
                               int64_t topk, float* weights, int32_t* ids, float* shared_w,
                               void* plan, void* stream);
+int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void* gu_meta,
+                                const void* dn_quant, const void* dn_meta,
+                                const void* sh_gu_quant, const void* sh_gu_meta,
+                                const void* sh_dn_quant, const void* sh_dn_meta, const void* plan,
+                                const void* ws, const float* weights, const float* shared_w,
+                                void* act, float* pairs, float* shared_out, int64_t M,
+                                int64_t max_slots, int64_t E, int64_t H, int64_t F, void* stream);
 int snowverify_moe_gate_up(int fmt, const void* gu_quant, const void* gu_meta,
                            const void* sh_gu_quant, const void* sh_gu_meta, const void* plan,
                            const void* ws, void* act, int64_t M, int64_t max_slots, int64_t E,
@@ -154,13 +161,13 @@ int moe_body(const Weight* w, const void* hidden, const void* router, void* out,
                                  shared ? ws.shared_w : nullptr, ws.plan, s);
   if (rc) return rc;
   const int64_t slots = M * K + (shared ? 1 : 0);
-  rc = snowverify_moe_gate_up(4, w[0].data[0], w[0].data[1], shared ? w[2].data[0] : nullptr,
-                              shared ? w[2].data[1] : nullptr, ws.plan, ws.ws, ws.act, M, slots,
-                              E, H, F, s);
-  if (rc) return rc;
-  rc = snowverify_moe_down(4, w[1].data[0], w[1].data[1], shared ? w[3].data[0] : nullptr,
-                           shared ? w[3].data[1] : nullptr, ws.plan, ws.act, ws.weights,
-                           ws.shared_w, ws.pairs, ws.shared_out, slots, E, H, F, s);
+  rc = snowverify_moe_gate_up_down(4, w[0].data[0], w[0].data[1], w[1].data[0], w[1].data[1],
+                                   shared ? w[2].data[0] : nullptr,
+                                   shared ? w[2].data[1] : nullptr,
+                                   shared ? w[3].data[0] : nullptr,
+                                   shared ? w[3].data[1] : nullptr, ws.plan, ws.ws, ws.weights,
+                                   ws.shared_w, ws.act, ws.pairs, ws.shared_out, M, slots, E, H,
+                                   F, s);
   if (rc) return rc;
   return snowverify_moe_combine(ws.pairs, shared ? ws.shared_out : nullptr, out, M, K, H, s);
 }

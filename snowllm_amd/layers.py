@@ -178,6 +178,22 @@ def moe_down(fmt, dn, sh_dn, plan, act, weights, shared_w, pairs, shared_out, ma
                                   max_slots, E, H, F, _stream()), "moe_down")
 
 
+def moe_gate_up_down(fmt, gu, dn, sh_gu, sh_dn, plan, ws, weights, shared_w, act, pairs,
+                     shared_out, M, max_slots, E, H, F):
+    """moe_gate_up then moe_down in one launch (same bits); launches on one device must be
+    stream-ordered (library-owned counters)."""
+    check(lib.snowverify_moe_gate_up_down(fmt, _p(gu[0]), _p(gu[1]), _p(dn[0]), _p(dn[1]),
+                                          _p(sh_gu[0]), _p(sh_gu[1]), _p(sh_dn[0]),
+                                          _p(sh_dn[1]), _p(plan), _p(ws), _p(weights),
+                                          _p(shared_w), _p(act), _p(pairs), _p(shared_out), M,
+                                          max_slots, E, H, F, _stream()), "moe_gate_up_down")
+
+
+def moe_sync_error():
+    """Non-zero once a fused expert launch timed out waiting for its activations."""
+    return int(lib.snowverify_moe_sync_error())
+
+
 def moe_combine(pairs, shared_out, out, M, topk, H):
     check(lib.snowverify_moe_combine(_p(pairs), _p(shared_out), _p(out), M, topk, H, _stream()),
           "moe_combine")

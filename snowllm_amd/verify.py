@@ -339,11 +339,11 @@ class VerifyModel:
                 if record_slots is not None:
                     record_slots[i:i + 1].copy_(self.plan[:4].view(torch.int32))
                 ns = T * c.topk + 1
-                Lops.moe_gate_up(c.ffn_fmt, lw.gu, lw.sh_gu, self.plan, self.ws_h2, self.moe_act,
-                                 T, ns, c.experts, H, c.expert_ffn)
-                Lops.moe_down(c.ffn_fmt, lw.dn, lw.sh_dn, self.plan, self.moe_act, self.route_w,
-                              self.shared_w, self.pairs, self.shared_out, ns, c.experts, H,
-                              c.expert_ffn)
+                # gate/up and down in one launch: a slot's down starts when its gate/up is done
+                Lops.moe_gate_up_down(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, self.plan,
+                                      self.ws_h2, self.route_w, self.shared_w, self.moe_act,
+                                      self.pairs, self.shared_out, T, ns, c.experts, H,
+                                      c.expert_ffn)
                 moe_out = True
             else:
                 Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,

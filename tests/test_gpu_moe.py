@@ -61,6 +61,56 @@ def test_route_plan(gpu, M):
         assert np.array_equal(p2[key], p[key])
 
 
+def test_gate_up_down_equals_separate_launches(gpu):
+    """Gate/up and down in one launch (down items wait for their slot's gate/up items) give the
+    bits of the two launches; consecutive launches of different sizes reuse the counters."""
+    from snowllm_amd import layers as L, ops
+    from snowllm_amd.verify import packed_random
+    gu = packed_random(4, E * 2 * F, H, 51)
+    dn = packed_random(4, E * H, F, 52)
+    sgu = packed_random(4, 2 * F, H, 53)
+    sdn = packed_random(4, H, F, 54)
+    for M, shared, spread in ((9, True, False), (16, True, True), (1, True, False),
+                              (9, False, True), (9, True, True)):
+        print(f"gate_up_down M={M} shared={shared} spread={spread}", flush=True)
+        g = torch.Generator(device="cuda").manual_seed(70 + M)
+        x = torch.randn(M, H, device="cuda", generator=g).bfloat16()
+        logits = torch.randn(M, E + 1, device="cuda", generator=g) * 2
+        if spread:  # every row on its own experts: the most slots
+            for r in range(M):
+                logits[r, (K * r) % E:(K * r) % E + K] += 40.0
+        w = torch.empty(M, K, device="cuda")
+        ids = torch.empty(M, K, dtype=torch.int32, device="cuda")
+        sw = torch.empty(M, device="cuda") if shared else None
+        plan = torch.empty(L.MOE_PLAN_BYTES, dtype=torch.uint8, device="cuda")
+        L.moe_route_plan(logits, E, K, w, ids, sw, plan)
+        ws = torch.empty(ops.gemm_kquant_a_ws_bytes(M, H), dtype=torch.uint8, device="cuda")
+        ops.gemm_kquant_prepare_a(x, ws)
+        ns = M * K + int(shared)
+        sg, sd = (sgu, sdn) if shared else ((None, None), (None, None))
+        outs = []
+        for fused in (False, True, True):
+            act = torch.zeros(ns, 16, F, dtype=torch.bfloat16, device="cuda")
+            pairs = torch.zeros(M * K, H, device="cuda")
+            sh_out = torch.zeros(M, H, device="cuda")
+            if fused:
+                L.moe_gate_up_down(4, gu, dn, sg, sd, plan, ws, w, sw, act, pairs, sh_out, M, ns,
+                                   E, H, F)
+            else:
+                L.moe_gate_up(4, gu, sg, plan, ws, act, M, ns, E, H, F)
+                L.moe_down(4, dn, sd, plan, act, w, sw, pairs, sh_out, ns, E, H, F)
+            torch.cuda.synchronize()
+            outs.append((act, pairs, sh_out))
+        p = L.parse_plan(plan)
+        for o in outs[1:]:
+            for sl in range(p["n_slots"]):
+                r = p["slot_rows"][sl]
+                assert torch.equal(o[0][sl, :r], outs[0][0][sl, :r])
+            assert torch.equal(o[1], outs[0][1])
+            assert torch.equal(o[2], outs[0][2])
+    assert L.moe_sync_error() == 0
+
+
 def _bf(x):
     return x.to(torch.bfloat16).double()
 
