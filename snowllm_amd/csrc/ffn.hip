@@ -619,12 +619,20 @@ __device__ __forceinline__ void act_operands(SbOperands<FMT, NTILE>& o, const ui
   for (int i = 0; i < 4; ++i) o.scale[i] = __shfl(xo.scale, 4 * kq + i, 64);
 }
 
-template <int FMT, int NTILE, int WS, bool DEVICE_SCOPE>
+// ONE_SB: S == WS, one superblock per wave (no second operand buffer, so fewer registers).
+template <int FMT, int NTILE, int WS, bool DEVICE_SCOPE, bool ONE_SB>
 __device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t* a, int F,
                                           int n_rows, int w, int S, int tile0, int lane,
                                           uint32_t Mv, floatx4* acc) {
   if (w >= S) return;
   const int kq = lane >> 4;
+  if constexpr (ONE_SB) {
+    SbOperands<FMT, NTILE> o;
+    load_sb<FMT, NTILE, false>(o, st, w, S, tile0, 1);
+    act_operands<FMT, NTILE, DEVICE_SCOPE>(o, a, F, n_rows, w, lane);
+    gemv_superblock<FMT, NTILE>(o, acc, kq, Mv);
+    return;
+  }
   SbOperands<FMT, NTILE> bufA, bufB;
   load_sb<FMT, NTILE, false>(bufA, st, w, S, tile0, 1);
   for (int s = w;;) {
@@ -642,8 +650,8 @@ __device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t*
 }
 
 // bx: the block's tile-group index; slot: the plan slot. DEVICE_SCOPE: the activations are read
-// with device-scope loads.
-template <int FMT, int NTILE, int WS, int GPB, bool DEVICE_SCOPE>
+// with device-scope loads. ONE_SB: F / QK == WS.
+template <int FMT, int NTILE, int WS, int GPB, bool DEVICE_SCOPE, bool ONE_SB>
 __device__ __forceinline__ void moe_down_body(
     int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
     int64_t dn_qbytes, int64_t dn_mbytes, const uint8_t* __restrict__ sh_quant,
@@ -665,11 +673,21 @@ __device__ __forceinline__ void moe_down_body(
   const int tile0 = (bx * GPB + gl) * NTILE;
   const GemvStreams st = make_streams<FMT>(q, m, nullptr, tiles, S, lane, 16);
   const uint32_t Mv = decode_magic<FMT>();
+  // the epilogue's destinations and gates for this lane's compact rows, fetched up front
+  const int rb = 4 * (lane >> 4);
+  int dst[4];
+  float gate[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ci = rb + i;
+    dst[i] = ci < n_rows ? (e >= E ? plan->row_of[slot][ci] : plan->pair_of[slot][ci]) : 0;
+    gate[i] = ci < n_rows ? (e >= E ? shared_w[dst[i]] : weights[dst[i]]) : 0.f;
+  }
   floatx4 acc[NTILE];
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
   if (tile0 < tiles)
-    down_loop<FMT, NTILE, WS, DEVICE_SCOPE>(st, act + (int64_t)slot * 16 * F, F, n_rows, sw, S,
+    down_loop<FMT, NTILE, WS, DEVICE_SCOPE, ONE_SB>(st, act + (int64_t)slot * 16 * F, F, n_rows, sw, S,
                                             tile0, lane, Mv, acc);
   if constexpr (WS > 1) {
 #pragma unroll
@@ -683,7 +701,6 @@ __device__ __forceinline__ void moe_down_body(
       for (int j = 1; j < WS; ++j) acc[t] += part[gl][j][t][lane];
     }
   }
-  const int rb = 4 * (lane >> 4);
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) {
     const int tile = tile0 + t;
@@ -691,28 +708,22 @@ __device__ __forceinline__ void moe_down_body(
     const int n = tile * TILE_N + (lane & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ci = rb + i;  // compact row
-      if (ci >= n_rows) break;
+      if (rb + i >= n_rows) break;  // compact row
       const float y = bf16_to_f32(f32_to_bf16(acc[t][i]));  // expert outputs are bf16 tensors
-      if (e >= E) {
-        const int row = plan->row_of[slot][ci];
-        shared_out[(int64_t)row * H + n] = y * shared_w[row];
-      } else {
-        const int p = plan->pair_of[slot][ci];
-        pairs[(int64_t)p * H + n] = y * weights[p];
-      }
+      float* out = e >= E ? shared_out : pairs;
+      out[(int64_t)dst[i] * H + n] = y * gate[i];
     }
   }
 }
 
-template <int FMT, int NTILE, int WS, int GPB>
+template <int FMT, int NTILE, int WS, int GPB, bool ONE_SB>
 __global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
     const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t dn_qbytes,
     int64_t dn_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
     const MoePlan* __restrict__ plan, int E, const uint16_t* __restrict__ act,
     const float* __restrict__ weights, const float* __restrict__ shared_w,
     float* __restrict__ pairs, float* __restrict__ shared_out, int H, int F) {
-  moe_down_body<FMT, NTILE, WS, GPB, false>(blockIdx.x, blockIdx.y, quant, meta, dn_qbytes,
+  moe_down_body<FMT, NTILE, WS, GPB, false, ONE_SB>(blockIdx.x, blockIdx.y, quant, meta, dn_qbytes,
                                             dn_mbytes, sh_quant, sh_meta, plan, E, act, weights,
                                             shared_w, pairs, shared_out, H, F);
 }
@@ -720,21 +731,24 @@ __global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
 // ---------------------------------------------------------------------------------------
 // Gate/up and down of every slot in one launch. Workgroups 0 .. GU-1 run gate/up items
 // (slot-major), the rest down items (slot-major). A gate/up item stores its activations with
-// device-scope stores and, once every wave's stores have completed, counts itself done for its
-// slot; a down item waits until all of its slot's gate/up items are counted, then reads the
-// activations with device-scope loads, and the slot's last down item clears the slot's two
-// counters for the next launch (one counter pair per slot, so the atomics spread over the
-// slots). Workgroups start in index order on each XCD, so a waiting item only waits for items
-// that have started and wait for nothing; the wait is bounded all the same, and a time-out is
-// recorded in g_moe_sync[MOE_SYNC_ERROR]. The counters are library-owned: launches of this
+// device-scope stores and, once every wave's stores have completed, sets its flag in each of
+// its slot's down items' flag lines; a down item waits until the flags of all of its slot's
+// gate/up items are set in its own line, clears them for the next launch and reads the
+// activations with device-scope loads. Each line has one reader, so nothing is counted and no
+// address is contended. Workgroups start in index order on each XCD, so a waiting item only
+// waits for items that have started and wait for nothing; the wait is bounded all the same,
+// and a time-out is recorded in g_moe_error. The flags are library-owned: launches of this
 // kernel on one device must be stream-ordered.
 // ---------------------------------------------------------------------------------------
-constexpr int MOE_SYNC_ERROR = 0, MOE_SYNC_UP = 1, MOE_SYNC_DOWN = 1 + MOE_MAX_SLOTS;
-__device__ uint32_t g_moe_sync[1 + 2 * MOE_MAX_SLOTS];
+constexpr int MOE_MAX_ITEMS = 32;  // gate/up or down items per slot
+__device__ __align__(256) uint32_t g_moe_flags[MOE_MAX_SLOTS][MOE_MAX_ITEMS][MOE_MAX_ITEMS];
+__device__ uint32_t g_moe_error;
 constexpr uint32_t MOE_WAIT_POLLS = 1u << 20;  // ~0.1 s: far beyond any gate/up item
 
-template <int FMT, int GU_WS, int GU_PPB, int DN_NTILE, int DN_WS, int DN_GPB>
-__global__ void __launch_bounds__(256) moe_experts_kernel(
+// Three waves per SIMD when the down items take one superblock per wave (the gate/up items then
+// bound the registers at 168); two otherwise.
+template <int FMT, int GU_WS, int GU_PPB, int DN_NTILE, int DN_WS, int DN_GPB, bool ONE_SB>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB ? 3 : 2, ONE_SB ? 3 : 2))) moe_experts_kernel(
     const uint8_t* __restrict__ gu_quant, const uint8_t* __restrict__ gu_meta, int64_t gu_qbytes,
     int64_t gu_mbytes, const uint8_t* __restrict__ sh_gu_quant,
     const uint8_t* __restrict__ sh_gu_meta, const uint8_t* __restrict__ dn_quant,
@@ -759,40 +773,30 @@ __global__ void __launch_bounds__(256) moe_experts_kernel(
     // wait for stores), then one count publishes the item
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(&g_moe_sync[MOE_SYNC_UP + slot], 1u, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    if ((int)threadIdx.x < dn_per_slot)
+      __hip_atomic_store(&g_moe_flags[slot][threadIdx.x][item % gu_per_slot], 1u,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   const int d = item - n_gu;
   const int slot = d / dn_per_slot;
   if (slot >= n_slots) return;
-  if (threadIdx.x == 0) {
+  if ((int)threadIdx.x < gu_per_slot) {  // one lane per gate/up item of the slot
+    uint32_t* flag = &g_moe_flags[slot][d % dn_per_slot][threadIdx.x];
     uint32_t polls = 0;
-    while (__hip_atomic_load(&g_moe_sync[MOE_SYNC_UP + slot], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)gu_per_slot) {
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
       if (++polls == MOE_WAIT_POLLS) {
-        __hip_atomic_store(&g_moe_sync[MOE_SYNC_ERROR], 1u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&g_moe_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
       __builtin_amdgcn_s_sleep(2);
     }
+    __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // sole reader
   }
   __syncthreads();
-  moe_down_body<FMT, DN_NTILE, DN_WS, DN_GPB, true>(
+  moe_down_body<FMT, DN_NTILE, DN_WS, DN_GPB, true, ONE_SB>(
       d % dn_per_slot, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
       plan, E, act, weights, shared_w, pairs, shared_out, H, F);
-  if (threadIdx.x == 0) {
-    const uint32_t done = __hip_atomic_fetch_add(&g_moe_sync[MOE_SYNC_DOWN + slot], 1u,
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (done == (uint32_t)dn_per_slot - 1) {  // the slot's last down item: nothing reads them now
-      __hip_atomic_store(&g_moe_sync[MOE_SYNC_UP + slot], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&g_moe_sync[MOE_SYNC_DOWN + slot], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
 }
 
 // out[r, n] = bf16(sum_k pairs[r*topk + k, n] + shared_out[r, n]) in a fixed order
@@ -1003,17 +1007,23 @@ SV_API int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_met
   const int64_t dn_q = H * F / 2, dn_m = H * (F / 256) * 16;
   const int groups = (int)(H / 16 / MOE_DN_NTILE);
   const dim3 grid((unsigned)((groups + MOE_DN_GPB - 1) / MOE_DN_GPB), (unsigned)max_slots);
-  hipLaunchKernelGGL((moe_down_kernel<4, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB>), grid,
-                     dim3(64 * MOE_DN_WS * MOE_DN_GPB), 0, Sx(stream), (const uint8_t*)dn_quant,
-                     (const uint8_t*)dn_meta, dn_q, dn_m, (const uint8_t*)sh_dn_quant,
-                     (const uint8_t*)sh_dn_meta, (const MoePlan*)plan, (int)E,
-                     (const uint16_t*)act, weights, shared_w, pairs, shared_out, (int)H, (int)F);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(64 * MOE_DN_WS * MOE_DN_GPB), 0, Sx(stream),
+                       (const uint8_t*)dn_quant, (const uint8_t*)dn_meta, dn_q, dn_m,
+                       (const uint8_t*)sh_dn_quant, (const uint8_t*)sh_dn_meta,
+                       (const MoePlan*)plan, (int)E, (const uint16_t*)act, weights, shared_w,
+                       pairs, shared_out, (int)H, (int)F);
+  };
+  if (F / QK == MOE_DN_WS)
+    launch(moe_down_kernel<4, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB, true>);
+  else
+    launch(moe_down_kernel<4, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB, false>);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
 
 // snowverify_moe_gate_up followed by snowverify_moe_down in one launch, with the same outputs
-// and bits (max_slots = M * topk + shared). Uses library-owned counters: calls on one device
+// and bits (max_slots = M * topk + shared). Uses library-owned flags: calls on one device
 // must be stream-ordered.
 SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void* gu_meta,
                                        const void* dn_quant, const void* dn_meta,
@@ -1030,16 +1040,24 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
   const int64_t dn_q = H * F / 2, dn_m = H * (F / 256) * 16;
   const int gu_per_slot = (int)(F / 16 / MOE_GU_PPB);
   const int dn_per_slot = (int)(H / 16 / MOE_DN_NTILE / MOE_DN_GPB);
+  if (gu_per_slot > MOE_MAX_ITEMS || dn_per_slot > MOE_MAX_ITEMS) return SV_ENOTSUP;
   const int64_t blocks = (int64_t)(gu_per_slot + dn_per_slot) * max_slots;
-  hipLaunchKernelGGL((moe_experts_kernel<4, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS,
-                                         MOE_DN_GPB>),
-                     dim3((unsigned)blocks), dim3(256), 0, Sx(stream), (const uint8_t*)gu_quant,
-                     (const uint8_t*)gu_meta, gu_q, gu_m, (const uint8_t*)sh_gu_quant,
-                     (const uint8_t*)sh_gu_meta, (const uint8_t*)dn_quant,
-                     (const uint8_t*)dn_meta, dn_q, dn_m, (const uint8_t*)sh_dn_quant,
-                     (const uint8_t*)sh_dn_meta, (const MoePlan*)plan, (int)E, ws,
-                     (uint16_t*)act, weights, shared_w, pairs, shared_out, (int)M, (int)H,
-                     (int)F, gu_per_slot, dn_per_slot, (int)max_slots);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, Sx(stream),
+                       (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
+                       (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
+                       (const uint8_t*)dn_quant, (const uint8_t*)dn_meta, dn_q, dn_m,
+                       (const uint8_t*)sh_dn_quant, (const uint8_t*)sh_dn_meta,
+                       (const MoePlan*)plan, (int)E, ws, (uint16_t*)act, weights, shared_w,
+                       pairs, shared_out, (int)M, (int)H, (int)F, gu_per_slot, dn_per_slot,
+                       (int)max_slots);
+  };
+  if (F / QK == MOE_DN_WS)
+    launch(moe_experts_kernel<4, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
+                              true>);
+  else
+    launch(moe_experts_kernel<4, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
+                              false>);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1048,8 +1066,8 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
 // activations (a bug, never expected); reading it blocks on the device.
 SV_API int snowverify_moe_sync_error(void) {
   uint32_t v = 0;
-  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_moe_sync), sizeof(v),
-                          MOE_SYNC_ERROR * sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess)
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_moe_error), sizeof(v), 0, hipMemcpyDeviceToHost) !=
+      hipSuccess)
     return -1;
   return (int)v;
 }

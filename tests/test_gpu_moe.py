@@ -61,9 +61,10 @@ def test_route_plan(gpu, M):
         assert np.array_equal(p2[key], p[key])
 
 
-def test_gate_up_down_equals_separate_launches(gpu):
+@pytest.mark.parametrize("E,F", [(E, F), (64, 1024)])  # one / two superblocks per down wave
+def test_gate_up_down_equals_separate_launches(gpu, E, F):
     """Gate/up and down in one launch (down items wait for their slot's gate/up items) give the
-    bits of the two launches; consecutive launches of different sizes reuse the counters."""
+    bits of the two launches; consecutive launches of different sizes reuse the flags."""
     from snowllm_amd import layers as L, ops
     from snowllm_amd.verify import packed_random
     gu = packed_random(4, E * 2 * F, H, 51)
@@ -72,7 +73,7 @@ def test_gate_up_down_equals_separate_launches(gpu):
     sdn = packed_random(4, H, F, 54)
     for M, shared, spread in ((9, True, False), (16, True, True), (1, True, False),
                               (9, False, True), (9, True, True)):
-        print(f"gate_up_down M={M} shared={shared} spread={spread}", flush=True)
+        print(f"gate_up_down E={E} F={F} M={M} shared={shared} spread={spread}", flush=True)
         g = torch.Generator(device="cuda").manual_seed(70 + M)
         x = torch.randn(M, H, device="cuda", generator=g).bfloat16()
         logits = torch.randn(M, E + 1, device="cuda", generator=g) * 2
