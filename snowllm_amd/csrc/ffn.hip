@@ -619,20 +619,12 @@ __device__ __forceinline__ void act_operands(SbOperands<FMT, NTILE>& o, const ui
   for (int i = 0; i < 4; ++i) o.scale[i] = __shfl(xo.scale, 4 * kq + i, 64);
 }
 
-// ONE_SB: S == WS, one superblock per wave (no second operand buffer, so fewer registers).
-template <int FMT, int NTILE, int WS, bool DEVICE_SCOPE, bool ONE_SB>
+template <int FMT, int NTILE, int WS, bool DEVICE_SCOPE>
 __device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t* a, int F,
                                           int n_rows, int w, int S, int tile0, int lane,
                                           uint32_t Mv, floatx4* acc) {
   if (w >= S) return;
   const int kq = lane >> 4;
-  if constexpr (ONE_SB) {
-    SbOperands<FMT, NTILE> o;
-    load_sb<FMT, NTILE, false>(o, st, w, S, tile0, 1);
-    act_operands<FMT, NTILE, DEVICE_SCOPE>(o, a, F, n_rows, w, lane);
-    gemv_superblock<FMT, NTILE>(o, acc, kq, Mv);
-    return;
-  }
   SbOperands<FMT, NTILE> bufA, bufB;
   load_sb<FMT, NTILE, false>(bufA, st, w, S, tile0, 1);
   for (int s = w;;) {
@@ -650,7 +642,8 @@ __device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t*
 }
 
 // bx: the block's tile-group index; slot: the plan slot. DEVICE_SCOPE: the activations are read
-// with device-scope loads. ONE_SB: F / QK == WS.
+// with device-scope loads. ONE_SB: F / QK == WS, one superblock per wave (no second operand
+// buffer, so fewer registers).
 template <int FMT, int NTILE, int WS, int GPB, bool DEVICE_SCOPE, bool ONE_SB>
 __device__ __forceinline__ void moe_down_body(
     int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
@@ -677,18 +670,35 @@ __device__ __forceinline__ void moe_down_body(
   const int rb = 4 * (lane >> 4);
   int dst[4];
   float gate[4];
+  auto fetch_epilogue = [&]() {
+    const int32_t* ids = e >= E ? plan->row_of[slot] : plan->pair_of[slot];
+    const float* gsrc = e >= E ? shared_w : weights;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ci = rb + i;
-    dst[i] = ci < n_rows ? (e >= E ? plan->row_of[slot][ci] : plan->pair_of[slot][ci]) : 0;
-    gate[i] = ci < n_rows ? (e >= E ? shared_w[dst[i]] : weights[dst[i]]) : 0.f;
-  }
+    for (int i = 0; i < 4; ++i) dst[i] = rb + i < n_rows ? ids[rb + i] : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gate[i] = rb + i < n_rows ? gsrc[dst[i]] : 0.f;
+  };
   floatx4 acc[NTILE];
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-  if (tile0 < tiles)
-    down_loop<FMT, NTILE, WS, DEVICE_SCOPE, ONE_SB>(st, act + (int64_t)slot * 16 * F, F, n_rows, sw, S,
-                                            tile0, lane, Mv, acc);
+  const uint16_t* slot_act = act + (int64_t)slot * 16 * F;
+  if constexpr (ONE_SB) {
+    // one superblock per wave (S == WS): its weights go out first, then the epilogue's
+    // operands, then the activations
+    const bool live = tile0 < tiles && sw < S;
+    SbOperands<FMT, NTILE> o;
+    if (live) load_sb<FMT, NTILE, false>(o, st, sw, S, tile0, 1);
+    fetch_epilogue();
+    if (live) {
+      act_operands<FMT, NTILE, DEVICE_SCOPE>(o, slot_act, F, n_rows, sw, lane);
+      gemv_superblock<FMT, NTILE>(o, acc, lane >> 4, Mv);
+    }
+  } else {
+    fetch_epilogue();
+    if (tile0 < tiles)
+      down_loop<FMT, NTILE, WS, DEVICE_SCOPE>(st, slot_act, F, n_rows, sw, S, tile0, lane, Mv,
+                                              acc);
+  }
   if constexpr (WS > 1) {
 #pragma unroll
     for (int t = 0; t < NTILE; ++t) part[gl][sw][t][lane] = acc[t];
@@ -778,11 +788,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
+  // slot and item index are wave-uniform: keep them scalar so that the weight offsets derived
+  // from them stay scalar through the divergent wait below
   const int d = item - n_gu;
-  const int slot = d / dn_per_slot;
+  const int slot = __builtin_amdgcn_readfirstlane(d / dn_per_slot);
+  const int didx = __builtin_amdgcn_readfirstlane(d % dn_per_slot);
   if (slot >= n_slots) return;
   if ((int)threadIdx.x < gu_per_slot) {  // one lane per gate/up item of the slot
-    uint32_t* flag = &g_moe_flags[slot][d % dn_per_slot][threadIdx.x];
+    uint32_t* flag = &g_moe_flags[slot][didx][threadIdx.x];
     uint32_t polls = 0;
     while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
       if (++polls == MOE_WAIT_POLLS) {
@@ -795,7 +808,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB
   }
   __syncthreads();
   moe_down_body<FMT, DN_NTILE, DN_WS, DN_GPB, true, ONE_SB>(
-      d % dn_per_slot, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
+      didx, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
       plan, E, act, weights, shared_w, pairs, shared_out, H, F);
 }
 

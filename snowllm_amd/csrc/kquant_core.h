@@ -290,31 +290,45 @@ struct GemvStreams {
   uint32_t v_scale_g[4];  // row-gathered streams: offsets of the scales of rows 4*kq + i
 };
 
+// The activation operands of superblock s from the workspace (GATHER: rows gathered per lane).
+template <int FMT, int NTILE, bool GATHER = false>
+__device__ __forceinline__ void load_sb_x(SbOperands<FMT, NTILE>& o, const GemvStreams& st,
+                                          int s) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o.x[j] = bload4(st.xop, st.v_xop, (uint32_t)((s * 8 + j) * 64 * 16));
+  o.sx0 = bload1(st.sxop, st.v_sx, (uint32_t)((s * 2 + 0) * 64 * 4));
+  o.sx1 = bload1(st.sxop, st.v_sx, (uint32_t)((s * 2 + 1) * 64 * 4));
+  if constexpr (GATHER) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o.scale[i] = bload1(st.scale, st.v_scale_g[i], (uint32_t)(s * 16 * 4));
+  } else {
+    o.scale = __builtin_bit_cast(floatx4, bload4(st.scale, st.v_scale, (uint32_t)(s * 16 * 4)));
+  }
+}
+
+// The weights of superblock s for tiles tile0 + t * tstride (t < NTILE).
+template <int FMT, int NTILE>
+__device__ __forceinline__ void load_sb_w(u32x4 (&q)[NTILE][QLayout<FMT>::kQuantVecs],
+                                          u32x4 (&m)[NTILE], const GemvStreams& st, int s, int S,
+                                          int tile0, int tstride) {
+  constexpr int QV = QLayout<FMT>::kQuantVecs;
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) {
+    const uint32_t ts = (uint32_t)((tile0 + t * tstride) * S + s);
+#pragma unroll
+    for (int i = 0; i < QV; ++i) q[t][i] = bload4(st.quant, st.v_quant, (ts * QV + i) * 64 * 16);
+    m[t] = bload4(st.meta, st.v_meta, ts * 16 * 16);
+  }
+}
+
 // Load the weights of superblock s for tiles tile0 + t * tstride (t < NTILE) and, when
 // WITH_X, its activation operands from the workspace.
 template <int FMT, int NTILE, bool WITH_X = true, bool GATHER = false>
 __device__ __forceinline__ void load_sb(SbOperands<FMT, NTILE>& o, const GemvStreams& st, int s,
                                         int S, int tile0, int tstride = 1) {
-  constexpr int QV = QLayout<FMT>::kQuantVecs;
-  if constexpr (WITH_X) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o.x[j] = bload4(st.xop, st.v_xop, (uint32_t)((s * 8 + j) * 64 * 16));
-    o.sx0 = bload1(st.sxop, st.v_sx, (uint32_t)((s * 2 + 0) * 64 * 4));
-    o.sx1 = bload1(st.sxop, st.v_sx, (uint32_t)((s * 2 + 1) * 64 * 4));
-    if constexpr (GATHER) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o.scale[i] = bload1(st.scale, st.v_scale_g[i], (uint32_t)(s * 16 * 4));
-    } else {
-      o.scale = __builtin_bit_cast(floatx4, bload4(st.scale, st.v_scale, (uint32_t)(s * 16 * 4)));
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < NTILE; ++t) {
-    const uint32_t ts = (uint32_t)((tile0 + t * tstride) * S + s);
-#pragma unroll
-    for (int i = 0; i < QV; ++i) o.q[t][i] = bload4(st.quant, st.v_quant, (ts * QV + i) * 64 * 16);
-    o.m[t] = bload4(st.meta, st.v_meta, ts * 16 * 16);
-  }
+  if constexpr (WITH_X) load_sb_x<FMT, NTILE, GATHER>(o, st, s);
+  load_sb_w<FMT, NTILE>(o.q, o.m, st, s, S, tile0, tstride);
 }
 
 // Multiply one superblock's operands into acc.
