@@ -325,7 +325,7 @@ def bench_step(args, name):
     single = {kk: v for kk, v in kern.items() if "+" not in kk}
     dom = max(single, key=lambda kk: single[kk]["us"])
     d = kern[dom]
-    traffic = read_traffic(dom)
+    traffic = read_traffic(dom) if cfg.name == TRAFFIC_WORKLOAD else None
 
     # reference CPU path (oracle, torch CPU) on a bounded sample: layer 0 x layers + head +
     # acceptance
@@ -371,10 +371,13 @@ def chain_rows(parents):
         rows.append(kids[0])
 
 
+TRAFFIC_WORKLOAD = "config4"  # the workload profiles/traffic.txt was measured on
+
+
 def read_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
     (profiles/traffic.txt: 'kernel | fetch_bytes | write_bytes' rows, already scaled by the
-    copy-kernel calibration), or None."""
+    copy-kernel calibration, measured on TRAFFIC_WORKLOAD), or None."""
     path = os.path.join(ROOT, "profiles", "traffic.txt")
     try:
         for line in open(path):

@@ -400,7 +400,7 @@ int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_meta,
 /* Extension, no counterpart in the reference (whose expert stages are internal to
  * snowllm_inference_moe): snowverify_moe_gate_up then snowverify_moe_down in one launch, same
  * outputs and bits; a down item starts as soon as its slot's gate/up items are done. Uses
- * library-owned counters, so calls on one device must be stream-ordered. */
+ * library-owned flags, so calls on one device must be stream-ordered. */
 int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void* gu_meta,
                                 const void* dn_quant, const void* dn_meta,
                                 const void* sh_gu_quant, const void* sh_gu_meta,
