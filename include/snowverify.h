@@ -196,6 +196,23 @@ int snowverify_paged_attention_qk(const void* proj, int64_t proj_stride, int64_t
                                   int64_t num_heads, int64_t num_kv_heads, int64_t head_size,
                                   int64_t page_size, int64_t table_stride, float scale,
                                   void* scratch, int64_t scratch_bytes, void* stream);
+/* Extension, no counterpart in the reference: snowverify_paged_attention_qk that also writes
+ * the output projection's operand workspace out_ws (as snowllm_gemm_kquant_prepare_a would
+ * from `out` viewed as [batch*tokens, num_heads*head_size]; snowllm_gemm_kquant_a_ws_bytes of
+ * that shape), so the projection runs snowllm_gemm_kquant_a_prepared with the same bits as
+ * snowllm_gemm_kquant_a on `out`. head_size 256 only (hipErrorNotSupported otherwise). */
+int snowverify_paged_attention_qk_ws(const void* proj, int64_t proj_stride,
+                                     int64_t q_head_stride, int64_t k_off, int64_t v_off,
+                                     const void* q_gamma, const void* k_gamma,
+                                     const float* cos_in, const float* sin_in, int64_t cs_stride,
+                                     int64_t half, float eps, const int32_t* slots, void* q_out,
+                                     void* k_pool, void* v_pool, void* out,
+                                     const int32_t* table, const int32_t* lens,
+                                     const uint64_t* tree, int64_t batch, int64_t tokens,
+                                     int64_t num_heads, int64_t num_kv_heads, int64_t head_size,
+                                     int64_t page_size, int64_t table_stride, float scale,
+                                     void* scratch, int64_t scratch_bytes, void* out_ws,
+                                     void* stream);
 
 /* Extension, no counterpart in the reference (a tuning knob): pages per context split of
  * snowverify_paged_attention; 0 = automatic. Returns the previous value. */

@@ -92,6 +92,8 @@ _SIGS = [
     ("snowverify_paged_attention", c_int, [P] * 7 + [c_int64] * 7 + [c_float, P, c_int64, S]),
     ("snowverify_paged_attention_qk", c_int, [P] + [c_int64] * 4 + [P] * 4 + [c_int64] * 2 +
      [c_float] + [P] * 8 + [c_int64] * 7 + [c_float, P, c_int64, S]),
+    ("snowverify_paged_attention_qk_ws", c_int, [P] + [c_int64] * 4 + [P] * 4 + [c_int64] * 2 +
+     [c_float] + [P] * 8 + [c_int64] * 7 + [c_float, P, c_int64, P, S]),
     ("snowverify_attention_pages_per_split", c_int, [c_int]),
     ("snowverify_attention_d_split", c_int, [c_int]),
     ("snowverify_attention_ring", c_int, [c_int]),

@@ -64,11 +64,14 @@ FUSED_QK_MAX_HALF = 64
 
 
 def paged_attention_qk(proj, q_gamma, k_gamma, cos, sin, eps, slots, k_pool, v_pool, out, table,
-                       lens, scale, scratch, *, num_heads, num_kv_heads, tree=None, q_out=None):
+                       lens, scale, scratch, *, num_heads, num_kv_heads, tree=None, q_out=None,
+                       ws_out=None):
     """QK-norm + RoPE + the block's K/V write fused into the attention (extension): proj
     [batch*T, n] bf16 = [q heads | k heads | v heads] (head size d); cos/sin [batch*T, half]
     f32; slots int32 [batch*T]. Same bits as qk_norm_rope_cache followed by
-    paged_attention_explicit; q_out receives the rotated q if given. half <= FUSED_QK_MAX_HALF."""
+    paged_attention_explicit; q_out receives the rotated q if given. half <= FUSED_QK_MAX_HALF.
+    ws_out (head size 256): the output projection's operand workspace for `out` as
+    [batch*T, num_heads*d], written as gemm_kquant_prepare_a would."""
     batch = lens.numel()
     M, n = proj.shape
     D = out.shape[2]
@@ -87,12 +90,19 @@ def paged_attention_qk(proj, q_gamma, k_gamma, cos, sin, eps, slots, k_pool, v_p
     need = paged_attention_explicit_scratch_bytes(batch, T, num_heads, num_kv_heads, D)
     if scratch is None or scratch.nbytes < need:
         raise SnowLLMError(f"paged attention needs {need} scratch bytes")
-    check(lib.snowverify_paged_attention_qk(
-        _p(proj), n, D, num_heads * D, (num_heads + num_kv_heads) * D, _p(q_gamma), _p(k_gamma),
-        _p(cos), _p(sin), cos.shape[1], cos.shape[1], eps, _p(slots), _p(q_out), _p(k_pool),
-        _p(v_pool), _p(out), _p(table), _p(lens), _p(tree), batch, T, num_heads, num_kv_heads, D,
-        PAGE, table.shape[1], float(scale), _p(scratch), scratch.nbytes, _stream()),
-        "paged_attention_qk")
+    args = (_p(proj), n, D, num_heads * D, (num_heads + num_kv_heads) * D, _p(q_gamma),
+            _p(k_gamma), _p(cos), _p(sin), cos.shape[1], cos.shape[1], eps, _p(slots), _p(q_out),
+            _p(k_pool), _p(v_pool), _p(out), _p(table), _p(lens), _p(tree), batch, T, num_heads,
+            num_kv_heads, D, PAGE, table.shape[1], float(scale), _p(scratch), scratch.nbytes)
+    if ws_out is None:
+        check(lib.snowverify_paged_attention_qk(*args, _stream()), "paged_attention_qk")
+        return
+    from .gemm import gemm_kquant_a_ws_bytes
+    wneed = gemm_kquant_a_ws_bytes(M, num_heads * D)
+    if ws_out.nbytes < wneed or not ws_out.is_contiguous():
+        raise SnowLLMError(f"paged_attention_qk: the projection workspace needs {wneed} bytes")
+    check(lib.snowverify_paged_attention_qk_ws(*args, _p(ws_out), _stream()),
+          "paged_attention_qk_ws")
 
 
 # ---------------------------------------------------------------------------------------

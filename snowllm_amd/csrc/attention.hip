@@ -25,6 +25,7 @@
 // group); rows >= T*G are padding. Row t of request b sees context keys [0, L - T) and block
 // key j (position L - T + j) iff bit j of its ancestor mask is set (causal: j <= t).
 #include "common.h"
+#include "kquant_core.h"
 #include "qknorm.h"
 
 namespace {
@@ -444,6 +445,100 @@ __global__ void __launch_bounds__(MERGE_THREADS) attn_merge_kernel(AttnArgs a,
   *(u32x2*)dst = u32x2{pack_bf16x2(v[0] * il, v[1] * il), pack_bf16x2(v[2] * il, v[3] * il)};
 }
 
+// The merge that also writes the output projection's operand workspace (D = 256: one head's
+// output is one 256-wide superblock of the projection's input row, so the projection can take
+// prepared operands instead of converting the bf16 output itself). A block covers MWS_ROWS
+// rows x all D columns of one (request, kv head, row tile); thread (group sg, row, word) sums
+// the splits s = sg mod MERGE_SG for 8 columns, and the MERGE_SG partial sums are added in a
+// fixed order: the same sums in the same order as attn_merge_kernel, so the same output bits.
+// Workspace rows are the output rows b * T + t; rows past them are left as they are (the
+// GEMV reads none of their operands).
+constexpr int MWS_ROWS = 2;  // rows per block: two half waves
+constexpr int MWS_THREADS = MWS_ROWS * (256 / 8) * MERGE_SG;  // 256
+
+template <int D>
+__global__ void __launch_bounds__(MWS_THREADS) attn_merge_ws_kernel(AttnArgs a,
+                                                                   uint16_t* __restrict__ out,
+                                                                   void* __restrict__ ws,
+                                                                   size_t tile_bytes) {
+  static_assert(D == 256, "one head per superblock");
+  __shared__ float w[MWS_ROWS][SPLITS_MAX];
+  __shared__ float inv_l[MWS_ROWS];
+  __shared__ floatx4 red[MERGE_SG][MWS_ROWS][D / 8][2];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int prog = blockIdx.x;  // (b, h, tile)
+  const int row0 = blockIdx.y * MWS_ROWS;
+  const int tile = prog % a.NRT, h = (prog / a.NRT) % a.Hkv, b = prog / (a.NRT * a.Hkv);
+  const int64_t pbase = (((int64_t)b * a.Hkv + h) * a.NRT + tile) * a.S;
+  if (wv < MWS_ROWS) {
+    const int row = row0 + wv;
+    float M = -__builtin_huge_valf();
+    for (int s = lane; s < a.S; s += 64) M = fmaxf(M, a.part_ml[((pbase + s) * 16 + row) * 2]);
+    M = wave_max(M);
+    const float Ms = (M == -__builtin_huge_valf()) ? 0.f : M;
+    float lsum = 0.f;
+    for (int s = lane; s < a.S; s += 64) {
+      const float* ml = a.part_ml + ((pbase + s) * 16 + row) * 2;
+      const float ws_ = __builtin_amdgcn_exp2f(ml[0] - Ms);
+      w[wv][s] = ws_;
+      lsum += ws_ * ml[1];
+    }
+    lsum = wave_sum(lsum);
+    if (lane == 0) inv_l[wv] = lsum > 0.f ? 1.0f / lsum : 0.f;
+  }
+  __syncthreads();
+  // wave sg sums splits s = sg mod MERGE_SG; a row's 32 words sit in one half wave (the operand
+  // conversion reduces over it)
+  const int sg = wv, rr = lane >> 5, lw = lane & 31;
+  const int row = row0 + rr;
+  const float* po = a.part_o + (pbase * 16 + row) * D + lw * 8;
+  const int64_t sstride = (int64_t)16 * D * MERGE_SG;
+  floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  int s = sg;
+  po += (int64_t)sg * 16 * D;
+  for (; s + 3 * MERGE_SG < a.S; s += 4 * MERGE_SG, po += 4 * sstride) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const floatx4 x0 = *(const floatx4*)(po + u * sstride);
+      const floatx4 x1 = *(const floatx4*)(po + u * sstride + 4);
+      acc0 += w[rr][s + u * MERGE_SG] * x0;
+      acc1 += w[rr][s + u * MERGE_SG] * x1;
+    }
+  }
+  for (; s < a.S; s += MERGE_SG, po += sstride) {
+    acc0 += w[rr][s] * *(const floatx4*)po;
+    acc1 += w[rr][s] * *(const floatx4*)(po + 4);
+  }
+  red[sg][rr][lw][0] = acc0;
+  red[sg][rr][lw][1] = acc1;
+  __syncthreads();
+  if (sg != 0) return;  // wave 0 (a whole wave) finishes the block
+  floatx4 v0 = red[0][rr][lw][0], v1 = red[0][rr][lw][1];
+#pragma unroll
+  for (int j = 1; j < MERGE_SG; ++j) {
+    v0 += red[j][rr][lw][0];
+    v1 += red[j][rr][lw][1];
+  }
+  const int rg = tile * 16 + row;
+  const bool live = rg < a.T * a.G;
+  const float il = inv_l[rr];
+  const int t = live ? rg / a.G : 0, g = live ? rg % a.G : 0;
+  const int hq = h * a.G + g;
+  const uint32_t yo[4] = {pack_bf16x2(v0[0] * il, v0[1] * il), pack_bf16x2(v0[2] * il, v0[3] * il),
+                          pack_bf16x2(v1[0] * il, v1[1] * il), pack_bf16x2(v1[2] * il, v1[3] * il)};
+  if (live)
+    *(u32x4*)(out + (((int64_t)b * a.T + t) * a.Hq + hq) * D + lw * 8) =
+        u32x4{yo[0], yo[1], yo[2], yo[3]};
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    y[2 * i] = __uint_as_float(yo[i] << 16);
+    y[2 * i + 1] = __uint_as_float(yo[i] & 0xffff0000u);
+  }
+  kq::word_operand(y, hq * 32 + lw, (int64_t)b * a.T + t, ws, tile_bytes,
+                   (int64_t)a.Hq * D / kq::QK, live);
+}
+
 inline int n_row_tiles(int T, int G) { return (T * G + 15) / 16; }
 
 int g_pages_per_split = 0;  // 0: automatic
@@ -543,11 +638,12 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
                          const uint64_t* tree, int64_t batch, int64_t tokens, int64_t num_heads,
                          int64_t num_kv_heads, int64_t head_size, int64_t page_size,
                          int64_t table_stride, float scale, void* scratch, int64_t scratch_bytes,
-                         void* stream) {
+                         void* stream, void* out_ws = nullptr) {
   if (batch <= 0 || tokens <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
       page_size != PAGE || table_stride <= 0)
     return SV_EINVAL;
   if (head_size != 128 && head_size != 256) return SV_ENOTSUP;
+  if (out_ws && head_size != 256) return SV_ENOTSUP;
   if (n_row_tiles((int)tokens, (int)(num_heads / num_kv_heads)) > MAX_TILES) return SV_ENOTSUP;
   if (scratch_bytes < snowverify_paged_attention_scratch_bytes(batch, tokens, num_heads,
                                                               num_kv_heads, head_size))
@@ -583,7 +679,14 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
     rc = launch_split<256>(a, nblocks, s);
     if (rc != SV_OK) return rc;
     SV_CHECK_LAUNCH();
-    hipLaunchKernelGGL(attn_merge_kernel<256>, mgrid, dim3(MERGE_THREADS), 0, s, a, (uint16_t*)out);
+    if (out_ws) {
+      const size_t tb = kq::xprep_tile_bytes(num_heads * head_size / kq::QK);
+      hipLaunchKernelGGL(attn_merge_ws_kernel<256>, dim3(mgrid.x, 16 / MWS_ROWS),
+                         dim3(MWS_THREADS), 0, s, a, (uint16_t*)out, out_ws, tb);
+    } else {
+      hipLaunchKernelGGL(attn_merge_kernel<256>, mgrid, dim3(MERGE_THREADS), 0, s, a,
+                         (uint16_t*)out);
+    }
   }
   SV_CHECK_LAUNCH();
   return SV_OK;
@@ -646,6 +749,46 @@ SV_API int snowverify_paged_attention_qk(
   return paged_attention_impl(a, nullptr, k_pool, v_pool, out, table, lens, tree, batch, tokens,
                               num_heads, num_kv_heads, head_size, page_size, table_stride, scale,
                               scratch, scratch_bytes, stream);
+}
+
+// Extension, no counterpart in the reference: snowverify_paged_attention_qk that also writes
+// the output projection's operand workspace (snowllm_gemm_kquant_a_prepared's ws for the
+// [batch*tokens, num_heads*head_size] output, snowllm_gemm_kquant_a_ws_bytes of that shape), so
+// the projection skips its own conversion of the bf16 output: the same operands, the same
+// bits. head_size 256 only (hipErrorNotSupported otherwise).
+SV_API int snowverify_paged_attention_qk_ws(
+    const void* proj, int64_t proj_stride, int64_t q_head_stride, int64_t k_off, int64_t v_off,
+    const void* q_gamma, const void* k_gamma, const float* cos_in, const float* sin_in,
+    int64_t cs_stride, int64_t half, float eps, const int32_t* slots, void* q_out, void* k_pool,
+    void* v_pool, void* out, const int32_t* table, const int32_t* lens, const uint64_t* tree,
+    int64_t batch, int64_t tokens, int64_t num_heads, int64_t num_kv_heads, int64_t head_size,
+    int64_t page_size, int64_t table_stride, float scale, void* scratch, int64_t scratch_bytes,
+    void* out_ws, void* stream) {
+  if (!out_ws) return SV_EINVAL;
+  if (!proj || !q_gamma || !k_gamma || !cos_in || !sin_in || !slots || half < 0 || half % 32 ||
+      2 * half > head_size || proj_stride % 8 || q_head_stride % 8 || k_off % 8 || v_off % 8)
+    return SV_EINVAL;
+  if (half > 32 * FUSED_MAX_HS) return SV_ENOTSUP;
+  AttnArgs a = {};
+  a.proj = (const uint16_t*)proj;
+  a.proj_stride = proj_stride;
+  a.q_head_stride = q_head_stride;
+  a.k_off = k_off;
+  a.v_off = v_off;
+  a.cs_stride = cs_stride;
+  a.q_gamma = (const uint16_t*)q_gamma;
+  a.k_gamma = (const uint16_t*)k_gamma;
+  a.cosv = cos_in;
+  a.sinv = sin_in;
+  a.slots = slots;
+  a.q_out = (uint16_t*)q_out;
+  a.k_pool_w = (uint16_t*)k_pool;
+  a.v_pool_w = (uint16_t*)v_pool;
+  a.rot_half = (int)half;
+  a.eps = eps;
+  return paged_attention_impl(a, nullptr, k_pool, v_pool, out, table, lens, tree, batch, tokens,
+                              num_heads, num_kv_heads, head_size, page_size, table_stride, scale,
+                              scratch, scratch_bytes, stream, out_ws);
 }
 
 // Tuning knob (extension, no reference counterpart): pages per split of the attention's

@@ -122,41 +122,7 @@ __global__ void __launch_bounds__(NORM_MAX_THREADS) norm_prep_kernel(
     if (res_out) *(u32x4*)(res_out + off) = v;
     if (y_out) *(u32x4*)(y_out + off) = u32x4{yo[0], yo[1], yo[2], yo[3]};
   }
-  // operand conversion of (row, superblock t / 32): power-of-two scale from the maximum
-  float mx = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, __builtin_fabsf(y[i]));
-  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(mx))));
-  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_QUAD_XOR2>(__float_as_uint(mx))));
-  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_HALF_MIRROR>(__float_as_uint(mx))));
-  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_MIRROR>(__float_as_uint(mx))));
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  int e = 0;
-  if (mx > 0.0f && mx <= 3.40282346638528859812e38f) {
-    int E = (int)((__float_as_uint(mx) >> 23) & 0xff) - 127;
-    if (E < -126) E = -126;
-    e = E - 14;  // scaled maximum lands in [2^14, 2^15)
-  }
-  uint16_t h[8];
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const _Float16 hv = (_Float16)__builtin_ldexpf(y[kperm_c(i)], -e);
-    h[i] = __builtin_bit_cast(uint16_t, hv);
-    sum += (float)hv;
-  }
-  // sub-block sum over its four k-groups: (g0 + g1) + (g2 + g3)
-  sum += __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(sum)));
-  sum += __uint_as_float(dpp_u32<DPP_QUAD_XOR2>(__float_as_uint(sum)));
-  if (!act) return;
-  const int sb = t >> 5, j = (t >> 2) & 7, kq = t & 3;
-  const int tile = (int)(row / TILE_M), r = (int)(row % TILE_M);
-  XPrepView view = xprep_view((char*)ws + tile * tile_bytes, H / QK);
-  view.xop[((int64_t)sb * 8 + j) * 64 + r + 16 * kq] =
-      u32x4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
-            h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
-  if (kq == 0) view.sxop[((int64_t)sb * 2 + (j >> 2)) * 64 + r + 16 * (j & 3)] = -sum;
-  if ((t & 31) == 0) view.scale[sb * 16 + r] = __builtin_ldexpf(1.0f, e);
+  word_operand(y, t, row, ws, tile_bytes, H / QK, act);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -135,6 +135,52 @@ __device__ __forceinline__ void convert_superblock(const uint16_t* __restrict__ 
   convert_words(raw, lane, o);
 }
 
+// Operand conversion of one 8-value word of a row, for producers that hold a row as 16-byte
+// words (thread wt of the row holds values 8 wt .. 8 wt + 7, so the 32 words of superblock
+// wt / 32 lie in one half wave and a sub-block's 4 words in one quad): the (row, superblock)
+// power-of-two scale from the maximum over the 32 words, the fp16 values in kperm order and
+// the negated sub-block sums, stored into the workspace of S superblocks per row. The same
+// operands as convert_superblock. Every lane of the wave calls it (DPP); store == false lanes
+// write nothing.
+__device__ __forceinline__ void word_operand(const float (&y)[8], int wt, int64_t row,
+                                             void* __restrict__ ws, size_t tile_bytes, int64_t S,
+                                             bool store) {
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, __builtin_fabsf(y[i]));
+  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(mx))));
+  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_QUAD_XOR2>(__float_as_uint(mx))));
+  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_HALF_MIRROR>(__float_as_uint(mx))));
+  mx = fmaxf(mx, __uint_as_float(dpp_u32<DPP_MIRROR>(__float_as_uint(mx))));
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.40282346638528859812e38f) {
+    int E = (int)((__float_as_uint(mx) >> 23) & 0xff) - 127;
+    if (E < -126) E = -126;
+    e = E - 14;  // scaled maximum lands in [2^14, 2^15)
+  }
+  uint16_t h[8];
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const _Float16 hv = (_Float16)__builtin_ldexpf(y[kperm_c(i)], -e);
+    h[i] = __builtin_bit_cast(uint16_t, hv);
+    sum += (float)hv;
+  }
+  // sub-block sum over its four k-groups: (g0 + g1) + (g2 + g3)
+  sum += __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(sum)));
+  sum += __uint_as_float(dpp_u32<DPP_QUAD_XOR2>(__float_as_uint(sum)));
+  if (!store) return;
+  const int sb = wt >> 5, j = (wt >> 2) & 7, kq = wt & 3;
+  const int tile = (int)(row / TILE_M), r = (int)(row % TILE_M);
+  XPrepView view = xprep_view((char*)ws + tile * tile_bytes, S);
+  view.xop[((int64_t)sb * 8 + j) * 64 + r + 16 * kq] =
+      u32x4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+            h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
+  if (kq == 0) view.sxop[((int64_t)sb * 2 + (j >> 2)) * 64 + r + 16 * (j & 3)] = -sum;
+  if ((wt & 31) == 0) view.scale[sb * 16 + r] = __builtin_ldexpf(1.0f, e);
+}
+
 // Store one superblock's operands into the workspace view.
 __device__ __forceinline__ void store_operands(const XPrepView& v, int64_t s, int lane,
                                                const XOperands& o) {

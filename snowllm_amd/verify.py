@@ -313,11 +313,14 @@ class VerifyModel:
                                        self.ws_h)
             if c.rot_half <= ops.FUSED_QK_MAX_HALF:
                 # QK-norm + RoPE + the block's K/V cache write inside the attention's launches
+                # with 256-wide heads the merge also writes the O projection's operands
+                ws_o = self.ws_a if c.head_dim == 256 else None
                 ops.paged_attention_qk(self.proj, lw.q_norm, lw.k_norm, self.cos, self.sin,
                                        c.eps, self.slots, self.k_pools[i], self.v_pools[i],
                                        self.attn, self.table, self.lens, c.head_dim ** -0.5,
                                        self.attn_scratch, num_heads=c.heads,
-                                       num_kv_heads=c.kv_heads, tree=self.tree, q_out=self.q)
+                                       num_kv_heads=c.kv_heads, tree=self.tree, q_out=self.q,
+                                       ws_out=ws_o)
             else:
                 Lops.qk_norm_rope_cache(self.proj, lw.q_norm, lw.k_norm, self.cos, self.sin,
                                         self.q, self.k_pools[i], self.v_pools[i], self.slots,
@@ -325,8 +328,12 @@ class VerifyModel:
                 ops.paged_attention_explicit(self.q, self.k_pools[i], self.v_pools[i], self.attn,
                                              self.table, self.lens, c.head_dim ** -0.5,
                                              self.attn_scratch, tree=self.tree)
-            ops.gemm_kquant_a(c.attn_fmt, self.attn.view(T, -1), lw.o[0], lw.o[1], self.o, T, H,
-                              c.heads * c.head_dim, self.ws_a)
+            if c.rot_half <= ops.FUSED_QK_MAX_HALF and c.head_dim == 256:
+                ops.gemm_kquant_a_prepared(c.attn_fmt, lw.o[0], lw.o[1], self.o, T, H,
+                                           c.heads * c.head_dim, self.ws_a)
+            else:
+                ops.gemm_kquant_a(c.attn_fmt, self.attn.view(T, -1), lw.o[0], lw.o[1], self.o, T,
+                                  H, c.heads * c.head_dim, self.ws_a)
             # feed-forward block
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
             if c.moe:

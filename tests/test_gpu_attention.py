@@ -178,3 +178,63 @@ def test_fused_qk_attention_refuses_wide_rotation():
                                c(1, 2, dt=torch.int32),
                                torch.tensor([T + 7], dtype=torch.int32, device="cuda"), D ** -0.5,
                                scratch, num_heads=Hq, num_kv_heads=Hkv)
+
+
+@pytest.mark.parametrize("lengths,T,Hq,Hkv,tree", [
+    ([8192 + 9], 9, 16, 2, False),        # config 4 shape
+    ([300 + 3, 1201 + 3], 3, 8, 2, True),  # two requests: workspace rows b * T + t
+])
+def test_merge_writes_projection_operands(lengths, T, Hq, Hkv, tree):
+    """With 256-wide heads the merge can also write the O projection's operand workspace: the
+    attention output and the projection (prepared operands) give the bits of the plain merge
+    followed by the projection converting the bf16 output itself."""
+    from snowllm_amd import ops
+    from snowllm_amd.verify import packed_random
+    D, half, N = 256, 32, 512
+    print(f"merge -> projection operands lengths={lengths} T={T} Hq={Hq} tree={tree}", flush=True)
+    g = torch.Generator().manual_seed(sum(lengths) + T)
+    batch = len(lengths)
+    pages = [(n + 15) // 16 for n in lengths]
+    total = sum(pages) + 3
+    perm = torch.randperm(total, generator=g).int()
+    table = torch.zeros(batch, max(pages), dtype=torch.int32)
+    off = 0
+    for b in range(batch):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    kp0 = torch.randn(total, Hkv, D // 16, 16, 16, generator=g).bfloat16()
+    vp0 = torch.randn(total, Hkv, 4, D, 4, generator=g).bfloat16()
+    proj = torch.randn(batch * T, (Hq + 2 * Hkv) * D, generator=g).bfloat16()
+    qg = (torch.rand(D, generator=g) + .5).bfloat16()
+    kg = (torch.rand(D, generator=g) + .5).bfloat16()
+    pos = torch.cat([torch.arange(n - T, n) for n in lengths])
+    ang = pos[:, None].float() * (1.0 / (1e4 ** (torch.arange(half).float() / half)))[None]
+    slots = torch.cat([(table[b, (torch.arange(n - T, n) // 16)] * 16 + torch.arange(n - T, n) % 16)
+                       for b, n in enumerate(lengths)]).int()
+    tr = None
+    if tree:
+        tr = torch.tensor(to_i64(tree_masks([-1, 0, 0][:T])) * batch, dtype=torch.int64).cuda()
+    w = packed_random(4, N, Hq * D, 77)
+    M, K = batch * T, Hq * D
+    scratch = torch.empty(ops.paged_attention_explicit_scratch_bytes(batch, T, Hq, Hkv, D),
+                          dtype=torch.uint8, device="cuda")
+    res = []
+    for fused_ws in (False, True, True):
+        kp, vp = kp0.clone().cuda(), vp0.clone().cuda()
+        out = torch.empty(M, Hq, D, dtype=torch.bfloat16, device="cuda")
+        ws = torch.full((ops.gemm_kquant_a_ws_bytes(M, K),), 0x7f, dtype=torch.uint8, device="cuda")
+        c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        ops.paged_attention_qk(proj.cuda(), qg.cuda(), kg.cuda(), ang.cos().cuda(), ang.sin().cuda(),
+                               1e-6, slots.cuda(), kp, vp, out, table.cuda(),
+                               torch.tensor(lengths, dtype=torch.int32).cuda(), D ** -0.5, scratch,
+                               num_heads=Hq, num_kv_heads=Hkv, tree=tr,
+                               ws_out=ws if fused_ws else None)
+        if fused_ws:
+            ops.gemm_kquant_a_prepared(4, w[0], w[1], c, M, N, K, ws)
+        else:
+            ops.gemm_kquant_a(4, out.view(M, K), w[0], w[1], c, M, N, K, ws)
+        torch.cuda.synchronize()
+        res.append((out, c, kp, vp))
+    for got in res[1:]:
+        for a_, b_ in zip(res[0], got):
+            assert torch.equal(a_, b_)
