@@ -325,7 +325,7 @@ def bench_step(args, name):
     single = {kk: v for kk, v in kern.items() if "+" not in kk}
     dom = max(single, key=lambda kk: single[kk]["us"])
     d = kern[dom]
-    traffic = read_traffic(dom) if cfg.name == TRAFFIC_WORKLOAD else None
+    traffic = read_traffic(dom) if cfg.name == CONFIGS[TRAFFIC_WORKLOAD].name else None
 
     # reference CPU path (oracle, torch CPU) on a bounded sample: layer 0 x layers + head +
     # acceptance
