@@ -218,8 +218,8 @@ int snowverify_paged_attention_qk_ws(const void* proj, int64_t proj_stride,
  * snowverify_paged_attention; 0 = automatic. Returns the previous value. */
 int snowverify_attention_pages_per_split(int pages);
 /* Extension, no counterpart in the reference (a tuning knob): waves per 16-row tile of the
- * attention's split kernel, 1 or 2 (two split the head's output columns); 0 = automatic.
- * Returns the previous value. */
+ * attention's split kernel, 1 or 2 (two split the head's output columns), or 3 (eight waves,
+ * one or two per tile, for five to seven tiles); 0 = automatic. Returns the previous value. */
 int snowverify_attention_d_split(int dh);
 /* Extension, no counterpart in the reference (a tuning knob): pages in the attention split
  * kernel's LDS ring, 4 or 8; 0 = automatic. Returns the previous value. */

@@ -91,6 +91,11 @@ __device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// s_waitcnt on the LDS/scalar counter only: this wave's LDS writes have completed.
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8));
+}
+
 // s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
 // expcnt 7 and lgkmcnt 15 = no wait on those).
 template <int N>
@@ -146,23 +151,33 @@ constexpr float RESCALE = 8.0f;  // p = 2^(s - m) stays <= 2^8 between rescales
 // chains; P^T of both pages forms one 16x16x32 B operand (slots 0..3 = page A keys 4kq + i,
 // slots 4..7 = page B keys 4kq + i) and V^T reads the same keys of both pages, so O^T += V^T P^T
 // takes half the MFMA cycles of two 16x16x16 steps. Keys of page B are masked when !has_b.
-template <int D, int DH>
+// SPLIT_S (two waves per row tile): each wave of the pair takes the S^T of one page and the
+// pair swaps them through LDS (xch: the tile's two 1 KiB halves), so a K page is read and
+// multiplied once per tile. XBAR: a wave of a mixed workgroup that computes its own S^T takes
+// part in the same barrier. Every wave of a workgroup makes the same number of barrier calls.
+template <int D, int DH, bool SPLIT_S = false, bool XBAR = false>
 __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t* sa,
                                              const uint8_t* sb, bool has_b,
                                              const bf16x8 (&qb)[D / 32], int pg, int L, int ctx,
                                              uint64_t anc, float qk_scale, int kq, int col,
-                                             int dhalf) {
+                                             int dhalf, floatx4 (*xch)[64] = nullptr) {
   using G = SlotGeo<D>;
   constexpr int DS = D / 32, DT = D / 16 / DH;
+  constexpr int NK = SPLIT_S ? 1 : 2;  // pages whose S^T this wave computes
+  static_assert(!SPLIT_S || DH == 2, "S^T is split between the two waves of a tile");
   // every LDS read of the chunk is issued before the first MFMA (V's latency then hides behind
   // the S products and the softmax)
-  u32x4 ka[DS], kb[DS];
+  u32x4 kr[NK][DS];
   u32x2 va[DT], vb[DT];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
     const int off = ((2 * ds + (kq >> 1)) * PAGE + col) * 32 + (kq & 1) * 16;
-    ka[ds] = *(const u32x4*)(sa + off);
-    kb[ds] = *(const u32x4*)(sb + off);
+    if constexpr (NK == 1) {
+      kr[0][ds] = *(const u32x4*)((dhalf ? sb : sa) + off);
+    } else {
+      kr[0][ds] = *(const u32x4*)(sa + off);
+      kr[NK - 1][ds] = *(const u32x4*)(sb + off);
+    }
   }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
@@ -171,11 +186,28 @@ __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t
     vb[dt] = *(const u32x2*)(sb + off);
   }
   __builtin_amdgcn_sched_barrier(0);
-  floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  floatx4 sk[NK];
 #pragma unroll
-  for (int ds = 0; ds < DS; ++ds) {
-    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka[ds]), qb[ds], s0, 0, 0, 0);
-    s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kb[ds]), qb[ds], s1, 0, 0, 0);
+  for (int k = 0; k < NK; ++k) sk[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+    for (int k = 0; k < NK; ++k)
+      sk[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[k][ds]),
+                                                     qb[ds], sk[k], 0, 0, 0);
+  floatx4 s0, s1;
+  if constexpr (SPLIT_S) {
+    const int lane = kq * 16 + col;
+    xch[dhalf][lane] = sk[0];
+    wait_lgkmcnt0();
+    block_barrier();
+    const floatx4 other = xch[dhalf ^ 1][lane];
+    s0 = dhalf ? other : sk[0];
+    s1 = dhalf ? sk[0] : other;
+  } else {
+    if constexpr (XBAR) block_barrier();
+    s0 = sk[0];
+    s1 = sk[NK - 1];
   }
   float sv[8];
   float cmax = -__builtin_huge_valf();
@@ -230,16 +262,32 @@ __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t
   }
 }
 
+// DH: waves per row tile, 1 or 2 for every tile; 3 = mixed: the first 2 NRT - NW tiles have one
+// wave each, the remaining NW - NRT tiles two (the pairs split S^T, see attend_chunk), so that
+// up to eight waves spread the tiles' matrix work evenly over the four SIMDs.
 template <int D, int CPW, int RING, int DH>
-__global__ void __launch_bounds__(DH == 1 ? MAX_TILES * 64 : MAX_TILES_DH * 2 * 64)
+__global__ void __launch_bounds__(DH == 2 ? MAX_TILES_DH * 2 * 64 : MAX_TILES * 64)
 attn_split_kernel(AttnArgs a) {
   using G = SlotGeo<D>;
-  constexpr int DS = D / 32, DT = D / 16 / DH;
+  constexpr int DS = D / 32;
+  constexpr bool MIXED = DH == 3;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING * G::BYTES];
-  const int NW = (int)(blockDim.x >> 6);  // NRT * DH
+  __shared__ floatx4 xch[MIXED ? MAX_TILES : 1][2][64];  // S^T swap of the pairs (mixed)
+  const int NW = (int)(blockDim.x >> 6);  // waves
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int w = wv / DH, dhalf = wv % DH;  // row tile, output-column part
+  int w, dhalf;  // row tile, output-column part
+  bool pair;     // two waves share the tile
+  if constexpr (DH == 1) {
+    w = wv, dhalf = 0, pair = false;
+  } else if constexpr (DH == 2) {
+    w = wv >> 1, dhalf = wv & 1, pair = true;
+  } else {
+    const int nx = 2 * a.NRT - NW;  // single-wave tiles
+    pair = wv >= nx;
+    w = pair ? nx + ((wv - nx) >> 1) : wv;
+    dhalf = pair ? (wv - nx) & 1 : 0;
+  }
   const int kq = lane >> 4, col = lane & 15;
   const int split = blockIdx.x % a.S;
   const int h = (blockIdx.x / a.S) % a.Hkv;
@@ -263,13 +311,43 @@ attn_split_kernel(AttnArgs a) {
   if (a.tree) anc = row_live ? a.tree[(int64_t)b * a.T + t] : 1ull;
   else anc = (t >= 63) ? ~0ull : ((2ull << t) - 1ull);
 
-  AttnState<D, DH> st;
-  // set just before the first chunk, so the accumulators are not live across the prologue
-  auto init_state = [&]() {
+  // the state, set just before the first chunk (the accumulators are not live across the
+  // prologue), and the partial results of a wave holding DHW-th of its tile's columns
+  auto init_state = [&](auto& st) {
+    constexpr int DT = (int)(sizeof(st.o) / sizeof(st.o[0]));
 #pragma unroll
     for (int i = 0; i < DT; ++i) st.o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
     st.m = -__builtin_huge_valf();
     st.l = 0.f;
+  };
+  auto write_partials = [&](auto& st) {
+    constexpr int DT = (int)(sizeof(st.o) / sizeof(st.o[0]));
+    // O^T lane holds row col, d = dt*16 + 4*kq + i
+    const int64_t pidx = ((((int64_t)b * a.Hkv + h) * a.NRT + w) * a.S + split);
+    float* po = a.part_o + pidx * 16 * D + (int64_t)col * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) *(floatx4*)(po + (dhalf * DT + dt) * 16 + 4 * kq) = st.o[dt];
+    // row sums: add the four lanes of each row in a fixed order
+    float l = st.l + __shfl_xor(st.l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (kq == 0 && dhalf == 0) {
+      float* pml = a.part_ml + (pidx * 16 + col) * 2;
+      pml[0] = st.m;
+      pml[1] = l;
+    }
+  };
+  // runs f with this wave's state type (D / 16 / DHW accumulator tiles)
+  auto with_state = [&](auto f) {
+    if constexpr (DH == 1 || DH == 2) {
+      AttnState<D, DH> st;
+      f(st);
+    } else if (pair) {
+      AttnState<D, 2> st;
+      f(st);
+    } else {
+      AttnState<D, 1> st;
+      f(st);
+    }
   };
 
   if (p0 < p1) {  // uniform over the workgroup
@@ -346,34 +424,30 @@ attn_split_kernel(AttnArgs a) {
           *(uint4*)(a.q_out + (m_row * a.Hq + hq) * D + ds * 32 + kq * 8) = o;
       }
     }
-    init_state();
-    int slot = 0;  // first ring slot of the current chunk (even)
-    for (int pg = p0; pg < p1; pg += 2) {
-      wait_vmcnt<(RING - 4) * CPW>();  // this wave's loads of pages pg, pg + 1 have landed
-      block_barrier();                 // ... and every wave's; the previous chunk is free
-      const int prev = slot == 0 ? RING - 2 : slot - 2;
-      issue(pg + RING - 2, prev);
-      issue(pg + RING - 1, prev + 1);
-      attend_chunk<D, DH>(st, ring + slot * G::BYTES, ring + (slot + 1) * G::BYTES, pg + 1 < p1,
-                          qb, pg, L, ctx, anc, a.qk_scale, kq, col, dhalf);
-      slot = slot == RING - 2 ? 0 : slot + 2;
-    }
-    wait_vmcnt<0>();  // no load may still target LDS when the workgroup retires
+    with_state([&](auto& st) {
+      constexpr int DT = (int)(sizeof(st.o) / sizeof(st.o[0]));
+      constexpr int DHW = D / 16 / DT;
+      init_state(st);
+      int slot = 0;  // first ring slot of the current chunk (even)
+      for (int pg = p0; pg < p1; pg += 2) {
+        wait_vmcnt<(RING - 4) * CPW>();  // this wave's loads of pages pg, pg + 1 have landed
+        block_barrier();                 // ... and every wave's; the previous chunk is free
+        const int prev = slot == 0 ? RING - 2 : slot - 2;
+        issue(pg + RING - 2, prev);
+        issue(pg + RING - 1, prev + 1);
+        attend_chunk<D, DHW, MIXED && DHW == 2, MIXED && DHW == 1>(
+            st, ring + slot * G::BYTES, ring + (slot + 1) * G::BYTES, pg + 1 < p1, qb, pg, L, ctx,
+            anc, a.qk_scale, kq, col, dhalf, xch[MIXED ? w : 0]);
+        slot = slot == RING - 2 ? 0 : slot + 2;
+      }
+      wait_vmcnt<0>();  // no load may still target LDS when the workgroup retires
+      write_partials(st);
+    });
   } else {
-    init_state();
-  }
-  // partial results: O^T lane holds row col, d = dt*16 + 4*kq + i
-  const int64_t pidx = ((((int64_t)b * a.Hkv + h) * a.NRT + w) * a.S + split);
-  float* po = a.part_o + pidx * 16 * D + (int64_t)col * D;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) *(floatx4*)(po + (dhalf * DT + dt) * 16 + 4 * kq) = st.o[dt];
-  // row sums: add the four lanes of each row in a fixed order
-  float l = st.l + __shfl_xor(st.l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
-  if (kq == 0 && dhalf == 0) {
-    float* pml = a.part_ml + (pidx * 16 + col) * 2;
-    pml[0] = st.m;
-    pml[1] = l;
+    with_state([&](auto& st) {
+      init_state(st);
+      write_partials(st);
+    });
   }
 }
 
@@ -583,7 +657,7 @@ int g_ring = 0;  // LDS ring pages: 0 automatic, 4 or 8
 template <int D, int DH, int RING>
 int launch_split_ring(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   constexpr int CH = SlotGeo<D>::CHUNKS;
-  const int nw = a.NRT * DH;
+  const int nw = DH == 3 ? MAX_TILES : a.NRT * DH;  // mixed: eight waves
   int cpw = 1;
   while (cpw * nw < CH) cpw *= 2;
   if (RING == 8 && cpw == 16) return launch_split_ring<D, DH, 4>(a, nblocks, s);  // vmcnt range
@@ -605,12 +679,15 @@ int launch_split_dh(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   return launch_split_ring<D, DH, 4>(a, nblocks, s);  // measured: as fast, half the LDS
 }
 
-int g_d_split = 0;  // 0: automatic, 1 or 2 forced
+int g_d_split = 0;  // 0: automatic, 1, 2 or 3 (mixed) forced
 
 template <int D>
 int launch_split(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
-  const int dh = g_d_split ? g_d_split : (a.NRT <= MAX_TILES_DH ? 2 : 1);
+  const int dh = g_d_split ? g_d_split
+                           : (a.NRT <= MAX_TILES_DH ? 2 : a.NRT < MAX_TILES ? 3 : 1);
   if (dh == 2 && a.NRT <= MAX_TILES_DH) return launch_split_dh<D, 2>(a, nblocks, s);
+  if (dh == 3 && a.NRT > MAX_TILES / 2 && a.NRT < MAX_TILES)
+    return launch_split_dh<D, 3>(a, nblocks, s);
   return launch_split_dh<D, 1>(a, nblocks, s);
 }
 
@@ -800,10 +877,11 @@ SV_API int snowverify_attention_pages_per_split(int pages) {
 }
 
 // Tuning knob (extension, no reference counterpart): waves per row tile of the attention's
-// split kernel (1 or 2; 0 restores the automatic choice). Returns the previous value.
+// split kernel (1 or 2; 3 = one or two per tile over eight waves; 0 restores the automatic
+// choice). Returns the previous value.
 SV_API int snowverify_attention_d_split(int dh) {
   const int prev = g_d_split;
-  g_d_split = (dh == 1 || dh == 2) ? dh : 0;
+  g_d_split = (dh == 1 || dh == 2 || dh == 3) ? dh : 0;
   return prev;
 }
 

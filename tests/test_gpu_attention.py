@@ -238,3 +238,49 @@ def test_merge_writes_projection_operands(lengths, T, Hq, Hkv, tree):
     for got in res[1:]:
         for a_, b_ in zip(res[0], got):
             assert torch.equal(a_, b_)
+
+
+@pytest.mark.parametrize("lengths,T,Hq,Hkv,D,tree", [
+    ([8192 + 9], 9, 16, 2, 256, False),          # config 4: five tiles (two single, three pairs)
+    ([3000 + 11], 11, 16, 2, 256, True),          # config 5 rows: six tiles
+    ([700 + 7, 333 + 7], 7, 16, 1, 128, False),   # seven tiles of 128-wide heads
+])
+def test_mixed_tile_waves_equal_one_wave_per_tile(lengths, T, Hq, Hkv, D, tree):
+    """Eight waves with one or two waves per row tile (the pairs split the S products) give the
+    bits of one wave per tile."""
+    from snowllm_amd import ops
+    from snowllm_amd._capi import lib
+    print(f"mixed tile waves lengths={lengths} T={T} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    g = torch.Generator().manual_seed(sum(lengths) + D)
+    batch = len(lengths)
+    pages = [(n + 15) // 16 for n in lengths]
+    total = sum(pages) + 3
+    perm = torch.randperm(total, generator=g).int()
+    table = torch.zeros(batch, max(pages), dtype=torch.int32)
+    off = 0
+    for b in range(batch):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    kp = torch.randn(total, Hkv, D // 16, 16, 16, generator=g).bfloat16().cuda()
+    vp = torch.randn(total, Hkv, 4, D, 4, generator=g).bfloat16().cuda()
+    q = torch.randn(batch * T, Hq, D, generator=g).bfloat16().cuda()
+    tr = None
+    if tree:
+        parents = [-1, 0, 1, 2, 3, 4, 0, 6, 7, 8, 9][:T]
+        tr = torch.tensor(to_i64(tree_masks(parents)) * batch, dtype=torch.int64).cuda()
+    lens = torch.tensor(lengths, dtype=torch.int32).cuda()
+    scratch = torch.empty(ops.paged_attention_explicit_scratch_bytes(batch, T, Hq, Hkv, D),
+                          dtype=torch.uint8, device="cuda")
+    outs = []
+    prev = lib.snowverify_attention_d_split(1)
+    try:
+        for dh in (1, 3):
+            lib.snowverify_attention_d_split(dh)
+            out = torch.empty_like(q)
+            ops.paged_attention_explicit(q, kp, vp, out, table.cuda(), lens, D ** -0.5, scratch,
+                                         tree=tr)
+            torch.cuda.synchronize()
+            outs.append(out)
+    finally:
+        lib.snowverify_attention_d_split(prev)
+    assert torch.equal(outs[0], outs[1])
