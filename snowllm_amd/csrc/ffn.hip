@@ -609,15 +609,16 @@ __device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t*
 
 // bx: the block's tile-group index; slot: the plan slot. DEVICE_SCOPE: the activations are read
 // with device-scope loads. ONE_SB: F / QK == WS, one superblock per wave (no second operand
-// buffer, so fewer registers).
-template <int FMT, int NTILE, int WS, int GPB, bool DEVICE_SCOPE, bool ONE_SB>
+// buffer, so fewer registers). wait(): called once by every wave before the activations are
+// read (in the one-superblock form, with the wave's weights already in flight).
+template <int FMT, int NTILE, int WS, int GPB, bool DEVICE_SCOPE, bool ONE_SB, class Wait>
 __device__ __forceinline__ void moe_down_body(
     int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
     int64_t dn_qbytes, int64_t dn_mbytes, const uint8_t* __restrict__ sh_quant,
     const uint8_t* __restrict__ sh_meta, const MoePlan* __restrict__ plan, int E,
     const uint16_t* __restrict__ act, const float* __restrict__ weights,
     const float* __restrict__ shared_w, float* __restrict__ pairs,
-    float* __restrict__ shared_out, int H, int F) {
+    float* __restrict__ shared_out, int H, int F, Wait&& wait) {
   __shared__ floatx4 part[GPB][WS][NTILE][64];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -655,12 +656,14 @@ __device__ __forceinline__ void moe_down_body(
     SbOperands<FMT, NTILE> o;
     if (live) load_sb<FMT, NTILE, false>(o, st, sw, S, tile0, 1);
     fetch_epilogue();
+    wait();
     if (live) {
       act_operands<FMT, NTILE, DEVICE_SCOPE>(o, slot_act, F, n_rows, sw, lane);
       gemv_superblock<FMT, NTILE>(o, acc, lane >> 4, Mv);
     }
   } else {
     fetch_epilogue();
+    wait();
     if (tile0 < tiles)
       down_loop<FMT, NTILE, WS, DEVICE_SCOPE>(st, slot_act, F, n_rows, sw, S, tile0, lane, Mv,
                                               acc);
@@ -701,7 +704,7 @@ __global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
     float* __restrict__ pairs, float* __restrict__ shared_out, int H, int F) {
   moe_down_body<FMT, NTILE, WS, GPB, false, ONE_SB>(blockIdx.x, blockIdx.y, quant, meta, dn_qbytes,
                                             dn_mbytes, sh_quant, sh_meta, plan, E, act, weights,
-                                            shared_w, pairs, shared_out, H, F);
+                                            shared_w, pairs, shared_out, H, F, [] {});
 }
 
 // ---------------------------------------------------------------------------------------
@@ -760,22 +763,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB
   const int slot = __builtin_amdgcn_readfirstlane(d / dn_per_slot);
   const int didx = __builtin_amdgcn_readfirstlane(d % dn_per_slot);
   if (slot >= n_slots) return;
-  if ((int)threadIdx.x < gu_per_slot) {  // one lane per gate/up item of the slot
-    uint32_t* flag = &g_moe_flags[slot][didx][threadIdx.x];
-    uint32_t polls = 0;
-    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-      if (++polls == MOE_WAIT_POLLS) {
-        __hip_atomic_store(&g_moe_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
+  // the wait for the slot's gate/up items, once the item's weights are in flight
+  auto wait = [&]() {
+    if ((int)threadIdx.x < gu_per_slot) {  // one lane per gate/up item of the slot
+      uint32_t* flag = &g_moe_flags[slot][didx][threadIdx.x];
+      uint32_t polls = 0;
+      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+        if (++polls == MOE_WAIT_POLLS) {
+          __hip_atomic_store(&g_moe_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
       }
-      __builtin_amdgcn_s_sleep(2);
+      __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // sole reader
     }
-    __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // sole reader
-  }
-  __syncthreads();
+    __syncthreads();
+  };
   moe_down_body<FMT, DN_NTILE, DN_WS, DN_GPB, true, ONE_SB>(
       didx, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
-      plan, E, act, weights, shared_w, pairs, shared_out, H, F);
+      plan, E, act, weights, shared_w, pairs, shared_out, H, F, wait);
 }
 
 // out[r, n] = bf16(sum_k pairs[r*topk + k, n] + shared_out[r, n]) in a fixed order
