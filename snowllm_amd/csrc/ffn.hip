@@ -51,20 +51,46 @@ struct MoeSource {
   int topk;
 };
 
+constexpr int MOE_WORDS_INFLIGHT = 8;  // top-k rows whose loads are all issued before the sums
+
 __device__ __forceinline__ u32x4 moe_words(const MoeSource& ms, int64_t row, int64_t H,
                                            int64_t col) {
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < ms.topk; ++k) {
-    const float4* src = (const float4*)(ms.pairs + (row * ms.topk + k) * H + col);
-    const float4 a = src[0], b = src[1];
-    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
-  }
+  float4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
   if (ms.shared) {
     const float4* src = (const float4*)(ms.shared + row * H + col);
-    const float4 a = src[0], b = src[1];
-    acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-    acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+    sa = src[0];
+    sb = src[1];
+  }
+  if (ms.topk <= MOE_WORDS_INFLIGHT) {
+    // every row's loads in flight first, then the sums in the same order as the loop below
+    float4 a[MOE_WORDS_INFLIGHT], b[MOE_WORDS_INFLIGHT];
+#pragma unroll
+    for (int k = 0; k < MOE_WORDS_INFLIGHT; ++k) {
+      if (k < ms.topk) {
+        const float4* src = (const float4*)(ms.pairs + (row * ms.topk + k) * H + col);
+        a[k] = src[0];
+        b[k] = src[1];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < MOE_WORDS_INFLIGHT; ++k) {
+      if (k < ms.topk) {
+        acc[0] += a[k].x; acc[1] += a[k].y; acc[2] += a[k].z; acc[3] += a[k].w;
+        acc[4] += b[k].x; acc[5] += b[k].y; acc[6] += b[k].z; acc[7] += b[k].w;
+      }
+    }
+  } else {
+    for (int k = 0; k < ms.topk; ++k) {
+      const float4* src = (const float4*)(ms.pairs + (row * ms.topk + k) * H + col);
+      const float4 a = src[0], b = src[1];
+      acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+      acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+    }
+  }
+  if (ms.shared) {  // the shared expert's row last
+    acc[0] += sa.x; acc[1] += sa.y; acc[2] += sa.z; acc[3] += sa.w;
+    acc[4] += sb.x; acc[5] += sb.y; acc[6] += sb.z; acc[7] += sb.w;
   }
   return u32x4{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
                pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7])};
@@ -86,13 +112,15 @@ __global__ void __launch_bounds__(NORM_MAX_THREADS) norm_prep_kernel(
   u32x4 v = {0u, 0u, 0u, 0u}, gv = {0u, 0u, 0u, 0u};
   if (act) gv = *(const u32x4*)(gamma + (int64_t)t * 8);
   if (live) {
+    u32x4 rv = {0u, 0u, 0u, 0u};
+    if (residual) rv = *(const u32x4*)(residual + off);  // in flight with the row's loads
     if (ms.pairs) {
       v = moe_words(ms, row, H, (int64_t)t * 8);
       if (ms.x_out) *(u32x4*)(ms.x_out + off) = v;
     } else {
       v = *(const u32x4*)(x + off);
     }
-    if (residual) v = add_bf16_words(v, *(const u32x4*)(residual + off));
+    if (residual) v = add_bf16_words(v, rv);
   }
   const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, gw[4] = {gv.x, gv.y, gv.z, gv.w};
   float ss = 0.f;
