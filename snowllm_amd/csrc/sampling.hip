@@ -92,6 +92,17 @@ __device__ __forceinline__ float row_temperature(const float* temperature, int r
   return (t > 0.0f) ? t : 1.0f;
 }
 
+// A thread's RUN elements base + k NT of a row of V, every load issued before the first use
+// (indices past the row read its last element; callers skip them).
+__device__ __forceinline__ void load_run(const float* __restrict__ x, int64_t base, int64_t V,
+                                         float (&v)[RUN]) {
+#pragma unroll
+  for (int k = 0; k < RUN; ++k) {
+    const int64_t i = base + (int64_t)k * NT;
+    v[k] = x[i < V ? i : V - 1];
+  }
+}
+
 __global__ void __launch_bounds__(NT) softmax_max(const float* __restrict__ logits, int64_t V,
                                                   const float* __restrict__ temperature,
                                                   SoftmaxTail tail, int C) {
@@ -100,10 +111,13 @@ __global__ void __launch_bounds__(NT) softmax_max(const float* __restrict__ logi
   const float* x = logits + (int64_t)row * V;
   const float T = row_temperature(temperature, row);
   uint64_t best = 0;
+  const int64_t base = (int64_t)c * CHUNK + threadIdx.x;
+  float xv[RUN];
+  load_run(x, base, V, xv);
+#pragma unroll
   for (int k = 0; k < RUN; ++k) {
-    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
-    if (i < V) {
-      uint32_t key = ord_key(__fdiv_rn(x[i], T));
+    if (base + (int64_t)k * NT < V) {
+      uint32_t key = ord_key(__fdiv_rn(xv[k], T));
       best = key > best ? key : best;
     }
   }
@@ -137,10 +151,14 @@ __global__ void __launch_bounds__(NT) softmax_exp(const float* __restrict__ logi
   float* e = dense + (int64_t)row * V;
   const float T = row_temperature(temperature, row);
   uint64_t sum = 0;
+  const int64_t base = (int64_t)c * CHUNK + threadIdx.x;
+  float xv[RUN];
+  load_run(x, base, V, xv);
+#pragma unroll
   for (int k = 0; k < RUN; ++k) {
-    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    const int64_t i = base + (int64_t)k * NT;
     if (i < V) {
-      float v = canon_exp(__fsub_rn(__fdiv_rn(x[i], T), M));
+      float v = canon_exp(__fsub_rn(__fdiv_rn(xv[k], T), M));
       e[i] = v;
       sum += canon_fix(v);
     }
@@ -162,9 +180,13 @@ __global__ void __launch_bounds__(NT) softmax_norm(float* __restrict__ dense, in
   __syncthreads();
   const float Z = s_z;
   float* e = dense + (int64_t)row * V;
+  const int64_t base = (int64_t)c * CHUNK + threadIdx.x;
+  float ev[RUN];
+  load_run(e, base, V, ev);
+#pragma unroll
   for (int k = 0; k < RUN; ++k) {
-    int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
-    if (i < V) e[i] = (Z > 0.0f) ? canon_div(e[i], Z) : 0.0f;
+    const int64_t i = base + (int64_t)k * NT;
+    if (i < V) e[i] = (Z > 0.0f) ? canon_div(ev[k], Z) : 0.0f;
   }
 }
 
