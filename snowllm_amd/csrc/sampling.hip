@@ -558,9 +558,11 @@ struct ResidualRow {
   bool subtract;        // false for the bonus position
   const uint32_t* bits = nullptr;  // staged rows: bit (id mod 2^16) set for every candidate id
   __device__ float operator()(int64_t k) const {
-    float pk = p[k];
+    return from_loaded(k, p[k], subtract ? ids[k] : 0);
+  }
+  // The same residual from p[k] and ids[k] already loaded (id unused for the bonus position).
+  __device__ float from_loaded(int64_t k, float pk, int64_t id) const {
     if (!subtract) return pk;
-    const int64_t id = ids[k];
     float qk;
     if (bits) {
       // q(id) = 0 unless id may be a candidate; candidates are then searched exactly
@@ -643,11 +645,21 @@ __global__ void __launch_bounds__(NT) reject_chunks(RejectArgs a, int C) {
   ResidualRow w = residual_row(a, r, first);
   stage_q(w, s_cand, s_q, s_bits);
   uint64_t rs = 0, ps = 0;
+  // every p and id load of the thread in flight before the first residual
+  float pv[RUN];
+  int64_t idv[RUN];
 #pragma unroll
   for (int k = 0; k < RUN; ++k) {
     const int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
     const int64_t ii = i < a.p_width ? i : a.p_width - 1;  // loads stay unconditional
-    const uint64_t r1 = canon_fix(w(ii)), p1 = canon_fix(w.p[ii]);
+    pv[k] = w.p[ii];
+    idv[k] = w.subtract ? w.ids[ii] : 0;
+  }
+#pragma unroll
+  for (int k = 0; k < RUN; ++k) {
+    const int64_t i = (int64_t)c * CHUNK + threadIdx.x + (int64_t)k * NT;
+    const int64_t ii = i < a.p_width ? i : a.p_width - 1;
+    const uint64_t r1 = canon_fix(w.from_loaded(ii, pv[k], idv[k])), p1 = canon_fix(pv[k]);
     if (i < a.p_width) {
       rs += r1;
       ps += p1;
