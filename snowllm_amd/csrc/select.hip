@@ -100,10 +100,16 @@ __global__ void __launch_bounds__(SEL_NT) select_chunks(const float* __restrict_
   const float* x = logits + row * V;
   uint64_t keys[SEL_RUN];
   uint64_t mine = 0;
+  float xv[SEL_RUN];
+#pragma unroll
+  for (int i = 0; i < SEL_RUN; ++i) {  // every load in flight before the first key
+    const int64_t id = (int64_t)c * SEL_CHUNK + i * SEL_NT + t;
+    xv[i] = x[id < V ? id : V - 1];
+  }
 #pragma unroll
   for (int i = 0; i < SEL_RUN; ++i) {
     const int64_t id = (int64_t)c * SEL_CHUNK + i * SEL_NT + t;
-    keys[i] = id < V ? sel_key(x[id], (uint32_t)id) : 0ull;
+    keys[i] = id < V ? sel_key(xv[i], (uint32_t)id) : 0ull;
     mine = keys[i] > mine ? keys[i] : mine;
   }
   s_max[t] = mine;
