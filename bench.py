@@ -278,6 +278,10 @@ def bench_step(args, name):
         g.replay()
     torch.cuda.synchronize()
     ms = time_events(lambda: g.replay(), args.steps, stream)
+    torch.cuda.synchronize()
+    if cfg.moe and Lops.moe_sync_error() != 0:
+        raise RuntimeError("a MoE expert hand-off timed out during the timed steps "
+                           "(its outputs were poisoned with NaN)")
     emitted = int(acc.accepted[0])  # accepted drafts + the correction/bonus token
     out_tokens = acc.out[0, :emitted].tolist()
     step_gbs = alg / (ms * 1e-3) / 1e9
@@ -336,12 +340,14 @@ def bench_step(args, name):
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_k weights x bf16 activations (fp16/bf16 MFMA, fp32 accumulate)",
-        "data": "synthetic, random-init weights (seeded), BASELINE generators",
+        "data": weights_note(cfg),
         "config": {"workload": cfg.name, "layers": cfg.layers, "hidden": cfg.hidden,
                    "block_rows": T, "context": cfg.context, "vocab": V,
                    "experts": cfg.experts, "topk": cfg.topk,
                    "attn_fmt": "q4_k" if cfg.attn_fmt == 4 else "q8_0",
-                   "tree": bool(cfg.tree_parents), "selector": sel is not None},
+                   "tree": bool(cfg.tree_parents), "selector": sel is not None,
+                   "rope": {"theta": cfg.rope_theta, "rotary_dims": 2 * cfg.rot_half,
+                            "head_dim": cfg.head_dim}},
         "verify_step_us": round(ms * 1e3, 1),
         "accepted_per_step": emitted, "accepted_drafts": emitted - 1,
         "emitted_tokens": out_tokens,
@@ -359,6 +365,20 @@ def bench_step(args, name):
                          "kind": "port", "cpu": cpu_model(), "sample": cpu["sample"],
                          "step_s": round(cpu["step_s"], 3)},
     }
+
+
+def weights_note(cfg):
+    """What the random-init weights are, for the JSON line."""
+    if cfg.centered:
+        q4 = ("Q4_K blocks zero-mean (d ~|N(0,2e-4^2)|, dmin = 8d, m = round(0.9375 sc)) so "
+              "that router logits stay ~N(0,1) per row; config 2's uniform mins would route "
+              "every row to the same experts")
+    else:
+        q4 = "Q4_K blocks from BASELINE config 2's generator"
+    q8 = "; Q8_0 attention as BASELINE config 5" if cfg.attn_fmt == 8 else ""
+    return (f"synthetic, random-init seeded weights: {q4}{q8}; fp16 embedding and LM head "
+            f"~N(0,0.02^2); bf16 router ~N(0,1/H); KV ~N(0,1); draft side from BASELINE "
+            f"config 1's generators")
 
 
 def chain_rows(parents):

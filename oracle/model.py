@@ -93,7 +93,15 @@ class LayerRef:
         return self._experts[e]
 
 
+def inv_freq(theta, rot_half):
+    """RoPE inverse frequencies theta^(-j / rot_half), j < rot_half: rotary dims 2*rot_half
+    in (i, i + rot_half) pairs (snowllm/ops/rope.py:11-24 takes them as a tensor)."""
+    return 1.0 / (theta ** (torch.arange(rot_half, dtype=torch.float32) / rot_half))
+
+
 def swiglu_ffn(x, gu, dn, F):
+    """SwiGLU over packed gate/up rows (gate rows first: snowllm/models/qwen3_5/
+    qwen3_5_weights.py:216,233 concatenates gate_proj then up_proj): down(silu(g) * u)."""
     g = linear(x, gu[:F])
     u = linear(x, gu[F:])
     act = bf(g / (1 + torch.exp(-g)) * u)
@@ -134,10 +142,40 @@ def route(logits, E, K):
     return ids, w / w.sum(-1, keepdim=True), torch.sigmoid(logits[:, E])
 
 
+def qk_norm_rope(t, gamma, cos, sin, half, eps):
+    """Per-head RMSNorm, then RoPE, rounded once to bf16 (snowllm/ops/attention_full.py:
+    736-784 normalises before it rotates; tests/test_lfm2_dspark_reference.py:16-27)."""
+    n = t * torch.rsqrt(t.square().mean(-1, keepdim=True) + eps) * gamma
+    return bf(rope(n, cos, sin, half))
+
+
+def moe_ffn(ref, h2, logits):
+    """Qwen-Next MoE of the normed rows h2 [T, H] given router logits [T, E + 1]: each row's
+    top-K experts weighted by the renormalised softmax, plus the shared expert weighted by
+    sigmoid(logit E); every expert output is a bf16 tensor, the weighted sum is rounded once.
+    Returns (output [T, H], routed ids [T, K])."""
+    c = ref.cfg
+    E, F, K = c.experts, c.expert_ffn, c.topk
+    T = h2.shape[0]
+    ids, w, gate = route(logits, E, K)
+    out = torch.zeros(T, c.hidden)
+    for t in range(T):
+        acc = torch.zeros(c.hidden)
+        for kk in range(K):
+            gu, dn = ref.expert(int(ids[t, kk]))
+            y = swiglu_ffn(h2[t:t + 1], gu, dn, F)[0]
+            acc += y * w[t, kk]
+        sh = swiglu_ffn(h2[t:t + 1], ref.sh_gu, ref.sh_dn, F)[0]
+        acc += sh * gate[t]
+        out[t] = acc
+    return bf(out), ids
+
+
 def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
     """One layer. x: block input [T, H] (bf16 values), res: residual stream or None,
     k_ctx/v_ctx: context keys/values [ctx, Hkv, D]; masks: per-row visibility bits over the
-    block. Returns (ffn output x', residual after the FFN update, attention output, routing)."""
+    block. Returns (FFN output x', the residual stream after the attention update r2 = o + r1,
+    attention output, routed ids or None). The next layer's input is x' with residual r2."""
     c = ref.cfg
     T = x.shape[0]
     D, Hq, Hkv = c.head_dim, c.heads, c.kv_heads
@@ -148,11 +186,8 @@ def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
     k = proj[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D)
     v = proj[:, (Hq + Hkv) * D:].view(T, Hkv, D)
 
-    def head_norm(t, g):
-        return t * torch.rsqrt(t.square().mean(-1, keepdim=True) + c.eps) * g
-
-    q = bf(rope(head_norm(q, ref.q_norm), cos, sin, c.rot_half))
-    k = bf(rope(head_norm(k, ref.k_norm), cos, sin, c.rot_half))
+    q = qk_norm_rope(q, ref.q_norm, cos, sin, c.rot_half, c.eps)
+    k = qk_norm_rope(k, ref.k_norm, cos, sin, c.rot_half, c.eps)
     keys = torch.cat([k_ctx.float(), k])
     vals = torch.cat([v_ctx.float(), v])
     attn = bf(masked_attention(q, keys, vals, visibility(k_ctx.shape[0], masks), D ** -0.5))
@@ -161,21 +196,8 @@ def layer_forward(ref, x, res, cos, sin, k_ctx, v_ctx, masks):
     h2 = rmsnorm(r2, ref.post_norm, c.eps)
     routing = None
     if c.moe:
-        E, F, K = c.experts, c.expert_ffn, c.topk
         logits = (h2.double() @ ref.router.double().T).float()
-        ids, w, gate = route(logits, E, K)
-        out = torch.zeros(T, c.hidden)
-        for t in range(T):
-            acc = torch.zeros(c.hidden)
-            for kk in range(K):
-                gu, dn = ref.expert(int(ids[t, kk]))
-                y = swiglu_ffn(h2[t:t + 1], gu, dn, F)[0]
-                acc += y * w[t, kk]
-            sh = swiglu_ffn(h2[t:t + 1], ref.sh_gu, ref.sh_dn, F)[0]
-            acc += sh * gate[t]
-            out[t] = acc
-        x2 = bf(out)
-        routing = ids
+        x2, routing = moe_ffn(ref, h2, logits)
     else:
         x2 = swiglu_ffn(h2, ref.gu, ref.dn, c.ffn)
     return x2, r2, attn, routing

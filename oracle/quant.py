@@ -43,33 +43,35 @@ def pack_scales_min_k4(sc: np.ndarray, mn: np.ndarray) -> np.ndarray:
     return s.astype(np.uint8)
 
 
-def _f16(b: np.ndarray, off: int) -> np.ndarray:
-    return np.ascontiguousarray(b[:, off:off + 2]).view(np.float16).astype(np.float32)[:, 0]
-
-
 def dequant_q4_k(raw: np.ndarray, n: int, k: int) -> np.ndarray:
-    """[n*k/256*144] bytes -> float32 [n, k] (dequant.py:82-92, in fp32 like the reference)."""
-    b = np.asarray(raw, dtype=np.uint8).reshape(-1, Q4_K_BYTES)
+    """[n*k/256*144] bytes -> float32 [n, k] (dequant.py:82-92, in fp32 like the reference).
+    Each weight is fp32(d * sc_j) * q - fp32(dmin * m_j), as there; torch ops only for speed."""
+    b = torch.from_numpy(np.ascontiguousarray(np.asarray(raw, dtype=np.uint8)).reshape(-1, Q4_K_BYTES))
     nb = b.shape[0]
-    d, dmin = _f16(b, 0), _f16(b, 2)
-    sc, mn = scales_min_k4(b[:, 4:16])
-    q = b[:, 16:144].astype(np.int32).reshape(nb, 4, 32)
-    d1 = (d[:, None] * sc[:, 0::2].astype(np.float32)).astype(np.float32)
-    m1 = (dmin[:, None] * mn[:, 0::2].astype(np.float32)).astype(np.float32)
-    d2 = (d[:, None] * sc[:, 1::2].astype(np.float32)).astype(np.float32)
-    m2 = (dmin[:, None] * mn[:, 1::2].astype(np.float32)).astype(np.float32)
-    out = np.empty((nb, 4, 64), dtype=np.float32)
-    out[:, :, :32] = d1[..., None] * (q & 0xF).astype(np.float32) - m1[..., None]
-    out[:, :, 32:] = d2[..., None] * (q >> 4).astype(np.float32) - m2[..., None]
-    return out.reshape(n, k)
+    dd = b[:, 0:4].contiguous().view(torch.float16).float()
+    d, dmin = dd[:, 0], dd[:, 1]
+    s = b[:, 4:16].int()
+    sc = torch.empty(nb, 8, dtype=torch.int32)
+    mn = torch.empty_like(sc)
+    sc[:, :4] = s[:, 0:4] & 63
+    mn[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)
+    mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    q = b[:, 16:144].reshape(nb, 4, 32)
+    dsc = d[:, None] * sc.float()
+    dmn = dmin[:, None] * mn.float()
+    out = torch.empty(nb, 4, 2, 32)
+    out[:, :, 0] = dsc[:, 0::2, None] * (q & 0xF).float() - dmn[:, 0::2, None]
+    out[:, :, 1] = dsc[:, 1::2, None] * (q >> 4).float() - dmn[:, 1::2, None]
+    return out.reshape(n, k).numpy()
 
 
 def dequant_q8_0(raw: np.ndarray, n: int, k: int) -> np.ndarray:
     """[n*k/32*34] bytes -> float32 [n, k] (dequant.py:31-32)."""
-    b = np.asarray(raw, dtype=np.uint8).reshape(-1, Q8_0_BYTES)
-    d = _f16(b, 0)
-    q = np.ascontiguousarray(b[:, 2:34]).view(np.int8).astype(np.float32)
-    return (d[:, None] * q).reshape(n, k)
+    b = torch.from_numpy(np.ascontiguousarray(np.asarray(raw, dtype=np.uint8)).reshape(-1, Q8_0_BYTES))
+    d = b[:, 0:2].contiguous().view(torch.float16).float()
+    q = b[:, 2:34].contiguous().view(torch.int8).float()
+    return (d * q).reshape(n, k).numpy()
 
 
 def make_q4_k(n: int, k: int, seed: int, d_std: float = 1e-3) -> np.ndarray:
@@ -81,6 +83,25 @@ def make_q4_k(n: int, k: int, seed: int, d_std: float = 1e-3) -> np.ndarray:
     sc = torch.randint(0, 64, (nb, 8), generator=g).numpy()
     mn = torch.randint(0, 64, (nb, 8), generator=g).numpy()
     dd = (torch.randn(nb, 2, generator=g) * d_std).abs().half().numpy()
+    qs = torch.randint(0, 256, (nb, 128), generator=g, dtype=torch.int32).numpy().astype(np.uint8)
+    blk = np.empty((nb, Q4_K_BYTES), dtype=np.uint8)
+    blk[:, 0:4] = dd.view(np.uint8).reshape(nb, 4)
+    blk[:, 4:16] = pack_scales_min_k4(sc, mn)
+    blk[:, 16:] = qs
+    return blk.reshape(-1)
+
+
+def make_q4_k_centered(n: int, k: int, seed: int, d_std: float = 2e-4) -> np.ndarray:
+    """Zero-mean synthetic Q4_K weight: scales uniform 0..63, m_j = round(0.9375 sc_j),
+    d = fp16(|N(0, d_std^2)|), dmin = fp16(8 d), so that w = d sc_j q - dmin m_j is about
+    d sc_j (q - 7.5). Returns uint8 [n*k/256*144]."""
+    assert k % QK_K == 0
+    g = torch.Generator().manual_seed(seed)
+    nb = n * k // QK_K
+    sc = torch.randint(0, 64, (nb, 8), generator=g).numpy()
+    mn = np.clip(np.round(sc * 0.9375), 0, 63).astype(np.int64)
+    d = (torch.randn(nb, generator=g) * d_std).abs()
+    dd = torch.stack([d, 8 * d], 1).half().numpy()
     qs = torch.randint(0, 256, (nb, 128), generator=g, dtype=torch.int32).numpy().astype(np.uint8)
     blk = np.empty((nb, Q4_K_BYTES), dtype=np.uint8)
     blk[:, 0:4] = dd.view(np.uint8).reshape(nb, 4)

@@ -176,7 +176,10 @@ __global__ void __launch_bounds__(NW * 64) dense_gemv(const u32x4* __restrict__ 
   const int tiles = (N + TILE_N - 1) / TILE_N;
   const int tile0 = blockIdx.x * NTILE;
   const int K = S * QK;
-  __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc((void*)w, 0, tiles * S * 8 * 64 * 16, 0x00020000);
+  // the block's own tiles as the buffer: offsets stay 32-bit whatever N * K is
+  const int own = tiles - tile0 < NTILE ? tiles - tile0 : NTILE;
+  __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(w + (int64_t)tile0 * S * 8 * 64), 0, own * S * 8 * 64 * 16, 0x00020000);
   __amdgpu_buffer_rsrc_t xr, sr;
   uint32_t vx, vs;
   if constexpr (WT == WT_F16) {
@@ -208,7 +211,7 @@ __global__ void __launch_bounds__(NW * 64) dense_gemv(const u32x4* __restrict__ 
     for (int t = 0; t < NTILE; ++t)
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        wb[t][j] = bload4(wr, lane * 16, (uint32_t)((((tile0 + t) * S + s) * 8 + j) * 64 * 16));
+        wb[t][j] = bload4(wr, lane * 16, (uint32_t)(((t * S + s) * 8 + j) * 64 * 16));
 #pragma unroll
     for (int t = 0; t < NTILE; ++t) {
       floatx4 sb = {0.f, 0.f, 0.f, 0.f};
@@ -280,7 +283,12 @@ struct MoePlan {
   int32_t slot_rows[MOE_MAX_SLOTS];        // rows routed to the slot
   int32_t row_of[MOE_MAX_SLOTS][16];       // compact position -> block row
   int32_t pair_of[MOE_MAX_SLOTS][16];      // compact position -> pair index (-1: shared)
+  uint32_t epoch;                          // nonzero, new for every plan written
 };
+
+// Plan generation counter: every plan kernel takes the next value (skipping 0) for its plan.
+// Plan kernels are stream-ordered on one device, so one thread updates it without atomics.
+__device__ uint32_t g_moe_epoch;
 
 // Row gather for one wave: compact row r = lane & 15 of the slot reads block row row_of[r]
 // from the operand workspace; rows past the slot's count read zeros (out-of-range offsets).
@@ -507,6 +515,10 @@ __device__ __forceinline__ void build_plan(const int32_t* ids_s, int M, int topk
       plan->slot_rows[off + before] = __popc(mask[t]);
     }
     if (t == 0) {
+      uint32_t ep = g_moe_epoch + 1u;
+      ep = ep ? ep : 1u;
+      g_moe_epoch = ep;
+      plan->epoch = ep;
       plan->n_routed = n_routed;
       if (shared) {
         plan->slot_expert[n_routed] = E;
@@ -638,7 +650,9 @@ __device__ __forceinline__ void down_loop(const GemvStreams& st, const uint16_t*
 // bx: the block's tile-group index; slot: the plan slot. DEVICE_SCOPE: the activations are read
 // with device-scope loads. ONE_SB: F / QK == WS, one superblock per wave (no second operand
 // buffer, so fewer registers). wait(): called once by every wave before the activations are
-// read (in the one-superblock form, with the wave's weights already in flight).
+// read (in the one-superblock form, with the wave's weights already in flight); it returns
+// true (the same in every wave) when the activations were never published, and the item then
+// writes NaN to every output it owns, so that a failed hand-off cannot pass as a result.
 template <int FMT, int NTILE, int WS, int GPB, bool DEVICE_SCOPE, bool ONE_SB, class Wait>
 __device__ __forceinline__ void moe_down_body(
     int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
@@ -677,6 +691,7 @@ __device__ __forceinline__ void moe_down_body(
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
   const uint16_t* slot_act = act + (int64_t)slot * 16 * F;
+  bool poisoned = false;
   if constexpr (ONE_SB) {
     // one superblock per wave (S == WS): its weights go out first, then the epilogue's
     // operands, then the activations
@@ -684,14 +699,14 @@ __device__ __forceinline__ void moe_down_body(
     SbOperands<FMT, NTILE> o;
     if (live) load_sb<FMT, NTILE, false>(o, st, sw, S, tile0, 1);
     fetch_epilogue();
-    wait();
+    poisoned = wait();
     if (live) {
       act_operands<FMT, NTILE, DEVICE_SCOPE>(o, slot_act, F, n_rows, sw, lane);
       gemv_superblock<FMT, NTILE>(o, acc, lane >> 4, Mv);
     }
   } else {
     fetch_epilogue();
-    wait();
+    poisoned = wait();
     if (tile0 < tiles)
       down_loop<FMT, NTILE, WS, DEVICE_SCOPE>(st, slot_act, F, n_rows, sw, S, tile0, lane, Mv,
                                               acc);
@@ -718,7 +733,7 @@ __device__ __forceinline__ void moe_down_body(
       if (rb + i >= n_rows) break;  // compact row
       const float y = bf16_to_f32(f32_to_bf16(acc[t][i]));  // expert outputs are bf16 tensors
       float* out = e >= E ? shared_out : pairs;
-      out[(int64_t)dst[i] * H + n] = y * gate[i];
+      out[(int64_t)dst[i] * H + n] = poisoned ? __builtin_nanf("") : y * gate[i];
     }
   }
 }
@@ -732,20 +747,33 @@ __global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
     float* __restrict__ pairs, float* __restrict__ shared_out, int H, int F) {
   moe_down_body<FMT, NTILE, WS, GPB, false, ONE_SB>(blockIdx.x, blockIdx.y, quant, meta, dn_qbytes,
                                             dn_mbytes, sh_quant, sh_meta, plan, E, act, weights,
-                                            shared_w, pairs, shared_out, H, F, [] {});
+                                            shared_w, pairs, shared_out, H, F,
+                                            [] { return false; });
 }
 
 // ---------------------------------------------------------------------------------------
 // Gate/up and down of every slot in one launch. Workgroups 0 .. GU-1 run gate/up items
 // (slot-major), the rest down items (slot-major). A gate/up item stores its activations with
-// device-scope stores and, once every wave's stores have completed, sets its flag in each of
-// its slot's down items' flag lines; a down item waits until the flags of all of its slot's
-// gate/up items are set in its own line, clears them for the next launch and reads the
-// activations with device-scope loads. Each line has one reader, so nothing is counted and no
-// address is contended. Workgroups start in index order on each XCD, so a waiting item only
-// waits for items that have started and wait for nothing; the wait is bounded all the same,
-// and a time-out is recorded in g_moe_error. The flags are library-owned: launches of this
-// kernel on one device must be stream-ordered.
+// device-scope stores and, once every wave's stores have completed, writes the plan's epoch
+// into its flag in each of its slot's down items' flag lines; a down item waits until the
+// flags of all of its slot's gate/up items hold the epoch in its own line, clears them and
+// reads the activations with device-scope loads. Each line has one reader, so nothing is
+// counted and no address is contended.
+//
+// Progress: every gate/up item has a lower workgroup index than every down item, and
+// workgroups are dispatched in index order (per XCD, and so overall for the ones an XCD
+// holds), so when a gate/up item waits for a CU slot, every workgroup holding one on its XCD
+// has a lower index: a gate/up item, which waits for nothing. Every gate/up item therefore
+// runs, and every wait ends. The wait is bounded all the same: on a time-out the down item
+// records g_moe_error and writes NaN instead of its outputs.
+//
+// Ordering: the activation stores and loads are device-scope (sc1) and the flags are
+// device-scope atomics; each gate/up wave waits for its stores' completion (vmcnt(0)) before
+// the barrier that precedes the flag store, and a down item issues its activation loads only
+// after its flag loads returned the epoch. The epoch comes from the plan, so a flag left set by
+// a gate/up item that finished after its down item gave up never matches a later plan; the
+// clear lets a plan be run twice. The flags are library-owned: launches of this kernel on one
+// device must be stream-ordered.
 // ---------------------------------------------------------------------------------------
 constexpr int MOE_MAX_ITEMS = 32;  // gate/up or down items per slot
 __device__ __align__(256) uint32_t g_moe_flags[MOE_MAX_SLOTS][MOE_MAX_ITEMS][MOE_MAX_ITEMS];
@@ -770,6 +798,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB
   const int item = blockIdx.x;
   const int n_gu = gu_per_slot * max_slots;
   const int n_slots = plan->n_slots;
+  const uint32_t epoch = plan->epoch;
   if (item < n_gu) {
     const int slot = item / gu_per_slot;
     if (slot >= n_slots) return;
@@ -781,7 +810,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if ((int)threadIdx.x < dn_per_slot)
-      __hip_atomic_store(&g_moe_flags[slot][threadIdx.x][item % gu_per_slot], 1u,
+      __hip_atomic_store(&g_moe_flags[slot][threadIdx.x][item % gu_per_slot], epoch,
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
@@ -792,13 +821,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB
   const int didx = __builtin_amdgcn_readfirstlane(d % dn_per_slot);
   if (slot >= n_slots) return;
   // the wait for the slot's gate/up items, once the item's weights are in flight
-  auto wait = [&]() {
+  __shared__ uint32_t timed_out;
+  auto wait = [&]() -> bool {
+    if (threadIdx.x == 0) timed_out = 0u;  // wave 0 holds every polling lane
     if ((int)threadIdx.x < gu_per_slot) {  // one lane per gate/up item of the slot
       uint32_t* flag = &g_moe_flags[slot][didx][threadIdx.x];
       uint32_t polls = 0;
-      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+      while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
         if (++polls == MOE_WAIT_POLLS) {
           __hip_atomic_store(&g_moe_error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          timed_out = 1u;
           break;
         }
         __builtin_amdgcn_s_sleep(2);
@@ -806,6 +838,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB
       __hip_atomic_store(flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // sole reader
     }
     __syncthreads();
+    return __builtin_amdgcn_readfirstlane(timed_out) != 0u;
   };
   moe_down_body<FMT, DN_NTILE, DN_WS, DN_GPB, true, ONE_SB>(
       didx, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
@@ -905,6 +938,8 @@ SV_API int snowverify_dense_shuffle(const void* src, void* dst, int64_t N, int64
 SV_API int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c, int64_t M,
                                  int64_t N, int64_t K, int c_is_bf16, void* stream) {
   if (M <= 0 || M > 16 || N <= 0 || K <= 0 || K % 256) return SV_EINVAL;
+  // 32-bit in-kernel offsets: one block's weights (<= 2 tiles) and the activations
+  if (N > (int64_t)1 << 30 || K > 65536) return SV_ENOTSUP;
   const int S = (int)(K / 256);
   hipStream_t s = Sx(stream);
   if (wt == WT_F16) {

@@ -52,6 +52,7 @@ class VerifyConfig:
     eps: float = 1e-6
     page: int = 16
     qk_norm: bool = True
+    centered: bool = True    # zero-mean Q4_K model weights (gguf_random); False: config 2's
 
     @property
     def moe(self):
@@ -65,9 +66,11 @@ class VerifyConfig:
 # BASELINE.json configs. RoPE: config 3 rotates the full head (theta 1e6); the 35B-A3B shape
 # rotates 64 of 256 dims (partial_rotary_factor 0.25, as the reference's Qwen3.5 loader
 # requires at snowllm/models/qwen3_5/qwen3_5_weights.py:443-445) with theta 1e7.
+# Config 3's linear weights are Q4_K "as in config 2" (its generator exactly); the MoE shapes
+# use zero-mean blocks so that the router logits stay ~N(0, 1) per row (gguf_random).
 CONFIG3 = VerifyConfig("config3_dense8b", layers=36, hidden=4096, heads=32, kv_heads=8,
                        head_dim=128, rot_half=64, rope_theta=1e6, vocab=151936, context=8192,
-                       block=9, ffn=14336)
+                       block=9, ffn=14336, centered=False)
 CONFIG4 = VerifyConfig("config4_moe35b_a3b", layers=40, hidden=2048, heads=16, kv_heads=2,
                        head_dim=256, rot_half=32, rope_theta=1e7, vocab=151936, context=8192,
                        block=9, experts=256, expert_ffn=512, topk=8)
@@ -132,8 +135,8 @@ def gguf_random(fmt, n, k, seed, device="cuda", centered=False):
     raise SnowLLMError(f"unknown format {fmt}")
 
 
-def packed_random(fmt, n, k, seed, keep_raw=False):
-    raw = gguf_random(fmt, n, k, seed, centered=True)
+def packed_random(fmt, n, k, seed, keep_raw=False, centered=True):
+    raw = gguf_random(fmt, n, k, seed, centered=centered)
     quant, meta = ops.gemm_kquant_shuffle_b(fmt, raw, n, k)
     return (quant, meta, raw if keep_raw else None)
 
@@ -159,7 +162,8 @@ class VerifyModel:
 
     def __init__(self, cfg: VerifyConfig, seed: int = 0, keep_raw=False, kv_std: float = 1.0):
         """keep_raw: keep the unshuffled GGUF bytes (and the router / LM head) for parity
-        checks -- True for every layer, or an int n for the first n layers."""
+        checks -- True for every layer, an int n for the first n layers, or a collection of
+        layer indices."""
         self.cfg = c = cfg
         self.keep_raw = keep_raw
         dev = "cuda"
@@ -175,29 +179,37 @@ class VerifyModel:
 
         self.layers = []
         for i in range(c.layers):
-            kr = bool(keep_raw) if isinstance(keep_raw, bool) else i < int(keep_raw)
+            if isinstance(keep_raw, bool):
+                kr = keep_raw
+            elif isinstance(keep_raw, int):
+                kr = i < keep_raw
+            else:
+                kr = i in keep_raw
+
+            def pk(fmt, n, k, j):
+                return packed_random(fmt, n, k, sub(i, j), kr, c.centered)
+
             lw = LayerWeights(in_norm=gamma(H), post_norm=gamma(H), q_norm=gamma(c.head_dim),
-                              k_norm=gamma(c.head_dim),
-                              qkv=packed_random(c.attn_fmt, c.qkv_n, H, sub(i, 0), kr),
-                              o=packed_random(c.attn_fmt, H, c.heads * c.head_dim, sub(i, 1), kr))
+                              k_norm=gamma(c.head_dim), qkv=pk(c.attn_fmt, c.qkv_n, H, 0),
+                              o=pk(c.attn_fmt, H, c.heads * c.head_dim, 1))
             if c.moe:
                 E, F = c.experts, c.expert_ffn
                 router = (torch.randn(E + 1, H, device=dev, generator=gen) / math.sqrt(H)).bfloat16()
                 lw.router = Lops.dense_shuffle(router)
-                lw.gu = packed_random(c.ffn_fmt, E * 2 * F, H, sub(i, 2), kr)
-                lw.dn = packed_random(c.ffn_fmt, E * H, F, sub(i, 3), kr)
-                lw.sh_gu = packed_random(c.ffn_fmt, 2 * F, H, sub(i, 4), kr)
-                lw.sh_dn = packed_random(c.ffn_fmt, H, F, sub(i, 5), kr)
+                lw.gu = pk(c.ffn_fmt, E * 2 * F, H, 2)
+                lw.dn = pk(c.ffn_fmt, E * H, F, 3)
+                lw.sh_gu = pk(c.ffn_fmt, 2 * F, H, 4)
+                lw.sh_dn = pk(c.ffn_fmt, H, F, 5)
                 if kr:
                     lw.raw["router"] = router
             else:
-                lw.gu = packed_random(c.ffn_fmt, 2 * c.ffn, H, sub(i, 2), kr)
-                lw.dn = packed_random(c.ffn_fmt, H, c.ffn, sub(i, 3), kr)
+                lw.gu = pk(c.ffn_fmt, 2 * c.ffn, H, 2)
+                lw.dn = pk(c.ffn_fmt, H, c.ffn, 3)
             self.layers.append(lw)
         self.embed = (0.02 * torch.randn(V, H, device=dev, generator=gen)).half()
         head = (0.02 * torch.randn(V, H, device=dev, generator=gen)).half()
         self.lm_head = Lops.dense_shuffle(head)
-        self.lm_head_raw = head if keep_raw else None
+        self.lm_head_raw = head if (keep_raw is not False and keep_raw != 0) else None
         self.final_norm = gamma(H)
         self.inv_freq = (1.0 / (c.rope_theta ** (torch.arange(c.rot_half, device=dev,
                                                              dtype=torch.float32) / c.rot_half)))

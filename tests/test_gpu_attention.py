@@ -77,8 +77,8 @@ def test_config4_shape():
 
 @pytest.mark.parametrize("v_scale", [3e6, 1e-12])
 def test_value_magnitudes_outside_fp16(v_scale):
-    """The split partials are fp16 with a power-of-two scale per row: values far outside fp16's
-    range merge without overflow or flush."""
+    """Values far outside fp16's range: the f32 split partials and the bf16 P.V products
+    (P as a bf16 hi + lo pair) merge without overflow or flush."""
     _case([2000 + 9], 9, 16, 2, 256, seed=7, v_scale=v_scale)
 
 

@@ -62,7 +62,8 @@ def test_layers_and_head_match_cpu_reference(gpu, kind):
         e_x = rel(m.x.float().cpu(), x2)
         e_r = rel(m.layer_residual.float().cpu(), r2)
         print(f"  layer {layer}: attn {e_attn:.2e}  ffn out {e_x:.2e}  residual {e_r:.2e}", flush=True)
-        assert e_attn < 1e-2 and e_r < 1e-2 and e_x < 2e-2
+        # about twice the largest observed on MI355X (attn 8.1e-4, residual 1.5e-3, FFN 5.5e-3)
+        assert e_attn < 2e-3 and e_r < 3e-3 and e_x < 1.1e-2
         if routing is not None:
             got = m.route_ids.cpu().long()
             assert torch.equal(got.sort(-1).values, routing.sort(-1).values)
@@ -72,7 +73,7 @@ def test_layers_and_head_match_cpu_reference(gpu, kind):
                              m.lm_head_raw.cpu(), cfg.eps)
     e_l = rel(logits.cpu(), want)
     print(f"  logits rel L2 {e_l:.2e}", flush=True)
-    assert e_l < 1e-2
+    assert e_l < 5e-7  # observed 1.1e-7
     # acceptance over the chain rows on the GPU's own logits: bit-exact vs the C oracle
     rows = list(range(T)) if not cfg.tree_parents else [0, 1, 2]
     acc = Acceptance(cfg.vocab, rows)
