@@ -148,10 +148,10 @@ void snowverify_gemv_variant(int v);
 
 /* Extension, no counterpart in the reference: fill the gemm_kquant_a operand workspace from
  * bf16 activations A[M, K] once, so that several weights sharing one input reuse it. */
-int snowllm_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws, void* stream);
+int snowverify_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws, void* stream);
 
 /* Extension, no counterpart in the reference: gemm_kquant_a on a prepared workspace. */
-int snowllm_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta, void* c,
+int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta, void* c,
                                    int64_t M, int64_t N, int64_t K, int c_is_bf16,
                                    const void* ws, void* stream);
 
@@ -197,9 +197,9 @@ int snowverify_paged_attention_qk(const void* proj, int64_t proj_stride, int64_t
                                   int64_t page_size, int64_t table_stride, float scale,
                                   void* scratch, int64_t scratch_bytes, void* stream);
 /* Extension, no counterpart in the reference: snowverify_paged_attention_qk that also writes
- * the output projection's operand workspace out_ws (as snowllm_gemm_kquant_prepare_a would
+ * the output projection's operand workspace out_ws (as snowverify_gemm_kquant_prepare_a would
  * from `out` viewed as [batch*tokens, num_heads*head_size]; snowllm_gemm_kquant_a_ws_bytes of
- * that shape), so the projection runs snowllm_gemm_kquant_a_prepared with the same bits as
+ * that shape), so the projection runs snowverify_gemm_kquant_a_prepared with the same bits as
  * snowllm_gemm_kquant_a on `out`. head_size 256 only (hipErrorNotSupported otherwise). */
 int snowverify_paged_attention_qk_ws(const void* proj, int64_t proj_stride,
                                      int64_t q_head_stride, int64_t k_off, int64_t v_off,
@@ -254,6 +254,15 @@ typedef struct PagedAttentionStep {
  * out [M, qkv_proj_n] bf16 = RMSNorm(residual += x) * gamma . W^T (no residual: RMSNorm(x);
  * no gamma: x). w[3]: the QKV k-quant weight, then split V / KV (absent). */
 int64_t snowllm_qkv_proj_scratch_bytes(int64_t M);                     /* _capi.py:251 */
+/* Sizing queries the reference's hot-path ops modules bind at import: the O projection's
+ * scratch (snowllm/_capi.py:254; ops/attention_full.py:512); the draft model's attention
+ * sizing (snowllm/_capi.py:300-301; ops/dflash.py:337-338), answered with the decode
+ * attention's for the active geometry -- the draft's layers are not carried; the hashed
+ * router's scratch (snowllm/_capi.py:351; ops/moe.py:279), 0: hashed routing is refused. */
+int64_t snowllm_attn_out_scale_oproj_scratch_bytes(int64_t rows);
+int64_t snowllm_draft_paged_attn_num_slots(int64_t num_seqs);
+int64_t snowllm_draft_paged_attn_workspace_size(int64_t num_slots, int64_t q_tokens);
+int64_t snowllm_moe_router_shuffle_bytes(int64_t rows);
 int snowllm_inference_qkv(const SnowllmWeight* w, const void* x, void* residual,
                           const void* gamma, float eps, void* scratch, void* out, int64_t M,
                           int path, const void* index_w, void* index_out, void* stream);
@@ -272,6 +281,43 @@ int64_t snowllm_paged_attention_scratch_bytes(int64_t batch, int64_t tokens, int
 int snowllm_paged_attention_varlen(int prefill, int64_t tokens, int chunk_decode);
 int snowllm_paged_attention(const PagedAttentionStep* step, void* scratch, int64_t bytes,
                             void* stream);
+/* Prepared attention metadata (snowllm/_capi.py:808-812; ops/attention_full.py:136-150):
+ * none is needed, so the size is 0 (the reference's wrapper then passes no prepared buffer and
+ * its runner skips the decode plan, engine/qwen_runner.py:202-208); prepare checks its
+ * arguments and launches nothing. */
+int64_t snowllm_paged_attention_prepared_bytes(int64_t batch, int64_t tokens, int64_t slots,
+                                               int varlen);
+int snowllm_paged_attention_prepare(const int32_t* lens, void* result, int64_t batch,
+                                    int64_t tokens, int64_t slots, int64_t block_size,
+                                    void* stream);
+/* Split-KV decode attention and its plan (snowllm/_capi.py:358, 371-373, 506-509; read at
+ * import by ops/attention_full.py:516-518, 565; called at :1147-1161, 1232-1238). The context
+ * splits are sized at launch from the block-table width and the kernels read the lengths
+ * themselves, so the plan is one int32 that nothing writes and the plan call only checks its
+ * arguments. A slot is one sequence's partials region. max_q_tokens: T * G <= 128 and
+ * T <= 64 for the active geometry. q rows are q_pitch elements apart (0: heads * head_size)
+ * from row q_row0; out [num_seqs * q_tokens, heads, head_size]; ws sized by
+ * snowllm_paged_decode_workspace_size(num_slots, q_tokens), num_slots >= num_seqs. */
+int64_t snowllm_paged_decode_max_q_tokens(void);
+int64_t snowllm_paged_decode_num_slots(int64_t num_seqs);
+int64_t snowllm_paged_decode_workspace_size(int64_t num_slots, int64_t q_tokens);
+int64_t snowllm_paged_decode_plan_elems(int64_t num_seqs, int64_t num_slots);
+int snowllm_paged_attn_decode_plan(const int32_t* seq_lens, int32_t* plan, int64_t num_seqs,
+                                   int64_t num_slots, int64_t block_size, int uniform,
+                                   void* stream);
+int snowllm_paged_attn_decode(const void* q, const int32_t* seq_lens, const void* k_cache,
+                              const void* v_cache, void* out, const int32_t* block_tables,
+                              const int32_t* plan, int64_t num_seqs, int64_t max_blocks,
+                              int64_t num_slots, void* ws, float scale, int64_t q_tokens,
+                              int64_t block_size, int64_t q_pitch, int64_t q_row0, void* stream);
+/* Query-block map of a varlen batch, host arithmetic on host arrays (snowllm/_capi.py:364-365;
+ * ops/attention_full.py:539-547): blocks of 16 query rows; the map holds (sequence, first row
+ * of the block in the sequence) int32 pairs. */
+int64_t snowllm_prefill_q_blocks(const int32_t* lens, int64_t B);
+void snowllm_prefill_q_block_map(const int32_t* lens, int64_t B, int32_t* map);
+/* Page sizes of the KV pools (snowllm/_capi.py:243; read at import by ops/_common.py:35-43):
+ * writes up to n to out (if not NULL) and returns their count (one: 16). */
+int64_t snowllm_kv_block_sizes(int64_t* out, int64_t n);
 /* MoE block (snowllm/_capi.py:315, 690-691, 805-807; ops/inference.py:54-95): w[4] = experts'
  * gate/up stack, experts' down stack, shared gate/up, shared down; router: repacked bf16
  * [E+1, hidden], the shared expert's gate last. The _norm form first sets residual += x and
@@ -280,7 +326,8 @@ int64_t snowllm_moe_workspace_bytes(int64_t rows);
 int64_t snowllm_inference_moe_workspace_bytes(int64_t rows, int64_t flags);
 int snowllm_inference_moe(const SnowllmWeight* w, const void* x, const void* router,
                           const int64_t* token_ids, const int32_t* tid2eid, void* out,
-                          void* scratch, int64_t capacity, int64_t M, int flags, void* stream);
+                          void* scratch, int64_t capacity, int64_t M, int64_t flags,
+                          void* stream);
 int snowllm_inference_moe_norm(const SnowllmWeight* w, const void* x, void* residual,
                                const void* gamma, float eps, void* hidden_row,
                                const void* router, void* out, void* scratch, int64_t capacity,

@@ -84,8 +84,8 @@ _SIGS = [
     ("snowllm_gemm_kquant_shuffle_b", c_int, [c_int, P, P, P, c_int64, c_int64, S]),
     ("snowllm_gemm_kquant_a_ws_bytes", c_int64, [c_int64, c_int64]),
     ("snowllm_gemm_kquant_a", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
-    ("snowllm_gemm_kquant_prepare_a", c_int, [P, c_int64, c_int64, P, S]),
-    ("snowllm_gemm_kquant_a_prepared", c_int, [c_int, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
+    ("snowverify_gemm_kquant_prepare_a", c_int, [P, c_int64, c_int64, P, S]),
+    ("snowverify_gemm_kquant_a_prepared", c_int, [c_int, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
     ("snowverify_gemv_variant", None, [c_int]),
     # paged attention
     ("snowverify_paged_attention_scratch_bytes", c_int64, [c_int64] * 5),
@@ -99,6 +99,10 @@ _SIGS = [
     ("snowverify_attention_ring", c_int, [c_int]),
     # geometry-driven operator entry points (reference signatures)
     ("snowllm_qkv_proj_scratch_bytes", c_int64, [c_int64]),
+    ("snowllm_attn_out_scale_oproj_scratch_bytes", c_int64, [c_int64]),
+    ("snowllm_draft_paged_attn_num_slots", c_int64, [c_int64]),
+    ("snowllm_draft_paged_attn_workspace_size", c_int64, [c_int64, c_int64]),
+    ("snowllm_moe_router_shuffle_bytes", c_int64, [c_int64]),
     ("snowllm_inference_qkv", c_int, [P, P, P, P, c_float, P, P, c_int64, c_int, P, P, S]),
     ("snowllm_attn_output_plan", c_int, [c_int64, c_int, c_int, P]),
     ("snowllm_attn_output_gate", P, [P, c_int, c_int]),
@@ -106,9 +110,21 @@ _SIGS = [
     ("snowllm_paged_attention_scratch_bytes", c_int64, [c_int64, c_int64, c_int]),
     ("snowllm_paged_attention_varlen", c_int, [c_int, c_int64, c_int]),
     ("snowllm_paged_attention", c_int, [P, P, c_int64, S]),
+    ("snowllm_paged_attention_prepared_bytes", c_int64, [c_int64, c_int64, c_int64, c_int]),
+    ("snowllm_paged_attention_prepare", c_int, [P, P, c_int64, c_int64, c_int64, c_int64, S]),
+    ("snowllm_paged_decode_max_q_tokens", c_int64, []),
+    ("snowllm_paged_decode_num_slots", c_int64, [c_int64]),
+    ("snowllm_paged_decode_workspace_size", c_int64, [c_int64, c_int64]),
+    ("snowllm_paged_decode_plan_elems", c_int64, [c_int64, c_int64]),
+    ("snowllm_paged_attn_decode_plan", c_int, [P, P, c_int64, c_int64, c_int64, c_int, S]),
+    ("snowllm_paged_attn_decode", c_int, [P] * 7 + [c_int64] * 3 + [P, c_float] + [c_int64] * 4
+     + [S]),
+    ("snowllm_prefill_q_blocks", c_int64, [P, c_int64]),
+    ("snowllm_prefill_q_block_map", None, [P, c_int64, P]),
+    ("snowllm_kv_block_sizes", c_int64, [c_void_p, c_int64]),
     ("snowllm_moe_workspace_bytes", c_int64, [c_int64]),
     ("snowllm_inference_moe_workspace_bytes", c_int64, [c_int64, c_int64]),
-    ("snowllm_inference_moe", c_int, [P] * 7 + [c_int64, c_int64, c_int, S]),
+    ("snowllm_inference_moe", c_int, [P] * 7 + [c_int64] * 3 + [S]),
     ("snowllm_inference_moe_norm", c_int, [P, P, P, P, c_float, P, P, P, P, c_int64, c_int64, S]),
     ("snowllm_fused_mlp_workspace_bytes", c_int64, [c_int64]),
     ("snowllm_inference_mlp", c_int, [P, P, P, P, c_int64, c_int, S]),

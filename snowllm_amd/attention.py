@@ -149,6 +149,68 @@ def paged_attention(q, pools, out, cu, table, lens, qmap, total_blocks, plan, wo
           "paged_attention")
 
 
+def paged_attention_prepare(lens, tokens, slots, block_size, varlen, arena=None):
+    """attention_full.py:136-150: this build needs no prepared metadata (size 0) -> None."""
+    batch = lens.numel()
+    if not lib.snowllm_paged_attention_prepared_bytes(batch, tokens, slots, int(varlen)):
+        return None
+    raise SnowLLMError("prepared attention metadata is not expected from this library")
+
+
+def paged_attention_uses_prepared(batch, tokens, varlen):
+    """attention_full.py:131-133."""
+    return bool(paged_attention_scratch_bytes(batch, tokens, varlen))
+
+
+PAGED_DECODE_MAX_Q_TOKENS = int(lib.snowllm_paged_decode_max_q_tokens())
+KV_BLOCK_SIZES = (PAGE,)
+
+
+def paged_decode_num_slots(num_seqs: int) -> int:
+    return int(lib.snowllm_paged_decode_num_slots(num_seqs))
+
+
+def paged_decode_workspace_size(num_slots: int, q_tokens: int = 1) -> int:
+    return int(lib.snowllm_paged_decode_workspace_size(num_slots, q_tokens))
+
+
+def paged_decode_plan_elems(num_seqs: int, num_slots: int) -> int:
+    return int(lib.snowllm_paged_decode_plan_elems(num_seqs, num_slots))
+
+
+def paged_attn_decode_plan(seq_lens, plan, num_slots, block_size, uniform=False) -> None:
+    """attention_full.py:1232-1238 (nothing to plan here; the arguments are checked)."""
+    _chk(seq_lens, "seq_lens", torch.int32)
+    _chk(plan, "plan", torch.int32)
+    check(lib.snowllm_paged_attn_decode_plan(_p(seq_lens), _p(plan), seq_lens.numel(), num_slots,
+                                             block_size, int(uniform), _stream()),
+          "paged_attn_decode_plan")
+
+
+def paged_attn_decode(q, seq_lens, k_cache, v_cache, out, block_tables, plan, workspace,
+                      num_seqs, num_slots, scale, block_size, q_tokens=1, q_pitch=0, q_row0=0):
+    """attention_full.py:1147-1161: split-KV decode attention of q_tokens rows per sequence,
+    causal within them; q rows q_pitch elements apart (0: contiguous) from row q_row0."""
+    _chk(block_tables, "block_tables", torch.int32)
+    _chk(plan, "plan", torch.int32)
+    _chk(seq_lens, "seq_lens", torch.int32)
+    check(lib.snowllm_paged_attn_decode(_p(q), _p(seq_lens), _p(k_cache), _p(v_cache), _p(out),
+                                        _p(block_tables), _p(plan), num_seqs,
+                                        block_tables.shape[1], num_slots, _p(workspace), scale,
+                                        q_tokens, block_size, q_pitch, q_row0, _stream()),
+          "paged_attn_decode")
+
+
+def prefill_q_plan(query_lens):
+    """attention_full.py:539-547: (query blocks, device map of (sequence, first row) pairs)."""
+    B = len(query_lens)
+    lens = (ctypes.c_int32 * B)(*query_lens)
+    total = lib.snowllm_prefill_q_blocks(lens, B)
+    buf = (ctypes.c_int32 * (total * 2))()
+    lib.snowllm_prefill_q_block_map(lens, B, buf)
+    return total, torch.frombuffer(memoryview(buf), dtype=torch.int32).clone().cuda()
+
+
 def attn_output_plan(m: int, prefill: bool, kv_int8: bool) -> tuple:
     """(elements of the attention output, scratch bytes) (attention_full.py:54-64)."""
     out = (ctypes.c_int64 * 2)()

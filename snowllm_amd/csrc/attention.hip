@@ -25,6 +25,7 @@
 // group); rows >= T*G are padding. Row t of request b sees context keys [0, L - T) and block
 // key j (position L - T + j) iff bit j of its ancestor mask is set (causal: j <= t).
 #include "common.h"
+#include "geometry.h"
 #include "kquant_core.h"
 #include "qknorm.h"
 
@@ -48,7 +49,8 @@ constexpr int MAX_TILES_DH = 4;  // up to 4 tiles, each tile's output columns sp
 constexpr int FUSED_MAX_HS = 2;
 
 struct AttnArgs {
-  const uint16_t* q;        // [batch*T, Hq, D]
+  const uint16_t* q;        // [batch*T, Hq, D], rows q_stride elements apart
+  int64_t q_stride;
   const uint16_t* k_pool;   // [blocks, Hkv, D/16, 16, 16]
   const uint16_t* v_pool;   // [blocks, Hkv, 4, D, 4]
   const int32_t* table;     // [batch, table_stride]
@@ -385,7 +387,7 @@ attn_split_kernel(AttnArgs a) {
       qk_fetch_aux<D>(qaux, a.q_gamma, a.cosv + m_row * a.cs_stride, a.sinv + m_row * a.cs_stride,
                       a.rot_half, kq);
     } else {
-      const uint16_t* qrow = a.q + (m_row * a.Hq + hq) * D;
+      const uint16_t* qrow = a.q + m_row * a.q_stride + (int64_t)hq * D;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
         if (row_live) qb[ds] = load_bf16x8(qrow + ds * 32 + kq * 8);
@@ -726,6 +728,7 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
                                                               num_kv_heads, head_size))
     return SV_EINVAL;
   a.q = (const uint16_t*)q;
+  if (a.q_stride == 0) a.q_stride = num_heads * head_size;
   a.k_pool = (const uint16_t*)k_pool;
   a.v_pool = (const uint16_t*)v_pool;
   a.table = table;
@@ -829,7 +832,7 @@ SV_API int snowverify_paged_attention_qk(
 }
 
 // Extension, no counterpart in the reference: snowverify_paged_attention_qk that also writes
-// the output projection's operand workspace (snowllm_gemm_kquant_a_prepared's ws for the
+// the output projection's operand workspace (snowverify_gemm_kquant_a_prepared's ws for the
 // [batch*tokens, num_heads*head_size] output, snowllm_gemm_kquant_a_ws_bytes of that shape), so
 // the projection skips its own conversion of the bf16 output: the same operands, the same
 // bits. head_size 256 only (hipErrorNotSupported otherwise).
@@ -891,4 +894,142 @@ SV_API int snowverify_attention_ring(int pages) {
   const int prev = g_ring;
   g_ring = (pages == 4 || pages == 8) ? pages : 0;
   return prev;
+}
+
+// ---------------------------------------------------------------------------------------
+// The reference's split-KV decode entry points (snowllm/_capi.py:243, 358, 364-365, 371-373,
+// 506-509, 808-812; ops/attention_full.py:516-518, 539-547, 565-575, 1147-1161, 1232-1238;
+// ops/_common.py:35-43), over the active geometry. This build sizes its context splits at
+// launch from the block-table width (one round of workgroups over the CUs) and every kernel
+// reads the sequence lengths itself, so the decode plan the reference computes from the
+// lengths carries nothing here: one int32 element, never written, and the plan call validates
+// its arguments and launches nothing. A "slot" is the partials region of one sequence.
+// ---------------------------------------------------------------------------------------
+namespace {
+int geo_group() {
+  const BuildGeometry& g = active_geometry();
+  return g.num_kv_heads > 0 && g.num_heads % g.num_kv_heads == 0
+             ? (int)(g.num_heads / g.num_kv_heads) : 0;
+}
+}  // namespace
+
+// Page sizes the KV pools support (snowllm/_capi.py:243; ops/_common.py:35-39): writes up to
+// n of them to out (when out is not null) and returns how many there are.
+SV_API int64_t snowllm_kv_block_sizes(int64_t* out, int64_t n) {
+  if (out && n > 0) out[0] = PAGE;
+  return 1;
+}
+
+// Largest query rows per request of the decode form (snowllm/_capi.py:371; read at import by
+// ops/attention_full.py:565): T * G <= 128 rows in one workgroup, T <= 64 (u64 masks).
+SV_API int64_t snowllm_paged_decode_max_q_tokens(void) {
+  const int G = geo_group();
+  if (G <= 0) return 0;
+  const int t = MAX_TILES * 16 / G;
+  return t < 64 ? t : 64;
+}
+
+// Partials regions for num_seqs sequences (snowllm/_capi.py:372).
+SV_API int64_t snowllm_paged_decode_num_slots(int64_t num_seqs) {
+  return num_seqs > 0 ? num_seqs : 0;
+}
+
+// Workspace bytes of snowllm_paged_attn_decode for num_slots sequences of q_tokens rows
+// (snowllm/_capi.py:358).
+SV_API int64_t snowllm_paged_decode_workspace_size(int64_t num_slots, int64_t q_tokens) {
+  const BuildGeometry& g = active_geometry();
+  if (num_slots <= 0 || q_tokens <= 0) return 0;
+  return snowverify_paged_attention_scratch_bytes(num_slots, q_tokens, g.num_heads,
+                                                  g.num_kv_heads, g.head_size);
+}
+
+// int32 elements of the decode plan (snowllm/_capi.py:373).
+SV_API int64_t snowllm_paged_decode_plan_elems(int64_t num_seqs, int64_t num_slots) {
+  (void)num_seqs;
+  (void)num_slots;
+  return 1;
+}
+
+// The decode plan (snowllm/_capi.py:509; ops/attention_full.py:1232-1238): nothing to compute
+// (see above); the arguments are checked.
+SV_API int snowllm_paged_attn_decode_plan(const int32_t* seq_lens, int32_t* plan,
+                                          int64_t num_seqs, int64_t num_slots,
+                                          int64_t block_size, int uniform, void* stream) {
+  (void)plan;
+  (void)uniform;
+  (void)stream;
+  if (!seq_lens || num_seqs <= 0 || num_slots < num_seqs) return SV_EINVAL;
+  if (block_size != PAGE) return SV_ENOTSUP;
+  return SV_OK;
+}
+
+// Split-KV decode attention (snowllm/_capi.py:506-508; ops/attention_full.py:1147-1161):
+// q_tokens query rows per sequence, causal within them, against bf16 pools. q rows are q_pitch
+// elements apart (0: num_heads * head_size) starting at row q_row0; out [num_seqs * q_tokens,
+// num_heads, head_size] bf16; ws as sized by snowllm_paged_decode_workspace_size(num_slots,
+// q_tokens) with num_slots >= num_seqs; block_tables [num_seqs, max_blocks].
+SV_API int snowllm_paged_attn_decode(const void* q, const int32_t* seq_lens, const void* k_cache,
+                                     const void* v_cache, void* out, const int32_t* block_tables,
+                                     const int32_t* plan, int64_t num_seqs, int64_t max_blocks,
+                                     int64_t num_slots, void* ws, float scale, int64_t q_tokens,
+                                     int64_t block_size, int64_t q_pitch, int64_t q_row0,
+                                     void* stream) {
+  (void)plan;
+  const BuildGeometry& g = active_geometry();
+  if (!q || !seq_lens || !k_cache || !v_cache || !out || !block_tables || !ws ||
+      num_seqs <= 0 || num_slots < num_seqs || q_tokens <= 0 || q_pitch < 0 || q_row0 < 0)
+    return SV_EINVAL;
+  if (q_pitch && q_pitch < g.num_heads * g.head_size) return SV_EINVAL;
+  if (block_size != PAGE) return SV_ENOTSUP;
+  AttnArgs a = {};
+  a.q_stride = q_pitch ? q_pitch : g.num_heads * g.head_size;
+  const uint16_t* q0 = (const uint16_t*)q + q_row0 * a.q_stride;
+  return paged_attention_impl(a, q0, k_cache, v_cache, out, block_tables, seq_lens, nullptr,
+                              num_seqs, q_tokens, g.num_heads, g.num_kv_heads, g.head_size,
+                              block_size, max_blocks, scale, ws,
+                              snowllm_paged_decode_workspace_size(num_slots, q_tokens), stream);
+}
+
+// Prepared attention metadata (snowllm/_capi.py:808-812; ops/attention_full.py:136-150): this
+// build needs none, so its size is 0 and the reference's wrapper hands no prepared buffer on;
+// the runner then skips the decode plan (engine/qwen_runner.py:202-208).
+SV_API int64_t snowllm_paged_attention_prepared_bytes(int64_t batch, int64_t tokens,
+                                                      int64_t slots, int varlen) {
+  (void)batch;
+  (void)tokens;
+  (void)slots;
+  (void)varlen;
+  return 0;
+}
+
+SV_API int snowllm_paged_attention_prepare(const int32_t* lens, void* result, int64_t batch,
+                                           int64_t tokens, int64_t slots, int64_t block_size,
+                                           void* stream) {
+  (void)result;
+  (void)slots;
+  (void)stream;
+  if (!lens || batch <= 0 || tokens <= 0) return SV_EINVAL;
+  if (block_size != PAGE) return SV_ENOTSUP;
+  return SV_OK;
+}
+
+// Query-block map of a varlen batch (snowllm/_capi.py:364-365; ops/attention_full.py:539-547),
+// host arithmetic over host arrays: blocks of 16 query rows; the map lists (sequence, first
+// row of the block within the sequence) pairs in order.
+SV_API int64_t snowllm_prefill_q_blocks(const int32_t* lens, int64_t B) {
+  if (!lens || B < 0) return -1;
+  int64_t total = 0;
+  for (int64_t b = 0; b < B; ++b) total += lens[b] > 0 ? (lens[b] + 15) / 16 : 0;
+  return total;
+}
+
+SV_API void snowllm_prefill_q_block_map(const int32_t* lens, int64_t B, int32_t* map) {
+  if (!lens || !map || B < 0) return;
+  int64_t i = 0;
+  for (int64_t b = 0; b < B; ++b)
+    for (int32_t r = 0; r < lens[b]; r += 16) {
+      map[2 * i] = (int32_t)b;
+      map[2 * i + 1] = r;
+      ++i;
+    }
 }

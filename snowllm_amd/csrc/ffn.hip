@@ -933,7 +933,7 @@ SV_API int snowverify_dense_shuffle(const void* src, void* dst, int64_t N, int64
 }
 
 // C[M, N] = A[M, K] W[N, K]^T, fp32 accumulate. wt 1: fp16 weights against the operand
-// workspace `act` (snowllm_gemm_kquant_prepare_a / snowverify_norm_prep); wt 2: bf16 weights
+// workspace `act` (snowverify_gemm_kquant_prepare_a / snowverify_norm_prep); wt 2: bf16 weights
 // against bf16 activations `act` [M, K]. M <= 16.
 SV_API int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c, int64_t M,
                                  int64_t N, int64_t K, int c_is_bf16, void* stream) {

@@ -62,8 +62,8 @@ int64_t snowllm_gemm_kquant_a_ws_bytes(int64_t M, int64_t K);
 int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, const uint8_t* meta,
                           void* c, int64_t M, int64_t N, int64_t K, int c_is_bf16, void* ws,
                           void* stream);
-int snowllm_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws, void* stream);
-int snowllm_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta, void* c,
+int snowverify_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws, void* stream);
+int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta, void* c,
                                    int64_t M, int64_t N, int64_t K, int c_is_bf16,
                                    const void* ws, void* stream);
 int snowverify_norm_prep(const void* x, const void* res_in, void* res_out, const void* gamma,
@@ -223,8 +223,37 @@ SV_API int snowllm_inference_qkv(const Weight* w, const void* x, void* residual,
   int rc = snowverify_norm_prep(x, residual, residual, gamma, nullptr, scratch, M, g.hidden, eps,
                                 stream);
   if (rc) return rc;
-  return snowllm_gemm_kquant_a_prepared(w[0].fmt, q, m, out, M, g.qkv_proj_n, g.hidden, 1,
+  return snowverify_gemm_kquant_a_prepared(w[0].fmt, q, m, out, M, g.qkv_proj_n, g.hidden, 1,
                                         scratch, stream);
+}
+
+// snowllm/_capi.py:254 (bound at import by ops/attention_full.py:512): scratch of the output
+// projection of `rows` rows, the projection's operand workspace (as snowllm_attn_output_plan).
+SV_API int64_t snowllm_attn_out_scale_oproj_scratch_bytes(int64_t rows) {
+  const BuildGeometry& g = active_geometry();
+  return rows <= 0 ? 0 : snowllm_gemm_kquant_a_ws_bytes(rows, g.num_heads * g.head_size);
+}
+
+// snowllm/_capi.py:300-301 (bound at import by ops/dflash.py:337-338): the draft model's
+// attention sizing. The draft model's own layers are not carried here; these answer with the
+// decode attention's sizing for the active geometry (one partials region per sequence).
+SV_API int64_t snowllm_draft_paged_attn_num_slots(int64_t num_seqs) {
+  return num_seqs > 0 ? num_seqs : 0;
+}
+
+SV_API int64_t snowllm_draft_paged_attn_workspace_size(int64_t num_slots, int64_t q_tokens) {
+  const BuildGeometry& g = active_geometry();
+  if (num_slots <= 0 || q_tokens <= 0) return 0;
+  return snowverify_paged_attention_scratch_bytes(num_slots, q_tokens, g.num_heads,
+                                                  g.num_kv_heads, g.head_size);
+}
+
+// snowllm/_capi.py:351 (bound at import by ops/moe.py:279): scratch of the hashed
+// (token-id -> expert) router, which this build does not carry (its MoE entry points refuse a
+// tid2eid table): 0.
+SV_API int64_t snowllm_moe_router_shuffle_bytes(int64_t rows) {
+  (void)rows;
+  return 0;
 }
 
 // snowllm/_capi.py:223 (ops/attention_full.py:54-64): elements of the attention output and the
@@ -311,14 +340,14 @@ SV_API int64_t snowllm_inference_moe_workspace_bytes(int64_t rows, int64_t flags
 // shared expert's gate last. x and out may be the same buffer. M <= 16.
 SV_API int snowllm_inference_moe(const Weight* w, const void* x, const void* router,
                                  const int64_t* token_ids, const int32_t* tid2eid, void* out,
-                                 void* scratch, int64_t capacity, int64_t M, int flags,
+                                 void* scratch, int64_t capacity, int64_t M, int64_t flags,
                                  void* stream) {
   if (token_ids || tid2eid || flags) return SV_ENOTSUP;
   if (!w || !x || !router || !out || !scratch || M <= 0 || M > MAX_ROWS || !moe_geometry_ok())
     return SV_EINVAL;
   const MoeWs ws = moe_ws(scratch, M);
   if (capacity < (int64_t)ws.bytes) return SV_EINVAL;
-  int rc = snowllm_gemm_kquant_prepare_a(x, M, active_geometry().hidden, ws.ws, stream);
+  int rc = snowverify_gemm_kquant_prepare_a(x, M, active_geometry().hidden, ws.ws, stream);
   if (rc) return rc;
   return moe_body(w, x, router, out, ws, M, stream);
 }
@@ -358,7 +387,7 @@ SV_API int snowllm_inference_mlp(const Weight* w, const void* x, void* out, void
   const BuildGeometry& g = active_geometry();
   if (!x || !out || !scratch || M <= 0 || M > MAX_ROWS || g.mlp_inter <= 0) return SV_EINVAL;
   const MlpWs ws = mlp_ws(scratch, M);
-  int rc = snowllm_gemm_kquant_prepare_a(x, M, g.hidden, ws.ws_x, stream);
+  int rc = snowverify_gemm_kquant_prepare_a(x, M, g.hidden, ws.ws_x, stream);
   if (rc) return rc;
   rc = snowverify_gate_up_swiglu(w[0].fmt, w[0].data[0], w[0].data[1], ws.ws_x, ws.act, M,
                                  g.mlp_inter, g.hidden, stream);
@@ -381,7 +410,7 @@ SV_API int snowllm_inference_head(const Weight* w, const void* x, float* out, vo
   if (!w || w->kind != 0 || !w->data[0]) return SV_ENOTSUP;
   const BuildGeometry& g = active_geometry();
   if (!x || !out || !scratch || M <= 0) return SV_EINVAL;
-  int rc = snowllm_gemm_kquant_prepare_a(x, M, g.hidden, scratch, stream);
+  int rc = snowverify_gemm_kquant_prepare_a(x, M, g.hidden, scratch, stream);
   if (rc) return rc;
   const int64_t tile_bytes = snowllm_gemm_kquant_a_ws_bytes(16, g.hidden);
   for (int64_t r0 = 0; r0 < M; r0 += 16) {

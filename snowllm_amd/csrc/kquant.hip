@@ -229,7 +229,7 @@ SV_API int64_t snowllm_gemm_kquant_a_ws_bytes(int64_t M, int64_t K) {
 
 // Extension (no counterpart in the reference): convert activations once into the operand
 // workspace so several weights that share an input (gate/up, Q/K/V) reuse it.
-SV_API int snowllm_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws,
+SV_API int snowverify_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* ws,
                                          void* stream) {
   if (M < 0 || K <= 0 || K % 256) return SV_EINVAL;
   if (M == 0) return SV_OK;
@@ -242,7 +242,7 @@ SV_API int snowllm_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, vo
 }
 
 // Extension (no counterpart in the reference): the GEMV on a prepared operand workspace.
-SV_API int snowllm_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta,
+SV_API int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta,
                                           void* c, int64_t M, int64_t N, int64_t K,
                                           int c_is_bf16, const void* ws, void* stream) {
   if (!fmt_ok(fmt) || M < 0 || N <= 0 || K <= 0 || K % 256 || N % TILE_N) return SV_EINVAL;
@@ -277,7 +277,7 @@ SV_API int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, c
                ? dispatch_gemv<FMT_Q4_K, true>(quant, meta, a, c, (int)M, (int)N, (int)(K / 256), c_is_bf16, s)
                : dispatch_gemv<FMT_Q8_0, true>(quant, meta, a, c, (int)M, (int)N, (int)(K / 256), c_is_bf16, s);
   }
-  int rc = snowllm_gemm_kquant_prepare_a(a, M, K, ws, stream);
+  int rc = snowverify_gemm_kquant_prepare_a(a, M, K, ws, stream);
   if (rc) return rc;
-  return snowllm_gemm_kquant_a_prepared(fmt, quant, meta, c, M, N, K, c_is_bf16, ws, stream);
+  return snowverify_gemm_kquant_a_prepared(fmt, quant, meta, c, M, N, K, c_is_bf16, ws, stream);
 }

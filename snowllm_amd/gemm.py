@@ -52,7 +52,7 @@ def gemm_kquant_prepare_a(a: torch.Tensor, ws: torch.Tensor) -> None:
     M, K = a.shape
     _chk(a, "a", torch.bfloat16, M, K)
     _chk(ws, "ws", torch.uint8, gemm_kquant_a_ws_bytes(M, K))
-    check(lib.snowllm_gemm_kquant_prepare_a(_p(a), M, K, _p(ws), _stream()), "gemm_kquant_prepare_a")
+    check(lib.snowverify_gemm_kquant_prepare_a(_p(a), M, K, _p(ws), _stream()), "gemm_kquant_prepare_a")
 
 
 def gemm_kquant_a_prepared(fmt: int, quant: torch.Tensor, meta: torch.Tensor, c: torch.Tensor,
@@ -61,5 +61,5 @@ def gemm_kquant_a_prepared(fmt: int, quant: torch.Tensor, meta: torch.Tensor, c:
     _chk(ws, "ws", torch.uint8, gemm_kquant_a_ws_bytes(M, K))
     bf16 = c.dtype is torch.bfloat16
     _chk(c, "c", torch.bfloat16 if bf16 else torch.float32, M, N)
-    check(lib.snowllm_gemm_kquant_a_prepared(fmt, _p(quant), _p(meta), _p(c), M, N, K, bf16, _p(ws),
+    check(lib.snowverify_gemm_kquant_a_prepared(fmt, _p(quant), _p(meta), _p(c), M, N, K, bf16, _p(ws),
                                              _stream()), "gemm_kquant_a_prepared")

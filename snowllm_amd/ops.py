@@ -12,7 +12,11 @@ from .attention import (kv_pool_bytes, paged_attention_explicit,  # noqa: F401
                         FUSED_QK_MAX_HALF,
                         paged_attention_scratch_bytes, paged_attention_varlen, attn_output_plan,
                         attn_output_shape, attn_output_gating, attn_output_project, rope_cos_sin,
-                        qk_norm_rope_cache)
+                        qk_norm_rope_cache, paged_attention_prepare,
+                        paged_attention_uses_prepared, PAGED_DECODE_MAX_Q_TOKENS, KV_BLOCK_SIZES,
+                        paged_decode_num_slots, paged_decode_workspace_size,
+                        paged_decode_plan_elems, paged_attn_decode_plan, paged_attn_decode,
+                        prefill_q_plan)
 from .inference import (KQuantProjWeight, KQuantExpertWeight, inference_qkv,  # noqa: F401
                         qkv_proj_scratch_bytes, inference_mlp, mlp_workspace_bytes,
                         inference_moe, inference_moe_norm, inference_moe_workspace_bytes,

@@ -44,3 +44,69 @@ def test_error_strings():
     assert _capi.lib.snowllm_error_string(1)
     with pytest.raises(Exception):
         _capi.check(1, "probe")
+
+
+def _type_name(t):
+    import ctypes
+    from snowllm_amd import _capi
+    if t is None:
+        return "None"
+    if t is _capi.Stream:
+        return "S"
+    if t is ctypes.c_void_p:
+        return "P"
+    if t is ctypes.c_int64:   # an alias of c_long here
+        return "c_int64"
+    return t.__name__
+
+
+def test_bindings_match_the_reference_signatures():
+    """Every snowllm_* entry point keeps the reference binding's ctypes signature
+    (snowllm/_capi.py:201-831, as recorded by tests/golden/make_reference_capi_signatures.py),
+    so that the reference's ops wrappers can call this library unchanged."""
+    import json
+    from snowllm_amd import _capi
+    ref = json.loads((ROOT / "tests" / "golden" / "reference_capi_signatures.json").read_text())
+    ref = ref["signatures"]
+    ours = {n: (r, a) for n, r, a in _capi._SIGS if n.startswith("snowllm_")}
+    # the ABI check is bound outside the table in the reference (snowllm/_capi.py:179-194)
+    ours.pop("snowllm_abi_version")
+    missing = sorted(set(ours) - set(ref))
+    assert not missing, f"snowllm_* names the reference does not declare: {missing}"
+    bad = []
+    for name, (res, args) in sorted(ours.items()):
+        want = ref[name]
+        got = {"restype": _type_name(res), "argtypes": [_type_name(a) for a in args]}
+        if got != want:
+            bad.append((name, got, want))
+    assert not bad, "\n".join(f"{n}: ours {g} reference {w}" for n, g, w in bad)
+    # the symbols the reference's hot-path ops modules look up at import are bound
+    # (ops/_common.py:42-43, attention_full.py:511-513, 565, dflash.py:337-338,
+    # embedding.py:44, moe.py:89, 279, mlp.py:71)
+    for name in ("snowllm_sampling_max_k", "snowllm_kv_block_sizes",
+                 "snowllm_paged_decode_max_q_tokens", "snowllm_paged_decode_plan_elems",
+                 "snowllm_qkv_proj_scratch_bytes", "snowllm_attn_out_scale_oproj_scratch_bytes",
+                 "snowllm_draft_paged_attn_workspace_size", "snowllm_draft_paged_attn_num_slots",
+                 "snowllm_lm_head_scratch_bytes", "snowllm_moe_workspace_bytes",
+                 "snowllm_fused_mlp_workspace_bytes", "snowllm_moe_router_shuffle_bytes"):
+        assert name in ours
+
+
+def test_decode_plan_queries():
+    """The split-KV decode sizing queries answer for the default geometry without a GPU."""
+    import ctypes
+    from snowllm_amd import _capi
+    lib = _capi.lib
+    buf = (ctypes.c_int64 * 4)()
+    assert lib.snowllm_kv_block_sizes(None, 0) == 1
+    assert lib.snowllm_kv_block_sizes(buf, 4) == 1 and buf[0] == 16
+    assert 1 <= lib.snowllm_paged_decode_max_q_tokens() <= 64
+    assert lib.snowllm_paged_decode_num_slots(3) == 3
+    assert lib.snowllm_paged_decode_plan_elems(3, 3) >= 1
+    lens = (ctypes.c_int32 * 3)(1, 17, 32)
+    total = lib.snowllm_prefill_q_blocks(lens, 3)
+    assert total == 1 + 2 + 2
+    m = (ctypes.c_int32 * (2 * total))()
+    lib.snowllm_prefill_q_block_map(lens, 3, m)
+    assert list(m) == [0, 0, 1, 0, 1, 16, 2, 0, 2, 16]
+    assert lib.snowllm_paged_attention_prepared_bytes(1, 9, 1, 0) == 0

@@ -180,3 +180,43 @@ def test_unsupported_features_are_refused(gpu, geometry_of):
     assert ops.attn_output_gating(torch.empty(9, 8, dtype=torch.bfloat16, device="cuda"),
                                   False, False)[0] == 0
     assert ops.paged_attention_varlen(True, 9, False) and not ops.paged_attention_varlen(False, 9, False)
+
+
+def test_split_kv_decode_entry_equals_explicit_attention(gpu, geometry_of):
+    """snowllm_paged_attn_decode (the reference's split-KV decode signature, with its plan call
+    and a q read at a row pitch from row q_row0) gives the explicit-shape attention's bits."""
+    from snowllm_amd import ops
+    from snowllm_amd.verify import VerifyConfig
+    cfg = VerifyConfig("decode_geo", layers=1, hidden=2048, heads=16, kv_heads=2, head_dim=256,
+                       rot_half=32, rope_theta=1e7, vocab=2048, context=3000, block=9,
+                       experts=16, expert_ffn=512, topk=4)
+    geometry_of(cfg)
+    print("split-KV decode entry, 3 sequences", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(31)
+    T, Hq, Hkv, D = 9, 16, 2, 256
+    lengths = [3000 + T, 777 + T, 40 + T]
+    B = len(lengths)
+    width = max((L + 15) // 16 for L in lengths)
+    blocks = B * width + 5
+    kp = torch.randn(blocks, Hkv, D // 16, 16, 16, device="cuda", generator=g).bfloat16()
+    vp = torch.randn(blocks, Hkv, 4, D, 4, device="cuda", generator=g).bfloat16()
+    table = torch.randperm(blocks, device="cuda", generator=g)[:B * width].int().view(B, width)
+    lens = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    pitch, row0 = Hq * D + 512, 2
+    buf = torch.randn(row0 + B * T, pitch, device="cuda", generator=g).bfloat16()
+    q = buf[row0:, :Hq * D].contiguous().view(B * T, Hq, D)
+    want = torch.empty_like(q)
+    scratch = torch.empty(ops.paged_attention_explicit_scratch_bytes(B, T, Hq, Hkv, D),
+                          dtype=torch.uint8, device="cuda")
+    ops.paged_attention_explicit(q, kp, vp, want, table, lens, D ** -0.5, scratch)
+    slots = ops.paged_decode_num_slots(B)
+    plan = torch.empty(ops.paged_decode_plan_elems(B, slots), dtype=torch.int32, device="cuda")
+    ws = torch.empty(ops.paged_decode_workspace_size(slots, T), dtype=torch.uint8, device="cuda")
+    ops.paged_attn_decode_plan(lens, plan, slots, 16)
+    got = torch.empty_like(q)
+    ops.paged_attn_decode(buf, lens, kp, vp, got, table, plan, ws, B, slots, D ** -0.5, 16,
+                          q_tokens=T, q_pitch=pitch, q_row0=row0)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert T <= ops.PAGED_DECODE_MAX_Q_TOKENS
+    assert ops.paged_attention_prepare(lens, T, slots, 16, False) is None
