@@ -155,6 +155,17 @@ int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8
                                    int64_t M, int64_t N, int64_t K, int c_is_bf16,
                                    const void* ws, void* stream);
 
+/* No counterpart in the reference: snowllm_gemm_kquant_a for callers that cannot allocate
+ * (code under HIP-graph capture, tight serving loops, harnesses that forbid hipMalloc). It
+ * allocates nothing and takes no workspace: up to 16 rows the GEMV converts the activations
+ * itself; above that the operand workspace is a device array inside the library, 2,244,608
+ * bytes per GPU for the life of the process. M <= 64 and K <= 16384, larger sizes return
+ * hipErrorInvalidValue. Calls on one GPU share that array: calls that overlap on one device
+ * (different streams) race. */
+int snowverify_gemm_kquant_a_noalloc(int fmt, const void* a, const uint8_t* quant,
+                                     const uint8_t* meta, void* c, int64_t M, int64_t N,
+                                     int64_t K, int c_is_bf16, void* stream);
+
 /* ---- paged attention --------------------------------------------------------------- */
 
 /* Scratch bytes of snowverify_paged_attention (split-KV partials). */

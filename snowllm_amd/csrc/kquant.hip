@@ -17,6 +17,8 @@
 // bf16 input.
 #include "kquant_core.h"
 
+#include <mutex>
+
 namespace {
 using namespace kq;
 
@@ -278,6 +280,62 @@ SV_API int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, c
                : dispatch_gemv<FMT_Q8_0, true>(quant, meta, a, c, (int)M, (int)N, (int)(K / 256), c_is_bf16, s);
   }
   int rc = snowverify_gemm_kquant_prepare_a(a, M, K, ws, stream);
+  if (rc) return rc;
+  return snowverify_gemm_kquant_a_prepared(fmt, quant, meta, c, M, N, K, c_is_bf16, ws, stream);
+}
+
+// ---------------------------------------------------------------------------------------
+// The no-allocation form of snowllm_gemm_kquant_a, for callers that cannot allocate (code
+// under HIP-graph capture, tight serving loops, harnesses that forbid hipMalloc). Up to 16
+// rows the GEMV converts the activations itself and needs no workspace; above that the
+// operand workspace lives in `scratch`, a file-scope device array of a fixed size -- each GPU
+// the library runs on holds its own copy until the process ends. Host code never passes the
+// array's name to a kernel: its device address is read once per device with
+// hipGetSymbolAddress, with that device current, and kept.
+// ---------------------------------------------------------------------------------------
+namespace {
+constexpr int64_t NOALLOC_MAX_M = 64, NOALLOC_MAX_K = 16384;
+constexpr size_t NOALLOC_WS_BYTES = 2244608;  // snowllm_gemm_kquant_a_ws_bytes(64, 16384)
+static __device__ __align__(256) uint8_t scratch[NOALLOC_WS_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES];
+
+// The current device's address of `scratch`.
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= MAX_DEVICES) return SV_ENOTSUP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!p) return SV_EINVAL;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SV_OK;
+}
+}  // namespace
+
+SV_API int snowverify_gemm_kquant_a_noalloc(int fmt, const void* a, const uint8_t* quant,
+                                            const uint8_t* meta, void* c, int64_t M, int64_t N,
+                                            int64_t K, int c_is_bf16, void* stream) {
+  if (!fmt_ok(fmt) || M < 0 || N <= 0 || K <= 0 || K % 256 || N % TILE_N) return SV_EINVAL;
+  if (M > NOALLOC_MAX_M || K > NOALLOC_MAX_K) return SV_EINVAL;  // beyond the array
+  if (M == 0) return SV_OK;
+  if (M <= TILE_M)  // the one-launch form: no workspace
+    return snowllm_gemm_kquant_a(fmt, a, quant, meta, c, M, N, K, c_is_bf16, nullptr, stream);
+  if ((size_t)snowllm_gemm_kquant_a_ws_bytes(M, K) > NOALLOC_WS_BYTES) return SV_EINVAL;
+  void* ws = nullptr;
+  int rc = scratch_address(&ws);
+  if (rc) return rc;
+  // the prep pass writes every byte of the workspace the GEMV reads (padding rows included),
+  // so nothing needs clearing between calls
+  rc = snowverify_gemm_kquant_prepare_a(a, M, K, ws, stream);
   if (rc) return rc;
   return snowverify_gemm_kquant_a_prepared(fmt, quant, meta, c, M, N, K, c_is_bf16, ws, stream);
 }

@@ -63,3 +63,21 @@ def gemm_kquant_a_prepared(fmt: int, quant: torch.Tensor, meta: torch.Tensor, c:
     _chk(c, "c", torch.bfloat16 if bf16 else torch.float32, M, N)
     check(lib.snowverify_gemm_kquant_a_prepared(fmt, _p(quant), _p(meta), _p(c), M, N, K, bf16, _p(ws),
                                              _stream()), "gemm_kquant_a_prepared")
+
+
+GEMM_NOALLOC_MAX_M, GEMM_NOALLOC_MAX_K = 64, 16384
+
+
+def gemm_kquant_a_noalloc(fmt: int, a: torch.Tensor, quant: torch.Tensor, meta: torch.Tensor,
+                          c: torch.Tensor, M: int, N: int, K: int) -> None:
+    """gemm_kquant_a without a workspace and without any allocation (extension, for callers
+    that cannot allocate): M <= 64, K <= 16384; the library's per-GPU operand array is shared,
+    so calls that overlap on one GPU race."""
+    if M > GEMM_NOALLOC_MAX_M or K > GEMM_NOALLOC_MAX_K:
+        raise SnowLLMError(f"gemm_kquant_a_noalloc: M={M}, K={K} exceed its workspace "
+                           f"(M <= {GEMM_NOALLOC_MAX_M}, K <= {GEMM_NOALLOC_MAX_K})")
+    _chk(a, "a", torch.bfloat16, M, K)
+    bf16 = c.dtype is torch.bfloat16
+    _chk(c, "c", torch.bfloat16 if bf16 else torch.float32, M, N)
+    check(lib.snowverify_gemm_kquant_a_noalloc(fmt, _p(a), _p(quant), _p(meta), _p(c), M, N, K,
+                                               bf16, _stream()), "gemm_kquant_a_noalloc")
