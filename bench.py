@@ -15,6 +15,8 @@ Workloads:
   config3  BASELINE config 3: the dense 8B-shaped step (36 layers, Q4_K, SwiGLU 14336).
   config5  BASELINE config 5: the MoE shape at 220000 tokens of context, tree block of 11 rows.
   gemv     BASELINE config 2: one Q4_K dequant-GEMV, M=9, K=4096, N=14336, bf16 out.
+  config1  BASELINE config 1: the acceptance alone (9 rows x 151936), T=1 rejection sampling
+           and greedy straight from the logits, with the list-based forms timed beside them.
 """
 import argparse
 import json
@@ -158,6 +160,127 @@ def bench_gemv(args):
 
 
 # ---------------------------------------------------------------------------------------
+# config 1: acceptance only
+# ---------------------------------------------------------------------------------------
+def acceptance_inputs(k=8, V=151936):
+    """target logits [k+1, V] and draft logits [k, V] ~N(0, 2^2), drafts
+    sampled from the draft softmax with seed 0, acceptance uniforms U(0,1) with seed 1."""
+    import torch
+    g10, g11 = torch.Generator().manual_seed(10), torch.Generator().manual_seed(11)
+    target = torch.randn(k + 1, V, generator=g10) * 2
+    draft = torch.randn(k, V, generator=g11) * 2
+    drafts = torch.multinomial(draft.softmax(-1), 1, generator=torch.Generator().manual_seed(0))
+    uniform = torch.rand(1, k + 1, generator=torch.Generator().manual_seed(1))
+    return target, draft, drafts.view(1, k), uniform
+
+
+def time_acceptance(reps=200):
+    """Config 1 on the device, inputs resident: (greedy us, rejection us) straight from the
+    logits, the list-based forms beside them, the accept lengths / emitted ids (checked
+    against the oracle) and the algorithmic bytes of each mode."""
+    import numpy as np
+    import torch
+    from snowllm_amd import ops
+    from oracle import accept as A
+    target, draft, drafts, uniform = acceptance_inputs()
+    k, V = drafts.shape[1], target.shape[1]
+    T = k + 1
+    dev = lambda x: x.cuda()
+    tl, dl, dr, u = dev(target), dev(draft), dev(drafts), dev(uniform)
+    ones = torch.ones(T, device="cuda")
+    kmax = torch.full((T,), ops.SAMPLING_MAX_K, dtype=torch.int32, device="cuda")
+    ws = torch.empty(ops.sample_workspace_bytes(T, V, V), dtype=torch.uint8, device="cuda")
+    q = torch.empty(k, V, device="cuda")
+    qid = torch.empty(k, V, dtype=torch.int64, device="cuda")
+    ops.probabilities(dl, kmax[:k], ones[:k], ones[:k], V, q, qid, ws)  # the draft side
+    q3, qid3 = q.view(1, k, V), qid.view(1, k, V)
+    slot = torch.zeros(1, dtype=torch.int32, device="cuda")
+    valid = torch.ones(1, dtype=torch.int32, device="cuda")
+    out = torch.empty(1, T, dtype=torch.int64, device="cuda")
+    acc = torch.empty(1, dtype=torch.int64, device="cuda")
+    tokens = torch.empty(1, T, dtype=torch.int64, device="cuda")
+    p = torch.empty(T, V, device="cuda")
+    pid = torch.empty(T, V, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def fused_rej():
+        ops.dflash.accept_reject(tl, dr, qid3, q3, slot, valid, u, out, acc)
+
+    def lists_rej():
+        ops.probabilities(tl, kmax, ones, ones, V, p, pid, ws)
+        ops.dflash.reject(p, pid, dr, qid3, q3, slot, valid, u, out, acc)
+
+    def fused_greedy():
+        ops.dflash.accept_greedy(tl, dr, tokens, acc)
+
+    def two_greedy():
+        ops.argmax(tl, out=tokens.view(-1))
+        ops.spec_accept(tokens, dr, out=acc)
+
+    res = {}
+    for name, fn in (("rejection", fused_rej), ("rejection_lists", lists_rej),
+                     ("greedy", fused_greedy), ("greedy_argmax_then_prefix", two_greedy)):
+        res[name] = round(timed_graph(fn, reps, stream, per=reps) * 1e3, 2)
+    # parity on the benchmark inputs (the oracle is the checker only)
+    fused_rej()
+    torch.cuda.synchronize()
+    p_ref = A.softmax(target.numpy())
+    q_ref = A.softmax(draft.numpy())
+    ident = np.tile(np.arange(V), (T, 1))
+    want_out, want_acc = A.reject(p_ref, ident, drafts.numpy(), ident[:k][None], q_ref[None],
+                                  np.zeros(1, np.int32), np.ones(1, np.int32), uniform.numpy())
+    assert np.array_equal(out.cpu().numpy(), want_out) and int(acc[0]) == int(want_acc[0])
+    rej = {"accepted": int(acc[0]), "emitted": out[0, :int(acc[0])].tolist()}
+    fused_greedy()
+    torch.cuda.synchronize()
+    want_tok = A.argmax(target.numpy())
+    assert np.array_equal(tokens.cpu().numpy()[0], want_tok)
+    gre = {"accepted": int(acc[0]), "emitted": tokens[0, :int(acc[0])].tolist()}
+    return {"us": res, "rejection": rej, "greedy": gre,
+            "alg_bytes": {"greedy": T * V * 4, "rejection": (T + k) * V * 4}}
+
+
+def bench_config1(args):
+    import numpy as np
+    import torch
+    from oracle import accept as A
+    r = time_acceptance(reps=max(args.steps, 50))
+    us_g, us_r = r["us"]["greedy"], r["us"]["rejection"]
+    gbs_r = r["alg_bytes"]["rejection"] / (us_r * 1e-6) / 1e9
+    gbs_g = r["alg_bytes"]["greedy"] / (us_g * 1e-6) / 1e9
+    # CPU path: the oracle's softmax + rejection and argmax + prefix on this host (kind port)
+    target, draft, drafts, uniform = acceptance_inputs()
+    T, V = target.shape
+    cores = cpu_cores()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < 5.0 or n < 3:
+        p = A.softmax(target.numpy())
+        q = A.softmax(draft.numpy())
+        ident = np.tile(np.arange(V), (T, 1))
+        A.reject(p, ident, drafts.numpy(), ident[:T - 1][None], q[None], np.zeros(1, np.int32),
+                 np.ones(1, np.int32), uniform.numpy())
+        n += 1
+    cpu_us = (time.perf_counter() - t0) / n * 1e6
+    return {
+        "metric": METRIC, "value": us_r, "unit": "us", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us_r / 1e3, 6), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32 logits, 44-bit fixed-point sums",
+        "data": "synthetic (BASELINE config 1 generators: N(0,2^2) logits, seeds 0/1)",
+        "config": {"workload": "config1_acceptance", "k": T - 1, "vocab": V,
+                   "modes": ["T=1.0 rejection (value)", "greedy"]},
+        "acceptance_us": r["us"], "rejection": r["rejection"], "greedy": r["greedy"],
+        "roofline": {"bound": "hbm", "kernel": "fa_max + fa_sum + fa_pick (step)", "achieved": round(gbs_r, 1),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs_r / PEAK_HBM_GBS, 4),
+                     "traffic": None, "alg_bytes_per_launch": r["alg_bytes"]["rejection"],
+                     "kernel_us": us_r, "greedy_gbs": round(gbs_g, 1)},
+        "cpu_baseline": {"value": round(cpu_us, 1), "unit": "us", "cores": 1, "kind": "port",
+                         "cpu": cpu_model(),
+                         "sample": f"oracle softmax x2 + rejection sampling (C, one thread) x{n}"},
+    }
+
+
+# ---------------------------------------------------------------------------------------
 # configs 3-5: the full verify step
 # ---------------------------------------------------------------------------------------
 def q4k_bytes(n, k):
@@ -203,14 +326,16 @@ def step_bytes(cfg, slots, selector=False):
     return total
 
 
-def timed_graph(fn, reps, stream):
+def timed_graph(fn, reps, stream, per=1):
+    """ms per replay of a graph holding `per` calls of fn (divided by per)."""
     import torch
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        fn()
+        for _ in range(per):
+            fn()
     g.replay()
     torch.cuda.synchronize()
-    return time_events(lambda: g.replay(), reps, stream)
+    return time_events(lambda: g.replay(), max(1, reps // per), stream) / per
 
 
 def bench_step(args, name):
@@ -325,8 +450,11 @@ def bench_step(args, name):
         sb = k * V * 4 + k * (2 * 16 + 1) * SEL_RANK * 2
         kern["draft_select (chunks + table + walk)"] = {
             "us": round(us, 3), "alg_bytes": int(sb), "gbs": round(sb / (us * 1e-6) / 1e9, 1)}
+    if cfg.name == CONFIGS["config4"].name:
+        # BASELINE config 1 (the acceptance alone) beside the north-star step
+        kern["config1_acceptance"] = time_acceptance(reps=200)
     # dominant single kernel per step (launch time x launches per step)
-    single = {kk: v for kk, v in kern.items() if "+" not in kk}
+    single = {kk: v for kk, v in kern.items() if "+" not in kk and "us" in v}
     dom = max(single, key=lambda kk: single[kk]["us"])
     d = kern[dom]
     traffic = read_traffic(dom) if cfg.name == CONFIGS[TRAFFIC_WORKLOAD].name else None
@@ -481,7 +609,8 @@ def bench_copy(args):
             "config": {"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes}}
 
 
-WORKLOADS = {"gemv": bench_gemv, "copy": bench_copy, "config3": lambda a: bench_step(a, "config3"),
+WORKLOADS = {"gemv": bench_gemv, "copy": bench_copy, "config1": bench_config1,
+             "config3": lambda a: bench_step(a, "config3"),
              "config4": lambda a: bench_step(a, "config4"),
              "config5": lambda a: bench_step(a, "config5")}
 

@@ -87,6 +87,27 @@ int snowllm_draft_reject(const float* p, const int64_t* ids, const int64_t* draf
                          int64_t* accepted, int64_t b, int64_t width, int64_t p_width,
                          int64_t q_width, void* stream);
 
+/* Extension: the acceptance straight from the target logits, for requests whose candidate
+ * lists are the whole vocabulary in vocabulary order (top-k >= vocab, top-p 1) -- the DFlash
+ * verify's rejection branch (snowllm/engine/dflash_sampling.py:61-69) with the arithmetic, and
+ * so the bits, of snowllm_sampling_softmax + snowllm_sampling_topk_topp + snowllm_draft_reject,
+ * in three launches that never materialise the probabilities and never wait on one another's
+ * workgroups. logits [b*width, vocab] f32, temperature [b*width] (NULL: 1; <= 0 counts as 1);
+ * the rest as snowllm_draft_reject. b*width <= 256, width <= 64. Calls on one device must be
+ * stream-ordered (library-owned statistics). */
+int snowverify_accept_reject(const float* logits, const float* temperature,
+                             const int64_t* drafts, const int64_t* cand, const float* q,
+                             const int32_t* slots, const int32_t* valid, const float* uniform,
+                             int64_t* out, int64_t* accepted, int64_t b, int64_t width,
+                             int64_t vocab, int64_t q_width, void* stream);
+/* Extension: the greedy branch (snowllm/engine/dflash_sampling.py:56-59; spec_decode.py:
+ * 196-207) in one launch: tokens [b, width] = argmax of each logit row (as
+ * snowllm_sampling_argmax), accepted [b] = 1 + leading matches with drafts [b, width-1] (as
+ * snowllm_spec_accept). Limits as snowverify_accept_reject. */
+int snowverify_accept_greedy(const float* logits, const int64_t* drafts, int64_t* tokens,
+                             int64_t* accepted, int64_t b, int64_t width, int64_t vocab,
+                             void* stream);
+
 /* ---- DFlash 2 candidate selector (snowllm/ops/dflash.py:164-198; semantics
  * tests/test_dflash_sampling.py:44-75, tests/test_dflash_selector_topk.py:42-61) ------------
  * Per position: the 16 largest logits (stable descending, NaN as -inf), scores = values +

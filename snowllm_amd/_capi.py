@@ -71,6 +71,8 @@ _SIGS = [
     ("snowllm_sampling_topk_topp", c_int, [P, P, P, c_int64, c_int64, c_int64, P, P, S]),
     ("snowllm_sampling_sample", c_int, [P] * 7 + [c_int64] * 4 + [S]),
     ("snowllm_draft_reject", c_int, [P] * 10 + [c_int64] * 4 + [S]),
+    ("snowverify_accept_reject", c_int, [P] * 10 + [c_int64] * 4 + [S]),
+    ("snowverify_accept_greedy", c_int, [P] * 4 + [c_int64] * 3 + [S]),
     # DFlash 2 selector
     ("snowllm_draft_select_scratch_bytes", c_int64, [c_int64]),
     ("snowllm_draft_select", c_int, [P] * 7 + [c_int64] * 3 + [S]),

@@ -974,3 +974,496 @@ SV_API int snowllm_draft_reject(const float* p, const int64_t* ids, const int64_
   }
   return SV_OK;
 }
+
+// =======================================================================================
+// Acceptance straight from the target logits, for requests whose candidate lists are the
+// whole vocabulary in vocabulary order (top-k at least the vocabulary, top-p 1): the
+// arithmetic of snowllm_sampling_softmax + snowllm_sampling_topk_topp + snowllm_draft_reject
+// on those rows -- the same bits -- without the dense [rows, V] probabilities, in three
+// launches; and the greedy form (argmax of every row + prefix acceptance) in one.
+//
+// Workgroup (row, w) takes slice w (FA_SLICE logits, FA_E per thread, coalesced) of a row.
+//   1. slice maxima of x / T;
+//   2. numerators e = exp(x / T - M) with the row maximum M, the slice's fixed-point sum and
+//      the draft token's numerator; the request's last workgroup to finish (a counter)
+//      forms every row's Z and the accepted prefix;
+//   3. the workgroups of the row where the prefix stops form the residual max(p - q, 0) (p at
+//      the bonus row) and its fixed-point sums per 4 * FA_NT-logit sub-chunk; the request's
+//      last one finds the sub-chunk holding floor(u R), counts its prefix there and writes
+//      the outputs.
+// Nothing waits for another workgroup. A counter advances by exactly FA_QUANTUM per launch
+// (each participant adds 1, one adds the quantum's rest), so the last arriver is the one
+// whose add completes the quantum; nothing is ever reset. Statistics are written with
+// device-scope stores, each thread waits for its stores (vmcnt(0)) before its workgroup's
+// add, and the last arriver reads them with device-scope loads after its add returned.
+// =======================================================================================
+namespace {
+
+constexpr int FA_NT = 512;                      // threads per workgroup
+constexpr int FA_E = 16;                        // logits per thread
+constexpr int FA_SLICE = FA_NT * FA_E;          // logits per workgroup
+constexpr int FA_P_MAX = (int)(VOCAB_MAX / FA_SLICE);  // slices per row
+constexpr int FA_SUB = 4 * FA_NT;               // logits per sub-chunk of a slice
+constexpr int FA_SUBCHUNKS = FA_E / 4;          // sub-chunks per slice
+constexpr int FA_ROWS = 256;                    // rows (b * width) per launch
+constexpr uint64_t FA_QUANTUM = 1ull << 20;
+static_assert(FA_SLICE * FA_P_MAX == VOCAB_MAX, "slices cover the vocabulary limit");
+
+__device__ uint32_t g_fa_maxkey[FA_ROWS][FA_P_MAX];
+__device__ uint64_t g_fa_sum[FA_ROWS][FA_P_MAX];
+__device__ uint32_t g_fa_edraft[FA_ROWS];       // a draft token's numerator (f32 bits)
+__device__ int32_t g_fa_first[FA_ROWS];         // per request: where the prefix stops
+__device__ uint64_t g_fa_rsub[FA_ROWS][FA_P_MAX][FA_SUBCHUNKS];
+__device__ uint64_t g_fa_psub[FA_ROWS][FA_P_MAX][FA_SUBCHUNKS];
+__device__ uint64_t g_fa_amax[FA_ROWS][FA_P_MAX];
+__device__ uint64_t g_fa_cnt[3][FA_ROWS];       // per request: stage 2, stage 3, greedy
+
+template <class T>
+__device__ __forceinline__ void dev_store(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T dev_load(T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// This workgroup's arrival at a request's counter of n participants (lead: the one that
+// adds the rest of the quantum). True in every thread of the workgroup that arrived last.
+__device__ bool fa_last_arrival(uint64_t* cnt, int n, bool lead) {
+  __shared__ uint32_t s_last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint64_t inc = lead ? FA_QUANTUM - (uint64_t)n + 1 : 1;
+    const uint64_t old =
+        __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = ((old + inc) & (FA_QUANTUM - 1)) == 0;
+  }
+  __syncthreads();
+  return s_last != 0;
+}
+
+struct FaArgs {
+  const float* logits;       // [b * width, V]
+  const float* temperature;  // [b * width] or null
+  const int64_t* drafts;     // [b, width - 1]
+  const int64_t* cand;       // [S, width - 1, q_width]
+  const float* q;
+  const int32_t* slots;
+  const int32_t* valid;
+  const float* uniform;      // [b, width]
+  int64_t* out;              // [b, width]
+  int64_t* accepted;         // [b]
+  int V, width, P;
+  int64_t q_width;
+};
+
+// x[i] / T of this thread's FA_E logits of slice w (loads at clamped indices, all in flight)
+__device__ __forceinline__ void fa_load_slice(const float* x, int lo, int V, float T,
+                                              float (&v)[FA_E]) {
+#pragma unroll
+  for (int k = 0; k < FA_E; ++k) {
+    const int i = lo + k * FA_NT + (int)threadIdx.x;
+    v[k] = x[i < V ? i : V - 1];
+  }
+#pragma unroll
+  for (int k = 0; k < FA_E; ++k) v[k] = __fdiv_rn(v[k], T);
+}
+
+// Statistics are read one per lane (a device-scope load is a round trip to memory; one
+// thread reading them in turn would pay it per value), then reduced in wave 0.
+__device__ __forceinline__ float fa_row_max(int row, int P) {
+  __shared__ uint32_t s_m;
+  if (threadIdx.x < WAVE) {
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < P; i += WAVE) {
+      const uint32_t k = dev_load(&g_fa_maxkey[row][i]);
+      m = k > m ? k : m;
+    }
+    m = wave_max(m);
+    if (threadIdx.x == 0) s_m = m;
+  }
+  __syncthreads();
+  return ord_key_to_float(s_m);
+}
+
+// Z of a row (wave 0; the result in lane 0 is broadcast through s_z by the caller).
+__device__ __forceinline__ uint64_t fa_row_zsum(int row, int P) {
+  uint64_t z = 0;
+  for (int i = threadIdx.x; i < P; i += WAVE) z += dev_load(&g_fa_sum[row][i]);
+  return wave_sum_u64(z);
+}
+
+__global__ void __launch_bounds__(FA_NT) fa_max_kernel(FaArgs a) {
+  __shared__ uint64_t red[FA_NT / WAVE];
+  const int w = blockIdx.x % a.P, row = blockIdx.x / a.P;
+  const int lo = w * FA_SLICE;
+  float v[FA_E];
+  fa_load_slice(a.logits + (int64_t)row * a.V, lo, a.V, row_temperature(a.temperature, row), v);
+  uint32_t mk = 0;
+#pragma unroll
+  for (int k = 0; k < FA_E; ++k) {
+    const uint32_t key = ord_key(v[k]);
+    if (lo + k * FA_NT + (int)threadIdx.x < a.V) mk = key > mk ? key : mk;
+  }
+  mk = (uint32_t)block_max_u64<FA_NT>(mk, red);
+  if (threadIdx.x == 0) dev_store(&g_fa_maxkey[row][w], mk);
+}
+
+__global__ void __launch_bounds__(FA_NT) fa_sum_kernel(FaArgs a) {
+  __shared__ uint64_t red[FA_NT / WAVE];
+  __shared__ float red_f[4];
+  const int P = a.P, width = a.width, length = width - 1, V = a.V;
+  const int w = blockIdx.x % P, row = blockIdx.x / P;
+  const int r = row / width, j = row % width;
+  const int t = threadIdx.x, lo = w * FA_SLICE;
+  float v[FA_E];
+  fa_load_slice(a.logits + (int64_t)row * V, lo, V, row_temperature(a.temperature, row), v);
+  const float M = fa_row_max(row, P);
+  const int64_t dtok = j < length ? a.drafts[(int64_t)r * length + j] : -1;
+  uint64_t sum = 0;
+#pragma unroll
+  for (int k = 0; k < FA_E; ++k) {
+    const int i = lo + k * FA_NT + t;
+    const float e = canon_exp(__fsub_rn(v[k], M));
+    if (i < V) {
+      sum += canon_fix(e);
+      if (i == dtok) dev_store(&g_fa_edraft[row], __float_as_uint(e));
+    }
+  }
+  sum = block_sum_u64<FA_NT>(sum, red);
+  if (t == 0) dev_store(&g_fa_sum[row][w], sum);
+  if (!fa_last_arrival(&g_fa_cnt[0][r], width * P, j == 0 && w == 0)) return;
+  // the request's last workgroup: u_j q(d_j) >= p(d_j) stops the accepted prefix. Every
+  // draft row's sums and numerator are read at once, one per thread.
+  __shared__ uint64_t s_rs[64][FA_P_MAX];
+  __shared__ float s_ed[64];
+  for (int i = t; i < length * P; i += FA_NT)
+    s_rs[i / P][i % P] = dev_load(&g_fa_sum[r * width + i / P][i % P]);
+  for (int jj = t; jj < length; jj += FA_NT)
+    s_ed[jj] = __uint_as_float(dev_load(&g_fa_edraft[r * width + jj]));
+  __syncthreads();
+  const int slot = a.slots[r];
+  const bool valid = a.valid[r] != 0;
+  // q(d_j) of every draft row at once: thread j looks its token up (the direct slot of an
+  // identity list, or a search of a short list); longer non-identity lists are searched by
+  // the whole block below
+  __shared__ float s_qt[64];
+  __shared__ int s_search;
+  if (t == 0) s_search = 0;
+  __syncthreads();
+  if (t < length) {
+    const int64_t token = a.drafts[(int64_t)r * length + t];
+    float qt = 1.0f;
+    if (valid) {
+      const int64_t qrow = ((int64_t)slot * length + t) * a.q_width;
+      const float* qr = a.q + qrow;
+      const int64_t* cr = a.cand + qrow;
+      if (token >= 0 && token < a.q_width && cr[token] == token) {
+        qt = qr[token];
+      } else if (a.q_width <= Q_STAGE) {
+        qt = row_prob_thread(qr, cr, a.q_width, token);
+      } else {
+        qt = -1.0f;
+        atomicOr(&s_search, 1);
+      }
+    }
+    s_qt[t] = qt;
+  }
+  __syncthreads();
+  if (s_search)
+    for (int jj = 0; jj < length; ++jj) {
+      if (s_qt[jj] >= 0.0f) continue;  // (uniform: every thread reads the same value)
+      const int64_t qrow = ((int64_t)slot * length + jj) * a.q_width;
+      const float qt = row_prob_block(a.q + qrow, a.cand + qrow, a.q_width,
+                                      a.drafts[(int64_t)r * length + jj], red_f);
+      if (t == 0) s_qt[jj] = qt;
+      __syncthreads();
+    }
+  if (t == 0) {
+    int first = length;
+    for (int jj = 0; jj < length; ++jj) {
+      const int64_t token = a.drafts[(int64_t)r * length + jj];
+      uint64_t z = 0;
+      for (int i = 0; i < P; ++i) z += s_rs[jj][i];
+      const float Zf = canon_unfix(z);
+      float pt = 0.0f;
+      if (token >= 0 && token < V) pt = Zf > 0.0f ? canon_div(s_ed[jj], Zf) : 0.0f;
+      if (__fmul_rn(a.uniform[(int64_t)r * width + jj], s_qt[jj]) >= pt) {
+        first = jj;
+        break;
+      }
+    }
+    g_fa_first[r] = first;
+  }
+}
+
+// The residual of row `first` for stage 3: q row staged (short candidate lists) or read
+// directly (the identity layout), or the one-hot draft when the proposal is not valid.
+__device__ ResidualRow fa_residual(const FaArgs& a, int r, int first, int64_t* s_cand,
+                                   float* s_q, uint32_t* s_bits) {
+  const int length = a.width - 1;
+  ResidualRow rr;
+  rr.p = nullptr;
+  rr.ids = nullptr;
+  rr.subtract = first < length;
+  if (rr.subtract && a.valid[r] != 0) {
+    const int64_t qrow = ((int64_t)a.slots[r] * length + first) * a.q_width;
+    rr.q = a.q + qrow;
+    rr.cand = a.cand + qrow;
+  } else {
+    rr.q = nullptr;
+    rr.cand = nullptr;
+  }
+  rr.q_width = a.q_width;
+  rr.draft = rr.subtract ? a.drafts[(int64_t)r * length + first] : -1;
+  stage_q(rr, s_cand, s_q, s_bits);
+  return rr;
+}
+
+__global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
+  __shared__ uint64_t red[FA_NT / WAVE];
+  __shared__ uint64_t s_sub[2][FA_NT / WAVE][FA_SUBCHUNKS];
+  __shared__ uint64_t buf[FA_NT];
+  __shared__ int64_t s_cand[Q_STAGE];
+  __shared__ float s_q[Q_STAGE];
+  __shared__ uint32_t s_bits[Q_BITS_WORDS];
+  __shared__ float s_zf;
+  __shared__ int s_slice, s_sub_i, s_use_p;
+  __shared__ uint64_t s_base, s_target;
+  const int P = a.P, width = a.width, length = width - 1, V = a.V;
+  const int w = blockIdx.x % P, r = blockIdx.x / P;
+  const int t = threadIdx.x, lo = w * FA_SLICE;
+  const int first = g_fa_first[r];
+  const int row = r * width + first;
+  const float* x = a.logits + (int64_t)row * V;
+  const float T = row_temperature(a.temperature, row);
+  float v[FA_E];
+  fa_load_slice(x, lo, V, T, v);
+  const float M = fa_row_max(row, P);
+  if (t < WAVE) {
+    const uint64_t z = fa_row_zsum(row, P);
+    if (t == 0) s_zf = canon_unfix(z);
+  }
+  ResidualRow rr = fa_residual(a, r, first, s_cand, s_q, s_bits);  // (synchronises the block)
+  const float Zf = s_zf;
+  // residual and p of every logit, summed per sub-chunk (sub-chunk c = k in [4c, 4c + 4)).
+  // An identity q row is read here, all of the thread's values at once.
+  float qv[FA_E];
+  int64_t cv[FA_E];
+  const bool direct_q = rr.q && !rr.bits && rr.subtract;
+  if (direct_q) {
+#pragma unroll
+    for (int k = 0; k < FA_E; ++k) {
+      const int i = lo + k * FA_NT + t;
+      const bool in_q = i < rr.q_width;
+      qv[k] = in_q ? rr.q[i] : 0.0f;
+      cv[k] = in_q ? rr.cand[i] : -1;
+    }
+  }
+  auto residual = [&](int k, int ii, float p) -> float {
+    if (!direct_q) return rr.from_loaded(ii, p, ii);
+    // as ResidualRow::from_loaded on an identity layout (ids[k] == k)
+    const float qk = cv[k] == ii ? qv[k] : row_prob_thread(rr.q, rr.cand, rr.q_width, ii);
+    const float d = __fsub_rn(p, qk);
+    return d > 0.0f ? d : 0.0f;
+  };
+  const int wv = t / WAVE, l = t % WAVE;
+#pragma unroll
+  for (int c = 0; c < FA_SUBCHUNKS; ++c) {
+    uint64_t rs = 0, ps = 0;
+#pragma unroll
+    for (int k = 4 * c; k < 4 * c + 4; ++k) {
+      const int i = lo + k * FA_NT + t;
+      const int ii = i < V ? i : V - 1;
+      const float e = canon_exp(__fsub_rn(v[k], M));
+      const float p = Zf > 0.0f ? canon_div(e, Zf) : 0.0f;
+      if (i < V) {  // (padding never reaches the list search)
+        rs += canon_fix(residual(k, ii, p));
+        ps += canon_fix(p);
+      }
+    }
+    rs = wave_sum_u64(rs);
+    ps = wave_sum_u64(ps);
+    if (l == 0) {
+      s_sub[0][wv][c] = rs;
+      s_sub[1][wv][c] = ps;
+    }
+  }
+  __syncthreads();
+  if (t < 2 * FA_SUBCHUNKS) {
+    const int kind = t / FA_SUBCHUNKS, c = t % FA_SUBCHUNKS;
+    uint64_t s = 0;
+    for (int q = 0; q < FA_NT / WAVE; ++q) s += s_sub[kind][q][c];
+    dev_store(kind ? &g_fa_psub[r][w][c] : &g_fa_rsub[r][w][c], s);
+  }
+  if (!fa_last_arrival(&g_fa_cnt[1][r], P, w == 0)) return;
+  // the request's last workgroup: #{k : prefix(k) <= floor(u R)} over the row; every
+  // sub-chunk sum read at once, one per thread
+  __shared__ uint64_t s_all[2][FA_P_MAX * FA_SUBCHUNKS];
+  for (int i = t; i < 2 * P * FA_SUBCHUNKS; i += FA_NT) {
+    const int kind = i / (P * FA_SUBCHUNKS), e = i % (P * FA_SUBCHUNKS);
+    s_all[kind][e] = kind ? dev_load(&g_fa_psub[r][e / FA_SUBCHUNKS][e % FA_SUBCHUNKS])
+                          : dev_load(&g_fa_rsub[r][e / FA_SUBCHUNKS][e % FA_SUBCHUNKS]);
+  }
+  __syncthreads();
+  if (t == 0) {
+    const int n = P * FA_SUBCHUNKS;
+    uint64_t R = 0;
+    for (int e = 0; e < n; ++e) R += s_all[0][e];
+    int use_p = 0;
+    if (R == 0) {
+      use_p = 1;
+      for (int e = 0; e < n; ++e) R += s_all[1][e];
+    }
+    const uint64_t target = canon_scale_floor(a.uniform[(int64_t)r * width + width - 1], R);
+    uint64_t pre = 0;
+    int si = 0, ci = 0;
+    bool found = false;
+    for (si = 0; si < P && !found; ++si)
+      for (ci = 0; ci < FA_SUBCHUNKS; ++ci) {
+        const uint64_t s = s_all[use_p][si * FA_SUBCHUNKS + ci];
+        if (pre + s > target) {
+          found = true;
+          break;
+        }
+        pre += s;
+      }
+    s_slice = found ? si - 1 : P;
+    s_sub_i = ci;
+    s_base = pre;
+    s_target = target;
+    s_use_p = use_p;
+  }
+  __syncthreads();
+  int64_t pick = V - 1;  // past every prefix: the last index (clamp)
+  if (s_slice < P) {
+    // the sub-chunk again in vocabulary order: thread t holds logits 4t .. 4t + 3
+    const bool use_p = s_use_p != 0;
+    const uint64_t target = s_target;
+    const int c0 = s_slice * FA_SLICE + s_sub_i * FA_SUB + 4 * t;
+    uint64_t f[4];
+    uint64_t run = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = c0 + e;
+      const int ii = i < V ? i : V - 1;
+      const float ex = canon_exp(__fsub_rn(__fdiv_rn(x[ii], T), M));
+      const float p = Zf > 0.0f ? canon_div(ex, Zf) : 0.0f;
+      const float wgt = use_p ? p : rr.from_loaded(ii, p, ii);
+      f[e] = i < V ? canon_fix(wgt) : 0;
+      run += f[e];
+    }
+    uint64_t pre = s_base + block_exclusive_scan_u64<FA_NT>(run, buf);
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (c0 + e < V) {
+        pre += f[e];
+        cnt += pre <= target;
+      }
+    }
+    cnt = (uint32_t)block_sum_u64<FA_NT>(cnt, red);
+    pick = (int64_t)s_slice * FA_SLICE + (int64_t)s_sub_i * FA_SUB + cnt;
+    if (pick > V - 1) pick = V - 1;
+  }
+  if (t < width) {
+    a.out[(int64_t)r * width + t] =
+        t < first ? a.drafts[(int64_t)r * length + t] : (t == first ? pick : -1);
+  }
+  if (t == 0) a.accepted[r] = first + 1;
+}
+
+__global__ void __launch_bounds__(FA_NT) fa_greedy_kernel(FaArgs a) {
+  __shared__ uint64_t red[FA_NT / WAVE];
+  __shared__ int64_t s_tok[64];
+  const int P = a.P, width = a.width, length = width - 1, V = a.V;
+  const int w = blockIdx.x % P, row = blockIdx.x / P;
+  const int r = row / width, j = row % width;
+  const int t = threadIdx.x, lo = w * FA_SLICE;
+  const float* x = a.logits + (int64_t)row * V;
+  float v[FA_E];
+#pragma unroll
+  for (int k = 0; k < FA_E; ++k) {
+    const int i = lo + k * FA_NT + t;
+    v[k] = x[i < V ? i : V - 1];
+  }
+  uint64_t best = 0;
+#pragma unroll
+  for (int k = 0; k < FA_E; ++k) {
+    const int i = lo + k * FA_NT + t;
+    const uint64_t key = argmax_key(v[k], (uint32_t)i);
+    if (i < V) best = key > best ? key : best;
+  }
+  best = block_max_u64<FA_NT>(best, red);
+  if (t == 0) dev_store(&g_fa_amax[row][w], best);
+  if (!fa_last_arrival(&g_fa_cnt[2][r], width * P, j == 0 && w == 0)) return;
+  __shared__ uint64_t s_keys[64][FA_P_MAX];
+  for (int i = t; i < width * P; i += FA_NT)
+    s_keys[i / P][i % P] = dev_load(&g_fa_amax[r * width + i / P][i % P]);
+  __syncthreads();
+  if (t < width) {
+    uint64_t b = 0;
+    for (int i = 0; i < P; ++i) b = s_keys[t][i] > b ? s_keys[t][i] : b;
+    const int64_t tok = (int64_t)argmax_key_index(b);
+    s_tok[t] = tok;
+    a.out[(int64_t)r * width + t] = tok;
+  }
+  __syncthreads();
+  if (t == 0) {
+    int64_t acc = 1;
+    while (acc < width && s_tok[acc - 1] == a.drafts[(int64_t)r * length + acc - 1]) ++acc;
+    a.accepted[r] = acc;
+  }
+}
+
+int fa_slices(int64_t V) { return (int)((V + FA_SLICE - 1) / FA_SLICE); }
+
+}  // namespace
+
+// Extension: rejection-sampling acceptance straight from the logits for requests whose
+// candidate lists are the whole vocabulary (see above). logits [b * width, vocab]; the
+// remaining arguments as snowllm_draft_reject with p = softmax(logits / T) over the
+// vocabulary. b * width <= 256, width <= 64. Calls on one device must be stream-ordered
+// (library-owned statistics and counters).
+SV_API int snowverify_accept_reject(const float* logits, const float* temperature,
+                                    const int64_t* drafts, const int64_t* cand, const float* q,
+                                    const int32_t* slots, const int32_t* valid,
+                                    const float* uniform, int64_t* out, int64_t* accepted,
+                                    int64_t b, int64_t width, int64_t vocab, int64_t q_width,
+                                    void* stream) {
+  if (b <= 0 || width < 1 || width > 64 || b * width > FA_ROWS || vocab <= 0 ||
+      vocab > VOCAB_MAX || q_width < 0 || !logits || !slots || !valid || !uniform || !out ||
+      !accepted || (width > 1 && !drafts))
+    return SV_EINVAL;
+  const int P = fa_slices(vocab);
+  FaArgs a{logits, temperature, drafts, cand, q, slots, valid, uniform, out, accepted,
+           (int)vocab, (int)width, P, q_width};
+  const dim3 rows((unsigned)(b * width * P)), reqs((unsigned)(b * P));
+  hipLaunchKernelGGL(fa_max_kernel, rows, dim3(FA_NT), 0, S(stream), a);
+  SV_CHECK_LAUNCH();
+  hipLaunchKernelGGL(fa_sum_kernel, rows, dim3(FA_NT), 0, S(stream), a);
+  SV_CHECK_LAUNCH();
+  hipLaunchKernelGGL(fa_pick_kernel, reqs, dim3(FA_NT), 0, S(stream), a);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Extension: greedy acceptance straight from the logits: tokens [b, width] = argmax of each
+// row (NaN as -inf, first index) and accepted [b] = 1 + leading matches with drafts [b,
+// width - 1] -- snowllm_sampling_argmax + snowllm_spec_accept in one launch. Limits as
+// snowverify_accept_reject.
+SV_API int snowverify_accept_greedy(const float* logits, const int64_t* drafts, int64_t* tokens,
+                                    int64_t* accepted, int64_t b, int64_t width, int64_t vocab,
+                                    void* stream) {
+  if (b <= 0 || width < 1 || width > 64 || b * width > FA_ROWS || vocab <= 0 ||
+      vocab > VOCAB_MAX || !logits || !tokens || !accepted || (width > 1 && !drafts))
+    return SV_EINVAL;
+  const int P = fa_slices(vocab);
+  FaArgs a{logits, nullptr, drafts, nullptr, nullptr, nullptr, nullptr, nullptr, tokens,
+           accepted, (int)vocab, (int)width, P, 0};
+  hipLaunchKernelGGL(fa_greedy_kernel, dim3((unsigned)(b * width * P)), dim3(FA_NT), 0,
+                     S(stream), a);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}

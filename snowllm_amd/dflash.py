@@ -93,3 +93,55 @@ def reject(probabilities, indices, drafts, candidate_ids, q, slots, valid, unifo
         _p(probabilities), _p(indices), _p(drafts), _p(candidate_ids), _p(q), _p(slots),
         _p(valid), _p(uniform), _p(out), _p(accepted), b, width, p_width, q_width, _stream()),
         "draft_reject")
+
+
+def accept_reject(logits, drafts, candidate_ids, q, slots, valid, uniform, out, accepted, *,
+                  temperature=None):
+    """Extension: rejection-sampling acceptance straight from the target logits [b*(k+1), V]
+    (three launches, no dense probabilities), for requests whose candidate lists are the whole vocabulary (top-k >= V,
+    top-p 1): the same results, bit for bit, as probabilities + reject on those rows.
+    temperature [b*(k+1)] or None (1). Returns False when the shape is beyond the fused
+    kernel's limits (nothing launched); the caller then takes probabilities + reject."""
+    b, length = drafts.shape
+    width = length + 1
+    rows, V = logits.shape
+    _chk(logits, "logits", torch.float32, b * width, V)
+    if temperature is not None:
+        _chk(temperature, "temperature", torch.float32, b * width)
+    _chk(drafts, "drafts", torch.int64, b, length)
+    _chk(candidate_ids, "candidate_ids", torch.int64, q.shape[0], length, q.shape[2])
+    _chk(q, "draft probabilities", torch.float32, *candidate_ids.shape)
+    _chk(slots, "request slots", torch.int32, b)
+    _chk(valid, "valid proposals", torch.int32, b)
+    _chk(uniform, "uniform", torch.float32, b, width)
+    _chk(out, "verified tokens", torch.int64, b, width)
+    _chk(accepted, "accepted", torch.int64, b)
+    rc = lib.snowverify_accept_reject(_p(logits), _p(temperature), _p(drafts), _p(candidate_ids),
+                                      _p(q), _p(slots), _p(valid), _p(uniform), _p(out),
+                                      _p(accepted), b, width, V, q.shape[2], _stream())
+    if rc == NOT_SUPPORTED:
+        return False
+    check(rc, "accept_reject")
+    return True
+
+
+def accept_greedy(logits, drafts, tokens, accepted):
+    """Extension: tokens [b, k+1] = argmax of each logit row, accepted [b] = 1 + leading
+    matches with drafts [b, k], in one launch. Returns False beyond the fused kernel's
+    limits (nothing launched)."""
+    b, length = drafts.shape
+    width = length + 1
+    rows, V = logits.shape
+    _chk(logits, "logits", torch.float32, b * width, V)
+    _chk(drafts, "drafts", torch.int64, b, length)
+    _chk(tokens, "tokens", torch.int64, b, width)
+    _chk(accepted, "accepted", torch.int64, b)
+    rc = lib.snowverify_accept_greedy(_p(logits), _p(drafts), _p(tokens), _p(accepted), b, width,
+                                      V, _stream())
+    if rc == NOT_SUPPORTED:
+        return False
+    check(rc, "accept_greedy")
+    return True
+
+
+NOT_SUPPORTED = 801  # hipErrorNotSupported

@@ -382,9 +382,11 @@ class VerifyModel:
 
 class Acceptance:
     """Rejection-sampling acceptance of the block against draft probabilities q (the draft
-    side's proposal): target probabilities over the full vocabulary (ops.sampling.
-    probabilities), then ops.dflash.reject (snowllm/engine/dflash_sampling.py:52-69).
-    For a tree block the chain rows[0..k] is accepted."""
+    side's proposal) over the full vocabulary at temperature 1 (snowllm/engine/
+    dflash_sampling.py:60-69): straight from the logits (ops.dflash.accept_reject), which
+    gives the bits of ops.sampling.probabilities + ops.dflash.reject. For a tree block the
+    chain rows[0..k] is accepted. The batch dispatch (greedy / whole vocabulary / candidate
+    lists) lives in snowllm_amd.dflash_sampling."""
 
     def __init__(self, vocab, chain_rows):
         dev = "cuda"
@@ -458,6 +460,12 @@ class Acceptance:
             src = self.chain_logits
         elif logits.shape[0] != self.T:
             src = logits[:self.T]  # chain = leading rows of the block (contiguous view)
+        # the whole vocabulary at T = 1: straight from the logits (the same bits as
+        # probabilities + reject, which runs when the shape is beyond the fused kernel)
+        if ops.dflash.accept_reject(src, self.drafts, self.qid, self.q, self.slot, self.valid,
+                                    self.uniform, self.out, self.accepted,
+                                    temperature=self.temp):
+            return self.out, self.accepted
         ops.probabilities(src, self.top_k, self.top_p, self.temp, self.V, self.p, self.pid, self.ws)
         ops.dflash.reject(self.p, self.pid, self.drafts, self.qid, self.q, self.slot, self.valid,
                           self.uniform, self.out, self.accepted)
