@@ -364,14 +364,45 @@ int snowllm_inference_moe_norm(const SnowllmWeight* w, const void* x, void* resi
                                const void* gamma, float eps, void* hidden_row,
                                const void* router, void* out, void* scratch, int64_t capacity,
                                int64_t M, void* stream);
+/* Expert and router repack from the GGUF layout (snowllm/_capi.py:313-314, 326-331;
+ * ops/moe.py:81-86, 136-162), over the active geometry (F = moe_inter, H = hidden): gate and
+ * up are the ffn_gate_exps / ffn_up_exps blocks [E, F, H], down the ffn_down_exps blocks
+ * [E, H, F] (fmt 4 = Q4_K, 8 = Q8_0; the MoE entry points compute Q4_K). Expert e's packed
+ * [2F, H] gate/up (gate rows first) and [H, F] down sit at e times their packed size, as
+ * snowllm_inference_moe reads them (kind 3). The router is bf16 [E + 1, H], shared gate last;
+ * a router bias returns hipErrorNotSupported. */
+int64_t snowllm_moe_kquant_gate_up_quant_bytes(int fmt, int64_t E);
+int64_t snowllm_moe_kquant_gate_up_meta_bytes(int fmt, int64_t E);
+int64_t snowllm_moe_kquant_down_quant_bytes(int fmt, int64_t E);
+int64_t snowllm_moe_kquant_down_meta_bytes(int fmt, int64_t E);
+int snowllm_moe_kquant_shuffle_gate_up(int fmt, const uint8_t* gate, const uint8_t* up,
+                                       uint8_t* quant, uint8_t* meta, int64_t E, void* stream);
+int snowllm_moe_kquant_shuffle_down(int fmt, const uint8_t* down, uint8_t* quant, uint8_t* meta,
+                                    int64_t E, void* stream);
+int64_t snowllm_moe_shuffle_router_bytes(void);
+int snowllm_moe_shuffle_router(const void* router, const void* bias, void* out, void* stream);
 /* Dense SwiGLU MLP (snowllm/_capi.py:599, 689; ops/inference.py:46-51): w[3] = packed [2F, H]
  * gate/up (gate rows first), separate up (absent), down. M <= 16. */
 int64_t snowllm_fused_mlp_workspace_bytes(int64_t M);
 int snowllm_inference_mlp(const SnowllmWeight* w, const void* x, void* out, void* scratch,
                           int64_t M, int decode, void* stream);
-/* LM head (snowllm/_capi.py:355, 692; ops/inference.py:98-104): logits [M, vocab] f32 for the
- * normalised rows x; w: the repacked fp16 [vocab, hidden] head (kind 0). */
+/* LM head (snowllm/_capi.py:317-321, 354-356, 692; ops/embedding.py:12-16, 44-73;
+ * ops/inference.py:98-104): logits [M, vocab] f32 for the normalised bf16 rows x. A 16-bit head
+ * is bf16 [vocab, hidden] repacked by snowllm_lm_head_shuffle_weight into
+ * snowllm_shuffle_bytes(vocab * hidden * 2) bytes (descriptor kind 0); a k-quant head is the
+ * GGUF Q4_K / Q8_0 blocks repacked by snowllm_lm_head_kquant_shuffle_weight (kind 2 or 3). */
+int64_t snowllm_shuffle_bytes(int64_t nbytes);
+int snowllm_lm_head_shuffle_weight(const void* w, void* out, void* stream);
+int64_t snowllm_lm_head_kquant_gguf_bytes(int fmt);
+int64_t snowllm_lm_head_kquant_quant_bytes(int fmt);
+int64_t snowllm_lm_head_kquant_meta_bytes(int fmt);
+int snowllm_lm_head_kquant_shuffle_weight(int fmt, const uint8_t* blocks, uint8_t* quant,
+                                          uint8_t* meta, void* stream);
 int64_t snowllm_lm_head_scratch_bytes(int64_t M);
+int snowllm_lm_head(const void* x, const void* w, float* logits, int64_t M, void* scratch,
+                    void* stream);
+int snowllm_lm_head_kquant(int fmt, const void* x, const void* quant, const void* meta,
+                           float* logits, int64_t M, void* scratch, void* stream);
 int snowllm_inference_head(const SnowllmWeight* w, const void* x, float* out, void* scratch,
                            int64_t M, void* stream);
 
@@ -397,6 +428,11 @@ int snowllm_gather_embedding(const int64_t* ids, const void* table, void* out, i
                              void* stream);
 int snowverify_gather_embedding(const int64_t* ids, const void* table, void* out, int64_t M,
                                 int64_t V, int64_t H, int table_f16, void* stream);
+/* Embedding gather from a Q4_K table (snowllm/_capi.py:726; ops/embedding.py:27-41): weight
+ * [vocab, hidden / 256 * 144] bytes of GGUF blocks -> bf16 [rows, hidden], each value
+ * fp32(d sc) q - fp32(dmin m) rounded once to bf16. hidden % 256 == 0. */
+int snowllm_gather_embedding_q4_k(const int64_t* ids, const void* weight, void* out, int64_t rows,
+                                  int64_t vocab, int64_t hidden, void* stream);
 
 /* RMSNorm y = x rsqrt(mean(x^2) + eps) gamma (snowllm/_capi.py:376, 381; ops/norm.py:66-97);
  * the residual form first sets residual = x + residual. */

@@ -125,6 +125,14 @@ _SIGS = [
     ("snowllm_prefill_q_blocks", c_int64, [P, c_int64]),
     ("snowllm_prefill_q_block_map", None, [P, c_int64, P]),
     ("snowllm_kv_block_sizes", c_int64, [c_void_p, c_int64]),
+    ("snowllm_moe_kquant_gate_up_quant_bytes", c_int64, [c_int, c_int64]),
+    ("snowllm_moe_kquant_gate_up_meta_bytes", c_int64, [c_int, c_int64]),
+    ("snowllm_moe_kquant_down_quant_bytes", c_int64, [c_int, c_int64]),
+    ("snowllm_moe_kquant_down_meta_bytes", c_int64, [c_int, c_int64]),
+    ("snowllm_moe_kquant_shuffle_gate_up", c_int, [c_int, P, P, P, P, c_int64, S]),
+    ("snowllm_moe_kquant_shuffle_down", c_int, [c_int, P, P, P, c_int64, S]),
+    ("snowllm_moe_shuffle_router_bytes", c_int64, []),
+    ("snowllm_moe_shuffle_router", c_int, [P, P, P, S]),
     ("snowllm_moe_workspace_bytes", c_int64, [c_int64]),
     ("snowllm_inference_moe_workspace_bytes", c_int64, [c_int64, c_int64]),
     ("snowllm_inference_moe", c_int, [P] * 7 + [c_int64] * 3 + [S]),
@@ -133,6 +141,15 @@ _SIGS = [
     ("snowllm_inference_mlp", c_int, [P, P, P, P, c_int64, c_int, S]),
     ("snowllm_lm_head_scratch_bytes", c_int64, [c_int64]),
     ("snowllm_inference_head", c_int, [P, P, P, P, c_int64, S]),
+    ("snowllm_shuffle_bytes", c_int64, [c_int64]),
+    ("snowllm_lm_head_shuffle_weight", c_int, [P, P, S]),
+    ("snowllm_lm_head", c_int, [P, P, P, c_int64, P, S]),
+    ("snowllm_lm_head_kquant_gguf_bytes", c_int64, [c_int]),
+    ("snowllm_lm_head_kquant_quant_bytes", c_int64, [c_int]),
+    ("snowllm_lm_head_kquant_meta_bytes", c_int64, [c_int]),
+    ("snowllm_lm_head_kquant_shuffle_weight", c_int, [c_int, P, P, P, S]),
+    ("snowllm_lm_head_kquant", c_int, [c_int, P, P, P, P, c_int64, P, S]),
+    ("snowllm_gather_embedding_q4_k", c_int, [P] * 3 + [c_int64] * 3 + [S]),
     ("snowllm_rope_cos_sin", c_int, [P, P, P, P, c_int64, S]),
     ("snowllm_qk_norm_rope_cache", c_int, [P, c_int64, P, c_int64, P, c_int64] + [P] * 10 + [c_int64, c_float, c_int64, S]),
     # geometry and layer plumbing

@@ -94,6 +94,14 @@ int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_meta,
                         int64_t F, void* stream);
 int snowverify_moe_combine(const float* pairs, const float* shared_out, void* out, int64_t M,
                            int64_t topk, int64_t H, void* stream);
+int64_t snowllm_kquant_quant_bytes(int fmt, int64_t N, int64_t K);
+int64_t snowllm_kquant_meta_bytes(int fmt, int64_t N, int64_t K);
+int64_t snowllm_kquant_gguf_bytes(int fmt, int64_t N, int64_t K);
+int snowllm_gemm_kquant_shuffle_b(int fmt, const uint8_t* gguf, uint8_t* quant, uint8_t* meta,
+                                  int64_t N, int64_t K, void* stream);
+int64_t snowverify_dense_bytes(int64_t N, int64_t K);
+int snowverify_dense_shuffle(const void* src, void* dst, int64_t N, int64_t K, int wt,
+                             void* stream);
 int64_t snowverify_paged_attention_scratch_bytes(int64_t batch, int64_t tokens,
                                                  int64_t num_heads, int64_t num_kv_heads,
                                                  int64_t head_size);
@@ -324,6 +332,96 @@ SV_API int snowllm_paged_attention(const PagedAttentionStep* st, void* scratch, 
                                     bytes, stream);
 }
 
+// ---- expert and router repack (snowllm/_capi.py:313-314, 326-331; ops/moe.py:81-86, 136-162)
+// The GGUF expert stacks (ffn_gate_exps / ffn_up_exps [E, F, H], ffn_down_exps [E, H, F],
+// each expert's rows back to back) become the layout the MoE kernels read: per expert e the
+// packed [2F, H] gate/up matrix (gate rows first) at e * its bytes, and the packed [H, F]
+// down matrix; each packed matrix is snowllm_gemm_kquant_shuffle_b's (quant, meta), whose
+// 16-row tiles are stored in order, so the gate half and the up half are packed separately
+// into the two halves. The +4 bytes of the single-matrix quant size come once, at the end.
+namespace {
+int64_t expert_quant(int fmt, int64_t N, int64_t K) {
+  const int64_t q = snowllm_kquant_quant_bytes(fmt, N, K);
+  return q < 0 ? -1 : q - 4;
+}
+bool expert_geometry(int fmt, int64_t E) {
+  const BuildGeometry& g = active_geometry();
+  return (fmt == 4 || fmt == 8) && E > 0 && g.moe_inter > 0 && g.hidden > 0 &&
+         expert_quant(fmt, g.moe_inter, g.hidden) > 0 && expert_quant(fmt, g.hidden, g.moe_inter) > 0;
+}
+}  // namespace
+
+SV_API int64_t snowllm_moe_kquant_gate_up_quant_bytes(int fmt, int64_t E) {
+  if (!expert_geometry(fmt, E)) return 0;
+  const BuildGeometry& g = active_geometry();
+  return E * 2 * expert_quant(fmt, g.moe_inter, g.hidden) + 4;
+}
+SV_API int64_t snowllm_moe_kquant_gate_up_meta_bytes(int fmt, int64_t E) {
+  if (!expert_geometry(fmt, E)) return 0;
+  const BuildGeometry& g = active_geometry();
+  return E * 2 * snowllm_kquant_meta_bytes(fmt, g.moe_inter, g.hidden);
+}
+SV_API int64_t snowllm_moe_kquant_down_quant_bytes(int fmt, int64_t E) {
+  if (!expert_geometry(fmt, E)) return 0;
+  const BuildGeometry& g = active_geometry();
+  return E * expert_quant(fmt, g.hidden, g.moe_inter) + 4;
+}
+SV_API int64_t snowllm_moe_kquant_down_meta_bytes(int fmt, int64_t E) {
+  if (!expert_geometry(fmt, E)) return 0;
+  const BuildGeometry& g = active_geometry();
+  return E * snowllm_kquant_meta_bytes(fmt, g.hidden, g.moe_inter);
+}
+
+SV_API int snowllm_moe_kquant_shuffle_gate_up(int fmt, const uint8_t* gate, const uint8_t* up,
+                                              uint8_t* quant, uint8_t* meta, int64_t E,
+                                              void* stream) {
+  if (!expert_geometry(fmt, E) || !gate || !up || !quant || !meta) return SV_EINVAL;
+  const BuildGeometry& g = active_geometry();
+  const int64_t F = g.moe_inter, H = g.hidden;
+  const int64_t src = snowllm_kquant_gguf_bytes(fmt, F, H);
+  const int64_t q = expert_quant(fmt, F, H), m = snowllm_kquant_meta_bytes(fmt, F, H);
+  for (int64_t e = 0; e < E; ++e)
+    for (int half = 0; half < 2; ++half) {
+      const uint8_t* from = (half ? up : gate) + e * src;
+      const int rc = snowllm_gemm_kquant_shuffle_b(fmt, from, quant + (2 * e + half) * q,
+                                                   meta + (2 * e + half) * m, F, H, stream);
+      if (rc) return rc;
+    }
+  return SV_OK;
+}
+
+SV_API int snowllm_moe_kquant_shuffle_down(int fmt, const uint8_t* down, uint8_t* quant,
+                                           uint8_t* meta, int64_t E, void* stream) {
+  if (!expert_geometry(fmt, E) || !down || !quant || !meta) return SV_EINVAL;
+  const BuildGeometry& g = active_geometry();
+  const int64_t F = g.moe_inter, H = g.hidden;
+  const int64_t src = snowllm_kquant_gguf_bytes(fmt, H, F);
+  const int64_t q = expert_quant(fmt, H, F), m = snowllm_kquant_meta_bytes(fmt, H, F);
+  for (int64_t e = 0; e < E; ++e) {
+    const int rc = snowllm_gemm_kquant_shuffle_b(fmt, down + e * src, quant + e * q, meta + e * m,
+                                                 H, F, stream);
+    if (rc) return rc;
+  }
+  return SV_OK;
+}
+
+// The bf16 router [E + 1, hidden] (the routed experts' rows, then the shared expert's gate row,
+// snowllm/models/qwen3_5/qwen3_5_weights.py:333-335) repacked for the router GEMV. A router
+// bias is not carried (hipErrorNotSupported).
+SV_API int64_t snowllm_moe_shuffle_router_bytes(void) {
+  const BuildGeometry& g = active_geometry();
+  if (!moe_geometry_ok()) return 0;
+  return snowverify_dense_bytes(g.moe_num_experts + 1, g.hidden);
+}
+
+SV_API int snowllm_moe_shuffle_router(const void* router, const void* bias, void* out,
+                                      void* stream) {
+  if (bias) return SV_ENOTSUP;
+  if (!router || !out || !moe_geometry_ok()) return SV_EINVAL;
+  const BuildGeometry& g = active_geometry();
+  return snowverify_dense_shuffle(router, out, g.moe_num_experts + 1, g.hidden, WT_BF16, stream);
+}
+
 // snowllm/_capi.py:315 and 690 -- scratch of the MoE block for `rows` rows (flags must be 0).
 SV_API int64_t snowllm_moe_workspace_bytes(int64_t rows) {
   if (rows <= 0 || !moe_geometry_ok()) return 0;
@@ -402,22 +500,73 @@ SV_API int64_t snowllm_lm_head_scratch_bytes(int64_t M) {
   return M <= 0 ? 0 : snowllm_gemm_kquant_a_ws_bytes(M, active_geometry().hidden);
 }
 
-// snowllm/_capi.py:692 (ops/inference.py:98-104; LMHead, models/qwen3_5/layers.py:209-228):
-// logits [M, vocab] f32 = x W^T for the normalised rows x, W the fp16 [vocab, hidden] head
-// repacked by snowverify_dense_shuffle (kind 0). Rows go in 16-row tiles.
-SV_API int snowllm_inference_head(const Weight* w, const void* x, float* out, void* scratch,
-                                  int64_t M, void* stream) {
-  if (!w || w->kind != 0 || !w->data[0]) return SV_ENOTSUP;
+// ---- LM head (snowllm/_capi.py:317-321, 354-356, 692; ops/embedding.py:12-16, 44-73;
+// ops/inference.py:98-104; LMHead, models/qwen3_5/layers.py:209-228) ------------------------
+// A 16-bit head is bf16 [vocab, hidden] repacked by snowllm_lm_head_shuffle_weight; a k-quant
+// head is the Q4_K / Q8_0 blocks of [vocab, hidden] repacked by
+// snowllm_lm_head_kquant_shuffle_weight (snowllm_gemm_kquant_shuffle_b's layout). Logits f32.
+
+// Bytes a repacked 16-bit weight of `nbytes` source bytes may need: rows are padded to a
+// multiple of 16, so at most 15 rows of the widest supported K (65536) are added.
+SV_API int64_t snowllm_shuffle_bytes(int64_t nbytes) {
+  return nbytes <= 0 ? 0 : nbytes + 15 * 65536 * 2;
+}
+
+SV_API int snowllm_lm_head_shuffle_weight(const void* w, void* out, void* stream) {
   const BuildGeometry& g = active_geometry();
-  if (!x || !out || !scratch || M <= 0) return SV_EINVAL;
-  int rc = snowverify_gemm_kquant_prepare_a(x, M, g.hidden, scratch, stream);
-  if (rc) return rc;
-  const int64_t tile_bytes = snowllm_gemm_kquant_a_ws_bytes(16, g.hidden);
+  if (!w || !out || g.vocab_size <= 0 || g.hidden <= 0) return SV_EINVAL;
+  return snowverify_dense_shuffle(w, out, g.vocab_size, g.hidden, WT_BF16, stream);
+}
+
+SV_API int64_t snowllm_lm_head_kquant_gguf_bytes(int fmt) {
+  const BuildGeometry& g = active_geometry();
+  return snowllm_kquant_gguf_bytes(fmt, g.vocab_size, g.hidden);
+}
+SV_API int64_t snowllm_lm_head_kquant_quant_bytes(int fmt) {
+  const BuildGeometry& g = active_geometry();
+  return snowllm_kquant_quant_bytes(fmt, g.vocab_size, g.hidden);
+}
+SV_API int64_t snowllm_lm_head_kquant_meta_bytes(int fmt) {
+  const BuildGeometry& g = active_geometry();
+  return snowllm_kquant_meta_bytes(fmt, g.vocab_size, g.hidden);
+}
+SV_API int snowllm_lm_head_kquant_shuffle_weight(int fmt, const uint8_t* blocks, uint8_t* quant,
+                                                 uint8_t* meta, void* stream) {
+  const BuildGeometry& g = active_geometry();
+  return snowllm_gemm_kquant_shuffle_b(fmt, blocks, quant, meta, g.vocab_size, g.hidden, stream);
+}
+
+// bf16 head: x [M, hidden] bf16 rows against the repacked head, 16 rows per launch.
+SV_API int snowllm_lm_head(const void* x, const void* w, float* logits, int64_t M, void* scratch,
+                           void* stream) {
+  (void)scratch;
+  const BuildGeometry& g = active_geometry();
+  if (!x || !w || !logits || M <= 0) return SV_EINVAL;
   for (int64_t r0 = 0; r0 < M; r0 += 16) {
     const int64_t rows = M - r0 < 16 ? M - r0 : 16;
-    rc = snowverify_dense_gemv(WT_F16, w->data[0], (const char*)scratch + (r0 / 16) * tile_bytes,
-                               out + r0 * g.vocab_size, rows, g.vocab_size, g.hidden, 0, stream);
+    const int rc = snowverify_dense_gemv(WT_BF16, w, (const uint16_t*)x + r0 * g.hidden,
+                                         logits + r0 * g.vocab_size, rows, g.vocab_size,
+                                         g.hidden, 0, stream);
     if (rc) return rc;
   }
   return SV_OK;
+}
+
+// k-quant head: scratch holds snowllm_lm_head_scratch_bytes(M).
+SV_API int snowllm_lm_head_kquant(int fmt, const void* x, const void* quant, const void* meta,
+                                  float* logits, int64_t M, void* scratch, void* stream) {
+  const BuildGeometry& g = active_geometry();
+  if (!x || !quant || !meta || !logits || !scratch || M <= 0) return SV_EINVAL;
+  return snowllm_gemm_kquant_a(fmt, x, (const uint8_t*)quant, (const uint8_t*)meta, logits, M,
+                               g.vocab_size, g.hidden, 0, scratch, stream);
+}
+
+// The descriptor form: kind 0 = bf16 head, kind 2 / 3 = k-quant head.
+SV_API int snowllm_inference_head(const Weight* w, const void* x, float* out, void* scratch,
+                                  int64_t M, void* stream) {
+  if (!w) return SV_EINVAL;
+  if (w->kind == 0 && w->data[0]) return snowllm_lm_head(x, w->data[0], out, M, scratch, stream);
+  if (kquant(w)) return snowllm_lm_head_kquant(w->fmt, x, w->data[0], w->data[1], out, M, scratch,
+                                              stream);
+  return SV_ENOTSUP;
 }

@@ -66,6 +66,45 @@ __global__ void gather_embedding_kernel(const int64_t* __restrict__ ids,
   }
 }
 
+// Embedding gather from a Q4_K table [V, H] (H / 256 blocks of 144 bytes per row): one
+// 256-thread block per row, thread t decodes element t of every block. A block is fp16 d at 0,
+// fp16 dmin at 2, twelve bytes of 6-bit scales/mins at 4 and 128 nibble bytes at 16; element
+// 64 g + 32 h + l is the low (h = 0) or high (h = 1) nibble of byte 16 + 32 g + l and uses
+// scale/min j = 2 g + h, where j < 4 takes sc = s[j] & 63, m = s[j + 4] & 63 and j >= 4 takes
+// sc = (s[j + 4] & 15) | (s[j - 4] >> 6) << 4, m = (s[j + 4] >> 4) | (s[j] >> 6) << 4. The
+// value is fp32(d sc) q - fp32(dmin m), two roundings (no fused multiply-add), then bf16.
+__global__ void __launch_bounds__(256) gather_embedding_q4k_kernel(
+    const int64_t* __restrict__ ids, const uint8_t* __restrict__ table, uint16_t* __restrict__ out,
+    int64_t V, int64_t H) {
+#pragma clang fp contract(off)
+  const int64_t m = blockIdx.x;
+  int64_t id = ids[m];
+  if (id < 0 || id >= V) id = 0;
+  const int64_t nb = H / 256;
+  const uint8_t* row = table + id * nb * 144;
+  const int t = threadIdx.x, g = t >> 6, h = (t >> 5) & 1, l = t & 31, j = 2 * g + h;
+  for (int64_t b = 0; b < nb; ++b) {
+    const uint8_t* blk = row + b * 144;
+    const float d = f16_to_f32((uint16_t)(blk[0] | blk[1] << 8));
+    const float dmin = f16_to_f32((uint16_t)(blk[2] | blk[3] << 8));
+    const uint8_t* s = blk + 4;
+    int sc, mn;
+    if (j < 4) {
+      sc = s[j] & 63;
+      mn = s[j + 4] & 63;
+    } else {
+      sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+      mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+    const uint8_t byte = blk[16 + 32 * g + l];
+    const float q = (float)(h ? byte >> 4 : byte & 15);
+    const float dsc = d * (float)sc;
+    const float dmn = dmin * (float)mn;
+    const float prod = dsc * q;
+    out[m * H + b * 256 + t] = f32_to_bf16(prod - dmn);
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // RMSNorm: y = x * rsqrt(mean(x^2) + eps) * gamma, fp32 math, bf16 out. With a residual,
 // the residual stream is updated first (residual = x + residual, rounded to bf16) and
@@ -283,6 +322,21 @@ SV_API int snowverify_gather_embedding(const int64_t* ids, const void* table, vo
 SV_API int snowllm_gather_embedding(const int64_t* ids, const void* table, void* out, int64_t M,
                                     void* stream) {
   return snowverify_gather_embedding(ids, table, out, M, g_geo.vocab_size, g_geo.hidden, 0, stream);
+}
+
+// Reference signature (snowllm/_capi.py:726; snowllm/ops/embedding.py:27-41): gather from a
+// Q4_K table [vocab, hidden / 256 * 144 bytes] -> bf16 [rows, hidden]; hidden % 256 == 0.
+// Ids outside [0, vocab) read row 0, as the 16-bit gather does.
+SV_API int snowllm_gather_embedding_q4_k(const int64_t* ids, const void* weight, void* out,
+                                         int64_t rows, int64_t vocab, int64_t hidden,
+                                         void* stream) {
+  if (rows < 0 || vocab <= 0 || hidden <= 0 || hidden % 256 || !weight || !out) return SV_EINVAL;
+  if (rows == 0) return SV_OK;
+  if (!ids) return SV_EINVAL;
+  hipLaunchKernelGGL(gather_embedding_q4k_kernel, dim3((unsigned)rows), dim3(256), 0, S(stream),
+                     ids, (const uint8_t*)weight, (uint16_t*)out, vocab, hidden);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
 }
 
 // Extension: RMSNorm with explicit width; residual may be null.

@@ -134,6 +134,64 @@ def inference_moe_norm(x, residual, gamma, eps, hidden_row, router, gate, down, 
                                          capacity, M, _stream()), "inference_moe_norm")
 
 
+def _expert_blocks(t, what, want):
+    if t.device.type != "cuda" or t.dtype != torch.uint8 or not t.is_contiguous():
+        raise SnowLLMError(f"{what}: contiguous uint8 GGUF blocks on the GPU expected")
+    if t.numel() != want:
+        raise SnowLLMError(f"{what}: {t.numel()} GGUF bytes, the active geometry needs {want}")
+
+
+def moe_kquant_shuffle_gate_up(gate, up, fmt: int, num_experts: int) -> KQuantExpertWeight:
+    """ffn_gate_exps / ffn_up_exps GGUF blocks [E, F, H] -> the experts' packed gate/up stack
+    (snowllm/ops/moe.py:136-145); F = moe_inter and H = hidden of the active geometry."""
+    from .gemm import kquant_bytes
+    g = _geometry()
+    want = num_experts * kquant_bytes(fmt, g.moe_inter, g.hidden)[2]
+    _expert_blocks(gate, "gate blocks", want)
+    _expert_blocks(up, "up blocks", want)
+    quant = torch.empty(lib.snowllm_moe_kquant_gate_up_quant_bytes(fmt, num_experts),
+                        dtype=torch.uint8, device="cuda")
+    meta = torch.empty(lib.snowllm_moe_kquant_gate_up_meta_bytes(fmt, num_experts),
+                       dtype=torch.uint8, device="cuda")
+    check(lib.snowllm_moe_kquant_shuffle_gate_up(fmt, _p(gate), _p(up), _p(quant), _p(meta),
+                                                 num_experts, _stream()),
+          "moe_kquant_shuffle_gate_up")
+    return KQuantExpertWeight(quant, meta, None, fmt)
+
+
+def moe_kquant_shuffle_down(down, fmt: int, num_experts: int) -> KQuantExpertWeight:
+    """ffn_down_exps GGUF blocks [E, H, F] -> the experts' packed down stack
+    (snowllm/ops/moe.py:148-160)."""
+    from .gemm import kquant_bytes
+    g = _geometry()
+    _expert_blocks(down, "down blocks", num_experts * kquant_bytes(fmt, g.hidden, g.moe_inter)[2])
+    quant = torch.empty(lib.snowllm_moe_kquant_down_quant_bytes(fmt, num_experts),
+                        dtype=torch.uint8, device="cuda")
+    meta = torch.empty(lib.snowllm_moe_kquant_down_meta_bytes(fmt, num_experts),
+                       dtype=torch.uint8, device="cuda")
+    check(lib.snowllm_moe_kquant_shuffle_down(fmt, _p(down), _p(quant), _p(meta), num_experts,
+                                              _stream()), "moe_kquant_shuffle_down")
+    return KQuantExpertWeight(quant, meta, None, fmt)
+
+
+def moe_shuffle_router(router, bias=None) -> torch.Tensor:
+    """bf16 router [E + 1, H] (routed experts, then the shared expert's gate) -> the router
+    GEMV's layout (snowllm/ops/moe.py:81-86). A bias is not supported."""
+    g = _geometry()
+    _chk(router, "router", torch.bfloat16, g.moe_num_experts + 1, g.hidden)
+    if bias is not None:
+        raise SnowLLMError("router bias: not supported by this library")
+    out = torch.empty(lib.snowllm_moe_shuffle_router_bytes(), dtype=torch.uint8, device="cuda")
+    check(lib.snowllm_moe_shuffle_router(_p(router), None, _p(out), _stream()),
+          "moe_shuffle_router")
+    return out
+
+
+def _geometry():
+    from .geometry import build_geometry
+    return build_geometry()
+
+
 def lm_head_scratch_bytes(M: int) -> int:
     return int(lib.snowllm_lm_head_scratch_bytes(int(M)))
 

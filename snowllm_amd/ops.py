@@ -20,6 +20,11 @@ from .attention import (kv_pool_bytes, paged_attention_explicit,  # noqa: F401
 from .inference import (KQuantProjWeight, KQuantExpertWeight, inference_qkv,  # noqa: F401
                         qkv_proj_scratch_bytes, inference_mlp, mlp_workspace_bytes,
                         inference_moe, inference_moe_norm, inference_moe_workspace_bytes,
-                        moe_workspace_bytes, inference_head, lm_head_scratch_bytes)
+                        moe_workspace_bytes, inference_head, lm_head_scratch_bytes,
+                        moe_kquant_shuffle_gate_up, moe_kquant_shuffle_down,
+                        moe_shuffle_router)
+from .embedding import (lm_head_shuffle_weight, gather_embedding,  # noqa: F401
+                        gather_embedding_q4_k, lm_head_kquant_shuffle_weight, lm_head_kquant,
+                        lm_head)
 from .geometry import (build_geometry, select_geometry, active_geometry,  # noqa: F401
                        define_geometry)

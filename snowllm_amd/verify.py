@@ -12,9 +12,10 @@ qwen3_5.py:32-78, layers.py:75-228) and its verify drivers (snowllm/engine/spec_
 263-309, 527-581). Every launch goes to torch's current stream and nothing allocates or
 synchronises inside step(), so the step can be captured in one HIP graph.
 
-Weights are random-initialised on the GPU from seeded generators (no checkpoint), in the
-formats of the BASELINE configs: Q4_K/Q8_0 GGUF blocks repacked with
-snowllm_gemm_kquant_shuffle_b, fp16 embedding and LM head, bf16 router and norms.
+Weights are either random-initialised on the GPU from seeded generators, in the formats of
+the BASELINE configs (Q4_K/Q8_0 GGUF blocks repacked with snowllm_gemm_kquant_shuffle_b, fp16
+embedding and LM head, bf16 router and norms), or read from a GGUF checkpoint
+(snowllm_amd.checkpoint: bf16 or Q4_K embedding, bf16 or k-quant head).
 """
 from dataclasses import dataclass, field, replace
 import math
@@ -26,6 +27,7 @@ from . import ops
 from ._capi import SnowLLMError
 
 Q4_K, Q8_0 = 4, 8
+HEAD_KQUANT = -1   # VerifyModel.head_wt for a Q4_K / Q8_0 head (lm_head = (quant, meta))
 
 
 @dataclass
@@ -77,6 +79,21 @@ CONFIG4 = VerifyConfig("config4_moe35b_a3b", layers=40, hidden=2048, heads=16, k
 CONFIG5 = replace(CONFIG4, name="config5_moe35b_a3b_220k_tree", context=220000, block=11,
                   attn_fmt=Q8_0, tree_parents=(-1, 0, 1, 2, 3, 4, 0, 6, 7, 8, 9))
 CONFIGS = {"config3": CONFIG3, "config4": CONFIG4, "config5": CONFIG5}
+
+
+def geometry_fields(cfg: VerifyConfig) -> dict:
+    """The BuildGeometry fields of a config, for ops.define_geometry (the reference-signature
+    entry points and the checkpoint repacks read their shapes from the active geometry)."""
+    d, moe = cfg.head_dim, cfg.moe
+    return dict(
+        hidden=cfg.hidden, num_heads=cfg.heads, num_kv_heads=cfg.kv_heads, head_size=d,
+        block_size=cfg.page, vocab_size=cfg.vocab, qkv_proj_n=cfg.qkv_n, qkv_q_head_stride=d,
+        qkv_off_k=cfg.heads * d, qkv_off_v=(cfg.heads + cfg.kv_heads) * d,
+        moe_num_experts=cfg.experts if moe else 0, moe_shared_expert=int(moe),
+        moe_topk=cfg.topk if moe else 0, moe_topk_all=cfg.topk + 1 if moe else 0,
+        moe_inter=cfg.expert_ffn if moe else 0, sampling_max_k=1 << 19,
+        lm_head_decode_max_m=256, mlp_inter=0 if moe else cfg.ffn,
+        mlp_gate_up_n=0 if moe else 2 * cfg.ffn)
 
 
 def tree_masks(parents):
@@ -155,19 +172,57 @@ class LayerWeights:
     sh_gu: tuple = None
     sh_dn: tuple = None
     raw: dict = field(default_factory=dict)  # unshuffled copies kept for parity checks
+    # formats of this layer's matrices where a checkpoint stores them differently from the
+    # config's attn_fmt / ffn_fmt (0: the config's)
+    qkv_fmt: int = 0
+    o_fmt: int = 0
+    dn_fmt: int = 0
 
 
 class VerifyModel:
     """Weights, KV pools and step buffers of one verify-step configuration."""
 
-    def __init__(self, cfg: VerifyConfig, seed: int = 0, keep_raw=False, kv_std: float = 1.0):
+    def __init__(self, cfg: VerifyConfig, seed: int = 0, keep_raw=False, kv_std: float = 1.0,
+                 weights=None):
         """keep_raw: keep the unshuffled GGUF bytes (and the router / LM head) for parity
         checks -- True for every layer, an int n for the first n layers, or a collection of
-        layer indices."""
+        layer indices. weights: None for seeded random weights, else a callable that installs
+        layers / embed / lm_head / head_wt / final_norm on the model (a checkpoint loader)."""
         self.cfg = c = cfg
         self.keep_raw = keep_raw
         dev = "cuda"
         torch.cuda.synchronize()
+        self.head_wt = Lops.WT_F16   # or WT_BF16, or HEAD_KQUANT with self.head_fmt
+        self.head_fmt = 0
+        self.embed_q4k = False       # True: self.embed holds Q4_K blocks [V, H / 256 * 144]
+        self.lm_head_raw = None
+        if weights is None:
+            self._random_weights(seed, keep_raw)
+        else:
+            weights(self)
+        self.inv_freq = (1.0 / (c.rope_theta ** (torch.arange(c.rot_half, device=dev,
+                                                             dtype=torch.float32) / c.rot_half)))
+        # KV cache: context + block pages, random page table (prior tokens ~ N(0, kv_std^2))
+        T = c.block
+        self.pages = (c.context + T + c.page - 1) // c.page
+        self.blocks = self.pages + 8
+        kvg = torch.Generator(device=dev).manual_seed(seed + 7)
+        shape_k = (self.blocks, c.kv_heads, c.head_dim // 16, c.page, 16)
+        shape_v = (self.blocks, c.kv_heads, c.page // 4, c.head_dim, 4)
+        self.k_pools, self.v_pools = [], []
+        for _ in range(c.layers):
+            k = torch.empty(shape_k, dtype=torch.bfloat16, device=dev)
+            v = torch.empty(shape_v, dtype=torch.bfloat16, device=dev)
+            k.normal_(0, kv_std, generator=kvg)
+            v.normal_(0, kv_std, generator=kvg)
+            self.k_pools.append(k)
+            self.v_pools.append(v)
+        perm = torch.randperm(self.blocks, device=dev, generator=kvg)[:self.pages]
+        self.table = perm.int().view(1, -1).contiguous()
+        self._alloc_step_buffers()
+
+    def _random_weights(self, seed, keep_raw):
+        c, dev = self.cfg, "cuda"
         gen = torch.Generator(device=dev).manual_seed(seed)
         H, V = c.hidden, c.vocab
 
@@ -211,26 +266,6 @@ class VerifyModel:
         self.lm_head = Lops.dense_shuffle(head)
         self.lm_head_raw = head if (keep_raw is not False and keep_raw != 0) else None
         self.final_norm = gamma(H)
-        self.inv_freq = (1.0 / (c.rope_theta ** (torch.arange(c.rot_half, device=dev,
-                                                             dtype=torch.float32) / c.rot_half)))
-        # KV cache: context + block pages, random page table (prior tokens ~ N(0, kv_std^2))
-        T = c.block
-        self.pages = (c.context + T + c.page - 1) // c.page
-        self.blocks = self.pages + 8
-        kvg = torch.Generator(device=dev).manual_seed(seed + 7)
-        shape_k = (self.blocks, c.kv_heads, c.head_dim // 16, c.page, 16)
-        shape_v = (self.blocks, c.kv_heads, c.page // 4, c.head_dim, 4)
-        self.k_pools, self.v_pools = [], []
-        for _ in range(c.layers):
-            k = torch.empty(shape_k, dtype=torch.bfloat16, device=dev)
-            v = torch.empty(shape_v, dtype=torch.bfloat16, device=dev)
-            k.normal_(0, kv_std, generator=kvg)
-            v.normal_(0, kv_std, generator=kvg)
-            self.k_pools.append(k)
-            self.v_pools.append(v)
-        perm = torch.randperm(self.blocks, device=dev, generator=kvg)[:self.pages]
-        self.table = perm.int().view(1, -1).contiguous()
-        self._alloc_step_buffers()
 
     # -----------------------------------------------------------------------------------
     def _alloc_step_buffers(self):
@@ -302,27 +337,32 @@ class VerifyModel:
         it out."""
         c, T = self.cfg, self.cfg.block
         H = c.hidden
-        Lops.gather_embedding(self.ids, self.embed, self.x)
+        if self.embed_q4k:
+            from .embedding import gather_embedding_q4_k
+            gather_embedding_q4_k(self.ids, self.embed, self.x)
+        else:
+            Lops.gather_embedding(self.ids, self.embed, self.x)
         Lops.rope_cos_sin(self.positions, self.inv_freq, self.cos, self.sin)
         res_in, res_out = None, self.res[0]
         n_layers = c.layers if upto_layer is None else upto_layer
         moe_out = False  # the previous layer's MoE output is still in (pairs, shared_out)
 
-        def norm(gamma, ws):
+        def norm(gamma, ws, y_out=None):
             # residual update + norm fused with the GEMV operand prep; after a MoE layer the
             # experts' combine is fused in too (self.x still receives the layer output)
             if moe_out:
                 Lops.norm_prep_moe(self.pairs, self.shared_out, c.topk, gamma, ws, c.eps,
-                                   x_out=self.x, res_in=res_in, res_out=res_out)
+                                   x_out=self.x, res_in=res_in, res_out=res_out, y_out=y_out)
             else:
-                Lops.norm_prep(self.x, gamma, ws, c.eps, res_in=res_in, res_out=res_out)
+                Lops.norm_prep(self.x, gamma, ws, c.eps, res_in=res_in, res_out=res_out,
+                               y_out=y_out)
 
         for i in range(n_layers):
             lw = self.layers[i]
             # attention block
             norm(lw.in_norm, self.ws_h)
-            ops.gemm_kquant_a_prepared(c.attn_fmt, lw.qkv[0], lw.qkv[1], self.proj, T, c.qkv_n, H,
-                                       self.ws_h)
+            ops.gemm_kquant_a_prepared(lw.qkv_fmt or c.attn_fmt, lw.qkv[0], lw.qkv[1], self.proj,
+                                       T, c.qkv_n, H, self.ws_h)
             if c.rot_half <= ops.FUSED_QK_MAX_HALF:
                 # QK-norm + RoPE + the block's K/V cache write inside the attention's launches
                 # with 256-wide heads the merge also writes the O projection's operands
@@ -341,11 +381,11 @@ class VerifyModel:
                                              self.table, self.lens, c.head_dim ** -0.5,
                                              self.attn_scratch, tree=self.tree)
             if c.rot_half <= ops.FUSED_QK_MAX_HALF and c.head_dim == 256:
-                ops.gemm_kquant_a_prepared(c.attn_fmt, lw.o[0], lw.o[1], self.o, T, H,
-                                           c.heads * c.head_dim, self.ws_a)
+                ops.gemm_kquant_a_prepared(lw.o_fmt or c.attn_fmt, lw.o[0], lw.o[1], self.o, T,
+                                           H, c.heads * c.head_dim, self.ws_a)
             else:
-                ops.gemm_kquant_a(c.attn_fmt, self.attn.view(T, -1), lw.o[0], lw.o[1], self.o, T,
-                                  H, c.heads * c.head_dim, self.ws_a)
+                ops.gemm_kquant_a(lw.o_fmt or c.attn_fmt, self.attn.view(T, -1), lw.o[0], lw.o[1],
+                                  self.o, T, H, c.heads * c.head_dim, self.ws_a)
             # feed-forward block
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
             if c.moe:
@@ -369,14 +409,23 @@ class VerifyModel:
                                res_out=res_out)
                 Lops.gate_up_swiglu(c.ffn_fmt, lw.gu[0], lw.gu[1], self.ws_h2, self.act, T,
                                     c.ffn, H)
-                ops.gemm_kquant_a(c.ffn_fmt, self.act, lw.dn[0], lw.dn[1], self.x, T, H, c.ffn,
-                                  self.ws_act)
+                ops.gemm_kquant_a(lw.dn_fmt or c.ffn_fmt, self.act, lw.dn[0], lw.dn[1], self.x, T,
+                                  H, c.ffn, self.ws_act)
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
         self.layer_residual = res_in  # residual stream entering the next layer (with self.x)
         # final norm + LM head (fp16 weights, f32 logits)
-        norm(self.final_norm, self.ws_f)
+        if self.head_wt == Lops.WT_BF16:
+            # the bf16 head GEMV reads the normalised rows themselves
+            norm(self.final_norm, self.ws_f, y_out=self.h2)
+            Lops.dense_gemv(Lops.WT_BF16, self.lm_head, self.h2, self.logits, T, c.vocab, H)
+        else:
+            norm(self.final_norm, self.ws_f)
+            if self.head_wt == HEAD_KQUANT:
+                ops.gemm_kquant_a_prepared(self.head_fmt, self.lm_head[0], self.lm_head[1],
+                                           self.logits, T, c.vocab, H, self.ws_f)
+            else:
+                Lops.dense_gemv(Lops.WT_F16, self.lm_head, self.ws_f, self.logits, T, c.vocab, H)
         self.final_residual = res_out
-        Lops.dense_gemv(Lops.WT_F16, self.lm_head, self.ws_f, self.logits, T, c.vocab, H)
         return self.logits
 
 

@@ -24,16 +24,8 @@ def geometry_of():
     from snowllm_amd import ops
 
     def install(cfg):
-        d = cfg.head_dim
-        ops.define_geometry(
-            hidden=cfg.hidden, num_heads=cfg.heads, num_kv_heads=cfg.kv_heads, head_size=d,
-            block_size=16, vocab_size=cfg.vocab, qkv_proj_n=cfg.qkv_n, qkv_q_head_stride=d,
-            qkv_off_k=cfg.heads * d, qkv_off_v=(cfg.heads + cfg.kv_heads) * d,
-            moe_num_experts=cfg.experts if cfg.moe else 0, moe_shared_expert=int(cfg.moe),
-            moe_topk=cfg.topk if cfg.moe else 0, moe_topk_all=cfg.topk + 1 if cfg.moe else 0,
-            moe_inter=cfg.expert_ffn if cfg.moe else 0, sampling_max_k=1 << 19,
-            lm_head_decode_max_m=256, mlp_inter=0 if cfg.moe else cfg.ffn,
-            mlp_gate_up_n=0 if cfg.moe else 2 * cfg.ffn)
+        from snowllm_amd.verify import geometry_fields
+        ops.define_geometry(**geometry_fields(cfg))
     yield install
     ops.select_geometry(0)
 
@@ -132,15 +124,25 @@ def test_moe_without_norm_and_head(gpu, geometry_of):
                   cfg.expert_ffn)
     torch.cuda.synchronize()
     assert torch.equal(out, want)
-    # LM head on normalised rows
+    # LM head on normalised rows: bf16 head (kind 0) and a Q8_0 head (kind 3), through the
+    # descriptor and the direct entry points, against the explicit GEMVs
+    from snowllm_amd.verify import gguf_random
     hs = torch.empty(ops.lm_head_scratch_bytes(T), dtype=torch.uint8, device="cuda")
-    logits = torch.empty(T, cfg.vocab, device="cuda")
-    ops.inference_head(y, m.lm_head, logits, hs)
-    ops.gemm_kquant_prepare_a(y, ws)
-    want_l = torch.empty_like(logits)
-    L.dense_gemv(L.WT_F16, m.lm_head, ws, want_l, T, cfg.vocab, H)
-    torch.cuda.synchronize()
-    assert torch.equal(logits, want_l)
+    head = (0.02 * torch.randn(cfg.vocab, H, device="cuda")).bfloat16()
+    hw = ops.lm_head_shuffle_weight(head)
+    want_l = torch.empty(T, cfg.vocab, device="cuda")
+    L.dense_gemv(L.WT_BF16, hw, y, want_l, T, cfg.vocab, H)
+    kraw = gguf_random(8, cfg.vocab, H, seed=5)
+    kw = ops.lm_head_kquant_shuffle_weight(kraw, 8)
+    want_k = torch.empty_like(want_l)
+    ops.gemm_kquant_a(8, y, kw.p0, kw.p1, want_k, T, cfg.vocab, H, ws)
+    for w, want, direct in ((hw, want_l, ops.lm_head), (kw, want_k, ops.lm_head_kquant)):
+        logits = torch.full_like(want_l, float("nan"))
+        ops.inference_head(y, w, logits, hs)
+        logits2 = torch.full_like(want_l, float("nan"))
+        direct(y, w, logits2, hs)
+        torch.cuda.synchronize()
+        assert torch.equal(logits, want) and torch.equal(logits2, want)
 
 
 def test_dense_mlp(gpu, geometry_of):
