@@ -406,6 +406,46 @@ int snowllm_lm_head_kquant(int fmt, const void* x, const void* quant, const void
 int snowllm_inference_head(const SnowllmWeight* w, const void* x, float* out, void* scratch,
                            int64_t M, void* stream);
 
+/* ---- DSpark Markov head (snowllm/_capi.py:567-573; snowllm/ops/dspark.py:10-16, 53-77;
+ * semantics tests/test_lfm2_dspark_reference.py:143-152) ----------------------------------
+ * Per request r and block row j: latent = w1[prev] (prev = anchor[r], then the previous row's
+ * pick; a prev outside [0, v) gives a zero latent), bias = w2 latent summed exactly and rounded
+ * once to bf16 (fp32 with fp32_bias), out[r, j] = argmax fp32(base + bias) (NaN as -inf, ties
+ * to the lowest index), confidence[r, j] = sigmoid([pre_head row, latent] . conf_weight +
+ * conf_bias). base f32 rows of stride base_stride; w2 packed by snowllm_dspark_pack_weight;
+ * b <= 16, rank % 8 == 0, rank <= 512; one launch per block row. Calls on one device must be
+ * stream-ordered (library-owned arrival counter). */
+int64_t snowllm_dspark_weight_bytes(int64_t n, int64_t k);
+int snowllm_dspark_pack_weight(const void* raw, void* packed, int64_t n, int64_t k, void* stream);
+int64_t snowllm_dspark_markov_workspace_bytes(int64_t b, int64_t v, int64_t rank, int64_t block);
+int snowllm_dspark_markov(const void* base, const void* w1, const void* w2, const int64_t* anchor,
+                          const void* pre_head, const float* conf_weight, const float* conf_bias,
+                          int64_t* out, float* confidence, void* workspace, int64_t b, int64_t v,
+                          int64_t rank, int64_t block, int64_t base_stride, int64_t h, int64_t ps,
+                          int64_t workspace_bytes, int fp32_bias, void* stream);
+
+/* ---- DFlash draft shape and the selector's hidden projection (snowllm/_capi.py:66-90,
+ * 227-239, 277, 282; snowllm/ops/dflash.py:21-135; models/qwen3_5/dflash_draft.py:187-204) --
+ * Any draft shape is accepted (hidden % 256 == 0). Projection `which` 7 (SELECTOR_HIDDEN):
+ * hp [m, 256] bf16 = hidden [m, draft hidden] W^T, fp32 accumulate, W bf16 (descriptor kind
+ * 0, repacked by snowllm_draft_proj_shuffle_w into snowllm_shuffle_bytes of its bytes) or
+ * Q4_K / Q8_0 (kind 2). The backbone's projections (0-6) return hipErrorNotSupported. */
+typedef struct DraftShape {
+  int64_t hidden, num_layers, num_heads, num_kv_heads, head_size, intermediate, num_taps;
+} DraftShape;
+int snowllm_select_draft(const DraftShape* shape);
+int64_t snowllm_draft_count(void);
+int snowllm_draft_shape(int i, DraftShape* out);
+int64_t snowllm_draft_name(int i, char* buf, int64_t n);
+int snowllm_draft_projection_shape(int which, int64_t* nk);
+int snowllm_draft_projection_plan(int which, const SnowllmWeight* w, int64_t m, int64_t* plan);
+int64_t snowllm_draft_projections_workspace_bytes(int64_t m);
+int snowllm_draft_projection(int which, const SnowllmWeight* w, const void* a, void* out,
+                             void* scratch, int64_t capacity, int64_t m, void* stream);
+int snowllm_draft_proj_shuffle_w(int which, const void* w, void* out, void* stream);
+int snowllm_draft_proj_shuffle_w_kquant(int which, int fmt, const uint8_t* blocks, uint8_t* quant,
+                                        uint8_t* meta, void* stream);
+
 /* ---- geometry ------------------------------------------------------------------------ */
 /* The reference compiles its shapes in (snowllm/_capi.py:44-113); here they are run-time
  * data. BuildGeometry has the reference's 37 int64 fields in the same order. */

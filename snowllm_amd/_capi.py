@@ -150,6 +150,20 @@ _SIGS = [
     ("snowllm_lm_head_kquant_shuffle_weight", c_int, [c_int, P, P, P, S]),
     ("snowllm_lm_head_kquant", c_int, [c_int, P, P, P, P, c_int64, P, S]),
     ("snowllm_gather_embedding_q4_k", c_int, [P] * 3 + [c_int64] * 3 + [S]),
+    ("snowllm_dspark_weight_bytes", c_int64, [c_int64] * 2),
+    ("snowllm_dspark_pack_weight", c_int, [P, P, c_int64, c_int64, S]),
+    ("snowllm_dspark_markov_workspace_bytes", c_int64, [c_int64] * 4),
+    ("snowllm_dspark_markov", c_int, [P] * 10 + [c_int64] * 8 + [c_int, S]),
+    ("snowllm_select_draft", c_int, [P]),
+    ("snowllm_draft_count", c_int64, []),
+    ("snowllm_draft_shape", c_int, [c_int, P]),
+    ("snowllm_draft_name", c_int64, [c_int, c_char_p, c_int64]),
+    ("snowllm_draft_projection_shape", c_int, [c_int, P]),
+    ("snowllm_draft_projection_plan", c_int, [c_int, P, c_int64, P]),
+    ("snowllm_draft_projections_workspace_bytes", c_int64, [c_int64]),
+    ("snowllm_draft_projection", c_int, [c_int, P, P, P, P, c_int64, c_int64, S]),
+    ("snowllm_draft_proj_shuffle_w", c_int, [c_int, P, P, S]),
+    ("snowllm_draft_proj_shuffle_w_kquant", c_int, [c_int, c_int, P, P, P, S]),
     ("snowllm_rope_cos_sin", c_int, [P, P, P, P, c_int64, S]),
     ("snowllm_qk_norm_rope_cache", c_int, [P, c_int64, P, c_int64, P, c_int64] + [P] * 10 + [c_int64, c_float, c_int64, S]),
     # geometry and layer plumbing

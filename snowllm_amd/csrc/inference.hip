@@ -18,6 +18,8 @@
 #include "common.h"
 #include "geometry.h"
 
+#include <string.h>
+
 namespace {
 
 struct Weight {  // snowllm/ops/inference.py:10-12
@@ -569,4 +571,113 @@ SV_API int snowllm_inference_head(const Weight* w, const void* x, float* out, vo
   if (kquant(w)) return snowllm_lm_head_kquant(w->fmt, x, w->data[0], w->data[1], out, M, scratch,
                                               stream);
   return SV_ENOTSUP;
+}
+
+// ---- DFlash draft: shape selection and the selector's hidden projection ------------------
+// (snowllm/_capi.py:66-90, 227-239, 277, 282; snowllm/ops/dflash.py:21-135;
+// models/qwen3_5/dflash_draft.py:187-204). The reference compiles its draft shapes in and
+// snowllm_select_draft picks one; here any shape is run-time data. Of the draft's projections
+// this build computes the one that feeds the candidate selector: SELECTOR_HIDDEN,
+// hp [m, 256] bf16 = hidden [m, draft hidden] W^T, W [256, draft hidden] bf16 (kind 0,
+// repacked by snowllm_draft_proj_shuffle_w) or Q4_K / Q8_0 (kind 2, repacked by
+// snowllm_draft_proj_shuffle_w_kquant); fp32 accumulate, one bf16 rounding. The backbone's
+// projections (FC, CTX_KV, QKV, O, GATE_UP, DOWN, CONV) return hipErrorNotSupported.
+struct DraftShape {  // snowllm/_capi.py:67-72
+  int64_t hidden, num_layers, num_heads, num_kv_heads, head_size, intermediate, num_taps;
+};
+namespace {
+constexpr int PROJ_SELECTOR_HIDDEN = 7;   // snowllm/ops/dflash.py:29
+constexpr int64_t SELECTOR_RANK = 256;    // the selector's codebook rank
+DraftShape g_draft;
+bool g_draft_set = false;
+
+bool selector_proj(int which) { return which == PROJ_SELECTOR_HIDDEN && g_draft_set; }
+}  // namespace
+
+SV_API int snowllm_select_draft(const DraftShape* s) {
+  if (!s || s->hidden <= 0 || s->hidden % 256 || s->hidden > 65536) return SV_EINVAL;
+  g_draft = *s;
+  g_draft_set = true;
+  return SV_OK;
+}
+SV_API int64_t snowllm_draft_count(void) { return g_draft_set ? 1 : 0; }
+SV_API int snowllm_draft_shape(int i, DraftShape* out) {
+  if (i != 0 || !g_draft_set || !out) return SV_EINVAL;
+  *out = g_draft;
+  return SV_OK;
+}
+SV_API int64_t snowllm_draft_name(int i, char* buf, int64_t n) {
+  const char* name = (i == 0 && g_draft_set) ? "selected" : "";
+  const int64_t len = (int64_t)strlen(name);
+  if (buf && n > 0) {
+    const int64_t c = len < n - 1 ? len : n - 1;
+    memcpy(buf, name, (size_t)c);
+    buf[c] = 0;
+  }
+  return len;
+}
+
+SV_API int snowllm_draft_projection_shape(int which, int64_t* nk) {
+  if (!nk) return SV_EINVAL;
+  if (!selector_proj(which)) return SV_ENOTSUP;
+  nk[0] = SELECTOR_RANK;
+  nk[1] = g_draft.hidden;
+  return SV_OK;
+}
+
+// plan = {n, k, scratch bytes} for m rows of the weight storage w (kind, fmt only).
+SV_API int snowllm_draft_projection_plan(int which, const Weight* w, int64_t m, int64_t* plan) {
+  if (!w || !plan || m <= 0) return SV_EINVAL;
+  if (!selector_proj(which)) return SV_ENOTSUP;
+  plan[0] = SELECTOR_RANK;
+  plan[1] = g_draft.hidden;
+  if (w->kind == 0) plan[2] = 0;
+  else if (w->kind == 2 && (w->fmt == 4 || w->fmt == 8))
+    plan[2] = snowllm_gemm_kquant_a_ws_bytes(m, g_draft.hidden);
+  else return SV_ENOTSUP;
+  return SV_OK;
+}
+
+SV_API int64_t snowllm_draft_projections_workspace_bytes(int64_t m) {
+  if (m <= 0 || !g_draft_set) return 0;
+  return snowllm_gemm_kquant_a_ws_bytes(m, g_draft.hidden);
+}
+
+SV_API int snowllm_draft_projection(int which, const Weight* w, const void* a, void* out,
+                                    void* scratch, int64_t capacity, int64_t m, void* stream) {
+  if (!w || !a || !out || m <= 0) return SV_EINVAL;
+  if (!selector_proj(which)) return SV_ENOTSUP;
+  const int64_t K = g_draft.hidden;
+  if (w->kind == 0 && w->data[0]) {
+    for (int64_t r0 = 0; r0 < m; r0 += 16) {
+      const int64_t rows = m - r0 < 16 ? m - r0 : 16;
+      const int rc = snowverify_dense_gemv(WT_BF16, w->data[0], (const uint16_t*)a + r0 * K,
+                                           (uint16_t*)out + r0 * SELECTOR_RANK, rows,
+                                           SELECTOR_RANK, K, 1, stream);
+      if (rc) return rc;
+    }
+    return SV_OK;
+  }
+  if (w->kind == 2 && w->data[0] && w->data[1]) {
+    if (!scratch || capacity < snowllm_gemm_kquant_a_ws_bytes(m, K)) return SV_EINVAL;
+    return snowllm_gemm_kquant_a(w->fmt, a, (const uint8_t*)w->data[0],
+                                 (const uint8_t*)w->data[1], out, m, SELECTOR_RANK, K, 1,
+                                 scratch, stream);
+  }
+  return SV_ENOTSUP;
+}
+
+// bf16 [256, draft hidden] -> the projection's layout (snowllm_shuffle_bytes of its bytes).
+SV_API int snowllm_draft_proj_shuffle_w(int which, const void* w, void* out, void* stream) {
+  if (!w || !out) return SV_EINVAL;
+  if (!selector_proj(which)) return SV_ENOTSUP;
+  return snowverify_dense_shuffle(w, out, SELECTOR_RANK, g_draft.hidden, WT_BF16, stream);
+}
+
+SV_API int snowllm_draft_proj_shuffle_w_kquant(int which, int fmt, const uint8_t* blocks,
+                                               uint8_t* quant, uint8_t* meta, void* stream) {
+  if (!blocks || !quant || !meta) return SV_EINVAL;
+  if (!selector_proj(which)) return SV_ENOTSUP;
+  return snowllm_gemm_kquant_shuffle_b(fmt, blocks, quant, meta, SELECTOR_RANK, g_draft.hidden,
+                                       stream);
 }

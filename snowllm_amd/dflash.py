@@ -1,5 +1,8 @@
 """DFlash 2 selector and acceptance (snowllm/ops/dflash.py:159-219): the candidate walk that
 proposes a draft path, and rejection sampling of a draft prefix."""
+import ctypes
+import enum
+
 import torch
 
 from ._capi import check, lib
@@ -145,3 +148,108 @@ def accept_greedy(logits, drafts, tokens, accepted):
 
 
 NOT_SUPPORTED = 801  # hipErrorNotSupported
+
+
+# ---- draft shape and the selector's hidden projection (snowllm/ops/dflash.py:21-135) -------
+class Proj(enum.IntEnum):
+    """Projection ids of the DFlash draft (snowllm/ops/dflash.py:21-29); this build computes
+    SELECTOR_HIDDEN."""
+    FC = 0
+    CTX_KV = 1
+    QKV = 2
+    O = 3  # noqa: E741
+    GATE_UP = 4
+    DOWN = 5
+    CONV = 6
+    SELECTOR_HIDDEN = 7
+
+
+DRAFT_SHAPE_FIELDS = ("hidden", "num_layers", "num_heads", "num_kv_heads", "head_size",
+                      "intermediate", "num_taps")
+
+
+class DraftShape(ctypes.Structure):   # snowllm/_capi.py:67-72
+    _fields_ = [(n, ctypes.c_int64) for n in DRAFT_SHAPE_FIELDS]
+
+
+_selected = None
+
+
+def select(geo) -> None:
+    """Install the draft's shape (any object with the DraftShape fields)."""
+    global _selected
+    shape = DraftShape(*(int(getattr(geo, n, 0) or 0) for n in DRAFT_SHAPE_FIELDS))
+    if lib.snowllm_select_draft(ctypes.byref(shape)) != 0:
+        raise SnowLLMError(f"draft shape not supported (hidden {shape.hidden} must be a positive "
+                           f"multiple of 256)")
+    _selected = geo
+
+
+def selected():
+    if _selected is None:
+        raise SnowLLMError("no DFlash draft is selected; call select(geometry) first")
+    return _selected
+
+
+def proj_shape(which: Proj) -> tuple:
+    nk = (ctypes.c_int64 * 2)()
+    check(lib.snowllm_draft_projection_shape(int(which), nk), "draft_projection_shape")
+    return tuple(nk)
+
+
+def proj_plan(which: Proj, w, m: int) -> tuple:
+    from .inference import _weight
+    plan = (ctypes.c_int64 * 3)()
+    weight = _weight(w)
+    check(lib.snowllm_draft_projection_plan(int(which), ctypes.byref(weight), int(m), plan),
+          "draft_projection_plan")
+    return tuple(plan)
+
+
+def proj_workspace_bytes(which: Proj, w, m: int) -> int:
+    return proj_plan(which, w, m)[2]
+
+
+def projections_workspace_bytes(m: int) -> int:
+    return int(lib.snowllm_draft_projections_workspace_bytes(int(m)))
+
+
+def proj_shuffle_w(which: Proj, w: torch.Tensor) -> torch.Tensor:
+    n, k = proj_shape(which)
+    _chk(w, f"draft {which.name} w", torch.bfloat16, n, k)
+    buf = torch.empty(lib.snowllm_shuffle_bytes(w.numel() * w.element_size()), dtype=torch.uint8,
+                      device="cuda")
+    check(lib.snowllm_draft_proj_shuffle_w(int(which), _p(w), _p(buf), _stream()),
+          "draft_proj_shuffle_w")
+    return buf
+
+
+def proj_shuffle_w_kquant(which: Proj, blocks: torch.Tensor, fmt: int):
+    from .inference import KQuantProjWeight
+    n, k = proj_shape(which)
+    _chk(blocks, f"draft {which.name} blocks", torch.uint8)
+    want = lib.snowllm_kquant_gguf_bytes(fmt, n, k)
+    if blocks.numel() != want:
+        raise SnowLLMError(f"draft {which.name}: expected {want} bytes of GGUF blocks for a "
+                           f"[{n}, {k}] weight at format {fmt}, got {blocks.numel()}")
+    quant = torch.empty(lib.snowllm_kquant_quant_bytes(fmt, n, k), dtype=torch.uint8, device="cuda")
+    meta = torch.empty(lib.snowllm_kquant_meta_bytes(fmt, n, k), dtype=torch.uint8, device="cuda")
+    check(lib.snowllm_draft_proj_shuffle_w_kquant(int(which), fmt, _p(blocks), _p(quant),
+                                                  _p(meta), _stream()),
+          "draft_proj_shuffle_w_kquant")
+    return KQuantProjWeight(quant, meta, fmt)
+
+
+def proj(which: Proj, a: torch.Tensor, w_shuffled, a_scratch, out: torch.Tensor) -> None:
+    """out [m, n] bf16 = a [m, k] W^T for a repacked bf16 or k-quant draft weight."""
+    from .inference import _weight
+    m = a.shape[0]
+    weight = _weight(w_shuffled)
+    n, k, need = proj_plan(which, w_shuffled, m)
+    _chk(a, "a", torch.bfloat16, m, k)
+    _chk(out, "out", torch.bfloat16, m, n)
+    capacity = 0 if a_scratch is None else a_scratch.nbytes
+    if capacity < need:
+        raise SnowLLMError(f"draft projection needs {need} scratch bytes, got {capacity}")
+    check(lib.snowllm_draft_projection(int(which), ctypes.byref(weight), _p(a), _p(out),
+                                       _p(a_scratch), capacity, m, _stream()), "draft_projection")

@@ -26,5 +26,7 @@ from .inference import (KQuantProjWeight, KQuantExpertWeight, inference_qkv,  # 
 from .embedding import (lm_head_shuffle_weight, gather_embedding,  # noqa: F401
                         gather_embedding_q4_k, lm_head_kquant_shuffle_weight, lm_head_kquant,
                         lm_head)
+from .dspark import (dspark_pack_weight, dspark_markov,  # noqa: F401
+                     dspark_markov_workspace_bytes)
 from .geometry import (build_geometry, select_geometry, active_geometry,  # noqa: F401
                        define_geometry)
