@@ -450,11 +450,18 @@ def bench_step(args, name):
         sb = k * V * 4 + k * (2 * 16 + 1) * SEL_RANK * 2
         kern["draft_select (chunks + table + walk)"] = {
             "us": round(us, 3), "alg_bytes": int(sb), "gbs": round(sb / (us * 1e-6) / 1e9, 1)}
+    adaptive = None
     if cfg.name == CONFIGS["config4"].name:
         # BASELINE config 1 (the acceptance alone) beside the north-star step
-        kern["config1_acceptance"] = time_acceptance(reps=200)
+        kern["config1_acceptance"] = dict(time_acceptance(reps=200), outside_step=True)
+        # the draft heads that produce the next proposal, and the adaptive prefix scheduler
+        # on this step's measured costs
+        heads = time_draft_heads(stream, V, k)
+        kern.update(heads)
+        adaptive = adaptive_prefix(m, heads["dspark_markov (per block row)"]["us"] * k * 1e-6)
     # dominant single kernel per step (launch time x launches per step)
-    single = {kk: v for kk, v in kern.items() if "+" not in kk and "us" in v}
+    single = {kk: v for kk, v in kern.items()
+              if "+" not in kk and "us" in v and not v.get("outside_step")}
     dom = max(single, key=lambda kk: single[kk]["us"])
     d = kern[dom]
     traffic = read_traffic(dom) if cfg.name == CONFIGS[TRAFFIC_WORKLOAD].name else None
@@ -488,11 +495,72 @@ def bench_step(args, name):
                      "traffic": traffic, "alg_bytes_per_launch": d["alg_bytes"],
                      "kernel_us": d["us"]},
         "kernels": kern,
+        "adaptive_prefix": adaptive,
         "init_s": round(init_s, 1),
         "cpu_baseline": {"value": round(cpu_value, 4), "unit": "tok/s", "cores": cpu["cores"],
                          "kind": "port", "cpu": cpu_model(), "sample": cpu["sample"],
                          "step_s": round(cpu["step_s"], 3)},
     }
+
+
+def time_draft_heads(stream, V, k, hidden=2048, markov_rank=256):
+    """The draft-side heads at the config-4 shapes (seeded synthetic weights): the DFlash 2
+    selector's hidden projection of k rows (bf16 [256, hidden]) and the DSpark Markov walk over
+    a block of k rows (W1, W2 bf16 [V, rank], with the confidence head), per launch."""
+    import torch
+    from snowllm_amd.draft_heads import MarkovHead, SelectorHead
+    g = torch.Generator(device="cuda").manual_seed(5)
+    out = {}
+    w = (torch.randn(SEL_RANK, hidden, device="cuda", generator=g) * hidden ** -.5).bfloat16()
+    codebook = torch.zeros(16, SEL_RANK, dtype=torch.bfloat16, device="cuda")
+    head = SelectorHead(hidden, w, codebook, codebook)
+    rows = torch.randn(k, hidden, device="cuda", generator=g).bfloat16()
+    hp = torch.empty(k, SEL_RANK, dtype=torch.bfloat16, device="cuda")
+    us = timed_graph(lambda: head.project(rows, hp), 50, stream, per=10) * 1e3
+    nb = SEL_RANK * hidden * 2 + k * (hidden + SEL_RANK) * 2
+    out["selector_hidden_projection"] = {"us": round(us, 3), "alg_bytes": nb,
+                                         "gbs": round(nb / (us * 1e-6) / 1e9, 1),
+                                         "outside_step": True}
+    W1 = (torch.randn(V, markov_rank, device="cuda", generator=g) * .25).bfloat16()
+    W2 = (torch.randn(V, markov_rank, device="cuda", generator=g) * .25).bfloat16()
+    conf_w = torch.randn(hidden + markov_rank, device="cuda", generator=g) * .05
+    mk = MarkovHead(W1, W2, conf_w, torch.zeros(1, device="cuda"))
+    logits = torch.randn(k, V, device="cuda", generator=g)
+    anchor = torch.zeros(1, dtype=torch.int64, device="cuda")
+    path = torch.empty(1, k, dtype=torch.int64, device="cuda")
+    conf = torch.empty(1, k, device="cuda")
+    mk.propose(rows, logits, anchor, path, conf)
+    us = timed_graph(lambda: mk.propose(rows, logits, anchor, path, conf), 20, stream) * 1e3 / k
+    nb = V * markov_rank * 2 + V * 4 + markov_rank * 2 + hidden * 2
+    out["dspark_markov (per block row)"] = {
+        "us": round(us, 3), "alg_bytes": nb, "gbs": round(nb / (us * 1e-6) / 1e9, 1),
+        "outside_step": True,
+        "note": "W2 (78 MB) is read by each of the block's rows; after the first it is largely "
+                "served from the 256 MB Infinity Cache"}
+    return out
+
+
+def adaptive_prefix(m, draft_s, rows=tuple(range(1, 17))):
+    """The DSpark prefix scheduler (snowllm/engine/dspark_schedule.py) on step costs measured
+    here: verify steps of 1..16 rows (eager and graph) plus the Markov head's time, and a
+    synthetic confidence profile (c_j = 0.9 * 0.97^j over 15 drafted tokens). Every row count
+    of a batch-1 block gets a captured graph, as the reference's profile of its decode shapes
+    (snowllm/engine/spec_decode.py:149-161)."""
+    from snowllm_amd.dspark_schedule import PrefixScheduler, profile_step_costs
+    cost = profile_step_costs(m, rows, draft_seconds=draft_s)
+    conf = [[0.9 * 0.97 ** j for j in range(15)]]
+    lengths = PrefixScheduler(16).choose([0], conf, [15], cost)
+    surv, s = [], 1.0
+    for c in conf[0]:
+        s *= c
+        surv.append(s)
+
+    def rate(n):
+        return (1 + sum(surv[:n])) / cost(1 + n)
+    return {"step_us_by_rows": {n: round(cost.graphs[n] * 1e6, 1) for n in rows},
+            "draft_us": round(draft_s * 1e6, 1), "confidence": "0.9*0.97^j, 15 drafts",
+            "chosen_drafts": lengths[0], "expected_tokens_per_s": round(rate(lengths[0]), 1),
+            "fixed_block8_tokens_per_s": round(rate(8), 1)}
 
 
 def weights_note(cfg):

@@ -413,7 +413,7 @@ int snowllm_inference_head(const SnowllmWeight* w, const void* x, float* out, vo
  * once to bf16 (fp32 with fp32_bias), out[r, j] = argmax fp32(base + bias) (NaN as -inf, ties
  * to the lowest index), confidence[r, j] = sigmoid([pre_head row, latent] . conf_weight +
  * conf_bias). base f32 rows of stride base_stride; w2 packed by snowllm_dspark_pack_weight;
- * b <= 16, rank % 8 == 0, rank <= 512; one launch per block row. Calls on one device must be
+ * b <= 16, rank % 8 == 0, rank <= 512, b * rank <= 4096; one launch per block row. Calls on one device must be
  * stream-ordered (library-owned arrival counter). */
 int64_t snowllm_dspark_weight_bytes(int64_t n, int64_t k);
 int snowllm_dspark_pack_weight(const void* raw, void* packed, int64_t n, int64_t k, void* stream);

@@ -13,18 +13,19 @@
 // so that one wave load of 1 KB gives each of 64 lanes a 16-byte chunk of its own vocabulary
 // row; each lane sums its row's products in fp64 -- exact for products of two bf16 values --
 // and rounds the sum once, so the bias does not depend on the summation order. Every
-// workgroup reduces its rows to one (value, index) key per request; the last workgroup to
-// arrive reduces the keys, writes the pick and the confidence, and the next row's launch reads
-// the pick as its latent index.
+// workgroup reduces its rows to one (value, index) key per request; the last workgroup of a
+// two-level arrival reduces the keys, writes the pick and the confidence, and the next row's
+// launch reads the pick as its latent index.
 #include "common.h"
 
 namespace {
 
-constexpr int DSP_WAVES = 4;               // 64-row tiles per workgroup
+constexpr int DSP_WAVES = 4;               // waves per 64-row tile (they split the rank)
 constexpr int DSP_NT = DSP_WAVES * WAVE;
 constexpr int DSP_MAX_B = 16;              // requests per call
 constexpr int DSP_MAX_RANK = 512;
 constexpr uint64_t DSP_QUANTUM = 1ull << 20;  // > workgroups of a launch
+constexpr int64_t DSP_MAX_V = (int64_t)1 << 31;
 
 // Arrivals of the last launch (library-owned; calls on one device are stream-ordered). Each
 // launch adds exactly one quantum, so the count stays a multiple of it between launches and
@@ -73,12 +74,41 @@ struct DspArgs {
   int b, rank, block, h, nwg, fp32_bias, j;
 };
 
+// Grid: G <= 1024 workgroups of 4 waves; wave k of workgroup g takes the 64-row tiles
+// 4 g + k, 4 g + k + 4 G, ... and keeps its best (value, index) key per request. Each lane sums
+// its row's products in fp64 with 8 chunk loads (128 bytes of the row) in flight.
+// Arrival is two-level so that no counter sees more than 32 arrivals: the workgroups of a
+// group of 32 count on the group's counter; the group's last arrival reduces the group's keys
+// and counts on the top counter, whose last arrival reduces the groups' keys and writes the
+// pick (and the confidence).
+constexpr int DSP_GRID = 1024, DSP_GROUP = 32, DSP_GROUPS = DSP_GRID / DSP_GROUP;
+__device__ uint64_t g_dsp_group[DSP_GROUPS];
+
+__device__ __forceinline__ bool dsp_arrive(uint64_t* cnt, int n, bool lead, uint32_t* s_flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint64_t inc = lead ? DSP_QUANTUM - (uint64_t)n + 1 : 1;
+    const uint64_t old = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = ((old + inc) & (DSP_QUANTUM - 1)) == 0;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+
+__device__ __forceinline__ uint64_t dsp_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// MB: a compile-time bound on the requests (1, 4 or 16), which sizes the registers.
+template <int MB>
 __global__ void __launch_bounds__(DSP_NT) dsp_markov_kernel(DspArgs a) {
-  __shared__ float s_lat[DSP_MAX_B * DSP_MAX_RANK];
-  __shared__ uint64_t s_red[DSP_WAVES][DSP_MAX_B];
-  __shared__ uint32_t s_last;
+  __shared__ float s_lat[4096];                  // latents f32 [b][rank], b rank <= 4096
+  __shared__ uint64_t s_key[DSP_WAVES][DSP_MAX_B];
+  __shared__ uint32_t s_flag;
   const int t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
-  const int B = a.b, R = a.rank, j = a.j;
+  const int B = a.b, R = a.rank, j = a.j, G = a.nwg;
   for (int i = t; i < B * R; i += DSP_NT) {
     const int r = i / R, e = i % R;
     const int64_t prev = j == 0 ? a.anchor[r] : a.out[(int64_t)r * a.block + j - 1];
@@ -86,78 +116,94 @@ __global__ void __launch_bounds__(DSP_NT) dsp_markov_kernel(DspArgs a) {
   }
   __syncthreads();
 
-  const int64_t tile = (int64_t)blockIdx.x * DSP_WAVES + w;
-  const int64_t row = tile * WAVE + lane;
-  const bool live = row < a.v;
-  double acc[DSP_MAX_B];
+  const int64_t tiles = (a.v + WAVE - 1) / WAVE;
+  const int chunks = R / 8;
+  uint64_t best[MB];
 #pragma unroll
-  for (int r = 0; r < DSP_MAX_B; ++r) acc[r] = 0.0;
-  if (tile * WAVE < a.v) {
+  for (int r = 0; r < MB; ++r) best[r] = 0;
+  for (int64_t tile = (int64_t)blockIdx.x * DSP_WAVES + w; tile < tiles;
+       tile += (int64_t)G * DSP_WAVES) {
     const int64_t rows_t = a.v - tile * WAVE < WAVE ? a.v - tile * WAVE : WAVE;
+    const int64_t row = tile * WAVE + lane;
+    const bool live = lane < rows_t;
     const uint4* src = (const uint4*)(a.w2 + tile * WAVE * (int64_t)R) + lane;
-    const int chunks = R / 8;
-#pragma unroll 4
-    for (int c = 0; c < chunks; ++c) {
-      uint4 q = {0u, 0u, 0u, 0u};
-      if (live) q = src[c * rows_t];
-      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-      float wv[8];
+    double acc[MB];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        wv[2 * e] = __uint_as_float(qw[e] << 16);
-        wv[2 * e + 1] = __uint_as_float(qw[e] & 0xffff0000u);
+    for (int r = 0; r < MB; ++r) acc[r] = 0.0;
+    for (int cb = 0; cb < chunks; cb += 8) {
+      uint4 q[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        q[u] = {0u, 0u, 0u, 0u};
+        if (live && cb + u < chunks) q[u] = src[(cb + u) * rows_t];
       }
 #pragma unroll
-      for (int r = 0; r < DSP_MAX_B; ++r) {
-        if (r < B) {
-          const float* L = s_lat + r * R + c * 8;
-          double s = acc[r];
+      for (int u = 0; u < 8; ++u) {
+        if (cb + u < chunks) {
+          const uint32_t qw[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+          float wv[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) s += (double)(wv[e] * L[e]);  // exact bf16 x bf16
-          acc[r] = s;
+          for (int e = 0; e < 4; ++e) {
+            wv[2 * e] = __uint_as_float(qw[e] << 16);
+            wv[2 * e + 1] = __uint_as_float(qw[e] & 0xffff0000u);
+          }
+#pragma unroll
+          for (int r = 0; r < MB; ++r) {
+            if (r < B) {
+              const float* L = s_lat + r * R + (cb + u) * 8;
+              double s0 = 0.0, s1 = 0.0;   // two chains; the sum stays exact
+#pragma unroll
+              for (int e = 0; e < 8; e += 2) {
+                s0 += (double)(wv[e] * L[e]);        // exact bf16 x bf16
+                s1 += (double)(wv[e + 1] * L[e + 1]);
+              }
+              acc[r] += s0 + s1;
+            }
+          }
         }
       }
     }
-  }
 #pragma unroll
-  for (int r = 0; r < DSP_MAX_B; ++r) {
-    if (r < B) {
-      uint64_t key = 0;
-      if (live) {
+    for (int r = 0; r < MB; ++r) {
+      if (r < B && live) {
         const float bias = a.fp32_bias ? (float)acc[r] : bf16_from_f64(acc[r]);
         const float x = a.base[((int64_t)r * a.block + j) * a.base_stride + row] + bias;
-        key = argmax_key(x, (uint32_t)row);
+        const uint64_t key = argmax_key(x, (uint32_t)row);
+        best[r] = key > best[r] ? key : best[r];
       }
-      key = wave_max_u64(key);
-      if (lane == 0) s_red[w][r] = key;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < MB; ++r) {
+    if (r < B) {
+      const uint64_t k = wave_max_u64(best[r]);
+      if (lane == 0) s_key[w][r] = k;
     }
   }
   __syncthreads();
+  uint64_t* wg_keys = a.partial;                          // [b][G]
+  uint64_t* group_keys = a.partial + (int64_t)B * G;      // [b][groups]
   if (t < B) {
-    uint64_t m = s_red[0][t];
-    for (int i = 1; i < DSP_WAVES; ++i) m = s_red[i][t] > m ? s_red[i][t] : m;
-    __hip_atomic_store(&a.partial[(int64_t)t * a.nwg + blockIdx.x], m, __ATOMIC_RELAXED,
+    uint64_t m = s_key[0][t];
+    for (int i = 1; i < DSP_WAVES; ++i) m = s_key[i][t] > m ? s_key[i][t] : m;
+    __hip_atomic_store(&wg_keys[(int64_t)t * G + blockIdx.x], m, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
-  // arrival: this workgroup's partial keys are stored before its count is added
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (t == 0) {
-    const uint64_t inc = blockIdx.x == 0 ? DSP_QUANTUM - (uint64_t)a.nwg + 1 : 1;
-    const uint64_t old =
-        __hip_atomic_fetch_add(&g_dsp_cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = ((old + inc) & (DSP_QUANTUM - 1)) == 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  // the last workgroup: one wave per request
+  const int group = blockIdx.x / DSP_GROUP, groups = (G + DSP_GROUP - 1) / DSP_GROUP;
+  const int g0 = group * DSP_GROUP, gn = G - g0 < DSP_GROUP ? G - g0 : DSP_GROUP;
+  if (!dsp_arrive(&g_dsp_group[group], gn, blockIdx.x == g0, &s_flag)) return;
+  // the group's last workgroup: its group's keys, one load per lane
   for (int r = w; r < B; r += DSP_WAVES) {
-    uint64_t m = 0;
-    for (int i = lane; i < a.nwg; i += WAVE) {
-      const uint64_t k = __hip_atomic_load(&a.partial[(int64_t)r * a.nwg + i], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-      m = k > m ? k : m;
-    }
+    uint64_t m = lane < gn ? dsp_load(&wg_keys[(int64_t)r * G + g0 + lane]) : 0;
+    m = wave_max_u64(m);
+    if (lane == 0)
+      __hip_atomic_store(&group_keys[r * groups + group], m, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!dsp_arrive(&g_dsp_cnt, groups, group == 0, &s_flag)) return;
+  // the last group: the pick and the confidence, one wave per request
+  for (int r = w; r < B; r += DSP_WAVES) {
+    uint64_t m = lane < groups ? dsp_load(&group_keys[r * groups + lane]) : 0;
     m = wave_max_u64(m);
     const int64_t at = (int64_t)r * a.block + j;
     if (lane == 0) a.out[at] = (int64_t)argmax_key_index(m);
@@ -175,7 +221,11 @@ __global__ void __launch_bounds__(DSP_NT) dsp_markov_kernel(DspArgs a) {
   }
 }
 
-int64_t dsp_nwg(int64_t v) { return ((v + WAVE - 1) / WAVE + DSP_WAVES - 1) / DSP_WAVES; }
+int64_t dsp_nwg(int64_t v) {
+  const int64_t tiles = (v + WAVE - 1) / WAVE;
+  const int64_t g = (tiles + DSP_WAVES - 1) / DSP_WAVES;
+  return g < DSP_GRID ? g : DSP_GRID;
+}
 
 }  // namespace
 
@@ -196,20 +246,23 @@ SV_API int snowllm_dspark_pack_weight(const void* raw, void* packed, int64_t n, 
   return SV_OK;
 }
 
-// Workspace of snowllm_dspark_markov: one 8-byte key per request and workgroup.
+// Workspace of snowllm_dspark_markov: 8-byte keys per request for every workgroup and
+// every group of workgroups.
 SV_API int64_t snowllm_dspark_markov_workspace_bytes(int64_t b, int64_t v, int64_t rank,
                                                      int64_t block) {
   (void)rank;
   (void)block;
   if (b <= 0 || v <= 0) return 0;
-  return ((b * dsp_nwg(v) * 8 + 255) / 256) * 256;
+  const int64_t g = dsp_nwg(v);
+  return ((b * (g + (g + DSP_GROUP - 1) / DSP_GROUP) * 8 + 255) / 256) * 256;
 }
 
 // base f32 [b * block, >= v] (row stride base_stride), w1 bf16 [v, rank], w2 packed by
 // snowllm_dspark_pack_weight, anchor i64 [b] -> out i64 [b, block]; with confidence (f32
 // [b, block]) also pre_head bf16 [b * block, >= h] (row stride ps), conf_weight f32
 // [h + rank] and an optional scalar conf_bias. fp32_bias keeps the bias in fp32 instead of
-// bf16. b <= 16, rank % 8 == 0 and rank <= 512. Calls on one device must be stream-ordered.
+// bf16. b <= 16, rank % 8 == 0, rank <= 512, b rank <= 4096. Calls on one device must be
+// stream-ordered.
 SV_API int snowllm_dspark_markov(const void* base, const void* w1, const void* w2,
                                  const int64_t* anchor, const void* pre_head,
                                  const float* conf_weight, const float* conf_bias, int64_t* out,
@@ -218,8 +271,8 @@ SV_API int snowllm_dspark_markov(const void* base, const void* w1, const void* w
                                  int64_t ps, int64_t workspace_bytes, int fp32_bias,
                                  void* stream) {
   if (!base || !w1 || !w2 || !anchor || !out || !workspace) return SV_EINVAL;
-  if (b <= 0 || b > DSP_MAX_B || v <= 0 || v > (int64_t)1 << 31 || rank <= 0 || rank % 8 ||
-      rank > DSP_MAX_RANK || block <= 0 || block > 1024 || base_stride < v)
+  if (b <= 0 || b > DSP_MAX_B || v <= 0 || v > DSP_MAX_V || rank <= 0 || rank % 8 ||
+      rank > DSP_MAX_RANK || b * rank > 4096 || block <= 0 || block > 1024 || base_stride < v)
     return SV_EINVAL;
   if (confidence && (!pre_head || !conf_weight || h <= 0 || ps < h)) return SV_EINVAL;
   if (workspace_bytes < snowllm_dspark_markov_workspace_bytes(b, v, rank, block)) return SV_EINVAL;
@@ -229,8 +282,15 @@ SV_API int snowllm_dspark_markov(const void* base, const void* w1, const void* w
             confidence ? (int)h : 0, (int)dsp_nwg(v), fp32_bias != 0, 0};
   for (int j = 0; j < block; ++j) {
     a.j = j;
-    hipLaunchKernelGGL(dsp_markov_kernel, dim3((unsigned)a.nwg), dim3(DSP_NT), 0,
-                       (hipStream_t)stream, a);
+    if (b == 1)
+      hipLaunchKernelGGL(dsp_markov_kernel<1>, dim3((unsigned)a.nwg), dim3(DSP_NT), 0,
+                         (hipStream_t)stream, a);
+    else if (b <= 4)
+      hipLaunchKernelGGL(dsp_markov_kernel<4>, dim3((unsigned)a.nwg), dim3(DSP_NT), 0,
+                         (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL(dsp_markov_kernel<DSP_MAX_B>, dim3((unsigned)a.nwg), dim3(DSP_NT), 0,
+                         (hipStream_t)stream, a);
     SV_CHECK_LAUNCH();
   }
   return SV_OK;

@@ -38,8 +38,9 @@ def dspark_markov(base, w1, w2, anchor, block, *, pre_head=None, conf_weight=Non
     _chk(w1, "DSpark Markov W1", torch.bfloat16, v, rank)
     _chk(w2, "DSpark packed W2", torch.bfloat16, v, rank)
     _chk(anchor, "DSpark anchors", torch.int64, b)
-    if b > MAX_BATCH:
-        raise SnowLLMError(f"DSpark Markov head: at most {MAX_BATCH} requests per call")
+    if b > MAX_BATCH or b * rank > 4096:
+        raise SnowLLMError(f"DSpark Markov head: at most {MAX_BATCH} requests per call and "
+                           f"requests x rank <= 4096")
     h = ps = 0
     if confidence is not None:
         if pre_head is None or conf_weight is None:
