@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/_capi.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """ctypes binding of libsnowverify.so, the gfx950 verify-step kernel library.
 
 Mirrors the loading pattern of the reference's binding (snowllm/_capi.py:144-194, 821-855):

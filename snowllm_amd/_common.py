@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/ops/_common.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """Operator plumbing shared by the wrappers (mirrors snowllm/ops/_common.py:48-100).
 
 Tensors are validated before every call -- device, dtype, shape and layout -- and raw

@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/ops/attention_full.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """Paged GQA attention of a verify block (snowllm/ops/attention_full.py:120-177).
 
 KV pools use the reference's page layouts (tests/test_lfm2_dspark_reference.py:30-36):

@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/ops/dflash.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """DFlash 2 selector and acceptance (snowllm/ops/dflash.py:159-219): the candidate walk that
 proposes a draft path, and rejection sampling of a draft prefix."""
 import ctypes

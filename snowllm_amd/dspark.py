@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/ops/dspark.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """The DSpark Markov head operators with the reference's names and arguments
 (snowllm/ops/dspark.py:10-16, 53-77)."""
 import torch

@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/ops/embedding.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """Embedding gather and LM head operators with the reference's names and arguments
 (snowllm/ops/embedding.py:12-73): a bf16 or Q4_K embedding table, a bf16 or k-quant head.
 Shapes come from the active geometry (vocab_size, hidden)."""

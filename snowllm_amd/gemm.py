@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/ops/gemm.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """GGUF k-quant GEMM operators (snowllm/ops/gemm.py:130-163).
 
 Format ids follow the reference (ops/moe.py:189-190): 4 = Q4_K, 8 = Q8_0.

@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/ops/inference.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """Geometry-driven operator entry points (mirrors snowllm/ops/inference.py:10-104): weights are
 marshalled into the reference's _Weight descriptor and the shapes come from the active
 geometry. The weights hold this library's repacked layouts (KQuantProjWeight from

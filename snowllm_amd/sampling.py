@@ -1,3 +1,7 @@
+# SPDX-License-Identifier: Apache-2.0
+# The operator names, signatures, argument checks and error texts here follow snowllm/ops/sampling.py
+# (SPDX-FileCopyrightText: Copyright contributors to the SnowLLM project), which this
+# module keeps so that the reference's callers can use it unchanged.
 """Sampling operators: argmax, temperature/top-k/top-p probabilities, sampling.
 
 Signatures and argument meanings follow snowllm/ops/sampling.py:28-91.
