@@ -458,7 +458,8 @@ def bench_step(args, name):
         # on this step's measured costs
         heads = time_draft_heads(stream, V, k)
         kern.update(heads)
-        adaptive = adaptive_prefix(m, heads["dspark_markov (per block row)"]["us"] * k * 1e-6)
+        if not args.no_adaptive:
+            adaptive = adaptive_prefix(m, heads["dspark_markov (per block row)"]["us"] * k * 1e-6)
     # dominant single kernel per step (launch time x launches per step)
     single = {kk: v for kk, v in kern.items()
               if "+" not in kk and "us" in v and not v.get("outside_step")}
@@ -689,6 +690,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="config4", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-adaptive", action="store_true",
+                    help="leave out the adaptive-prefix cost profile (the profiler's runs at "
+                         "1-16 rows would mix into a kernel trace of the step)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only (one-GPU boxes); "

@@ -213,14 +213,24 @@ __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t
   }
   float sv[8];
   float cmax = -__builtin_huge_valf();
+  if (has_b && (pg + 2) * PAGE <= ctx) {
+    // both pages lie wholly in the context before the block: every key is visible (the same
+    // scores as the masked form below, without its per-key tests)
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int pos = (pg + (i >> 2)) * PAGE + 4 * kq + (i & 3);
-    bool vis = pos < L && (i < 4 || has_b);
-    if (vis && pos >= ctx) vis = (anc >> (pos - ctx)) & 1ull;
-    const float x = (i < 4 ? s0[i & 3] : s1[i & 3]) * qk_scale;
-    sv[i] = vis ? x : -__builtin_huge_valf();
-    cmax = sv[i] > cmax ? sv[i] : cmax;
+    for (int i = 0; i < 8; ++i) {
+      sv[i] = (i < 4 ? s0[i & 3] : s1[i & 3]) * qk_scale;
+      cmax = sv[i] > cmax ? sv[i] : cmax;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int pos = (pg + (i >> 2)) * PAGE + 4 * kq + (i & 3);
+      bool vis = pos < L && (i < 4 || has_b);
+      if (vis && pos >= ctx) vis = (anc >> (pos - ctx)) & 1ull;
+      const float x = (i < 4 ? s0[i & 3] : s1[i & 3]) * qk_scale;
+      sv[i] = vis ? x : -__builtin_huge_valf();
+      cmax = sv[i] > cmax ? sv[i] : cmax;
+    }
   }
   // Lazy rescaling: the row maximum (shared by the four lanes of a row, which hold different
   // keys of one P^T column) moves only when some score exceeds it by more than 2^RESCALE in
@@ -295,20 +305,29 @@ attn_split_kernel(AttnArgs a) {
   const int h = (blockIdx.x / a.S) % a.Hkv;
   const int b = blockIdx.x / (a.S * a.Hkv);
 
-  int L = a.lens[b];
-  if (L > a.table_stride * PAGE) L = a.table_stride * PAGE;  // never read past the table row
-  const int ctx = L - a.T;
-  const int n_pages = (L + PAGE - 1) / PAGE;
-  const int p0 = split * a.pages_per_split;
-  int p1 = p0 + a.pages_per_split;
-  if (p1 > n_pages) p1 = n_pages;
-
   // this lane's query row (column of S^T / O^T)
   const int r = w * 16 + col;
   const bool row_live = r < a.T * a.G;
   const int t = row_live ? r / a.G : 0;
   const int g = row_live ? r % a.G : 0;
   const int hq = h * a.G + g;
+  const int64_t m_row = (int64_t)b * a.T + t;
+  // The block ids of the split's first pages need no sequence length: they load with it, so
+  // that the page loads wait for one round trip instead of two (block table through the
+  // constant address space: scalar loads, which count on lgkmcnt and so never wait for the
+  // page loads in flight on vmcnt).
+  const int p0 = split * a.pages_per_split;
+  const cint32* trow = (const cint32*)(a.table + (int64_t)b * a.table_stride);
+  int pre[RING - 2];
+#pragma unroll
+  for (int i = 0; i < RING - 2; ++i)
+    pre[i] = trow[p0 + i < a.table_stride ? p0 + i : a.table_stride - 1];
+  int L = a.lens[b];
+  if (L > a.table_stride * PAGE) L = a.table_stride * PAGE;  // never read past the table row
+  const int ctx = L - a.T;
+  const int n_pages = (L + PAGE - 1) / PAGE;
+  int p1 = p0 + a.pages_per_split;
+  if (p1 > n_pages) p1 = n_pages;
   uint64_t anc;
   if (a.tree) anc = row_live ? a.tree[(int64_t)b * a.T + t] : 1ull;
   else anc = (t >= 63) ? ~0ull : ((2ull << t) - 1ull);
@@ -359,7 +378,6 @@ attn_split_kernel(AttnArgs a) {
     bf16x8 qb[DS];
     QkRaw<D> qraw;
     QkAux<D> qaux;
-    const int64_t m_row = (int64_t)b * a.T + t;
     if (a.proj) {
       // the block rows whose cache position falls in this split: K normalised and rotated,
       // K and V into the pools (wave 0, 16 rows per pass)
@@ -399,12 +417,13 @@ attn_split_kernel(AttnArgs a) {
     const int64_t block_bytes = page_bytes * a.Hkv;
     const uint8_t* kbase = (const uint8_t*)a.k_pool + h * page_bytes;
     const uint8_t* vbase = (const uint8_t*)a.v_pool + h * page_bytes;
-    // block table through the constant address space: scalar loads, which count on lgkmcnt
-    // and so never wait for the page loads in flight on vmcnt
-    const cint32* trow = (const cint32*)(a.table + (int64_t)b * a.table_stride);
     // pages past the split reload page p0 into a free slot (keeps the load count uniform)
     auto issue = [&](int pg, int slot_idx) {
-      const int64_t blk = trow[pg < p1 ? pg : p0];
+      const int pgc = pg < p1 ? pg : p0;
+      int64_t blk = pgc - p0 < RING - 2 ? pre[0] : trow[pgc];
+#pragma unroll
+      for (int i = 1; i < RING - 2; ++i)
+        if (pgc - p0 == i) blk = pre[i];
       dma_page<D, CPW>(kbase + blk * block_bytes, vbase + blk * block_bytes,
                        ring + slot_idx * G::BYTES, wv, NW, lane);
     };
@@ -454,11 +473,68 @@ attn_split_kernel(AttnArgs a) {
 }
 
 // Merge the splits: out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s. A block covers
-// MERGE_ROWS rows x MERGE_D columns of one (request, kv head, row tile); wave j computes the
-// split weights of row j, then thread (group sg, row, 4 columns) sums the splits s = sg mod
-// MERGE_SG, and the MERGE_SG partial sums are added in a fixed order.
-constexpr int MERGE_ROWS = 4, MERGE_D = 64, MERGE_SG = 4;
-constexpr int MERGE_THREADS = MERGE_ROWS * (MERGE_D / 4) * MERGE_SG;  // 256
+// MERGE_ROWS rows x MERGE_D columns of one (request, kv head, row tile). Wave sg sums the
+// splits s = sg mod MERGE_SG in increasing s, the MERGE_SG partial sums are added in wave
+// order, and wave j < MERGE_ROWS also computes the split weights of row j. Every wave issues
+// the loads of its first MERGE_PF splits before the weights are known, so that the partials
+// and the (m, l) pairs come back in one round trip.
+constexpr int MERGE_ROWS = 4, MERGE_D = 64, MERGE_SG = 8, MERGE_PF = 16;
+constexpr int MERGE_THREADS = MERGE_ROWS * (MERGE_D / 4) * MERGE_SG;  // 512
+
+// The split weights of one row (one wave): w[s] = 2^(m_s - M), 1 / sum_s w[s] l_s.
+__device__ __forceinline__ void merge_weights(const AttnArgs& a, int64_t pbase, int row,
+                                              float* w, float* inv_l, int lane) {
+  float M = -__builtin_huge_valf();
+  for (int s = lane; s < a.S; s += 64) M = fmaxf(M, a.part_ml[((pbase + s) * 16 + row) * 2]);
+  M = wave_max(M);
+  const float Ms = (M == -__builtin_huge_valf()) ? 0.f : M;
+  float lsum = 0.f;
+  for (int s = lane; s < a.S; s += 64) {
+    const float* ml = a.part_ml + ((pbase + s) * 16 + row) * 2;
+    const float ws = __builtin_amdgcn_exp2f(ml[0] - Ms);
+    w[s] = ws;
+    lsum += ws * ml[1];
+  }
+  lsum = wave_sum(lsum);
+  if (lane == 0) *inv_l = lsum > 0.f ? 1.0f / lsum : 0.f;
+}
+
+// acc (NV floatx4 of this thread's columns) += sum over this group's splits of w[s] * O_s, in
+// increasing s; po points at split sg's first column word, sstride = one group step.
+template <int NV>
+__device__ __forceinline__ void merge_group(const AttnArgs& a, const float* po, int64_t sstride,
+                                            const float* w, int sg, floatx4 (&pf)[MERGE_PF][NV],
+                                            floatx4 (&acc)[NV]) {
+  for (int s0 = sg;; s0 += MERGE_PF * MERGE_SG) {
+#pragma unroll
+    for (int k = 0; k < MERGE_PF; ++k) {
+      const int s = s0 + k * MERGE_SG;
+      if (s < a.S)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc[v] += w[s] * pf[k][v];
+    }
+    const int next = s0 + MERGE_PF * MERGE_SG;
+    if (next >= a.S) break;
+    // splits past this batch: the next MERGE_PF, all loads in flight
+    po += MERGE_PF * sstride;
+#pragma unroll
+    for (int k = 0; k < MERGE_PF; ++k)
+      if (next + k * MERGE_SG < a.S)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) pf[k][v] = *(const floatx4*)(po + k * sstride + 4 * v);
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void merge_prefetch(const AttnArgs& a, const float* po,
+                                               int64_t sstride, int sg,
+                                               floatx4 (&pf)[MERGE_PF][NV]) {
+#pragma unroll
+  for (int k = 0; k < MERGE_PF; ++k)
+    if (sg + k * MERGE_SG < a.S)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) pf[k][v] = *(const floatx4*)(po + k * sstride + 4 * v);
+}
 
 template <int D>
 __global__ void __launch_bounds__(MERGE_THREADS) attn_merge_kernel(AttnArgs a,
@@ -472,42 +548,17 @@ __global__ void __launch_bounds__(MERGE_THREADS) attn_merge_kernel(AttnArgs a,
   const int d0 = blockIdx.z * MERGE_D;
   const int tile = prog % a.NRT, h = (prog / a.NRT) % a.Hkv, b = prog / (a.NRT * a.Hkv);
   const int64_t pbase = (((int64_t)b * a.Hkv + h) * a.NRT + tile) * a.S;
-  {
-    const int row = row0 + wv;
-    float M = -__builtin_huge_valf();
-    for (int s = lane; s < a.S; s += 64) M = fmaxf(M, a.part_ml[((pbase + s) * 16 + row) * 2]);
-    M = wave_max(M);
-    const float Ms = (M == -__builtin_huge_valf()) ? 0.f : M;
-    float lsum = 0.f;
-    for (int s = lane; s < a.S; s += 64) {
-      const float* ml = a.part_ml + ((pbase + s) * 16 + row) * 2;
-      const float ws = __builtin_amdgcn_exp2f(ml[0] - Ms);
-      w[wv][s] = ws;
-      lsum += ws * ml[1];
-    }
-    lsum = wave_sum(lsum);
-    if (lane == 0) inv_l[wv] = lsum > 0.f ? 1.0f / lsum : 0.f;
-  }
-  __syncthreads();
   const int sg = wv, rr = lane >> 4, d4 = lane & 15;
   const int row = row0 + rr;
-  const float* po = a.part_o + (pbase * 16 + row) * D + d0 + 4 * d4;
   const int64_t sstride = (int64_t)16 * D * MERGE_SG;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  int s = sg;
-  po += (int64_t)sg * 16 * D;
-  for (; s + 3 * MERGE_SG < a.S; s += 4 * MERGE_SG, po += 4 * sstride) {
-    const floatx4 x0 = *(const floatx4*)(po);
-    const floatx4 x1 = *(const floatx4*)(po + sstride);
-    const floatx4 x2 = *(const floatx4*)(po + 2 * sstride);
-    const floatx4 x3 = *(const floatx4*)(po + 3 * sstride);
-    acc += w[rr][s] * x0;
-    acc += w[rr][s + MERGE_SG] * x1;
-    acc += w[rr][s + 2 * MERGE_SG] * x2;
-    acc += w[rr][s + 3 * MERGE_SG] * x3;
-  }
-  for (; s < a.S; s += MERGE_SG, po += sstride) acc += w[rr][s] * *(const floatx4*)po;
-  red[sg][rr][d4] = acc;
+  const float* po = a.part_o + ((pbase + sg) * 16 + row) * D + d0 + 4 * d4;
+  floatx4 pf[MERGE_PF][1];
+  merge_prefetch<1>(a, po, sstride, sg, pf);
+  if (wv < MERGE_ROWS) merge_weights(a, pbase, row0 + wv, w[wv], &inv_l[wv], lane);
+  __syncthreads();
+  floatx4 acc[1] = {{0.f, 0.f, 0.f, 0.f}};
+  merge_group<1>(a, po, sstride, w[rr], sg, pf, acc);
+  red[sg][rr][d4] = acc[0];
   __syncthreads();
   if (sg != 0) return;
   floatx4 v = red[0][rr][d4];
@@ -524,13 +575,13 @@ __global__ void __launch_bounds__(MERGE_THREADS) attn_merge_kernel(AttnArgs a,
 // The merge that also writes the output projection's operand workspace (D = 256: one head's
 // output is one 256-wide superblock of the projection's input row, so the projection can take
 // prepared operands instead of converting the bf16 output itself). A block covers MWS_ROWS
-// rows x all D columns of one (request, kv head, row tile); thread (group sg, row, word) sums
-// the splits s = sg mod MERGE_SG for 8 columns, and the MERGE_SG partial sums are added in a
-// fixed order: the same sums in the same order as attn_merge_kernel, so the same output bits.
+// rows x all D columns of one (request, kv head, row tile); wave sg sums the splits
+// s = sg mod MERGE_SG for 8 columns per thread, and the MERGE_SG partial sums are added in
+// wave order: the same sums in the same order as attn_merge_kernel, so the same output bits.
 // Workspace rows are the output rows b * T + t; rows past them are left as they are (the
 // GEMV reads none of their operands).
 constexpr int MWS_ROWS = 2;  // rows per block: two half waves
-constexpr int MWS_THREADS = MWS_ROWS * (256 / 8) * MERGE_SG;  // 256
+constexpr int MWS_THREADS = MWS_ROWS * (256 / 8) * MERGE_SG;  // 512
 
 template <int D>
 __global__ void __launch_bounds__(MWS_THREADS) attn_merge_ws_kernel(AttnArgs a,
@@ -546,47 +597,19 @@ __global__ void __launch_bounds__(MWS_THREADS) attn_merge_ws_kernel(AttnArgs a,
   const int row0 = blockIdx.y * MWS_ROWS;
   const int tile = prog % a.NRT, h = (prog / a.NRT) % a.Hkv, b = prog / (a.NRT * a.Hkv);
   const int64_t pbase = (((int64_t)b * a.Hkv + h) * a.NRT + tile) * a.S;
-  if (wv < MWS_ROWS) {
-    const int row = row0 + wv;
-    float M = -__builtin_huge_valf();
-    for (int s = lane; s < a.S; s += 64) M = fmaxf(M, a.part_ml[((pbase + s) * 16 + row) * 2]);
-    M = wave_max(M);
-    const float Ms = (M == -__builtin_huge_valf()) ? 0.f : M;
-    float lsum = 0.f;
-    for (int s = lane; s < a.S; s += 64) {
-      const float* ml = a.part_ml + ((pbase + s) * 16 + row) * 2;
-      const float ws_ = __builtin_amdgcn_exp2f(ml[0] - Ms);
-      w[wv][s] = ws_;
-      lsum += ws_ * ml[1];
-    }
-    lsum = wave_sum(lsum);
-    if (lane == 0) inv_l[wv] = lsum > 0.f ? 1.0f / lsum : 0.f;
-  }
-  __syncthreads();
-  // wave sg sums splits s = sg mod MERGE_SG; a row's 32 words sit in one half wave (the operand
-  // conversion reduces over it)
+  // a row's 32 words sit in one half wave (the operand conversion reduces over it)
   const int sg = wv, rr = lane >> 5, lw = lane & 31;
   const int row = row0 + rr;
-  const float* po = a.part_o + (pbase * 16 + row) * D + lw * 8;
   const int64_t sstride = (int64_t)16 * D * MERGE_SG;
-  floatx4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-  int s = sg;
-  po += (int64_t)sg * 16 * D;
-  for (; s + 3 * MERGE_SG < a.S; s += 4 * MERGE_SG, po += 4 * sstride) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const floatx4 x0 = *(const floatx4*)(po + u * sstride);
-      const floatx4 x1 = *(const floatx4*)(po + u * sstride + 4);
-      acc0 += w[rr][s + u * MERGE_SG] * x0;
-      acc1 += w[rr][s + u * MERGE_SG] * x1;
-    }
-  }
-  for (; s < a.S; s += MERGE_SG, po += sstride) {
-    acc0 += w[rr][s] * *(const floatx4*)po;
-    acc1 += w[rr][s] * *(const floatx4*)(po + 4);
-  }
-  red[sg][rr][lw][0] = acc0;
-  red[sg][rr][lw][1] = acc1;
+  const float* po = a.part_o + ((pbase + sg) * 16 + row) * D + lw * 8;
+  floatx4 pf[MERGE_PF][2];
+  merge_prefetch<2>(a, po, sstride, sg, pf);
+  if (wv < MWS_ROWS) merge_weights(a, pbase, row0 + wv, w[wv], &inv_l[wv], lane);
+  __syncthreads();
+  floatx4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  merge_group<2>(a, po, sstride, w[rr], sg, pf, acc);
+  red[sg][rr][lw][0] = acc[0];
+  red[sg][rr][lw][1] = acc[1];
   __syncthreads();
   if (sg != 0) return;  // wave 0 (a whole wave) finishes the block
   floatx4 v0 = red[0][rr][lw][0], v1 = red[0][rr][lw][1];
