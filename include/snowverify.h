@@ -539,6 +539,17 @@ int snowverify_norm_prep_moe(const float* pairs, const float* shared_out, int64_
                              void* x_out, const void* res_in, void* res_out, const void* gamma,
                              void* y_out, void* ws, int64_t M, int64_t H, float eps,
                              void* stream);
+/* The post-attention block of a MoE layer up to the experts in one launch, with the bits of
+ * snowverify_norm_prep (res_out, y_out, ws) + snowverify_dense_gemv (bf16 router [E (+1), H]
+ * repacked by snowverify_dense_shuffle; f32 logits [M, E (+1)]) + snowverify_moe_route_plan
+ * (weights/ids [M, topk], shared_w [M] or NULL for no shared expert, plan). res_out must not
+ * alias x or res_in. M <= 16; H a multiple of 512, <= 4096, M * (H + 8) * 2 <= 65536; E <= 256;
+ * M * topk <= 135. Library-owned counter: calls on one device must be stream-ordered. */
+int snowverify_norm_router_plan(const void* x, const void* res_in, void* res_out,
+                                const void* gamma, float eps, void* ws, void* y_out,
+                                const void* router, float* logits, int64_t M, int64_t H,
+                                int64_t E, int64_t topk, float* weights, int32_t* ids,
+                                float* shared_w, void* plan, void* stream);
 /* 16-bit weight GEMV: repack size, repack (wt 1 = fp16, 2 = bf16), and C = A W^T (fp16 weights
  * take the operand workspace, bf16 weights bf16 activations). M <= 16. */
 int64_t snowverify_dense_bytes(int64_t N, int64_t K);

@@ -199,6 +199,8 @@ _SIGS = [
     ("snowverify_moe_plan_bytes", c_int64, []),
     ("snowverify_moe_plan", c_int, [P, c_int64, c_int64, c_int64, c_int, P, S]),
     ("snowverify_moe_route_plan", c_int, [P, c_int64, c_int64, c_int64, c_int64, P, P, P, P, S]),
+    ("snowverify_norm_router_plan", c_int, [P] * 4 + [c_float] + [P] * 4 + [c_int64] * 4 +
+     [P] * 4 + [S]),
     ("snowverify_moe_gate_up", c_int, [c_int] + [P] * 7 + [c_int64] * 5 + [S]),
     ("snowverify_moe_down", c_int, [c_int] + [P] * 10 + [c_int64] * 4 + [S]),
     ("snowverify_moe_gate_up_down", c_int, [c_int] + [P] * 15 + [c_int64] * 5 + [S]),

@@ -434,6 +434,7 @@ attn_split_kernel(AttnArgs a) {
       // this lane's query row, normalised and rotated while the first pages load (angles of
       // sub-blocks past the first, when half > 32, load here behind the pages)
       uint4 qo[DS];
+      wait_vmcnt<(RING - 2) * CPW>();  // the row and its operands, not the pages behind them
       qk_norm_rope<D, FUSED_MAX_HS>(qraw, qaux, a.cosv + m_row * a.cs_stride, a.sinv + m_row * a.cs_stride,
                       a.rot_half, a.eps, kq, qo);
 #pragma unroll

@@ -120,6 +120,20 @@ __device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
   return ab > cd ? ab : cd;
 }
 
+__device__ __forceinline__ uint32_t wave_min_u32_dpp(uint32_t v) {
+  uint32_t o;
+  o = dpp_u32<DPP_QUAD_XOR1>(v); v = o < v ? o : v;
+  o = dpp_u32<DPP_QUAD_XOR2>(v); v = o < v ? o : v;
+  o = dpp_u32<DPP_HALF_MIRROR>(v); v = o < v ? o : v;
+  o = dpp_u32<DPP_MIRROR>(v); v = o < v ? o : v;
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  const uint32_t ab = a < b ? a : b, cd = c < d ? c : d;
+  return ab < cd ? ab : cd;
+}
+
 // Sum in a fixed order (pairs, quads, 8s, 16s, then rows 0 + 1 + 2 + 3).
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(v)));

@@ -403,32 +403,10 @@ __global__ void __launch_bounds__(WS * PPB * 64) gate_up_kernel(
 // ---------------------------------------------------------------------------------------
 constexpr int ROUTE_THREADS = 1024;  // 16 waves: one per row (M <= 16), four for the plan
 
-// 64-bit maximum over the wave on the VALU: DPP within each 16-lane row, row broadcasts 15 and
-// 31 across rows, then lane 63 holds the result. No scalar round trips, no branches.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint64_t dpp_max_u64_step(uint64_t v) {
-  const uint32_t h = (uint32_t)(v >> 32), l = (uint32_t)v;
-  const uint32_t nh = (uint32_t)__builtin_amdgcn_update_dpp((int)h, (int)h, CTRL, ROW_MASK, 0xF, false);
-  const uint32_t nl = (uint32_t)__builtin_amdgcn_update_dpp((int)l, (int)l, CTRL, ROW_MASK, 0xF, false);
-  const uint64_t n = ((uint64_t)nh << 32) | nl;
-  return n > v ? n : v;
-}
-__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
-  v = dpp_max_u64_step<DPP_QUAD_XOR1, 0xF>(v);
-  v = dpp_max_u64_step<DPP_QUAD_XOR2, 0xF>(v);
-  v = dpp_max_u64_step<DPP_HALF_MIRROR, 0xF>(v);
-  v = dpp_max_u64_step<DPP_MIRROR, 0xF>(v);
-  v = dpp_max_u64_step<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
-  v = dpp_max_u64_step<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
-  const uint32_t h = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-  const uint32_t l = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-  return ((uint64_t)h << 32) | l;
-}
-
 // Softmax over E <= 256 logits (expert e = lane + 64 i), then the top-k in descending order
 // with ties to the lower expert id: lane k ends with the k-th pick's probability and id. Each
-// lane sorts its four candidates once; a round takes the wave maximum of the lanes' heads as
-// (ordered key, ~expert id) and the winning lane drops its head.
+// lane sorts its four candidates once; a round takes the wave maximum of the lanes' heads in
+// the order (ordered key, then lower expert id) and the winning lane drops its head.
 __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, int topk, int lane,
                                           float& my_p, int& my_id, float& ksum) {
   float v[4];
@@ -455,7 +433,8 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
   // sort the lane's candidates: key descending, then id ascending (a five-comparator network
   // under that total order)
   auto cswap = [&](int a, int b) {
-    const bool sw = key[b] > key[a] || (key[b] == key[a] && id[b] < id[a]);
+    // bitwise, not short-circuit: no branches
+    const bool sw = (key[b] > key[a]) | ((key[b] == key[a]) & (id[b] < id[a]));
     const uint32_t ka = key[a], ia = id[a];
     key[a] = sw ? key[b] : key[a];
     id[a] = sw ? id[b] : id[a];
@@ -463,12 +442,19 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
     id[b] = sw ? ia : id[b];
   };
   cswap(0, 1); cswap(2, 3); cswap(0, 2); cswap(1, 3); cswap(1, 2);
-  my_p = 0.f;
   my_id = -1;
+  float my_v = 0.f;  // the pick's logit (lane k: the k-th pick)
   for (int k = 0; k < topk; ++k) {
-    const uint64_t best = wave_max_u64_dpp(((uint64_t)key[0] << 32) | (0xffffffffu - id[0]));
-    const int e = (int)(0xffffffffu - (uint32_t)best);
-    const float ve = ord_key_to_float((uint32_t)(best >> 32));
+    // the largest head key, then (ties) the lowest expert id among the lanes holding it: the
+    // maximum of (key, ~id) with a 32-bit reduction in the common case of one such lane
+    const uint32_t km = wave_max_u32_dpp(key[0]);
+    const uint64_t tied = __ballot(key[0] == km);
+    int e;
+    if (__popcll(tied) == 1)
+      e = __builtin_amdgcn_readlane((int)id[0], (int)__builtin_ctzll(tied));
+    else
+      e = (int)wave_min_u32_dpp(key[0] == km ? id[0] : 0xffffffffu);
+    const float ve = ord_key_to_float(km);
     const bool pop = lane == (e & 63);
     key[0] = pop ? key[1] : key[0];
     id[0] = pop ? id[1] : id[0];
@@ -477,13 +463,15 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
     key[2] = pop ? key[3] : key[2];
     id[2] = pop ? id[3] : id[2];
     key[3] = pop ? 0u : key[3];
-    const float p = __expf(ve - mx) / sum;
-    my_p = lane == k ? p : my_p;
+    my_v = lane == k ? ve : my_v;
     my_id = lane == k ? e : my_id;
   }
+  // the picks' probabilities, every lane at once (the same operations as one at a time)
+  my_p = lane < topk ? __expf(my_v - mx) / sum : 0.f;
   ksum = 0.f;
-  for (int k = 0; k < topk; ++k)
-    ksum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), k));
+#pragma unroll
+  for (int k = 0; k < 16; ++k)
+    if (k < topk) ksum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), k));
 }
 
 // Plan from ids_s[M * topk] in LDS; all ROUTE_THREADS threads call it.
@@ -586,6 +574,209 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_plan_kernel(const int32_t* 
   if (t < M * topk) ids_s[t] = ids[t];
   __syncthreads();
   build_plan(ids_s, M, topk, E, shared, mask, slot_of, wave_cnt, plan);
+}
+
+// ---------------------------------------------------------------------------------------
+// The post-attention block of a MoE layer up to the experts in one launch: residual update +
+// RMSNorm + the experts' operand conversion (norm_prep_kernel), the router GEMV over the
+// normalised rows (dense_gemv, bf16 weights) and the routing + plan (moe_route_plan_kernel).
+// One workgroup per 16 router columns; every workgroup normalises all M rows itself into LDS
+// (the same sums in the same order as norm_prep_kernel: the thread of word t of a row is
+// lane t % 64 of the row's wave t / 64), with its router weights in flight behind the rows, and
+// workgroup j < 16 also writes row j of res_out, y_out and the operand workspace. The logits go out with
+// device-scope stores; the last workgroup to count itself in (an atomic counter, no wait)
+// reads them back with device-scope loads and routes and plans the block, then clears the
+// counter for the next launch. Every result has the bits of the three separate launches.
+// Launches on one device must be stream-ordered (library-owned counter).
+// ---------------------------------------------------------------------------------------
+constexpr int NR_THREADS = 1024;  // 16 waves: one per routed row; the GEMV takes dense_gemv's
+constexpr int NR_MAXP = 8;        // row passes held in registers (M <= 8 * 8192 / H)
+__device__ uint32_t g_router_arrive;
+
+__global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ res_out, const uint16_t* __restrict__ gamma,
+    uint16_t* __restrict__ y_out, void* __restrict__ ws, size_t tile_bytes, float eps,
+    const u32x4* __restrict__ router, float* __restrict__ logits, int M, int H, int E, int topk,
+    float* __restrict__ weights, int32_t* __restrict__ ids, float* __restrict__ shared_w,
+    MoePlan* __restrict__ plan) {
+  // router rows: the E experts, then the shared expert's gate when shared_w is given
+  extern __shared__ __attribute__((aligned(16))) uint8_t nr_lds[];  // y rows, H + 8 apart
+  __shared__ float part_ss[NR_MAXP][NR_THREADS / 64];
+  __shared__ floatx4 part[NR_THREADS / 64][64];
+  __shared__ uint32_t last;
+  __shared__ int32_t ids_s[16 * 16];
+  __shared__ uint32_t mask[256];
+  __shared__ int32_t slot_of[256];
+  __shared__ int32_t wave_cnt[4];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int kq = lane >> 4, r = lane & 15;
+  const int S = H / QK, N = E + (shared_w ? 1 : 0);
+  const int ystride = H + 8;  // bf16 elements between the LDS rows (a row's 16 B reads spread)
+  uint16_t* ylds = (uint16_t*)nr_lds;
+  // this workgroup's router tile: dense_gemv's waves (8 from 8 superblocks, else 4) take
+  // superblocks s = wave, wave + NWG, ...
+  const int NWG = S >= 8 ? 8 : 4;
+  const int tile = blockIdx.x;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(router + (int64_t)tile * S * 8 * 64), 0, S * 8 * 64 * 16, 0x00020000);
+  u32x4 wb[8];
+
+  // residual + RMSNorm of every row: RP rows per pass, H / 8 threads per row; every pass's
+  // words are loaded before any sum (one round trip), the passes' sums meet in one barrier
+  const int wpr = H / 8, RP = NR_THREADS / wpr, wpw = wpr / 64;  // words, rows, waves per row
+  const int tr = t % wpr, rsub = t / wpr;
+  const int npass = (M + RP - 1) / RP;  // passes holding rows < M (<= NR_MAXP: host-checked)
+  const u32x4 gv = *(const u32x4*)(gamma + (int64_t)tr * 8);
+  u32x4 xv[NR_MAXP], rv[NR_MAXP];
+#pragma unroll
+  for (int p = 0; p < NR_MAXP; ++p) {
+    const int row = p * RP + rsub;
+    xv[p] = rv[p] = u32x4{0u, 0u, 0u, 0u};
+    if (p < npass && row < M) {
+      const int64_t off = (int64_t)row * H + (int64_t)tr * 8;
+      xv[p] = *(const u32x4*)(x + off);
+      if (residual) rv[p] = *(const u32x4*)(residual + off);
+    }
+  }
+  // the router weights behind the rows (the norm needs only the rows)
+  if (wv < NWG && wv < S)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wb[j] = bload4(wr, lane * 16, (uint32_t)((wv * 8 + j) * 64 * 16));
+#pragma unroll
+  for (int p = 0; p < NR_MAXP; ++p) {
+    if (p >= npass) break;  // uniform
+    const int row = p * RP + rsub;
+    if (residual && row < M) xv[p] = add_bf16_words(xv[p], rv[p]);
+    const uint32_t vw[4] = {xv[p].x, xv[p].y, xv[p].z, xv[p].w};
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = __uint_as_float(vw[i] << 16), b = __uint_as_float(vw[i] & 0xffff0000u);
+      ss = __builtin_fmaf(a, a, ss);
+      ss = __builtin_fmaf(b, b, ss);
+    }
+    ss = wave_sum_dpp(ss);
+    if (lane == 0) part_ss[p][wv] = ss;
+  }
+  __syncthreads();
+  const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
+  auto normalise = [&](const u32x4& v, float inv, uint32_t (&yo)[4], float (&y)[8]) {
+    const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      yo[i] = pack_bf16x2(__uint_as_float(vw[i] << 16) * inv * __uint_as_float(gw[i] << 16),
+                          __uint_as_float(vw[i] & 0xffff0000u) * inv *
+                              __uint_as_float(gw[i] & 0xffff0000u));
+      y[2 * i] = __uint_as_float(yo[i] << 16);
+      y[2 * i + 1] = __uint_as_float(yo[i] & 0xffff0000u);
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < NR_MAXP; ++p) {
+    if (p >= npass) break;  // uniform
+    const int row = p * RP + rsub;
+    float tot = 0.f;
+    for (int w = 0; w < wpw; ++w) tot += part_ss[p][rsub * wpw + w];
+    const float inv = __frsqrt_rn(tot / (float)H + eps);
+    float y[8];
+    uint32_t yo[4];
+    normalise(xv[p], inv, yo, y);
+    if (row < M) *(u32x4*)(ylds + row * ystride + tr * 8) = u32x4{yo[0], yo[1], yo[2], yo[3]};
+    // workgroup j writes row j's results (the 16 rows of the operand tile over 16 workgroups;
+    // the first workgroup writes them all when there are fewer)
+    const bool own = gridDim.x >= 16 ? row == (int)blockIdx.x : blockIdx.x == 0;
+    if (own && row < M) {
+      const int64_t off = (int64_t)row * H + (int64_t)tr * 8;
+      if (res_out) *(u32x4*)(res_out + off) = xv[p];
+      if (y_out) *(u32x4*)(y_out + off) = u32x4{yo[0], yo[1], yo[2], yo[3]};
+    }
+    if (own && row < 16) word_operand(y, tr, row, ws, tile_bytes, H / QK, true);  // wave-uniform
+  }
+  // the tile's rows past the passes get zero operands, as norm_prep_kernel writes them
+  for (int row0 = npass * RP; row0 < 16; row0 += RP) {  // uniform
+    const int row = row0 + rsub;
+    const bool own = gridDim.x >= 16 ? row == (int)blockIdx.x : blockIdx.x == 0;
+    float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (own && row < 16) word_operand(y, tr, row, ws, tile_bytes, H / QK, true);
+  }
+  __syncthreads();  // the rows are in LDS
+
+  // router GEMV from the LDS rows (dense_gemv's bf16 form: the same products and sums)
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = wv; wv < NWG && s < S; s += NWG) {
+    if (s != wv)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wb[j] = bload4(wr, lane * 16, (uint32_t)((s * 8 + j) * 64 * 16));
+    u32x4 xa[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      xa[j] = r < M ? *(const u32x4*)(ylds + r * ystride + s * QK + j * 32 + kq * 8)
+                    : u32x4{0u, 0u, 0u, 0u};
+    floatx4 sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[j]),
+                                                   __builtin_bit_cast(bf16x8, wb[j]), sb, 0, 0, 0);
+    acc += sb * floatx4{1.f, 1.f, 1.f, 1.f};
+  }
+  if (wv < NWG) part[wv][lane] = acc;
+  __syncthreads();
+  if (wv == 0) {
+    floatx4 v = part[0][lane];
+    for (int ww = 1; ww < NWG; ++ww) v += part[ww][lane];
+    const int n = tile * TILE_N + (lane & 15);
+    const int rb = 4 * (lane >> 4);
+    if (n < N)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (rb + i < M)
+          __hip_atomic_store(logits + (int64_t)(rb + i) * N + n, v[i], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // count in once this workgroup's logits have been written; the last one routes and plans
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (t == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(&g_router_arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == gridDim.x - 1 ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!last) return;
+  if (t == 0) __hip_atomic_store(&g_router_arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // every workgroup's logits, back through LDS (the y rows are no longer needed)
+  float* lg = (float*)nr_lds;
+  constexpr int LG_PER = (16 * 257 + NR_THREADS - 1) / NR_THREADS;  // all loads in flight
+  float lv[LG_PER];
+#pragma unroll
+  for (int k = 0; k < LG_PER; ++k) {
+    const int i = t + k * NR_THREADS;
+    lv[k] = i < M * N ? __hip_atomic_load(logits + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                      : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < LG_PER; ++k)
+    if (t + k * NR_THREADS < M * N) lg[t + k * NR_THREADS] = lv[k];
+  if (t < 256) mask[t] = 0u;
+  __syncthreads();
+  // moe_route_plan_kernel's routing, wave w on row w
+  for (int row = wv; row < M; row += NR_THREADS / 64) {
+    const float* l = lg + row * N;
+    const float gate = shared_w ? l[E] : 0.f;
+    float my_p, ksum;
+    int my_id;
+    route_row(l, E, topk, lane, my_p, my_id, ksum);
+    if (lane < topk) {
+      weights[row * topk + lane] = my_p / ksum;
+      ids[row * topk + lane] = my_id;
+      ids_s[row * topk + lane] = my_id;
+    }
+    if (lane == 0 && shared_w) shared_w[row] = 1.0f / (1.0f + __expf(-gate));
+  }
+  __syncthreads();
+  build_plan(ids_s, M, topk, E, shared_w != nullptr, mask, slot_of, wave_cnt, plan);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -913,6 +1104,35 @@ SV_API int snowverify_norm_prep_moe(const float* pairs, const float* shared_out,
   if (x_out && (x_out == res_out || x_out == y_out)) return SV_EINVAL;
   return launch_norm_prep(nullptr, MoeSource{pairs, shared_out, (uint16_t*)x_out, (int)topk},
                           res_in, res_out, gamma, y_out, ws, M, H, eps, Sx(stream));
+}
+
+// snowverify_norm_prep (x + res_in -> res_out, RMSNorm * gamma -> y_out and the operand
+// workspace ws) + snowverify_dense_gemv (bf16 router [E (+1), H] repacked, over the normalised
+// rows, f32 logits [M, E (+1)]) + snowverify_moe_route with the plan, in one launch and with
+// their bits. shared_w null: no shared expert (E router rows). M <= 16, H a multiple of 512 up
+// to 4096 with M * (H + 8) * 2 <= 64 KiB, E <= 256, M * topk <= 135. Uses a library-owned
+// counter: calls on one device must be stream-ordered.
+SV_API int snowverify_norm_router_plan(const void* x, const void* res_in, void* res_out,
+                                       const void* gamma, float eps, void* ws, void* y_out,
+                                       const void* router, float* logits, int64_t M, int64_t H,
+                                       int64_t E, int64_t topk, float* weights, int32_t* ids,
+                                       float* shared_w, void* plan, void* stream) {
+  if (!x || !gamma || !ws || !router || !logits || !weights || !ids || !plan || M <= 0 ||
+      M > 16 || H <= 0 || H % 512 || H > 4096 || E <= 0 || E > 256 || topk <= 0 || topk > 16 ||
+      topk > E || M * topk > 135)
+    return SV_EINVAL;
+  if (res_out && (res_out == x || res_out == res_in)) return SV_EINVAL;  // read by every block
+  const int64_t N = E + (shared_w ? 1 : 0);
+  const size_t lds = std::max((size_t)(M * (H + 8) * 2), (size_t)(M * N * 4));
+  if (lds > 65536 || (M + 8192 / H - 1) / (8192 / H) > NR_MAXP) return SV_ENOTSUP;
+  hipLaunchKernelGGL(norm_router_plan_kernel, dim3((unsigned)((N + TILE_N - 1) / TILE_N)),
+                     dim3(NR_THREADS), lds, Sx(stream), (const uint16_t*)x,
+                     (const uint16_t*)res_in, (uint16_t*)res_out, (const uint16_t*)gamma,
+                     (uint16_t*)y_out, ws, xprep_tile_bytes(H / 256), eps, (const u32x4*)router,
+                     logits, (int)M, (int)H, (int)E, (int)topk, weights, ids, shared_w,
+                     (MoePlan*)plan);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
 }
 
 // Bytes of a repacked 16-bit weight [N, K] (N padded to a multiple of 16).

@@ -156,6 +156,26 @@ def moe_route_plan(logits, E, topk, weights, ids, shared_w, plan):
           "moe_route_plan")
 
 
+def norm_router_plan(x, gamma, ws, eps, router, logits, topk, weights, ids, shared_w, plan, *,
+                     res_in=None, res_out=None, y_out=None):
+    """norm_prep + the bf16 router GEMV (dense_gemv) + moe_route_plan in one launch, with their
+    bits: logits [M, E (+1 with shared_w)] f32."""
+    M, H = x.shape
+    _chk(x, "x", torch.bfloat16, M, H)
+    _chk(gamma, "gamma", torch.bfloat16, H)
+    for t, n in ((res_in, "res_in"), (res_out, "res_out"), (y_out, "y_out")):
+        if t is not None:
+            _chk(t, n, torch.bfloat16, M, H)
+    E = logits.shape[1] - (1 if shared_w is not None else 0)
+    _chk(logits, "router logits", torch.float32, M, logits.shape[1])
+    _chk(weights, "routing weights", torch.float32, M, topk)
+    _chk(ids, "routing ids", torch.int32, M, topk)
+    check(lib.snowverify_norm_router_plan(_p(x), _p(res_in), _p(res_out), _p(gamma), eps, _p(ws),
+                                          _p(y_out), _p(router), _p(logits), M, H, E, topk,
+                                          _p(weights), _p(ids), _p(shared_w), _p(plan),
+                                          _stream()), "norm_router_plan")
+
+
 def moe_experts(fmt, gu, dn, sh_gu, sh_dn, plan, ws, weights, shared_w, act, pairs, shared_out,
                 out, M, topk, E, H, F):
     """gu/dn/sh_gu/sh_dn: (quant, meta) pairs of the stacked expert weights."""

@@ -194,6 +194,11 @@ class VerifyModel:
         torch.cuda.synchronize()
         self.head_wt = Lops.WT_F16   # or WT_BF16, or HEAD_KQUANT with self.head_fmt
         self.head_fmt = 0
+        # MoE layers: post-attention norm, router and routing/plan in one launch where the
+        # fused kernel takes the shape (False: the three separate launches, the same bits)
+        self.fuse_router = bool(c.moe and c.hidden % 512 == 0 and c.hidden <= 4096 and
+                                c.block * (c.hidden + 8) * 2 <= 65536 and
+                                c.block * (c.experts + 1) * 4 <= 65536)
         self.embed_q4k = False       # True: self.embed holds Q4_K blocks [V, H / 256 * 144]
         self.lm_head_raw = None
         if weights is None:
@@ -388,13 +393,20 @@ class VerifyModel:
                                   self.o, T, H, c.heads * c.head_dim, self.ws_a)
             # feed-forward block
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
-            if c.moe:
+            if c.moe and self.fuse_router:
+                # post-attention norm + router GEMV + routing and plan: one launch
+                Lops.norm_router_plan(self.o, lw.post_norm, self.ws_h2, c.eps, lw.router,
+                                      self.router_logits, c.topk, self.route_w, self.route_ids,
+                                      self.shared_w, self.plan, res_in=res_in, res_out=res_out,
+                                      y_out=self.h2)
+            elif c.moe:
                 Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,
                                res_out=res_out, y_out=self.h2)
                 Lops.dense_gemv(Lops.WT_BF16, lw.router, self.h2, self.router_logits, T,
                                 c.experts + 1, H)
                 Lops.moe_route_plan(self.router_logits, c.experts, c.topk, self.route_w,
                                     self.route_ids, self.shared_w, self.plan)
+            if c.moe:
                 if record_slots is not None:
                     record_slots[i:i + 1].copy_(self.plan[:4].view(torch.int32))
                 ns = T * c.topk + 1

@@ -198,3 +198,50 @@ def test_norm_prep_moe_equals_combine_then_norm(gpu, M, shared):
         outs.append((x, res_out, y, ws))
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("M,Hd,shared", [(9, 2048, True), (1, 2048, True), (15, 2048, False),
+                                         (11, 512, True), (5, 4096, True)])
+def test_norm_router_plan_equals_separate_launches(gpu, M, Hd, shared):
+    """Post-attention norm + router GEMV + routing/plan in one launch (every workgroup
+    normalises the rows itself; the last one to finish routes and plans) gives the bits of
+    norm_prep, dense_gemv and moe_route_plan, on two launches in a row."""
+    from snowllm_amd import layers as L
+    print(f"norm+router+plan M={M} H={Hd} shared={shared}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(M * 7 + Hd)
+    N = E + (1 if shared else 0)
+    x = torch.randn(M, Hd, device="cuda", generator=g).bfloat16()
+    res = (torch.randn(M, Hd, device="cuda", generator=g) * 4).bfloat16()
+    gamma = (1 + 0.1 * torch.randn(Hd, device="cuda", generator=g)).bfloat16()
+    router = (torch.randn(N, Hd, device="cuda", generator=g) / Hd ** 0.5).bfloat16()
+    rw = L.dense_shuffle(router)
+    from snowllm_amd import ops
+    nws = ops.gemm_kquant_a_ws_bytes(M, Hd)
+
+    def bufs():
+        return dict(res_out=torch.zeros(M, Hd, dtype=torch.bfloat16, device="cuda"),
+                    y=torch.zeros(M, Hd, dtype=torch.bfloat16, device="cuda"),
+                    ws=torch.zeros(nws, dtype=torch.uint8, device="cuda"),
+                    logits=torch.zeros(M, N, device="cuda"),
+                    w=torch.zeros(M, K, device="cuda"),
+                    ids=torch.zeros(M, K, dtype=torch.int32, device="cuda"),
+                    sw=torch.zeros(M, device="cuda") if shared else None,
+                    plan=torch.zeros(L.MOE_PLAN_BYTES, dtype=torch.uint8, device="cuda"))
+
+    a = bufs()
+    L.norm_prep(x, gamma, a["ws"], 1e-6, res_in=res, res_out=a["res_out"], y_out=a["y"])
+    L.dense_gemv(L.WT_BF16, rw, a["y"], a["logits"], M, N, Hd)
+    L.moe_route_plan(a["logits"], E, K, a["w"], a["ids"], a["sw"], a["plan"])
+    outs = []
+    for _ in range(2):
+        b = bufs()
+        L.norm_router_plan(x, gamma, b["ws"], 1e-6, rw, b["logits"], K, b["w"], b["ids"], b["sw"],
+                           b["plan"], res_in=res, res_out=b["res_out"], y_out=b["y"])
+        outs.append(b)
+    torch.cuda.synchronize()
+    for b in outs:
+        for key in ("res_out", "y", "ws", "logits", "w", "ids") + (("sw",) if shared else ()):
+            assert torch.equal(a[key], b[key]), key
+        # the plan, but for its epoch (the last word: every plan gets a new one)
+        assert torch.equal(a["plan"][:-4], b["plan"][:-4])
+    assert L.parse_plan(outs[1]["plan"])["n_slots"] == L.parse_plan(a["plan"])["n_slots"]
