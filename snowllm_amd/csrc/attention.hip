@@ -575,14 +575,14 @@ __global__ void __launch_bounds__(MERGE_THREADS) attn_merge_kernel(AttnArgs a,
 
 // The merge that also writes the output projection's operand workspace (D = 256: one head's
 // output is one 256-wide superblock of the projection's input row, so the projection can take
-// prepared operands instead of converting the bf16 output itself). A block covers MWS_ROWS
-// rows x all D columns of one (request, kv head, row tile); wave sg sums the splits
-// s = sg mod MERGE_SG for 8 columns per thread, and the MERGE_SG partial sums are added in
-// wave order: the same sums in the same order as attn_merge_kernel, so the same output bits.
+// prepared operands instead of converting the bf16 output itself). A block covers one row x
+// all D columns of one (request, kv head, row tile) -- one block per row puts twice the blocks
+// of two rows per block on the CUs; half wave sg sums the splits s = sg mod MERGE_SG for 8
+// columns per thread, and the MERGE_SG partial sums are added in group order: the same sums in
+// the same order as attn_merge_kernel, so the same output bits.
 // Workspace rows are the output rows b * T + t; rows past them are left as they are (the
 // GEMV reads none of their operands).
-constexpr int MWS_ROWS = 2;  // rows per block: two half waves
-constexpr int MWS_THREADS = MWS_ROWS * (256 / 8) * MERGE_SG;  // 512
+constexpr int MWS_THREADS = (256 / 8) * MERGE_SG;  // 256: one row, a split group per half wave
 
 template <int D>
 __global__ void __launch_bounds__(MWS_THREADS) attn_merge_ws_kernel(AttnArgs a,
@@ -590,43 +590,43 @@ __global__ void __launch_bounds__(MWS_THREADS) attn_merge_ws_kernel(AttnArgs a,
                                                                    void* __restrict__ ws,
                                                                    size_t tile_bytes) {
   static_assert(D == 256, "one head per superblock");
-  __shared__ float w[MWS_ROWS][SPLITS_MAX];
-  __shared__ float inv_l[MWS_ROWS];
-  __shared__ floatx4 red[MERGE_SG][MWS_ROWS][D / 8][2];
+  __shared__ float w[SPLITS_MAX];
+  __shared__ float inv_l;
+  __shared__ floatx4 red[MERGE_SG][D / 8][2];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int prog = blockIdx.x;  // (b, h, tile)
-  const int row0 = blockIdx.y * MWS_ROWS;
+  const int row = blockIdx.y;
   const int tile = prog % a.NRT, h = (prog / a.NRT) % a.Hkv, b = prog / (a.NRT * a.Hkv);
+  const int rg = tile * 16 + row;
+  if (rg >= a.T * a.G) return;  // a padding row: no output, no operands (uniform)
   const int64_t pbase = (((int64_t)b * a.Hkv + h) * a.NRT + tile) * a.S;
-  // a row's 32 words sit in one half wave (the operand conversion reduces over it)
-  const int sg = wv, rr = lane >> 5, lw = lane & 31;
-  const int row = row0 + rr;
+  // half wave sg sums split group sg; a row's 32 words sit in one half wave (the operand
+  // conversion reduces over it)
+  const int sg = tid >> 5, lw = tid & 31;
   const int64_t sstride = (int64_t)16 * D * MERGE_SG;
   const float* po = a.part_o + ((pbase + sg) * 16 + row) * D + lw * 8;
   floatx4 pf[MERGE_PF][2];
   merge_prefetch<2>(a, po, sstride, sg, pf);
-  if (wv < MWS_ROWS) merge_weights(a, pbase, row0 + wv, w[wv], &inv_l[wv], lane);
+  if (wv == 0) merge_weights(a, pbase, row, w, &inv_l, lane);
   __syncthreads();
   floatx4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  merge_group<2>(a, po, sstride, w[rr], sg, pf, acc);
-  red[sg][rr][lw][0] = acc[0];
-  red[sg][rr][lw][1] = acc[1];
+  merge_group<2>(a, po, sstride, w, sg, pf, acc);
+  red[sg][lw][0] = acc[0];
+  red[sg][lw][1] = acc[1];
   __syncthreads();
-  if (sg != 0) return;  // wave 0 (a whole wave) finishes the block
-  floatx4 v0 = red[0][rr][lw][0], v1 = red[0][rr][lw][1];
+  if (wv != 0) return;  // wave 0 (a whole wave; its upper half repeats the lower) finishes
+  floatx4 v0 = red[0][lw][0], v1 = red[0][lw][1];
 #pragma unroll
   for (int j = 1; j < MERGE_SG; ++j) {
-    v0 += red[j][rr][lw][0];
-    v1 += red[j][rr][lw][1];
+    v0 += red[j][lw][0];
+    v1 += red[j][lw][1];
   }
-  const int rg = tile * 16 + row;
-  const bool live = rg < a.T * a.G;
-  const float il = inv_l[rr];
-  const int t = live ? rg / a.G : 0, g = live ? rg % a.G : 0;
+  const float il = inv_l;
+  const int t = rg / a.G, g = rg % a.G;
   const int hq = h * a.G + g;
   const uint32_t yo[4] = {pack_bf16x2(v0[0] * il, v0[1] * il), pack_bf16x2(v0[2] * il, v0[3] * il),
                           pack_bf16x2(v1[0] * il, v1[1] * il), pack_bf16x2(v1[2] * il, v1[3] * il)};
-  if (live)
+  if (lane < 32)
     *(u32x4*)(out + (((int64_t)b * a.T + t) * a.Hq + hq) * D + lw * 8) =
         u32x4{yo[0], yo[1], yo[2], yo[3]};
   float y[8];
@@ -636,7 +636,7 @@ __global__ void __launch_bounds__(MWS_THREADS) attn_merge_ws_kernel(AttnArgs a,
     y[2 * i + 1] = __uint_as_float(yo[i] & 0xffff0000u);
   }
   kq::word_operand(y, hq * 32 + lw, (int64_t)b * a.T + t, ws, tile_bytes,
-                   (int64_t)a.Hq * D / kq::QK, live);
+                   (int64_t)a.Hq * D / kq::QK, lane < 32);
 }
 
 inline int n_row_tiles(int T, int G) { return (T * G + 15) / 16; }
@@ -785,8 +785,8 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
     SV_CHECK_LAUNCH();
     if (out_ws) {
       const size_t tb = kq::xprep_tile_bytes(num_heads * head_size / kq::QK);
-      hipLaunchKernelGGL(attn_merge_ws_kernel<256>, dim3(mgrid.x, 16 / MWS_ROWS),
-                         dim3(MWS_THREADS), 0, s, a, (uint16_t*)out, out_ws, tb);
+      hipLaunchKernelGGL(attn_merge_ws_kernel<256>, dim3(mgrid.x, 16), dim3(MWS_THREADS), 0, s,
+                         a, (uint16_t*)out, out_ws, tb);
     } else {
       hipLaunchKernelGGL(attn_merge_kernel<256>, mgrid, dim3(MERGE_THREADS), 0, s, a,
                          (uint16_t*)out);
