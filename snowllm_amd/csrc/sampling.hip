@@ -987,10 +987,10 @@ SV_API int snowllm_draft_reject(const float* p, const int64_t* ids, const int64_
 //   2. numerators e = exp(x / T - M) with the row maximum M, the slice's fixed-point sum and
 //      the draft token's numerator; the request's last workgroup to finish (a counter)
 //      forms every row's Z and the accepted prefix;
-//   3. the workgroups of the row where the prefix stops form the residual max(p - q, 0) (p at
-//      the bonus row) and its fixed-point sums per 4 * FA_NT-logit sub-chunk; the request's
-//      last one finds the sub-chunk holding floor(u R), counts its prefix there and writes
-//      the outputs.
+//   3. one workgroup per 4 * FA_NT-logit sub-chunk of the row where the prefix stops forms
+//      the residual max(p - q, 0) (p at the bonus row) and its fixed-point sums; the
+//      request's last one finds the sub-chunk holding floor(u R) (a wave's prefix scan over
+//      the sub-chunk sums), counts its prefix there and writes the outputs.
 // Nothing waits for another workgroup. A counter advances by exactly FA_QUANTUM per launch
 // (each participant adds 1, one adds the quantum's rest), so the last arriver is the one
 // whose add completes the quantum; nothing is ever reset. Statistics are written with
@@ -1223,7 +1223,7 @@ __device__ ResidualRow fa_residual(const FaArgs& a, int r, int first, int64_t* s
 
 __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
   __shared__ uint64_t red[FA_NT / WAVE];
-  __shared__ uint64_t s_sub[2][FA_NT / WAVE][FA_SUBCHUNKS];
+  __shared__ uint64_t s_sub[2][FA_NT / WAVE];
   __shared__ uint64_t buf[FA_NT];
   __shared__ int64_t s_cand[Q_STAGE];
   __shared__ float s_q[Q_STAGE];
@@ -1231,15 +1231,24 @@ __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
   __shared__ float s_zf;
   __shared__ int s_slice, s_sub_i, s_use_p;
   __shared__ uint64_t s_base, s_target;
+  // one workgroup per sub-chunk c of slice w (the thread's logits k in [4c, 4c + 4) of the
+  // slice): four times the workgroups of one per slice, a quarter of the arithmetic each
   const int P = a.P, width = a.width, length = width - 1, V = a.V;
-  const int w = blockIdx.x % P, r = blockIdx.x / P;
+  const int w = (blockIdx.x / FA_SUBCHUNKS) % P, r = blockIdx.x / (FA_SUBCHUNKS * P);
+  const int c = blockIdx.x % FA_SUBCHUNKS;
   const int t = threadIdx.x, lo = w * FA_SLICE;
   const int first = g_fa_first[r];
   const int row = r * width + first;
   const float* x = a.logits + (int64_t)row * V;
   const float T = row_temperature(a.temperature, row);
-  float v[FA_E];
-  fa_load_slice(x, lo, V, T, v);
+  float v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int i = lo + (4 * c + k) * FA_NT + t;
+    v[k] = x[i < V ? i : V - 1];
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = __fdiv_rn(v[k], T);
   const float M = fa_row_max(row, P);
   if (t < WAVE) {
     const uint64_t z = fa_row_zsum(row, P);
@@ -1247,15 +1256,15 @@ __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
   }
   ResidualRow rr = fa_residual(a, r, first, s_cand, s_q, s_bits);  // (synchronises the block)
   const float Zf = s_zf;
-  // residual and p of every logit, summed per sub-chunk (sub-chunk c = k in [4c, 4c + 4)).
-  // An identity q row is read here, all of the thread's values at once.
-  float qv[FA_E];
-  int64_t cv[FA_E];
+  // residual and p of the sub-chunk's logits, summed. An identity q row is read here, all of
+  // the thread's values at once.
+  float qv[4];
+  int64_t cv[4];
   const bool direct_q = rr.q && !rr.bits && rr.subtract;
   if (direct_q) {
 #pragma unroll
-    for (int k = 0; k < FA_E; ++k) {
-      const int i = lo + k * FA_NT + t;
+    for (int k = 0; k < 4; ++k) {
+      const int i = lo + (4 * c + k) * FA_NT + t;
       const bool in_q = i < rr.q_width;
       qv[k] = in_q ? rr.q[i] : 0.0f;
       cv[k] = in_q ? rr.cand[i] : -1;
@@ -1269,12 +1278,11 @@ __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
     return d > 0.0f ? d : 0.0f;
   };
   const int wv = t / WAVE, l = t % WAVE;
-#pragma unroll
-  for (int c = 0; c < FA_SUBCHUNKS; ++c) {
+  {
     uint64_t rs = 0, ps = 0;
 #pragma unroll
-    for (int k = 4 * c; k < 4 * c + 4; ++k) {
-      const int i = lo + k * FA_NT + t;
+    for (int k = 0; k < 4; ++k) {
+      const int i = lo + (4 * c + k) * FA_NT + t;
       const int ii = i < V ? i : V - 1;
       const float e = canon_exp(__fsub_rn(v[k], M));
       const float p = Zf > 0.0f ? canon_div(e, Zf) : 0.0f;
@@ -1286,18 +1294,17 @@ __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
     rs = wave_sum_u64(rs);
     ps = wave_sum_u64(ps);
     if (l == 0) {
-      s_sub[0][wv][c] = rs;
-      s_sub[1][wv][c] = ps;
+      s_sub[0][wv] = rs;
+      s_sub[1][wv] = ps;
     }
   }
   __syncthreads();
-  if (t < 2 * FA_SUBCHUNKS) {
-    const int kind = t / FA_SUBCHUNKS, c = t % FA_SUBCHUNKS;
+  if (t < 2) {
     uint64_t s = 0;
-    for (int q = 0; q < FA_NT / WAVE; ++q) s += s_sub[kind][q][c];
-    dev_store(kind ? &g_fa_psub[r][w][c] : &g_fa_rsub[r][w][c], s);
+    for (int q = 0; q < FA_NT / WAVE; ++q) s += s_sub[t][q];
+    dev_store(t ? &g_fa_psub[r][w][c] : &g_fa_rsub[r][w][c], s);
   }
-  if (!fa_last_arrival(&g_fa_cnt[1][r], P, w == 0)) return;
+  if (!fa_last_arrival(&g_fa_cnt[1][r], P * FA_SUBCHUNKS, w == 0 && c == 0)) return;
   // the request's last workgroup: #{k : prefix(k) <= floor(u R)} over the row; every
   // sub-chunk sum read at once, one per thread
   __shared__ uint64_t s_all[2][FA_P_MAX * FA_SUBCHUNKS];
@@ -1307,33 +1314,54 @@ __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
                           : dev_load(&g_fa_rsub[r][e / FA_SUBCHUNKS][e % FA_SUBCHUNKS]);
   }
   __syncthreads();
-  if (t == 0) {
+  if (t < WAVE) {
+    // wave 0: R, the target floor(u R) and the first sub-chunk whose running sum exceeds it
+    // (lane l holds sub-chunks 2l and 2l + 1; integer sums, so the same R and prefix as a
+    // sequential walk)
     const int n = P * FA_SUBCHUNKS;
-    uint64_t R = 0;
-    for (int e = 0; e < n; ++e) R += s_all[0][e];
+    const int e0 = 2 * t, e1 = 2 * t + 1;
+    uint64_t a0 = e0 < n ? s_all[0][e0] : 0, a1 = e1 < n ? s_all[0][e1] : 0;
+    uint64_t R = wave_sum_u64(a0 + a1);
     int use_p = 0;
-    if (R == 0) {
+    if (R == 0) {  // (uniform)
       use_p = 1;
-      for (int e = 0; e < n; ++e) R += s_all[1][e];
+      a0 = e0 < n ? s_all[1][e0] : 0;
+      a1 = e1 < n ? s_all[1][e1] : 0;
+      R = wave_sum_u64(a0 + a1);
     }
     const uint64_t target = canon_scale_floor(a.uniform[(int64_t)r * width + width - 1], R);
-    uint64_t pre = 0;
-    int si = 0, ci = 0;
-    bool found = false;
-    for (si = 0; si < P && !found; ++si)
-      for (ci = 0; ci < FA_SUBCHUNKS; ++ci) {
-        const uint64_t s = s_all[use_p][si * FA_SUBCHUNKS + ci];
-        if (pre + s > target) {
-          found = true;
-          break;
-        }
-        pre += s;
+    const uint64_t pair = a0 + a1;
+    uint64_t incl = pair;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+      const uint32_t lo32 = (uint32_t)__shfl_up((int)(uint32_t)incl, d, WAVE);
+      const uint32_t hi32 = (uint32_t)__shfl_up((int)(uint32_t)(incl >> 32), d, WAVE);
+      if (t >= d) incl += ((uint64_t)hi32 << 32) | lo32;
+    }
+    const uint64_t excl = incl - pair;
+    const uint64_t b0 = __ballot(e0 < n && excl + a0 > target);
+    const uint64_t b1 = __ballot(e1 < n && excl + pair > target);
+    const uint64_t any = b0 | b1;
+    if (t == 0) {
+      s_target = target;
+      s_use_p = use_p;
+    }
+    if (any == 0) {
+      if (t == 0) {
+        s_slice = P;
+        s_sub_i = FA_SUBCHUNKS;
+        s_base = R;
       }
-    s_slice = found ? si - 1 : P;
-    s_sub_i = ci;
-    s_base = pre;
-    s_target = target;
-    s_use_p = use_p;
+    } else {
+      const int L = (int)__builtin_ctzll(any);
+      const bool at0 = (b0 >> L) & 1ull;
+      if (t == L) {
+        const int e = at0 ? e0 : e1;
+        s_slice = e / FA_SUBCHUNKS;
+        s_sub_i = e % FA_SUBCHUNKS;
+        s_base = at0 ? excl : excl + a0;
+      }
+    }
   }
   __syncthreads();
   int64_t pick = V - 1;  // past every prefix: the last index (clamp)
@@ -1439,7 +1467,7 @@ SV_API int snowverify_accept_reject(const float* logits, const float* temperatur
   const int P = fa_slices(vocab);
   FaArgs a{logits, temperature, drafts, cand, q, slots, valid, uniform, out, accepted,
            (int)vocab, (int)width, P, q_width};
-  const dim3 rows((unsigned)(b * width * P)), reqs((unsigned)(b * P));
+  const dim3 rows((unsigned)(b * width * P)), reqs((unsigned)(b * P * FA_SUBCHUNKS));
   hipLaunchKernelGGL(fa_max_kernel, rows, dim3(FA_NT), 0, S(stream), a);
   SV_CHECK_LAUNCH();
   hipLaunchKernelGGL(fa_sum_kernel, rows, dim3(FA_NT), 0, S(stream), a);

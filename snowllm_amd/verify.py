@@ -506,12 +506,14 @@ class Acceptance:
         """Run the selector: drafts, candidate ids and q for this step; block_ids [k + 1], if
         given, receives anchor + drafts (the verify block's input ids)."""
         s = self.sel
+        if block_ids is not None:
+            # the walk writes the drafts straight into the block's ids (after the anchor), and
+            # the acceptance reads them there: no copy in the step
+            self.drafts = block_ids[1:].view(1, self.T - 1)
         ops.dflash.select_path(s["hp"], s["logits"], s["pred"], s["succ"], s["anchor"],
                                self.drafts, self.sel_scratch, temperature=s["temperature"],
                                uniform=s["uniform"], slots=self.slot, candidate_ids=self.qid,
                                probabilities=self.q)
-        if block_ids is not None:
-            block_ids[1:].copy_(self.drafts.view(-1))
         return self.drafts
 
     def __call__(self, logits):
