@@ -1017,6 +1017,11 @@ __device__ uint64_t g_fa_rsub[FA_ROWS][FA_P_MAX][FA_SUBCHUNKS];
 __device__ uint64_t g_fa_psub[FA_ROWS][FA_P_MAX][FA_SUBCHUNKS];
 __device__ uint64_t g_fa_amax[FA_ROWS][FA_P_MAX];
 __device__ uint64_t g_fa_cnt[3][FA_ROWS];       // per request: stage 2, stage 3, greedy
+// the first level of two-level arrivals: per row (stage 2, greedy) or per slice (stage 3), a
+// counter per 128-byte line, so that the many workgroups of a launch finishing together do not
+// all queue on one address
+constexpr int FA_LINE = 16;  // uint64 per 128-byte line
+__device__ __attribute__((aligned(128))) uint64_t g_fa_cnt1[3][FA_ROWS * FA_P_MAX][FA_LINE];
 
 template <class T>
 __device__ __forceinline__ void dev_store(T* p, T v) {
@@ -1029,6 +1034,8 @@ __device__ __forceinline__ T dev_load(T* p) {
 
 // This workgroup's arrival at a request's counter of n participants (lead: the one that
 // adds the rest of the quantum). True in every thread of the workgroup that arrived last.
+// Device-scope atomics on one address complete one after another, so a launch's many
+// workgroups count in two levels (fa_last_arrival2).
 __device__ bool fa_last_arrival(uint64_t* cnt, int n, bool lead) {
   __shared__ uint32_t s_last;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores have completed
@@ -1041,6 +1048,17 @@ __device__ bool fa_last_arrival(uint64_t* cnt, int n, bool lead) {
   }
   __syncthreads();
   return s_last != 0;
+}
+
+// Two levels: the last of n1 workgroups at cnt1 goes on to cnt2 as one of its n2
+// participants; true in the workgroup that arrives last there. lead1 / lead2 add the quanta's
+// rests. Every participant's stores completed before its first-level add, and each level's
+// last arrival saw the count of everything before it, so the final workgroup's device-scope
+// loads, issued after its second add returned, see every participant's stores.
+__device__ bool fa_last_arrival2(uint64_t* cnt1, int n1, bool lead1, uint64_t* cnt2, int n2,
+                                 bool lead2) {
+  if (!fa_last_arrival(cnt1, n1, lead1)) return false;
+  return fa_last_arrival(cnt2, n2, lead2);
 }
 
 struct FaArgs {
@@ -1133,7 +1151,7 @@ __global__ void __launch_bounds__(FA_NT) fa_sum_kernel(FaArgs a) {
   }
   sum = block_sum_u64<FA_NT>(sum, red);
   if (t == 0) dev_store(&g_fa_sum[row][w], sum);
-  if (!fa_last_arrival(&g_fa_cnt[0][r], width * P, j == 0 && w == 0)) return;
+  if (!fa_last_arrival2(g_fa_cnt1[0][row], P, w == 0, &g_fa_cnt[0][r], width, j == 0)) return;
   // the request's last workgroup: u_j q(d_j) >= p(d_j) stops the accepted prefix. Every
   // draft row's sums and numerator are read at once, one per thread.
   __shared__ uint64_t s_rs[64][FA_P_MAX];
@@ -1304,7 +1322,9 @@ __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
     for (int q = 0; q < FA_NT / WAVE; ++q) s += s_sub[t][q];
     dev_store(t ? &g_fa_psub[r][w][c] : &g_fa_rsub[r][w][c], s);
   }
-  if (!fa_last_arrival(&g_fa_cnt[1][r], P * FA_SUBCHUNKS, w == 0 && c == 0)) return;
+  if (!fa_last_arrival2(g_fa_cnt1[1][r * FA_P_MAX + w], FA_SUBCHUNKS, c == 0, &g_fa_cnt[1][r], P,
+                        w == 0))
+    return;
   // the request's last workgroup: #{k : prefix(k) <= floor(u R)} over the row; every
   // sub-chunk sum read at once, one per thread
   __shared__ uint64_t s_all[2][FA_P_MAX * FA_SUBCHUNKS];
@@ -1425,7 +1445,7 @@ __global__ void __launch_bounds__(FA_NT) fa_greedy_kernel(FaArgs a) {
   }
   best = block_max_u64<FA_NT>(best, red);
   if (t == 0) dev_store(&g_fa_amax[row][w], best);
-  if (!fa_last_arrival(&g_fa_cnt[2][r], width * P, j == 0 && w == 0)) return;
+  if (!fa_last_arrival2(g_fa_cnt1[2][row], P, w == 0, &g_fa_cnt[2][r], width, j == 0)) return;
   __shared__ uint64_t s_keys[64][FA_P_MAX];
   for (int i = t; i < width * P; i += FA_NT)
     s_keys[i / P][i % P] = dev_load(&g_fa_amax[r * width + i / P][i % P]);
