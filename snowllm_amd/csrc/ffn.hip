@@ -640,10 +640,15 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
       if (residual) rv[p] = *(const u32x4*)(residual + off);
     }
   }
-  // the router weights behind the rows (the norm needs only the rows)
-  if (wv < NWG && wv < S)
+  // the router weights behind the rows (the norm needs only the rows); every wave issues the
+  // same eight loads (out of the buffer's range, so reading nothing, in the waves without a
+  // superblock) so that the rows' wait below is vmcnt(8) in every wave
+  {
+    const uint32_t wvo = wv < NWG && wv < S ? (uint32_t)lane * 16 : 0x80000000u;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) wb[j] = bload4(wr, lane * 16, (uint32_t)((wv * 8 + j) * 64 * 16));
+    for (int j = 0; j < 8; ++j) wb[j] = bload4(wr, wvo, (uint32_t)((wv * 8 + j) * 64 * 16));
+  }
+  __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));  // vmcnt(8): the rows, not the weights
 #pragma unroll
   for (int p = 0; p < NR_MAXP; ++p) {
     if (p >= npass) break;  // uniform
