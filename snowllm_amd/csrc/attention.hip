@@ -158,8 +158,7 @@ constexpr float RESCALE = 8.0f;  // p = 2^(s - m) stays <= 2^8 between rescales
 // multiplied once per tile. XBAR: a wave of a mixed workgroup that computes its own S^T takes
 // part in the same barrier. Every wave of a workgroup makes the same number of barrier calls.
 template <int D, int DH, bool SPLIT_S = false, bool XBAR = false>
-__device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t* sa,
-                                             const uint8_t* sb, bool has_b,
+__device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t* sa, bool has_b,
                                              const bf16x8 (&qb)[D / 32], int pg, int L, int ctx,
                                              uint64_t anc, float qk_scale, int kq, int col,
                                              int dhalf, floatx4 (*xch)[64] = nullptr) {
@@ -167,10 +166,28 @@ __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t
   constexpr int DS = D / 32, DT = D / 16 / DH;
   constexpr int NK = SPLIT_S ? 1 : 2;  // pages whose S^T this wave computes
   static_assert(!SPLIT_S || DH == 2, "S^T is split between the two waves of a tile");
-  // every LDS read of the chunk is issued before the first MFMA (V's latency then hides behind
-  // the S products and the softmax)
+  const uint8_t* sb = sa + G::BYTES;  // the chunk's second page: the next ring slot
+  // V^T operands first: one ds_read2st64_b64 per d tile reads the same 8 bytes (keys 4kq..4kq+3
+  // at one d) of both slots, G::BYTES apart, into the x,y (page A) and z,w (page B) halves of
+  // the MFMA's A operand. The compiler does not count these reads, so they are issued before
+  // its own K reads (LDS reads complete in order: its waits for K then also cover them) and an
+  // explicit wait precedes their use.
+  static_assert(G::BYTES % 512 == 0 && G::BYTES / 512 + (DT * 2 * 16 * 8) / 512 <= 255,
+                "ds_read2st64 offsets");
+  u32x4 vr[DT];
+  {
+    const uint32_t v0 = (uint32_t)(uintptr_t)(const lds_void*)(sa + G::KBYTES) +
+                        kq * (G::VGROUP + G::VPAD) + (dhalf * DT * 16 + col) * 8;
+    uint32_t va[4];
+#pragma unroll
+    for (int i = 0; i < 4 && i < DT; ++i) va[i] = v0 + i * 128;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      asm volatile("ds_read2st64_b64 %0, %1 offset0:%2 offset1:%3"
+                   : "=v"(vr[dt])
+                   : "v"(va[dt & 3]), "i"(dt >> 2), "i"((dt >> 2) + G::BYTES / 512));
+  }
   u32x4 kr[NK][DS];
-  u32x2 va[DT], vb[DT];
 #pragma unroll
   for (int ds = 0; ds < DS; ++ds) {
     const int off = ((2 * ds + (kq >> 1)) * PAGE + col) * 32 + (kq & 1) * 16;
@@ -180,12 +197,6 @@ __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t
       kr[0][ds] = *(const u32x4*)(sa + off);
       kr[NK - 1][ds] = *(const u32x4*)(sb + off);
     }
-  }
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    const int off = G::KBYTES + kq * (G::VGROUP + G::VPAD) + ((dhalf * DT + dt) * 16 + col) * 8;
-    va[dt] = *(const u32x2*)(sa + off);
-    vb[dt] = *(const u32x2*)(sb + off);
   }
   __builtin_amdgcn_sched_barrier(0);
   floatx4 sk[NK];
@@ -211,27 +222,26 @@ __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t
     s0 = sk[0];
     s1 = sk[NK - 1];
   }
+  // raw scores (masked keys -inf); the softmax scale goes into the exponent's fma, and the
+  // maximum of the raw scores times the (positive) scale is the maximum of the scaled ones
   float sv[8];
-  float cmax = -__builtin_huge_valf();
   if (has_b && (pg + 2) * PAGE <= ctx) {
     // both pages lie wholly in the context before the block: every key is visible (the same
     // scores as the masked form below, without its per-key tests)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      sv[i] = (i < 4 ? s0[i & 3] : s1[i & 3]) * qk_scale;
-      cmax = sv[i] > cmax ? sv[i] : cmax;
-    }
+    for (int i = 0; i < 8; ++i) sv[i] = i < 4 ? s0[i & 3] : s1[i & 3];
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int pos = (pg + (i >> 2)) * PAGE + 4 * kq + (i & 3);
       bool vis = pos < L && (i < 4 || has_b);
       if (vis && pos >= ctx) vis = (anc >> (pos - ctx)) & 1ull;
-      const float x = (i < 4 ? s0[i & 3] : s1[i & 3]) * qk_scale;
-      sv[i] = vis ? x : -__builtin_huge_valf();
-      cmax = sv[i] > cmax ? sv[i] : cmax;
+      sv[i] = vis ? (i < 4 ? s0[i & 3] : s1[i & 3]) : -__builtin_huge_valf();
     }
   }
+  float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                     fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+  cmax *= qk_scale;
   // Lazy rescaling: the row maximum (shared by the four lanes of a row, which hold different
   // keys of one P^T column) moves only when some score exceeds it by more than 2^RESCALE in
   // the exp2 domain; otherwise p <= 2^RESCALE and nothing is rescaled. The decision is
@@ -249,26 +259,33 @@ __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t
     st.l *= alpha;
     st.m = m_new;
   }
-  const float msafe = (st.m == -__builtin_huge_valf()) ? 0.f : st.m;
+  const float nm = (st.m == -__builtin_huge_valf()) ? 0.f : -st.m;
   float p[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    p[i] = __builtin_amdgcn_exp2f(sv[i] - msafe);
+    p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[i], qk_scale, nm));
     st.l += p[i];
   }
-  // P^T as a bf16 pair (hi + lo residual): ~16 significant bits through the MFMA
-  float plo[8];
+  // P^T as a bf16 pair through the MFMA, ~16 significant bits: hi = p truncated to its upper
+  // 16 bits (the packed pair is a byte permute of two values), lo = p - hi (exact in fp32),
+  // rounded to bf16
+  uint32_t ph[4], pl[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) plo[i] = p[i] - bf16_to_f32(f32_to_bf16(p[i]));
-  const u32x4 pw = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
-                    pack_bf16x2(p[6], p[7])};
-  const u32x4 pwl = {pack_bf16x2(plo[0], plo[1]), pack_bf16x2(plo[2], plo[3]),
-                     pack_bf16x2(plo[4], plo[5]), pack_bf16x2(plo[6], plo[7])};
-  const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
-  const bf16x8 pbl = __builtin_bit_cast(bf16x8, pwl);
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t a = __float_as_uint(p[2 * j]), b = __float_as_uint(p[2 * j + 1]);
+    ph[j] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+    pl[j] = pack_bf16x2(p[2 * j] - __uint_as_float(a & 0xffff0000u),
+                        p[2 * j + 1] - __uint_as_float(b & 0xffff0000u));
+  }
+  const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{ph[0], ph[1], ph[2], ph[3]});
+  const bf16x8 pbl = __builtin_bit_cast(bf16x8, u32x4{pl[0], pl[1], pl[2], pl[3]});
+  // the V^T reads have completed (and the registers are not used before this point)
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) asm volatile("" : "+v"(vr[dt]));
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
-    const bf16x8 vt = __builtin_bit_cast(bf16x8, u32x4{va[dt].x, va[dt].y, vb[dt].x, vb[dt].y});
+    const bf16x8 vt = __builtin_bit_cast(bf16x8, vr[dt]);
     floatx4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pb, st.o[dt], 0, 0, 0);
     st.o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pbl, o, 0, 0, 0);
   }
@@ -458,7 +475,7 @@ attn_split_kernel(AttnArgs a) {
         issue(pg + RING - 2, prev);
         issue(pg + RING - 1, prev + 1);
         attend_chunk<D, DHW, MIXED && DHW == 2, MIXED && DHW == 1>(
-            st, ring + slot * G::BYTES, ring + (slot + 1) * G::BYTES, pg + 1 < p1, qb, pg, L, ctx,
+            st, ring + slot * G::BYTES, pg + 1 < p1, qb, pg, L, ctx,
             anc, a.qk_scale, kq, col, dhalf, xch[MIXED ? w : 0]);
         slot = slot == RING - 2 ? 0 : slot + 2;
       }
