@@ -474,37 +474,41 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
     if (k < topk) ksum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), k));
 }
 
-// Plan from ids_s[M * topk] in LDS; all ROUTE_THREADS threads call it.
-__device__ __forceinline__ void build_plan(const int32_t* ids_s, int M, int topk, int E, int shared,
-                                          uint32_t* mask, int32_t* slot_of, int32_t* wave_cnt,
-                                          MoePlan* __restrict__ plan) {
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  for (int p = t; p < M * topk; p += blockDim.x) {
-    const int e = ids_s[p];
-    if (e >= 0 && e < E) atomicOr(&mask[e], 1u << (p / topk));
+// Plan from the expert row masks (mask[e] bit r: block row r is routed to expert e; complete
+// and visible to every thread) and the picks ids_s[M * topk] in LDS; ep_prev = g_moe_epoch,
+// loaded by the caller. Every wave takes the four ballots of the 256 expert flags itself, so
+// slots need no exchange between waves: waves 0-3 write the expert slots, waves 4-7 the (row,
+// pick) lists, waves 8+ the shared expert's rows, all at once. Needs ROUTE_THREADS threads.
+__device__ __forceinline__ void plan_from_masks(const int32_t* ids_s, int M, int topk, int E,
+                                               int shared, const uint32_t* mask, uint32_t ep_prev,
+                                               MoePlan* __restrict__ plan) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  uint32_t mk[4];
+  uint64_t bal[4];
+  int cnt[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    mk[i] = lane + 64 * i < E ? mask[lane + 64 * i] : 0u;
+    bal[i] = __ballot(mk[i] != 0u);
+    cnt[i] = __popcll(bal[i]);
   }
-  __syncthreads();
-  bool used = false;
-  int before = 0;
+  const int n_routed = cnt[0] + cnt[1] + cnt[2] + cnt[3];
+  const uint64_t below = (1ull << lane) - 1ull;
   if (w < 4) {
-    used = t < E && mask[t] != 0u;
-    const uint64_t bal = __ballot(used);
-    before = __popcll(bal & ((1ull << lane) - 1ull));
-    if (lane == 0) wave_cnt[w] = __popcll(bal);
-  }
-  __syncthreads();
-  const int n_routed = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
-  if (w < 4) {
+    // expert e = t: its slot is the number of used experts below it
     int off = 0;
-    for (int ww = 0; ww < w; ++ww) off += wave_cnt[ww];
-    slot_of[t] = used ? off + before : -1;
-    if (used) {
-      plan->slot_expert[off + before] = t;
-      plan->slot_rows[off + before] = __popc(mask[t]);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) off += i < w ? cnt[i] : 0;
+    const uint32_t me = w == 0 ? mk[0] : w == 1 ? mk[1] : w == 2 ? mk[2] : mk[3];
+    const uint64_t bw = w == 0 ? bal[0] : w == 1 ? bal[1] : w == 2 ? bal[2] : bal[3];
+    if (me != 0u) {
+      const int sl = off + __popcll(bw & below);
+      plan->slot_expert[sl] = t;
+      plan->slot_rows[sl] = __popc(me);
     }
     if (t == 0) {
-      uint32_t ep = g_moe_epoch + 1u;
-      ep = ep ? ep : 1u;
+      const uint32_t ep = (ep_prev + 1u) != 0u ? ep_prev + 1u : 1u;  // skips 0
       g_moe_epoch = ep;
       plan->epoch = ep;
       plan->n_routed = n_routed;
@@ -514,23 +518,26 @@ __device__ __forceinline__ void build_plan(const int32_t* ids_s, int M, int topk
       }
       plan->n_slots = n_routed + (shared ? 1 : 0);
     }
-  }
-  __syncthreads();
-  // compact row lists: a row's position in its slot = routed rows of the expert before it
-  for (int p = t; p < M * topk; p += blockDim.x) {
-    const int e = ids_s[p];
+  } else if (w < 8) {
+    // pick p: its row's position in the slot = rows routed to the expert before it
+    const int p = t - 256;
+    const int e = p < M * topk ? ids_s[p] : -1;
     if (e >= 0 && e < E) {
-      const int r = p / topk, sl = slot_of[e];
+      const int g = e >> 6, r = p / topk;
+      const uint64_t bg = g == 0 ? bal[0] : g == 1 ? bal[1] : g == 2 ? bal[2] : bal[3];
+      const int sl = (g > 0 ? cnt[0] : 0) + (g > 1 ? cnt[1] : 0) + (g > 2 ? cnt[2] : 0) +
+                     __popcll(bg & ((1ull << (e & 63)) - 1ull));
       const int pos = __popc(mask[e] & ((1u << r) - 1u));
       plan->row_of[sl][pos] = r;
       plan->pair_of[sl][pos] = p;
     }
-  }
-  if (shared)
-    for (int r = t; r < M; r += blockDim.x) {
+  } else if (shared) {
+    const int r = t - 512;
+    if (r < M) {
       plan->row_of[n_routed][r] = r;
       plan->pair_of[n_routed][r] = -1;
     }
+  }
 }
 
 __global__ void __launch_bounds__(ROUTE_THREADS) moe_route_plan_kernel(
@@ -539,11 +546,11 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_route_plan_kernel(
     MoePlan* __restrict__ plan) {
   __shared__ int32_t ids_s[16 * 16];
   __shared__ uint32_t mask[256];
-  __shared__ int32_t slot_of[256];
-  __shared__ int32_t wave_cnt[4];
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const uint32_t ep_prev = plan ? g_moe_epoch : 0u;
   if (t < 256) mask[t] = 0u;
+  __syncthreads();
   if (w < M) {
     const float* l = logits + (int64_t)w * stride;
     const float gate = shared_w ? l[E] : 0.f;
@@ -554,12 +561,13 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_route_plan_kernel(
       weights[w * topk + lane] = my_p / ksum;
       ids[w * topk + lane] = my_id;
       ids_s[w * topk + lane] = my_id;
+      if (my_id >= 0 && my_id < E) atomicOr(&mask[my_id], 1u << w);
     }
     if (lane == 0 && shared_w) shared_w[w] = 1.0f / (1.0f + __expf(-gate));
   }
   if (!plan) return;
   __syncthreads();
-  build_plan(ids_s, M, topk, E, shared_w != nullptr, mask, slot_of, wave_cnt, plan);
+  plan_from_masks(ids_s, M, topk, E, shared_w != nullptr, mask, ep_prev, plan);
 }
 
 __global__ void __launch_bounds__(ROUTE_THREADS) moe_plan_kernel(const int32_t* __restrict__ ids,
@@ -567,13 +575,15 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_plan_kernel(const int32_t* 
                                                                 MoePlan* __restrict__ plan) {
   __shared__ int32_t ids_s[16 * 16];
   __shared__ uint32_t mask[256];
-  __shared__ int32_t slot_of[256];
-  __shared__ int32_t wave_cnt[4];
   const int t = threadIdx.x;
+  const uint32_t ep_prev = g_moe_epoch;
   if (t < 256) mask[t] = 0u;
-  if (t < M * topk) ids_s[t] = ids[t];
+  const int e = t < M * topk ? ids[t] : -1;
+  if (t < M * topk) ids_s[t] = e;
   __syncthreads();
-  build_plan(ids_s, M, topk, E, shared, mask, slot_of, wave_cnt, plan);
+  if (e >= 0 && e < E) atomicOr(&mask[e], 1u << (t / topk));
+  __syncthreads();
+  plan_from_masks(ids_s, M, topk, E, shared, mask, ep_prev, plan);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -607,8 +617,6 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
   __shared__ uint32_t last;
   __shared__ int32_t ids_s[16 * 16];
   __shared__ uint32_t mask[256];
-  __shared__ int32_t slot_of[256];
-  __shared__ int32_t wave_cnt[4];
   const int t = threadIdx.x, lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
   const int kq = lane >> 4, r = lane & 15;
@@ -765,6 +773,7 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
   for (int k = 0; k < LG_PER; ++k)
     if (t + k * NR_THREADS < M * N) lg[t + k * NR_THREADS] = lv[k];
   if (t < 256) mask[t] = 0u;
+  const uint32_t ep_prev = g_moe_epoch;
   __syncthreads();
   // moe_route_plan_kernel's routing, wave w on row w
   for (int row = wv; row < M; row += NR_THREADS / 64) {
@@ -777,11 +786,12 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
       weights[row * topk + lane] = my_p / ksum;
       ids[row * topk + lane] = my_id;
       ids_s[row * topk + lane] = my_id;
+      if (my_id >= 0 && my_id < E) atomicOr(&mask[my_id], 1u << row);
     }
     if (lane == 0 && shared_w) shared_w[row] = 1.0f / (1.0f + __expf(-gate));
   }
   __syncthreads();
-  build_plan(ids_s, M, topk, E, shared_w != nullptr, mask, slot_of, wave_cnt, plan);
+  plan_from_masks(ids_s, M, topk, E, shared_w != nullptr, mask, ep_prev, plan);
 }
 
 // ---------------------------------------------------------------------------------------
