@@ -120,6 +120,21 @@ __device__ __forceinline__ uint32_t wave_max_u32_dpp(uint32_t v) {
   return ab > cd ? ab : cd;
 }
 
+// Wave maximum left in every lane (no scalar round trip): the row maxima by DPP, then the
+// gfx950 row-pair and half-wave swaps (v_permlane16_swap: rows 0<->1 and 2<->3;
+// v_permlane32_swap: lanes 0-31 <-> 32-63).
+__device__ __forceinline__ uint32_t wave_max_u32_all(uint32_t v) {
+  uint32_t o;
+  o = dpp_u32<DPP_QUAD_XOR1>(v); v = o > v ? o : v;
+  o = dpp_u32<DPP_QUAD_XOR2>(v); v = o > v ? o : v;
+  o = dpp_u32<DPP_HALF_MIRROR>(v); v = o > v ? o : v;
+  o = dpp_u32<DPP_MIRROR>(v); v = o > v ? o : v;
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = r[0] > r[1] ? r[0] : r[1];
+  const auto q = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return q[0] > q[1] ? q[0] : q[1];
+}
+
 __device__ __forceinline__ uint32_t wave_min_u32_dpp(uint32_t v) {
   uint32_t o;
   o = dpp_u32<DPP_QUAD_XOR1>(v); v = o < v ? o : v;

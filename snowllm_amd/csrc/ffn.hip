@@ -403,33 +403,29 @@ __global__ void __launch_bounds__(WS * PPB * 64) gate_up_kernel(
 // ---------------------------------------------------------------------------------------
 constexpr int ROUTE_THREADS = 1024;  // 16 waves: one per row (M <= 16), four for the plan
 
-// Softmax over E <= 256 logits (expert e = lane + 64 i), then the top-k in descending order
-// with ties to the lower expert id: lane k ends with the k-th pick's probability and id. Each
-// lane sorts its four candidates once; a round takes the wave maximum of the lanes' heads in
-// the order (ordered key, then lower expert id) and the winning lane drops its head.
+// Top-k of E <= 256 logits (expert e = lane + 64 i) in descending order with ties to the
+// lower expert id, and the picks' renormalised softmax weights: lane k ends with the k-th
+// pick's id and weight. Each lane sorts its four candidates once; a round takes the wave
+// maximum of the lanes' heads (left in every lane), the lanes holding it (ballot; on a tie
+// the lowest expert id among them) and the winning lane drops its head. The softmax order is
+// the logits' order (exp is monotonic, so the picks are the same), and the renormalised
+// weight of pick k is p_k / sum_j p_j = e^(v_k - v_0) / sum_j e^(v_j - v_0) (v_0 the largest
+// logit): the full softmax sum cancels, so it is never formed.
 __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, int topk, int lane,
-                                          float& my_p, int& my_id, float& ksum) {
-  float v[4];
+                                          float& my_w, int& my_id) {
   uint32_t key[4];  // ordered keys; 0 = past E
   uint32_t id[4];
+  {
+    float v[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = l[lane + 64 * i < E ? lane + 64 * i : 0];  // all in flight
+    for (int i = 0; i < 4; ++i) v[i] = l[lane + 64 * i < E ? lane + 64 * i : 0];  // all in flight
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = e < E ? v[i] : -__builtin_huge_valf();
-    key[i] = e < E ? ord_key(v[i]) : 0u;
-    id[i] = (uint32_t)e;
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane + 64 * i;
+      key[i] = e < E ? ord_key(v[i]) : 0u;
+      id[i] = (uint32_t)e;
+    }
   }
-  uint32_t km = key[0] > key[1] ? key[0] : key[1];
-  km = key[2] > km ? key[2] : km;
-  km = key[3] > km ? key[3] : km;
-  const float mx = ord_key_to_float(wave_max_u32_dpp(km));
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (lane + 64 * i < E) sum += __expf(v[i] - mx);
-  sum = wave_sum_dpp(sum);
   // sort the lane's candidates: key descending, then id ascending (a five-comparator network
   // under that total order)
   auto cswap = [&](int a, int b) {
@@ -443,19 +439,17 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
   };
   cswap(0, 1); cswap(2, 3); cswap(0, 2); cswap(1, 3); cswap(1, 2);
   my_id = -1;
-  float my_v = 0.f;  // the pick's logit (lane k: the k-th pick)
+  uint32_t my_key = 0u;  // lane k: the k-th pick's key
   for (int k = 0; k < topk; ++k) {
-    // the largest head key, then (ties) the lowest expert id among the lanes holding it: the
-    // maximum of (key, ~id) with a 32-bit reduction in the common case of one such lane
-    const uint32_t km = wave_max_u32_dpp(key[0]);
+    const uint32_t km = wave_max_u32_all(key[0]);
     const uint64_t tied = __ballot(key[0] == km);
-    int e;
+    int wl;  // the winning lane: the only one holding km, else the one with the lowest id
     if (__popcll(tied) == 1)
-      e = __builtin_amdgcn_readlane((int)id[0], (int)__builtin_ctzll(tied));
+      wl = (int)__builtin_ctzll(tied);
     else
-      e = (int)wave_min_u32_dpp(key[0] == km ? id[0] : 0xffffffffu);
-    const float ve = ord_key_to_float(km);
-    const bool pop = lane == (e & 63);
+      wl = (int)(wave_min_u32_dpp(key[0] == km ? id[0] : 0xffffffffu) & 63u);
+    const int e = __builtin_amdgcn_readlane((int)id[0], wl);
+    const bool pop = lane == wl;
     key[0] = pop ? key[1] : key[0];
     id[0] = pop ? id[1] : id[0];
     key[1] = pop ? key[2] : key[1];
@@ -463,15 +457,18 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
     key[2] = pop ? key[3] : key[2];
     id[2] = pop ? id[3] : id[2];
     key[3] = pop ? 0u : key[3];
-    my_v = lane == k ? ve : my_v;
+    my_key = lane == k ? km : my_key;
     my_id = lane == k ? e : my_id;
   }
-  // the picks' probabilities, every lane at once (the same operations as one at a time)
-  my_p = lane < topk ? __expf(my_v - mx) / sum : 0.f;
-  ksum = 0.f;
-#pragma unroll
-  for (int k = 0; k < 16; ++k)
-    if (k < topk) ksum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), k));
+  // weights over the picks (lanes < topk <= 16, all in the first row of 16 lanes)
+  const float v0 = ord_key_to_float((uint32_t)__builtin_amdgcn_readlane((int)my_key, 0));
+  const float ek = lane < topk ? __expf(ord_key_to_float(my_key) - v0) : 0.f;
+  float ks = ek;
+  ks += __uint_as_float(dpp_u32<DPP_QUAD_XOR1>(__float_as_uint(ks)));
+  ks += __uint_as_float(dpp_u32<DPP_QUAD_XOR2>(__float_as_uint(ks)));
+  ks += __uint_as_float(dpp_u32<DPP_HALF_MIRROR>(__float_as_uint(ks)));
+  ks += __uint_as_float(dpp_u32<DPP_MIRROR>(__float_as_uint(ks)));
+  my_w = lane < topk ? ek / ks : 0.f;
 }
 
 // Plan from the expert row masks (mask[e] bit r: block row r is routed to expert e; complete
@@ -554,11 +551,11 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_route_plan_kernel(
   if (w < M) {
     const float* l = logits + (int64_t)w * stride;
     const float gate = shared_w ? l[E] : 0.f;
-    float my_p, ksum;
+    float my_w;
     int my_id;
-    route_row(l, E, topk, lane, my_p, my_id, ksum);
+    route_row(l, E, topk, lane, my_w, my_id);
     if (lane < topk) {
-      weights[w * topk + lane] = my_p / ksum;
+      weights[w * topk + lane] = my_w;
       ids[w * topk + lane] = my_id;
       ids_s[w * topk + lane] = my_id;
       if (my_id >= 0 && my_id < E) atomicOr(&mask[my_id], 1u << w);
@@ -779,11 +776,11 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
   for (int row = wv; row < M; row += NR_THREADS / 64) {
     const float* l = lg + row * N;
     const float gate = shared_w ? l[E] : 0.f;
-    float my_p, ksum;
+    float my_w;
     int my_id;
-    route_row(l, E, topk, lane, my_p, my_id, ksum);
+    route_row(l, E, topk, lane, my_w, my_id);
     if (lane < topk) {
-      weights[row * topk + lane] = my_p / ksum;
+      weights[row * topk + lane] = my_w;
       ids[row * topk + lane] = my_id;
       ids_s[row * topk + lane] = my_id;
       if (my_id >= 0 && my_id < E) atomicOr(&mask[my_id], 1u << row);
