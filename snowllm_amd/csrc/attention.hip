@@ -294,15 +294,22 @@ __device__ __forceinline__ void attend_chunk(AttnState<D, DH>& st, const uint8_t
 // DH: waves per row tile, 1 or 2 for every tile; 3 = mixed: the first 2 NRT - NW tiles have one
 // wave each, the remaining NW - NRT tiles two (the pairs split S^T, see attend_chunk), so that
 // up to eight waves spread the tiles' matrix work evenly over the four SIMDs.
+// The fields the prologue needs first come again as leading scalar arguments: those arrive
+// preloaded in SGPRs, while the struct is read from kernel-argument memory.
 template <int D, int CPW, int RING, int DH>
 __global__ void __launch_bounds__(DH == 2 ? MAX_TILES_DH * 2 * 64 : MAX_TILES * 64)
-attn_split_kernel(AttnArgs a) {
+attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict__ h_lens,
+                  int h_S, int h_Hkv, int h_pps, int h_tstride, int h_T, int h_G, int h_NRT,
+                  AttnArgs a) {
+  a.table = h_table, a.lens = h_lens, a.S = h_S, a.Hkv = h_Hkv, a.pages_per_split = h_pps;
+  a.table_stride = h_tstride, a.T = h_T, a.G = h_G, a.NRT = h_NRT;
   using G = SlotGeo<D>;
   constexpr int DS = D / 32;
   constexpr bool MIXED = DH == 3;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING * G::BYTES];
   __shared__ floatx4 xch[MIXED ? MAX_TILES : 1][2][64];  // S^T swap of the pairs (mixed)
-  const int NW = (int)(blockDim.x >> 6);  // waves
+  const int NW = DH == 3 ? MAX_TILES : h_NRT * DH;  // waves (the launch's; blockDim would be a
+                                                   // kernel-argument load)
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int w, dhalf;  // row tile, output-column part
@@ -709,14 +716,18 @@ int launch_split_ring(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   while (cpw * nw < CH) cpw *= 2;
   if (RING == 8 && cpw == 16) return launch_split_ring<D, DH, 4>(a, nblocks, s);  // vmcnt range
   const dim3 grid((unsigned)nblocks), block((unsigned)(64 * nw));
+#define SV_SPLIT(CPW_, RING_)                                                                   \
+  hipLaunchKernelGGL((attn_split_kernel<D, CPW_, RING_, DH>), grid, block, 0, s, a.table, a.lens, \
+                     a.S, a.Hkv, a.pages_per_split, a.table_stride, a.T, a.G, a.NRT, a)
   switch (cpw) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<D, 1, RING, DH>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<D, 2, RING, DH>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_split_kernel<D, 4, RING, DH>), grid, block, 0, s, a); break;
-    case 8: hipLaunchKernelGGL((attn_split_kernel<D, 8, RING, DH>), grid, block, 0, s, a); break;
-    case 16: hipLaunchKernelGGL((attn_split_kernel<D, 16, 4, DH>), grid, block, 0, s, a); break;
+    case 1: SV_SPLIT(1, RING); break;
+    case 2: SV_SPLIT(2, RING); break;
+    case 4: SV_SPLIT(4, RING); break;
+    case 8: SV_SPLIT(8, RING); break;
+    case 16: SV_SPLIT(16, 4); break;
     default: return SV_ENOTSUP;
   }
+#undef SV_SPLIT
   return SV_OK;
 }
 

@@ -96,11 +96,15 @@ __device__ __forceinline__ u32x4 moe_words(const MoeSource& ms, int64_t row, int
                pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7])};
 }
 
+// (The arguments the loads need come first: the first 56 bytes arrive preloaded in SGPRs.)
 __global__ void __launch_bounds__(NORM_MAX_THREADS) norm_prep_kernel(
-    const uint16_t* __restrict__ x, MoeSource ms, const uint16_t* __restrict__ residual,
-    uint16_t* __restrict__ res_out, const uint16_t* __restrict__ gamma,
-    uint16_t* __restrict__ y_out, void* __restrict__ ws, size_t tile_bytes, int64_t M, int64_t H,
-    float eps) {
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
+    const uint16_t* __restrict__ gamma, const float* __restrict__ src_pairs,
+    const float* __restrict__ src_shared, int M32, int H32, int src_topk, float eps,
+    uint16_t* __restrict__ x_out, uint16_t* __restrict__ res_out, uint16_t* __restrict__ y_out,
+    void* __restrict__ ws, size_t tile_bytes) {
+  const MoeSource ms{src_pairs, src_shared, x_out, src_topk};
+  const int64_t M = M32, H = H32;
   __shared__ float part[NORM_MAX_THREADS / 64];
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63;
@@ -600,11 +604,12 @@ constexpr int NR_THREADS = 1024;  // 16 waves: one per routed row; the GEMV take
 constexpr int NR_MAXP = 8;        // row passes held in registers (M <= 8 * 8192 / H)
 __device__ uint32_t g_router_arrive;
 
+// (The arguments the first loads need come first: they arrive preloaded in SGPRs.)
 __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual,
-    uint16_t* __restrict__ res_out, const uint16_t* __restrict__ gamma,
-    uint16_t* __restrict__ y_out, void* __restrict__ ws, size_t tile_bytes, float eps,
-    const u32x4* __restrict__ router, float* __restrict__ logits, int M, int H, int E, int topk,
+    const uint16_t* __restrict__ gamma, const u32x4* __restrict__ router, int M, int H, int E,
+    int topk, float eps, uint16_t* __restrict__ res_out, uint16_t* __restrict__ y_out,
+    void* __restrict__ ws, size_t tile_bytes, float* __restrict__ logits,
     float* __restrict__ weights, int32_t* __restrict__ ids, float* __restrict__ shared_w,
     MoePlan* __restrict__ plan) {
   // router rows: the E experts, then the shared expert's gate when shared_w is given
@@ -987,16 +992,17 @@ constexpr uint32_t MOE_WAIT_POLLS = 1u << 20;  // ~0.1 s: far beyond any gate/up
 // bound the registers at 168); two otherwise.
 template <int FMT, int GU_WS, int GU_PPB, int DN_NTILE, int DN_WS, int DN_GPB, bool ONE_SB>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB ? 3 : 2, ONE_SB ? 3 : 2))) moe_experts_kernel(
-    const uint8_t* __restrict__ gu_quant, const uint8_t* __restrict__ gu_meta, int64_t gu_qbytes,
-    int64_t gu_mbytes, const uint8_t* __restrict__ sh_gu_quant,
+    // first the arguments of the plan read and the gate/up weight addresses: the first 56
+    // bytes arrive preloaded in SGPRs
+    const MoePlan* __restrict__ plan, const uint8_t* __restrict__ gu_quant,
+    const uint8_t* __restrict__ gu_meta, int64_t gu_qbytes, int64_t gu_mbytes, int gu_per_slot,
+    int dn_per_slot, int max_slots, int E, const uint8_t* __restrict__ sh_gu_quant,
     const uint8_t* __restrict__ sh_gu_meta, const uint8_t* __restrict__ dn_quant,
     const uint8_t* __restrict__ dn_meta, int64_t dn_qbytes, int64_t dn_mbytes,
     const uint8_t* __restrict__ sh_dn_quant, const uint8_t* __restrict__ sh_dn_meta,
-    const MoePlan* __restrict__ plan, int E, const void* __restrict__ ws,
-    uint16_t* __restrict__ act, const float* __restrict__ weights,
+    const void* __restrict__ ws, uint16_t* __restrict__ act, const float* __restrict__ weights,
     const float* __restrict__ shared_w, float* __restrict__ pairs,
-    float* __restrict__ shared_out, int M, int H, int F, int gu_per_slot, int dn_per_slot,
-    int max_slots) {
+    float* __restrict__ shared_out, int M, int H, int F) {
   static_assert(GU_WS * GU_PPB * 64 == 256 && DN_WS * DN_GPB * 64 == 256, "256-thread items");
   const int item = blockIdx.x;
   const int n_gu = gu_per_slot * max_slots;
@@ -1067,9 +1073,9 @@ int launch_norm_prep(const void* x, MoeSource ms, const void* res_in, void* res_
   const int64_t S = H / 256, mt = (M + 15) / 16;
   const int threads = (int)((H / 8 + 63) / 64 * 64);
   hipLaunchKernelGGL(norm_prep_kernel, dim3((unsigned)(mt * 16)), dim3(threads), 0, s,
-                     (const uint16_t*)x, ms, (const uint16_t*)res_in, (uint16_t*)res_out,
-                     (const uint16_t*)gamma, (uint16_t*)y_out, ws, xprep_tile_bytes(S), M, H,
-                     eps);
+                     (const uint16_t*)x, (const uint16_t*)res_in, (const uint16_t*)gamma,
+                     ms.pairs, ms.shared, (int)M, (int)H, ms.topk, eps, ms.x_out,
+                     (uint16_t*)res_out, (uint16_t*)y_out, ws, xprep_tile_bytes(S));
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1139,10 +1145,10 @@ SV_API int snowverify_norm_router_plan(const void* x, const void* res_in, void* 
   if (lds > 65536 || (M + 8192 / H - 1) / (8192 / H) > NR_MAXP) return SV_ENOTSUP;
   hipLaunchKernelGGL(norm_router_plan_kernel, dim3((unsigned)((N + TILE_N - 1) / TILE_N)),
                      dim3(NR_THREADS), lds, Sx(stream), (const uint16_t*)x,
-                     (const uint16_t*)res_in, (uint16_t*)res_out, (const uint16_t*)gamma,
-                     (uint16_t*)y_out, ws, xprep_tile_bytes(H / 256), eps, (const u32x4*)router,
-                     logits, (int)M, (int)H, (int)E, (int)topk, weights, ids, shared_w,
-                     (MoePlan*)plan);
+                     (const uint16_t*)res_in, (const uint16_t*)gamma, (const u32x4*)router,
+                     (int)M, (int)H, (int)E, (int)topk, eps, (uint16_t*)res_out,
+                     (uint16_t*)y_out, ws, xprep_tile_bytes(H / 256), logits, weights, ids,
+                     shared_w, (MoePlan*)plan);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1324,13 +1330,13 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
   const int64_t blocks = (int64_t)(gu_per_slot + dn_per_slot) * max_slots;
   auto launch = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, Sx(stream),
-                       (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
+                       (const MoePlan*)plan, (const uint8_t*)gu_quant, (const uint8_t*)gu_meta,
+                       gu_q, gu_m, gu_per_slot, dn_per_slot, (int)max_slots, (int)E,
                        (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
                        (const uint8_t*)dn_quant, (const uint8_t*)dn_meta, dn_q, dn_m,
-                       (const uint8_t*)sh_dn_quant, (const uint8_t*)sh_dn_meta,
-                       (const MoePlan*)plan, (int)E, ws, (uint16_t*)act, weights, shared_w,
-                       pairs, shared_out, (int)M, (int)H, (int)F, gu_per_slot, dn_per_slot,
-                       (int)max_slots);
+                       (const uint8_t*)sh_dn_quant, (const uint8_t*)sh_dn_meta, ws,
+                       (uint16_t*)act, weights, shared_w, pairs, shared_out, (int)M, (int)H,
+                       (int)F);
   };
   if (F / QK == MOE_DN_WS)
     launch(moe_experts_kernel<4, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
