@@ -325,9 +325,8 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
     dhalf = pair ? (wv - nx) & 1 : 0;
   }
   const int kq = lane >> 4, col = lane & 15;
-  const int split = blockIdx.x % a.S;
-  const int h = (blockIdx.x / a.S) % a.Hkv;
-  const int b = blockIdx.x / (a.S * a.Hkv);
+  // grid (S, Hkv, batch): the workgroups of a head's splits stay consecutive, and no division
+  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
 
   // this lane's query row (column of S^T / O^T)
   const int r = w * 16 + col;
@@ -568,10 +567,11 @@ __global__ void __launch_bounds__(MERGE_THREADS) attn_merge_kernel(AttnArgs a,
   __shared__ float inv_l[MERGE_ROWS];
   __shared__ floatx4 red[MERGE_SG][MERGE_ROWS][MERGE_D / 4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int prog = blockIdx.x;  // (b, h, tile)
-  const int row0 = blockIdx.y * MERGE_ROWS;
-  const int d0 = blockIdx.z * MERGE_D;
-  const int tile = prog % a.NRT, h = (prog / a.NRT) % a.Hkv, b = prog / (a.NRT * a.Hkv);
+  // grid (tile, h * row groups + row group, b * column groups + column group)
+  constexpr int RG = 16 / MERGE_ROWS, DG = D / MERGE_D;
+  const int tile = blockIdx.x, h = blockIdx.y / RG, b = blockIdx.z / DG;
+  const int row0 = (blockIdx.y % RG) * MERGE_ROWS;
+  const int d0 = (blockIdx.z % DG) * MERGE_D;
   const int64_t pbase = (((int64_t)b * a.Hkv + h) * a.NRT + tile) * a.S;
   const int sg = wv, rr = lane >> 4, d4 = lane & 15;
   const int row = row0 + rr;
@@ -609,18 +609,21 @@ __global__ void __launch_bounds__(MERGE_THREADS) attn_merge_kernel(AttnArgs a,
 constexpr int MWS_THREADS = (256 / 8) * MERGE_SG;  // 256: one row, a split group per half wave
 
 template <int D>
-__global__ void __launch_bounds__(MWS_THREADS) attn_merge_ws_kernel(AttnArgs a,
-                                                                   uint16_t* __restrict__ out,
-                                                                   void* __restrict__ ws,
-                                                                   size_t tile_bytes) {
+// (The fields the first loads need come again as leading scalar arguments: those arrive
+// preloaded in SGPRs, while the struct is read from kernel-argument memory.)
+__global__ void __launch_bounds__(MWS_THREADS) attn_merge_ws_kernel(
+    float* __restrict__ h_part_o, float* __restrict__ h_part_ml, int h_S, int h_NRT, int h_Hkv,
+    int h_T, int h_G, int h_Hq, AttnArgs a, uint16_t* __restrict__ out, void* __restrict__ ws,
+    size_t tile_bytes) {
+  a.part_o = h_part_o, a.part_ml = h_part_ml, a.S = h_S, a.NRT = h_NRT, a.Hkv = h_Hkv;
+  a.T = h_T, a.G = h_G, a.Hq = h_Hq;
   static_assert(D == 256, "one head per superblock");
   __shared__ float w[SPLITS_MAX];
   __shared__ float inv_l;
   __shared__ floatx4 red[MERGE_SG][D / 8][2];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int prog = blockIdx.x;  // (b, h, tile)
-  const int row = blockIdx.y;
-  const int tile = prog % a.NRT, h = (prog / a.NRT) % a.Hkv, b = prog / (a.NRT * a.Hkv);
+  // grid (tile, 16 h + row, b)
+  const int tile = blockIdx.x, row = blockIdx.y & 15, h = blockIdx.y >> 4, b = blockIdx.z;
   const int rg = tile * 16 + row;
   if (rg >= a.T * a.G) return;  // a padding row: no output, no operands (uniform)
   const int64_t pbase = (((int64_t)b * a.Hkv + h) * a.NRT + tile) * a.S;
@@ -715,7 +718,8 @@ int launch_split_ring(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   int cpw = 1;
   while (cpw * nw < CH) cpw *= 2;
   if (RING == 8 && cpw == 16) return launch_split_ring<D, DH, 4>(a, nblocks, s);  // vmcnt range
-  const dim3 grid((unsigned)nblocks), block((unsigned)(64 * nw));
+  const dim3 grid((unsigned)a.S, (unsigned)a.Hkv, (unsigned)(nblocks / ((int64_t)a.S * a.Hkv))),
+      block((unsigned)(64 * nw));
 #define SV_SPLIT(CPW_, RING_)                                                                   \
   hipLaunchKernelGGL((attn_split_kernel<D, CPW_, RING_, DH>), grid, block, 0, s, a.table, a.lens, \
                      a.S, a.Hkv, a.pages_per_split, a.table_stride, a.T, a.G, a.NRT, a)
@@ -779,6 +783,8 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
     return SV_EINVAL;
   if (head_size != 128 && head_size != 256) return SV_ENOTSUP;
   if (out_ws && head_size != 256) return SV_ENOTSUP;
+  // grid y/z extents: 16 * kv heads and batch * (head_size / 64) stay within 65535
+  if (num_kv_heads > 4095 || batch * (head_size / MERGE_D) > 65535) return SV_ENOTSUP;
   if (n_row_tiles((int)tokens, (int)(num_heads / num_kv_heads)) > MAX_TILES) return SV_ENOTSUP;
   if (scratch_bytes < snowverify_paged_attention_scratch_bytes(batch, tokens, num_heads,
                                                               num_kv_heads, head_size))
@@ -804,7 +810,8 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
   a.part_ml = (float*)((char*)scratch + align256(parts * head_size * 4));
   hipStream_t s = (hipStream_t)stream;
   const int64_t nblocks = batch * a.Hkv * a.S;
-  const dim3 mgrid((unsigned)(batch * a.Hkv * a.NRT), 16 / MERGE_ROWS, (unsigned)(head_size / MERGE_D));
+  const dim3 mgrid((unsigned)a.NRT, (unsigned)(a.Hkv * (16 / MERGE_ROWS)),
+                   (unsigned)(batch * (head_size / MERGE_D)));
   int rc;
   if (head_size == 128) {
     rc = launch_split<128>(a, nblocks, s);
@@ -817,8 +824,11 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
     SV_CHECK_LAUNCH();
     if (out_ws) {
       const size_t tb = kq::xprep_tile_bytes(num_heads * head_size / kq::QK);
-      hipLaunchKernelGGL(attn_merge_ws_kernel<256>, dim3(mgrid.x, 16), dim3(MWS_THREADS), 0, s,
-                         a, (uint16_t*)out, out_ws, tb);
+      hipLaunchKernelGGL(attn_merge_ws_kernel<256>,
+                         dim3((unsigned)a.NRT, (unsigned)(16 * a.Hkv), (unsigned)batch),
+                         dim3(MWS_THREADS), 0, s,
+                         a.part_o, a.part_ml, a.S, a.NRT, a.Hkv, a.T, a.G, a.Hq, a,
+                         (uint16_t*)out, out_ws, tb);
     } else {
       hipLaunchKernelGGL(attn_merge_kernel<256>, mgrid, dim3(MERGE_THREADS), 0, s, a,
                          (uint16_t*)out);
