@@ -633,22 +633,36 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
       (void*)(router + (int64_t)tile * S * 8 * 64), 0, S * 8 * 64 * 16, 0x00020000);
   u32x4 wb[8];
 
-  // residual + RMSNorm of every row: RP rows per pass, H / 8 threads per row; every pass's
-  // words are loaded before any sum (one round trip), the passes' sums meet in one barrier
-  const int wpr = H / 8, RP = NR_THREADS / wpr, wpw = wpr / 64;  // words, rows, waves per row
-  const int tr = t % wpr, rsub = t / wpr;
-  const int npass = (M + RP - 1) / RP;  // passes holding rows < M (<= NR_MAXP: host-checked)
-  const u32x4 gv = *(const u32x4*)(gamma + (int64_t)tr * 8);
+  // residual + RMSNorm of every row: RP rows per pass, wpr = H / 8 threads per row (whole
+  // waves: H % 512 == 0); every pass's words are loaded before any sum (one round trip), the
+  // passes' sums meet in one barrier. The four waves of a SIMD issue this prologue one after
+  // another, so it is kept short: shifts when wpr is a power of two, bounds-checked buffer
+  // loads (rows past M read as zero) at one vector offset per pass.
+  const int wpr = H >> 3;
+  int tr, rsub, RP;
+  if ((wpr & (wpr - 1)) == 0) {  // uniform
+    const int lg = __builtin_ctz(wpr);
+    rsub = t >> lg, tr = t & (wpr - 1), RP = NR_THREADS >> lg;
+  } else {
+    rsub = t / wpr, tr = t - rsub * wpr, RP = NR_THREADS / wpr;
+  }
+  const int wpw = wpr >> 6;  // waves per row
+  const uint32_t rbytes = (uint32_t)(M * H * 2), pstride = (uint32_t)(RP * H * 2);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, rbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)residual, 0, residual ? rbytes : 0u, 0x00020000);
+  const uint32_t voff = (uint32_t)(rsub * H + tr * 8) * 2;
+  // gamma: the first row group's waves load it and pass it on through LDS (every row group
+  // needs the same words)
+  __shared__ u32x4 gam_s[4096 / 8];
+  u32x4 gv = {0u, 0u, 0u, 0u};
+  if (rsub == 0) gv = *(const u32x4*)(gamma + (int64_t)tr * 8);  // wave-uniform
   u32x4 xv[NR_MAXP], rv[NR_MAXP];
 #pragma unroll
   for (int p = 0; p < NR_MAXP; ++p) {
-    const int row = p * RP + rsub;
-    xv[p] = rv[p] = u32x4{0u, 0u, 0u, 0u};
-    if (p < npass && row < M) {
-      const int64_t off = (int64_t)row * H + (int64_t)tr * 8;
-      xv[p] = *(const u32x4*)(x + off);
-      if (residual) rv[p] = *(const u32x4*)(residual + off);
-    }
+    if (p * RP >= M) break;  // uniform; passes <= NR_MAXP (host-checked)
+    xv[p] = bload4(xr, voff + p * pstride, 0u);
+    rv[p] = bload4(rr, voff + p * pstride, 0u);
   }
   // the router weights behind the rows (the norm needs only the rows); every wave issues the
   // same eight loads (out of the buffer's range, so reading nothing, in the waves without a
@@ -659,11 +673,11 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
     for (int j = 0; j < 8; ++j) wb[j] = bload4(wr, wvo, (uint32_t)((wv * 8 + j) * 64 * 16));
   }
   __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));  // vmcnt(8): the rows, not the weights
+  if (rsub == 0) gam_s[tr] = gv;
 #pragma unroll
   for (int p = 0; p < NR_MAXP; ++p) {
-    if (p >= npass) break;  // uniform
-    const int row = p * RP + rsub;
-    if (residual && row < M) xv[p] = add_bf16_words(xv[p], rv[p]);
+    if (p * RP >= M) break;  // uniform
+    if (residual) xv[p] = add_bf16_words(xv[p], rv[p]);
     const uint32_t vw[4] = {xv[p].x, xv[p].y, xv[p].z, xv[p].w};
     float ss = 0.f;
 #pragma unroll
@@ -676,6 +690,7 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
     if (lane == 0) part_ss[p][wv] = ss;
   }
   __syncthreads();
+  gv = gam_s[tr];
   const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w};
   auto normalise = [&](const u32x4& v, float inv, uint32_t (&yo)[4], float (&y)[8]) {
     const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
@@ -688,33 +703,35 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
       y[2 * i + 1] = __uint_as_float(yo[i] & 0xffff0000u);
     }
   };
+  // workgroup j writes row j's results (the 16 rows of the operand tile over 16 workgroups;
+  // the first workgroup writes them all when there are fewer)
+  auto owns = [&](int row) { return gridDim.x >= 16 ? row == (int)blockIdx.x : blockIdx.x == 0; };
 #pragma unroll
   for (int p = 0; p < NR_MAXP; ++p) {
-    if (p >= npass) break;  // uniform
+    if (p * RP >= M) break;  // uniform
     const int row = p * RP + rsub;
+    if (row >= M) break;  // uniform: the last pass's row groups past M
     float tot = 0.f;
     for (int w = 0; w < wpw; ++w) tot += part_ss[p][rsub * wpw + w];
     const float inv = __frsqrt_rn(tot / (float)H + eps);
     float y[8];
     uint32_t yo[4];
     normalise(xv[p], inv, yo, y);
-    if (row < M) *(u32x4*)(ylds + row * ystride + tr * 8) = u32x4{yo[0], yo[1], yo[2], yo[3]};
-    // workgroup j writes row j's results (the 16 rows of the operand tile over 16 workgroups;
-    // the first workgroup writes them all when there are fewer)
-    const bool own = gridDim.x >= 16 ? row == (int)blockIdx.x : blockIdx.x == 0;
-    if (own && row < M) {
+    *(u32x4*)(ylds + row * ystride + tr * 8) = u32x4{yo[0], yo[1], yo[2], yo[3]};
+    if (owns(row)) {  // wave-uniform
       const int64_t off = (int64_t)row * H + (int64_t)tr * 8;
       if (res_out) *(u32x4*)(res_out + off) = xv[p];
       if (y_out) *(u32x4*)(y_out + off) = u32x4{yo[0], yo[1], yo[2], yo[3]};
+      if (row < 16) word_operand(y, tr, row, ws, tile_bytes, H / QK, true);
     }
-    if (own && row < 16) word_operand(y, tr, row, ws, tile_bytes, H / QK, true);  // wave-uniform
   }
-  // the tile's rows past the passes get zero operands, as norm_prep_kernel writes them
-  for (int row0 = npass * RP; row0 < 16; row0 += RP) {  // uniform
+  // the tile's rows past M get zero operands, as norm_prep_kernel writes them
+  for (int row0 = 0; row0 < 16; row0 += RP) {  // uniform
     const int row = row0 + rsub;
-    const bool own = gridDim.x >= 16 ? row == (int)blockIdx.x : blockIdx.x == 0;
-    float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (own && row < 16) word_operand(y, tr, row, ws, tile_bytes, H / QK, true);
+    if (row >= M && row < 16 && owns(row)) {
+      float y[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      word_operand(y, tr, row, ws, tile_bytes, H / QK, true);
+    }
   }
   __syncthreads();  // the rows are in LDS
 
