@@ -308,6 +308,13 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
   constexpr bool MIXED = DH == 3;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING * G::BYTES];
   __shared__ floatx4 xch[MIXED ? MAX_TILES : 1][2][64];  // S^T swap of the pairs (mixed)
+  // Q operands of the row tiles that two waves share: the first wave of the pair fetches (and,
+  // fused, normalises and rotates) the rows and passes the operands on through LDS
+  constexpr int QSH_PAIRS = MIXED ? MAX_TILES - 5 : (DH == 2 ? MAX_TILES_DH : 0);
+  constexpr size_t QSH_BYTES = (size_t)QSH_PAIRS * DS * 64 * 16;
+  constexpr bool QSHARE =
+      QSH_PAIRS > 0 && RING * G::BYTES + QSH_BYTES + sizeof(xch) <= 150 * 1024;
+  __shared__ u32x4 qsh[QSHARE ? QSH_PAIRS : 1][DS][64];
   const int NW = DH == 3 ? MAX_TILES : h_NRT * DH;  // waves (the launch's; blockDim would be a
                                                    // kernel-argument load)
   const int lane = threadIdx.x & 63;
@@ -397,7 +404,11 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
   if (p0 < p1) {  // uniform over the workgroup
     // Q^T operand (8 consecutive d per k-step), loaded before the page loads are queued; the
     // fused form fetches the raw projection row and its norm operands here and normalises the
-    // row once the first pages are on their way
+    // row once the first pages are on their way. The second wave of a shared tile takes the
+    // operands from LDS after the loop's first barrier instead.
+    const int qpi = MIXED ? w - (2 * a.NRT - NW) : w;  // the tile's index among the pairs
+    const bool q_from_lds = QSHARE && pair && dhalf == 1;  // wave-uniform
+    const bool q_to_lds = QSHARE && pair && dhalf == 0;
     bf16x8 qb[DS];
     QkRaw<D> qraw;
     QkAux<D> qaux;
@@ -423,11 +434,13 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
         wait_vmcnt<0>();  // the block's K/V stores are done ...
         block_barrier();  // ... before any wave queues a page load
       }
-      qk_fetch<D>(qraw, a.proj + m_row * a.proj_stride + (int64_t)hq * a.q_head_stride, kq,
-                  row_live);
-      qk_fetch_aux<D>(qaux, a.q_gamma, a.cosv + m_row * a.cs_stride, a.sinv + m_row * a.cs_stride,
-                      a.rot_half, kq);
-    } else {
+      if (!q_from_lds) {
+        qk_fetch<D>(qraw, a.proj + m_row * a.proj_stride + (int64_t)hq * a.q_head_stride, kq,
+                    row_live);
+        qk_fetch_aux<D>(qaux, a.q_gamma, a.cosv + m_row * a.cs_stride,
+                        a.sinv + m_row * a.cs_stride, a.rot_half, kq);
+      }
+    } else if (!q_from_lds) {
       const uint16_t* qrow = a.q + m_row * a.q_stride + (int64_t)hq * D;
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) {
@@ -453,7 +466,7 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
     // pages go two per step (one 32-key chunk); RING - 2 pages are queued ahead of a step
 #pragma unroll
     for (int i = 0; i < RING - 2; ++i) issue(p0 + i, i);
-    if (a.proj) {
+    if (a.proj && !q_from_lds) {
       // this lane's query row, normalised and rotated while the first pages load (angles of
       // sub-blocks past the first, when half > 32, load here behind the pages)
       uint4 qo[DS];
@@ -469,6 +482,11 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
           *(uint4*)(a.q_out + (m_row * a.Hq + hq) * D + ds * 32 + kq * 8) = o;
       }
     }
+    if (q_to_lds) {
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) qsh[qpi][ds][lane] = __builtin_bit_cast(u32x4, qb[ds]);
+      wait_lgkmcnt0();  // visible to the pair's other wave at the loop's first barrier
+    }
     with_state([&](auto& st) {
       constexpr int DT = (int)(sizeof(st.o) / sizeof(st.o[0]));
       constexpr int DHW = D / 16 / DT;
@@ -477,6 +495,9 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
       for (int pg = p0; pg < p1; pg += 2) {
         wait_vmcnt<(RING - 4) * CPW>();  // this wave's loads of pages pg, pg + 1 have landed
         block_barrier();                 // ... and every wave's; the previous chunk is free
+        if (q_from_lds && pg == p0)
+#pragma unroll
+          for (int ds = 0; ds < DS; ++ds) qb[ds] = __builtin_bit_cast(bf16x8, qsh[qpi][ds][lane]);
         const int prev = slot == 0 ? RING - 2 : slot - 2;
         issue(pg + RING - 2, prev);
         issue(pg + RING - 1, prev + 1);
