@@ -1112,9 +1112,10 @@ __device__ __forceinline__ uint64_t fa_row_zsum(int row, int P) {
   return wave_sum_u64(z);
 }
 
-__global__ void __launch_bounds__(FA_NT) fa_max_kernel(FaArgs a) {
+__global__ void __launch_bounds__(FA_NT) fa_max_kernel(const float* __restrict__ h_logits, const float* __restrict__ h_temperature, int h_V, int h_width, int h_P, FaArgs a) {
+  a.logits = h_logits, a.temperature = h_temperature, a.V = h_V, a.width = h_width, a.P = h_P;
   __shared__ uint64_t red[FA_NT / WAVE];
-  const int w = blockIdx.x % a.P, row = blockIdx.x / a.P;
+  const int w = blockIdx.x, row = blockIdx.y;  // grid (P, rows)
   const int lo = w * FA_SLICE;
   float v[FA_E];
   fa_load_slice(a.logits + (int64_t)row * a.V, lo, a.V, row_temperature(a.temperature, row), v);
@@ -1128,11 +1129,12 @@ __global__ void __launch_bounds__(FA_NT) fa_max_kernel(FaArgs a) {
   if (threadIdx.x == 0) dev_store(&g_fa_maxkey[row][w], mk);
 }
 
-__global__ void __launch_bounds__(FA_NT) fa_sum_kernel(FaArgs a) {
+__global__ void __launch_bounds__(FA_NT) fa_sum_kernel(const float* __restrict__ h_logits, const float* __restrict__ h_temperature, int h_V, int h_width, int h_P, FaArgs a) {
+  a.logits = h_logits, a.temperature = h_temperature, a.V = h_V, a.width = h_width, a.P = h_P;
   __shared__ uint64_t red[FA_NT / WAVE];
   __shared__ float red_f[4];
   const int P = a.P, width = a.width, length = width - 1, V = a.V;
-  const int w = blockIdx.x % P, row = blockIdx.x / P;
+  const int w = blockIdx.x, row = blockIdx.y;  // grid (P, rows)
   const int r = row / width, j = row % width;
   const int t = threadIdx.x, lo = w * FA_SLICE;
   float v[FA_E];
@@ -1239,7 +1241,8 @@ __device__ ResidualRow fa_residual(const FaArgs& a, int r, int first, int64_t* s
   return rr;
 }
 
-__global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
+__global__ void __launch_bounds__(FA_NT) fa_pick_kernel(const float* __restrict__ h_logits, const float* __restrict__ h_temperature, int h_V, int h_width, int h_P, FaArgs a) {
+  a.logits = h_logits, a.temperature = h_temperature, a.V = h_V, a.width = h_width, a.P = h_P;
   __shared__ uint64_t red[FA_NT / WAVE];
   __shared__ uint64_t s_sub[2][FA_NT / WAVE];
   __shared__ uint64_t buf[FA_NT];
@@ -1252,8 +1255,7 @@ __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
   // one workgroup per sub-chunk c of slice w (the thread's logits k in [4c, 4c + 4) of the
   // slice): four times the workgroups of one per slice, a quarter of the arithmetic each
   const int P = a.P, width = a.width, length = width - 1, V = a.V;
-  const int w = (blockIdx.x / FA_SUBCHUNKS) % P, r = blockIdx.x / (FA_SUBCHUNKS * P);
-  const int c = blockIdx.x % FA_SUBCHUNKS;
+  const int c = blockIdx.x, w = blockIdx.y, r = blockIdx.z;  // grid (sub-chunks, P, b)
   const int t = threadIdx.x, lo = w * FA_SLICE;
   const int first = g_fa_first[r];
   const int row = r * width + first;
@@ -1422,11 +1424,12 @@ __global__ void __launch_bounds__(FA_NT) fa_pick_kernel(FaArgs a) {
   if (t == 0) a.accepted[r] = first + 1;
 }
 
-__global__ void __launch_bounds__(FA_NT) fa_greedy_kernel(FaArgs a) {
+__global__ void __launch_bounds__(FA_NT) fa_greedy_kernel(const float* __restrict__ h_logits, const float* __restrict__ h_temperature, int h_V, int h_width, int h_P, FaArgs a) {
+  a.logits = h_logits, a.temperature = h_temperature, a.V = h_V, a.width = h_width, a.P = h_P;
   __shared__ uint64_t red[FA_NT / WAVE];
   __shared__ int64_t s_tok[64];
   const int P = a.P, width = a.width, length = width - 1, V = a.V;
-  const int w = blockIdx.x % P, row = blockIdx.x / P;
+  const int w = blockIdx.x, row = blockIdx.y;  // grid (P, rows)
   const int r = row / width, j = row % width;
   const int t = threadIdx.x, lo = w * FA_SLICE;
   const float* x = a.logits + (int64_t)row * V;
@@ -1487,12 +1490,17 @@ SV_API int snowverify_accept_reject(const float* logits, const float* temperatur
   const int P = fa_slices(vocab);
   FaArgs a{logits, temperature, drafts, cand, q, slots, valid, uniform, out, accepted,
            (int)vocab, (int)width, P, q_width};
-  const dim3 rows((unsigned)(b * width * P)), reqs((unsigned)(b * P * FA_SUBCHUNKS));
-  hipLaunchKernelGGL(fa_max_kernel, rows, dim3(FA_NT), 0, S(stream), a);
+  // grids without division (slice in x); the fields the first loads need come again as
+  // leading arguments, which arrive preloaded in SGPRs (the struct does not)
+  const dim3 rows((unsigned)P, (unsigned)(b * width)), reqs(FA_SUBCHUNKS, (unsigned)P, (unsigned)b);
+  hipLaunchKernelGGL(fa_max_kernel, rows, dim3(FA_NT), 0, S(stream), logits, temperature,
+                     (int)vocab, (int)width, P, a);
   SV_CHECK_LAUNCH();
-  hipLaunchKernelGGL(fa_sum_kernel, rows, dim3(FA_NT), 0, S(stream), a);
+  hipLaunchKernelGGL(fa_sum_kernel, rows, dim3(FA_NT), 0, S(stream), logits, temperature,
+                     (int)vocab, (int)width, P, a);
   SV_CHECK_LAUNCH();
-  hipLaunchKernelGGL(fa_pick_kernel, reqs, dim3(FA_NT), 0, S(stream), a);
+  hipLaunchKernelGGL(fa_pick_kernel, reqs, dim3(FA_NT), 0, S(stream), logits, temperature,
+                     (int)vocab, (int)width, P, a);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1510,8 +1518,8 @@ SV_API int snowverify_accept_greedy(const float* logits, const int64_t* drafts, 
   const int P = fa_slices(vocab);
   FaArgs a{logits, nullptr, drafts, nullptr, nullptr, nullptr, nullptr, nullptr, tokens,
            accepted, (int)vocab, (int)width, P, 0};
-  hipLaunchKernelGGL(fa_greedy_kernel, dim3((unsigned)(b * width * P)), dim3(FA_NT), 0,
-                     S(stream), a);
+  hipLaunchKernelGGL(fa_greedy_kernel, dim3((unsigned)P, (unsigned)(b * width)), dim3(FA_NT), 0,
+                     S(stream), logits, (const float*)nullptr, (int)vocab, (int)width, P, a);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }

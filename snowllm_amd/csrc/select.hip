@@ -178,16 +178,19 @@ __device__ __forceinline__ float round_bf16(float f) {
 // corr[p][c] for previous token p (the previous row's candidate p, or the anchor at j = 0).
 // ---------------------------------------------------------------------------------------
 template <int E>  // terms per lane: r = lane * E + i, R = 64 E
+// (The merge's inputs come first: they arrive preloaded in SGPRs; grid (ell, b), no division.)
 __global__ void __launch_bounds__(SEL_K * 64) select_table(
+    uint64_t* __restrict__ h_chunk_keys, uint64_t* __restrict__ h_top_keys, int C, int ell32,
     const uint16_t* __restrict__ hp, const uint16_t* __restrict__ pred,
     const uint16_t* __restrict__ succ, const int64_t* __restrict__ anchor,
-    const float* __restrict__ temperature, const float* __restrict__ uniform, int64_t ell, int C,
+    const float* __restrict__ temperature, const float* __restrict__ uniform,
     SelectScratch sc) {
   constexpr int R = 64 * E;
   __shared__ uint64_t s_top[SEL_K];
   __shared__ uint64_t s_prev[SEL_K];
-  const int64_t row = blockIdx.x;
-  const int64_t b = row / ell, j = row % ell;
+  sc.chunk_keys = h_chunk_keys, sc.top_keys = h_top_keys;
+  const int64_t ell = ell32, j = blockIdx.x, b = blockIdx.y;
+  const int64_t row = b * ell + j;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (w == 0) merge_row(sc, row, C, lane, s_top);
@@ -261,11 +264,15 @@ __global__ void __launch_bounds__(SEL_K * 64) select_table(
 // ---------------------------------------------------------------------------------------
 // 3. the walk: follow the tabulated picks from p = 0 (the anchor) and emit the lists.
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(64) select_walk(const int32_t* __restrict__ slots,
+// (The tables' pointers come first: they arrive preloaded in SGPRs.)
+__global__ void __launch_bounds__(64) select_walk(int32_t* __restrict__ h_pick,
+                                                  uint64_t* __restrict__ h_top_keys,
+                                                  float* __restrict__ h_q, int64_t ell,
+                                                  const int32_t* __restrict__ slots,
                                                   int64_t* __restrict__ path,
                                                   int64_t* __restrict__ cand_out,
-                                                  float* __restrict__ q_out, int64_t ell,
-                                                  SelectScratch sc) {
+                                                  float* __restrict__ q_out, SelectScratch sc) {
+  sc.pick = h_pick, sc.top_keys = h_top_keys, sc.q = h_q;
   __shared__ int32_t s_pick[SEL_ELL_MAX][SEL_K];
   __shared__ __attribute__((aligned(16))) uint64_t s_top[SEL_ELL_MAX][SEL_K];
   __shared__ __attribute__((aligned(16))) float s_q[SEL_ELL_MAX][SEL_K][SEL_K];
@@ -315,12 +322,13 @@ int launch_select(const void* hp, const float* logits, const void* pred, const v
   SV_CHECK_LAUNCH();
   auto table = R == 64 ? select_table<1> : R == 128 ? select_table<2>
              : R == 256 ? select_table<4> : select_table<8>;
-  hipLaunchKernelGGL(table, dim3((unsigned)n), dim3(SEL_K * 64), 0, s, (const uint16_t*)hp,
+  hipLaunchKernelGGL(table, dim3((unsigned)ell, (unsigned)b), dim3(SEL_K * 64), 0, s,
+                     sc.chunk_keys, sc.top_keys, C, (int)ell, (const uint16_t*)hp,
                      (const uint16_t*)pred, (const uint16_t*)succ, anchor, temperature, uniform,
-                     ell, C, sc);
-  SV_CHECK_LAUNCH();
-  hipLaunchKernelGGL(select_walk, dim3((unsigned)b), dim3(64), 0, s, slots, path, cand, q, ell,
                      sc);
+  SV_CHECK_LAUNCH();
+  hipLaunchKernelGGL(select_walk, dim3((unsigned)b), dim3(64), 0, s, sc.pick, sc.top_keys, sc.q,
+                     ell, slots, path, cand, q, sc);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
