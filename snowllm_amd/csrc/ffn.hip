@@ -1215,15 +1215,20 @@ SV_API int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* met
   if ((fmt != 4 && fmt != 8) || M <= 0 || M > 16 || F <= 0 || F % 16 || K % 256) return SV_EINVAL;
   const int S = (int)(K / 256);
   hipStream_t s = Sx(stream);
-  const dim3 grid((unsigned)(F / 16), 1);
+  // two pairs per workgroup, two waves per pair: at FFN 14336 the 448 workgroups are all
+  // resident at once (two per CU at most), where one pair on four waves left 896 workgroups, a
+  // round and three quarters (measured at BASELINE config 3: 22.4 -> 20.6 us per call, step
+  // 3.266 -> 3.182 ms; eight waves per pair: 26.2 us)
+  constexpr int WS = 2, PPB = 2;
+  const dim3 grid((unsigned)((F / 16 + PPB - 1) / PPB), 1);
   if (fmt == 4)
-    hipLaunchKernelGGL((gate_up_kernel<4, 4, 1>), grid, dim3(256), 0, s, (const uint8_t*)quant,
-                       (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr, 0, ws, (uint16_t*)act,
-                       (int)M, (int)F, S);
+    hipLaunchKernelGGL((gate_up_kernel<4, WS, PPB>), grid, dim3(64 * WS * PPB), 0, s,
+                       (const uint8_t*)quant, (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr,
+                       0, ws, (uint16_t*)act, (int)M, (int)F, S);
   else
-    hipLaunchKernelGGL((gate_up_kernel<8, 4, 1>), grid, dim3(256), 0, s, (const uint8_t*)quant,
-                       (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr, 0, ws, (uint16_t*)act,
-                       (int)M, (int)F, S);
+    hipLaunchKernelGGL((gate_up_kernel<8, WS, PPB>), grid, dim3(64 * WS * PPB), 0, s,
+                       (const uint8_t*)quant, (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr,
+                       0, ws, (uint16_t*)act, (int)M, (int)F, S);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
