@@ -62,9 +62,13 @@ int snowllm_sampling_softmax(const float* logits, float* dense, int64_t rows, in
 
 /* Top-k / top-p candidate lists from dense probabilities (snowllm/_capi.py:586;
  * snowllm/ops/sampling.py:90-91): values f32 [rows, width], ids i64 [rows, width]. Rows whose
- * top_k covers the vocabulary with top_p >= 1 are written in vocabulary order; rows with
- * top_k <= 1024 are sorted by probability (ties to the lower id), renormalised and truncated
- * by top-p; unused slots are (0, -1). Other rows are written as (NaN, -2). */
+ * top_k covers the vocabulary with top_p >= 1 are written in vocabulary order; every other row
+ * (any top_k up to the vocabulary, any top_p) is sorted by probability (ties to the lower id),
+ * renormalised over its top k and truncated by top-p (entries past the cut keep their id with
+ * probability 0); unused slots are (0, -1). `dense` must start a workspace of
+ * snowllm_sampling_workspace_bytes(rows, vocab, width) bytes (lists wider than 1024 are sorted
+ * behind the dense block). A row whose top_k exceeds `width` cannot be written and comes out
+ * as (NaN, -2): callers size the width as the batch's largest top_k, as the reference's do. */
 int snowllm_sampling_topk_topp(const float* dense, float* values, int64_t* ids, int64_t rows,
                                int64_t vocab, int64_t width, const int32_t* top_k,
                                const float* top_p, void* stream);
@@ -75,6 +79,15 @@ int snowllm_sampling_sample(const float* logits, const int32_t* top_k, const flo
                             const float* temperature, const float* uniform, int64_t* out,
                             void* ws, int64_t ws_bytes, int64_t B, int64_t V, int64_t width,
                             void* stream);
+
+/* Repetition / frequency / presence penalties on one logit row (snowllm/_capi.py:589; wrapper
+ * snowllm/ops/sampling.py:94-100): for each of the n listed token ids (unique; the request's
+ * prompt and output ids) with output count c, logit = logit > 0 ? logit / repetition :
+ * logit * repetition, then logit - frequency * c, then logit - presence (when c > 0). Ids
+ * outside [0, vocab) are skipped. */
+int snowllm_sampling_penalties(float* logits, const int64_t* ids, const int32_t* counts, int n,
+                               int vocab, float presence, float frequency, float repetition,
+                               void* stream);
 
 /* Rejection sampling of a draft prefix plus residual/bonus resample (snowllm/_capi.py:289;
  * wrapper snowllm/ops/dflash.py:201-219; semantics tests/test_dflash_sampling.py:94-119).
@@ -93,7 +106,9 @@ int snowllm_draft_reject(const float* p, const int64_t* ids, const int64_t* draf
  * so the bits, of snowllm_sampling_softmax + snowllm_sampling_topk_topp + snowllm_draft_reject,
  * in three launches that never materialise the probabilities and never wait on one another's
  * workgroups. logits [b*width, vocab] f32, temperature [b*width] (NULL: 1; <= 0 counts as 1);
- * the rest as snowllm_draft_reject. b*width <= 256, width <= 64. Calls on one device must be
+ * the rest as snowllm_draft_reject. b*width <= 256, width <= 64 (larger shapes return
+ * hipErrorNotSupported with nothing launched: the caller then takes snowllm_sampling_softmax +
+ * snowllm_sampling_topk_topp + snowllm_draft_reject). Calls on one device must be
  * stream-ordered (library-owned statistics). */
 int snowverify_accept_reject(const float* logits, const float* temperature,
                              const int64_t* drafts, const int64_t* cand, const float* q,
@@ -510,7 +525,8 @@ int snowverify_qk_norm_rope_cache(const void* proj, int64_t stride, const void* 
                                   int64_t page, float eps, void* stream);
 
 /* slot = table[seq, pos / page] * page + pos % page (snowllm/_capi.py:361; ops/cache.py:40-53;
- * spec_decode.py:183). */
+ * spec_decode.py:183). Rows with a negative seq or pos, a page past the table's width or a
+ * negative (padding) table entry get slot -1, which the cache writers skip. */
 int snowllm_resolve_slots(const int32_t* table, int64_t stride, const int32_t* seq,
                           const int32_t* pos, int32_t* out, int64_t M, int64_t page, void* stream);
 
@@ -543,7 +559,7 @@ int snowverify_norm_prep_moe(const float* pairs, const float* shared_out, int64_
  * snowverify_norm_prep (res_out, y_out, ws) + snowverify_dense_gemv (bf16 router [E (+1), H]
  * repacked by snowverify_dense_shuffle; f32 logits [M, E (+1)]) + snowverify_moe_route_plan
  * (weights/ids [M, topk], shared_w [M] or NULL for no shared expert, plan). res_out must not
- * alias x or res_in. M <= 16; H a multiple of 512, <= 4096, M * (H + 8) * 2 <= 65536; E <= 256;
+ * alias x or res_in. M <= 16; H a multiple of 512, <= 4096, M * (H + 8) * 2 <= 131072; E <= 256;
  * M * topk <= 135. Library-owned counter: calls on one device must be stream-ordered. */
 int snowverify_norm_router_plan(const void* x, const void* res_in, void* res_out,
                                 const void* gamma, float eps, void* ws, void* y_out,

@@ -17,6 +17,8 @@
  *   probabilities   tests/test_dflash_sampling.py:199-209, snowllm/engine/request.py:29-35
  *   reject          tests/test_dflash_sampling.py:94-119
  *   sample          tests/test_dflash_sampling.py:212-217
+ *   penalties       snowllm/ops/sampling.py:94-100 (closed kernel: the published convention,
+ *                   pinned by tests/test_runtime_buffers.py:136-143 and exact-arithmetic cases)
  */
 #include <math.h>
 #include <stdint.h>
@@ -167,8 +169,6 @@ static int cmp_desc(const void* a, const void* b) {
   return x->idx < y->idx ? -1 : (x->idx > y->idx);
 }
 
-#define TOPK_MAX 1024
-
 int oc_topk_topp(const float* dense, float* values, int64_t* ids, int64_t rows, int64_t vocab,
                  int64_t width, const int32_t* top_k, const float* top_p) {
   int unsupported = 0;
@@ -188,7 +188,7 @@ int oc_topk_topp(const float* dense, float* values, int64_t* ids, int64_t rows, 
       }
       continue;
     }
-    if (k > TOPK_MAX || k > width) {
+    if (k > width) {  /* the list cannot hold the top k */
       for (int64_t i = 0; i < width; ++i) { ov[i] = NAN; oi[i] = -2; }
       unsupported = 1;
       continue;
@@ -198,7 +198,8 @@ int oc_topk_topp(const float* dense, float* values, int64_t* ids, int64_t rows, 
     uint64_t S = 0;
     for (int64_t i = 0; i < k; ++i) S += oc_fix(p[buf[i].idx]);
     const float Sf = oc_unfix(S);
-    uint64_t fix[TOPK_MAX];
+    uint64_t* fix = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)k);
+    int* dropped = (int*)malloc(sizeof(int) * (size_t)k);
     for (int64_t i = 0; i < k; ++i) {
       float v = Sf > 0.0f ? oc_div(p[buf[i].idx], Sf) : 0.0f;
       ov[i] = v;
@@ -206,10 +207,9 @@ int oc_topk_topp(const float* dense, float* values, int64_t* ids, int64_t rows, 
       fix[i] = oc_fix(v);
     }
     for (int64_t i = k; i < width; ++i) { ov[i] = 0.0f; oi[i] = -1; }
-    if (!nucleus) continue;
+    if (!nucleus) { free(fix); free(dropped); continue; }
     const double limit = (double)tp * (double)(1ull << FIX_BITS);
     uint64_t pre = 0, kept = 0;
-    int dropped[TOPK_MAX];
     for (int64_t i = 0; i < k; ++i) {
       int keep = (double)pre < limit;
       pre += fix[i];
@@ -219,9 +219,31 @@ int oc_topk_topp(const float* dense, float* values, int64_t* ids, int64_t rows, 
     const float Kf = oc_unfix(kept);
     for (int64_t i = 0; i < k; ++i)
       ov[i] = (dropped[i] || !(Kf > 0.0f)) ? 0.0f : oc_div(ov[i], Kf);
+    free(fix);
+    free(dropped);
   }
   free(buf);
   return unsupported;
+}
+
+/* ---- penalties: snowllm/ops/sampling.py:94-100, staged by snowllm/engine/sampler.py:187-220 --
+ * The reference kernel is closed; this restates the published convention of OpenAI-style
+ * sampling parameters (also the reference's own test expectation at
+ * tests/test_runtime_buffers.py:136-143: repetition 2 turns a logit of 8 into 4): a listed id's
+ * logit is divided by the repetition penalty when positive and multiplied by it otherwise,
+ * then frequency * count and presence (count > 0) are subtracted, one binary32 operation each. */
+void oc_penalties(float* logits, const int64_t* ids, const int32_t* counts, int64_t n,
+                  int64_t vocab, float presence, float frequency, float repetition) {
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t t = ids[i];
+    if (t < 0 || t >= vocab) continue;
+    const int c = counts[i];
+    float x = logits[t];
+    if (repetition != 1.0f) x = x > 0.0f ? x / repetition : x * repetition;
+    x = x - frequency * (float)c;
+    x = x - (c > 0 ? presence : 0.0f);
+    logits[t] = x;
+  }
 }
 
 /* ---- sample: pick = #(u >= cumsum(values)) clamped: tests/test_dflash_sampling.py:212-217 */

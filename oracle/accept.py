@@ -37,6 +37,7 @@ for name, res, args in [
     ("oc_softmax", None, [_P, _P, _I, _I, _P]),
     ("oc_topk_topp", ctypes.c_int, [_P, _P, _P, _I, _I, _I, _P, _P]),
     ("oc_pick_rows", None, [_P, _P, _I, _I, _P, _P]),
+    ("oc_penalties", None, [_P, _P, _P, _I, _I, ctypes.c_float, ctypes.c_float, ctypes.c_float]),
     ("oc_reject", None, [_P] * 10 + [_I] * 4),
     ("oc_round_bf16", ctypes.c_float, [ctypes.c_float]),
     ("oc_select_dot", ctypes.c_float, [_P, _P, _P, _I, ctypes.c_int]),
@@ -185,3 +186,13 @@ def select(hp, logits, pred, succ, anchor, temperature=None, uniform=None, slots
     _lib.oc_select(_ptr(h), _ptr(x), _ptr(pr), _ptr(sc), _ptr(a), _ptr(t), _ptr(u), _ptr(s),
                    _ptr(path), _ptr(cand), _ptr(q), b, ell, V, R)
     return path, cand, q
+
+
+def penalties(logits, ids, counts, presence, frequency, repetition):
+    """accept.c: oc_penalties on a copy of one logit row."""
+    x = _c(logits, np.float32).copy()
+    i = _c(ids, np.int64)
+    c = _c(counts, np.int32)
+    _lib.oc_penalties(_ptr(x), _ptr(i), _ptr(c), i.shape[0], x.shape[0], presence, frequency,
+                      repetition)
+    return x

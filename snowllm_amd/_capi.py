@@ -74,6 +74,7 @@ _SIGS = [
     ("snowllm_sampling_softmax", c_int, [P, P, c_int64, c_int64, P, S]),
     ("snowllm_sampling_topk_topp", c_int, [P, P, P, c_int64, c_int64, c_int64, P, P, S]),
     ("snowllm_sampling_sample", c_int, [P] * 7 + [c_int64] * 4 + [S]),
+    ("snowllm_sampling_penalties", c_int, [P, P, P, c_int, c_int, c_float, c_float, c_float, S]),
     ("snowllm_draft_reject", c_int, [P] * 10 + [c_int64] * 4 + [S]),
     ("snowverify_accept_reject", c_int, [P] * 10 + [c_int64] * 4 + [S]),
     ("snowverify_accept_greedy", c_int, [P] * 4 + [c_int64] * 3 + [S]),

@@ -228,15 +228,22 @@ int launch_qk_norm_rope_cache(const QkvSources& src, const void* q_gamma, const 
   return SV_OK;
 }
 
-// slot = table[row_seq, pos / page] * page + pos % page (snowllm/engine/spec_decode.py:183)
+// slot = table[row_seq, pos / page] * page + pos % page (snowllm/engine/spec_decode.py:183).
+// A row whose sequence or position is negative, whose page lies past the table's width, or
+// whose table entry is negative (padding) gets slot -1, which the cache writers skip.
 __global__ void resolve_slots_kernel(const int32_t* __restrict__ table, int64_t stride,
                                      const int32_t* __restrict__ seq, const int32_t* __restrict__ pos,
                                      int32_t* __restrict__ out, int64_t M, int64_t page) {
   const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (m >= M) return;
-  const int32_t p = pos[m];
+  const int64_t p = pos[m], b = seq[m];
+  if (p < 0 || b < 0) {
+    out[m] = -1;
+    return;
+  }
   const int64_t col = p / page;
-  out[m] = (col < stride) ? (int32_t)(table[seq[m] * stride + col] * page + p % page) : -1;
+  const int64_t blk = col < stride ? (int64_t)table[b * stride + col] : -1;
+  out[m] = blk >= 0 ? (int32_t)(blk * page + p % page) : -1;
 }
 
 // SwiGLU: out[m, i] = silu(gu[m, i]) * gu[m, F + i] (bf16)

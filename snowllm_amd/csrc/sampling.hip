@@ -278,14 +278,16 @@ __global__ void __launch_bounds__(TOPK_NT) topk_topp_rows(
     return;
   }
   if (chunk != 0) return;
-  if (k64 > TOPK_MAX || k64 > width) {
-    // Unsupported list shape: the row is marked with id -2 and NaN values.
+  if (k64 > width) {
+    // a top-k wider than the list cannot be written: the row is marked with id -2 and NaN
+    // values (callers size the width as the batch's largest top-k, as the reference's do)
     for (int64_t i = threadIdx.x; i < width; i += TOPK_NT) {
       out_v[i] = __builtin_nanf("");
       out_i[i] = -2;
     }
     return;
   }
+  if (k64 > TOPK_MAX) return;  // the wide-list kernels below write the row
   const int k = (int)k64;
   uint32_t tau;
   int above;
@@ -451,6 +453,310 @@ __device__ uint32_t count_in_chunk(const W& w, int64_t n, int c, uint64_t base, 
     }
   }
   return (uint32_t)block_sum_u64<NT>(cnt, red);
+}
+
+// ---------------------------------------------------------------------------------------
+// Wide candidate lists: rows whose top-k exceeds TOPK_MAX (up to the whole vocabulary, with
+// or without top-p). The whole row is sorted -- probability descending, ties to the lower id,
+// the order of the short lists above -- by a stable least-significant-digit radix sort of
+// (~ord_key(p), index) items over the 32 key bits, 8 bits per pass; each pass is a chunk
+// histogram, a per-row scan of (digit, chunk) counts and a stable scatter. The lists then get
+// the short lists' arithmetic on the sorted order: S = sum of the top k in fixed point,
+// v = p / S, the top-p cut at the first exclusive fixed-point prefix >= top_p * 2^44 (found
+// chunk by chunk), v / K over the kept prefix and 0 past it. The sorted items live in the
+// sampling workspace behind the candidate lists (snowllm_sampling_workspace_bytes reserves
+// them when width > TOPK_MAX).
+// ---------------------------------------------------------------------------------------
+constexpr int MODE_IDENT = 0, MODE_SMALL = 1, MODE_WIDE = 2, MODE_BAD = 3;
+
+__device__ __forceinline__ int list_mode(const int32_t* top_k, const float* top_p, int row,
+                                         int64_t V, int64_t width, int64_t* k_out,
+                                         bool* nucleus_out) {
+  int64_t k = top_k ? (int64_t)top_k[row] : V;
+  if (k <= 0 || k > V) k = V;
+  const float tp = top_p ? top_p[row] : 1.0f;
+  const bool nucleus = tp < 1.0f;
+  *k_out = k;
+  *nucleus_out = nucleus;
+  if (k >= V && !nucleus) return MODE_IDENT;
+  if (k > width) return MODE_BAD;
+  return k <= TOPK_MAX ? MODE_SMALL : MODE_WIDE;
+}
+
+struct WideArgs {
+  const float* dense;
+  const int32_t* top_k;
+  const float* top_p;
+  uint64_t* items[2];   // [rows, V] ping-pong
+  uint32_t* hist;       // [rows, 256, C]
+  uint64_t* part_s;     // [rows, C] fixed-point sums of the top k
+  uint64_t* part_v;     // [rows, C] fixed-point sums of v = p / S
+  uint64_t* cut;        // [rows, 2] first dropped position, kept sum K
+  int64_t V, width;
+  int C;
+};
+
+__device__ __forceinline__ uint64_t wide_item(float p, int64_t i) {
+  return ((uint64_t)(~ord_key(p)) << 32) | (uint64_t)(uint32_t)i;
+}
+
+__device__ __forceinline__ bool wide_row(const WideArgs& a, int row, int64_t* k, bool* nuc) {
+  return list_mode(a.top_k, a.top_p, row, a.V, a.width, k, nuc) == MODE_WIDE;
+}
+
+// Item e of the pass's input: pass 0 reads the probabilities themselves (index order).
+__device__ __forceinline__ uint64_t wide_load(const WideArgs& a, int pass, int row, int64_t e) {
+  if (pass == 0) return wide_item(a.dense[(int64_t)row * a.V + e], e);
+  return a.items[(pass - 1) & 1][(int64_t)row * a.V + e];
+}
+
+__global__ void __launch_bounds__(NT) wide_hist(WideArgs a, int pass) {
+  __shared__ uint32_t h[256];
+  const int c = blockIdx.x, row = blockIdx.y;
+  int64_t k;
+  bool nuc;
+  if (!wide_row(a, row, &k, &nuc)) return;
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const int shift = 32 + 8 * pass;
+  uint64_t it[RUN];
+#pragma unroll
+  for (int j = 0; j < RUN; ++j) {
+    const int64_t e = (int64_t)c * CHUNK + (int64_t)j * NT + threadIdx.x;
+    it[j] = wide_load(a, pass, row, e < a.V ? e : a.V - 1);
+  }
+#pragma unroll
+  for (int j = 0; j < RUN; ++j) {
+    const int64_t e = (int64_t)c * CHUNK + (int64_t)j * NT + threadIdx.x;
+    if (e < a.V) atomicAdd(&h[(uint32_t)(it[j] >> shift) & 0xffu], 1u);
+  }
+  __syncthreads();
+  a.hist[((int64_t)row * 256 + threadIdx.x) * a.C + c] = h[threadIdx.x];
+}
+
+// Exclusive scan of a row's (digit, chunk) counts, in place: one workgroup per row.
+constexpr int WIDE_SCAN_NT = 1024;
+__global__ void __launch_bounds__(WIDE_SCAN_NT) wide_scan(WideArgs a) {
+  __shared__ uint32_t buf[WIDE_SCAN_NT];
+  const int row = blockIdx.x;
+  int64_t k;
+  bool nuc;
+  if (!wide_row(a, row, &k, &nuc)) return;
+  uint32_t* h = a.hist + (int64_t)row * 256 * a.C;
+  const int n = 256 * a.C;
+  const int per = (n + WIDE_SCAN_NT - 1) / WIDE_SCAN_NT;
+  const int lo = threadIdx.x * per;
+  uint32_t run = 0;
+  for (int i = lo; i < lo + per && i < n; ++i) run += h[i];
+  buf[threadIdx.x] = run;
+  __syncthreads();
+  for (int off = 1; off < WIDE_SCAN_NT; off <<= 1) {
+    const uint32_t v = threadIdx.x >= (unsigned)off ? buf[threadIdx.x - off] : 0u;
+    __syncthreads();
+    buf[threadIdx.x] += v;
+    __syncthreads();
+  }
+  uint32_t pre = buf[threadIdx.x] - run;
+  for (int i = lo; i < lo + per && i < n; ++i) {
+    const uint32_t v = h[i];
+    h[i] = pre;
+    pre += v;
+  }
+}
+
+// Stable scatter: element e = c * CHUNK + j * NT + t goes in round j, lane order within the
+// round, so ranks follow e. A wave finds the lanes sharing its digit with eight ballots.
+__global__ void __launch_bounds__(NT) wide_scatter(WideArgs a, int pass) {
+  __shared__ uint32_t base[256];
+  __shared__ uint32_t wcnt[NT / WAVE][256];
+  const int c = blockIdx.x, row = blockIdx.y;
+  int64_t k;
+  bool nuc;
+  if (!wide_row(a, row, &k, &nuc)) return;
+  const int t = threadIdx.x, w = t / WAVE, lane = t % WAVE;
+  const int shift = 32 + 8 * pass;
+  base[t] = a.hist[((int64_t)row * 256 + t) * a.C + c];
+#pragma unroll
+  for (int ww = 0; ww < NT / WAVE; ++ww) wcnt[ww][t] = 0u;
+  uint64_t it[RUN];
+#pragma unroll
+  for (int j = 0; j < RUN; ++j) {
+    const int64_t e = (int64_t)c * CHUNK + (int64_t)j * NT + t;
+    it[j] = wide_load(a, pass, row, e < a.V ? e : a.V - 1);
+  }
+  uint64_t* out = a.items[pass & 1] + (int64_t)row * a.V;
+  const uint64_t below = (1ull << lane) - 1ull;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < RUN; ++j) {
+    const int64_t e = (int64_t)c * CHUNK + (int64_t)j * NT + t;
+    const bool live = e < a.V;
+    const uint32_t d = (uint32_t)(it[j] >> shift) & 0xffu;
+    uint64_t same = __ballot(live);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const uint64_t ones = __ballot((d >> b) & 1u);
+      same &= ((d >> b) & 1u) ? ones : ~ones;
+    }
+    const uint32_t rank = (uint32_t)__popcll(same & below);
+    if (live && rank == 0) wcnt[w][d] = (uint32_t)__popcll(same);
+    __syncthreads();
+    if (live) {
+      uint32_t pos = base[d] + rank;
+      for (int ww = 0; ww < w; ++ww) pos += wcnt[ww][d];
+      out[pos] = it[j];
+    }
+    __syncthreads();
+    uint32_t tot = 0;
+#pragma unroll
+    for (int ww = 0; ww < NT / WAVE; ++ww) {
+      tot += wcnt[ww][t];
+      wcnt[ww][t] = 0u;
+    }
+    base[t] += tot;
+    __syncthreads();
+  }
+}
+
+// p of sorted position i (the probability itself, read back by its index).
+__device__ __forceinline__ float wide_p(const WideArgs& a, int row, uint64_t item) {
+  return a.dense[(int64_t)row * a.V + (uint32_t)item];
+}
+
+__device__ __forceinline__ float wide_sum_f(const uint64_t* part, int C, uint64_t* red) {
+  uint64_t s = 0;
+  for (int i = threadIdx.x; i < C; i += NT) s += part[i];
+  return canon_unfix(block_sum_u64<NT>(s, red));
+}
+
+// Fixed-point sums of the top k per chunk of the sorted row.
+__global__ void __launch_bounds__(NT) wide_sums(WideArgs a) {
+  __shared__ uint64_t red[NT / WAVE];
+  const int c = blockIdx.x, row = blockIdx.y;
+  int64_t k;
+  bool nuc;
+  if (!wide_row(a, row, &k, &nuc)) return;
+  const uint64_t* it = a.items[1] + (int64_t)row * a.V;
+  uint64_t s = 0;
+  for (int j = 0; j < RUN; ++j) {
+    const int64_t i = (int64_t)c * CHUNK + (int64_t)j * NT + threadIdx.x;
+    if (i < k) s += canon_fix(wide_p(a, row, it[i]));
+  }
+  s = block_sum_u64<NT>(s, red);
+  if (threadIdx.x == 0) a.part_s[(int64_t)row * a.C + c] = s;
+}
+
+// v = p / S over the top k, and its fixed-point sums per chunk (nucleus rows).
+__global__ void __launch_bounds__(NT) wide_vsums(WideArgs a) {
+  __shared__ uint64_t red[NT / WAVE];
+  const int c = blockIdx.x, row = blockIdx.y;
+  int64_t k;
+  bool nuc;
+  if (!wide_row(a, row, &k, &nuc) || !nuc) return;
+  const float Sf = wide_sum_f(a.part_s + (int64_t)row * a.C, a.C, red);
+  const uint64_t* it = a.items[1] + (int64_t)row * a.V;
+  uint64_t s = 0;
+  for (int j = 0; j < RUN; ++j) {
+    const int64_t i = (int64_t)c * CHUNK + (int64_t)j * NT + threadIdx.x;
+    if (i < k) s += canon_fix(Sf > 0.0f ? canon_div(wide_p(a, row, it[i]), Sf) : 0.0f);
+  }
+  s = block_sum_u64<NT>(s, red);
+  if (threadIdx.x == 0) a.part_v[(int64_t)row * a.C + c] = s;
+}
+
+// The top-p cut: position `cut` of the first element whose exclusive prefix reaches the limit
+// (k when none does) and the kept sum K. One workgroup per nucleus row.
+__global__ void __launch_bounds__(NT) wide_cut(WideArgs a) {
+  __shared__ uint64_t buf[NT];
+  __shared__ uint64_t red[NT / WAVE];
+  __shared__ int s_chunk;
+  __shared__ uint64_t s_base;
+  const int row = blockIdx.x;
+  int64_t k;
+  bool nuc;
+  if (!wide_row(a, row, &k, &nuc) || !nuc) return;
+  const double limit = (double)a.top_p[row] * (double)(1ull << SV_FIX_BITS);
+  const uint64_t* pv = a.part_v + (int64_t)row * a.C;
+  const float Sf = wide_sum_f(a.part_s + (int64_t)row * a.C, a.C, red);
+  if (threadIdx.x == 0) {
+    uint64_t pre = 0;
+    int c = 0;
+    for (; c < a.C; ++c) {
+      if ((double)(pre + pv[c]) >= limit) break;
+      pre += pv[c];
+    }
+    s_chunk = c;
+    s_base = pre;
+  }
+  __syncthreads();
+  const int c = s_chunk;
+  uint64_t cut = (uint64_t)k, kept = s_base;
+  if (c < a.C) {
+    // exclusive prefixes inside chunk c, thread t owning RUN consecutive positions
+    const uint64_t* it = a.items[1] + (int64_t)row * a.V;
+    const int64_t lo = (int64_t)c * CHUNK + (int64_t)threadIdx.x * RUN;
+    uint64_t f[RUN];
+    uint64_t run = 0;
+#pragma unroll
+    for (int j = 0; j < RUN; ++j) {
+      const int64_t i = lo + j;
+      f[j] = i < k ? canon_fix(Sf > 0.0f ? canon_div(wide_p(a, row, it[i]), Sf) : 0.0f) : 0ull;
+      run += f[j];
+    }
+    uint64_t pre = s_base + block_exclusive_scan_u64<NT>(run, buf);
+    uint64_t n_keep = 0, keep_sum = 0;
+#pragma unroll
+    for (int j = 0; j < RUN; ++j) {
+      if (lo + j < k && (double)pre < limit) {
+        ++n_keep;
+        keep_sum += f[j];
+      }
+      pre += f[j];
+    }
+    n_keep = block_sum_u64<NT>(n_keep, red);
+    keep_sum = block_sum_u64<NT>(keep_sum, red);
+    cut = (uint64_t)c * CHUNK + n_keep;
+    kept = s_base + keep_sum;
+  } else {
+    uint64_t s = 0;
+    for (int i = threadIdx.x; i < a.C; i += NT) s += pv[i];
+    kept = block_sum_u64<NT>(s, red);
+  }
+  if (threadIdx.x == 0) {
+    a.cut[(int64_t)row * 2 + 0] = cut;
+    a.cut[(int64_t)row * 2 + 1] = kept;
+  }
+}
+
+// The lists: sorted ids, v = p / S (then v / K inside the top-p prefix, 0 past it); slots
+// past k are (0, -1).
+__global__ void __launch_bounds__(NT) wide_write(WideArgs a, float* __restrict__ values,
+                                                 int64_t* __restrict__ ids) {
+  __shared__ uint64_t red[NT / WAVE];
+  const int c = blockIdx.x, row = blockIdx.y;
+  int64_t k;
+  bool nuc;
+  if (!wide_row(a, row, &k, &nuc)) return;
+  const float Sf = wide_sum_f(a.part_s + (int64_t)row * a.C, a.C, red);
+  const int64_t cut = nuc ? (int64_t)a.cut[(int64_t)row * 2 + 0] : k;
+  const float Kf = nuc ? canon_unfix(a.cut[(int64_t)row * 2 + 1]) : 1.0f;
+  const uint64_t* it = a.items[1] + (int64_t)row * a.V;
+  float* ov = values + (int64_t)row * a.width;
+  int64_t* oi = ids + (int64_t)row * a.width;
+  for (int j = 0; j < RUN; ++j) {
+    const int64_t i = (int64_t)c * CHUNK + (int64_t)j * NT + threadIdx.x;
+    if (i >= a.width) break;
+    if (i < k) {
+      const uint64_t item = it[i];
+      float v = Sf > 0.0f ? canon_div(wide_p(a, row, item), Sf) : 0.0f;
+      if (nuc) v = (i >= cut || !(Kf > 0.0f)) ? 0.0f : canon_div(v, Kf);
+      ov[i] = v;
+      oi[i] = (int64_t)(uint32_t)item;
+    } else {
+      ov[i] = 0.0f;
+      oi[i] = -1;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -789,6 +1095,30 @@ __global__ void __launch_bounds__(NT) sample_pick(const float* __restrict__ valu
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Repetition / frequency / presence penalties on one logit row, for the listed token ids
+// (the prompt's and output's ids of a request, each once) with their output counts: the
+// repetition penalty divides a positive logit and multiplies a non-positive one, then the
+// frequency penalty times the count and the presence penalty (count > 0) are subtracted, one
+// binary32 operation each (the published convention of OpenAI-style sampling parameters).
+// ---------------------------------------------------------------------------------------
+__global__ void penalties_kernel(float* __restrict__ logits, const int64_t* __restrict__ ids,
+                                 const int32_t* __restrict__ counts, int n, int vocab,
+                                 float presence, float frequency, float repetition) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t t = ids[i];
+  if (t < 0 || t >= vocab) return;
+  const int c = counts[i];
+  float x = logits[t];
+  // plain operators: this file's contract(off) keeps the product and the difference apart
+  // (the __f*_rn helpers are header code that the compiler may fuse into an fma)
+  if (repetition != 1.0f) x = x > 0.0f ? x / repetition : x * repetition;
+  x = x - frequency * (float)c;
+  x = x - (c > 0 ? presence : 0.0f);
+  logits[t] = x;
+}
+
 inline hipStream_t S(void* s) { return (hipStream_t)s; }
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -832,8 +1162,23 @@ SV_API int snowllm_spec_accept(const int64_t* tokens, const int64_t* drafts, int
 // Workspace: dense probabilities [batch, vocab] f32, then the softmax row statistics, then
 // the candidate lists used by snowllm_sampling_sample (values f32 and ids i64 [batch, width])
 // and their chunk sums.
-SV_API int64_t snowllm_sampling_workspace_bytes(int64_t batch, int64_t vocab, int64_t width) {
-  if (batch < 0 || vocab <= 0) return 0;
+// Penalties on one logit row (snowllm/_capi.py:589; wrapper snowllm/ops/sampling.py:94-100).
+SV_API int snowllm_sampling_penalties(float* logits, const int64_t* ids, const int32_t* counts,
+                                      int n, int vocab, float presence, float frequency,
+                                      float repetition, void* stream) {
+  if (n < 0 || vocab <= 0 || !(repetition > 0.0f)) return SV_EINVAL;
+  if (n == 0) return SV_OK;
+  if (!logits || !ids || !counts) return SV_EINVAL;
+  hipLaunchKernelGGL(penalties_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     S(stream), logits, ids, counts, n, vocab, presence, frequency, repetition);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// Lists wider than TOPK_MAX add the wide-list sort: two [batch, vocab] u64 item buffers, the
+// per-pass chunk histograms and the per-row sums.
+namespace {
+size_t lists_bytes(int64_t batch, int64_t vocab, int64_t width) {
   const int64_t C = chunks_of(vocab);
   const int64_t Cw = chunks_of(width > 0 ? width : 1);
   size_t bytes = align256((size_t)batch * vocab * 4);
@@ -842,6 +1187,43 @@ SV_API int64_t snowllm_sampling_workspace_bytes(int64_t batch, int64_t vocab, in
   bytes += align256((size_t)batch * width * 4);
   bytes += align256((size_t)batch * width * 8);
   bytes += align256((size_t)batch * Cw * 8);
+  return bytes;
+}
+
+WideArgs wide_view(const float* dense, int64_t rows, int64_t vocab, int64_t width,
+                   const int32_t* top_k, const float* top_p) {
+  const int64_t C = chunks_of(vocab);
+  char* p = (char*)dense + lists_bytes(rows, vocab, width);
+  WideArgs a;
+  a.dense = dense;
+  a.top_k = top_k;
+  a.top_p = top_p;
+  a.items[0] = (uint64_t*)p;
+  p += align256((size_t)rows * vocab * 8);
+  a.items[1] = (uint64_t*)p;
+  p += align256((size_t)rows * vocab * 8);
+  a.hist = (uint32_t*)p;
+  p += align256((size_t)rows * 256 * C * 4);
+  a.part_s = (uint64_t*)p;
+  p += align256((size_t)rows * C * 8);
+  a.part_v = (uint64_t*)p;
+  p += align256((size_t)rows * C * 8);
+  a.cut = (uint64_t*)p;
+  a.V = vocab;
+  a.width = width;
+  a.C = (int)C;
+  return a;
+}
+}  // namespace
+
+SV_API int64_t snowllm_sampling_workspace_bytes(int64_t batch, int64_t vocab, int64_t width) {
+  if (batch < 0 || vocab <= 0) return 0;
+  size_t bytes = lists_bytes(batch, vocab, width);
+  if (width > TOPK_MAX) {
+    const int64_t C = chunks_of(vocab);
+    bytes += 2 * align256((size_t)batch * vocab * 8) + align256((size_t)batch * 256 * C * 4) +
+             2 * align256((size_t)batch * C * 8) + align256((size_t)batch * 16);
+  }
   return (int64_t)bytes;
 }
 
@@ -883,6 +1265,28 @@ int launch_topk_topp(const float* dense, float* values, int64_t* ids, int64_t ro
   hipLaunchKernelGGL(topk_topp_rows, dim3((unsigned)rows, (unsigned)chunks_of(width)),
                      dim3(TOPK_NT), 0, s, dense, values, ids, vocab, width, top_k, top_p);
   SV_CHECK_LAUNCH();
+  if (width <= TOPK_MAX) return SV_OK;  // no row can need a wide list
+  if (rows > 65535) return SV_ENOTSUP;    // rows are the grids' y dimension
+  // rows wider than TOPK_MAX: sort, sums, top-p cut, lists (the other rows return at once)
+  const WideArgs a = wide_view(dense, rows, vocab, width, top_k, top_p);
+  const dim3 grid((unsigned)a.C, (unsigned)rows);
+  for (int pass = 0; pass < 4; ++pass) {
+    hipLaunchKernelGGL(wide_hist, grid, dim3(NT), 0, s, a, pass);
+    SV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(wide_scan, dim3((unsigned)rows), dim3(WIDE_SCAN_NT), 0, s, a);
+    SV_CHECK_LAUNCH();
+    hipLaunchKernelGGL(wide_scatter, grid, dim3(NT), 0, s, a, pass);
+    SV_CHECK_LAUNCH();
+  }
+  hipLaunchKernelGGL(wide_sums, grid, dim3(NT), 0, s, a);
+  SV_CHECK_LAUNCH();
+  hipLaunchKernelGGL(wide_vsums, grid, dim3(NT), 0, s, a);
+  SV_CHECK_LAUNCH();
+  hipLaunchKernelGGL(wide_cut, dim3((unsigned)rows), dim3(NT), 0, s, a);
+  SV_CHECK_LAUNCH();
+  hipLaunchKernelGGL(wide_write, dim3((unsigned)chunks_of(width), (unsigned)rows), dim3(NT), 0,
+                     s, a, values, ids);
+  SV_CHECK_LAUNCH();
   return SV_OK;
 }
 }  // namespace
@@ -894,8 +1298,10 @@ SV_API int snowllm_sampling_softmax(const float* logits, float* dense, int64_t r
   return launch_softmax(logits, dense, rows, vocab, temperature, S(stream));
 }
 
-// Rows whose top-k exceeds 1024 without keeping the whole vocabulary (or with top-p below 1
-// over the whole vocabulary) are not supported: they are written as (NaN, -2).
+// Every top-k up to the vocabulary, with or without top-p. `dense` must be the start of a
+// workspace of snowllm_sampling_workspace_bytes(rows, vocab, width) bytes (the wide lists
+// sort behind the dense block). A row whose top-k exceeds `width` cannot be written and
+// comes out as (NaN, -2); callers size the width as the largest top-k of the batch.
 SV_API int snowllm_sampling_topk_topp(const float* dense, float* values, int64_t* ids,
                                       int64_t rows, int64_t vocab, int64_t width,
                                       const int32_t* top_k, const float* top_p, void* stream) {
@@ -1483,10 +1889,11 @@ SV_API int snowverify_accept_reject(const float* logits, const float* temperatur
                                     const float* uniform, int64_t* out, int64_t* accepted,
                                     int64_t b, int64_t width, int64_t vocab, int64_t q_width,
                                     void* stream) {
-  if (b <= 0 || width < 1 || width > 64 || b * width > FA_ROWS || vocab <= 0 ||
-      vocab > VOCAB_MAX || q_width < 0 || !logits || !slots || !valid || !uniform || !out ||
-      !accepted || (width > 1 && !drafts))
+  if (b <= 0 || width < 1 || vocab <= 0 || q_width < 0 || !logits || !slots || !valid ||
+      !uniform || !out || !accepted || (width > 1 && !drafts))
     return SV_EINVAL;
+  // beyond the fused kernels' shapes: the caller takes probabilities + draft_reject
+  if (width > 64 || b * width > FA_ROWS || vocab > VOCAB_MAX) return SV_ENOTSUP;
   const int P = fa_slices(vocab);
   FaArgs a{logits, temperature, drafts, cand, q, slots, valid, uniform, out, accepted,
            (int)vocab, (int)width, P, q_width};
@@ -1512,9 +1919,11 @@ SV_API int snowverify_accept_reject(const float* logits, const float* temperatur
 SV_API int snowverify_accept_greedy(const float* logits, const int64_t* drafts, int64_t* tokens,
                                     int64_t* accepted, int64_t b, int64_t width, int64_t vocab,
                                     void* stream) {
-  if (b <= 0 || width < 1 || width > 64 || b * width > FA_ROWS || vocab <= 0 ||
-      vocab > VOCAB_MAX || !logits || !tokens || !accepted || (width > 1 && !drafts))
+  if (b <= 0 || width < 1 || vocab <= 0 || !logits || !tokens || !accepted ||
+      (width > 1 && !drafts))
     return SV_EINVAL;
+  // beyond the fused kernel's shapes: the caller takes argmax + spec_accept
+  if (width > 64 || b * width > FA_ROWS || vocab > VOCAB_MAX) return SV_ENOTSUP;
   const int P = fa_slices(vocab);
   FaArgs a{logits, nullptr, drafts, nullptr, nullptr, nullptr, nullptr, nullptr, tokens,
            accepted, (int)vocab, (int)width, P, 0};

@@ -1,54 +1,44 @@
 """The DFlash/DSpark verify-side acceptance and its dispatch (snowllm/engine/dflash_sampling.py:
 8-69), on this build's kernels.
 
-Per verify step, for a batch of requests each holding k drafts (block width k + 1):
+Per verify step, for a batch of requests each holding k drafts (block width k + 1), after the
+sampler's penalties and no-repeat-n-gram masks on the logits (snowllm/engine/sampler.py:
+84-117):
 
 - every request greedy (temperature <= 0): argmax of every row, then 1 + leading matches
-  (snowllm/engine/dflash_sampling.py:56-59) -- one launch (snowverify_accept_greedy);
+  (snowllm/engine/dflash_sampling.py:56-59, where Sampler.sample takes ops.argmax when every
+  row is greedy) -- one launch (snowverify_accept_greedy);
 - otherwise target probabilities with each request's sampling parameters, then rejection
   sampling against the draft's 16-candidate proposal, read at the request's stable slot
   (snowllm/engine/dflash_sampling.py:60-69): `valid` is 1 when the request's drafts are the
   proposal remembered for its slot, uniforms are drawn as [count, width]. When every request
   keeps the whole vocabulary (top-k covering it, top-p 1) this runs straight from the logits
   without materialising probabilities (snowverify_accept_reject, three launches); otherwise
-  snowllm_sampling_softmax + _topk_topp and snowllm_draft_reject.
+  the sampler's probability lists (snowllm_sampling_softmax + _topk_topp, any top-k and
+  top-p) and snowllm_draft_reject.
 
-The argmax of the greedy branch is the logits' (NaN as -inf, ties to the first index, as
-ops.argmax); the reference's branch samples each row's top-1 list, which names the same token
-except where two probabilities round to the same value.
+Per-step parameters go through pinned staging buffers reserved once (sampler.Staged).
 """
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import ops
 from ._capi import SnowLLMError
 from .dflash import SELECTOR_TOP_K, accept_greedy, accept_reject, reject, select_path
-
-
-@dataclass
-class SamplingParams:
-    """The per-request parameters the verify dispatch reads (snowllm/engine/request.py:
-    12-35)."""
-    temperature: float = 0.0
-    top_k: int = 0
-    top_p: float = 1.0
-
-    def kernel_top_k(self) -> int:                       # request.py:29-32
-        if self.temperature <= 0.0:
-            return 1
-        return self.top_k if 0 < self.top_k <= ops.SAMPLING_MAX_K else ops.SAMPLING_MAX_K
-
-    def kernel_temperature(self) -> float:               # request.py:34-35
-        return self.temperature if self.temperature > 0.0 else 1.0
+from .sampler import Sampler, SamplingParams, Staged  # noqa: F401  (SamplingParams re-exported)
 
 
 @dataclass(eq=False)
 class VerifyRequest:
-    """One request of a verify batch: its stable slot, sampling parameters and drafts."""
+    """One request of a verify batch: its stable slot, sampling parameters and drafts, and
+    the prompt and output ids the penalties and n-gram masks read."""
     slot: int
     params: SamplingParams
     drafts: tuple = ()
+    prompt: tuple = ()
+    out: list = field(default_factory=list)
 
 
 class DFlashAcceptance:
@@ -57,10 +47,16 @@ class DFlashAcceptance:
     pool the selector fills, and the verify dispatch."""
 
     def __init__(self, max_seqs: int, block: int, vocab: int, *, seed: int = 0,
-                 selector_top_k: int = SELECTOR_TOP_K):
+                 selector_top_k: int = SELECTOR_TOP_K, sampler: Sampler = None,
+                 max_tokens: int = 4096):
         dev = "cuda"
         self.block, self.length, self.vocab = block, block - 1, vocab
-        self.rng = torch.Generator(device=dev).manual_seed(seed)
+        if sampler is None:
+            sampler = Sampler(seed=seed)
+            sampler.reserve(max_seqs * block, vocab, max_tokens=max_tokens,
+                            max_requests=max_seqs)
+        self.sampler = sampler
+        self.rng = sampler.rng
         self.proposals = [None] * max_seqs
         self.temperature = torch.zeros(max_seqs, dtype=torch.float32, device=dev)
         self.slots = torch.arange(max_seqs, dtype=torch.int32, device=dev)
@@ -73,9 +69,12 @@ class DFlashAcceptance:
         self.width_max = min(vocab, ops.SAMPLING_MAX_K)
         self.p = torch.empty(rows * self.width_max, dtype=torch.float32, device=dev)
         self.p_ids = torch.empty(rows * self.width_max, dtype=torch.int64, device=dev)
-        self.ws = torch.empty(ops.sample_workspace_bytes(rows, vocab, self.width_max),
-                              dtype=torch.uint8, device=dev)
         self.tokens = torch.empty(rows, dtype=torch.int64, device=dev)
+        self.staged_temp = Staged(max_seqs, torch.float32)
+        self.staged_slots = Staged(max_seqs, torch.int32)
+        self.verify_slots = Staged(max_seqs, torch.int32)
+        self.verify_valid = Staged(max_seqs, torch.int32)
+        self.verify_temp = Staged(rows, torch.float32)
         self.accepted = torch.empty(max_seqs, dtype=torch.int64, device=dev)
         self.verify_uniform = torch.empty(rows, dtype=torch.float32, device=dev)
         self.path = None  # which branch the last verify took: "greedy", "fused", "lists"
@@ -86,8 +85,9 @@ class DFlashAcceptance:
         samples."""
         count = len(batch)
         temps = [r.params.temperature for r in batch]
-        self.temperature[:count].copy_(torch.tensor(temps, dtype=torch.float32))
-        self.slots[:count].copy_(torch.tensor([r.slot for r in batch], dtype=torch.int32))
+        self.temperature[:count].copy_(self.staged_temp.write(np.asarray(temps, np.float32)))
+        self.slots[:count].copy_(self.staged_slots.write(
+            np.asarray([r.slot for r in batch], np.int32)))
         if any(t > 0 for t in temps):
             self.uniform[:count].uniform_(generator=self.rng)
 
@@ -115,39 +115,38 @@ class DFlashAcceptance:
 
     # -- verify (dflash_sampling.py:54-69) ---------------------------------------------------
     def verify(self, logits, batch, drafts):
-        """logits [count * width, V] of the verify block, drafts [count, width - 1] int64 on
-        the device -> (tokens [count, width], accepted [count])."""
+        """logits [count * width, V] of the verify block (penalties and n-gram masks are
+        applied to them in place), drafts [count, width - 1] int64 on the device ->
+        (tokens [count, width], accepted [count])."""
         count, width = len(batch), self.block
         if logits.shape != (count * width, self.vocab):
             raise SnowLLMError(f"verify logits must be [{count * width}, {self.vocab}]")
         tokens = self.tokens[:count * width].view(count, width)
         accepted = self.accepted[:count]
+        rows = [r for r in batch for _ in range(width)]
         if all(r.params.temperature <= 0 for r in batch):
             self.path = "greedy"
+            self.sampler.prepare(logits, rows)
             if not accept_greedy(logits, drafts, tokens, accepted):
                 ops.argmax(logits, out=tokens.view(-1))
                 ops.spec_accept(tokens, drafts, out=accepted)
             return tokens, accepted
-        rows = [r for r in batch for _ in range(width)]
-        valid = torch.tensor([int(tuple(r.drafts) == self.proposals[r.slot]) for r in batch],
-                             dtype=torch.int32, device="cuda")
-        slots = torch.tensor([r.slot for r in batch], dtype=torch.int32, device="cuda")
+        valid = self.verify_valid.write(np.asarray(
+            [int(tuple(r.drafts) == self.proposals[r.slot]) for r in batch], np.int32))
+        slots = self.verify_slots.write(np.asarray([r.slot for r in batch], np.int32))
         uniform = self.verify_uniform[:count * width].view(count, width)
         uniform.uniform_(generator=self.rng)
-        temp = torch.tensor([r.params.kernel_temperature() for r in rows], dtype=torch.float32,
-                            device="cuda")
         ks = [r.params.kernel_top_k() for r in rows]
         whole = all(k >= self.vocab for k in ks) and all(r.params.top_p >= 1.0 for r in rows)
-        if whole and accept_reject(logits, drafts, self.candidates, self.q, slots, valid,
-                                   uniform, tokens, accepted, temperature=temp):
-            self.path = "fused"
-            return tokens, accepted
+        self.sampler.prepare(logits, rows)
+        if whole:
+            temp = self.verify_temp.write(np.asarray([r.params.kernel_temperature() for r in rows],
+                                                     np.float32))
+            if accept_reject(logits, drafts, self.candidates, self.q, slots, valid, uniform,
+                             tokens, accepted, temperature=temp):
+                self.path = "fused"
+                return tokens, accepted
         self.path = "lists"
-        width_p = min(max(ks), self.vocab)
-        n = len(rows) * width_p
-        p, ids = self.p[:n].view(-1, width_p), self.p_ids[:n].view(-1, width_p)
-        top_k = torch.tensor(ks, dtype=torch.int32, device="cuda")
-        top_p = torch.tensor([r.params.top_p for r in rows], dtype=torch.float32, device="cuda")
-        ops.probabilities(logits, top_k, top_p, temp, width_p, p, ids, self.ws)
+        p, ids = self.sampler.probabilities(logits, rows, self.p, self.p_ids, prepared=True)
         reject(p, ids, drafts, self.candidates, self.q, slots, valid, uniform, tokens, accepted)
         return tokens, accepted

@@ -1,3 +1,8 @@
+# SPDX-License-Identifier: Apache-2.0
+# The function names, arguments, results, error texts and the steps of the algorithm here follow
+# snowllm/engine/dspark_schedule.py (SPDX-FileCopyrightText: Copyright contributors to the
+# SnowLLM project), which this module keeps so that the reference's callers choose the same
+# prefixes with it.
 """Adaptive verify-prefix scheduling for DSpark drafts (snowllm/engine/dspark_schedule.py:7-85,
 used by snowllm/engine/spec_decode.py:143-166), with the same functions, arguments, results and
 errors, on step costs measured on this build's verify step (profile_step_costs).

@@ -80,3 +80,14 @@ def probabilities(logits, top_k, top_p, temperature, width, out, indices, worksp
                                        _stream()), "sampling_softmax")
     check(lib.snowllm_sampling_topk_topp(_p(dense), _p(out), _p(indices), rows, vocab, width,
                                          _p(top_k), _p(top_p), _stream()), "sampling_topk_topp")
+
+
+def penalties(logits, ids, counts, presence, frequency, repetition):
+    """Repetition / frequency / presence penalties on one logit row for the listed token ids
+    and their output counts (ops/sampling.py:94-100)."""
+    _chk(logits, "penalty logits", torch.float32, logits.numel())
+    _chk(ids, "penalty token IDs", torch.int64, ids.numel())
+    _chk(counts, "penalty counts", torch.int32, ids.numel())
+    check(lib.snowllm_sampling_penalties(_p(logits), _p(ids), _p(counts), ids.numel(),
+                                         logits.numel(), presence, frequency, repetition,
+                                         _stream()), "sampling_penalties")

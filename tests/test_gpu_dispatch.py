@@ -167,7 +167,7 @@ def test_verify_dispatch_branches_bit_exact(gpu):
     batches = {
         "greedy": [SamplingParams(0.0), SamplingParams(-1.0)],
         "fused": [SamplingParams(1.0), SamplingParams(0.8, top_k=0), SamplingParams(1.2)],
-        "lists": [SamplingParams(0.0), SamplingParams(1.0), SamplingParams(0.7, 50, 0.9)],
+        "lists": [SamplingParams(0.0), SamplingParams(1.0), SamplingParams(0.7, top_k=50, top_p=0.9)],
     }
     for want_path, params in batches.items():
         count = len(params)

@@ -170,3 +170,84 @@ def test_probabilities_match_reference_target_probabilities():
     picked = (torch.from_numpy(uniform)[:, None] >= torch.from_numpy(values).cumsum(-1)).sum(-1).clamp_max(66)
     want = torch.from_numpy(ids).gather(1, picked[:, None]).view(-1)
     assert np.array_equal(A.pick_rows(values, ids, uniform), want.numpy())
+
+
+def test_wide_lists_match_reference_target_probabilities():
+    """Lists of any width: top-k beyond 1024 and top-p over the whole vocabulary
+    (snowllm/engine/request.py:29-35 gives top_k 0 the whole vocabulary), against the
+    reference test's torch semantics (tests/test_dflash_sampling.py:199-209) at V = 151,936:
+    the same distribution, the same number of kept tokens, and the kept ids in the order of
+    torch's stable descending sort of the probabilities."""
+    V = 151936
+    g = torch.Generator().manual_seed(5)
+    params = [(1., 0, .9), (1., 2000, 1.), (.8, 5000, .7), (1.3, 1500, .95)]
+    logits = torch.randn(len(params), V, generator=g) * 2
+    temp = torch.tensor([t for t, _, _ in params])
+    top_k = torch.tensor([k if 0 < k <= V else V for _, k, _ in params], dtype=torch.int32)
+    top_p = torch.tensor([p for _, _, p in params])
+    values, ids = A.probabilities(logits.numpy(), top_k.numpy(), top_p.numpy(), temp.numpy(), V)
+    actual = torch.zeros(len(params), V).scatter_add_(
+        1, torch.from_numpy(ids).clamp_min(0), torch.from_numpy(values))
+    expected = R.target_probabilities(logits, temp, top_k, top_p)
+    for i, (t, k, p) in enumerate(params):
+        err = ((actual[i] - expected[i]).norm() / expected[i].norm()).item()
+        assert err < 1e-6, (i, err)
+        kept = int((expected[i] > 0).sum())
+        assert int((torch.from_numpy(values[i]) > 0).sum()) == kept
+        order = torch.sort((logits[i] / t).softmax(-1), descending=True, stable=True).indices
+        assert np.array_equal(ids[i, :kept], order[:kept].numpy()), i
+        width = k if 0 < k <= V else V
+        assert (ids[i, width:] == -1).all() and (values[i, kept:] == 0).all()
+
+
+def test_lists_narrower_than_top_k_are_marked():
+    """A row whose top-k does not fit the list width is written as (NaN, -2) and reported."""
+    logits = np.random.default_rng(1).standard_normal((2, 300)).astype(np.float32)
+    dense = A.softmax(logits)
+    values, ids, bad = A.topk_topp(dense, 40, np.array([50, 10], np.int32),
+                                   np.array([1., .9], np.float32))
+    assert bad and (ids[0] == -2).all() and np.isnan(values[0]).all()
+    assert (ids[1, :10] >= 0).all() and (ids[1, 10:] == -1).all()
+
+
+def test_banned_ngram_tokens_known_answers():
+    # the reference's own cases (tests/test_mineru.py:123-128)
+    from snowllm_amd.ngram import banned_ngram_tokens
+    assert banned_ngram_tokens([1, 2, 3, 1, 2], 3) == [3]
+    assert banned_ngram_tokens([1, 2, 3, 1, 4], 3) == []
+    assert banned_ngram_tokens([3, 1, 3], 1) == [1, 3]
+    assert banned_ngram_tokens([1, 2], 0) == []
+    assert banned_ngram_tokens([1, 2], 4) == []
+    # brute force over short streams
+    rng = np.random.default_rng(2)
+    for _ in range(200):
+        toks = rng.integers(0, 4, rng.integers(0, 9)).tolist()
+        size = int(rng.integers(0, 5))
+        want = set()
+        if size > 0 and len(toks) >= size - 1:
+            tail = toks[len(toks) - (size - 1):] if size > 1 else []
+            for i in range(len(toks) - size + 1):
+                if toks[i:i + size - 1] == tail:
+                    want.add(toks[i + size - 1])
+        assert banned_ngram_tokens(toks, size) == sorted(want), (toks, size)
+
+
+def test_penalties_known_answers():
+    # tests/test_runtime_buffers.py:136-143: repetition 2 turns a listed logit of 8 into 4
+    x = np.full(16, 8.0, np.float32)
+    got = A.penalties(x, np.array([1, 2]), np.array([0, 1], np.int32), 0.0, 0.0, 2.0)
+    assert got[1] == 4.0 and got[2] == 4.0 and got[0] == 8.0 and got[3] == 8.0
+    # exactly representable cases pin the formula: repetition divides positive and multiplies
+    # non-positive logits (prompt ids included, count 0), frequency scales with the count,
+    # presence needs a count
+    x = np.array([3.0, -3.0, 3.0, -1.0, 5.0, 0.0], np.float32)
+    ids = np.array([0, 1, 2, 3, 5, 99])
+    counts = np.array([0, 0, 3, 2, 1, 4], np.int32)
+    got = A.penalties(x, ids, counts, 0.5, 0.25, 1.5)
+    want = np.array([2.0, -4.5, 2.0 - 0.75 - 0.5, -1.5 - 0.5 - 0.5, 5.0, 0.0 - 0.25 - 0.5],
+                    np.float32)
+    assert np.array_equal(got, want)
+    # ids outside the vocabulary are skipped, repetition 1 leaves the sign rule out
+    got = A.penalties(np.array([1.0, -2.0], np.float32), np.array([-1, 1, 7]),
+                      np.array([5, 2, 1], np.int32), 1.0, 0.5, 1.0)
+    assert np.array_equal(got, np.array([1.0, -4.0], np.float32))
