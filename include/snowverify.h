@@ -567,7 +567,8 @@ int snowverify_norm_router_plan(const void* x, const void* res_in, void* res_out
                                 int64_t E, int64_t topk, float* weights, int32_t* ids,
                                 float* shared_w, void* plan, void* stream);
 /* 16-bit weight GEMV: repack size, repack (wt 1 = fp16, 2 = bf16), and C = A W^T (fp16 weights
- * take the operand workspace, bf16 weights bf16 activations). M <= 16. */
+ * take the operand workspace, bf16 weights bf16 activations). M <= 256; each workgroup loads a
+ * weight tile once for up to four 16-row tiles. */
 int64_t snowverify_dense_bytes(int64_t N, int64_t K);
 int snowverify_dense_shuffle(const void* src, void* dst, int64_t N, int64_t K, int wt,
                              void* stream);

@@ -11,6 +11,8 @@
 // repack produces them). The shared expert has its own pair of matrices.
 #include "kquant_core.h"
 
+#include <mutex>
+
 namespace {
 using namespace kq;
 
@@ -165,14 +167,20 @@ __global__ void __launch_bounds__(NORM_MAX_THREADS) norm_prep_kernel(
 // ---------------------------------------------------------------------------------------
 constexpr int WT_F16 = 1;
 constexpr int WT_BF16 = 2;
+constexpr int DENSE_MT = 4;        // row tiles per dense_gemv workgroup above two
+constexpr int DENSE_MAX_M = 256;   // rows of one verify step
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-template <int WT, int NTILE, int NW>
+// One launch covers up to MT 16-row tiles of the rows (blockIdx.y: the group of MT tiles):
+// each superblock's weights are loaded once and multiplied against every tile's operands, so
+// a wide verify block streams the weights once per MT tiles. Each row's arithmetic is the
+// same whatever MT is (an MFMA row depends on its own operands only).
+template <int WT, int NTILE, int NW, int MT>
 __global__ void __launch_bounds__(NW * 64) dense_gemv(const u32x4* __restrict__ w,
                                                       const void* __restrict__ act,
                                                       void* __restrict__ c, int M, int N, int S,
-                                                      int c_bf16) {
+                                                      int c_bf16, size_t tile_bytes) {
   __shared__ floatx4 part[NW][NTILE][64];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -180,36 +188,40 @@ __global__ void __launch_bounds__(NW * 64) dense_gemv(const u32x4* __restrict__ 
   const int tiles = (N + TILE_N - 1) / TILE_N;
   const int tile0 = blockIdx.x * NTILE;
   const int K = S * QK;
+  const int m0 = blockIdx.y * MT;                       // first row tile of the group
+  const int row_tiles = (M + TILE_M - 1) / TILE_M;
+  const int mt = row_tiles - m0 < MT ? row_tiles - m0 : MT;
   // the block's own tiles as the buffer: offsets stay 32-bit whatever N * K is
   const int own = tiles - tile0 < NTILE ? tiles - tile0 : NTILE;
   __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(w + (int64_t)tile0 * S * 8 * 64), 0, own * S * 8 * 64 * 16, 0x00020000);
-  __amdgpu_buffer_rsrc_t xr, sr;
-  uint32_t vx, vs;
-  if constexpr (WT == WT_F16) {
-    XPrepView xv = xprep_view((void*)act, S);
-    xr = __builtin_amdgcn_make_buffer_rsrc((void*)xv.xop, 0, S * 8 * 64 * 16, 0x00020000);
-    sr = __builtin_amdgcn_make_buffer_rsrc((void*)xv.scale, 0, S * 16 * 4, 0x00020000);
-    vx = r < M ? lane * 16 : 0x80000000u;
-    vs = kq * 16;
-  } else {
-    xr = __builtin_amdgcn_make_buffer_rsrc((void*)act, 0, M * K * 2, 0x00020000);
-    sr = xr;
-    vx = r < M ? (uint32_t)(r * K * 2 + kq * 16) : 0x80000000u;
-    vs = 0;
-  }
-  floatx4 acc[NTILE];
+  __amdgpu_buffer_rsrc_t xr[MT], sr[MT];
+  uint32_t vx[MT], vs[MT];
 #pragma unroll
-  for (int t = 0; t < NTILE; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int s = wv; s < S; s += NW) {
-    u32x4 xa[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if constexpr (WT == WT_F16) xa[j] = bload4(xr, vx, (uint32_t)((s * 8 + j) * 64 * 16));
-      else xa[j] = bload4(xr, vx, (uint32_t)((s * QK + j * 32) * 2));
+  for (int m = 0; m < MT; ++m) {
+    const int rows = M - (m0 + m) * TILE_M;  // valid rows of tile m0 + m (<= 0: none)
+    if constexpr (WT == WT_F16) {
+      XPrepView xv = xprep_view((char*)act + (size_t)(m0 + m) * tile_bytes, S);
+      xr[m] = __builtin_amdgcn_make_buffer_rsrc((void*)xv.xop, 0, S * 8 * 64 * 16, 0x00020000);
+      sr[m] = __builtin_amdgcn_make_buffer_rsrc((void*)xv.scale, 0, S * 16 * 4, 0x00020000);
+      vx[m] = r < rows ? lane * 16 : 0x80000000u;
+      vs[m] = kq * 16;
+    } else {
+      const int rv = rows < TILE_M ? (rows > 0 ? rows : 0) : TILE_M;
+      xr[m] = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)((const uint16_t*)act + (int64_t)(m0 + m) * TILE_M * K), 0, rv * K * 2,
+          0x00020000);
+      sr[m] = xr[m];
+      vx[m] = r < rows ? (uint32_t)(r * K * 2 + kq * 16) : 0x80000000u;
+      vs[m] = 0;
     }
-    floatx4 scale = {1.f, 1.f, 1.f, 1.f};
-    if constexpr (WT == WT_F16) scale = __builtin_bit_cast(floatx4, bload4(sr, vs, (uint32_t)(s * 16 * 4)));
+  }
+  floatx4 acc[MT][NTILE];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int t = 0; t < NTILE; ++t) acc[m][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int s = wv; s < S; s += NW) {
     u32x4 wb[NTILE][8];
 #pragma unroll
     for (int t = 0; t < NTILE; ++t)
@@ -217,37 +229,55 @@ __global__ void __launch_bounds__(NW * 64) dense_gemv(const u32x4* __restrict__ 
       for (int j = 0; j < 8; ++j)
         wb[t][j] = bload4(wr, lane * 16, (uint32_t)(((t * S + s) * 8 + j) * 64 * 16));
 #pragma unroll
-    for (int t = 0; t < NTILE; ++t) {
-      floatx4 sb = {0.f, 0.f, 0.f, 0.f};
+    for (int m = 0; m < MT; ++m) {
+      if (m >= mt) break;  // uniform
+      u32x4 xa[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        if constexpr (WT == WT_F16)
-          sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xa[j]),
-                                                      __builtin_bit_cast(half8, wb[t][j]), sb, 0, 0, 0);
-        else
-          sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[j]),
-                                                       __builtin_bit_cast(bf16x8, wb[t][j]), sb, 0, 0, 0);
+        if constexpr (WT == WT_F16) xa[j] = bload4(xr[m], vx[m], (uint32_t)((s * 8 + j) * 64 * 16));
+        else xa[j] = bload4(xr[m], vx[m], (uint32_t)((s * QK + j * 32) * 2));
       }
-      acc[t] += sb * scale;
+      floatx4 scale = {1.f, 1.f, 1.f, 1.f};
+      if constexpr (WT == WT_F16)
+        scale = __builtin_bit_cast(floatx4, bload4(sr[m], vs[m], (uint32_t)(s * 16 * 4)));
+#pragma unroll
+      for (int t = 0; t < NTILE; ++t) {
+        floatx4 sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if constexpr (WT == WT_F16)
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, xa[j]),
+                                                        __builtin_bit_cast(half8, wb[t][j]), sb, 0, 0, 0);
+          else
+            sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xa[j]),
+                                                         __builtin_bit_cast(bf16x8, wb[t][j]), sb, 0, 0, 0);
+        }
+        acc[m][t] += sb * scale;
+      }
     }
   }
-  combine_waves<NTILE, NW>(part, acc, wv, lane);
-  for (int idx = threadIdx.x; idx < NTILE * 64; idx += NW * 64) {
-    const int t = idx >> 6, l = idx & 63;
-    const int tile = tile0 + t;
-    if (tile >= tiles) continue;
-    floatx4 v = part[0][t][l];
 #pragma unroll
-    for (int ww = 1; ww < NW; ++ww) v += part[ww][t][l];
-    const int n = tile * TILE_N + (l & 15);
-    if (n >= N) continue;
-    const int rb = 4 * (l >> 4);
+  for (int m = 0; m < MT; ++m) {
+    if (m >= mt) break;  // uniform
+    if (m) __syncthreads();  // the previous tile's partials are read
+    combine_waves<NTILE, NW>(part, acc[m], wv, lane);
+    for (int idx = threadIdx.x; idx < NTILE * 64; idx += NW * 64) {
+      const int t = idx >> 6, l = idx & 63;
+      const int tile = tile0 + t;
+      if (tile >= tiles) continue;
+      floatx4 v = part[0][t][l];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = rb + i;
-      if (row >= M) break;
-      if (c_bf16) ((uint16_t*)c)[(int64_t)row * N + n] = f32_to_bf16(v[i]);
-      else ((float*)c)[(int64_t)row * N + n] = v[i];
+      for (int ww = 1; ww < NW; ++ww) v += part[ww][t][l];
+      const int n = tile * TILE_N + (l & 15);
+      if (n >= N) continue;
+      const int rb = (m0 + m) * TILE_M + 4 * (l >> 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = rb + i;
+        if (row >= M) break;
+        if (c_bf16) ((uint16_t*)c)[(int64_t)row * N + n] = f32_to_bf16(v[i]);
+        else ((float*)c)[(int64_t)row * N + n] = v[i];
+      }
     }
   }
 }
@@ -602,6 +632,7 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_plan_kernel(const int32_t* 
 // ---------------------------------------------------------------------------------------
 constexpr int NR_THREADS = 1024;  // 16 waves: one per routed row; the GEMV takes dense_gemv's
 constexpr int NR_MAXP = 8;        // row passes held in registers (M <= 8 * 8192 / H)
+constexpr int NR_MAX_LDS = 128 * 1024;  // dynamic LDS beside the ~27 KiB of static arrays
 __device__ uint32_t g_router_arrive;
 
 // (The arguments the first loads need come first: they arrive preloaded in SGPRs.)
@@ -1101,8 +1132,18 @@ template <int WT, int NTILE, int NW>
 int launch_dense(const void* w, const void* act, void* c, int M, int N, int S, int c_bf16,
                  hipStream_t s) {
   const int tiles = (N + TILE_N - 1) / TILE_N;
-  hipLaunchKernelGGL((dense_gemv<WT, NTILE, NW>), dim3((tiles + NTILE - 1) / NTILE), dim3(NW * 64),
-                     0, s, (const u32x4*)w, act, c, M, N, S, c_bf16);
+  const int row_tiles = (M + TILE_M - 1) / TILE_M;
+  const size_t tb = xprep_tile_bytes(S);
+  if (row_tiles == 1)
+    hipLaunchKernelGGL((dense_gemv<WT, NTILE, NW, 1>), dim3((tiles + NTILE - 1) / NTILE),
+                       dim3(NW * 64), 0, s, (const u32x4*)w, act, c, M, N, S, c_bf16, tb);
+  else if (row_tiles == 2)
+    hipLaunchKernelGGL((dense_gemv<WT, NTILE, NW, 2>), dim3((tiles + NTILE - 1) / NTILE),
+                       dim3(NW * 64), 0, s, (const u32x4*)w, act, c, M, N, S, c_bf16, tb);
+  else
+    hipLaunchKernelGGL((dense_gemv<WT, NTILE, NW, DENSE_MT>),
+                       dim3((tiles + NTILE - 1) / NTILE, (row_tiles + DENSE_MT - 1) / DENSE_MT),
+                       dim3(NW * 64), 0, s, (const u32x4*)w, act, c, M, N, S, c_bf16, tb);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1145,7 +1186,7 @@ SV_API int snowverify_norm_prep_moe(const float* pairs, const float* shared_out,
 // workspace ws) + snowverify_dense_gemv (bf16 router [E (+1), H] repacked, over the normalised
 // rows, f32 logits [M, E (+1)]) + snowverify_moe_route with the plan, in one launch and with
 // their bits. shared_w null: no shared expert (E router rows). M <= 16, H a multiple of 512 up
-// to 4096 with M * (H + 8) * 2 <= 64 KiB, E <= 256, M * topk <= 135. Uses a library-owned
+// to 4096 with M * (H + 8) * 2 <= 128 KiB, E <= 256, M * topk <= 135. Uses a library-owned
 // counter: calls on one device must be stream-ordered.
 SV_API int snowverify_norm_router_plan(const void* x, const void* res_in, void* res_out,
                                        const void* gamma, float eps, void* ws, void* y_out,
@@ -1159,7 +1200,18 @@ SV_API int snowverify_norm_router_plan(const void* x, const void* res_in, void* 
   if (res_out && (res_out == x || res_out == res_in)) return SV_EINVAL;  // read by every block
   const int64_t N = E + (shared_w ? 1 : 0);
   const size_t lds = std::max((size_t)(M * (H + 8) * 2), (size_t)(M * N * 4));
-  if (lds > 65536 || (M + 8192 / H - 1) / (8192 / H) > NR_MAXP) return SV_ENOTSUP;
+  if (lds > NR_MAX_LDS || (M + 8192 / H - 1) / (8192 / H) > NR_MAXP) return SV_ENOTSUP;
+  if (lds > 65536) {
+    // beyond the default dynamic LDS limit (16 rows of H = 2048 with their padding): raise
+    // the kernel's limit once, up to the CU's 160 KiB
+    static std::once_flag once;
+    static hipError_t attr = hipSuccess;
+    std::call_once(once, [] {
+      attr = hipFuncSetAttribute((const void*)norm_router_plan_kernel,
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, NR_MAX_LDS);
+    });
+    if (attr != hipSuccess) return (int)attr;
+  }
   hipLaunchKernelGGL(norm_router_plan_kernel, dim3((unsigned)((N + TILE_N - 1) / TILE_N)),
                      dim3(NR_THREADS), lds, Sx(stream), (const uint16_t*)x,
                      (const uint16_t*)res_in, (const uint16_t*)gamma, (const u32x4*)router,
@@ -1188,11 +1240,12 @@ SV_API int snowverify_dense_shuffle(const void* src, void* dst, int64_t N, int64
 }
 
 // C[M, N] = A[M, K] W[N, K]^T, fp32 accumulate. wt 1: fp16 weights against the operand
-// workspace `act` (snowverify_gemm_kquant_prepare_a / snowverify_norm_prep); wt 2: bf16 weights
-// against bf16 activations `act` [M, K]. M <= 16.
+// workspace `act` (snowverify_gemm_kquant_prepare_a / snowverify_norm_prep, one 16-row tile
+// after the other); wt 2: bf16 weights against bf16 activations `act` [M, K]. M <= 256: a
+// workgroup multiplies each weight tile against up to four row tiles.
 SV_API int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c, int64_t M,
                                  int64_t N, int64_t K, int c_is_bf16, void* stream) {
-  if (M <= 0 || M > 16 || N <= 0 || K <= 0 || K % 256) return SV_EINVAL;
+  if (M <= 0 || M > DENSE_MAX_M || N <= 0 || K <= 0 || K % 256) return SV_EINVAL;
   // 32-bit in-kernel offsets: one block's weights (<= 2 tiles) and the activations
   if (N > (int64_t)1 << 30 || K > 65536) return SV_ENOTSUP;
   const int S = (int)(K / 256);

@@ -28,6 +28,8 @@ from ._capi import SnowLLMError
 
 Q4_K, Q8_0 = 4, 8
 HEAD_KQUANT = -1   # VerifyModel.head_wt for a Q4_K / Q8_0 head (lm_head = (quant, meta))
+# rows of one verify step over all its requests (SPEC_MAX_STEP_ROWS, snowllm/defaults.py:9)
+MAX_STEP_ROWS = 256
 
 
 @dataclass
@@ -183,11 +185,17 @@ class VerifyModel:
     """Weights, KV pools and step buffers of one verify-step configuration."""
 
     def __init__(self, cfg: VerifyConfig, seed: int = 0, keep_raw=False, kv_std: float = 1.0,
-                 weights=None):
+                 weights=None, batch: int = 1):
         """keep_raw: keep the unshuffled GGUF bytes (and the router / LM head) for parity
         checks -- True for every layer, an int n for the first n layers, or a collection of
         layer indices. weights: None for seeded random weights, else a callable that installs
-        layers / embed / lm_head / head_wt / final_norm on the model (a checkpoint loader)."""
+        layers / embed / lm_head / head_wt / final_norm on the model (a checkpoint loader).
+        batch: requests verified together, each with cfg.block rows (at most cfg.block for a
+        ragged batch, see set_batch) and its own pages of the KV pools; batch * block <=
+        MAX_STEP_ROWS."""
+        if batch < 1 or batch * cfg.block > MAX_STEP_ROWS:
+            raise SnowLLMError(f"a verify step holds at most {MAX_STEP_ROWS} rows")
+        self.batch = batch
         self.cfg = c = cfg
         self.keep_raw = keep_raw
         dev = "cuda"
@@ -196,9 +204,16 @@ class VerifyModel:
         self.head_fmt = 0
         # MoE layers: post-attention norm, router and routing/plan in one launch where the
         # fused kernel takes the shape (False: the three separate launches, the same bits)
+        # the MoE and the 16-bit GEMVs take at most 16 rows per launch: a step of more rows
+        # runs them on row chunks (the fused router on chunks whose rows fit its LDS)
+        M = batch * c.block
+        self.rows = M
+        self.row_chunks = [(r0, min(16, M - r0)) for r0 in range(0, M, 16)]
+        self.moe_chunks = self.row_chunks
+        chunk = min(16, M)
         self.fuse_router = bool(c.moe and c.hidden % 512 == 0 and c.hidden <= 4096 and
-                                c.block * (c.hidden + 8) * 2 <= 65536 and
-                                c.block * (c.experts + 1) * 4 <= 65536)
+                                chunk * (c.hidden + 8) * 2 <= 131072 and
+                                chunk * (c.experts + 1) * 4 <= 131072)
         self.embed_q4k = False       # True: self.embed holds Q4_K blocks [V, H / 256 * 144]
         self.lm_head_raw = None
         if weights is None:
@@ -207,10 +222,11 @@ class VerifyModel:
             weights(self)
         self.inv_freq = (1.0 / (c.rope_theta ** (torch.arange(c.rot_half, device=dev,
                                                              dtype=torch.float32) / c.rot_half)))
-        # KV cache: context + block pages, random page table (prior tokens ~ N(0, kv_std^2))
+        # KV cache: context + block pages per request, random page table (prior tokens ~
+        # N(0, kv_std^2))
         T = c.block
         self.pages = (c.context + T + c.page - 1) // c.page
-        self.blocks = self.pages + 8
+        self.blocks = batch * self.pages + 8
         kvg = torch.Generator(device=dev).manual_seed(seed + 7)
         shape_k = (self.blocks, c.kv_heads, c.head_dim // 16, c.page, 16)
         shape_v = (self.blocks, c.kv_heads, c.page // 4, c.head_dim, 4)
@@ -222,8 +238,8 @@ class VerifyModel:
             v.normal_(0, kv_std, generator=kvg)
             self.k_pools.append(k)
             self.v_pools.append(v)
-        perm = torch.randperm(self.blocks, device=dev, generator=kvg)[:self.pages]
-        self.table = perm.int().view(1, -1).contiguous()
+        perm = torch.randperm(self.blocks, device=dev, generator=kvg)[:batch * self.pages]
+        self.table = perm.int().view(batch, -1).contiguous()
         self._alloc_step_buffers()
 
     def _random_weights(self, seed, keep_raw):
@@ -274,18 +290,22 @@ class VerifyModel:
 
     # -----------------------------------------------------------------------------------
     def _alloc_step_buffers(self):
-        c, T, dev = self.cfg, self.cfg.block, "cuda"
+        c, dev = self.cfg, "cuda"
+        T = self.rows            # all rows of the step: batch * block
+        B = self.batch
         H = c.hidden
         bf = torch.bfloat16
         self.ids = torch.zeros(T, dtype=torch.int64, device=dev)
         self.positions = torch.zeros(T, dtype=torch.int64, device=dev)
         self.slots = torch.zeros(T, dtype=torch.int32, device=dev)
-        self.lens = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.lens = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.lengths = [c.block] * B   # rows per request (ragged batches: set_batch)
         self.tree = None
         if c.tree_parents:
             self.tree = torch.tensor([m - (1 << 64) if m >= 1 << 63 else m
-                                      for m in tree_masks(c.tree_parents)],
+                                      for m in tree_masks(c.tree_parents)] * B,
                                      dtype=torch.int64, device=dev)
+        self._chain_tree = None  # ancestor masks of a ragged chain batch (set_batch)
         self.cos = torch.empty(T, c.rot_half, dtype=torch.float32, device=dev)
         self.sin = torch.empty_like(self.cos)
         self.x = torch.empty(T, H, dtype=bf, device=dev)         # layer input (block output)
@@ -301,16 +321,21 @@ class VerifyModel:
         self.ws_a = torch.empty(ops.gemm_kquant_a_ws_bytes(T, c.heads * c.head_dim),
                                 dtype=torch.uint8, device=dev)
         self.attn_scratch = torch.empty(
-            ops.paged_attention_explicit_scratch_bytes(1, T, c.heads, c.kv_heads, c.head_dim),
+            ops.paged_attention_explicit_scratch_bytes(B, c.block, c.heads, c.kv_heads,
+                                                       c.head_dim),
             dtype=torch.uint8, device=dev)
+        self.ws_tile = ops.gemm_kquant_a_ws_bytes(16, H)   # one 16-row tile of ws_h / ws_h2
         if c.moe:
             E, F, K = c.experts, c.expert_ffn, c.topk
             self.router_logits = torch.empty(T, E + 1, dtype=torch.float32, device=dev)
             self.route_w = torch.empty(T, K, dtype=torch.float32, device=dev)
             self.route_ids = torch.empty(T, K, dtype=torch.int32, device=dev)
             self.shared_w = torch.empty(T, dtype=torch.float32, device=dev)
-            self.plan = torch.empty(Lops.MOE_PLAN_BYTES, dtype=torch.uint8, device=dev)
-            self.moe_act = torch.empty(T * K + 1, 16, F, dtype=bf, device=dev)
+            self.plans = [torch.empty(Lops.MOE_PLAN_BYTES, dtype=torch.uint8, device=dev)
+                          for _ in self.moe_chunks]
+            self.plan = self.plans[0]
+            mc = max(m for _, m in self.moe_chunks)
+            self.moe_act = torch.empty(mc * K + 1, 16, F, dtype=bf, device=dev)
             self.pairs = torch.empty(T * K, H, dtype=torch.float32, device=dev)
             self.shared_out = torch.empty(T, H, dtype=torch.float32, device=dev)
         else:
@@ -322,17 +347,53 @@ class VerifyModel:
 
     def set_block(self, ids, context=None):
         """Stage one block: ids [T] (last token + drafts) at positions context..context+T-1
-        (tree blocks: context + depth). Host-side, outside the timed/captured step."""
-        c, T = self.cfg, self.cfg.block
-        ctx = c.context if context is None else context
+        (tree blocks: context + depth). Host-side, outside the timed/captured step. A batched
+        model stages every request with the same block (set_batch for anything else)."""
+        B = self.batch
+        ids = torch.as_tensor(ids, dtype=torch.int64).view(1, -1).expand(B, -1)
+        ctx = self.cfg.context if context is None else context
+        self.set_batch(ids, [ctx] * B)
+
+    def set_batch(self, ids, contexts, lengths=None):
+        """Stage a batch: ids [batch, T] (each request's last token + drafts; a ragged request
+        uses its first lengths[b] ids), request b's rows at positions contexts[b] + t (tree
+        blocks: + depth) with its K/V written at those positions of its pages. Ragged batches
+        (a length below the block) keep the padded layout [batch, T]: the padding rows write no
+        cache (slot -1) and see only themselves, the real rows never see them (ancestor masks
+        of the chain), and their logits are ignored. Host-side, outside the captured step; a
+        graph captured with one ragged/uniform shape must be replayed with the same kind."""
+        c, B, T = self.cfg, self.batch, self.cfg.block
         dev = "cuda"
+        ids = torch.as_tensor(ids, dtype=torch.int64).view(B, T)
+        lengths = [T] * B if lengths is None else [int(n) for n in lengths]
+        if len(contexts) != B or len(lengths) != B or not all(1 <= n <= T for n in lengths):
+            raise SnowLLMError("set_batch: one context and a length in 1..block per request")
+        if any(n < T for n in lengths) and (c.tree_parents or T > 64):
+            raise SnowLLMError("set_batch: ragged lengths apply to chain blocks of <= 64 rows")
+        if any(x < 0 or x + T > self.pages * c.page for x in contexts):
+            raise SnowLLMError("set_batch: a request's block runs past its pages")
         depth = tree_depths(c.tree_parents) if c.tree_parents else list(range(T))
-        self.ids.copy_(torch.as_tensor(ids, dtype=torch.int64, device=dev))
-        self.positions.copy_(torch.tensor([ctx + d for d in depth], dtype=torch.int64, device=dev))
-        rows = torch.arange(ctx, ctx + T, dtype=torch.int64)
-        tbl = self.table.view(-1).cpu().long()
-        self.slots.copy_((tbl[rows // c.page] * c.page + rows % c.page).int().to(dev))
-        self.lens.fill_(ctx + T)
+        tbl = self.table.cpu().long()
+        pos, slots = [], []
+        for b in range(B):
+            for t in range(T):
+                p = contexts[b] + t
+                pos.append(contexts[b] + depth[t])
+                slots.append(int(tbl[b, p // c.page]) * c.page + p % c.page if t < lengths[b]
+                             else -1)
+        self.ids.copy_(ids.reshape(-1).to(dev))
+        self.positions.copy_(torch.tensor(pos, dtype=torch.int64, device=dev))
+        self.slots.copy_(torch.tensor(slots, dtype=torch.int32, device=dev))
+        self.lens.copy_(torch.tensor([x + T for x in contexts], dtype=torch.int32, device=dev))
+        self.lengths = lengths
+        if not c.tree_parents:
+            if all(n == T for n in lengths):
+                self.tree = None
+            else:
+                masks = [((2 << t) - 1) if t < n else (1 << t) for n in lengths for t in range(T)]
+                self._chain_tree = torch.tensor([m - (1 << 64) if m >= 1 << 63 else m
+                                                 for m in masks], dtype=torch.int64, device=dev)
+                self.tree = self._chain_tree
 
     # -----------------------------------------------------------------------------------
     def forward(self, *, upto_layer=None, record_slots=None):
@@ -340,7 +401,7 @@ class VerifyModel:
         int32 [layers] device tensor that receives each MoE layer's plan size (routed unique
         experts + shared) for byte accounting; it adds one copy per layer, so timed steps leave
         it out."""
-        c, T = self.cfg, self.cfg.block
+        c, T = self.cfg, self.rows
         H = c.hidden
         if self.embed_q4k:
             from .embedding import gather_embedding_q4_k
@@ -393,34 +454,47 @@ class VerifyModel:
                                   self.o, T, H, c.heads * c.head_dim, self.ws_a)
             # feed-forward block
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
-            if c.moe and self.fuse_router:
-                # post-attention norm + router GEMV + routing and plan: one launch
-                Lops.norm_router_plan(self.o, lw.post_norm, self.ws_h2, c.eps, lw.router,
-                                      self.router_logits, c.topk, self.route_w, self.route_ids,
-                                      self.shared_w, self.plan, res_in=res_in, res_out=res_out,
-                                      y_out=self.h2)
-            elif c.moe:
-                Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,
-                               res_out=res_out, y_out=self.h2)
-                Lops.dense_gemv(Lops.WT_BF16, lw.router, self.h2, self.router_logits, T,
-                                c.experts + 1, H)
-                Lops.moe_route_plan(self.router_logits, c.experts, c.topk, self.route_w,
-                                    self.route_ids, self.shared_w, self.plan)
             if c.moe:
-                if record_slots is not None:
-                    record_slots[i:i + 1].copy_(self.plan[:4].view(torch.int32))
-                ns = T * c.topk + 1
-                # gate/up and down in one launch: a slot's down starts when its gate/up is done
-                Lops.moe_gate_up_down(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, self.plan,
-                                      self.ws_h2, self.route_w, self.shared_w, self.moe_act,
-                                      self.pairs, self.shared_out, T, ns, c.experts, H,
-                                      c.expert_ffn)
+                # the router, routing and experts on row chunks of at most 16 rows (one chunk
+                # for a single block); chunk j's operands are its rows' tiles of ws_h2
+                if not self.fuse_router:
+                    Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,
+                                   res_out=res_out, y_out=self.h2)
+                K = c.topk
+                for j, (r0, n) in enumerate(self.moe_chunks):
+                    rs = slice(r0, r0 + n)
+                    ws = self._ws_rows(self.ws_h2, r0)
+                    plan = self.plans[j]
+                    if self.fuse_router:
+                        # post-attention norm + router GEMV + routing and plan: one launch
+                        Lops.norm_router_plan(self.o[rs], lw.post_norm, ws, c.eps, lw.router,
+                                              self.router_logits[rs], K, self.route_w[rs],
+                                              self.route_ids[rs], self.shared_w[rs], plan,
+                                              res_in=res_in[rs], res_out=res_out[rs],
+                                              y_out=self.h2[rs])
+                    else:
+                        Lops.dense_gemv(Lops.WT_BF16, lw.router, self.h2[rs],
+                                        self.router_logits[rs], n, c.experts + 1, H)
+                        Lops.moe_route_plan(self.router_logits[rs], c.experts, K,
+                                            self.route_w[rs], self.route_ids[rs],
+                                            self.shared_w[rs], plan)
+                    if record_slots is not None:
+                        record_slots[i:i + 1].add_(plan[:4].view(torch.int32))
+                    # gate/up and down in one launch: a slot's down starts when its gate/up
+                    # is done
+                    Lops.moe_gate_up_down(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, plan,
+                                          ws, self.route_w[rs], self.shared_w[rs],
+                                          self.moe_act, self.pairs[r0 * K:(r0 + n) * K],
+                                          self.shared_out[rs], n, n * K + 1, c.experts, H,
+                                          c.expert_ffn)
                 moe_out = True
             else:
                 Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,
                                res_out=res_out)
-                Lops.gate_up_swiglu(c.ffn_fmt, lw.gu[0], lw.gu[1], self.ws_h2, self.act, T,
-                                    c.ffn, H)
+                for r0, n in self.row_chunks:
+                    Lops.gate_up_swiglu(c.ffn_fmt, lw.gu[0], lw.gu[1],
+                                        self._ws_rows(self.ws_h2, r0), self.act[r0:r0 + n], n,
+                                        c.ffn, H)
                 ops.gemm_kquant_a(lw.dn_fmt or c.ffn_fmt, self.act, lw.dn[0], lw.dn[1], self.x, T,
                                   H, c.ffn, self.ws_act)
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
@@ -440,49 +514,62 @@ class VerifyModel:
         self.final_residual = res_out
         return self.logits
 
+    def _ws_rows(self, ws, r0):
+        """The operand-workspace view whose first tile is rows r0.. (r0 a multiple of 16 or
+        0): the workspace is laid out per 16-row tile."""
+        if r0 % 16:
+            raise SnowLLMError("row chunks start on 16-row tiles")
+        return ws[(r0 // 16) * self.ws_tile:]
+
 
 class Acceptance:
     """Rejection-sampling acceptance of the block against draft probabilities q (the draft
     side's proposal) over the full vocabulary at temperature 1 (snowllm/engine/
     dflash_sampling.py:60-69): straight from the logits (ops.dflash.accept_reject), which
     gives the bits of ops.sampling.probabilities + ops.dflash.reject. For a tree block the
-    chain rows[0..k] is accepted. The batch dispatch (greedy / whole vocabulary / candidate
-    lists) lives in snowllm_amd.dflash_sampling."""
+    chain rows[0..k] is accepted. batch: requests of `block` rows each (logits [batch * block,
+    V]), request b's chain at rows b * block + rows. The batch dispatch (greedy / whole
+    vocabulary / candidate lists) lives in snowllm_amd.dflash_sampling."""
 
-    def __init__(self, vocab, chain_rows):
+    def __init__(self, vocab, chain_rows, batch=1, block=None):
         dev = "cuda"
         self.rows = list(chain_rows)
         T = len(self.rows)
         k = T - 1
-        self.V, self.T = vocab, T
-        self.top_k = torch.full((T,), ops.SAMPLING_MAX_K, dtype=torch.int32, device=dev)
-        self.top_p = torch.ones(T, device=dev)
-        self.temp = torch.ones(T, device=dev)
-        self.p = torch.empty(T, vocab, device=dev)
-        self.pid = torch.empty(T, vocab, dtype=torch.int64, device=dev)
-        self.ws = torch.empty(ops.sample_workspace_bytes(T, vocab, vocab), dtype=torch.uint8, device=dev)
-        self.q = torch.empty(1, k, vocab, device=dev)
-        self.qid = torch.arange(vocab, dtype=torch.int64, device=dev).repeat(1, k, 1).contiguous()
-        self.drafts = torch.zeros(1, k, dtype=torch.int64, device=dev)
-        self.uniform = torch.zeros(1, T, device=dev)
-        self.slot = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.valid = torch.ones(1, dtype=torch.int32, device=dev)
-        self.out = torch.empty(1, T, dtype=torch.int64, device=dev)
-        self.accepted = torch.empty(1, dtype=torch.int64, device=dev)
+        B = batch
+        block = T if block is None else block
+        self.V, self.T, self.B, self.block = vocab, T, B, block
+        n = B * T
+        self.top_k = torch.full((n,), ops.SAMPLING_MAX_K, dtype=torch.int32, device=dev)
+        self.top_p = torch.ones(n, device=dev)
+        self.temp = torch.ones(n, device=dev)
+        self.p = torch.empty(n, vocab, device=dev)
+        self.pid = torch.empty(n, vocab, dtype=torch.int64, device=dev)
+        self.ws = torch.empty(ops.sample_workspace_bytes(n, vocab, vocab), dtype=torch.uint8, device=dev)
+        self.q = torch.empty(B, k, vocab, device=dev)
+        self.qid = torch.arange(vocab, dtype=torch.int64, device=dev).repeat(B, k, 1).contiguous()
+        self.drafts = torch.zeros(B, k, dtype=torch.int64, device=dev)
+        self.uniform = torch.zeros(B, T, device=dev)
+        self.slot = torch.arange(B, dtype=torch.int32, device=dev)
+        self.valid = torch.ones(B, dtype=torch.int32, device=dev)
+        self.out = torch.empty(B, T, dtype=torch.int64, device=dev)
+        self.accepted = torch.empty(B, dtype=torch.int64, device=dev)
         self.chain_logits = None
-        if self.rows != list(range(T)):
-            self.chain_logits = torch.empty(T, vocab, device=dev)
-            self.chain_index = torch.tensor(self.rows, dtype=torch.int64, device=dev)
+        if self.rows != list(range(block)) or B * T != B * block:
+            self.chain_logits = torch.empty(n, vocab, device=dev)
+            self.chain_index = torch.tensor([b * block + r for b in range(B) for r in self.rows],
+                                            dtype=torch.int64, device=dev)
 
     def set_draft(self, draft_logits, drafts, uniform):
-        """Draft side (outside the step): q = softmax(draft logits) over the vocabulary."""
-        k = self.T - 1
-        ones = torch.ones(k, device="cuda")
-        qid = torch.empty(k, self.V, dtype=torch.int64, device="cuda")
-        q = self.q.view(k, self.V)
-        ops.probabilities(draft_logits, self.top_k[:k], ones, ones, self.V, q, qid, self.ws)
-        self.drafts.copy_(drafts.view(1, k))
-        self.uniform.copy_(uniform.view(1, self.T))
+        """Draft side (outside the step): q = softmax(draft logits) over the vocabulary.
+        draft_logits [batch * k, V], drafts [batch, k], uniform [batch, k + 1]."""
+        k, B = self.T - 1, self.B
+        ones = torch.ones(B * k, device="cuda")
+        qid = torch.empty(B * k, self.V, dtype=torch.int64, device="cuda")
+        q = self.q.view(B * k, self.V)
+        ops.probabilities(draft_logits, self.top_k[:B * k], ones, ones, self.V, q, qid, self.ws)
+        self.drafts.copy_(drafts.view(B, k))
+        self.uniform.copy_(uniform.view(B, self.T))
 
     def set_selector(self, hp, draft_logits, pred, succ, anchor, temperature, select_uniform,
                      uniform):
@@ -491,22 +578,22 @@ class Acceptance:
         dflash_sampling.py:44-48); the rejection step then reads those candidate lists by
         request slot. hp [k, rank], draft_logits [k, V], codebooks [V, rank], anchor [1],
         temperature [1], select_uniform [1, k], uniform [1, k + 1]."""
-        k = self.T - 1
+        k, B = self.T - 1, self.B
         dev = "cuda"
         self.sel = dict(hp=hp, logits=draft_logits, pred=pred, succ=succ,
-                        anchor=anchor.view(1), temperature=temperature.view(1),
-                        uniform=select_uniform.view(1, k))
-        self.q = torch.empty(1, k, 16, device=dev)
-        self.qid = torch.empty(1, k, 16, dtype=torch.int64, device=dev)
-        self.sel_scratch = torch.empty(ops.dflash.select_scratch_bytes(k), dtype=torch.uint8,
+                        anchor=anchor.view(B), temperature=temperature.view(B),
+                        uniform=select_uniform.view(B, k))
+        self.q = torch.empty(B, k, 16, device=dev)
+        self.qid = torch.empty(B, k, 16, dtype=torch.int64, device=dev)
+        self.sel_scratch = torch.empty(ops.dflash.select_scratch_bytes(B * k), dtype=torch.uint8,
                                        device=dev)
-        self.uniform.copy_(uniform.view(1, self.T))
+        self.uniform.copy_(uniform.view(B, self.T))
 
     def propose(self, block_ids=None):
         """Run the selector: drafts, candidate ids and q for this step; block_ids [k + 1], if
         given, receives anchor + drafts (the verify block's input ids)."""
         s = self.sel
-        if block_ids is not None:
+        if block_ids is not None and self.B == 1:
             # the walk writes the drafts straight into the block's ids (after the anchor), and
             # the acceptance reads them there: no copy in the step
             self.drafts = block_ids[1:].view(1, self.T - 1)
@@ -514,6 +601,9 @@ class Acceptance:
                                self.drafts, self.sel_scratch, temperature=s["temperature"],
                                uniform=s["uniform"], slots=self.slot, candidate_ids=self.qid,
                                probabilities=self.q)
+        if block_ids is not None and self.B > 1:
+            # each request's block: its anchor, then its drafts
+            block_ids.view(self.B, self.block)[:, 1:self.T].copy_(self.drafts)
         return self.drafts
 
     def __call__(self, logits):
@@ -521,8 +611,8 @@ class Acceptance:
         if self.chain_logits is not None:
             torch.index_select(logits, 0, self.chain_index, out=self.chain_logits)
             src = self.chain_logits
-        elif logits.shape[0] != self.T:
-            src = logits[:self.T]  # chain = leading rows of the block (contiguous view)
+        elif logits.shape[0] != self.B * self.T:
+            src = logits[:self.B * self.T]  # chain = leading rows (contiguous view)
         # the whole vocabulary at T = 1: straight from the logits (the same bits as
         # probabilities + reject, which runs when the shape is beyond the fused kernel)
         if ops.dflash.accept_reject(src, self.drafts, self.qid, self.q, self.slot, self.valid,
