@@ -300,16 +300,18 @@ def use_selector(cfg):
     return cfg.moe and not cfg.tree_parents
 
 
-def step_bytes(cfg, slots, selector=False):
+def step_bytes(cfg, slots, selector=False, batch=1):
     """Algorithmic HBM bytes of one verify step: every weight byte the step must read once
-    (the touched experts only), the KV cache of the context plus the block's new rows, the
-    LM head, the logits/probabilities of the acceptance, and (with the selector) the draft
-    logits plus the codebook rows the selector gathers (16 candidates and 16 previous
-    tokens per position)."""
+    (the touched experts only), the KV cache of the context plus the block's new rows of every
+    request, the LM head, the logits/probabilities of the acceptance, and (with the selector)
+    the draft logits plus the codebook rows the selector gathers (16 candidates and 16
+    previous tokens per position). slots[i]: expert slots layer i reads (unique experts +
+    shared, per 16-row chunk)."""
     H, T, V = cfg.hidden, cfg.block, cfg.vocab
     wb = q4k_bytes if cfg.attn_fmt == 4 else q80_bytes
     attn_w = wb(cfg.qkv_n, H) + wb(H, cfg.heads * cfg.head_dim)
-    kv = (cfg.context + T) * cfg.kv_heads * cfg.head_dim * 2 * 2
+    kv = batch * (cfg.context + T) * cfg.kv_heads * cfg.head_dim * 2 * 2
+    T = batch * T   # rows of the step from here on
     total = 0
     for i in range(cfg.layers):
         total += attn_w + kv + 2 * 2 * H * 2  # + norm weights (bf16), negligible
@@ -321,8 +323,8 @@ def step_bytes(cfg, slots, selector=False):
     total += V * H * 2 + T * H * 2  # LM head (fp16), embedding rows
     total += 3 * T * V * 4          # logits write, probabilities read + write
     if selector:
-        k = T - 1
-        total += k * V * 4 + k * (2 * 16 + 1) * SEL_RANK * 2
+        k = cfg.block - 1
+        total += batch * (k * V * 4 + k * (2 * 16 + 1) * SEL_RANK * 2)
     return total
 
 
@@ -345,34 +347,37 @@ def bench_step(args, name):
     from snowllm_amd.verify import CONFIGS, VerifyModel, Acceptance
 
     cfg = CONFIGS[name]
+    B = args.batch
     T, V, k = cfg.block, cfg.vocab, None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    m = VerifyModel(cfg, seed=0, keep_raw=1)  # raw GGUF bytes of layer 0 for the CPU baseline
+    # raw GGUF bytes of layer 0 for the CPU baseline
+    m = VerifyModel(cfg, seed=0, keep_raw=1, batch=B)
     torch.cuda.synchronize()
     init_s = time.perf_counter() - t0
-    ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(7))
-    m.set_block(ids)
+    ids = torch.randint(0, V, (B, T), generator=torch.Generator().manual_seed(7))
+    m.set_batch(ids, [cfg.context] * B)
     rows = list(range(T)) if not cfg.tree_parents else chain_rows(cfg.tree_parents)
     k = len(rows) - 1
-    acc = Acceptance(V, rows)
+    acc = Acceptance(V, rows, batch=B, block=T)
     # draft side (BASELINE config 1 generators): draft logits ~N(0, 2^2), drafts sampled from
-    # the draft softmax with seed 0, acceptance uniforms U(0, 1) with seed 1
+    # the draft softmax with seed 0, acceptance uniforms U(0, 1) with seed 1 (one block of
+    # them per request)
     g0, g1 = torch.Generator().manual_seed(0), torch.Generator().manual_seed(1)
-    draft_logits = torch.randn(k, V, generator=g0) * 2
-    drafts = torch.multinomial(draft_logits.softmax(-1), 1, generator=g0).view(1, k)
-    uniform = torch.rand(1, k + 1, generator=g1)
+    draft_logits = torch.randn(B * k, V, generator=g0) * 2
+    drafts = torch.multinomial(draft_logits.softmax(-1), 1, generator=g0).view(B, k)
+    uniform = torch.rand(B, k + 1, generator=g1)
     # config 4 is quoted with the DFlash 2 selector in the step: it walks the draft logits
     # (codebook rank 256, seeded synthetic codebooks and selector projection) at T = 1.0,
     # proposes the drafts and hands its 16-candidate lists to the rejection step
     sel = None
     if use_selector(cfg):
         g2 = torch.Generator().manual_seed(2)
-        hp = (torch.randn(k, SEL_RANK, generator=g2) * .2).bfloat16()
+        hp = (torch.randn(B * k, SEL_RANK, generator=g2) * .2).bfloat16()
         pred = (torch.randn(V, SEL_RANK, generator=g2) * .2).bfloat16()
         succ = (torch.randn(V, SEL_RANK, generator=g2) * .2).bfloat16()
-        sel_u = torch.rand(1, k, generator=g2)
-        sel = dict(hp=hp, pred=pred, succ=succ, anchor=ids[:1].clone(), temp=torch.ones(1),
+        sel_u = torch.rand(B, k, generator=g2)
+        sel = dict(hp=hp, pred=pred, succ=succ, anchor=ids[:, 0].clone(), temp=torch.ones(B),
                    u=sel_u)
         acc.set_selector(hp.cuda(), draft_logits.cuda(), pred.cuda(), succ.cuda(),
                          sel["anchor"].cuda(), sel["temp"].cuda(), sel_u.cuda(), uniform.cuda())
@@ -394,7 +399,7 @@ def bench_step(args, name):
     acc(m.logits)
     torch.cuda.synchronize()
     slots_np = slots.cpu().numpy()
-    alg = step_bytes(cfg, slots_np, selector=sel is not None)
+    alg = step_bytes(cfg, slots_np, selector=sel is not None, batch=B)
     # the timed region: K graph replays of the whole step, inputs resident in HBM
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
@@ -407,8 +412,11 @@ def bench_step(args, name):
     if cfg.moe and Lops.moe_sync_error() != 0:
         raise RuntimeError("a MoE expert hand-off timed out during the timed steps "
                            "(its outputs were poisoned with NaN)")
-    emitted = int(acc.accepted[0])  # accepted drafts + the correction/bonus token
-    out_tokens = acc.out[0, :emitted].tolist()
+    # accepted drafts + the correction/bonus token, over the batch's requests
+    emitted = int(acc.accepted.sum())
+    out_tokens = [acc.out[b, :int(acc.accepted[b])].tolist() for b in range(B)]
+    if B == 1:
+        out_tokens = out_tokens[0]
     step_gbs = alg / (ms * 1e-3) / 1e9
 
     # per-kernel launch times (HIP events, launch stream), each rotated over the layers so the
@@ -426,24 +434,29 @@ def bench_step(args, name):
         kern[label] = {"us": round(us, 3), "alg_bytes": int(alg_bytes),
                        "gbs": round(alg_bytes / (us * 1e-6) / 1e9, 1)}
 
-    last_slots = int(slots_np[-1]) if cfg.moe else 0
     wb = q4k_bytes if cfg.attn_fmt == 4 else q80_bytes
+    R = m.rows   # all rows of the step
     per_launch("kquant_gemv qkv", lambda i: ops.gemm_kquant_a_prepared(
-        c.attn_fmt, Lw[i].qkv[0], Lw[i].qkv[1], m.proj, T, c.qkv_n, H, m.ws_h), wb(c.qkv_n, H))
+        c.attn_fmt, Lw[i].qkv[0], Lw[i].qkv[1], m.proj, R, c.qkv_n, H, m.ws_h), wb(c.qkv_n, H))
     per_launch("paged_attention (split + merge)", lambda i: ops.paged_attention_explicit(
         m.q, m.k_pools[i], m.v_pools[i], m.attn, m.table, m.lens, c.head_dim ** -0.5,
-        m.attn_scratch, tree=m.tree), (c.context + T) * c.kv_heads * c.head_dim * 4)
+        m.attn_scratch, tree=m.tree), B * (c.context + T) * c.kv_heads * c.head_dim * 4)
     if cfg.moe:
         F = c.expert_ffn
-        ns = T * c.topk + 1
-        # the expert gate/up and down GEMVs: one launch (moe_experts_kernel)
+        # the expert gate/up and down GEMVs: one launch (moe_experts_kernel) per 16-row chunk;
+        # timed on the first chunk with the plan the last layer left for it
+        n0 = m.moe_chunks[0][1]
+        plan0 = m.plans[0]
+        slots0 = int(plan0[:4].view(torch.int32).item())
         per_launch("moe_experts", lambda i: Lops.moe_gate_up_down(
-            c.ffn_fmt, Lw[i].gu, Lw[i].dn, Lw[i].sh_gu, Lw[i].sh_dn, m.plan, m.ws_h2, m.route_w,
-            m.shared_w, m.moe_act, m.pairs, m.shared_out, T, ns, c.experts, H, F),
-            last_slots * (q4k_bytes(2 * F, H) + q4k_bytes(H, F)))
+            c.ffn_fmt, Lw[i].gu, Lw[i].dn, Lw[i].sh_gu, Lw[i].sh_dn, plan0, m.ws_h2,
+            m.route_w[:n0], m.shared_w[:n0], m.moe_act, m.pairs[:n0 * c.topk], m.shared_out[:n0],
+            n0, n0 * c.topk + 1, c.experts, H, F),
+            slots0 * (q4k_bytes(2 * F, H) + q4k_bytes(H, F)))
     else:
+        n0 = m.row_chunks[0][1]
         per_launch("gate_up_swiglu", lambda i: Lops.gate_up_swiglu(
-            c.ffn_fmt, Lw[i].gu[0], Lw[i].gu[1], m.ws_h2, m.act, T, c.ffn, H),
+            c.ffn_fmt, Lw[i].gu[0], Lw[i].gu[1], m.ws_h2, m.act[:n0], n0, c.ffn, H),
             q4k_bytes(2 * c.ffn, H))
     if sel is not None:
         us = timed_graph(lambda: acc.propose(), 5, stream) * 1e3
@@ -451,7 +464,7 @@ def bench_step(args, name):
         kern["draft_select (chunks + table + walk)"] = {
             "us": round(us, 3), "alg_bytes": int(sb), "gbs": round(sb / (us * 1e-6) / 1e9, 1)}
     adaptive = None
-    if cfg.name == CONFIGS["config4"].name:
+    if cfg.name == CONFIGS["config4"].name and B == 1:
         # BASELINE config 1 (the acceptance alone) beside the north-star step
         kern["config1_acceptance"] = dict(time_acceptance(reps=200), outside_step=True)
         # the draft heads that produce the next proposal, and the adaptive prefix scheduler
@@ -469,15 +482,21 @@ def bench_step(args, name):
 
     # reference CPU path (oracle, torch CPU) on a bounded sample: layer 0 x layers + head +
     # acceptance
-    cpu = cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform, sel)
-    cpu_value = emitted / (cpu["step_s"])
+    cpu = cpu_step_baseline(m, cfg, rows, draft_logits[:k], drafts[:1], uniform[:1],
+                            sel and dict(sel, hp=sel["hp"][:k], anchor=sel["anchor"][:1],
+                                         temp=sel["temp"][:1], u=sel["u"][:1]))
+    # the CPU path verifies one request per step; a batch costs B of them
+    cpu_value = emitted / (cpu["step_s"] * B)
+    if B > 1:
+        cpu["sample"] += f"; x{B} requests (the CPU path verifies one request at a time)"
     return {
         "metric": METRIC, "value": round(emitted / (ms * 1e-3), 2), "unit": "tok/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_k weights x bf16 activations (fp16/bf16 MFMA, fp32 accumulate)",
         "data": weights_note(cfg),
-        "config": {"workload": cfg.name, "layers": cfg.layers, "hidden": cfg.hidden,
+        "config": {"workload": cfg.name + (f"_batch{B}" if B > 1 else ""),
+                   "layers": cfg.layers, "hidden": cfg.hidden, "requests": B,
                    "block_rows": T, "context": cfg.context, "vocab": V,
                    "experts": cfg.experts, "topk": cfg.topk,
                    "attn_fmt": "q4_k" if cfg.attn_fmt == 4 else "q8_0",
@@ -621,9 +640,10 @@ def cpu_step_baseline(m, cfg, rows, draft_logits, drafts, uniform, sel=None):
     torch.set_num_threads(cores)
     T = cfg.block
     masks = tree_masks(cfg.tree_parents) if cfg.tree_parents else [(2 << t) - 1 for t in range(T)]
-    x = m.embed[m.ids].cpu().float()
-    cos, sin = RM.rope_tables(m.positions.cpu(), m.inv_freq.cpu())
-    pages = m.table.view(-1).long().cpu()
+    # the first request of the batch
+    x = m.embed[m.ids[:T]].cpu().float()
+    cos, sin = RM.rope_tables(m.positions[:T].cpu(), m.inv_freq.cpu())
+    pages = m.table[0].long().cpu()
     kctx = RM.cache_rows(m.k_pools[0].cpu(), pages, cfg.kv_heads, cfg.head_dim, 16, key=True)[:cfg.context]
     vctx = RM.cache_rows(m.v_pools[0].cpu(), pages, cfg.kv_heads, cfg.head_dim, 16, key=False)[:cfg.context]
     lw0 = m.layers[0]
@@ -690,6 +710,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="config4", choices=sorted(WORKLOADS))
+    ap.add_argument("--batch", type=int, default=1,
+                    help="requests verified together in one step (configs 3-5; rows = batch x "
+                         "block <= 256)")
     ap.add_argument("--no-adaptive", action="store_true",
                     help="leave out the adaptive-prefix cost profile (the profiler's runs at "
                          "1-16 rows would mix into a kernel trace of the step)")

@@ -86,6 +86,180 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv(const u32x4* __restrict__
 }
 
 // ---------------------------------------------------------------------------------------
+// The same GEMV over MT 16-row tiles at once (a verify step wider than 16 rows): each wave
+// loads a superblock's weights once, decodes them once into the fp16 B operands, and multiplies
+// them against the prepared operands of every row tile (blockIdx.y: the group of MT tiles).
+// The per-row arithmetic and the waves' superblock split are those of kquant_gemv with NW
+// waves, so every row gets the bits of the 16-row launch.
+// ---------------------------------------------------------------------------------------
+template <int FMT>
+struct DecodedSb {
+  half8 b[8];     // B operands of the 8 sub-blocks
+  float a[8];     // per-sub-block scales (odd Q4_K sub-blocks: x 1/16 for the 16 q encoding)
+  float beta_lo, beta_hi;
+};
+
+template <int FMT>
+__device__ __forceinline__ void decode_sb(const u32x4* qv, u32x4 meta, int kq, uint32_t M,
+                                          DecodedSb<FMT>& d) {
+  if constexpr (FMT == FMT_Q4_K) {
+    const float dd = f16_to_f32((uint16_t)(meta.x & 0xffff));
+    const float dmin = f16_to_f32((uint16_t)(meta.x >> 16));
+    const uint32_t s0 = meta.y, s1 = meta.z, s2 = meta.w;
+    const uint32_t sc03 = s0 & 0x3f3f3f3fu;
+    const uint32_t m03 = s1 & 0x3f3f3f3fu;
+    const uint32_t sc47 = (s2 & 0x0f0f0f0fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t m47 = ((s2 >> 4) & 0x0f0f0f0fu) | ((s1 >> 2) & 0x30303030u);
+    float a[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[i] = dd * byte_f(sc03, i);
+      a[4 + i] = dd * byte_f(sc47, i);
+    }
+    const float m_lo = dmin * byte_f(m03, kq);
+    const float m_hi = dmin * byte_f(m47, kq);
+    const float off = (kq & 1) ? 64.0f : 1024.0f;
+    d.beta_lo = __builtin_fmaf(off, dd * byte_f(sc03, kq), m_lo);
+    d.beta_hi = __builtin_fmaf(off, dd * byte_f(sc47, kq), m_hi);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) d.a[j] = (j & 1) ? a[j] * 0.0625f : a[j];
+    q4_group(qv[0].x, qv[0].y, M, d.b[0], d.b[1]);
+    q4_group(qv[0].z, qv[0].w, M, d.b[2], d.b[3]);
+    q4_group(qv[1].x, qv[1].y, M, d.b[4], d.b[5]);
+    q4_group(qv[1].z, qv[1].w, M, d.b[6], d.b[7]);
+  } else {
+    const uint32_t dw[4] = {meta.x, meta.y, meta.z, meta.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      d.a[2 * i] = f16_to_f32((uint16_t)(dw[i] & 0xffff));
+      d.a[2 * i + 1] = f16_to_f32((uint16_t)(dw[i] >> 16));
+    }
+    d.beta_lo = 1152.0f * f16_to_f32((uint16_t)(((kq & 1) ? (dw[kq >> 1] >> 16) : dw[kq >> 1]) & 0xffff));
+    d.beta_hi = 1152.0f * f16_to_f32((uint16_t)(((kq & 1) ? (dw[2 + (kq >> 1)] >> 16) : dw[2 + (kq >> 1)]) & 0xffff));
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {
+      d.b[2 * jp] = q8_sub(qv[jp].x, qv[jp].y, M);
+      d.b[2 * jp + 1] = q8_sub(qv[jp].z, qv[jp].w, M);
+    }
+  }
+}
+
+// tile_superblock's arithmetic on decoded weights: the same products and sums in the same order.
+template <int FMT>
+__device__ __forceinline__ floatx4 apply_sb(const DecodedSb<FMT>& d, const half8* xa, float sx0,
+                                            float sx1) {
+  const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+  floatx4 acc = zero;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], d.b[j], zero, 0, 0, 0);
+    acc += d.a[j] * c;
+  }
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sx0, d.beta_lo, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(sx1, d.beta_hi, acc, 0, 0, 0);
+  return acc;
+}
+
+template <int FMT, int NW, int MT>
+__global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restrict__ quant,
+                                                          const u32x4* __restrict__ meta,
+                                                          const void* __restrict__ ws,
+                                                          void* __restrict__ c, int M, int N,
+                                                          int S, int c_bf16, size_t tile_bytes) {
+  constexpr int QV = QLayout<FMT>::kQuantVecs;
+  __shared__ floatx4 part[NW][1][64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kq = lane >> 4, r = lane & 15;
+  const int tiles = N / TILE_N;
+  const int tile = blockIdx.x;
+  const int m0 = blockIdx.y * MT;
+  const int row_tiles = (M + TILE_M - 1) / TILE_M;
+  const int mt = row_tiles - m0 < MT ? row_tiles - m0 : MT;
+  const GemvStreams st = make_streams<FMT>(quant, meta, ws, tiles, S, lane, 16);
+  __amdgpu_buffer_rsrc_t xr[MT], sxr[MT], scr[MT];
+  uint32_t vx[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    XPrepView xv = xprep_view((char*)ws + (size_t)(m0 + m) * tile_bytes, S);
+    xr[m] = __builtin_amdgcn_make_buffer_rsrc((void*)xv.xop, 0, S * 8 * 64 * 16, 0x00020000);
+    sxr[m] = __builtin_amdgcn_make_buffer_rsrc((void*)xv.sxop, 0, S * 2 * 64 * 4, 0x00020000);
+    scr[m] = __builtin_amdgcn_make_buffer_rsrc((void*)xv.scale, 0, S * 16 * 4, 0x00020000);
+    vx[m] = r < M - (m0 + m) * TILE_M ? lane * 16 : 0x80000000u;
+  }
+  const uint32_t Mv = decode_magic<FMT>();
+  floatx4 acc[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int s = w; s < S; s += NW) {
+    u32x4 q[1][QV], mt4[1];
+    load_sb_w<FMT, 1>(q, mt4, st, s, S, tile, 1);
+    // every row tile's operands of this superblock in flight with the weights
+    u32x4 x[MT][8];
+    float sx0[MT], sx1[MT];
+    floatx4 sc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m >= mt) break;  // uniform
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[m][j] = bload4(xr[m], vx[m], (uint32_t)((s * 8 + j) * 64 * 16));
+      sx0[m] = bload1(sxr[m], lane * 4, (uint32_t)((s * 2 + 0) * 64 * 4));
+      sx1[m] = bload1(sxr[m], lane * 4, (uint32_t)((s * 2 + 1) * 64 * 4));
+      sc[m] = __builtin_bit_cast(floatx4, bload4(scr[m], kq * 16, (uint32_t)(s * 16 * 4)));
+    }
+    DecodedSb<FMT> d;
+    decode_sb<FMT>(q[0], mt4[0], kq, Mv, d);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m >= mt) break;  // uniform
+      half8 xa[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x[m][j]);
+      const floatx4 sb = apply_sb<FMT>(d, xa, sx0[m], sx1[m]);
+      acc[m] += sb * sc[m];
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m >= mt) break;  // uniform
+    if (m) __syncthreads();
+    combine_waves<1, NW>(part, &acc[m], w, lane);
+    if (threadIdx.x < 64) {
+      const int l = threadIdx.x;
+      floatx4 v = part[0][0][l];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) v += part[ww][0][l];
+      const int n = tile * TILE_N + (l & 15);
+      const int rb = (m0 + m) * TILE_M + 4 * (l >> 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = rb + i;
+        if (row >= M) break;
+        if (c_bf16) ((uint16_t*)c)[(int64_t)row * N + n] = f32_to_bf16(v[i]);
+        else ((float*)c)[(int64_t)row * N + n] = v[i];
+      }
+    }
+  }
+}
+
+template <int FMT, int NW>
+int launch_gemv_mt(const void* quant, const void* meta, const void* ws, void* c, int M, int N,
+                   int S, int c_bf16, hipStream_t s) {
+  const int tiles = N / TILE_N;
+  const int row_tiles = (M + TILE_M - 1) / TILE_M;
+  const size_t tb = xprep_tile_bytes(S);
+  auto go = [&](auto kern, int mt) {
+    hipLaunchKernelGGL(kern, dim3(tiles, (row_tiles + mt - 1) / mt), dim3(NW * 64), 0, s,
+                       (const u32x4*)quant, (const u32x4*)meta, ws, c, M, N, S, c_bf16, tb);
+  };
+  if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2>, 2);
+  else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3>, 3);
+  else go(kquant_gemv_mt<FMT, NW, 4>, 4);
+  SV_CHECK_LAUNCH();
+  return SV_OK;
+}
+
+// ---------------------------------------------------------------------------------------
 // Repack GGUF blocks into (quant, meta).
 // ---------------------------------------------------------------------------------------
 __global__ void shuffle_q4k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ quant,
@@ -134,6 +308,13 @@ __global__ void shuffle_q80(const uint8_t* __restrict__ gguf, uint8_t* __restric
 }
 
 bool fmt_ok(int fmt) { return fmt == FMT_Q4_K || fmt == FMT_Q8_0; }
+
+// The GEMV kernels address a weight through one buffer resource with 32-bit offsets: its
+// packed quants (N * K / 2 bytes for Q4_K, N * K for Q8_0) must stay below 4 GiB.
+bool weight_fits(int fmt, int64_t N, int64_t K) {
+  const int64_t qbytes = fmt == FMT_Q4_K ? N * (K / 2) : N * K;
+  return qbytes <= (int64_t)0xFFFFFC00 && N * (K / 256) * 256 <= (int64_t)0xFFFFFFFF;
+}
 
 template <int FMT, int NTILE, int NW, bool RAW = false>
 int launch_gemv(const void* quant, const void* meta, const void* ws, void* c, int M, int N, int S,
@@ -248,12 +429,22 @@ SV_API int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, cons
                                           void* c, int64_t M, int64_t N, int64_t K,
                                           int c_is_bf16, const void* ws, void* stream) {
   if (!fmt_ok(fmt) || M < 0 || N <= 0 || K <= 0 || K % 256 || N % TILE_N) return SV_EINVAL;
+  if (!weight_fits(fmt, N, K)) return SV_ENOTSUP;
   if (M == 0) return SV_OK;
   hipStream_t s = (hipStream_t)stream;
   const int64_t S = K / 256;
   const size_t tb = xprep_tile_bytes(S);
   const int64_t mt = (M + TILE_M - 1) / TILE_M;
   const size_t esz = c_is_bf16 ? 2 : 4;
+  if (mt > 1 && g_gemv_variant == 0) {
+    // wider than one row tile: every weight tile decoded once for up to four row tiles (the
+    // waves split the superblocks as the automatic 16-row launch does: the same bits)
+    if (fmt == FMT_Q4_K)
+      return S >= 8 ? launch_gemv_mt<FMT_Q4_K, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, s)
+                    : launch_gemv_mt<FMT_Q4_K, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, s);
+    return S >= 8 ? launch_gemv_mt<FMT_Q8_0, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, s)
+                  : launch_gemv_mt<FMT_Q8_0, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, s);
+  }
   for (int64_t t = 0; t < mt; ++t) {
     const int rows = (int)((M - t * TILE_M) < TILE_M ? (M - t * TILE_M) : TILE_M);
     void* ct = (char*)c + (size_t)t * TILE_M * N * esz;
@@ -270,6 +461,7 @@ SV_API int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, c
                                  void* c, int64_t M, int64_t N, int64_t K, int c_is_bf16, void* ws,
                                  void* stream) {
   if (!fmt_ok(fmt) || M < 0 || N <= 0 || K <= 0 || K % 256 || N % TILE_N) return SV_EINVAL;
+  if (!weight_fits(fmt, N, K)) return SV_ENOTSUP;
   if (M == 0) return SV_OK;
   if (M <= TILE_M && M * K * 2 <= INT32_MAX) {
     // one launch: the GEMV converts the bf16 activations itself (same operands as the

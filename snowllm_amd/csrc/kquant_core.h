@@ -403,8 +403,15 @@ __device__ __forceinline__ GemvStreams make_streams(const void* quant, const voi
   const int kq = lane >> 4, r = lane & 15;
   XPrepView xv = xprep_view((void*)ws, S);
   GemvStreams st;
-  st.quant = __builtin_amdgcn_make_buffer_rsrc((void*)quant, 0, tiles * S * QV * 64 * 16, 0x00020000);
-  st.meta = __builtin_amdgcn_make_buffer_rsrc((void*)meta, 0, tiles * S * 16 * 16, 0x00020000);
+  // byte ranges in 64 bits, clamped to what one buffer resource holds (the entry points refuse
+  // weights whose offsets would not fit 32 bits)
+  const int64_t qn = (int64_t)tiles * S * QV * 64 * 16, mn = (int64_t)tiles * S * 16 * 16;
+  st.quant = __builtin_amdgcn_make_buffer_rsrc((void*)quant, 0,
+                                               (int)(uint32_t)(qn < 0xFFFFFFFFll ? qn : 0xFFFFFFFFll),
+                                               0x00020000);
+  st.meta = __builtin_amdgcn_make_buffer_rsrc((void*)meta, 0,
+                                              (int)(uint32_t)(mn < 0xFFFFFFFFll ? mn : 0xFFFFFFFFll),
+                                              0x00020000);
   st.xop = __builtin_amdgcn_make_buffer_rsrc((void*)xv.xop, 0, S * 8 * 64 * 16, 0x00020000);
   st.sxop = __builtin_amdgcn_make_buffer_rsrc((void*)xv.sxop, 0, S * 2 * 64 * 4, 0x00020000);
   st.scale = __builtin_amdgcn_make_buffer_rsrc((void*)xv.scale, 0, S * 16 * 4, 0x00020000);

@@ -398,9 +398,9 @@ class VerifyModel:
     # -----------------------------------------------------------------------------------
     def forward(self, *, upto_layer=None, record_slots=None):
         """Target model over the staged block -> self.logits [T, V] f32. record_slots: optional
-        int32 [layers] device tensor that receives each MoE layer's plan size (routed unique
-        experts + shared) for byte accounting; it adds one copy per layer, so timed steps leave
-        it out."""
+        int32 [layers] device tensor that receives each MoE layer's unique routed experts over
+        all rows + the shared expert, for byte accounting; it adds a count per layer, so timed
+        steps leave it out."""
         c, T = self.cfg, self.rows
         H = c.hidden
         if self.embed_q4k:
@@ -478,8 +478,7 @@ class VerifyModel:
                         Lops.moe_route_plan(self.router_logits[rs], c.experts, K,
                                             self.route_w[rs], self.route_ids[rs],
                                             self.shared_w[rs], plan)
-                    if record_slots is not None:
-                        record_slots[i:i + 1].add_(plan[:4].view(torch.int32))
+
                     # gate/up and down in one launch: a slot's down starts when its gate/up
                     # is done
                     Lops.moe_gate_up_down(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, plan,
@@ -487,6 +486,10 @@ class VerifyModel:
                                           self.moe_act, self.pairs[r0 * K:(r0 + n) * K],
                                           self.shared_out[rs], n, n * K + 1, c.experts, H,
                                           c.expert_ffn)
+                if record_slots is not None:
+                    # unique routed experts of the whole step + the shared expert
+                    used = torch.bincount(self.route_ids.view(-1).long(), minlength=c.experts)
+                    record_slots[i:i + 1].copy_((used > 0).sum().view(1) + 1)
                 moe_out = True
             else:
                 Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,

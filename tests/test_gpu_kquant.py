@@ -116,3 +116,31 @@ def test_every_gemv_variant(gpu, fmt):
                 assert torch.equal(c, c2), v
         finally:
             lib.snowverify_gemv_variant(0)
+
+
+@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("n,k", [(5120, 2048), (512, 4096), (256, 1024)])
+def test_wide_block_gemv_equals_row_tiles(gpu, fmt, n, k):
+    """Verify steps wider than 16 rows (B x T <= 256): one launch decodes each weight tile once
+    for up to four row tiles; every row gets the bits of the 16-row launch, and the result
+    stays within the fp64 oracle's tolerance."""
+    from snowllm_amd import ops
+    raw = Q.make_q4_k(n, k, seed=n + 3) if fmt == 4 else Q.make_q8_0(n, k, seed=n + 3)
+    quant, meta = ops.gemm_kquant_shuffle_b(fmt, torch.from_numpy(raw).cuda(), n, k)
+    w = Q.dequant(raw, fmt, n, k)
+    tb = ops.gemm_kquant_a_ws_bytes(16, k)
+    for m in (17, 36, 48, 64, 100, 256):
+        print(f"wide gemv fmt={fmt} M={m} N={n} K={k}", flush=True)
+        x = Q.make_activations(m, k, seed=m + 1)
+        ws = torch.empty(ops.gemm_kquant_a_ws_bytes(m, k), dtype=torch.uint8, device="cuda")
+        c = torch.empty(m, n, device="cuda")
+        ops.gemm_kquant_a(fmt, x.cuda(), quant, meta, c, m, n, k, ws)
+        tiles = torch.empty_like(c)
+        for r0 in range(0, m, 16):
+            rows = min(16, m - r0)
+            at = (r0 // 16) * tb
+            ops.gemm_kquant_a_prepared(fmt, quant, meta, tiles[r0:r0 + rows], rows, n, k,
+                                       ws[at:at + tb])
+        torch.cuda.synchronize()
+        assert torch.equal(c, tiles), m
+        assert Q.rel_l2(c.cpu().numpy(), Q.gemv_reference(x, w)) < TOL
