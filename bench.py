@@ -145,8 +145,8 @@ def bench_gemv(args):
                    "weight_copies_rotated": copies},
         "roofline": {"bound": "hbm", "kernel": "kquant_gemv<Q4_K>", "achieved": round(achieved, 1),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": None, "alg_bytes_per_launch": alg_bytes,
-                     "kernel_us": round(ms_gemv * 1e3, 3)},
+                     "traffic": read_traffic("kquant_gemv<Q4_K>", "gemv"),
+                     "alg_bytes_per_launch": alg_bytes, "kernel_us": round(ms_gemv * 1e3, 3)},
         "timings_us": {"op_eager": round(ms_step * 1e3, 3), "op_graph": round(us, 3),
                        "gemv_kernel_eager": round(ms_gemv * 1e3, 3)},
         "tflops_effective": round(flops / (ms_gemv * 1e-3) / 1e12, 1),
@@ -472,13 +472,16 @@ def bench_step(args, name):
         heads = time_draft_heads(stream, V, k)
         kern.update(heads)
         if not args.no_adaptive:
-            adaptive = adaptive_prefix(m, heads["dspark_markov (per block row)"]["us"] * k * 1e-6)
-    # dominant single kernel per step (launch time x launches per step)
-    single = {kk: v for kk, v in kern.items()
-              if "+" not in kk and "us" in v and not v.get("outside_step")}
-    dom = max(single, key=lambda kk: single[kk]["us"])
+            adaptive = adaptive_prefix(m, heads["dspark_markov (per block row)"]["us"] * k * 1e-6,
+                                       heads["_markov_confidence"])
+        kern.pop("_markov_confidence", None)
+    # dominant kernel of the step (launch time; every candidate runs once per layer); the
+    # attention counts as its split + merge pair
+    per_step = {kk: (1 if kk.startswith("draft_select") else cfg.layers) for kk in kern}
+    single = {kk: v for kk, v in kern.items() if "us" in v and not v.get("outside_step")}
+    dom = max(single, key=lambda kk: single[kk]["us"] * per_step[kk])
     d = kern[dom]
-    traffic = read_traffic(dom) if cfg.name == CONFIGS[TRAFFIC_WORKLOAD].name else None
+    traffic = read_traffic(dom, name) if B == 1 else None
 
     # reference CPU path (oracle, torch CPU) on a bounded sample: layer 0 x layers + head +
     # acceptance
@@ -557,18 +560,28 @@ def time_draft_heads(stream, V, k, hidden=2048, markov_rank=256):
         "outside_step": True,
         "note": "W2 (78 MB) is read by each of the block's rows; after the first it is largely "
                 "served from the 256 MB Infinity Cache"}
+    # the head's own confidences over a 15-draft proposal: the adaptive scheduler's input
+    # (snowllm/engine/spec_decode.py:157-166 feeds it the drafter's confidences per request)
+    n = 15
+    rows15 = torch.randn(n, hidden, device="cuda", generator=g).bfloat16()
+    logits15 = torch.randn(n, V, device="cuda", generator=g)
+    path15 = torch.empty(1, n, dtype=torch.int64, device="cuda")
+    conf15 = torch.empty(1, n, device="cuda")
+    mk.propose(rows15, logits15, anchor, path15, conf15)
+    out["_markov_confidence"] = [round(float(c), 4) for c in conf15[0].cpu()]
     return out
 
 
-def adaptive_prefix(m, draft_s, rows=tuple(range(1, 17))):
+def adaptive_prefix(m, draft_s, confidence, rows=tuple(range(1, 17))):
     """The DSpark prefix scheduler (snowllm/engine/dspark_schedule.py) on step costs measured
-    here: verify steps of 1..16 rows (eager and graph) plus the Markov head's time, and a
-    synthetic confidence profile (c_j = 0.9 * 0.97^j over 15 drafted tokens). Every row count
-    of a batch-1 block gets a captured graph, as the reference's profile of its decode shapes
+    here: verify steps of 1..16 rows (eager and graph) plus the Markov head's time, and the
+    Markov head's own confidences over a 15-draft proposal (random-init weights, so they say
+    nothing about draft quality; a trained head's would). Every row count of a batch-1 block
+    gets a captured graph, as the reference's profile of its decode shapes
     (snowllm/engine/spec_decode.py:149-161)."""
     from snowllm_amd.dspark_schedule import PrefixScheduler, profile_step_costs
     cost = profile_step_costs(m, rows, draft_seconds=draft_s)
-    conf = [[0.9 * 0.97 ** j for j in range(15)]]
+    conf = [list(confidence)]
     lengths = PrefixScheduler(16).choose([0], conf, [15], cost)
     surv, s = [], 1.0
     for c in conf[0]:
@@ -578,7 +591,9 @@ def adaptive_prefix(m, draft_s, rows=tuple(range(1, 17))):
     def rate(n):
         return (1 + sum(surv[:n])) / cost(1 + n)
     return {"step_us_by_rows": {n: round(cost.graphs[n] * 1e6, 1) for n in rows},
-            "draft_us": round(draft_s * 1e6, 1), "confidence": "0.9*0.97^j, 15 drafts",
+            "draft_us": round(draft_s * 1e6, 1),
+            "confidence": {"source": "dspark_markov confidence head (15 drafts)",
+                           "values": conf[0]},
             "chosen_drafts": lengths[0], "expected_tokens_per_s": round(rate(lengths[0]), 1),
             "fixed_block8_tokens_per_s": round(rate(8), 1)}
 
@@ -607,14 +622,18 @@ def chain_rows(parents):
         rows.append(kids[0])
 
 
-TRAFFIC_WORKLOAD = "config4"  # the workload profiles/traffic.txt was measured on
+# the committed rocprofv3 PMC summaries and the workloads they were measured on
+TRAFFIC_FILES = {"config4": "traffic.txt", "config5": "traffic_config5.txt",
+                 "gemv": "traffic_gemv.txt"}
 
 
-def read_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
-    (profiles/traffic.txt: 'kernel | fetch_bytes | write_bytes' rows, already scaled by the
-    copy-kernel calibration, measured on TRAFFIC_WORKLOAD), or None."""
-    path = os.path.join(ROOT, "profiles", "traffic.txt")
+def read_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary of `workload`
+    (profiles/traffic*.txt: 'kernel | fetch_bytes | write_bytes' rows, already scaled by the
+    copy-kernel calibration), or None."""
+    if workload not in TRAFFIC_FILES:
+        return None
+    path = os.path.join(ROOT, "profiles", TRAFFIC_FILES[workload])
     try:
         for line in open(path):
             parts = [x.strip() for x in line.split("|")]
