@@ -11,12 +11,15 @@ Follows the reference's GGUF path for the parts this build computes:
     moe_kquant_shuffle_gate_up / _down (qwen3_5_weights.py:307-335, ops/moe.py:136-162), the
     shared expert as a one-expert stack (qwen3_5_weights.py:296-304), the router as
     [ffn_gate_inp; ffn_gate_inp_shexp] bf16 (qwen3_5_weights.py:333-335);
-  - the embedding as bf16 or Q4_K blocks and the head as bf16 or Q4_K / Q8_0 blocks, tied to
-    the embedding when the file has no output.weight (qwen3_5_weights.py:405-421).
+  - the embedding as bf16 or Q4_K blocks and the head as bf16 or Q4_K / Q5_K / Q6_K / Q8_0
+    blocks, tied to the embedding when the file has no output.weight
+    (qwen3_5_weights.py:405-421).
 
 Scope: every layer must be full GQA attention with QK-norm and no output gate, followed by a
-SwiGLU MLP or a routed MoE with a shared expert whose width equals the experts'; matrices in
-Q4_K or Q8_0, with q/k/v in one format and the experts and the shared expert all Q4_K.
+SwiGLU MLP or a routed MoE with a shared expert whose width equals the experts'; attention and
+dense matrices in Q4_K, Q5_K, Q6_K or Q8_0 (the formats the reference's GEMM takes, snowllm/
+checkpoint/gguf/source.py:263-272), with q/k/v in one format, gate/up in one and down in any;
+the experts and the shared expert all Q4_K.
 Anything else raises SnowLLMError naming the tensor; nothing falls back to another path.
 """
 import torch
@@ -81,8 +84,8 @@ def config_from_gguf(g: GGUF, *, context: int, block: int, tree_parents=(),
 def _kfmt(g: GGUF, name: str) -> int:
     q = g[name].quant.name
     if q not in KQUANT_FORMAT:
-        raise SnowLLMError(f"{g.path.name}: {name} is {q}; this build computes Q4_K and Q8_0 "
-                           f"matrices")
+        raise SnowLLMError(f"{g.path.name}: {name} is {q}; this build computes Q4_K, Q5_K, "
+                           f"Q6_K and Q8_0 matrices")
     return KQUANT_FORMAT[q]
 
 

@@ -1265,7 +1265,9 @@ SV_API int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c
 // [2F, K] k-quant weight (gate rows first) and ws the prepared operands of x. M <= 16.
 SV_API int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* meta, const void* ws,
                                      void* act, int64_t M, int64_t F, int64_t K, void* stream) {
-  if ((fmt != 4 && fmt != 8) || M <= 0 || M > 16 || F <= 0 || F % 16 || K % 256) return SV_EINVAL;
+  if ((fmt != 4 && fmt != 5 && fmt != 6 && fmt != 8) || M <= 0 || M > 16 || F <= 0 || F % 16 ||
+      K % 256)
+    return SV_EINVAL;
   const int S = (int)(K / 256);
   hipStream_t s = Sx(stream);
   // two pairs per workgroup, two waves per pair: at FFN 14336 the 448 workgroups are all
@@ -1274,14 +1276,15 @@ SV_API int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* met
   // 3.266 -> 3.182 ms; eight waves per pair: 26.2 us)
   constexpr int WS = 2, PPB = 2;
   const dim3 grid((unsigned)((F / 16 + PPB - 1) / PPB), 1);
-  if (fmt == 4)
-    hipLaunchKernelGGL((gate_up_kernel<4, WS, PPB>), grid, dim3(64 * WS * PPB), 0, s,
-                       (const uint8_t*)quant, (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr,
-                       0, ws, (uint16_t*)act, (int)M, (int)F, S);
-  else
-    hipLaunchKernelGGL((gate_up_kernel<8, WS, PPB>), grid, dim3(64 * WS * PPB), 0, s,
-                       (const uint8_t*)quant, (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr,
-                       0, ws, (uint16_t*)act, (int)M, (int)F, S);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(64 * WS * PPB), 0, s, (const uint8_t*)quant,
+                       (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr, 0, ws,
+                       (uint16_t*)act, (int)M, (int)F, S);
+  };
+  if (fmt == 4) go(gate_up_kernel<4, WS, PPB>);
+  else if (fmt == 5) go(gate_up_kernel<5, WS, PPB>);
+  else if (fmt == 6) go(gate_up_kernel<6, WS, PPB>);
+  else go(gate_up_kernel<8, WS, PPB>);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }

@@ -18,6 +18,7 @@
 #include "kquant_core.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace {
 using namespace kq;
@@ -307,12 +308,82 @@ __global__ void shuffle_q80(const uint8_t* __restrict__ gguf, uint8_t* __restric
   }
 }
 
-bool fmt_ok(int fmt) { return fmt == FMT_Q4_K || fmt == FMT_Q8_0; }
+// Q5_K: the Q4_K nibble layout of qs (@48), then each lane's 8 qh bytes (@16) after the tile-
+// superblock's nibbles; meta as Q4_K (d, dmin, scales: the block's first 16 bytes).
+__global__ void shuffle_q5k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ quant,
+                            uint8_t* __restrict__ meta, int64_t N, int64_t S) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= N * S) return;
+  const int64_t n = id / S, s = id % S;
+  const uint8_t* blk = gguf + (n * S + s) * 176;
+  const int64_t tile = n / TILE_N;
+  const int col = (int)(n % TILE_N);
+  const int64_t ts = tile * S + s;
+  uint8_t* mo = meta + (ts * 16 + col) * 16;
+  for (int i = 0; i < 16; ++i) mo[i] = blk[i];
+  const uint8_t* qh = blk + 16;
+  const uint8_t* qs = blk + 48;
+  uint8_t* base = quant + ts * 2560;
+  for (int kq = 0; kq < 4; ++kq) {
+    const int lane = col + 16 * kq;
+    for (int h = 0; h < 2; ++h) {
+      uint8_t* qo = base + (h * 64 + lane) * 16;
+      for (int i = 0; i < 8; ++i) {
+        qo[i] = qs[64 * h + 8 * kq + i];
+        qo[8 + i] = qs[64 * h + 32 + 8 * kq + i];
+      }
+    }
+    uint8_t* ho = base + 2048 + lane * 8;
+    for (int i = 0; i < 8; ++i) ho[i] = qh[8 * kq + i];
+  }
+}
+
+// Q6_K: per lane three 16-byte vectors (ql of half 0, ql of half 1, qh of both halves, each
+// the bytes l = 8 kq .. 8 kq + 7 of its two 32-byte runs); meta: the 16 int8 scales per
+// column, and after every tile-superblock's scales the fp16 d per (tile-superblock, column).
+__global__ void shuffle_q6k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ quant,
+                            uint8_t* __restrict__ meta, int64_t N, int64_t S) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= N * S) return;
+  const int64_t n = id / S, s = id % S;
+  const uint8_t* blk = gguf + (n * S + s) * 210;
+  const int64_t tile = n / TILE_N;
+  const int col = (int)(n % TILE_N);
+  const int64_t ts = tile * S + s;
+  uint8_t* mo = meta + (ts * 16 + col) * 16;
+  for (int i = 0; i < 16; ++i) mo[i] = blk[192 + i];
+  uint8_t* dd = meta + N * S * 16 + (ts * 16 + col) * 2;
+  dd[0] = blk[208];
+  dd[1] = blk[209];
+  const uint8_t* ql = blk;
+  const uint8_t* qh = blk + 128;
+  uint8_t* base = quant + ts * 3072;
+  for (int kq = 0; kq < 4; ++kq) {
+    const int lane = col + 16 * kq;
+    for (int half = 0; half < 2; ++half) {
+      uint8_t* qo = base + (half * 64 + lane) * 16;
+      for (int i = 0; i < 8; ++i) {
+        qo[i] = ql[64 * half + 8 * kq + i];
+        qo[8 + i] = ql[64 * half + 32 + 8 * kq + i];
+      }
+    }
+    uint8_t* ho = base + (2 * 64 + lane) * 16;
+    for (int i = 0; i < 8; ++i) {
+      ho[i] = qh[8 * kq + i];
+      ho[8 + i] = qh[32 + 8 * kq + i];
+    }
+  }
+}
+
+bool fmt_ok(int fmt) {
+  return fmt == FMT_Q4_K || fmt == FMT_Q5_K || fmt == FMT_Q6_K || fmt == FMT_Q8_0;
+}
 
 // The GEMV kernels address a weight through one buffer resource with 32-bit offsets: its
 // packed quants (N * K / 2 bytes for Q4_K, N * K for Q8_0) must stay below 4 GiB.
 bool weight_fits(int fmt, int64_t N, int64_t K) {
-  const int64_t qbytes = fmt == FMT_Q4_K ? N * (K / 2) : N * K;
+  const int64_t qbytes = fmt == FMT_Q4_K ? N * (K / 2) : fmt == FMT_Q5_K ? N * (K / 256) * 160
+                         : fmt == FMT_Q6_K ? N * (K / 256) * 192 : N * K;
   return qbytes <= (int64_t)0xFFFFFC00 && N * (K / 256) * 256 <= (int64_t)0xFFFFFFFF;
 }
 
@@ -328,6 +399,18 @@ int launch_gemv(const void* quant, const void* meta, const void* ws, void* c, in
 }
 
 int g_gemv_variant = 0;  // 0 = automatic; see snowverify_gemv_variant
+
+// Calls f with std::integral_constant<int, FMT> for a supported format id.
+template <class F>
+int by_format(int fmt, F&& f) {
+  switch (fmt) {
+    case FMT_Q4_K: return f(std::integral_constant<int, FMT_Q4_K>{});
+    case FMT_Q5_K: return f(std::integral_constant<int, FMT_Q5_K>{});
+    case FMT_Q6_K: return f(std::integral_constant<int, FMT_Q6_K>{});
+    case FMT_Q8_0: return f(std::integral_constant<int, FMT_Q8_0>{});
+    default: return SV_EINVAL;
+  }
+}
 
 template <int FMT, bool RAW = false>
 int dispatch_gemv(const void* quant, const void* meta, const void* ws, void* c, int M, int N,
@@ -367,18 +450,27 @@ int dispatch_gemv(const void* quant, const void* meta, const void* ws, void* c, 
 SV_API int64_t snowllm_kquant_gguf_bytes(int fmt, int64_t N, int64_t K) {
   if (N < 0 || K < 0) return -1;
   if (fmt == FMT_Q4_K) return K % 256 ? -1 : N * (K / 256) * 144;
+  if (fmt == FMT_Q5_K) return K % 256 ? -1 : N * (K / 256) * 176;
+  if (fmt == FMT_Q6_K) return K % 256 ? -1 : N * (K / 256) * 210;
   if (fmt == FMT_Q8_0) return K % 32 ? -1 : N * (K / 32) * 34;
   return -1;
 }
 
+// Repacked sizes: quant + meta - 4 = the GGUF bytes (the quant buffer keeps 4 bytes of slack).
 SV_API int64_t snowllm_kquant_quant_bytes(int fmt, int64_t N, int64_t K) {
   if (!fmt_ok(fmt) || N < 0 || K % 256 || N % TILE_N) return -1;
-  return (fmt == FMT_Q4_K ? N * K / 2 : N * K) + 4;
+  const int64_t blocks = N * (K / 256);
+  switch (fmt) {
+    case FMT_Q4_K: return blocks * 128 + 4;
+    case FMT_Q5_K: return blocks * 160 + 4;
+    case FMT_Q6_K: return blocks * 192 + 4;
+    default: return N * K + 4;
+  }
 }
 
 SV_API int64_t snowllm_kquant_meta_bytes(int fmt, int64_t N, int64_t K) {
   if (!fmt_ok(fmt) || N < 0 || K % 256 || N % TILE_N) return -1;
-  return N * (K / 256) * 16;
+  return N * (K / 256) * (fmt == FMT_Q6_K ? 18 : 16);
 }
 
 SV_API int snowllm_kquant_supported(int fmt) { return fmt_ok(fmt) ? 1 : 0; }
@@ -396,6 +488,12 @@ SV_API int snowllm_gemm_kquant_shuffle_b(int fmt, const uint8_t* gguf, uint8_t* 
   hipStream_t s = (hipStream_t)stream;
   if (fmt == FMT_Q4_K)
     hipLaunchKernelGGL(shuffle_q4k, dim3((unsigned)((total + nt - 1) / nt)), dim3(nt), 0, s, gguf,
+                       quant, meta, N, S);
+  else if (fmt == FMT_Q5_K)
+    hipLaunchKernelGGL(shuffle_q5k, dim3((unsigned)((total + nt - 1) / nt)), dim3(nt), 0, s, gguf,
+                       quant, meta, N, S);
+  else if (fmt == FMT_Q6_K)
+    hipLaunchKernelGGL(shuffle_q6k, dim3((unsigned)((total + nt - 1) / nt)), dim3(nt), 0, s, gguf,
                        quant, meta, N, S);
   else
     hipLaunchKernelGGL(shuffle_q80, dim3((unsigned)((total + nt - 1) / nt)), dim3(nt), 0, s, gguf,
@@ -436,7 +534,7 @@ SV_API int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, cons
   const size_t tb = xprep_tile_bytes(S);
   const int64_t mt = (M + TILE_M - 1) / TILE_M;
   const size_t esz = c_is_bf16 ? 2 : 4;
-  if (mt > 1 && g_gemv_variant == 0) {
+  if (mt > 1 && g_gemv_variant == 0 && (fmt == FMT_Q4_K || fmt == FMT_Q8_0)) {
     // wider than one row tile: every weight tile decoded once for up to four row tiles (the
     // waves split the superblocks as the automatic 16-row launch does: the same bits)
     if (fmt == FMT_Q4_K)
@@ -449,9 +547,10 @@ SV_API int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, cons
     const int rows = (int)((M - t * TILE_M) < TILE_M ? (M - t * TILE_M) : TILE_M);
     void* ct = (char*)c + (size_t)t * TILE_M * N * esz;
     const void* wst = (const char*)ws + t * tb;
-    int rc = fmt == FMT_Q4_K
-                 ? dispatch_gemv<FMT_Q4_K>(quant, meta, wst, ct, rows, (int)N, (int)S, c_is_bf16, s)
-                 : dispatch_gemv<FMT_Q8_0>(quant, meta, wst, ct, rows, (int)N, (int)S, c_is_bf16, s);
+    int rc = by_format(fmt, [&](auto F) {
+      return dispatch_gemv<decltype(F)::value>(quant, meta, wst, ct, rows, (int)N, (int)S,
+                                               c_is_bf16, s);
+    });
     if (rc) return rc;
   }
   return SV_OK;
@@ -467,9 +566,10 @@ SV_API int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, c
     // one launch: the GEMV converts the bf16 activations itself (same operands as the
     // prepared path, so the same results); ws is not touched
     hipStream_t s = (hipStream_t)stream;
-    return fmt == FMT_Q4_K
-               ? dispatch_gemv<FMT_Q4_K, true>(quant, meta, a, c, (int)M, (int)N, (int)(K / 256), c_is_bf16, s)
-               : dispatch_gemv<FMT_Q8_0, true>(quant, meta, a, c, (int)M, (int)N, (int)(K / 256), c_is_bf16, s);
+    return by_format(fmt, [&](auto F) {
+      return dispatch_gemv<decltype(F)::value, true>(quant, meta, a, c, (int)M, (int)N,
+                                                     (int)(K / 256), c_is_bf16, s);
+    });
   }
   int rc = snowverify_gemm_kquant_prepare_a(a, M, K, ws, stream);
   if (rc) return rc;

@@ -21,6 +21,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int FMT_Q4_K = 4;
+constexpr int FMT_Q5_K = 5;
+constexpr int FMT_Q6_K = 6;
 constexpr int FMT_Q8_0 = 8;
 constexpr int QK = 256;          // weights per superblock
 constexpr int TILE_N = 16;       // columns per MFMA tile
@@ -232,14 +234,87 @@ __device__ __forceinline__ float byte_f(uint32_t w, int i) {
 // One 16-column x 256-weight tile. Returns the superblock's contribution in the C layout
 // (column lane & 15, rows 4*(lane >> 4) + i), still in units of the operand scaling.
 // xa: A operands of the 8 sub-blocks, sx0/sx1: negated sub-block sums (f32 MFMA A operand).
+// Q5_K: the fifth bit of sub-block j's weights, placed on the 16-bit lanes of q4_group's four
+// words (bytes (0, 2), (1, 3) of qa and of qb), at bit `at` (4: low nibbles, 8: high nibbles,
+// which q4_group leaves at 16 q).
+__device__ __forceinline__ void q5_bits(uint32_t qa, uint32_t qb, int j, int at, uint32_t (&e)[4]) {
+  e[0] = ((qa >> j) & 0x00010001u) << at;
+  e[1] = ((qa >> (8 + j)) & 0x00010001u) << at;
+  e[2] = ((qb >> j) & 0x00010001u) << at;
+  e[3] = ((qb >> (8 + j)) & 0x00010001u) << at;
+}
+
+__device__ __forceinline__ half8 or_half8(half8 v, const uint32_t (&e)[4]) {
+  u32x4 w = __builtin_bit_cast(u32x4, v);
+  w.x |= e[0];
+  w.y |= e[1];
+  w.z |= e[2];
+  w.w |= e[3];
+  return __builtin_bit_cast(half8, w);
+}
+
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// Q6_K: the exact fp16 values q - 32 of one 32-weight run in kperm slot order, from its ql
+// words (wa, wb: bytes l = 8 kq .. 8 kq + 7), the nibble shift (0 low, 4 high) and its qh words
+// (ha, hb) with the run's bit pair at hs.
+__device__ __forceinline__ half8 q6_run(uint32_t wa, uint32_t wb, uint32_t ha, uint32_t hb, int sh,
+                                        int hs, uint32_t M) {
+  const uint32_t w0 = and_or((wa >> sh) & 0x000f000fu, 0xffffffffu, ((ha >> hs) & 0x00030003u) << 4);
+  const uint32_t w1 = and_or((wa >> (8 + sh)) & 0x000f000fu, 0xffffffffu,
+                             ((ha >> (8 + hs)) & 0x00030003u) << 4);
+  const uint32_t w2 = and_or((wb >> sh) & 0x000f000fu, 0xffffffffu, ((hb >> hs) & 0x00030003u) << 4);
+  const uint32_t w3 = and_or((wb >> (8 + sh)) & 0x000f000fu, 0xffffffffu,
+                             ((hb >> (8 + hs)) & 0x00030003u) << 4);
+  // 0x6400 | q = 1024 + q exactly; minus 1056 gives q - 32 exactly
+  const half2v off = {(_Float16)1056.0f, (_Float16)1056.0f};
+  const half2v v0 = __builtin_bit_cast(half2v, w0 | M) - off;
+  const half2v v1 = __builtin_bit_cast(half2v, w1 | M) - off;
+  const half2v v2 = __builtin_bit_cast(half2v, w2 | M) - off;
+  const half2v v3 = __builtin_bit_cast(half2v, w3 | M) - off;
+  return as_half8(__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                  __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3));
+}
+
+__device__ __forceinline__ float sbyte_f(uint32_t w, int i) {
+  return (float)(int8_t)((w >> (8 * i)) & 0xffu);
+}
+
 template <int FMT>
-__device__ __forceinline__ floatx4 tile_superblock(const u32x4* qv, u32x4 meta, const half8* xa,
-                                                   float sx0, float sx1, int kq, uint32_t M) {
+__device__ __forceinline__ floatx4 tile_superblock(const u32x4* qv, u32x4 meta, uint32_t dq,
+                                                   const half8* xa, float sx0, float sx1, int kq,
+                                                   uint32_t M) {
   const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
   floatx4 acc = zero;
   float a[8];
   float beta_lo, beta_hi;  // beta for sub-blocks kq and kq + 4
-  if constexpr (FMT == FMT_Q4_K) {
+  if constexpr (FMT == FMT_Q6_K) {
+    // w = d sc_g (q - 32) with a scale per 16 weights: each 32-weight run is multiplied twice,
+    // once with the B lanes of its first 16 weights (kq < 2) and once with the rest, each
+    // product scaled by its own sc; q - 32 is exact in fp16, so no offset term is needed
+    const float d = f16_to_f32((uint16_t)((threadIdx.x & 1) ? (dq >> 16) : (dq & 0xffff)));
+    const uint32_t keep_lo = kq < 2 ? 0xffffffffu : 0u, keep_hi = ~keep_lo;
+    const uint32_t sw[4] = {meta.x, meta.y, meta.z, meta.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int n = j >> 2, p = j & 3;
+      const u32x4 ql = qv[n];
+      const uint32_t wa = (p & 1) ? ql.z : ql.x, wb = (p & 1) ? ql.w : ql.y;
+      const uint32_t ha = n ? qv[2].z : qv[2].x, hb = n ? qv[2].w : qv[2].y;
+      const half8 b = q6_run(wa, wb, ha, hb, (p >> 1) * 4, 2 * p, M);
+      const u32x4 bw = __builtin_bit_cast(u32x4, b);
+      const half8 b_lo = __builtin_bit_cast(half8, bw & keep_lo);
+      const half8 b_hi = __builtin_bit_cast(half8, bw & keep_hi);
+      const int si = 8 * n + 2 * p;  // scales of weights l < 16 and l >= 16
+      const float s_lo = d * sbyte_f(sw[si >> 2], si & 3);
+      const float s_hi = d * sbyte_f(sw[(si + 1) >> 2], (si + 1) & 3);
+      floatx4 c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], b_lo, zero, 0, 0, 0);
+      acc += s_lo * c;
+      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[j], b_hi, zero, 0, 0, 0);
+      acc += s_hi * c;
+    }
+    return acc;
+  } else if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q5_K) {
     const float d = f16_to_f32((uint16_t)(meta.x & 0xffff));
     const float dmin = f16_to_f32((uint16_t)(meta.x >> 16));
     const uint32_t s0 = meta.y, s1 = meta.z, s2 = meta.w;
@@ -261,22 +336,36 @@ __device__ __forceinline__ floatx4 tile_superblock(const u32x4* qv, u32x4 meta, 
     const u32x4 q0 = qv[0], q1 = qv[1];
     half8 lo, hi;
     floatx4 c;
+    // Q5_K: OR the fifth bits into the nibble lanes (bit 4 of 1024 + q, bit 8 of 1024 + 16 q)
+    auto fifth = [&](int j, half8& l, half8& h) {
+      if constexpr (FMT == FMT_Q5_K) {
+        uint32_t e[4];
+        q5_bits(qv[2].x, qv[2].y, j, 4, e);
+        l = or_half8(l, e);
+        q5_bits(qv[2].x, qv[2].y, j + 1, 8, e);
+        h = or_half8(h, e);
+      }
+    };
     q4_group(q0.x, q0.y, M, lo, hi);
+    fifth(0, lo, hi);
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0], lo, zero, 0, 0, 0);
     acc += a[0] * c;
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1], hi, zero, 0, 0, 0);
     acc += (a[1] * 0.0625f) * c;
     q4_group(q0.z, q0.w, M, lo, hi);
+    fifth(2, lo, hi);
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[2], lo, zero, 0, 0, 0);
     acc += a[2] * c;
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[3], hi, zero, 0, 0, 0);
     acc += (a[3] * 0.0625f) * c;
     q4_group(q1.x, q1.y, M, lo, hi);
+    fifth(4, lo, hi);
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[4], lo, zero, 0, 0, 0);
     acc += a[4] * c;
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[5], hi, zero, 0, 0, 0);
     acc += (a[5] * 0.0625f) * c;
     q4_group(q1.z, q1.w, M, lo, hi);
+    fifth(6, lo, hi);
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[6], lo, zero, 0, 0, 0);
     acc += a[6] * c;
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[7], hi, zero, 0, 0, 0);
@@ -307,9 +396,21 @@ __device__ __forceinline__ floatx4 tile_superblock(const u32x4* qv, u32x4 meta, 
   return acc;
 }
 
+// Repacked weight layout per 16-column tile and superblock ("tile-superblock", ts):
+//   Q4_K  quant 2 KiB: [half][lane][16 B] nibbles (bytes 0-7 of group 2 half + 8 kq.., 8-15
+//         of group 2 half + 1); meta [col][16 B] = d, dmin, 12 scale bytes.
+//   Q5_K  quant 2.5 KiB: the Q4_K nibbles, then [lane][8 B] = qh[8 kq ..]; meta as Q4_K.
+//   Q6_K  quant 3 KiB: [3][lane][16 B]: ql of half 0 (bytes 0-7: ql[8 kq ..], 8-15:
+//         ql[32 + 8 kq ..]), ql of half 1 (+64), qh (bytes 0-7: qh[8 kq ..], 8-15:
+//         qh[32 + 8 kq ..]); meta [col][16 B] = the 16 int8 scales, then after all
+//         tile-superblocks' scales one fp16 d per (ts, col).
+//   Q8_0  quant 4 KiB: [4][lane][16 B] int8; meta [col][16 B] = the 8 fp16 scales.
 template <int FMT>
 struct QLayout {
-  static constexpr int kQuantVecs = FMT == FMT_Q4_K ? 2 : 4;  // u32x4 per lane per superblock
+  // u32x4 per lane per superblock (Q5_K's third holds the 8 qh bytes in .x, .y)
+  static constexpr int kQuantVecs = FMT == FMT_Q4_K ? 2 : FMT == FMT_Q8_0 ? 4 : 3;
+  static constexpr int kTsBytes = FMT == FMT_Q4_K ? 2048 : FMT == FMT_Q5_K ? 2560
+                                  : FMT == FMT_Q6_K ? 3072 : 4096;  // quant bytes per ts
 };
 
 // Per-wave operands of one superblock for NTILE column tiles.
@@ -320,6 +421,7 @@ struct SbOperands {
   floatx4 scale;  // 2^e of rows 4*(lane>>4) + 0..3
   u32x4 q[NTILE][QLayout<FMT>::kQuantVecs];
   u32x4 m[NTILE];
+  uint32_t dq[NTILE];  // Q6_K: the word holding this lane's column d (fp16)
 };
 
 __device__ __forceinline__ u32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -328,11 +430,20 @@ __device__ __forceinline__ u32x4 bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff,
 __device__ __forceinline__ float bload1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
+__device__ __forceinline__ uint32_t bload1u(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2 bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
 
 // Buffer resources and per-lane byte offsets of the streams one wave reads.
 struct GemvStreams {
   __amdgpu_buffer_rsrc_t quant, meta, xop, sxop, scale;
+  __amdgpu_buffer_rsrc_t dmeta;  // Q6_K: the fp16 d per (tile-superblock, column)
   uint32_t v_quant, v_meta, v_xop, v_sx, v_scale;  // per-lane byte offsets
+  uint32_t v_dq;  // Q6_K: this lane's column's d word
   uint32_t v_scale_g[4];  // row-gathered streams: offsets of the scales of rows 4*kq + i
 };
 
@@ -359,12 +470,31 @@ __device__ __forceinline__ void load_sb_w(u32x4 (&q)[NTILE][QLayout<FMT>::kQuant
                                           u32x4 (&m)[NTILE], const GemvStreams& st, int s, int S,
                                           int tile0, int tstride) {
   constexpr int QV = QLayout<FMT>::kQuantVecs;
+  constexpr uint32_t TB = QLayout<FMT>::kTsBytes;
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) {
     const uint32_t ts = (uint32_t)((tile0 + t * tstride) * S + s);
+    if constexpr (FMT == FMT_Q5_K) {
+      q[t][0] = bload4(st.quant, st.v_quant, ts * TB);
+      q[t][1] = bload4(st.quant, st.v_quant, ts * TB + 1024);
+      const u32x2 h = bload2(st.quant, st.v_quant >> 1, ts * TB + 2048);
+      q[t][2] = u32x4{h.x, h.y, 0u, 0u};
+    } else {
 #pragma unroll
-    for (int i = 0; i < QV; ++i) q[t][i] = bload4(st.quant, st.v_quant, (ts * QV + i) * 64 * 16);
+      for (int i = 0; i < QV; ++i) q[t][i] = bload4(st.quant, st.v_quant, ts * TB + i * 1024);
+    }
     m[t] = bload4(st.meta, st.v_meta, ts * 16 * 16);
+  }
+}
+
+// Q6_K: the word holding the fp16 d of this lane's column, for tiles tile0 + t * tstride.
+template <int NTILE>
+__device__ __forceinline__ void load_sb_d(uint32_t (&dq)[NTILE], const GemvStreams& st, int s,
+                                          int S, int tile0, int tstride) {
+#pragma unroll
+  for (int t = 0; t < NTILE; ++t) {
+    const uint32_t ts = (uint32_t)((tile0 + t * tstride) * S + s);
+    dq[t] = bload1u(st.dmeta, st.v_dq, ts * 16 * 2);
   }
 }
 
@@ -375,6 +505,7 @@ __device__ __forceinline__ void load_sb(SbOperands<FMT, NTILE>& o, const GemvStr
                                         int S, int tile0, int tstride = 1) {
   if constexpr (WITH_X) load_sb_x<FMT, NTILE, GATHER>(o, st, s);
   load_sb_w<FMT, NTILE>(o.q, o.m, st, s, S, tile0, tstride);
+  if constexpr (FMT == FMT_Q6_K) load_sb_d<NTILE>(o.dq, st, s, S, tile0, tstride);
 }
 
 // Multiply one superblock's operands into acc.
@@ -386,7 +517,7 @@ __device__ __forceinline__ void gemv_superblock(const SbOperands<FMT, NTILE>& o,
   for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, o.x[j]);
 #pragma unroll
   for (int t = 0; t < NTILE; ++t) {
-    floatx4 sb = tile_superblock<FMT>(o.q[t], o.m[t], xa, o.sx0, o.sx1, kq, Mv);
+    floatx4 sb = tile_superblock<FMT>(o.q[t], o.m[t], o.dq[t], xa, o.sx0, o.sx1, kq, Mv);
     acc[t] += sb * o.scale;
   }
 }
@@ -405,7 +536,7 @@ __device__ __forceinline__ GemvStreams make_streams(const void* quant, const voi
   GemvStreams st;
   // byte ranges in 64 bits, clamped to what one buffer resource holds (the entry points refuse
   // weights whose offsets would not fit 32 bits)
-  const int64_t qn = (int64_t)tiles * S * QV * 64 * 16, mn = (int64_t)tiles * S * 16 * 16;
+  const int64_t qn = (int64_t)tiles * S * QLayout<FMT>::kTsBytes, mn = (int64_t)tiles * S * 16 * 16;
   st.quant = __builtin_amdgcn_make_buffer_rsrc((void*)quant, 0,
                                                (int)(uint32_t)(qn < 0xFFFFFFFFll ? qn : 0xFFFFFFFFll),
                                                0x00020000);
@@ -415,6 +546,11 @@ __device__ __forceinline__ GemvStreams make_streams(const void* quant, const voi
   st.xop = __builtin_amdgcn_make_buffer_rsrc((void*)xv.xop, 0, S * 8 * 64 * 16, 0x00020000);
   st.sxop = __builtin_amdgcn_make_buffer_rsrc((void*)xv.sxop, 0, S * 2 * 64 * 4, 0x00020000);
   st.scale = __builtin_amdgcn_make_buffer_rsrc((void*)xv.scale, 0, S * 16 * 4, 0x00020000);
+  // Q6_K: the d values follow the scales (one fp16 per (tile-superblock, column))
+  st.dmeta = __builtin_amdgcn_make_buffer_rsrc((char*)meta + mn, 0,
+                                               (int)(uint32_t)(mn / 8 < 0xFFFFFFFFll ? mn / 8 : 0xFFFFFFFFll),
+                                               0x00020000);
+  st.v_dq = (uint32_t)((r & ~1) * 2);
   st.v_quant = lane * 16;
   st.v_meta = r * 16;
   st.v_xop = r < rows ? lane * 16 : 0x80000000u;
@@ -428,7 +564,7 @@ __device__ __forceinline__ GemvStreams make_streams(const void* quant, const voi
 // folding while remaining an ordinary instruction for the compiler's hazard tracking.
 template <int FMT>
 __device__ __forceinline__ uint32_t decode_magic() {
-  constexpr int M = FMT == FMT_Q4_K ? 0x64006400 : 0x64646464;
+  constexpr int M = FMT == FMT_Q8_0 ? 0x64646464 : 0x64006400;
   return (uint32_t)__builtin_amdgcn_update_dpp(0, M, 0xE4, 0xF, 0xF, false);
 }
 

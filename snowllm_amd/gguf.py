@@ -57,8 +57,8 @@ class Quant:
 
 
 # The ggml type ids with their block geometry (values fixed by the GGUF format). The verify
-# path computes on Q4_K and Q8_0 weights and F32/F16/BF16 norms, embeddings and heads; the
-# other entries let a checkpoint that also holds them be opened.
+# path computes on Q4_K, Q5_K, Q6_K and Q8_0 weights and F32/F16/BF16 norms, embeddings and
+# heads; the other entries let a checkpoint that also holds them be opened.
 _QUANTS = [
     ("F32", 0, 1, 4, torch.float32), ("F16", 1, 1, 2, torch.float16),
     ("BF16", 30, 1, 2, torch.bfloat16), ("F64", 28, 1, 8, torch.float64),
@@ -72,7 +72,7 @@ _QUANTS = [
 QUANTS = {name: Quant(name, tid, blk, size, dt) for name, tid, blk, size, dt in _QUANTS}
 _BY_ID = {q.type_id: q for q in QUANTS.values()}
 # this library's k-quant format ids (the reference's snowllm/ops/moe.py:189-190)
-KQUANT_FORMAT = {"Q4_K": 4, "Q8_0": 8}
+KQUANT_FORMAT = {"Q4_K": 4, "Q5_K": 5, "Q6_K": 6, "Q8_0": 8}
 
 
 @dataclasses.dataclass

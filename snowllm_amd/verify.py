@@ -26,7 +26,7 @@ from . import layers as Lops
 from . import ops
 from ._capi import SnowLLMError
 
-Q4_K, Q8_0 = 4, 8
+Q4_K, Q5_K, Q6_K, Q8_0 = 4, 5, 6, 8
 HEAD_KQUANT = -1   # VerifyModel.head_wt for a Q4_K / Q8_0 head (lm_head = (quant, meta))
 # rows of one verify step over all its requests (SPEC_MAX_STEP_ROWS, snowllm/defaults.py:9)
 MAX_STEP_ROWS = 256
@@ -142,6 +142,32 @@ def gguf_random(fmt, n, k, seed, device="cuda", centered=False):
         mid = (mn[:, :4] & 63) | ((mn[:, 4:] >> 4) << 6)
         hi = (sc[:, 4:] & 15) | ((mn[:, 4:] & 15) << 4)
         raw[:, 4:16] = torch.cat([lo, mid, hi], 1).to(torch.uint8)
+        return raw.view(-1)
+    if fmt == Q5_K:
+        # Q4_K's form with a fifth bit (qh uniform); centered: dmin = 16 d, m_j = round(0.96875
+        # sc_j), so that w ~ d sc_j (q - 15.5)
+        nb = n * k // 256
+        raw = torch.randint(0, 256, (nb, 176), dtype=torch.uint8, device=device, generator=g)
+        dstd = 8e-5 if centered else 1e-3
+        d = (torch.randn(nb, device=device, generator=g) * dstd).abs()
+        dd = torch.stack([d, 16 * d if centered else d], 1).half()
+        raw[:, 0:4] = dd.view(torch.uint8).view(nb, 4)
+        if centered:
+            sc = torch.randint(0, 64, (nb, 8), dtype=torch.int32, device=device, generator=g)
+            mn = torch.round(sc.float() * 0.96875).int().clamp_(0, 63)
+            lo = (sc[:, :4] & 63) | ((sc[:, 4:] >> 4) << 6)
+            mid = (mn[:, :4] & 63) | ((mn[:, 4:] >> 4) << 6)
+            hi = (sc[:, 4:] & 15) | ((mn[:, 4:] & 15) << 4)
+            raw[:, 4:16] = torch.cat([lo, mid, hi], 1).to(torch.uint8)
+        return raw.view(-1)
+    if fmt == Q6_K:
+        # ql/qh uniform, int8 scales uniform in -64..64, d = fp16(|N(0, s^2)|): w = d sc (q - 32)
+        nb = n * k // 256
+        raw = torch.randint(0, 256, (nb, 210), dtype=torch.uint8, device=device, generator=g)
+        sc = torch.randint(-64, 65, (nb, 16), dtype=torch.int8, device=device, generator=g)
+        raw[:, 192:208] = sc.view(torch.uint8)
+        d = (torch.randn(nb, device=device, generator=g) * (3.5e-5 if centered else 1e-4)).abs()
+        raw[:, 208:210] = d.half().view(torch.uint8).view(nb, 2)
         return raw.view(-1)
     if fmt == Q8_0:
         nb = n * k // 32

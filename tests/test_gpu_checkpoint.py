@@ -43,6 +43,9 @@ CASES = [
     ("moe", {}, 1),
     ("moe", {"attn_fmt": 8}, 3),
     ("dense", {"attn_fmt": 8}, 1),
+    # the other k-quants of a Q4_K_M / UD-Q4_K_XL file
+    ("moe", {"attn_fmt": 6}, 1),
+    ("dense", {"attn_fmt": 5, "ffn_fmt": 6}, 2),
 ]
 
 
@@ -159,3 +162,31 @@ def test_gather_embedding_q4_k_equals_dequant(gpu):
         blk = raw.reshape(V, -1)[rows.numpy()].reshape(-1)
         want = torch.from_numpy(Q.dequant_q4_k(blk, len(ids), H)).bfloat16()
         assert torch.equal(out.cpu(), want)
+
+
+@pytest.mark.parametrize("head_q", ["Q6_K", "Q5_K"])
+def test_q6k_q5k_head(gpu, tmp_path, default_geometry, head_q):
+    """A Q6_K (Q4_K_M's usual output.weight) or Q5_K head read from the checkpoint: the logits
+    against the oracle's decode of the same blocks."""
+    from snowllm_amd.checkpoint import load_gguf, model_tensors, save_gguf
+    from snowllm_amd.verify import HEAD_KQUANT, VerifyModel, gguf_random
+    fmt = {"Q5_K": 5, "Q6_K": 6}[head_q]
+    cfg = tiny("dense")
+    _say(f"checkpoint with a {head_q} head")
+    m = VerifyModel(cfg, seed=5, keep_raw=True)
+    V, H = cfg.vocab, cfg.hidden
+    head = gguf_random(fmt, V, H, seed=23).cpu()
+    tensors = [t for t in model_tensors(m) if t[0] != "output.weight"]
+    tensors += [("output.weight", (V, H), head_q, head)]
+    lm = load_gguf(save_gguf(tmp_path / "h.gguf", cfg, tensors), context=cfg.context,
+                   block=cfg.block, seed=5)
+    assert lm.head_wt == HEAD_KQUANT and lm.head_fmt == fmt
+    lm.set_block(torch.arange(cfg.block) * 11)
+    logits = lm.forward().clone()
+    torch.cuda.synchronize()
+    ref = RM.head_reference(lm.x.float().cpu(), lm.layer_residual.float().cpu(),
+                            lm.final_norm.cpu(), torch.from_numpy(Q.dequant(head.numpy(), fmt, V, H)),
+                            cfg.eps)
+    e = rel(logits.cpu(), ref)
+    _say(f"  {head_q} head logits rel L2 {e:.2e}")
+    assert e < 1e-3

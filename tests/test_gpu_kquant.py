@@ -21,12 +21,12 @@ def _run(fmt, raw, x, n, k, out_dtype=torch.float32):
     return c.float().cpu().numpy(), (quant, meta, ws)
 
 
-@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("fmt", [4, 5, 6, 8])
 @pytest.mark.parametrize("m", [1, 9, 16, 17])
 @pytest.mark.parametrize("n,k", [(384, 1024), (5120, 2048), (2048, 4096)])
 def test_gemv_matches_oracle(gpu, fmt, m, n, k):
     print(f"gemv fmt={fmt} M={m} N={n} K={k}", flush=True)
-    raw = Q.make_q4_k(n, k, seed=n + k) if fmt == 4 else Q.make_q8_0(n, k, seed=n + k)
+    raw = Q.make(fmt, n, k, seed=n + k)
     x = Q.make_activations(m, k, seed=m)
     got, _ = _run(fmt, raw, x, n, k)
     want = Q.gemv_reference(x, Q.dequant(raw, fmt, n, k))
@@ -144,3 +144,36 @@ def test_wide_block_gemv_equals_row_tiles(gpu, fmt, n, k):
         torch.cuda.synchronize()
         assert torch.equal(c, tiles), m
         assert Q.rel_l2(c.cpu().numpy(), Q.gemv_reference(x, w)) < TOL
+
+
+@pytest.mark.parametrize("fmt", [5, 6])
+def test_q5k_q6k_config2_shape_and_forms(gpu, fmt):
+    """Q5_K / Q6_K (the other k-quants of Q4_K_M checkpoints, snowllm/checkpoint/gguf/
+    source.py:263-272) at the config-2 shape: the one-launch form equals the prepared form bit
+    for bit, both within 1e-3 of the fp64 product of the oracle's decode; the repacked bytes
+    add up to the GGUF bytes; the tile shapes of the variant knob agree."""
+    from snowllm_amd import ops
+    n, k, m = 14336, 4096, 9
+    raw = Q.make(fmt, n, k, seed=fmt)
+    quant_b, meta_b, gguf_b = ops.kquant_bytes(fmt, n, k)
+    assert quant_b - 4 + meta_b == gguf_b == raw.size
+    x = Q.make_activations(m, k, seed=7)
+    got, (quant, meta, ws) = _run(fmt, raw, x, n, k)
+    want = Q.gemv_reference(x, Q.dequant(raw, fmt, n, k))
+    err = Q.rel_l2(got, want)
+    print(f"fmt {fmt} config-2 shape rel L2 {err:.2e}", flush=True)
+    assert err < TOL
+    c2 = torch.empty(m, n, device="cuda")
+    ops.gemm_kquant_prepare_a(x.cuda(), ws)
+    ops.gemm_kquant_a_prepared(fmt, quant, meta, c2, m, n, k, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(c2.cpu().numpy(), got)
+    from snowllm_amd import _capi
+    for v in (1, 2, 4, 5):
+        _capi.lib.snowverify_gemv_variant(v)
+        try:
+            ops.gemm_kquant_a_prepared(fmt, quant, meta, c2, m, n, k, ws)
+            torch.cuda.synchronize()
+        finally:
+            _capi.lib.snowverify_gemv_variant(0)
+        assert Q.rel_l2(c2.cpu().numpy(), want) < TOL, v

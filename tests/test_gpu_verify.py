@@ -27,6 +27,9 @@ def tiny(kind):
     if kind == "tree":
         return VerifyConfig("tiny_tree", experts=16, expert_ffn=256, topk=4, attn_fmt=8,
                             tree_parents=(-1, 0, 1, 0, 3), **dict(base, block=5))
+    if kind == "dense_q6k_q5k":   # Q6_K attention, Q5_K MLP (Q4_K_M's other k-quants)
+        return VerifyConfig("tiny_dense_k56", ffn=512, attn_fmt=6, ffn_fmt=5,
+                            **dict(base, kv_heads=1, rot_half=64))
     raise ValueError(kind)
 
 
@@ -35,7 +38,7 @@ def rel(a, b):
     return ((a - b).norm() / b.norm().clamp_min(1e-12)).item()
 
 
-@pytest.mark.parametrize("kind", ["dense", "moe", "tree"])
+@pytest.mark.parametrize("kind", ["dense", "moe", "tree", "dense_q6k_q5k"])
 def test_layers_and_head_match_cpu_reference(gpu, kind):
     from snowllm_amd.verify import VerifyModel, tree_masks, Acceptance
     cfg = tiny(kind)
