@@ -152,7 +152,8 @@ int snowverify_draft_select(const void* hp, const float* logits, const void* pre
                             int64_t b, int64_t ell, int64_t v, int64_t rank, void* stream);
 
 /* ---- GGUF k-quant GEMV ----------------------------------------------------------------- */
-/* Format ids as in the reference (snowllm/ops/moe.py:189-190): 4 = Q4_K, 8 = Q8_0. */
+/* Format ids as in the reference (snowllm/ops/moe.py:189-190, checkpoint/gguf/source.py:33):
+ * 4 = Q4_K, 5 = Q5_K, 6 = Q6_K, 8 = Q8_0. */
 
 /* Sizes of the GGUF blocks and of the packed (quant, meta) pair for an [N, K] weight
  * (snowllm/_capi.py:323-325; snowllm/ops/gemm.py:130-133). quant - 4 + meta == gguf.
@@ -168,6 +169,12 @@ int snowllm_kquant_supported(int fmt);
  * snowllm/ops/gemm.py:136-147). */
 int snowllm_gemm_kquant_shuffle_b(int fmt, const uint8_t* gguf, uint8_t* quant, uint8_t* meta,
                                   int64_t N, int64_t K, void* stream);
+/* Extension, no counterpart in the reference: repack two GGUF tensors of one format, `top`
+ * (rows 0 .. n_top - 1) and `bottom` (rows n_top .. N - 1), as one [N, K] matrix -- an expert's
+ * [gate; up] from its two stacks (snowllm_gemm_kquant_shuffle_b is the single-tensor case). */
+int snowverify_kquant_shuffle_split(int fmt, const uint8_t* top, const uint8_t* bottom,
+                                    int64_t n_top, uint8_t* quant, uint8_t* meta, int64_t N,
+                                    int64_t K, void* stream);
 
 /* Activation workspace bytes for gemm_kquant_a (snowllm/_capi.py:620). */
 int64_t snowllm_gemm_kquant_a_ws_bytes(int64_t M, int64_t K);

@@ -66,19 +66,23 @@ class LayerRef:
         self.post_norm = lw.post_norm.cpu().float()
         self.q_norm = lw.q_norm.cpu().float()
         self.k_norm = lw.k_norm.cpu().float()
-        self.qkv = dequant_raw(lw.qkv[2], c.attn_fmt, c.qkv_n, H)
-        self.o = dequant_raw(lw.o[2], c.attn_fmt, H, c.heads * c.head_dim)
+        # a layer's own formats where they differ from the config's (0 or absent: the config's)
+        own = lambda obj, name: getattr(obj, name, 0) or 0  # noqa: E731
+        self.qkv = dequant_raw(lw.qkv[2], own(lw, "qkv_fmt") or c.attn_fmt, c.qkv_n, H)
+        self.o = dequant_raw(lw.o[2], own(lw, "o_fmt") or c.attn_fmt, H, c.heads * c.head_dim)
+        self.gu_fmt = own(lw, "gu_fmt") or c.ffn_fmt
+        self.dn_fmt = own(lw, "dn_fmt") or own(c, "down_fmt") or c.ffn_fmt
         if c.moe:
             F = c.expert_ffn
             self.router = lw.raw["router"].cpu().float()
             self._gu_raw = lw.gu[2].cpu()
             self._dn_raw = lw.dn[2].cpu()
             self._experts = {}
-            self.sh_gu = dequant_raw(lw.sh_gu[2], c.ffn_fmt, 2 * F, H)
-            self.sh_dn = dequant_raw(lw.sh_dn[2], c.ffn_fmt, H, F)
+            self.sh_gu = dequant_raw(lw.sh_gu[2], self.gu_fmt, 2 * F, H)
+            self.sh_dn = dequant_raw(lw.sh_dn[2], self.dn_fmt, H, F)
         else:
-            self.gu = dequant_raw(lw.gu[2], c.ffn_fmt, 2 * c.ffn, H)
-            self.dn = dequant_raw(lw.dn[2], c.ffn_fmt, H, c.ffn)
+            self.gu = dequant_raw(lw.gu[2], self.gu_fmt, 2 * c.ffn, H)
+            self.dn = dequant_raw(lw.dn[2], self.dn_fmt, H, c.ffn)
 
     def expert(self, e):
         """(gate_up [2F, H], down [H, F]) of routed expert e."""
@@ -87,8 +91,8 @@ class LayerRef:
             H, F = c.hidden, c.expert_ffn
             gb = self._gu_raw.numel() // c.experts
             db = self._dn_raw.numel() // c.experts
-            gu = dequant_raw(self._gu_raw[e * gb:(e + 1) * gb], c.ffn_fmt, 2 * F, H)
-            dn = dequant_raw(self._dn_raw[e * db:(e + 1) * db], c.ffn_fmt, H, F)
+            gu = dequant_raw(self._gu_raw[e * gb:(e + 1) * gb], self.gu_fmt, 2 * F, H)
+            dn = dequant_raw(self._dn_raw[e * db:(e + 1) * db], self.dn_fmt, H, F)
             self._experts[e] = (gu, dn)
         return self._experts[e]
 

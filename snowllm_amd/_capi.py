@@ -89,6 +89,7 @@ _SIGS = [
     ("snowllm_kquant_meta_bytes", c_int64, [c_int, c_int64, c_int64]),
     ("snowllm_kquant_supported", c_int, [c_int]),
     ("snowllm_gemm_kquant_shuffle_b", c_int, [c_int, P, P, P, c_int64, c_int64, S]),
+    ("snowverify_kquant_shuffle_split", c_int, [c_int, P, P, c_int64, P, P, c_int64, c_int64, S]),
     ("snowllm_gemm_kquant_a_ws_bytes", c_int64, [c_int64, c_int64]),
     ("snowllm_gemm_kquant_a", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
     ("snowverify_gemm_kquant_prepare_a", c_int, [P, c_int64, c_int64, P, S]),

@@ -19,7 +19,9 @@ Scope: every layer must be full GQA attention with QK-norm and no output gate, f
 SwiGLU MLP or a routed MoE with a shared expert whose width equals the experts'; attention and
 dense matrices in Q4_K, Q5_K, Q6_K or Q8_0 (the formats the reference's GEMM takes, snowllm/
 checkpoint/gguf/source.py:263-272), with q/k/v in one format, gate/up in one and down in any;
-the experts and the shared expert all Q4_K.
+the experts' gate/up in Q4_K, Q5_K or Q6_K and their down in the same format or a wider one
+(Q4_K_M files store some layers' ffn_down_exps as Q6_K), the shared expert in the routed
+experts' formats. Formats may change from layer to layer.
 Anything else raises SnowLLMError naming the tensor; nothing falls back to another path.
 """
 import torch
@@ -42,6 +44,12 @@ def config_from_gguf(g: GGUF, *, context: int, block: int, tree_parents=(),
                      name: str = None) -> VerifyConfig:
     """The VerifyConfig of a checkpoint (names.py:37-100), checked against what this build
     computes."""
+    if g.arch not in ARCHITECTURES:
+        raise SnowLLMError(f"{g.path.name} is a {g.arch!r} checkpoint; this build's verify step "
+                           f"reads {' and '.join(map(repr, ARCHITECTURES))} checkpoints")
+    if (g.arch == "qwen35moe") != bool(_int(g, "{arch}.expert_count", 0)):
+        raise SnowLLMError(f"{g.path.name}: a {g.arch!r} checkpoint "
+                           f"{'without' if g.arch == 'qwen35moe' else 'with'} experts")
     nextn = _int(g, "{arch}.nextn_predict_layers", 0) or 0
     layers = int(g.need("{arch}.block_count")) - nextn
     interval = _int(g, "{arch}.full_attention_interval", 1)
@@ -68,10 +76,7 @@ def config_from_gguf(g: GGUF, *, context: int, block: int, tree_parents=(),
         if shared != F:
             raise SnowLLMError(f"{g.path.name}: shared expert width {shared} differs from the "
                                f"experts' {F}; this build runs both in one launch of width F")
-        fmt = _kfmt(g, "blk.0.ffn_gate_exps.weight")
-        if fmt != KQUANT_FORMAT["Q4_K"]:
-            raise SnowLLMError(f"{g.path.name}: the experts are {g['blk.0.ffn_gate_exps.weight'].quant.name};"
-                               f" this build's MoE kernels compute Q4_K experts")
+        fmt = _expert_fmt(g, "blk.0.ffn_gate_exps.weight")
         fields.update(experts=experts, expert_ffn=F,
                       topk=int(g.need("{arch}.expert_used_count")), ffn_fmt=fmt)
     else:
@@ -79,6 +84,20 @@ def config_from_gguf(g: GGUF, *, context: int, block: int, tree_parents=(),
                       ffn_fmt=_kfmt(g, "blk.0.ffn_gate.weight"))
     fields["attn_fmt"] = _kfmt(g, "blk.0.attn_q.weight")
     return VerifyConfig(name or f"gguf:{g.path.name}", **fields)
+
+
+# the reference's architecture names (snowllm/checkpoint/gguf/names.py:16-17): MoE, dense
+ARCHITECTURES = ("qwen35moe", "qwen35")
+# expert formats the MoE kernels compute: gate/up in one of these, down in the same or a wider
+EXPERT_FORMATS = (KQUANT_FORMAT["Q4_K"], KQUANT_FORMAT["Q5_K"], KQUANT_FORMAT["Q6_K"])
+
+
+def _expert_fmt(g: GGUF, name: str) -> int:
+    fmt = _kfmt(g, name)
+    if fmt not in EXPERT_FORMATS:
+        raise SnowLLMError(f"{g.path.name}: {name} is {g[name].quant.name}; this build's MoE "
+                           f"kernels compute Q4_K, Q5_K and Q6_K experts")
+    return fmt
 
 
 def _kfmt(g: GGUF, name: str) -> int:
@@ -144,6 +163,13 @@ def _layer(g: GGUF, cfg: VerifyConfig, i: int) -> LayerWeights:
     for n in ("attn_q_norm.weight", "attn_k_norm.weight"):
         if p + n not in g:
             raise SnowLLMError(f"{g.path.name}: no {p + n}; this build applies QK-norm")
+    if cfg.moe:   # checked before any tensor is read
+        gu_fmt = _expert_fmt(g, p + "ffn_gate_exps.weight")
+        dn_fmt = _expert_fmt(g, p + "ffn_down_exps.weight")
+        if dn_fmt < gu_fmt:
+            raise SnowLLMError(f"{g.path.name}: {p}ffn_down_exps.weight is narrower than the "
+                               f"experts' gate/up; the MoE kernels take down in the gate/up "
+                               f"format or a wider one")
     raw, qkv_fmt = _blocks(g, [p + n for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight")])
     qkv = ops.gemm_kquant_shuffle_b(qkv_fmt, raw, cfg.qkv_n, H)
     raw, o_fmt = _blocks(g, [p + "attn_output.weight"])
@@ -162,23 +188,24 @@ def _layer(g: GGUF, cfg: VerifyConfig, i: int) -> LayerWeights:
         router = torch.cat([_bf16(g, p + "ffn_gate_inp.weight"),
                             _bf16(g, p + "ffn_gate_inp_shexp.weight").reshape(1, H)])
         lw.router = ops.moe_shuffle_router(router)
-        fmt = cfg.ffn_fmt
         for n, shape in (("ffn_gate_exps", (E, F, H)), ("ffn_up_exps", (E, F, H)),
                          ("ffn_down_exps", (E, H, F)), ("ffn_gate_shexp", (F, H)),
                          ("ffn_up_shexp", (F, H)), ("ffn_down_shexp", (H, F))):
             _shape(g, p + n + ".weight", *shape)
-        gate, _ = _blocks(g, [p + "ffn_gate_exps.weight"], fmt)
-        up, _ = _blocks(g, [p + "ffn_up_exps.weight"], fmt)
-        gu = ops.moe_kquant_shuffle_gate_up(gate, up, fmt, E)
+        gate, _ = _blocks(g, [p + "ffn_gate_exps.weight"], gu_fmt)
+        up, _ = _blocks(g, [p + "ffn_up_exps.weight"], gu_fmt)
+        gu = ops.moe_kquant_shuffle_gate_up(gate, up, gu_fmt, E)
         del gate, up
-        down, _ = _blocks(g, [p + "ffn_down_exps.weight"], fmt)
-        dn = ops.moe_kquant_shuffle_down(down, fmt, E)
+        down, _ = _blocks(g, [p + "ffn_down_exps.weight"], dn_fmt)
+        dn = ops.moe_kquant_shuffle_down(down, dn_fmt, E)
         del down
-        sg, _ = _blocks(g, [p + "ffn_gate_shexp.weight"], fmt)
-        su, _ = _blocks(g, [p + "ffn_up_shexp.weight"], fmt)
-        sd, _ = _blocks(g, [p + "ffn_down_shexp.weight"], fmt)
-        sh_gu = ops.moe_kquant_shuffle_gate_up(sg, su, fmt, 1)
-        sh_dn = ops.moe_kquant_shuffle_down(sd, fmt, 1)
+        # one launch computes the routed and shared experts: the same formats for both
+        sg, _ = _blocks(g, [p + "ffn_gate_shexp.weight"], gu_fmt)
+        su, _ = _blocks(g, [p + "ffn_up_shexp.weight"], gu_fmt)
+        sd, _ = _blocks(g, [p + "ffn_down_shexp.weight"], dn_fmt)
+        sh_gu = ops.moe_kquant_shuffle_gate_up(sg, su, gu_fmt, 1)
+        sh_dn = ops.moe_kquant_shuffle_down(sd, dn_fmt, 1)
+        lw.gu_fmt, lw.dn_fmt = gu_fmt, dn_fmt
         lw.gu, lw.dn = (gu.p0, gu.p1, None), (dn.p0, dn.p1, None)
         lw.sh_gu, lw.sh_dn = (sh_gu.p0, sh_gu.p1, None), (sh_dn.p0, sh_dn.p1, None)
     else:
@@ -186,8 +213,9 @@ def _layer(g: GGUF, cfg: VerifyConfig, i: int) -> LayerWeights:
         _shape(g, p + "ffn_gate.weight", F, H)
         _shape(g, p + "ffn_up.weight", F, H)
         _shape(g, p + "ffn_down.weight", H, F)
-        raw, _ = _blocks(g, [p + "ffn_gate.weight", p + "ffn_up.weight"], cfg.ffn_fmt)
-        lw.gu = (*ops.gemm_kquant_shuffle_b(cfg.ffn_fmt, raw, 2 * F, H), None)
+        raw, gu_fmt = _blocks(g, [p + "ffn_gate.weight", p + "ffn_up.weight"])
+        lw.gu = (*ops.gemm_kquant_shuffle_b(gu_fmt, raw, 2 * F, H), None)
+        lw.gu_fmt = gu_fmt
         raw, dn_fmt = _blocks(g, [p + "ffn_down.weight"])
         lw.dn = (*ops.gemm_kquant_shuffle_b(dn_fmt, raw, H, F), None)
         lw.dn_fmt = dn_fmt
@@ -249,26 +277,28 @@ def model_tensors(model: VerifyModel, *, tied: bool = False):
         for n, t in (("attn_norm", lw.in_norm), ("post_attention_norm", lw.post_norm),
                      ("attn_q_norm", lw.q_norm), ("attn_k_norm", lw.k_norm)):
             out.append((p + n + ".weight", tuple(t.shape), "F32", f32(t)))
+        gu_fmt = lw.gu_fmt or cfg.ffn_fmt
+        dn_fmt = lw.dn_fmt or cfg.down_fmt or cfg.ffn_fmt
         if cfg.moe:
             E, F = cfg.experts, cfg.expert_ffn
             router = f32(lw.raw["router"])
             out += [(p + "ffn_gate_inp.weight", (E, H), "F32", router[:E]),
                     (p + "ffn_gate_inp_shexp.weight", (H,), "F32", router[E])]
-            gu, fa = rows(lw.gu[2], cfg.ffn_fmt, H)
+            gu, fa = rows(lw.gu[2], gu_fmt, H)
             gu = gu.view(E, 2, F, -1)
-            dn, _ = rows(lw.dn[2], cfg.ffn_fmt, F)
-            sgu, _ = rows(lw.sh_gu[2], cfg.ffn_fmt, H)
-            sdn, _ = rows(lw.sh_dn[2], cfg.ffn_fmt, F)
+            dn, da = rows(lw.dn[2], dn_fmt, F)
+            sgu, _ = rows(lw.sh_gu[2], gu_fmt, H)
+            sdn, _ = rows(lw.sh_dn[2], dn_fmt, F)
             out += [(p + "ffn_gate_exps.weight", (E, F, H), fa, gu[:, 0].contiguous()),
                     (p + "ffn_up_exps.weight", (E, F, H), fa, gu[:, 1].contiguous()),
-                    (p + "ffn_down_exps.weight", (E, H, F), fa, dn),
+                    (p + "ffn_down_exps.weight", (E, H, F), da, dn),
                     (p + "ffn_gate_shexp.weight", (F, H), fa, sgu[:F]),
                     (p + "ffn_up_shexp.weight", (F, H), fa, sgu[F:]),
-                    (p + "ffn_down_shexp.weight", (H, F), fa, sdn)]
+                    (p + "ffn_down_shexp.weight", (H, F), da, sdn)]
         else:
             F = cfg.ffn
-            gu, fa = rows(lw.gu[2], cfg.ffn_fmt, H)
-            dn, da = rows(lw.dn[2], lw.dn_fmt or cfg.ffn_fmt, F)
+            gu, fa = rows(lw.gu[2], gu_fmt, H)
+            dn, da = rows(lw.dn[2], dn_fmt, F)
             out += [(p + "ffn_gate.weight", (F, H), fa, gu[:F]),
                     (p + "ffn_up.weight", (F, H), fa, gu[F:]),
                     (p + "ffn_down.weight", (H, F), da, dn)]

@@ -12,6 +12,7 @@
 #include "kquant_core.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace {
 using namespace kq;
@@ -1038,8 +1039,9 @@ constexpr uint32_t MOE_WAIT_POLLS = 1u << 20;  // ~0.1 s: far beyond any gate/up
 
 // Three waves per SIMD when the down items take one superblock per wave (the gate/up items then
 // bound the registers at 168); two otherwise.
-template <int FMT, int GU_WS, int GU_PPB, int DN_NTILE, int DN_WS, int DN_GPB, bool ONE_SB>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB ? 3 : 2, ONE_SB ? 3 : 2))) moe_experts_kernel(
+template <int FMT, int DN_FMT, int GU_WS, int GU_PPB, int DN_NTILE, int DN_WS, int DN_GPB,
+          bool ONE_SB, int WAVES = (ONE_SB ? 3 : 2)>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) moe_experts_kernel(
     // first the arguments of the plan read and the gate/up weight addresses: the first 56
     // bytes arrive preloaded in SGPRs
     const MoePlan* __restrict__ plan, const uint8_t* __restrict__ gu_quant,
@@ -1097,7 +1099,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONE_SB
     __syncthreads();
     return __builtin_amdgcn_readfirstlane(timed_out) != 0u;
   };
-  moe_down_body<FMT, DN_NTILE, DN_WS, DN_GPB, true, ONE_SB>(
+  moe_down_body<DN_FMT, DN_NTILE, DN_WS, DN_GPB, true, ONE_SB>(
       didx, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
       plan, E, act, weights, shared_w, pairs, shared_out, H, F, wait);
 }
@@ -1334,6 +1336,16 @@ SV_API int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_
 // then holds about twice the waves of one per pair, so the few workgroups that do not fit the
 // first round over the CUs (more than 64 expert slots) finish in half the time (measured on
 // MI355X: 30.0 -> 27.2 us gate/up, 25.1 -> 21.5 us down at 65 slots; +0.7 us at 57).
+// Expert formats the MoE kernels take, and one packed expert matrix's bytes (the stacks hold
+// expert e at e * these).
+extern "C" int64_t snowllm_kquant_quant_bytes(int fmt, int64_t N, int64_t K);
+extern "C" int64_t snowllm_kquant_meta_bytes(int fmt, int64_t N, int64_t K);
+namespace {
+bool expert_fmt(int f) { return f == 4 || f == 5 || f == 6; }
+int64_t packed_quant(int f, int64_t N, int64_t K) { return snowllm_kquant_quant_bytes(f, N, K) - 4; }
+int64_t packed_meta(int f, int64_t N, int64_t K) { return snowllm_kquant_meta_bytes(f, N, K); }
+}  // namespace
+
 constexpr int MOE_GU_WS = 2, MOE_GU_PPB = 2;             // gate/up: waves per pair, pairs per block
 constexpr int MOE_DN_NTILE = 4, MOE_DN_WS = 2, MOE_DN_GPB = 2;  // down: tiles per group, waves
                                                                  // per group, groups per block
@@ -1344,17 +1356,21 @@ SV_API int snowverify_moe_gate_up(int fmt, const void* gu_quant, const void* gu_
                                   const void* plan, const void* ws, void* act, int64_t M,
                                   int64_t max_slots, int64_t E, int64_t H, int64_t F,
                                   void* stream) {
-  if (fmt != 4 || M <= 0 || M > 16 || max_slots <= 0 || max_slots > MOE_MAX_SLOTS || H % 256 ||
-      F % 256)
+  if (!expert_fmt(fmt) || M <= 0 || M > 16 || max_slots <= 0 || max_slots > MOE_MAX_SLOTS ||
+      H % 256 || F % 256)
     return SV_EINVAL;
-  const int64_t gu_q = 2 * F * H / 2, gu_m = 2 * F * (H / 256) * 16;
+  const int64_t gu_q = packed_quant(fmt, 2 * F, H), gu_m = packed_meta(fmt, 2 * F, H);
   const dim3 grid((unsigned)((F / 16 + MOE_GU_PPB - 1) / MOE_GU_PPB), (unsigned)max_slots);
-  hipLaunchKernelGGL((gate_up_kernel<4, MOE_GU_WS, MOE_GU_PPB>), grid,
-                     dim3(64 * MOE_GU_WS * MOE_GU_PPB), 0,
-                     Sx(stream), (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
-                     (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
-                     (const MoePlan*)plan, (int)E, ws, (uint16_t*)act, (int)M, (int)F,
-                     (int)(H / 256));
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(64 * MOE_GU_WS * MOE_GU_PPB), 0, Sx(stream),
+                       (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
+                       (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
+                       (const MoePlan*)plan, (int)E, ws, (uint16_t*)act, (int)M, (int)F,
+                       (int)(H / 256));
+  };
+  if (fmt == 4) go(gate_up_kernel<4, MOE_GU_WS, MOE_GU_PPB>);
+  else if (fmt == 5) go(gate_up_kernel<5, MOE_GU_WS, MOE_GU_PPB>);
+  else go(gate_up_kernel<6, MOE_GU_WS, MOE_GU_PPB>);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1366,9 +1382,9 @@ SV_API int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_met
                                const void* act, const float* weights, const float* shared_w,
                                float* pairs, float* shared_out, int64_t max_slots, int64_t E,
                                int64_t H, int64_t F, void* stream) {
-  if (fmt != 4 || max_slots <= 0 || max_slots > MOE_MAX_SLOTS || H % 256 || F % 256)
+  if (!expert_fmt(fmt) || max_slots <= 0 || max_slots > MOE_MAX_SLOTS || H % 256 || F % 256)
     return SV_EINVAL;
-  const int64_t dn_q = H * F / 2, dn_m = H * (F / 256) * 16;
+  const int64_t dn_q = packed_quant(fmt, H, F), dn_m = packed_meta(fmt, H, F);
   const int groups = (int)(H / 16 / MOE_DN_NTILE);
   const dim3 grid((unsigned)((groups + MOE_DN_GPB - 1) / MOE_DN_GPB), (unsigned)max_slots);
   auto launch = [&](auto kern) {
@@ -1378,10 +1394,14 @@ SV_API int snowverify_moe_down(int fmt, const void* dn_quant, const void* dn_met
                        (const MoePlan*)plan, (int)E, (const uint16_t*)act, weights, shared_w,
                        pairs, shared_out, (int)H, (int)F);
   };
-  if (F / QK == MOE_DN_WS)
-    launch(moe_down_kernel<4, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB, true>);
-  else
-    launch(moe_down_kernel<4, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB, false>);
+  auto by = [&](auto f) {
+    constexpr int D = decltype(f)::value;
+    if (F / QK == MOE_DN_WS) launch(moe_down_kernel<D, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB, true>);
+    else launch(moe_down_kernel<D, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB, false>);
+  };
+  if (fmt == 4) by(std::integral_constant<int, 4>{});
+  else if (fmt == 5) by(std::integral_constant<int, 5>{});
+  else by(std::integral_constant<int, 6>{});
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1397,11 +1417,13 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
                                        const float* shared_w, void* act, float* pairs,
                                        float* shared_out, int64_t M, int64_t max_slots,
                                        int64_t E, int64_t H, int64_t F, void* stream) {
-  if (fmt != 4 || M <= 0 || M > 16 || max_slots <= 0 || max_slots > MOE_MAX_SLOTS || H % 256 ||
-      F % 256 || (F / 16) % MOE_GU_PPB || (H / 16 / MOE_DN_NTILE) % MOE_DN_GPB)
+  const int gu_fmt = fmt & 0xff, dn_fmt = (fmt >> 8) ? ((fmt >> 8) & 0xff) : gu_fmt;
+  if (!expert_fmt(gu_fmt) || !expert_fmt(dn_fmt) || M <= 0 || M > 16 || max_slots <= 0 ||
+      max_slots > MOE_MAX_SLOTS || H % 256 || F % 256 || (F / 16) % MOE_GU_PPB ||
+      (H / 16 / MOE_DN_NTILE) % MOE_DN_GPB)
     return SV_EINVAL;
-  const int64_t gu_q = 2 * F * H / 2, gu_m = 2 * F * (H / 256) * 16;
-  const int64_t dn_q = H * F / 2, dn_m = H * (F / 256) * 16;
+  const int64_t gu_q = packed_quant(gu_fmt, 2 * F, H), gu_m = packed_meta(gu_fmt, 2 * F, H);
+  const int64_t dn_q = packed_quant(dn_fmt, H, F), dn_m = packed_meta(dn_fmt, H, F);
   const int gu_per_slot = (int)(F / 16 / MOE_GU_PPB);
   const int dn_per_slot = (int)(H / 16 / MOE_DN_NTILE / MOE_DN_GPB);
   if (gu_per_slot > MOE_MAX_ITEMS || dn_per_slot > MOE_MAX_ITEMS) return SV_ENOTSUP;
@@ -1416,12 +1438,29 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
                        (uint16_t*)act, weights, shared_w, pairs, shared_out, (int)M, (int)H,
                        (int)F);
   };
-  if (F / QK == MOE_DN_WS)
-    launch(moe_experts_kernel<4, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
-                              true>);
-  else
-    launch(moe_experts_kernel<4, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
-                              false>);
+  // Q4_K pairs: three waves per SIMD (168 registers); formats with wider weight operands
+  // (Q5_K's qh, Q6_K's third vector) at two
+  auto pick = [&](auto gu, auto dn) {
+    constexpr int G = decltype(gu)::value, D = decltype(dn)::value;
+    constexpr bool q4 = G == 4 && D == 4;
+    if (F / QK == MOE_DN_WS)
+      launch(moe_experts_kernel<G, D, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
+                                true, q4 ? 3 : 2>);
+    else
+      launch(moe_experts_kernel<G, D, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
+                                false, 2>);
+    return SV_OK;
+  };
+  using I4 = std::integral_constant<int, 4>;
+  using I5 = std::integral_constant<int, 5>;
+  using I6 = std::integral_constant<int, 6>;
+  if (gu_fmt == 4 && dn_fmt == 4) pick(I4{}, I4{});
+  else if (gu_fmt == 4 && dn_fmt == 5) pick(I4{}, I5{});
+  else if (gu_fmt == 4 && dn_fmt == 6) pick(I4{}, I6{});
+  else if (gu_fmt == 5 && dn_fmt == 5) pick(I5{}, I5{});
+  else if (gu_fmt == 5 && dn_fmt == 6) pick(I5{}, I6{});
+  else if (gu_fmt == 6 && dn_fmt == 6) pick(I6{}, I6{});
+  else return SV_ENOTSUP;  // down below gate/up precision: not a GGUF mix
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1459,10 +1498,11 @@ SV_API int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_
                                   int64_t topk, int64_t E, int64_t H, int64_t F, void* stream) {
   if (M * topk > MOE_MAX_SLOTS - 1) return SV_EINVAL;
   const int64_t slots = M * topk + (sh_gu_quant ? 1 : 0);
-  int rc = snowverify_moe_gate_up(fmt, gu_quant, gu_meta, sh_gu_quant, sh_gu_meta, plan, ws, act,
+  const int gu_fmt = fmt & 0xff, dn_fmt = (fmt >> 8) ? ((fmt >> 8) & 0xff) : gu_fmt;
+  int rc = snowverify_moe_gate_up(gu_fmt, gu_quant, gu_meta, sh_gu_quant, sh_gu_meta, plan, ws, act,
                                   M, slots, E, H, F, stream);
   if (rc != SV_OK) return rc;
-  rc = snowverify_moe_down(fmt, dn_quant, dn_meta, sh_dn_quant, sh_dn_meta, plan, act, weights,
+  rc = snowverify_moe_down(dn_fmt, dn_quant, dn_meta, sh_dn_quant, sh_dn_meta, plan, act, weights,
                            shared_w, pairs, shared_out, slots, E, H, F, stream);
   if (rc != SV_OK) return rc;
   return snowverify_moe_combine(pairs, sh_gu_quant ? shared_out : nullptr, out, M, topk, H, stream);

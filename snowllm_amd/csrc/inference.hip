@@ -161,8 +161,12 @@ int moe_body(const Weight* w, const void* hidden, const void* router, void* out,
   const BuildGeometry& g = active_geometry();
   const int64_t E = g.moe_num_experts, K = g.moe_topk, H = g.hidden, F = g.moe_inter;
   const bool shared = !absent(&w[2]);
-  if (!kquant(&w[0]) || !kquant(&w[1]) || w[0].fmt != 4 || w[1].fmt != 4) return SV_ENOTSUP;
-  if (shared && (!kquant(&w[2]) || !kquant(&w[3]) || w[2].fmt != 4 || w[3].fmt != 4))
+  // experts: gate/up in Q4_K, Q5_K or Q6_K, down in the same or a wider k-quant; the shared
+  // expert in the routed experts' formats
+  auto efmt = [](int f) { return f == 4 || f == 5 || f == 6; };
+  if (!kquant(&w[0]) || !kquant(&w[1]) || !efmt(w[0].fmt) || !efmt(w[1].fmt)) return SV_ENOTSUP;
+  if (shared && (!kquant(&w[2]) || !kquant(&w[3]) || w[2].fmt != w[0].fmt ||
+                 w[3].fmt != w[1].fmt))
     return SV_ENOTSUP;
   if (shared != (g.moe_shared_expert != 0)) return SV_EINVAL;
   int rc = snowverify_dense_gemv(WT_BF16, router, hidden, ws.logits, M, E + 1, H, 0, s);
@@ -171,7 +175,8 @@ int moe_body(const Weight* w, const void* hidden, const void* router, void* out,
                                  shared ? ws.shared_w : nullptr, ws.plan, s);
   if (rc) return rc;
   const int64_t slots = M * K + (shared ? 1 : 0);
-  rc = snowverify_moe_gate_up_down(4, w[0].data[0], w[0].data[1], w[1].data[0], w[1].data[1],
+  rc = snowverify_moe_gate_up_down(w[0].fmt | (w[1].fmt << 8), w[0].data[0], w[0].data[1],
+                                   w[1].data[0], w[1].data[1],
                                    shared ? w[2].data[0] : nullptr,
                                    shared ? w[2].data[1] : nullptr,
                                    shared ? w[3].data[0] : nullptr,
@@ -341,6 +346,9 @@ SV_API int snowllm_paged_attention(const PagedAttentionStep* st, void* scratch, 
 // down matrix; each packed matrix is snowllm_gemm_kquant_shuffle_b's (quant, meta), whose
 // 16-row tiles are stored in order, so the gate half and the up half are packed separately
 // into the two halves. The +4 bytes of the single-matrix quant size come once, at the end.
+extern "C" int snowverify_kquant_shuffle_split(int fmt, const uint8_t* top, const uint8_t* bottom,
+                                               int64_t n_top, uint8_t* quant, uint8_t* meta,
+                                               int64_t N, int64_t K, void* stream);
 namespace {
 int64_t expert_quant(int fmt, int64_t N, int64_t K) {
   const int64_t q = snowllm_kquant_quant_bytes(fmt, N, K);
@@ -348,7 +356,7 @@ int64_t expert_quant(int fmt, int64_t N, int64_t K) {
 }
 bool expert_geometry(int fmt, int64_t E) {
   const BuildGeometry& g = active_geometry();
-  return (fmt == 4 || fmt == 8) && E > 0 && g.moe_inter > 0 && g.hidden > 0 &&
+  return (fmt == 4 || fmt == 5 || fmt == 6 || fmt == 8) && E > 0 && g.moe_inter > 0 && g.hidden > 0 &&
          expert_quant(fmt, g.moe_inter, g.hidden) > 0 && expert_quant(fmt, g.hidden, g.moe_inter) > 0;
 }
 }  // namespace
@@ -381,14 +389,15 @@ SV_API int snowllm_moe_kquant_shuffle_gate_up(int fmt, const uint8_t* gate, cons
   const BuildGeometry& g = active_geometry();
   const int64_t F = g.moe_inter, H = g.hidden;
   const int64_t src = snowllm_kquant_gguf_bytes(fmt, F, H);
-  const int64_t q = expert_quant(fmt, F, H), m = snowllm_kquant_meta_bytes(fmt, F, H);
-  for (int64_t e = 0; e < E; ++e)
-    for (int half = 0; half < 2; ++half) {
-      const uint8_t* from = (half ? up : gate) + e * src;
-      const int rc = snowllm_gemm_kquant_shuffle_b(fmt, from, quant + (2 * e + half) * q,
-                                                   meta + (2 * e + half) * m, F, H, stream);
-      if (rc) return rc;
-    }
+  const int64_t q = expert_quant(fmt, 2 * F, H), m = snowllm_kquant_meta_bytes(fmt, 2 * F, H);
+  // each expert's [gate; up] as one [2F, H] matrix (gate rows first), read from its two
+  // sources; for formats without a per-matrix tail this is the two halves packed one after
+  // the other
+  for (int64_t e = 0; e < E; ++e) {
+    const int rc = snowverify_kquant_shuffle_split(fmt, gate + e * src, up + e * src, F,
+                                                   quant + e * q, meta + e * m, 2 * F, H, stream);
+    if (rc) return rc;
+  }
   return SV_OK;
 }
 

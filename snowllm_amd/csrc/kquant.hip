@@ -263,12 +263,21 @@ int launch_gemv_mt(const void* quant, const void* meta, const void* ws, void* c,
 // ---------------------------------------------------------------------------------------
 // Repack GGUF blocks into (quant, meta).
 // ---------------------------------------------------------------------------------------
-__global__ void shuffle_q4k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ quant,
+// Rows n >= n_split come from `bottom` (row n - n_split), so that two GGUF tensors of one
+// format repack as one matrix ([gate; up] of an expert); single matrices pass n_split = N.
+__device__ __forceinline__ const uint8_t* src_block(const uint8_t* top, const uint8_t* bottom,
+                                                    int64_t n_split, int64_t n, int64_t s,
+                                                    int64_t S, int64_t bytes) {
+  return n < n_split ? top + (n * S + s) * bytes : bottom + ((n - n_split) * S + s) * bytes;
+}
+
+__global__ void shuffle_q4k(const uint8_t* __restrict__ gguf, const uint8_t* __restrict__ gguf2,
+                            int64_t n_split, uint8_t* __restrict__ quant,
                             uint8_t* __restrict__ meta, int64_t N, int64_t S) {
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= N * S) return;
   const int64_t n = id / S, s = id % S;
-  const uint8_t* blk = gguf + (n * S + s) * 144;
+  const uint8_t* blk = src_block(gguf, gguf2, n_split, n, s, S, 144);
   const int64_t tile = n / TILE_N;
   const int col = (int)(n % TILE_N);
   const int64_t ts = tile * S + s;
@@ -286,7 +295,8 @@ __global__ void shuffle_q4k(const uint8_t* __restrict__ gguf, uint8_t* __restric
     }
 }
 
-__global__ void shuffle_q80(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ quant,
+__global__ void shuffle_q80(const uint8_t* __restrict__ gguf, const uint8_t* __restrict__ gguf2,
+                            int64_t n_split, uint8_t* __restrict__ quant,
                             uint8_t* __restrict__ meta, int64_t N, int64_t S) {
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= N * S) return;
@@ -295,7 +305,7 @@ __global__ void shuffle_q80(const uint8_t* __restrict__ gguf, uint8_t* __restric
   const int col = (int)(n % TILE_N);
   const int64_t ts = tile * S + s;
   for (int j = 0; j < 8; ++j) {
-    const uint8_t* blk = gguf + ((n * S + s) * 8 + j) * 34;
+    const uint8_t* blk = src_block(gguf, gguf2, n_split, n, s, S, 8 * 34) + j * 34;
     uint8_t* mo = meta + (ts * 16 + col) * 16 + 2 * j;
     mo[0] = blk[0];
     mo[1] = blk[1];
@@ -310,12 +320,13 @@ __global__ void shuffle_q80(const uint8_t* __restrict__ gguf, uint8_t* __restric
 
 // Q5_K: the Q4_K nibble layout of qs (@48), then each lane's 8 qh bytes (@16) after the tile-
 // superblock's nibbles; meta as Q4_K (d, dmin, scales: the block's first 16 bytes).
-__global__ void shuffle_q5k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ quant,
+__global__ void shuffle_q5k(const uint8_t* __restrict__ gguf, const uint8_t* __restrict__ gguf2,
+                            int64_t n_split, uint8_t* __restrict__ quant,
                             uint8_t* __restrict__ meta, int64_t N, int64_t S) {
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= N * S) return;
   const int64_t n = id / S, s = id % S;
-  const uint8_t* blk = gguf + (n * S + s) * 176;
+  const uint8_t* blk = src_block(gguf, gguf2, n_split, n, s, S, 176);
   const int64_t tile = n / TILE_N;
   const int col = (int)(n % TILE_N);
   const int64_t ts = tile * S + s;
@@ -341,12 +352,13 @@ __global__ void shuffle_q5k(const uint8_t* __restrict__ gguf, uint8_t* __restric
 // Q6_K: per lane three 16-byte vectors (ql of half 0, ql of half 1, qh of both halves, each
 // the bytes l = 8 kq .. 8 kq + 7 of its two 32-byte runs); meta: the 16 int8 scales per
 // column, and after every tile-superblock's scales the fp16 d per (tile-superblock, column).
-__global__ void shuffle_q6k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ quant,
+__global__ void shuffle_q6k(const uint8_t* __restrict__ gguf, const uint8_t* __restrict__ gguf2,
+                            int64_t n_split, uint8_t* __restrict__ quant,
                             uint8_t* __restrict__ meta, int64_t N, int64_t S) {
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= N * S) return;
   const int64_t n = id / S, s = id % S;
-  const uint8_t* blk = gguf + (n * S + s) * 210;
+  const uint8_t* blk = src_block(gguf, gguf2, n_split, n, s, S, 210);
   const int64_t tile = n / TILE_N;
   const int col = (int)(n % TILE_N);
   const int64_t ts = tile * S + s;
@@ -479,27 +491,35 @@ SV_API int snowllm_kquant_supported(int fmt) { return fmt_ok(fmt) ? 1 : 0; }
 // (0 = automatic, 1..6 = fixed (tiles per workgroup, waves) pairs). Process-global.
 SV_API void snowverify_gemv_variant(int v) { g_gemv_variant = v; }
 
-SV_API int snowllm_gemm_kquant_shuffle_b(int fmt, const uint8_t* gguf, uint8_t* quant,
-                                         uint8_t* meta, int64_t N, int64_t K, void* stream) {
-  if (!fmt_ok(fmt) || N <= 0 || K <= 0 || K % 256 || N % TILE_N) return SV_EINVAL;
+// Extension (no counterpart in the reference): repack two GGUF tensors of one format, `top`
+// (rows 0 .. n_top - 1) and `bottom` (rows n_top .. N - 1), as one [N, K] matrix -- an
+// expert's [gate; up] from its two stacks.
+SV_API int snowverify_kquant_shuffle_split(int fmt, const uint8_t* top, const uint8_t* bottom,
+                                           int64_t n_top, uint8_t* quant, uint8_t* meta,
+                                           int64_t N, int64_t K, void* stream) {
+  if (!fmt_ok(fmt) || N <= 0 || K <= 0 || K % 256 || N % TILE_N || n_top < 0 || n_top > N ||
+      !top || (n_top < N && !bottom))
+    return SV_EINVAL;
   const int64_t S = K / 256;
   const int64_t total = N * S;
   const int nt = 256;
   hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)((total + nt - 1) / nt));
   if (fmt == FMT_Q4_K)
-    hipLaunchKernelGGL(shuffle_q4k, dim3((unsigned)((total + nt - 1) / nt)), dim3(nt), 0, s, gguf,
-                       quant, meta, N, S);
+    hipLaunchKernelGGL(shuffle_q4k, grid, dim3(nt), 0, s, top, bottom, n_top, quant, meta, N, S);
   else if (fmt == FMT_Q5_K)
-    hipLaunchKernelGGL(shuffle_q5k, dim3((unsigned)((total + nt - 1) / nt)), dim3(nt), 0, s, gguf,
-                       quant, meta, N, S);
+    hipLaunchKernelGGL(shuffle_q5k, grid, dim3(nt), 0, s, top, bottom, n_top, quant, meta, N, S);
   else if (fmt == FMT_Q6_K)
-    hipLaunchKernelGGL(shuffle_q6k, dim3((unsigned)((total + nt - 1) / nt)), dim3(nt), 0, s, gguf,
-                       quant, meta, N, S);
+    hipLaunchKernelGGL(shuffle_q6k, grid, dim3(nt), 0, s, top, bottom, n_top, quant, meta, N, S);
   else
-    hipLaunchKernelGGL(shuffle_q80, dim3((unsigned)((total + nt - 1) / nt)), dim3(nt), 0, s, gguf,
-                       quant, meta, N, S);
+    hipLaunchKernelGGL(shuffle_q80, grid, dim3(nt), 0, s, top, bottom, n_top, quant, meta, N, S);
   SV_CHECK_LAUNCH();
   return SV_OK;
+}
+
+SV_API int snowllm_gemm_kquant_shuffle_b(int fmt, const uint8_t* gguf, uint8_t* quant,
+                                         uint8_t* meta, int64_t N, int64_t K, void* stream) {
+  return snowverify_kquant_shuffle_split(fmt, gguf, nullptr, N, quant, meta, N, K, stream);
 }
 
 SV_API int64_t snowllm_gemm_kquant_a_ws_bytes(int64_t M, int64_t K) {

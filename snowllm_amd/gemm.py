@@ -35,6 +35,33 @@ def gemm_kquant_shuffle_b(fmt: int, b_gguf: torch.Tensor, N: int,
     return quant, meta
 
 
+def kquant_shuffle_stack(fmt: int, b_gguf: torch.Tensor, count: int, N: int,
+                         K: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """`count` [N, K] GGUF weights stored one after another (an expert stack [E, N, K]) ->
+    (quant, meta) with each weight repacked on its own, weight e at e * (quant bytes - 4) and
+    e * meta bytes: the layout of snowllm_moe_kquant_shuffle_gate_up / _down, which the MoE
+    kernels read (Q6_K's per-matrix tail of fp16 scales makes it differ from one repack of
+    the [count * N, K] matrix)."""
+    quant_bytes, meta_bytes, gguf_bytes = kquant_bytes(fmt, N, K)
+    if quant_bytes < 0 or meta_bytes < 0 or count <= 0:
+        raise SnowLLMError(f"kquant_shuffle_stack: format {fmt}, {count} x [{N}, {K}] is not "
+                           f"supported")
+    _chk(b_gguf, "b_gguf", torch.uint8)
+    if b_gguf.numel() != count * gguf_bytes:
+        raise SnowLLMError(f"kquant_shuffle_stack: expected {count * gguf_bytes} bytes, got "
+                           f"{b_gguf.numel()}")
+    if fmt != 6:
+        # no per-matrix tail: the stack repacks as one matrix, to the same bytes
+        return gemm_kquant_shuffle_b(fmt, b_gguf, count * N, K)
+    qs = quant_bytes - 4   # the 4 slack bytes behind each weight are read, never written
+    quant, meta = empty_bytes(count * qs + 4), empty_bytes(count * meta_bytes)
+    for e in range(count):
+        check(lib.snowllm_gemm_kquant_shuffle_b(fmt, _p(b_gguf) + e * gguf_bytes,
+                                                _p(quant) + e * qs, _p(meta) + e * meta_bytes,
+                                                N, K, _stream()), "kquant_shuffle_stack")
+    return quant, meta
+
+
 def gemm_kquant_a_ws_bytes(M: int, K: int) -> int:
     return int(lib.snowllm_gemm_kquant_a_ws_bytes(int(M), int(K)))
 

@@ -178,7 +178,8 @@ def norm_router_plan(x, gamma, ws, eps, router, logits, topk, weights, ids, shar
 
 def moe_experts(fmt, gu, dn, sh_gu, sh_dn, plan, ws, weights, shared_w, act, pairs, shared_out,
                 out, M, topk, E, H, F):
-    """gu/dn/sh_gu/sh_dn: (quant, meta) pairs of the stacked expert weights."""
+    """gu/dn/sh_gu/sh_dn: (quant, meta) pairs of the stacked expert weights; fmt: the gate/up
+    format id (4, 5, 6 for Q4_K, Q5_K, Q6_K) | the down format id << 8 (0: the gate/up's)."""
     check(lib.snowverify_moe_experts(fmt, _p(gu[0]), _p(gu[1]), _p(dn[0]), _p(dn[1]),
                                      _p(sh_gu[0]), _p(sh_gu[1]), _p(sh_dn[0]), _p(sh_dn[1]),
                                      _p(plan), _p(ws), _p(weights), _p(shared_w), _p(act),
@@ -187,12 +188,14 @@ def moe_experts(fmt, gu, dn, sh_gu, sh_dn, plan, ws, weights, shared_w, act, pai
 
 
 def moe_gate_up(fmt, gu, sh_gu, plan, ws, act, M, max_slots, E, H, F):
+    """fmt: the gate/up format id (4, 5, 6)."""
     check(lib.snowverify_moe_gate_up(fmt, _p(gu[0]), _p(gu[1]), _p(sh_gu[0]), _p(sh_gu[1]), _p(plan),
                                      _p(ws), _p(act), M, max_slots, E, H, F, _stream()),
           "moe_gate_up")
 
 
 def moe_down(fmt, dn, sh_dn, plan, act, weights, shared_w, pairs, shared_out, max_slots, E, H, F):
+    """fmt: the down format id (4, 5, 6)."""
     check(lib.snowverify_moe_down(fmt, _p(dn[0]), _p(dn[1]), _p(sh_dn[0]), _p(sh_dn[1]), _p(plan),
                                   _p(act), _p(weights), _p(shared_w), _p(pairs), _p(shared_out),
                                   max_slots, E, H, F, _stream()), "moe_down")
@@ -201,7 +204,8 @@ def moe_down(fmt, dn, sh_dn, plan, act, weights, shared_w, pairs, shared_out, ma
 def moe_gate_up_down(fmt, gu, dn, sh_gu, sh_dn, plan, ws, weights, shared_w, act, pairs,
                      shared_out, M, max_slots, E, H, F):
     """moe_gate_up then moe_down in one launch (same bits); launches on one device must be
-    stream-ordered (library-owned counters)."""
+    stream-ordered (library-owned counters). fmt as moe_experts'; down in the gate/up format
+    or a wider one."""
     check(lib.snowverify_moe_gate_up_down(fmt, _p(gu[0]), _p(gu[1]), _p(dn[0]), _p(dn[1]),
                                           _p(sh_gu[0]), _p(sh_gu[1]), _p(sh_dn[0]),
                                           _p(sh_dn[1]), _p(plan), _p(ws), _p(weights),

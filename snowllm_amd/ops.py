@@ -5,7 +5,7 @@ from .sampling import (SAMPLING_MAX_K, argmax, probabilities, sample,  # noqa: F
 from .metadata import spec_accept  # noqa: F401
 from . import dflash  # noqa: F401
 from .gemm import (Q4_K, Q8_0, gemm_kquant_a, gemm_kquant_a_ws_bytes,  # noqa: F401
-                   gemm_kquant_shuffle_b, kquant_bytes,
+                   gemm_kquant_shuffle_b, kquant_bytes, kquant_shuffle_stack,
                    gemm_kquant_prepare_a, gemm_kquant_a_prepared, gemm_kquant_a_noalloc)
 from .attention import (kv_pool_bytes, paged_attention_explicit,  # noqa: F401
                         paged_attention_explicit_scratch_bytes, paged_attention, paged_attention_qk,

@@ -52,6 +52,7 @@ class VerifyConfig:
     shared_expert: bool = True
     attn_fmt: int = Q4_K
     ffn_fmt: int = Q4_K
+    down_fmt: int = 0        # format of the down projections when it differs (0: ffn_fmt)
     tree_parents: tuple = ()  # non-empty: tree block (ancestor mask) instead of a chain
     eps: float = 1e-6
     page: int = 16
@@ -180,9 +181,14 @@ def gguf_random(fmt, n, k, seed, device="cuda", centered=False):
     raise SnowLLMError(f"unknown format {fmt}")
 
 
-def packed_random(fmt, n, k, seed, keep_raw=False, centered=True):
+def packed_random(fmt, n, k, seed, keep_raw=False, centered=True, stack=1):
+    """(quant, meta, raw GGUF bytes or None) of a seeded random [n, k] weight; stack > 1: n
+    rows of `stack` equal weights (an expert stack), each repacked on its own."""
     raw = gguf_random(fmt, n, k, seed, centered=centered)
-    quant, meta = ops.gemm_kquant_shuffle_b(fmt, raw, n, k)
+    if stack > 1:
+        quant, meta = ops.kquant_shuffle_stack(fmt, raw, stack, n // stack, k)
+    else:
+        quant, meta = ops.gemm_kquant_shuffle_b(fmt, raw, n, k)
     return (quant, meta, raw if keep_raw else None)
 
 
@@ -204,6 +210,7 @@ class LayerWeights:
     # config's attn_fmt / ffn_fmt (0: the config's)
     qkv_fmt: int = 0
     o_fmt: int = 0
+    gu_fmt: int = 0
     dn_fmt: int = 0
 
 
@@ -288,8 +295,8 @@ class VerifyModel:
             else:
                 kr = i in keep_raw
 
-            def pk(fmt, n, k, j):
-                return packed_random(fmt, n, k, sub(i, j), kr, c.centered)
+            def pk(fmt, n, k, j, stack=1):
+                return packed_random(fmt, n, k, sub(i, j), kr, c.centered, stack)
 
             lw = LayerWeights(in_norm=gamma(H), post_norm=gamma(H), q_norm=gamma(c.head_dim),
                               k_norm=gamma(c.head_dim), qkv=pk(c.attn_fmt, c.qkv_n, H, 0),
@@ -298,15 +305,16 @@ class VerifyModel:
                 E, F = c.experts, c.expert_ffn
                 router = (torch.randn(E + 1, H, device=dev, generator=gen) / math.sqrt(H)).bfloat16()
                 lw.router = Lops.dense_shuffle(router)
-                lw.gu = pk(c.ffn_fmt, E * 2 * F, H, 2)
-                lw.dn = pk(c.ffn_fmt, E * H, F, 3)
+                lw.gu = pk(c.ffn_fmt, E * 2 * F, H, 2, E)
+                lw.dn = pk(c.down_fmt or c.ffn_fmt, E * H, F, 3, E)
                 lw.sh_gu = pk(c.ffn_fmt, 2 * F, H, 4)
-                lw.sh_dn = pk(c.ffn_fmt, H, F, 5)
+                lw.sh_dn = pk(c.down_fmt or c.ffn_fmt, H, F, 5)
                 if kr:
                     lw.raw["router"] = router
             else:
                 lw.gu = pk(c.ffn_fmt, 2 * c.ffn, H, 2)
-                lw.dn = pk(c.ffn_fmt, H, c.ffn, 3)
+                lw.dn = pk(c.down_fmt or c.ffn_fmt, H, c.ffn, 3)
+            lw.dn_fmt = c.down_fmt
             self.layers.append(lw)
         self.embed = (0.02 * torch.randn(V, H, device=dev, generator=gen)).half()
         head = (0.02 * torch.randn(V, H, device=dev, generator=gen)).half()
@@ -480,6 +488,8 @@ class VerifyModel:
                                   self.o, T, H, c.heads * c.head_dim, self.ws_a)
             # feed-forward block
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
+            gu_fmt = lw.gu_fmt or c.ffn_fmt
+            dn_fmt = lw.dn_fmt or c.down_fmt or c.ffn_fmt
             if c.moe:
                 # the router, routing and experts on row chunks of at most 16 rows (one chunk
                 # for a single block); chunk j's operands are its rows' tiles of ws_h2
@@ -507,7 +517,7 @@ class VerifyModel:
 
                     # gate/up and down in one launch: a slot's down starts when its gate/up
                     # is done
-                    Lops.moe_gate_up_down(c.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, plan,
+                    Lops.moe_gate_up_down(gu_fmt | dn_fmt << 8, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, plan,
                                           ws, self.route_w[rs], self.shared_w[rs],
                                           self.moe_act, self.pairs[r0 * K:(r0 + n) * K],
                                           self.shared_out[rs], n, n * K + 1, c.experts, H,
@@ -521,10 +531,10 @@ class VerifyModel:
                 Lops.norm_prep(self.o, lw.post_norm, self.ws_h2, c.eps, res_in=res_in,
                                res_out=res_out)
                 for r0, n in self.row_chunks:
-                    Lops.gate_up_swiglu(c.ffn_fmt, lw.gu[0], lw.gu[1],
+                    Lops.gate_up_swiglu(gu_fmt, lw.gu[0], lw.gu[1],
                                         self._ws_rows(self.ws_h2, r0), self.act[r0:r0 + n], n,
                                         c.ffn, H)
-                ops.gemm_kquant_a(lw.dn_fmt or c.ffn_fmt, self.act, lw.dn[0], lw.dn[1], self.x, T,
+                ops.gemm_kquant_a(dn_fmt, self.act, lw.dn[0], lw.dn[1], self.x, T,
                                   H, c.ffn, self.ws_act)
             res_in, res_out = res_out, self.res[1] if res_out is self.res[0] else self.res[0]
         self.layer_residual = res_in  # residual stream entering the next layer (with self.x)

@@ -220,7 +220,8 @@ def _fake_tensors(cfg, fmt="Q4_K", **override):
             for n, shape in (("ffn_gate_exps", (E, F, H)), ("ffn_up_exps", (E, F, H)),
                              ("ffn_down_exps", (E, H, F)), ("ffn_gate_shexp", (F, H)),
                              ("ffn_up_shexp", (F, H)), ("ffn_down_shexp", (H, F))):
-                add(p + n + ".weight", shape, override.get("ffn_fmt", fmt))
+                q = override.get("ffn_fmt", fmt)
+                add(p + n + ".weight", shape, override.get("down_fmt", q) if "down" in n else q)
         else:
             add(p + "ffn_gate.weight", (cfg.ffn, H), fmt)
             add(p + "ffn_up.weight", (cfg.ffn, H), fmt)
@@ -266,16 +267,44 @@ def test_checkpoints_outside_the_path_are_refused(tmp_path):
         _refused(tmp_path, cfg, {"qwen35moe.full_attention_interval": 4})
     with pytest.raises(SnowLLMError, match="shared expert width"):
         _refused(tmp_path, cfg, {"qwen35moe.expert_shared_feed_forward_length": 512})
-    with pytest.raises(SnowLLMError, match="Q6_K"):
-        _refused(tmp_path, cfg, ffn_fmt="Q6_K")
-    with pytest.raises(SnowLLMError, match="Q4_K experts"):
+    with pytest.raises(SnowLLMError, match="Q6_K experts"):
         _refused(tmp_path, cfg, ffn_fmt="Q8_0")
+    with pytest.raises(SnowLLMError, match="narrower than the experts' gate/up"):
+        _refused(tmp_path, cfg, layer=True, ffn_fmt="Q6_K", down_fmt="Q4_K")
+    with pytest.raises(SnowLLMError, match="'llama' checkpoint"):
+        _refused(tmp_path, cfg, {"general.architecture": "llama",
+                                 **{k.replace("qwen35moe", "llama"): v
+                                    for k, v in C_meta(cfg).items() if k.startswith("qwen35moe")}})
+    with pytest.raises(SnowLLMError, match="without experts"):
+        _refused(tmp_path, _tiny_cfg(False), {"general.architecture": "qwen35moe",
+                                              **{k.replace("qwen35", "qwen35moe", 1): v
+                                                 for k, v in C_meta(_tiny_cfg(False)).items()
+                                                 if k.startswith("qwen35.")}})
     with pytest.raises(SnowLLMError, match="output gate"):
         _refused(tmp_path, cfg, layer=True, q_rows=2 * cfg.heads * cfg.head_dim)
     with pytest.raises(SnowLLMError, match="linear-attention"):
         _refused(tmp_path, cfg, layer=True, extra=("ssm_a",))
     with pytest.raises(SnowLLMError, match="one k-quant format"):
         _refused(tmp_path, cfg, layer=True, k_fmt="Q8_0")
+
+
+def C_meta(cfg):
+    from snowllm_amd import checkpoint as C
+    return C.gguf_metadata(cfg)
+
+
+@pytest.mark.parametrize("gu,dn", [("Q5_K", "Q5_K"), ("Q6_K", "Q6_K"), ("Q4_K", "Q6_K")])
+def test_expert_formats_taken(tmp_path, gu, dn):
+    """Q4_K_M / Q5_K_M / Q6_K files: experts in Q4_K, Q5_K or Q6_K, down as wide or wider."""
+    from snowllm_amd import checkpoint as C
+    from snowllm_amd.gguf import KQUANT_FORMAT
+    cfg = _tiny_cfg(True)
+    g = GGUF(write_gguf(tmp_path / "m.gguf", C.gguf_metadata(cfg),
+                        _fake_tensors(cfg, ffn_fmt=gu, down_fmt=dn)))
+    try:
+        assert C.config_from_gguf(g, context=300, block=9).ffn_fmt == KQUANT_FORMAT[gu]
+    finally:
+        g.close()
 
 
 def test_norm_weight_convention():

@@ -91,13 +91,16 @@ def test_reference_dataflow_layer_matches_verify_model(gpu, geometry_of):
     assert torch.equal(blk, m.x)
 
 
-def test_moe_without_norm_and_head(gpu, geometry_of):
+@pytest.mark.parametrize("down_fmt", [0, 6])   # 6: Q6_K down under Q4_K gate/up (Q4_K_M)
+def test_moe_without_norm_and_head(gpu, geometry_of, down_fmt):
+    from dataclasses import replace
     from snowllm_amd import layers as L
     from snowllm_amd import ops
     from snowllm_amd.verify import VerifyModel
-    cfg = tiny("moe")
+    cfg = replace(tiny("moe"), down_fmt=down_fmt)
+    dn_f = down_fmt or cfg.ffn_fmt
     geometry_of(cfg)
-    print("reference-signature MoE / head, tiny moe", flush=True)
+    print(f"reference-signature MoE / head, tiny moe, down format {dn_f}", flush=True)
     m = VerifyModel(cfg, seed=9)
     T, H = cfg.block, cfg.hidden
     m.set_block(torch.arange(T) * 3)
@@ -108,9 +111,9 @@ def test_moe_without_norm_and_head(gpu, geometry_of):
     out = torch.empty(T, H, dtype=torch.bfloat16, device="cuda")
     mws = torch.empty(ops.inference_moe_workspace_bytes(T), dtype=torch.uint8, device="cuda")
     gate = ops.KQuantExpertWeight(lw.gu[0], lw.gu[1], None, cfg.ffn_fmt)
-    down = ops.KQuantExpertWeight(lw.dn[0], lw.dn[1], None, cfg.ffn_fmt)
+    down = ops.KQuantExpertWeight(lw.dn[0], lw.dn[1], None, dn_f)
     sh_gate = ops.KQuantProjWeight(lw.sh_gu[0], lw.sh_gu[1], cfg.ffn_fmt)
-    sh_down = ops.KQuantProjWeight(lw.sh_dn[0], lw.sh_dn[1], cfg.ffn_fmt)
+    sh_down = ops.KQuantProjWeight(lw.sh_dn[0], lw.sh_dn[1], dn_f)
     ops.inference_moe(y, lw.router, gate, down, sh_gate, sh_down, out, mws)
     # explicit path on the same rows
     ws = torch.empty(ops.gemm_kquant_a_ws_bytes(T, H), dtype=torch.uint8, device="cuda")
@@ -119,7 +122,7 @@ def test_moe_without_norm_and_head(gpu, geometry_of):
     L.moe_route_plan(m.router_logits, cfg.experts, cfg.topk, m.route_w, m.route_ids, m.shared_w,
                      m.plan)
     want = torch.empty_like(out)
-    L.moe_experts(cfg.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, m.plan, ws, m.route_w,
+    L.moe_experts(cfg.ffn_fmt | dn_f << 8, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, m.plan, ws, m.route_w,
                   m.shared_w, m.moe_act, m.pairs, m.shared_out, want, T, cfg.topk, cfg.experts, H,
                   cfg.expert_ffn)
     torch.cuda.synchronize()

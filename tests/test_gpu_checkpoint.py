@@ -46,6 +46,10 @@ CASES = [
     # the other k-quants of a Q4_K_M / UD-Q4_K_XL file
     ("moe", {"attn_fmt": 6}, 1),
     ("dense", {"attn_fmt": 5, "ffn_fmt": 6}, 2),
+    # experts: Q4_K with Q6_K down (Q4_K_M), Q5_K with Q6_K down (Q5_K_M), all Q6_K
+    ("moe", {"down_fmt": 6}, 1),
+    ("moe", {"attn_fmt": 5, "ffn_fmt": 5, "down_fmt": 6}, 2),
+    ("moe", {"attn_fmt": 6, "ffn_fmt": 6}, 1),
 ]
 
 

@@ -61,19 +61,24 @@ def test_route_plan(gpu, M):
         assert np.array_equal(p2[key], p[key])
 
 
-@pytest.mark.parametrize("E,F", [(E, F), (64, 1024)])  # one / two superblocks per down wave
-def test_gate_up_down_equals_separate_launches(gpu, E, F):
+# one / two superblocks per down wave; expert formats (gate/up, down): Q4_K_M keeps some
+# layers' down in Q6_K, Q5_K_M / Q6_K files store the experts in those formats
+@pytest.mark.parametrize("E,F,gu_f,dn_f", [(E, F, 4, 4), (64, 1024, 4, 4), (E, F, 4, 6),
+                                           (E, F, 6, 6), (64, 1024, 5, 6), (E, F, 5, 5)])
+def test_gate_up_down_equals_separate_launches(gpu, E, F, gu_f, dn_f):
     """Gate/up and down in one launch (down items wait for their slot's gate/up items) give the
     bits of the two launches; consecutive launches of different sizes reuse the flags."""
     from snowllm_amd import layers as L, ops
     from snowllm_amd.verify import packed_random
-    gu = packed_random(4, E * 2 * F, H, 51)
-    dn = packed_random(4, E * H, F, 52)
-    sgu = packed_random(4, 2 * F, H, 53)
-    sdn = packed_random(4, H, F, 54)
-    for M, shared, spread in ((9, True, False), (16, True, True), (1, True, False),
-                              (9, False, True), (9, True, True)):
-        print(f"gate_up_down E={E} F={F} M={M} shared={shared} spread={spread}", flush=True)
+    gu = packed_random(gu_f, E * 2 * F, H, 51, stack=E)
+    dn = packed_random(dn_f, E * H, F, 52, stack=E)
+    sgu = packed_random(gu_f, 2 * F, H, 53)
+    sdn = packed_random(dn_f, H, F, 54)
+    cases = ((9, True, False), (16, True, True), (1, True, False), (9, False, True),
+             (9, True, True))
+    for M, shared, spread in cases if (gu_f, dn_f) == (4, 4) else cases[:2]:
+        print(f"gate_up_down E={E} F={F} fmt={gu_f}/{dn_f} M={M} shared={shared} "
+              f"spread={spread}", flush=True)
         g = torch.Generator(device="cuda").manual_seed(70 + M)
         x = torch.randn(M, H, device="cuda", generator=g).bfloat16()
         logits = torch.randn(M, E + 1, device="cuda", generator=g) * 2
@@ -95,11 +100,11 @@ def test_gate_up_down_equals_separate_launches(gpu, E, F):
             pairs = torch.zeros(M * K, H, device="cuda")
             sh_out = torch.zeros(M, H, device="cuda")
             if fused:
-                L.moe_gate_up_down(4, gu, dn, sg, sd, plan, ws, w, sw, act, pairs, sh_out, M, ns,
-                                   E, H, F)
+                L.moe_gate_up_down(gu_f | dn_f << 8, gu, dn, sg, sd, plan, ws, w, sw, act, pairs,
+                                   sh_out, M, ns, E, H, F)
             else:
-                L.moe_gate_up(4, gu, sg, plan, ws, act, M, ns, E, H, F)
-                L.moe_down(4, dn, sd, plan, act, w, sw, pairs, sh_out, ns, E, H, F)
+                L.moe_gate_up(gu_f, gu, sg, plan, ws, act, M, ns, E, H, F)
+                L.moe_down(dn_f, dn, sd, plan, act, w, sw, pairs, sh_out, ns, E, H, F)
             torch.cuda.synchronize()
             outs.append((act, pairs, sh_out))
         p = L.parse_plan(plan)
@@ -116,15 +121,16 @@ def _bf(x):
     return x.to(torch.bfloat16).double()
 
 
-@pytest.mark.parametrize("M", [9, 3])
-def test_experts_match_dequantized_reference(gpu, M):
+@pytest.mark.parametrize("M,gu_f,dn_f", [(9, 4, 4), (3, 4, 4), (9, 5, 5), (9, 6, 6), (9, 4, 6),
+                                          (3, 5, 6)])
+def test_experts_match_dequantized_reference(gpu, M, gu_f, dn_f):
     from snowllm_amd import layers as L, ops
     from snowllm_amd.verify import packed_random
-    print(f"moe experts M={M} H={H} F={F} E={E} top{K}", flush=True)
-    gu = packed_random(4, E * 2 * F, H, 11, keep_raw=True)
-    dn = packed_random(4, E * H, F, 12, keep_raw=True)
-    sgu = packed_random(4, 2 * F, H, 13, keep_raw=True)
-    sdn = packed_random(4, H, F, 14, keep_raw=True)
+    print(f"moe experts M={M} H={H} F={F} E={E} top{K} fmt={gu_f}/{dn_f}", flush=True)
+    gu = packed_random(gu_f, E * 2 * F, H, 11, keep_raw=True, stack=E)
+    dn = packed_random(dn_f, E * H, F, 12, keep_raw=True, stack=E)
+    sgu = packed_random(gu_f, 2 * F, H, 13, keep_raw=True)
+    sdn = packed_random(dn_f, H, F, 14, keep_raw=True)
     g = torch.Generator(device="cuda").manual_seed(20 + M)
     x = torch.randn(M, H, device="cuda", generator=g).bfloat16()
     logits = torch.randn(M, E + 1, device="cuda", generator=g) * 2
@@ -139,7 +145,8 @@ def test_experts_match_dequantized_reference(gpu, M):
     pairs = torch.empty(M * K, H, device="cuda")
     shared = torch.empty(M, H, device="cuda")
     out = torch.empty(M, H, dtype=torch.bfloat16, device="cuda")
-    L.moe_experts(4, gu, dn, sgu, sdn, plan, ws, w, sw, act, pairs, shared, out, M, K, E, H, F)
+    L.moe_experts(gu_f | dn_f << 8, gu, dn, sgu, sdn, plan, ws, w, sw, act, pairs, shared, out,
+                  M, K, E, H, F)
     torch.cuda.synchronize()
     # CPU reference over the touched experts
     xc = x.cpu().double()
@@ -159,11 +166,11 @@ def test_experts_match_dequantized_reference(gpu, M):
         for k in range(K):
             e = int(ids_c[r, k])
             if e not in cache:
-                cache[e] = (torch.from_numpy(Q.dequant(gub[e * gbytes:(e + 1) * gbytes], 4, 2 * F, H)).double(),
-                            torch.from_numpy(Q.dequant(dnb[e * dbytes:(e + 1) * dbytes], 4, H, F)).double())
+                cache[e] = (torch.from_numpy(Q.dequant(gub[e * gbytes:(e + 1) * gbytes], gu_f, 2 * F, H)).double(),
+                            torch.from_numpy(Q.dequant(dnb[e * dbytes:(e + 1) * dbytes], dn_f, H, F)).double())
             want[r] += w_c[r, k] * ffn(xc[r:r + 1], *cache[e])[0]
-    sg = torch.from_numpy(Q.dequant(sgu[2].cpu().numpy(), 4, 2 * F, H)).double()
-    sd = torch.from_numpy(Q.dequant(sdn[2].cpu().numpy(), 4, H, F)).double()
+    sg = torch.from_numpy(Q.dequant(sgu[2].cpu().numpy(), gu_f, 2 * F, H)).double()
+    sd = torch.from_numpy(Q.dequant(sdn[2].cpu().numpy(), dn_f, H, F)).double()
     want += sw_c[:, None] * ffn(xc, sg, sd)
     err = ((out.cpu().double() - want).norm() / want.norm()).item()
     print(f"  experts rel L2 {err:.2e} ({len(cache)} experts touched)", flush=True)

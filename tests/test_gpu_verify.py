@@ -30,6 +30,9 @@ def tiny(kind):
     if kind == "dense_q6k_q5k":   # Q6_K attention, Q5_K MLP (Q4_K_M's other k-quants)
         return VerifyConfig("tiny_dense_k56", ffn=512, attn_fmt=6, ffn_fmt=5,
                             **dict(base, kv_heads=1, rot_half=64))
+    if kind == "moe_q5k_q6k":     # Q5_K experts with Q6_K down (a Q5_K_M file's MoE layers)
+        return VerifyConfig("tiny_moe_k56", experts=16, expert_ffn=256, topk=4, ffn_fmt=5,
+                            down_fmt=6, **base)
     raise ValueError(kind)
 
 
@@ -38,7 +41,7 @@ def rel(a, b):
     return ((a - b).norm() / b.norm().clamp_min(1e-12)).item()
 
 
-@pytest.mark.parametrize("kind", ["dense", "moe", "tree", "dense_q6k_q5k"])
+@pytest.mark.parametrize("kind", ["dense", "moe", "tree", "dense_q6k_q5k", "moe_q5k_q6k"])
 def test_layers_and_head_match_cpu_reference(gpu, kind):
     from snowllm_amd.verify import VerifyModel, tree_masks, Acceptance
     cfg = tiny(kind)
