@@ -198,6 +198,15 @@ int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8
                                    int64_t M, int64_t N, int64_t K, int c_is_bf16,
                                    const void* ws, void* stream);
 
+/* Extension, no counterpart in the reference: snowverify_gemm_kquant_a_prepared writing row m
+ * of the result at c + m * ldc elements (N <= ldc < 2^31), so that weights of different
+ * formats fill the column ranges of one output: the Q|K and V rows of an attention projection
+ * whose GGUF tensors differ in format (snowllm_inference_qkv's split form). Same bits per
+ * element as the contiguous form. */
+int snowverify_gemm_kquant_a_prepared_ld(int fmt, const uint8_t* quant, const uint8_t* meta,
+                                         void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                         int c_is_bf16, const void* ws, void* stream);
+
 /* No counterpart in the reference: snowllm_gemm_kquant_a for callers that cannot allocate
  * (code under HIP-graph capture, tight serving loops, harnesses that forbid hipMalloc). It
  * allocates nothing and takes no workspace: up to 16 rows the GEMV converts the activations
@@ -306,7 +315,9 @@ typedef struct PagedAttentionStep {
 
 /* QKV projection with the input norm fused (snowllm/_capi.py:688; ops/inference.py:34-43):
  * out [M, qkv_proj_n] bf16 = RMSNorm(residual += x) * gamma . W^T (no residual: RMSNorm(x);
- * no gamma: x). w[3]: the QKV k-quant weight, then split V / KV (absent). */
+ * no gamma: x). w[3]: the QKV k-quant weight, then an optional split V (w[0] then holds the
+ * Q|K rows [qkv_off_v, hidden] and w[1] the V rows in its own format), then a bf16 KV (absent:
+ * hipErrorNotSupported). */
 int64_t snowllm_qkv_proj_scratch_bytes(int64_t M);                     /* _capi.py:251 */
 /* Sizing queries the reference's hot-path ops modules bind at import: the O projection's
  * scratch (snowllm/_capi.py:254; ops/attention_full.py:512); the draft model's attention

@@ -68,7 +68,13 @@ class LayerRef:
         self.k_norm = lw.k_norm.cpu().float()
         # a layer's own formats where they differ from the config's (0 or absent: the config's)
         own = lambda obj, name: getattr(obj, name, 0) or 0  # noqa: E731
-        self.qkv = dequant_raw(lw.qkv[2], own(lw, "qkv_fmt") or c.attn_fmt, c.qkv_n, H)
+        v = getattr(lw, "v", None)
+        if v is None:
+            self.qkv = dequant_raw(lw.qkv[2], own(lw, "qkv_fmt") or c.attn_fmt, c.qkv_n, H)
+        else:   # q|k rows, then the V rows in their own format
+            nqk = (c.heads + c.kv_heads) * c.head_dim
+            self.qkv = torch.cat([dequant_raw(lw.qkv[2], own(lw, "qkv_fmt") or c.attn_fmt, nqk, H),
+                                  dequant_raw(v[2], lw.v_fmt, c.qkv_n - nqk, H)])
         self.o = dequant_raw(lw.o[2], own(lw, "o_fmt") or c.attn_fmt, H, c.heads * c.head_dim)
         self.gu_fmt = own(lw, "gu_fmt") or c.ffn_fmt
         self.dn_fmt = own(lw, "dn_fmt") or own(c, "down_fmt") or c.ffn_fmt

@@ -94,6 +94,8 @@ _SIGS = [
     ("snowllm_gemm_kquant_a", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
     ("snowverify_gemm_kquant_prepare_a", c_int, [P, c_int64, c_int64, P, S]),
     ("snowverify_gemm_kquant_a_prepared", c_int, [c_int, P, P, P, c_int64, c_int64, c_int64, c_int, P, S]),
+    ("snowverify_gemm_kquant_a_prepared_ld", c_int,
+     [c_int, P, P, P, c_int64, c_int64, c_int64, c_int64, c_int, P, S]),
     ("snowverify_gemm_kquant_a_noalloc", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, c_int, S]),
     ("snowverify_gemv_variant", None, [c_int]),
     # paged attention

@@ -18,7 +18,8 @@ Follows the reference's GGUF path for the parts this build computes:
 Scope: every layer must be full GQA attention with QK-norm and no output gate, followed by a
 SwiGLU MLP or a routed MoE with a shared expert whose width equals the experts'; attention and
 dense matrices in Q4_K, Q5_K, Q6_K or Q8_0 (the formats the reference's GEMM takes, snowllm/
-checkpoint/gguf/source.py:263-272), with q/k/v in one format, gate/up in one and down in any;
+checkpoint/gguf/source.py:263-272), with q/k in one format and v in the same or another
+(qwen3_5_weights.py:95-109), gate/up in one and down in any;
 the experts' gate/up in Q4_K, Q5_K or Q6_K and their down in the same format or a wider one
 (Q4_K_M files store some layers' ffn_down_exps as Q6_K), the shared expert in the routed
 experts' formats. Formats may change from layer to layer.
@@ -170,15 +171,27 @@ def _layer(g: GGUF, cfg: VerifyConfig, i: int) -> LayerWeights:
             raise SnowLLMError(f"{g.path.name}: {p}ffn_down_exps.weight is narrower than the "
                                f"experts' gate/up; the MoE kernels take down in the gate/up "
                                f"format or a wider one")
-    raw, qkv_fmt = _blocks(g, [p + n for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight")])
-    qkv = ops.gemm_kquant_shuffle_b(qkv_fmt, raw, cfg.qkv_n, H)
+    names = [p + n for n in ("attn_q.weight", "attn_k.weight", "attn_v.weight")]
+    v = v_fmt = None
+    if len({_kfmt(g, n) for n in names}) == 1:
+        raw, qkv_fmt = _blocks(g, names)
+        qkv = ops.gemm_kquant_shuffle_b(qkv_fmt, raw, cfg.qkv_n, H)
+    else:
+        # q|k in one format and v in its own (qwen3_5_weights.py:95-109): two GEMVs into the
+        # columns of one projection output
+        nqk = (cfg.heads + cfg.kv_heads) * d
+        raw, qkv_fmt = _blocks(g, names[:2])
+        qkv = ops.gemm_kquant_shuffle_b(qkv_fmt, raw, nqk, H)
+        raw, v_fmt = _blocks(g, names[2:])
+        v = (*ops.gemm_kquant_shuffle_b(v_fmt, raw, cfg.qkv_n - nqk, H), None)
     raw, o_fmt = _blocks(g, [p + "attn_output.weight"])
     o = ops.gemm_kquant_shuffle_b(o_fmt, raw, H, q_rows)
     lw = LayerWeights(in_norm=_gamma(g, p + "attn_norm.weight"),
                       post_norm=_gamma(g, p + "post_attention_norm.weight"),
                       q_norm=_gamma(g, p + "attn_q_norm.weight"),
                       k_norm=_gamma(g, p + "attn_k_norm.weight"),
-                      qkv=(*qkv, None), o=(*o, None), qkv_fmt=qkv_fmt, o_fmt=o_fmt)
+                      qkv=(*qkv, None), o=(*o, None), qkv_fmt=qkv_fmt, o_fmt=o_fmt, v=v,
+                      v_fmt=v_fmt or 0)
     if cfg.moe:
         E, F = cfg.experts, cfg.expert_ffn
         if p + "ffn_gate_inp_shexp.weight" not in g:
@@ -270,8 +283,14 @@ def model_tensors(model: VerifyModel, *, tied: bool = False):
         qkv, qa = rows(lw.qkv[2], lw.qkv_fmt or cfg.attn_fmt, H)
         nq, nk = cfg.heads * d, cfg.kv_heads * d
         out += [(p + "attn_q.weight", (nq, H), qa, qkv[:nq]),
-                (p + "attn_k.weight", (nk, H), qa, qkv[nq:nq + nk]),
-                (p + "attn_v.weight", (nk, H), qa, qkv[nq + nk:])]
+                (p + "attn_k.weight", (nk, H), qa, qkv[nq:nq + nk])]
+        if lw.v is None:
+            out.append((p + "attn_v.weight", (nk, H), qa, qkv[nq + nk:]))
+        else:
+            if lw.v[2] is None:
+                raise SnowLLMError("model_tensors needs a model built with keep_raw=True")
+            vr, va = rows(lw.v[2], lw.v_fmt, H)
+            out.append((p + "attn_v.weight", (nk, H), va, vr))
         o, oa = rows(lw.o[2], lw.o_fmt or cfg.attn_fmt, nq)
         out.append((p + "attn_output.weight", (H, nq), oa, o))
         for n, t in (("attn_norm", lw.in_norm), ("post_attention_norm", lw.post_norm),

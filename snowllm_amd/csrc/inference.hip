@@ -68,6 +68,9 @@ int snowverify_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K, void* 
 int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta, void* c,
                                    int64_t M, int64_t N, int64_t K, int c_is_bf16,
                                    const void* ws, void* stream);
+int snowverify_gemm_kquant_a_prepared_ld(int fmt, const uint8_t* quant, const uint8_t* meta,
+                                         void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                         int c_is_bf16, const void* ws, void* stream);
 int snowverify_norm_prep(const void* x, const void* res_in, void* res_out, const void* gamma,
                          void* y_out, void* ws, int64_t M, int64_t H, float eps, void* stream);
 int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c, int64_t M, int64_t N,
@@ -220,26 +223,45 @@ SV_API int64_t snowllm_qkv_proj_scratch_bytes(int64_t M) {
 // snowllm/_capi.py:688 (ops/inference.py:34-43; QKVProj, models/qwen3_5/layers.py:33-50):
 // out [M, qkv_proj_n] bf16 = y W^T with y = RMSNorm(residual += x) * gamma when gamma is given
 // (y = RMSNorm(x) * gamma without a residual; y = x without gamma). w[0]: the QKV k-quant
-// weight; w[1], w[2] (split V / KV) must be absent, as must the indexer.
+// weight, or with w[1] present the Q|K rows [qkv_off_v, hidden] and w[1] the V rows
+// [kv heads * head size, hidden] in their own format (the split of
+// models/qwen3_5/qwen3_5_weights.py:95-109: GGUF files keep attn_v wider than attn_q/attn_k);
+// w[2] (a bf16 KV) and the indexer are not carried (hipErrorNotSupported).
 SV_API int snowllm_inference_qkv(const Weight* w, const void* x, void* residual,
                                  const void* gamma, float eps, void* scratch, void* out,
                                  int64_t M, int path, const void* index_w, void* index_out,
                                  void* stream) {
   (void)path;  // the reference's execution-path hint; one path here
   const BuildGeometry& g = active_geometry();
-  if (!w || !kquant(&w[0]) || !absent(&w[1]) || !absent(&w[2]) || index_w || index_out)
+  if (!w || !kquant(&w[0]) || !absent(&w[2]) || index_w || index_out) return SV_ENOTSUP;
+  const bool split = !absent(&w[1]);
+  if (split && (!kquant(&w[1]) || g.qkv_off_v + g.num_kv_heads * g.head_size != g.qkv_proj_n))
     return SV_ENOTSUP;
   if (M <= 0 || !x || !out || !scratch) return SV_EINVAL;
   const auto* q = (const uint8_t*)w[0].data[0];
   const auto* m = (const uint8_t*)w[0].data[1];
-  if (!gamma)
-    return snowllm_gemm_kquant_a(w[0].fmt, x, q, m, out, M, g.qkv_proj_n, g.hidden, 1, scratch,
-                                 stream);
-  int rc = snowverify_norm_prep(x, residual, residual, gamma, nullptr, scratch, M, g.hidden, eps,
-                                stream);
+  if (!split) {
+    if (!gamma)
+      return snowllm_gemm_kquant_a(w[0].fmt, x, q, m, out, M, g.qkv_proj_n, g.hidden, 1,
+                                   scratch, stream);
+    int rc = snowverify_norm_prep(x, residual, residual, gamma, nullptr, scratch, M, g.hidden,
+                                  eps, stream);
+    if (rc) return rc;
+    return snowverify_gemm_kquant_a_prepared(w[0].fmt, q, m, out, M, g.qkv_proj_n, g.hidden, 1,
+                                          scratch, stream);
+  }
+  // split: the operands once, then Q|K and V into their columns of out
+  int rc = gamma ? snowverify_norm_prep(x, residual, residual, gamma, nullptr, scratch, M,
+                                        g.hidden, eps, stream)
+                 : snowverify_gemm_kquant_prepare_a(x, M, g.hidden, scratch, stream);
   if (rc) return rc;
-  return snowverify_gemm_kquant_a_prepared(w[0].fmt, q, m, out, M, g.qkv_proj_n, g.hidden, 1,
-                                        scratch, stream);
+  rc = snowverify_gemm_kquant_a_prepared_ld(w[0].fmt, q, m, out, g.qkv_proj_n, M, g.qkv_off_v,
+                                            g.hidden, 1, scratch, stream);
+  if (rc) return rc;
+  return snowverify_gemm_kquant_a_prepared_ld(
+      w[1].fmt, (const uint8_t*)w[1].data[0], (const uint8_t*)w[1].data[1],
+      (uint16_t*)out + g.qkv_off_v, g.qkv_proj_n, M, g.qkv_proj_n - g.qkv_off_v, g.hidden, 1,
+      scratch, stream);
 }
 
 // snowllm/_capi.py:254 (bound at import by ops/attention_full.py:512): scratch of the output

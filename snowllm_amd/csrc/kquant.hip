@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv(const u32x4* __restrict__
                                                        const u32x4* __restrict__ meta,
                                                        const void* __restrict__ ws,
                                                        void* __restrict__ c, int M, int N, int S,
-                                                       int c_bf16) {
+                                                       int c_bf16, int ldc) {
   __shared__ floatx4 part[NW][NTILE][64];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -80,8 +80,8 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv(const u32x4* __restrict__
     for (int i = 0; i < 4; ++i) {
       const int row = rb + i;
       if (row >= M) break;
-      if (c_bf16) ((uint16_t*)c)[(int64_t)row * N + n] = f32_to_bf16(v[i]);
-      else ((float*)c)[(int64_t)row * N + n] = v[i];
+      if (c_bf16) ((uint16_t*)c)[(int64_t)row * ldc + n] = f32_to_bf16(v[i]);
+      else ((float*)c)[(int64_t)row * ldc + n] = v[i];
     }
   }
 }
@@ -166,7 +166,8 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
                                                           const u32x4* __restrict__ meta,
                                                           const void* __restrict__ ws,
                                                           void* __restrict__ c, int M, int N,
-                                                          int S, int c_bf16, size_t tile_bytes) {
+                                                          int S, int c_bf16, size_t tile_bytes,
+                                                          int ldc) {
   constexpr int QV = QLayout<FMT>::kQuantVecs;
   __shared__ floatx4 part[NW][1][64];
   const int lane = threadIdx.x & 63;
@@ -236,8 +237,8 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
       for (int i = 0; i < 4; ++i) {
         const int row = rb + i;
         if (row >= M) break;
-        if (c_bf16) ((uint16_t*)c)[(int64_t)row * N + n] = f32_to_bf16(v[i]);
-        else ((float*)c)[(int64_t)row * N + n] = v[i];
+        if (c_bf16) ((uint16_t*)c)[(int64_t)row * ldc + n] = f32_to_bf16(v[i]);
+        else ((float*)c)[(int64_t)row * ldc + n] = v[i];
       }
     }
   }
@@ -245,13 +246,13 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
 
 template <int FMT, int NW>
 int launch_gemv_mt(const void* quant, const void* meta, const void* ws, void* c, int M, int N,
-                   int S, int c_bf16, hipStream_t s) {
+                   int S, int c_bf16, int ldc, hipStream_t s) {
   const int tiles = N / TILE_N;
   const int row_tiles = (M + TILE_M - 1) / TILE_M;
   const size_t tb = xprep_tile_bytes(S);
   auto go = [&](auto kern, int mt) {
     hipLaunchKernelGGL(kern, dim3(tiles, (row_tiles + mt - 1) / mt), dim3(NW * 64), 0, s,
-                       (const u32x4*)quant, (const u32x4*)meta, ws, c, M, N, S, c_bf16, tb);
+                       (const u32x4*)quant, (const u32x4*)meta, ws, c, M, N, S, c_bf16, tb, ldc);
   };
   if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2>, 2);
   else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3>, 3);
@@ -401,11 +402,11 @@ bool weight_fits(int fmt, int64_t N, int64_t K) {
 
 template <int FMT, int NTILE, int NW, bool RAW = false>
 int launch_gemv(const void* quant, const void* meta, const void* ws, void* c, int M, int N, int S,
-                int c_bf16, hipStream_t s) {
+                int c_bf16, int ldc, hipStream_t s) {
   const int tiles = N / TILE_N;
   const int grid = (tiles + NTILE - 1) / NTILE;
   hipLaunchKernelGGL((kquant_gemv<FMT, NTILE, NW, RAW>), dim3(grid), dim3(NW * 64), 0, s,
-                     (const u32x4*)quant, (const u32x4*)meta, ws, c, M, N, S, c_bf16);
+                     (const u32x4*)quant, (const u32x4*)meta, ws, c, M, N, S, c_bf16, ldc);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -426,14 +427,14 @@ int by_format(int fmt, F&& f) {
 
 template <int FMT, bool RAW = false>
 int dispatch_gemv(const void* quant, const void* meta, const void* ws, void* c, int M, int N,
-                  int S, int c_bf16, hipStream_t s) {
+                  int S, int c_bf16, int ldc, hipStream_t s) {
   switch (g_gemv_variant) {
-    case 1: return launch_gemv<FMT, 1, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 2: return launch_gemv<FMT, 2, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 3: return launch_gemv<FMT, 4, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 4: return launch_gemv<FMT, 1, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 5: return launch_gemv<FMT, 2, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    case 6: return launch_gemv<FMT, 4, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+    case 1: return launch_gemv<FMT, 1, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
+    case 2: return launch_gemv<FMT, 2, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
+    case 3: return launch_gemv<FMT, 4, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
+    case 4: return launch_gemv<FMT, 1, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
+    case 5: return launch_gemv<FMT, 2, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
+    case 6: return launch_gemv<FMT, 4, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
     default: break;
   }
   const int tiles = N / TILE_N;
@@ -443,14 +444,14 @@ int dispatch_gemv(const void* quant, const void* meta, const void* ws, void* c, 
   if (S >= 8) {
     // (Q8_0 keeps two tiles: four tiles of int8 quants exceed the register file)
     if (tiles >= 4 * 192 && FMT == FMT_Q4_K)
-      return launch_gemv<FMT, 4, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    if (tiles >= 2 * 128 && S <= 8) return launch_gemv<FMT, 2, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+      return launch_gemv<FMT, 4, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
+    if (tiles >= 2 * 128 && S <= 8) return launch_gemv<FMT, 2, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
     if (!RAW && FMT == FMT_Q4_K && tiles >= 3 * 128 && S <= 16)
-      return launch_gemv<FMT, 2, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
-    return launch_gemv<FMT, 1, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+      return launch_gemv<FMT, 2, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
+    return launch_gemv<FMT, 1, 8, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
   }
-  if (tiles >= 2 * 256) return launch_gemv<FMT, 2, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
-  return launch_gemv<FMT, 1, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, s);
+  if (tiles >= 2 * 256) return launch_gemv<FMT, 2, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
+  return launch_gemv<FMT, 1, 4, RAW>(quant, meta, ws, c, M, N, S, c_bf16, ldc, s);
 }
 
 }  // namespace
@@ -542,11 +543,16 @@ SV_API int snowverify_gemm_kquant_prepare_a(const void* a, int64_t M, int64_t K,
   return SV_OK;
 }
 
-// Extension (no counterpart in the reference): the GEMV on a prepared operand workspace.
-SV_API int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta,
-                                          void* c, int64_t M, int64_t N, int64_t K,
-                                          int c_is_bf16, const void* ws, void* stream) {
-  if (!fmt_ok(fmt) || M < 0 || N <= 0 || K <= 0 || K % 256 || N % TILE_N) return SV_EINVAL;
+// Extension (no counterpart in the reference): the GEMV on a prepared operand workspace,
+// writing row m of the result at c + m * ldc (ldc >= N elements), so that two weights of
+// different formats fill the column ranges of one output (Q|K and V of a fused projection).
+SV_API int snowverify_gemm_kquant_a_prepared_ld(int fmt, const uint8_t* quant,
+                                                const uint8_t* meta, void* c, int64_t ldc,
+                                                int64_t M, int64_t N, int64_t K, int c_is_bf16,
+                                                const void* ws, void* stream) {
+  if (!fmt_ok(fmt) || M < 0 || N <= 0 || K <= 0 || K % 256 || N % TILE_N || ldc < N ||
+      ldc > INT32_MAX)
+    return SV_EINVAL;
   if (!weight_fits(fmt, N, K)) return SV_ENOTSUP;
   if (M == 0) return SV_OK;
   hipStream_t s = (hipStream_t)stream;
@@ -554,26 +560,35 @@ SV_API int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, cons
   const size_t tb = xprep_tile_bytes(S);
   const int64_t mt = (M + TILE_M - 1) / TILE_M;
   const size_t esz = c_is_bf16 ? 2 : 4;
+  const int ld = (int)ldc;
   if (mt > 1 && g_gemv_variant == 0 && (fmt == FMT_Q4_K || fmt == FMT_Q8_0)) {
     // wider than one row tile: every weight tile decoded once for up to four row tiles (the
     // waves split the superblocks as the automatic 16-row launch does: the same bits)
     if (fmt == FMT_Q4_K)
-      return S >= 8 ? launch_gemv_mt<FMT_Q4_K, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, s)
-                    : launch_gemv_mt<FMT_Q4_K, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, s);
-    return S >= 8 ? launch_gemv_mt<FMT_Q8_0, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, s)
-                  : launch_gemv_mt<FMT_Q8_0, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, s);
+      return S >= 8 ? launch_gemv_mt<FMT_Q4_K, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s)
+                    : launch_gemv_mt<FMT_Q4_K, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s);
+    return S >= 8 ? launch_gemv_mt<FMT_Q8_0, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s)
+                  : launch_gemv_mt<FMT_Q8_0, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s);
   }
   for (int64_t t = 0; t < mt; ++t) {
     const int rows = (int)((M - t * TILE_M) < TILE_M ? (M - t * TILE_M) : TILE_M);
-    void* ct = (char*)c + (size_t)t * TILE_M * N * esz;
+    void* ct = (char*)c + (size_t)t * TILE_M * ldc * esz;
     const void* wst = (const char*)ws + t * tb;
     int rc = by_format(fmt, [&](auto F) {
       return dispatch_gemv<decltype(F)::value>(quant, meta, wst, ct, rows, (int)N, (int)S,
-                                               c_is_bf16, s);
+                                               c_is_bf16, ld, s);
     });
     if (rc) return rc;
   }
   return SV_OK;
+}
+
+// Extension (no counterpart in the reference): the GEMV on a prepared operand workspace.
+SV_API int snowverify_gemm_kquant_a_prepared(int fmt, const uint8_t* quant, const uint8_t* meta,
+                                          void* c, int64_t M, int64_t N, int64_t K,
+                                          int c_is_bf16, const void* ws, void* stream) {
+  return snowverify_gemm_kquant_a_prepared_ld(fmt, quant, meta, c, N, M, N, K, c_is_bf16, ws,
+                                              stream);
 }
 
 SV_API int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, const uint8_t* meta,
@@ -588,7 +603,7 @@ SV_API int snowllm_gemm_kquant_a(int fmt, const void* a, const uint8_t* quant, c
     hipStream_t s = (hipStream_t)stream;
     return by_format(fmt, [&](auto F) {
       return dispatch_gemv<decltype(F)::value, true>(quant, meta, a, c, (int)M, (int)N,
-                                                     (int)(K / 256), c_is_bf16, s);
+                                                     (int)(K / 256), c_is_bf16, (int)N, s);
     });
   }
   int rc = snowverify_gemm_kquant_prepare_a(a, M, K, ws, stream);

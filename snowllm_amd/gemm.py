@@ -87,13 +87,24 @@ def gemm_kquant_prepare_a(a: torch.Tensor, ws: torch.Tensor) -> None:
 
 
 def gemm_kquant_a_prepared(fmt: int, quant: torch.Tensor, meta: torch.Tensor, c: torch.Tensor,
-                           M: int, N: int, K: int, ws: torch.Tensor) -> None:
-    """gemm_kquant_a on a workspace filled by gemm_kquant_prepare_a (extension)."""
+                           M: int, N: int, K: int, ws: torch.Tensor, col: int = None) -> None:
+    """gemm_kquant_a on a workspace filled by gemm_kquant_prepare_a (extension). col: write
+    columns [col, col + N) of a wider c [M, ldc] (snowverify_gemm_kquant_a_prepared_ld)."""
     _chk(ws, "ws", torch.uint8, gemm_kquant_a_ws_bytes(M, K))
     bf16 = c.dtype is torch.bfloat16
-    _chk(c, "c", torch.bfloat16 if bf16 else torch.float32, M, N)
-    check(lib.snowverify_gemm_kquant_a_prepared(fmt, _p(quant), _p(meta), _p(c), M, N, K, bf16, _p(ws),
-                                             _stream()), "gemm_kquant_a_prepared")
+    if col is None:
+        _chk(c, "c", torch.bfloat16 if bf16 else torch.float32, M, N)
+        check(lib.snowverify_gemm_kquant_a_prepared(fmt, _p(quant), _p(meta), _p(c), M, N, K, bf16,
+                                                 _p(ws), _stream()), "gemm_kquant_a_prepared")
+        return
+    ldc = c.shape[-1] if c.dim() == 2 else -1
+    _chk(c, "c", torch.bfloat16 if bf16 else torch.float32, M, ldc)
+    if col < 0 or col + N > ldc:
+        raise SnowLLMError(f"gemm_kquant_a_prepared: columns [{col}, {col + N}) outside c's {ldc}")
+    check(lib.snowverify_gemm_kquant_a_prepared_ld(fmt, _p(quant), _p(meta),
+                                                   _p(c) + col * c.element_size(), ldc, M, N, K,
+                                                   bf16, _p(ws), _stream()),
+          "gemm_kquant_a_prepared")
 
 
 GEMM_NOALLOC_MAX_M, GEMM_NOALLOC_MAX_K = 64, 16384

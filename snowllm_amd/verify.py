@@ -53,6 +53,7 @@ class VerifyConfig:
     attn_fmt: int = Q4_K
     ffn_fmt: int = Q4_K
     down_fmt: int = 0        # format of the down projections when it differs (0: ffn_fmt)
+    v_fmt: int = 0           # V rows in their own format, q|k in attn_fmt (0: one q|k|v weight)
     tree_parents: tuple = ()  # non-empty: tree block (ancestor mask) instead of a chain
     eps: float = 1e-6
     page: int = 16
@@ -212,6 +213,10 @@ class LayerWeights:
     o_fmt: int = 0
     gu_fmt: int = 0
     dn_fmt: int = 0
+    # V rows of the attention projection in their own format (then qkv holds the q|k rows):
+    # GGUF files keep attn_v wider than attn_q / attn_k in some layers
+    v: tuple = None
+    v_fmt: int = 0
 
 
 class VerifyModel:
@@ -298,9 +303,13 @@ class VerifyModel:
             def pk(fmt, n, k, j, stack=1):
                 return packed_random(fmt, n, k, sub(i, j), kr, c.centered, stack)
 
+            nqk = (c.heads + c.kv_heads) * c.head_dim
             lw = LayerWeights(in_norm=gamma(H), post_norm=gamma(H), q_norm=gamma(c.head_dim),
-                              k_norm=gamma(c.head_dim), qkv=pk(c.attn_fmt, c.qkv_n, H, 0),
+                              k_norm=gamma(c.head_dim),
+                              qkv=pk(c.attn_fmt, nqk if c.v_fmt else c.qkv_n, H, 0),
                               o=pk(c.attn_fmt, H, c.heads * c.head_dim, 1))
+            if c.v_fmt:
+                lw.v, lw.v_fmt = pk(c.v_fmt, c.qkv_n - nqk, H, 6), c.v_fmt
             if c.moe:
                 E, F = c.experts, c.expert_ffn
                 router = (torch.randn(E + 1, H, device=dev, generator=gen) / math.sqrt(H)).bfloat16()
@@ -461,8 +470,15 @@ class VerifyModel:
             lw = self.layers[i]
             # attention block
             norm(lw.in_norm, self.ws_h)
-            ops.gemm_kquant_a_prepared(lw.qkv_fmt or c.attn_fmt, lw.qkv[0], lw.qkv[1], self.proj,
-                                       T, c.qkv_n, H, self.ws_h)
+            if lw.v is None:
+                ops.gemm_kquant_a_prepared(lw.qkv_fmt or c.attn_fmt, lw.qkv[0], lw.qkv[1],
+                                           self.proj, T, c.qkv_n, H, self.ws_h)
+            else:   # q|k and v in their formats, into their columns of proj
+                nqk = (c.heads + c.kv_heads) * c.head_dim
+                ops.gemm_kquant_a_prepared(lw.qkv_fmt or c.attn_fmt, lw.qkv[0], lw.qkv[1],
+                                           self.proj, T, nqk, H, self.ws_h, col=0)
+                ops.gemm_kquant_a_prepared(lw.v_fmt, lw.v[0], lw.v[1], self.proj, T,
+                                           c.qkv_n - nqk, H, self.ws_h, col=nqk)
             if c.rot_half <= ops.FUSED_QK_MAX_HALF:
                 # QK-norm + RoPE + the block's K/V cache write inside the attention's launches
                 # with 256-wide heads the merge also writes the O projection's operands

@@ -30,12 +30,15 @@ def geometry_of():
     ops.select_geometry(0)
 
 
-def test_reference_dataflow_layer_matches_verify_model(gpu, geometry_of):
+# v_fmt 6: q|k Q4_K and v Q6_K, the split projection (qwen3_5_weights.py:95-109)
+@pytest.mark.parametrize("v_fmt", [0, 6])
+def test_reference_dataflow_layer_matches_verify_model(gpu, geometry_of, v_fmt):
+    from dataclasses import replace
     from snowllm_amd import ops
     from snowllm_amd.verify import VerifyModel
-    cfg = tiny("moe")
+    cfg = replace(tiny("moe"), v_fmt=v_fmt)
     geometry_of(cfg)
-    print("reference-signature layer, tiny moe", flush=True)
+    print(f"reference-signature layer, tiny moe, v format {v_fmt or cfg.attn_fmt}", flush=True)
     m = VerifyModel(cfg, seed=8)
     T, H, d = cfg.block, cfg.hidden, cfg.head_dim
     m.set_block(torch.arange(T) * 11)
@@ -50,7 +53,8 @@ def test_reference_dataflow_layer_matches_verify_model(gpu, geometry_of):
     proj = torch.empty(T, cfg.qkv_n, dtype=bf, device="cuda")
     scratch = torch.empty(ops.qkv_proj_scratch_bytes(T), dtype=torch.uint8, device="cuda")
     w_qkv = ops.KQuantProjWeight(lw.qkv[0], lw.qkv[1], cfg.attn_fmt)
-    ops.inference_qkv(residual, w_qkv, None, None, None, scratch, proj, 0, None, lw.in_norm,
+    w_v = ops.KQuantProjWeight(lw.v[0], lw.v[1], lw.v_fmt) if v_fmt else None
+    ops.inference_qkv(residual, w_qkv, None, w_v, None, scratch, proj, 0, None, lw.in_norm,
                       cfg.eps)
     cos = torch.empty(T, 64, device="cuda")
     sin = torch.empty_like(cos)

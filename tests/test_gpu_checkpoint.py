@@ -50,6 +50,9 @@ CASES = [
     ("moe", {"down_fmt": 6}, 1),
     ("moe", {"attn_fmt": 5, "ffn_fmt": 5, "down_fmt": 6}, 2),
     ("moe", {"attn_fmt": 6, "ffn_fmt": 6}, 1),
+    # attn_v wider than attn_q / attn_k: the split projection
+    ("moe", {"v_fmt": 6, "down_fmt": 6}, 1),
+    ("dense", {"attn_fmt": 8, "v_fmt": 5}, 1),
 ]
 
 
@@ -70,6 +73,8 @@ def test_gguf_model_matches_its_source(gpu, tmp_path, default_geometry, kind, ov
                                 cfg.ffn_fmt)
     for i, (a, b) in enumerate(zip(m.layers, lm.layers)):
         names = ["qkv", "o", "gu", "dn"] + (["sh_gu", "sh_dn"] if cfg.moe else [])
+        assert (a.v is None) == (b.v is None) and a.v_fmt == b.v_fmt, i
+        names += ["v"] if a.v is not None else []
         for n in names:
             wa, wb = getattr(a, n), getattr(b, n)
             # the last 4 quant bytes are read slack, never written

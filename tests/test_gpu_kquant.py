@@ -177,3 +177,30 @@ def test_q5k_q6k_config2_shape_and_forms(gpu, fmt):
         finally:
             _capi.lib.snowverify_gemv_variant(0)
         assert Q.rel_l2(c2.cpu().numpy(), want) < TOL, v
+
+
+@pytest.mark.parametrize("m", [9, 40])   # one row tile; the wide-block form (three tiles)
+def test_strided_gemv_fills_columns(gpu, m):
+    """snowverify_gemm_kquant_a_prepared_ld: a Q4_K q|k weight and a Q6_K v weight fill their
+    column ranges of one [M, N1 + N2] output with the bits of the contiguous launches, and the
+    columns around them stay untouched."""
+    from snowllm_amd import ops
+    k, n1, n2 = 2048, 1536, 256
+    raws = (Q.make(4, n1, k, seed=31), Q.make(6, n2, k, seed=32))
+    packs = [ops.gemm_kquant_shuffle_b(f, torch.from_numpy(r).cuda(), n, k)
+             for f, r, n in ((4, raws[0], n1), (6, raws[1], n2))]
+    x = Q.make_activations(m, k, seed=m).cuda()
+    ws = torch.empty(ops.gemm_kquant_a_ws_bytes(m, k), dtype=torch.uint8, device="cuda")
+    ops.gemm_kquant_prepare_a(x, ws)
+    for dtype in (torch.bfloat16, torch.float32):
+        print(f"strided gemv M={m} {dtype}", flush=True)
+        out = torch.full((m, n1 + n2 + 16), 7.0, dtype=dtype, device="cuda")
+        ops.gemm_kquant_a_prepared(4, *packs[0], out, m, n1, k, ws, col=0)
+        ops.gemm_kquant_a_prepared(6, *packs[1], out, m, n2, k, ws, col=n1 + 16)
+        a = torch.empty(m, n1, dtype=dtype, device="cuda")
+        b = torch.empty(m, n2, dtype=dtype, device="cuda")
+        ops.gemm_kquant_a_prepared(4, *packs[0], a, m, n1, k, ws)
+        ops.gemm_kquant_a_prepared(6, *packs[1], b, m, n2, k, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out[:, :n1], a) and torch.equal(out[:, n1 + 16:], b)
+        assert bool((out[:, n1:n1 + 16] == 7.0).all())

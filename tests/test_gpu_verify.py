@@ -30,9 +30,9 @@ def tiny(kind):
     if kind == "dense_q6k_q5k":   # Q6_K attention, Q5_K MLP (Q4_K_M's other k-quants)
         return VerifyConfig("tiny_dense_k56", ffn=512, attn_fmt=6, ffn_fmt=5,
                             **dict(base, kv_heads=1, rot_half=64))
-    if kind == "moe_q5k_q6k":     # Q5_K experts with Q6_K down (a Q5_K_M file's MoE layers)
+    if kind == "moe_q5k_q6k":     # Q5_K experts with Q6_K down and Q6_K attn_v (a Q5_K_M
         return VerifyConfig("tiny_moe_k56", experts=16, expert_ffn=256, topk=4, ffn_fmt=5,
-                            down_fmt=6, **base)
+                            down_fmt=6, v_fmt=6, **base)   # file's MoE layers)
     raise ValueError(kind)
 
 
