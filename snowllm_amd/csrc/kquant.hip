@@ -195,7 +195,9 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
   for (int m = 0; m < MT; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
   for (int s = w; s < S; s += NW) {
     u32x4 q[1][QV], mt4[1];
+    uint32_t dq[1] = {0u};
     load_sb_w<FMT, 1>(q, mt4, st, s, S, tile, 1);
+    if constexpr (FMT == FMT_Q6_K) load_sb_d<1>(dq, st, s, S, tile, 1);
     // every row tile's operands of this superblock in flight with the weights
     u32x4 x[MT][8];
     float sx0[MT], sx1[MT];
@@ -209,16 +211,30 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
       sx1[m] = bload1(sxr[m], lane * 4, (uint32_t)((s * 2 + 1) * 64 * 4));
       sc[m] = __builtin_bit_cast(floatx4, bload4(scr[m], kq * 16, (uint32_t)(s * 16 * 4)));
     }
-    DecodedSb<FMT> d;
-    decode_sb<FMT>(q[0], mt4[0], kq, Mv, d);
+    if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q8_0) {
+      DecodedSb<FMT> d;
+      decode_sb<FMT>(q[0], mt4[0], kq, Mv, d);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (m >= mt) break;  // uniform
-      half8 xa[8];
+      for (int m = 0; m < MT; ++m) {
+        if (m >= mt) break;  // uniform
+        half8 xa[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x[m][j]);
-      const floatx4 sb = apply_sb<FMT>(d, xa, sx0[m], sx1[m]);
-      acc[m] += sb * sc[m];
+        for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x[m][j]);
+        const floatx4 sb = apply_sb<FMT>(d, xa, sx0[m], sx1[m]);
+        acc[m] += sb * sc[m];
+      }
+    } else {
+      // Q5_K / Q6_K: the weights loaded once, decoded again for each row tile by the 16-row
+      // kernel's own routine (their decoded operands do not fit the registers of four tiles)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m >= mt) break;  // uniform
+        half8 xa[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x[m][j]);
+        const floatx4 sb = tile_superblock<FMT>(q[0], mt4[0], dq[0], xa, sx0[m], sx1[m], kq, Mv);
+        acc[m] += sb * sc[m];
+      }
     }
   }
 #pragma unroll
@@ -254,9 +270,13 @@ int launch_gemv_mt(const void* quant, const void* meta, const void* ws, void* c,
     hipLaunchKernelGGL(kern, dim3(tiles, (row_tiles + mt - 1) / mt), dim3(NW * 64), 0, s,
                        (const u32x4*)quant, (const u32x4*)meta, ws, c, M, N, S, c_bf16, tb, ldc);
   };
-  if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2>, 2);
-  else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3>, 3);
-  else go(kquant_gemv_mt<FMT, NW, 4>, 4);
+  if constexpr (FMT == FMT_Q6_K) {
+    go(kquant_gemv_mt<FMT, NW, 2>, 2);  // Q6_K's three tiles of operands spill the registers
+  } else {
+    if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2>, 2);
+    else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3>, 3);
+    else go(kquant_gemv_mt<FMT, NW, 4>, 4);
+  }
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -561,14 +581,14 @@ SV_API int snowverify_gemm_kquant_a_prepared_ld(int fmt, const uint8_t* quant,
   const int64_t mt = (M + TILE_M - 1) / TILE_M;
   const size_t esz = c_is_bf16 ? 2 : 4;
   const int ld = (int)ldc;
-  if (mt > 1 && g_gemv_variant == 0 && (fmt == FMT_Q4_K || fmt == FMT_Q8_0)) {
-    // wider than one row tile: every weight tile decoded once for up to four row tiles (the
+  if (mt > 1 && g_gemv_variant == 0) {
+    // wider than one row tile: every weight tile loaded once for up to four row tiles (the
     // waves split the superblocks as the automatic 16-row launch does: the same bits)
-    if (fmt == FMT_Q4_K)
-      return S >= 8 ? launch_gemv_mt<FMT_Q4_K, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s)
-                    : launch_gemv_mt<FMT_Q4_K, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s);
-    return S >= 8 ? launch_gemv_mt<FMT_Q8_0, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s)
-                  : launch_gemv_mt<FMT_Q8_0, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s);
+    return by_format(fmt, [&](auto F) {
+      constexpr int FM = decltype(F)::value;
+      return S >= 8 ? launch_gemv_mt<FM, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s)
+                    : launch_gemv_mt<FM, 4>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s);
+    });
   }
   for (int64_t t = 0; t < mt; ++t) {
     const int rows = (int)((M - t * TILE_M) < TILE_M ? (M - t * TILE_M) : TILE_M);

@@ -118,14 +118,14 @@ def test_every_gemv_variant(gpu, fmt):
             lib.snowverify_gemv_variant(0)
 
 
-@pytest.mark.parametrize("fmt", [4, 8])
+@pytest.mark.parametrize("fmt", [4, 5, 6, 8])
 @pytest.mark.parametrize("n,k", [(5120, 2048), (512, 4096), (256, 1024)])
 def test_wide_block_gemv_equals_row_tiles(gpu, fmt, n, k):
     """Verify steps wider than 16 rows (B x T <= 256): one launch decodes each weight tile once
     for up to four row tiles; every row gets the bits of the 16-row launch, and the result
     stays within the fp64 oracle's tolerance."""
     from snowllm_amd import ops
-    raw = Q.make_q4_k(n, k, seed=n + 3) if fmt == 4 else Q.make_q8_0(n, k, seed=n + 3)
+    raw = Q.make(fmt, n, k, seed=n + 3)
     quant, meta = ops.gemm_kquant_shuffle_b(fmt, torch.from_numpy(raw).cuda(), n, k)
     w = Q.dequant(raw, fmt, n, k)
     tb = ops.gemm_kquant_a_ws_bytes(16, k)
