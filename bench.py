@@ -305,8 +305,8 @@ def step_bytes(cfg, slots, selector=False, batch=1):
     (the touched experts only), the KV cache of the context plus the block's new rows of every
     request, the LM head, the logits/probabilities of the acceptance, and (with the selector)
     the draft logits plus the codebook rows the selector gathers (16 candidates and 16
-    previous tokens per position). slots[i]: expert slots layer i reads (unique experts +
-    shared, per 16-row chunk)."""
+    previous tokens per position). slots[i]: the experts layer i must read (the unique
+    experts the step's rows touch + the shared expert)."""
     H, T, V = cfg.hidden, cfg.block, cfg.vocab
     wb = q4k_bytes if cfg.attn_fmt == 4 else q80_bytes
     attn_w = wb(cfg.qkv_n, H) + wb(H, cfg.heads * cfg.head_dim)
@@ -443,15 +443,15 @@ def bench_step(args, name):
         m.attn_scratch, tree=m.tree), B * (c.context + T) * c.kv_heads * c.head_dim * 4)
     if cfg.moe:
         F = c.expert_ffn
-        # the expert gate/up and down GEMVs: one launch (moe_experts_kernel) per 16-row chunk;
-        # timed on the first chunk with the plan the last layer left for it
+        # the expert gate/up and down GEMVs: one launch (moe_experts_kernel) per plan of up to
+        # 64 rows; timed on the first plan as the last layer left it
         n0 = m.moe_chunks[0][1]
         plan0 = m.plans[0]
         slots0 = int(plan0[:4].view(torch.int32).item())
         per_launch("moe_experts", lambda i: Lops.moe_gate_up_down(
             c.ffn_fmt, Lw[i].gu, Lw[i].dn, Lw[i].sh_gu, Lw[i].sh_dn, plan0, m.ws_h2,
             m.route_w[:n0], m.shared_w[:n0], m.moe_act, m.pairs[:n0 * c.topk], m.shared_out[:n0],
-            n0, n0 * c.topk + 1, c.experts, H, F),
+            n0, m.moe_slots[0], c.experts, H, F),
             slots0 * (q4k_bytes(2 * F, H) + q4k_bytes(H, F)))
     else:
         n0 = m.row_chunks[0][1]

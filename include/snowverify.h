@@ -386,7 +386,8 @@ int64_t snowllm_kv_block_sizes(int64_t* out, int64_t n);
 /* MoE block (snowllm/_capi.py:315, 690-691, 805-807; ops/inference.py:54-95): w[4] = experts'
  * gate/up stack, experts' down stack, shared gate/up, shared down; router: repacked bf16
  * [E+1, hidden], the shared expert's gate last. The _norm form first sets residual += x and
- * hidden_row = RMSNorm(residual) * gamma. x and out may alias. M <= 16. */
+ * hidden_row = RMSNorm(residual) * gamma. x and out may alias. M <= 64 (the workspace query
+ * returns 0 above). */
 int64_t snowllm_moe_workspace_bytes(int64_t rows);
 int64_t snowllm_inference_moe_workspace_bytes(int64_t rows, int64_t flags);
 int snowllm_inference_moe(const SnowllmWeight* w, const void* x, const void* router,
@@ -578,7 +579,7 @@ int snowverify_norm_prep_moe(const float* pairs, const float* shared_out, int64_
  * repacked by snowverify_dense_shuffle; f32 logits [M, E (+1)]) + snowverify_moe_route_plan
  * (weights/ids [M, topk], shared_w [M] or NULL for no shared expert, plan). res_out must not
  * alias x or res_in. M <= 16; H a multiple of 512, <= 4096, M * (H + 8) * 2 <= 131072; E <= 256;
- * M * topk <= 135. Library-owned counter: calls on one device must be stream-ordered. */
+ * topk <= 16. Library-owned counter: calls on one device must be stream-ordered. */
 int snowverify_norm_router_plan(const void* x, const void* res_in, void* res_out,
                                 const void* gamma, float eps, void* ws, void* y_out,
                                 const void* router, float* logits, int64_t M, int64_t H,
@@ -595,8 +596,14 @@ int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c, int64
 /* act[M, F] = silu(x Wg^T) * (x Wu^T), gate_up the packed [2F, K] k-quant weight. */
 int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* meta, const void* ws,
                               void* act, int64_t M, int64_t F, int64_t K, void* stream);
-/* MoE: plan of the experts the block touches (device side), then the experts of one layer. */
+/* MoE: plan of the experts the block touches (device side), then the experts of one layer.
+ * A plan holds up to 64 block rows (M * topk <= 512): each expert the block touches takes one
+ * slot per 16 of its rows (its rows in ascending order), experts in ascending id, then the
+ * shared expert ceil(M / 16) slots; snowverify_moe_max_slots(M, topk, E, shared) bounds the
+ * slots (the expert launches' max_slots and their activation scratch [slots, 16, F]; 0 past
+ * the limits). */
 int64_t snowverify_moe_plan_bytes(void);
+int64_t snowverify_moe_max_slots(int64_t M, int64_t topk, int64_t E, int shared);
 int snowverify_moe_plan(const int32_t* ids, int64_t M, int64_t topk, int64_t E, int shared,
                         void* plan, void* stream);
 /* snowverify_moe_route and snowverify_moe_plan in one launch (shared slot iff shared_w). */

@@ -201,6 +201,7 @@ _SIGS = [
     ("snowverify_dense_gemv", c_int, [c_int, P, P, P, c_int64, c_int64, c_int64, c_int, S]),
     ("snowverify_gate_up_swiglu", c_int, [c_int, P, P, P, P, c_int64, c_int64, c_int64, S]),
     ("snowverify_moe_plan_bytes", c_int64, []),
+    ("snowverify_moe_max_slots", c_int64, [c_int64, c_int64, c_int64, c_int]),
     ("snowverify_moe_plan", c_int, [P, c_int64, c_int64, c_int64, c_int, P, S]),
     ("snowverify_moe_route_plan", c_int, [P, c_int64, c_int64, c_int64, c_int64, P, P, P, P, S]),
     ("snowverify_norm_router_plan", c_int, [P] * 4 + [c_float] + [P] * 4 + [c_int64] * 4 +

@@ -308,35 +308,65 @@ __global__ void dense_shuffle_kernel(const uint16_t* __restrict__ src, uint16_t*
 // act_out: [slots, 16, F] bf16 (MoE; rows >= M zero) or [M, F] (dense).
 // ---------------------------------------------------------------------------------------
 // MoE plan: per slot (a routed expert the block touches, then the shared expert) the rows
-// routed to it in ascending order, compacted, and each row's (row * topk + k) pair index.
+// routed to it in ascending order, compacted, and each row's (row * topk + k) pair index. A
+// block of up to MOE_MAX_M rows: an expert with more than 16 rows takes several consecutive
+// slots of 16 (its rows in order), so that every slot fits one 16-row operand tile and each
+// expert's weights are read once per 16 of its rows; the shared expert takes ceil(M / 16).
 // ---------------------------------------------------------------------------------------
-constexpr int MOE_MAX_SLOTS = 136;
+constexpr int MOE_MAX_M = 64;       // block rows per plan
+constexpr int MOE_MAX_PICKS = 512;  // rows * topk per plan
+// routed slots <= unique experts + picks / 16 (an expert of c rows takes <= 1 + c / 16), then
+// the shared expert's ceil(M / 16)
+constexpr int MOE_MAX_SLOTS = 256 + MOE_MAX_PICKS / 16 + MOE_MAX_M / 16;  // 292
 struct MoePlan {
-  int32_t n_slots;                         // routed unique experts + shared expert
-  int32_t n_routed;
+  int32_t n_slots;                         // routed slots + shared slots
+  int32_t n_routed;                        // routed slots
   int32_t slot_expert[MOE_MAX_SLOTS];      // expert id per slot (E = shared)
-  int32_t slot_rows[MOE_MAX_SLOTS];        // rows routed to the slot
+  int32_t slot_rows[MOE_MAX_SLOTS];        // rows of the slot (<= 16)
   int32_t row_of[MOE_MAX_SLOTS][16];       // compact position -> block row
   int32_t pair_of[MOE_MAX_SLOTS][16];      // compact position -> pair index (-1: shared)
   uint32_t epoch;                          // nonzero, new for every plan written
 };
+
+// Slots a plan of M rows, topk picks each, can take (routed + shared).
+inline int64_t moe_plan_slots(int64_t M, int64_t topk, int64_t E, bool shared) {
+  const int64_t picks = M * topk;
+  return std::min(E, picks) + picks / 16 + (shared ? (M + 15) / 16 : 0);
+}
 
 // Plan generation counter: every plan kernel takes the next value (skipping 0) for its plan.
 // Plan kernels are stream-ordered on one device, so one thread updates it without atomics.
 __device__ uint32_t g_moe_epoch;
 
 // Row gather for one wave: compact row r = lane & 15 of the slot reads block row row_of[r]
-// from the operand workspace; rows past the slot's count read zeros (out-of-range offsets).
+// from the operand workspace (row R in 16-row tile R / 16, tiles tile_bytes apart); rows past
+// the slot's count read zeros (out-of-range offsets). The streams' ranges cover the block's
+// `tiles` operand tiles.
 __device__ __forceinline__ void gather_rows(GemvStreams& st, const int32_t* rows, int n_rows,
-                                            int lane) {
+                                            int lane, const void* ws, int S, int tiles,
+                                            uint32_t tile_bytes) {
   const int r = lane & 15, kq = lane >> 4;
   const int R = r < n_rows ? rows[r] : -1;
-  st.v_xop = R >= 0 ? (uint32_t)((R + 16 * kq) * 16) : 0x80000000u;
-  st.v_sx = R >= 0 ? (uint32_t)((R + 16 * kq) * 4) : 0x80000000u;
+  const uint32_t tr = R >= 0 ? (uint32_t)(R >> 4) * tile_bytes : 0u;
+  const int rr = R & 15;
+  st.v_xop = R >= 0 ? tr + (uint32_t)((rr + 16 * kq) * 16) : 0x80000000u;
+  st.v_sx = R >= 0 ? tr + (uint32_t)((rr + 16 * kq) * 4) : 0x80000000u;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int ci = 4 * kq + i;
-    st.v_scale_g[i] = ci < n_rows ? (uint32_t)(rows[ci] * 4) : 0x80000000u;
+    const int Ri = ci < n_rows ? rows[ci] : -1;
+    st.v_scale_g[i] = Ri >= 0 ? (uint32_t)(Ri >> 4) * tile_bytes + (uint32_t)((Ri & 15) * 4)
+                              : 0x80000000u;
+  }
+  if (tiles > 1) {
+    const XPrepView xv = xprep_view((void*)ws, S);
+    const uint32_t more = (uint32_t)(tiles - 1) * tile_bytes;
+    st.xop = __builtin_amdgcn_make_buffer_rsrc((void*)xv.xop, 0, (int)(more + S * 8 * 64 * 16),
+                                               0x00020000);
+    st.sxop = __builtin_amdgcn_make_buffer_rsrc((void*)xv.sxop, 0, (int)(more + S * 2 * 64 * 4),
+                                                0x00020000);
+    st.scale = __builtin_amdgcn_make_buffer_rsrc((void*)xv.scale, 0, (int)(more + S * 16 * 4),
+                                                 0x00020000);
   }
 }
 
@@ -378,7 +408,8 @@ __device__ __forceinline__ void gate_up_body(
   floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
   if (pair < half_tiles) {
     if (plan) {
-      gather_rows(st, plan->row_of[slot], n_rows, lane);
+      gather_rows(st, plan->row_of[slot], n_rows, lane, ws, S, (M + 15) >> 4,
+                  (uint32_t)xprep_tile_bytes(S));
       gemv_loop<FMT, 2, WS, true>(st, sw, S, pair, half_tiles, kq, Mv, acc);
     } else {
       gemv_loop<FMT, 2, WS>(st, sw, S, pair, half_tiles, kq, Mv, acc);
@@ -506,68 +537,83 @@ __device__ __forceinline__ void route_row(const float* __restrict__ l, int E, in
   my_w = lane < topk ? ek / ks : 0.f;
 }
 
+// Inclusive sum over the wave's lanes (lane order).
+__device__ __forceinline__ int wave_incl_sum(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    v += lane >= d ? o : 0;
+  }
+  return v;
+}
+
 // Plan from the expert row masks (mask[e] bit r: block row r is routed to expert e; complete
 // and visible to every thread) and the picks ids_s[M * topk] in LDS; ep_prev = g_moe_epoch,
-// loaded by the caller. Every wave takes the four ballots of the 256 expert flags itself, so
-// slots need no exchange between waves: waves 0-3 write the expert slots, waves 4-7 the (row,
-// pick) lists, waves 8+ the shared expert's rows, all at once. Needs ROUTE_THREADS threads.
+// loaded by the caller. Expert e of c rows takes ceil(c / 16) consecutive slots, experts in
+// ascending id; every wave forms the slots' prefix over the 256 experts itself (four groups of
+// 64, a wave sum each), so slots need no exchange between waves: waves 0-3 write the expert
+// slots, waves 4-11 the (row, pick) lists, waves 12-13 the shared expert's rows, all at once.
+// Needs ROUTE_THREADS threads.
 __device__ __forceinline__ void plan_from_masks(const int32_t* ids_s, int M, int topk, int E,
-                                               int shared, const uint32_t* mask, uint32_t ep_prev,
+                                               int shared, const uint64_t* mask, uint32_t ep_prev,
                                                MoePlan* __restrict__ plan) {
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-  uint32_t mk[4];
-  uint64_t bal[4];
-  int cnt[4];
+  uint64_t mk[4];
+  int base[4];  // first slot of expert lane + 64 i
+  int n_routed = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    mk[i] = lane + 64 * i < E ? mask[lane + 64 * i] : 0u;
-    bal[i] = __ballot(mk[i] != 0u);
-    cnt[i] = __popcll(bal[i]);
+    mk[i] = lane + 64 * i < E ? mask[lane + 64 * i] : 0ull;
+    const int v = (__popcll(mk[i]) + 15) >> 4;
+    const int incl = wave_incl_sum(v, lane);
+    base[i] = n_routed + incl - v;
+    n_routed += __builtin_amdgcn_readlane(incl, 63);
   }
-  const int n_routed = cnt[0] + cnt[1] + cnt[2] + cnt[3];
-  const uint64_t below = (1ull << lane) - 1ull;
+  const int n_shared = shared ? (M + 15) >> 4 : 0;
   if (w < 4) {
-    // expert e = t: its slot is the number of used experts below it
-    int off = 0;
-#pragma unroll
-    for (int i = 0; i < 3; ++i) off += i < w ? cnt[i] : 0;
-    const uint32_t me = w == 0 ? mk[0] : w == 1 ? mk[1] : w == 2 ? mk[2] : mk[3];
-    const uint64_t bw = w == 0 ? bal[0] : w == 1 ? bal[1] : w == 2 ? bal[2] : bal[3];
-    if (me != 0u) {
-      const int sl = off + __popcll(bw & below);
-      plan->slot_expert[sl] = t;
-      plan->slot_rows[sl] = __popc(me);
+    // expert e = t: its slots, 16 of its rows each
+    const uint64_t me = w == 0 ? mk[0] : w == 1 ? mk[1] : w == 2 ? mk[2] : mk[3];
+    const int b = w == 0 ? base[0] : w == 1 ? base[1] : w == 2 ? base[2] : base[3];
+    const int c = __popcll(me);
+    for (int j = 0; 16 * j < c; ++j) {
+      plan->slot_expert[b + j] = t;
+      plan->slot_rows[b + j] = c - 16 * j < 16 ? c - 16 * j : 16;
     }
     if (t == 0) {
       const uint32_t ep = (ep_prev + 1u) != 0u ? ep_prev + 1u : 1u;  // skips 0
       g_moe_epoch = ep;
       plan->epoch = ep;
       plan->n_routed = n_routed;
-      if (shared) {
-        plan->slot_expert[n_routed] = E;
-        plan->slot_rows[n_routed] = M;
+      for (int j = 0; j < n_shared; ++j) {
+        plan->slot_expert[n_routed + j] = E;
+        plan->slot_rows[n_routed + j] = M - 16 * j < 16 ? M - 16 * j : 16;
       }
-      plan->n_slots = n_routed + (shared ? 1 : 0);
+      plan->n_slots = n_routed + n_shared;
     }
-  } else if (w < 8) {
-    // pick p: its row's position in the slot = rows routed to the expert before it
+  } else if (w < 12) {
+    // pick p: its row's position among the rows routed to its expert, then that position's slot
     const int p = t - 256;
     const int e = p < M * topk ? ids_s[p] : -1;
+    // every lane takes part in the exchanges; the slot base of expert e from lane e % 64 of
+    // group e / 64
+    const int src = e >= 0 ? (e & 63) : 0;
+    int bg[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bg[i] = __shfl(base[i], src, 64);
     if (e >= 0 && e < E) {
       const int g = e >> 6, r = p / topk;
-      const uint64_t bg = g == 0 ? bal[0] : g == 1 ? bal[1] : g == 2 ? bal[2] : bal[3];
-      const int sl = (g > 0 ? cnt[0] : 0) + (g > 1 ? cnt[1] : 0) + (g > 2 ? cnt[2] : 0) +
-                     __popcll(bg & ((1ull << (e & 63)) - 1ull));
-      const int pos = __popc(mask[e] & ((1u << r) - 1u));
-      plan->row_of[sl][pos] = r;
-      plan->pair_of[sl][pos] = p;
+      const int b = g == 0 ? bg[0] : g == 1 ? bg[1] : g == 2 ? bg[2] : bg[3];
+      const int pos = __popcll(mask[e] & ((1ull << r) - 1ull));
+      const int sl = b + (pos >> 4);
+      plan->row_of[sl][pos & 15] = r;
+      plan->pair_of[sl][pos & 15] = p;
     }
-  } else if (shared) {
-    const int r = t - 512;
+  } else if (w < 14 && shared) {
+    const int r = t - 768;
     if (r < M) {
-      plan->row_of[n_routed][r] = r;
-      plan->pair_of[n_routed][r] = -1;
+      plan->row_of[n_routed + (r >> 4)][r & 15] = r;
+      plan->pair_of[n_routed + (r >> 4)][r & 15] = -1;
     }
   }
 }
@@ -576,26 +622,27 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_route_plan_kernel(
     const float* __restrict__ logits, int64_t stride, int M, int E, int topk,
     float* __restrict__ weights, int32_t* __restrict__ ids, float* __restrict__ shared_w,
     MoePlan* __restrict__ plan) {
-  __shared__ int32_t ids_s[16 * 16];
-  __shared__ uint32_t mask[256];
+  __shared__ int32_t ids_s[MOE_MAX_PICKS];
+  __shared__ uint64_t mask[256];
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const uint32_t ep_prev = plan ? g_moe_epoch : 0u;
-  if (t < 256) mask[t] = 0u;
+  if (t < 256) mask[t] = 0ull;
   __syncthreads();
-  if (w < M) {
-    const float* l = logits + (int64_t)w * stride;
+  for (int row = w; row < M; row += ROUTE_THREADS / 64) {  // wave w: rows w, w + 16, ...
+    const float* l = logits + (int64_t)row * stride;
     const float gate = shared_w ? l[E] : 0.f;
     float my_w;
     int my_id;
     route_row(l, E, topk, lane, my_w, my_id);
     if (lane < topk) {
-      weights[w * topk + lane] = my_w;
-      ids[w * topk + lane] = my_id;
-      ids_s[w * topk + lane] = my_id;
-      if (my_id >= 0 && my_id < E) atomicOr(&mask[my_id], 1u << w);
+      weights[row * topk + lane] = my_w;
+      ids[row * topk + lane] = my_id;
+      ids_s[row * topk + lane] = my_id;
+      if (my_id >= 0 && my_id < E)
+        atomicOr((unsigned long long*)&mask[my_id], 1ull << row);
     }
-    if (lane == 0 && shared_w) shared_w[w] = 1.0f / (1.0f + __expf(-gate));
+    if (lane == 0 && shared_w) shared_w[row] = 1.0f / (1.0f + __expf(-gate));
   }
   if (!plan) return;
   __syncthreads();
@@ -605,15 +652,15 @@ __global__ void __launch_bounds__(ROUTE_THREADS) moe_route_plan_kernel(
 __global__ void __launch_bounds__(ROUTE_THREADS) moe_plan_kernel(const int32_t* __restrict__ ids,
                                                                 int M, int topk, int E, int shared,
                                                                 MoePlan* __restrict__ plan) {
-  __shared__ int32_t ids_s[16 * 16];
-  __shared__ uint32_t mask[256];
+  __shared__ int32_t ids_s[MOE_MAX_PICKS];
+  __shared__ uint64_t mask[256];
   const int t = threadIdx.x;
   const uint32_t ep_prev = g_moe_epoch;
-  if (t < 256) mask[t] = 0u;
+  if (t < 256) mask[t] = 0ull;
   const int e = t < M * topk ? ids[t] : -1;
   if (t < M * topk) ids_s[t] = e;
   __syncthreads();
-  if (e >= 0 && e < E) atomicOr(&mask[e], 1u << (t / topk));
+  if (e >= 0 && e < E) atomicOr((unsigned long long*)&mask[e], 1ull << (t / topk));
   __syncthreads();
   plan_from_masks(ids_s, M, topk, E, shared, mask, ep_prev, plan);
 }
@@ -649,8 +696,8 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
   __shared__ float part_ss[NR_MAXP][NR_THREADS / 64];
   __shared__ floatx4 part[NR_THREADS / 64][64];
   __shared__ uint32_t last;
-  __shared__ int32_t ids_s[16 * 16];
-  __shared__ uint32_t mask[256];
+  __shared__ int32_t ids_s[MOE_MAX_PICKS];
+  __shared__ uint64_t mask[256];
   const int t = threadIdx.x, lane = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
   const int kq = lane >> 4, r = lane & 15;
@@ -823,7 +870,7 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
 #pragma unroll
   for (int k = 0; k < LG_PER; ++k)
     if (t + k * NR_THREADS < M * N) lg[t + k * NR_THREADS] = lv[k];
-  if (t < 256) mask[t] = 0u;
+  if (t < 256) mask[t] = 0ull;
   const uint32_t ep_prev = g_moe_epoch;
   __syncthreads();
   // moe_route_plan_kernel's routing, wave w on row w
@@ -837,7 +884,8 @@ __global__ void __launch_bounds__(NR_THREADS) norm_router_plan_kernel(
       weights[row * topk + lane] = my_w;
       ids[row * topk + lane] = my_id;
       ids_s[row * topk + lane] = my_id;
-      if (my_id >= 0 && my_id < E) atomicOr(&mask[my_id], 1u << row);
+      if (my_id >= 0 && my_id < E)
+        atomicOr((unsigned long long*)&mask[my_id], 1ull << row);
     }
     if (lane == 0 && shared_w) shared_w[row] = 1.0f / (1.0f + __expf(-gate));
   }
@@ -1188,7 +1236,7 @@ SV_API int snowverify_norm_prep_moe(const float* pairs, const float* shared_out,
 // workspace ws) + snowverify_dense_gemv (bf16 router [E (+1), H] repacked, over the normalised
 // rows, f32 logits [M, E (+1)]) + snowverify_moe_route with the plan, in one launch and with
 // their bits. shared_w null: no shared expert (E router rows). M <= 16, H a multiple of 512 up
-// to 4096 with M * (H + 8) * 2 <= 128 KiB, E <= 256, M * topk <= 135. Uses a library-owned
+// to 4096 with M * (H + 8) * 2 <= 128 KiB, E <= 256, topk <= 16. Uses a library-owned
 // counter: calls on one device must be stream-ordered.
 SV_API int snowverify_norm_router_plan(const void* x, const void* res_in, void* res_out,
                                        const void* gamma, float eps, void* ws, void* y_out,
@@ -1197,7 +1245,7 @@ SV_API int snowverify_norm_router_plan(const void* x, const void* res_in, void* 
                                        float* shared_w, void* plan, void* stream) {
   if (!x || !gamma || !ws || !router || !logits || !weights || !ids || !plan || M <= 0 ||
       M > 16 || H <= 0 || H % 512 || H > 4096 || E <= 0 || E > 256 || topk <= 0 || topk > 16 ||
-      topk > E || M * topk > 135)
+      topk > E)
     return SV_EINVAL;
   if (res_out && (res_out == x || res_out == res_in)) return SV_EINVAL;  // read by every block
   const int64_t N = E + (shared_w ? 1 : 0);
@@ -1293,10 +1341,20 @@ SV_API int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* met
 
 SV_API int64_t snowverify_moe_plan_bytes(void) { return (int64_t)sizeof(MoePlan); }
 
-// Plan the block's experts from top-k ids [M, topk] (i32). M * topk <= 135, E <= 256, M <= 16.
+// The most slots a plan of M rows with topk picks each can take (an expert with more than 16
+// rows takes one slot per 16; the shared expert ceil(M / 16)): the max_slots the expert
+// launches need, and the slots of their activation scratch [slots, 16, F]. 0 past the limits.
+SV_API int64_t snowverify_moe_max_slots(int64_t M, int64_t topk, int64_t E, int shared) {
+  if (M <= 0 || M > MOE_MAX_M || topk <= 0 || M * topk > MOE_MAX_PICKS || E <= 0 || E > 256)
+    return 0;
+  return moe_plan_slots(M, topk, E, shared != 0);
+}
+
+// Plan the block's experts from top-k ids [M, topk] (i32). M <= 64, M * topk <= 512, E <= 256.
 SV_API int snowverify_moe_plan(const int32_t* ids, int64_t M, int64_t topk, int64_t E, int shared,
                                void* plan, void* stream) {
-  if (M <= 0 || M > 16 || topk <= 0 || M * topk > 135 || E <= 0 || E > 256) return SV_EINVAL;
+  if (M <= 0 || M > MOE_MAX_M || topk <= 0 || M * topk > MOE_MAX_PICKS || E <= 0 || E > 256)
+    return SV_EINVAL;
   hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(ROUTE_THREADS), 0, Sx(stream), ids, (int)M,
                      (int)topk, (int)E, shared, (MoePlan*)plan);
   SV_CHECK_LAUNCH();
@@ -1308,8 +1366,8 @@ SV_API int snowverify_moe_plan(const int32_t* ids, int64_t M, int64_t topk, int6
 SV_API int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, int64_t E,
                                 int64_t topk, float* weights, int32_t* ids, float* shared_w,
                                 void* stream) {
-  if (M < 0 || M > 16 || E <= 0 || E > 256 || topk <= 0 || topk > 16 || topk > E ||
-      stride < E + (shared_w ? 1 : 0))
+  if (M < 0 || M > MOE_MAX_M || E <= 0 || E > 256 || topk <= 0 || topk > 16 || topk > E ||
+      M * topk > MOE_MAX_PICKS || stride < E + (shared_w ? 1 : 0))
     return SV_EINVAL;
   if (M == 0) return SV_OK;
   hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(ROUTE_THREADS), 0, Sx(stream), logits,
@@ -1322,8 +1380,8 @@ SV_API int snowverify_moe_route(const float* logits, int64_t stride, int64_t M, 
 SV_API int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_t M, int64_t E,
                                      int64_t topk, float* weights, int32_t* ids, float* shared_w,
                                      void* plan, void* stream) {
-  if (M <= 0 || M > 16 || E <= 0 || E > 256 || topk <= 0 || topk > 16 || topk > E ||
-      M * topk > 135 || stride < E + (shared_w ? 1 : 0) || !plan)
+  if (M <= 0 || M > MOE_MAX_M || E <= 0 || E > 256 || topk <= 0 || topk > 16 || topk > E ||
+      M * topk > MOE_MAX_PICKS || stride < E + (shared_w ? 1 : 0) || !plan)
     return SV_EINVAL;
   hipLaunchKernelGGL(moe_route_plan_kernel, dim3(1), dim3(ROUTE_THREADS), 0, Sx(stream), logits,
                      stride, (int)M, (int)E, (int)topk, weights, ids, shared_w, (MoePlan*)plan);
@@ -1331,7 +1389,8 @@ SV_API int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_
   return SV_OK;
 }
 
-// MoE expert stages (Q4_K). act scratch [M*topk + 1, 16, F] bf16 (compact rows per slot).
+// MoE expert stages (Q4_K, Q5_K, Q6_K). act scratch [max_slots, 16, F] bf16 (compact rows
+// per slot; max_slots from snowverify_moe_max_slots). M <= 64 block rows.
 // Each tile pair (gate/up) or tile group (down) splits its superblocks over two waves: a launch
 // then holds about twice the waves of one per pair, so the few workgroups that do not fit the
 // first round over the CUs (more than 64 expert slots) finish in half the time (measured on
@@ -1356,8 +1415,8 @@ SV_API int snowverify_moe_gate_up(int fmt, const void* gu_quant, const void* gu_
                                   const void* plan, const void* ws, void* act, int64_t M,
                                   int64_t max_slots, int64_t E, int64_t H, int64_t F,
                                   void* stream) {
-  if (!expert_fmt(fmt) || M <= 0 || M > 16 || max_slots <= 0 || max_slots > MOE_MAX_SLOTS ||
-      H % 256 || F % 256)
+  if (!expert_fmt(fmt) || M <= 0 || M > MOE_MAX_M || max_slots <= 0 ||
+      max_slots > MOE_MAX_SLOTS || H % 256 || F % 256)
     return SV_EINVAL;
   const int64_t gu_q = packed_quant(fmt, 2 * F, H), gu_m = packed_meta(fmt, 2 * F, H);
   const dim3 grid((unsigned)((F / 16 + MOE_GU_PPB - 1) / MOE_GU_PPB), (unsigned)max_slots);
@@ -1418,7 +1477,7 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
                                        float* shared_out, int64_t M, int64_t max_slots,
                                        int64_t E, int64_t H, int64_t F, void* stream) {
   const int gu_fmt = fmt & 0xff, dn_fmt = (fmt >> 8) ? ((fmt >> 8) & 0xff) : gu_fmt;
-  if (!expert_fmt(gu_fmt) || !expert_fmt(dn_fmt) || M <= 0 || M > 16 || max_slots <= 0 ||
+  if (!expert_fmt(gu_fmt) || !expert_fmt(dn_fmt) || M <= 0 || M > MOE_MAX_M || max_slots <= 0 ||
       max_slots > MOE_MAX_SLOTS || H % 256 || F % 256 || (F / 16) % MOE_GU_PPB ||
       (H / 16 / MOE_DN_NTILE) % MOE_DN_GPB)
     return SV_EINVAL;
@@ -1486,8 +1545,9 @@ SV_API int snowverify_moe_combine(const float* pairs, const float* shared_out, v
   return SV_OK;
 }
 
-// MoE experts of one layer (Q4_K): gate/up, down and combine. ws: prepared operands of the
-// normalised hidden [M, H]; act scratch [M*topk + 1, 16, F] bf16; pairs [M*topk, H] f32;
+// MoE experts of one layer: gate/up, down and combine. ws: prepared operands of the normalised
+// hidden [M, H] (M <= 64); act scratch [snowverify_moe_max_slots(M, topk, E, shared), 16, F]
+// bf16; pairs [M*topk, H] f32;
 // shared_out [M, H] f32; out [M, H] bf16 = sum_k w_k expert_k(x) + sigmoid(g) shared(x).
 SV_API int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_meta,
                                   const void* dn_quant, const void* dn_meta, const void* sh_gu_quant,
@@ -1496,8 +1556,8 @@ SV_API int snowverify_moe_experts(int fmt, const void* gu_quant, const void* gu_
                                   const float* weights, const float* shared_w, void* act,
                                   float* pairs, float* shared_out, void* out, int64_t M,
                                   int64_t topk, int64_t E, int64_t H, int64_t F, void* stream) {
-  if (M * topk > MOE_MAX_SLOTS - 1) return SV_EINVAL;
-  const int64_t slots = M * topk + (sh_gu_quant ? 1 : 0);
+  const int64_t slots = snowverify_moe_max_slots(M, topk, E, sh_gu_quant != nullptr);
+  if (slots <= 0) return SV_EINVAL;
   const int gu_fmt = fmt & 0xff, dn_fmt = (fmt >> 8) ? ((fmt >> 8) & 0xff) : gu_fmt;
   int rc = snowverify_moe_gate_up(gu_fmt, gu_quant, gu_meta, sh_gu_quant, sh_gu_meta, plan, ws, act,
                                   M, slots, E, H, F, stream);

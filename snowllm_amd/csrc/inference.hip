@@ -38,7 +38,8 @@ struct PagedAttentionStep {  // snowllm/ops/attention_full.py:120-123
 };
 
 constexpr int WT_F16 = 1, WT_BF16 = 2;  // snowverify_dense_gemv weight types
-constexpr int MAX_ROWS = 16;            // rows per MoE / dense-GEMV call (one 16-row tile)
+constexpr int MAX_ROWS = 16;            // rows per dense-MLP call (one 16-row tile)
+constexpr int MOE_ROWS = 64;            // rows per MoE call (the plan's limit)
 
 inline size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -78,6 +79,7 @@ int snowverify_dense_gemv(int wt, const void* w, const void* act, void* c, int64
 int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* meta, const void* ws,
                               void* act, int64_t M, int64_t F, int64_t K, void* stream);
 int64_t snowverify_moe_plan_bytes(void);
+int64_t snowverify_moe_max_slots(int64_t M, int64_t topk, int64_t E, int shared);
 int snowverify_moe_route_plan(const float* logits, int64_t stride, int64_t M, int64_t E,
                               int64_t topk, float* weights, int32_t* ids, float* shared_w,
                               void* plan, void* stream);
@@ -145,7 +147,8 @@ MoeWs moe_ws(void* base, int64_t M) {
   w.ids = (int32_t*)c.take((size_t)M * K * 4);
   w.shared_w = (float*)c.take((size_t)M * 4);
   w.plan = c.take((size_t)snowverify_moe_plan_bytes());
-  w.act = c.take((size_t)(M * K + 1) * 16 * F * 2);
+  // activation scratch for every slot the plan can take (16 compact rows each)
+  w.act = c.take((size_t)snowverify_moe_max_slots(M, K, E, 1) * 16 * F * 2);
   w.pairs = (float*)c.take((size_t)M * K * H * 4);
   w.shared_out = (float*)c.take((size_t)M * H * 4);
   w.bytes = c.used;
@@ -177,7 +180,7 @@ int moe_body(const Weight* w, const void* hidden, const void* router, void* out,
   rc = snowverify_moe_route_plan(ws.logits, E + 1, M, E, K, ws.weights, ws.ids,
                                  shared ? ws.shared_w : nullptr, ws.plan, s);
   if (rc) return rc;
-  const int64_t slots = M * K + (shared ? 1 : 0);
+  const int64_t slots = snowverify_moe_max_slots(M, K, E, shared);
   rc = snowverify_moe_gate_up_down(w[0].fmt | (w[1].fmt << 8), w[0].data[0], w[0].data[1],
                                    w[1].data[0], w[1].data[1],
                                    shared ? w[2].data[0] : nullptr,
@@ -457,7 +460,7 @@ SV_API int snowllm_moe_shuffle_router(const void* router, const void* bias, void
 
 // snowllm/_capi.py:315 and 690 -- scratch of the MoE block for `rows` rows (flags must be 0).
 SV_API int64_t snowllm_moe_workspace_bytes(int64_t rows) {
-  if (rows <= 0 || !moe_geometry_ok()) return 0;
+  if (rows <= 0 || rows > MOE_ROWS || !moe_geometry_ok()) return 0;
   return (int64_t)moe_ws(nullptr, rows).bytes;
 }
 
@@ -468,13 +471,13 @@ SV_API int64_t snowllm_inference_moe_workspace_bytes(int64_t rows, int64_t flags
 // snowllm/_capi.py:691 (ops/inference.py:60-76): out [M, hidden] = MoE(x) for normalised x.
 // w: experts' gate/up stack, experts' down stack, shared gate/up, shared down (absent when the
 // geometry has no shared expert); router: the repacked bf16 [E + 1, hidden] router with the
-// shared expert's gate last. x and out may be the same buffer. M <= 16.
+// shared expert's gate last. x and out may be the same buffer. M <= 64.
 SV_API int snowllm_inference_moe(const Weight* w, const void* x, const void* router,
                                  const int64_t* token_ids, const int32_t* tid2eid, void* out,
                                  void* scratch, int64_t capacity, int64_t M, int64_t flags,
                                  void* stream) {
   if (token_ids || tid2eid || flags) return SV_ENOTSUP;
-  if (!w || !x || !router || !out || !scratch || M <= 0 || M > MAX_ROWS || !moe_geometry_ok())
+  if (!w || !x || !router || !out || !scratch || M <= 0 || M > MOE_ROWS || !moe_geometry_ok())
     return SV_EINVAL;
   const MoeWs ws = moe_ws(scratch, M);
   if (capacity < (int64_t)ws.bytes) return SV_EINVAL;
@@ -485,13 +488,13 @@ SV_API int snowllm_inference_moe(const Weight* w, const void* x, const void* rou
 
 // snowllm/_capi.py:805-807 (ops/inference.py:82-95; FusedMoE with the post-attention norm,
 // models/qwen3_5/qwen3_5.py:38-41): residual += x; hidden_row = RMSNorm(residual) * gamma;
-// out = MoE(hidden_row). x and out may be the same buffer. M <= 16.
+// out = MoE(hidden_row). x and out may be the same buffer. M <= 64.
 SV_API int snowllm_inference_moe_norm(const Weight* w, const void* x, void* residual,
                                       const void* gamma, float eps, void* hidden_row,
                                       const void* router, void* out, void* scratch,
                                       int64_t capacity, int64_t M, void* stream) {
   if (!w || !x || !residual || !gamma || !hidden_row || !router || !out || !scratch || M <= 0 ||
-      M > MAX_ROWS || !moe_geometry_ok())
+      M > MOE_ROWS || !moe_geometry_ok())
     return SV_EINVAL;
   const MoeWs ws = moe_ws(scratch, M);
   if (capacity < (int64_t)ws.bytes) return SV_EINVAL;

@@ -36,9 +36,9 @@ struct XPrepView {
   float* scale;   // [S][16] 2^e per (superblock, row): undoes the operand scaling
 };
 
-inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-inline size_t xprep_tile_bytes(int64_t S) {
+__host__ __device__ inline size_t xprep_tile_bytes(int64_t S) {
   return align256((size_t)S * 8 * 64 * 16) + align256((size_t)S * 2 * 64 * 4) +
          align256((size_t)S * 16 * 4);
 }

@@ -239,4 +239,15 @@ def parse_plan(plan):
             "pair_of": pair_of[:n].copy()}
 
 
-MOE_MAX_SLOTS = 136
+MOE_MAX_SLOTS = 292   # slots a plan struct holds (csrc/ffn.hip MoePlan)
+MOE_MAX_ROWS = 64     # block rows per plan
+
+
+def moe_max_slots(M, topk, E, shared=True):
+    """The most slots a plan of M rows can take (one per 16 rows of an expert, the shared
+    expert's ceil(M / 16)): the expert launches' max_slots and their activation scratch rows."""
+    n = int(lib.snowverify_moe_max_slots(M, topk, E, int(bool(shared))))
+    if n <= 0:
+        raise SnowLLMError(f"a MoE plan takes at most {MOE_MAX_ROWS} rows and 512 picks "
+                           f"(M={M}, topk={topk}, E={E})")
+    return n

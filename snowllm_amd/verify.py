@@ -247,10 +247,14 @@ class VerifyModel:
         M = batch * c.block
         self.rows = M
         self.row_chunks = [(r0, min(16, M - r0)) for r0 in range(0, M, 16)]
-        self.moe_chunks = self.row_chunks
-        chunk = min(16, M)
-        self.fuse_router = bool(c.moe and c.hidden % 512 == 0 and c.hidden <= 4096 and
-                                chunk * (c.hidden + 8) * 2 <= 131072 and
+        # one MoE plan per 64 rows (an expert with more than 16 of them takes a slot per 16),
+        # so each expert's weights are read once per 16 of its rows across the whole batch
+        R = Lops.MOE_MAX_ROWS
+        self.moe_chunks = [(r0, min(R, M - r0)) for r0 in range(0, M, R)]
+        # norm + router + routing/plan in one launch holds up to 16 rows
+        chunk = max(n for _, n in self.moe_chunks)
+        self.fuse_router = bool(c.moe and chunk <= 16 and c.hidden % 512 == 0 and
+                                c.hidden <= 4096 and chunk * (c.hidden + 8) * 2 <= 131072 and
                                 chunk * (c.experts + 1) * 4 <= 131072)
         self.embed_q4k = False       # True: self.embed holds Q4_K blocks [V, H / 256 * 144]
         self.lm_head_raw = None
@@ -377,8 +381,8 @@ class VerifyModel:
             self.plans = [torch.empty(Lops.MOE_PLAN_BYTES, dtype=torch.uint8, device=dev)
                           for _ in self.moe_chunks]
             self.plan = self.plans[0]
-            mc = max(m for _, m in self.moe_chunks)
-            self.moe_act = torch.empty(mc * K + 1, 16, F, dtype=bf, device=dev)
+            self.moe_slots = [Lops.moe_max_slots(n, K, E) for _, n in self.moe_chunks]
+            self.moe_act = torch.empty(max(self.moe_slots), 16, F, dtype=bf, device=dev)
             self.pairs = torch.empty(T * K, H, dtype=torch.float32, device=dev)
             self.shared_out = torch.empty(T, H, dtype=torch.float32, device=dev)
         else:
@@ -536,8 +540,8 @@ class VerifyModel:
                     Lops.moe_gate_up_down(gu_fmt | dn_fmt << 8, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, plan,
                                           ws, self.route_w[rs], self.shared_w[rs],
                                           self.moe_act, self.pairs[r0 * K:(r0 + n) * K],
-                                          self.shared_out[rs], n, n * K + 1, c.experts, H,
-                                          c.expert_ffn)
+                                          self.shared_out[rs], n, self.moe_slots[j],
+                                          c.experts, H, c.expert_ffn)
                 if record_slots is not None:
                     # unique routed experts of the whole step + the shared expert
                     used = torch.bincount(self.route_ids.view(-1).long(), minlength=c.experts)

@@ -21,12 +21,45 @@ def _route_reference(logits, topk):
     return ids, w / w.sum(-1, keepdim=True), torch.sigmoid(logits[:, E].double())
 
 
-@pytest.mark.parametrize("M", [1, 9, 16])
-def test_route_plan(gpu, M):
+def _expected_plan(ids_np, M, shared=True):
+    """The plan's slots by brute force: experts in ascending id, each expert's rows in
+    ascending order, 16 per slot; then the shared expert's rows, 16 per slot."""
+    K = ids_np.shape[1]
+    slots = []
+    for e in np.unique(ids_np):
+        rows = [r for r in range(M) if e in ids_np[r]]
+        for j in range(0, len(rows), 16):
+            part = rows[j:j + 16]
+            slots.append((int(e), part, [r * K + list(ids_np[r]).index(e) for r in part]))
+    n_routed = len(slots)
+    if shared:
+        for j in range(0, M, 16):
+            part = list(range(j, min(M, j + 16)))
+            slots.append((E, part, [-1] * len(part)))
+    return slots, n_routed
+
+
+def _check_plan(p, ids_np, M, shared=True):
+    slots, n_routed = _expected_plan(ids_np, M, shared)
+    assert p["n_routed"] == n_routed and p["n_slots"] == len(slots)
+    for s, (e, rows, pairs) in enumerate(slots):
+        n = len(rows)
+        assert p["slot_expert"][s] == e and p["slot_rows"][s] == n, s
+        assert list(p["row_of"][s][:n]) == rows, s
+        assert list(p["pair_of"][s][:n]) == pairs, s
+
+
+# up to 16 rows: one slot per expert; 36 and 64 rows (batched verify): an expert routed more
+# than 16 rows takes one slot per 16 ("hot": every row routed to expert 5)
+@pytest.mark.parametrize("M,hot", [(1, False), (9, False), (16, False), (36, False), (36, True),
+                                   (64, True)])
+def test_route_plan(gpu, M, hot):
     from snowllm_amd import layers as L
-    print(f"route+plan M={M}", flush=True)
+    print(f"route+plan M={M} hot={hot}", flush=True)
     g = torch.Generator(device="cuda").manual_seed(M)
     logits = torch.randn(M, E + 1, device="cuda", generator=g)
+    if hot:
+        logits[:, 5] += 50.0
     w = torch.empty(M, K, device="cuda")
     ids = torch.empty(M, K, dtype=torch.int32, device="cuda")
     sw = torch.empty(M, device="cuda")
@@ -37,18 +70,12 @@ def test_route_plan(gpu, M):
     assert torch.equal(ids.cpu().long(), rid)
     assert torch.allclose(w.cpu().double(), rw, rtol=1e-5, atol=1e-7)
     assert torch.allclose(sw.cpu().double(), rsw, rtol=1e-5, atol=1e-7)
-    # plan: unique experts ascending, then the shared slot; compact rows ascending per slot
     p = L.parse_plan(plan)
     ids_np = ids.cpu().numpy()
-    uniq = np.unique(ids_np)
-    assert p["n_routed"] == len(uniq) and p["n_slots"] == len(uniq) + 1
-    assert np.array_equal(p["slot_expert"][:-1], uniq) and p["slot_expert"][-1] == E
-    for s, e in enumerate(uniq):
-        rows = [r for r in range(M) if e in ids_np[r]]
-        assert p["slot_rows"][s] == len(rows)
-        assert list(p["row_of"][s][:len(rows)]) == rows
-        assert list(p["pair_of"][s][:len(rows)]) == [r * K + list(ids_np[r]).index(e) for r in rows]
-    assert p["slot_rows"][-1] == M and list(p["row_of"][-1][:M]) == list(range(M))
+    _check_plan(p, ids_np, M)
+    assert p["n_slots"] <= L.moe_max_slots(M, K, E)
+    if hot:
+        assert list(p["slot_expert"]).count(5) == (M + 15) // 16
     # the separate route + plan entry points agree with the fused one
     w2, ids2 = torch.empty_like(w), torch.empty_like(ids)
     plan2 = torch.zeros_like(plan)
@@ -56,9 +83,7 @@ def test_route_plan(gpu, M):
     L.moe_plan(ids2, E, plan2, shared=True)
     torch.cuda.synchronize()
     assert torch.equal(ids2, ids) and torch.equal(w2, w)
-    p2 = L.parse_plan(plan2)
-    for key in ("slot_expert", "slot_rows"):
-        assert np.array_equal(p2[key], p[key])
+    _check_plan(L.parse_plan(plan2), ids_np, M)
 
 
 # one / two superblocks per down wave; expert formats (gate/up, down): Q4_K_M keeps some
@@ -74,17 +99,21 @@ def test_gate_up_down_equals_separate_launches(gpu, E, F, gu_f, dn_f):
     dn = packed_random(dn_f, E * H, F, 52, stack=E)
     sgu = packed_random(gu_f, 2 * F, H, 53)
     sdn = packed_random(dn_f, H, F, 54)
-    cases = ((9, True, False), (16, True, True), (1, True, False), (9, False, True),
-             (9, True, True))
-    for M, shared, spread in cases if (gu_f, dn_f) == (4, 4) else cases[:2]:
+    # (rows, shared, routing): "spread" puts every row on its own experts (the most slots),
+    # "hot" every row on expert 3 (one slot per 16 rows of it)
+    cases = ((9, True, ""), (16, True, "spread"), (1, True, ""), (9, False, "spread"),
+             (9, True, "spread"), (36, True, "hot"), (64, True, "spread"), (40, False, "hot"))
+    for M, shared, route in cases if (gu_f, dn_f) == (4, 4) else cases[:2] + cases[5:6]:
         print(f"gate_up_down E={E} F={F} fmt={gu_f}/{dn_f} M={M} shared={shared} "
-              f"spread={spread}", flush=True)
+              f"routing={route}", flush=True)
         g = torch.Generator(device="cuda").manual_seed(70 + M)
         x = torch.randn(M, H, device="cuda", generator=g).bfloat16()
         logits = torch.randn(M, E + 1, device="cuda", generator=g) * 2
-        if spread:  # every row on its own experts: the most slots
+        if route == "spread":
             for r in range(M):
                 logits[r, (K * r) % E:(K * r) % E + K] += 40.0
+        elif route == "hot":
+            logits[:, 3] += 40.0
         w = torch.empty(M, K, device="cuda")
         ids = torch.empty(M, K, dtype=torch.int32, device="cuda")
         sw = torch.empty(M, device="cuda") if shared else None
@@ -92,7 +121,7 @@ def test_gate_up_down_equals_separate_launches(gpu, E, F, gu_f, dn_f):
         L.moe_route_plan(logits, E, K, w, ids, sw, plan)
         ws = torch.empty(ops.gemm_kquant_a_ws_bytes(M, H), dtype=torch.uint8, device="cuda")
         ops.gemm_kquant_prepare_a(x, ws)
-        ns = M * K + int(shared)
+        ns = L.moe_max_slots(M, K, E, shared)
         sg, sd = (sgu, sdn) if shared else ((None, None), (None, None))
         outs = []
         for fused in (False, True, True):
@@ -122,7 +151,7 @@ def _bf(x):
 
 
 @pytest.mark.parametrize("M,gu_f,dn_f", [(9, 4, 4), (3, 4, 4), (9, 5, 5), (9, 6, 6), (9, 4, 6),
-                                          (3, 5, 6)])
+                                          (3, 5, 6), (36, 4, 4), (40, 4, 6)])
 def test_experts_match_dequantized_reference(gpu, M, gu_f, dn_f):
     from snowllm_amd import layers as L, ops
     from snowllm_amd.verify import packed_random
@@ -134,6 +163,8 @@ def test_experts_match_dequantized_reference(gpu, M, gu_f, dn_f):
     g = torch.Generator(device="cuda").manual_seed(20 + M)
     x = torch.randn(M, H, device="cuda", generator=g).bfloat16()
     logits = torch.randn(M, E + 1, device="cuda", generator=g) * 2
+    if M > 16:   # more than 16 rows of one expert: several slots of it, and of the shared one
+        logits[:, 7] += 40.0
     w = torch.empty(M, K, device="cuda")
     ids = torch.empty(M, K, dtype=torch.int32, device="cuda")
     sw = torch.empty(M, device="cuda")
@@ -141,7 +172,7 @@ def test_experts_match_dequantized_reference(gpu, M, gu_f, dn_f):
     L.moe_route_plan(logits, E, K, w, ids, sw, plan)
     ws = torch.empty(ops.gemm_kquant_a_ws_bytes(M, H), dtype=torch.uint8, device="cuda")
     ops.gemm_kquant_prepare_a(x, ws)
-    act = torch.empty(M * K + 1, 16, F, dtype=torch.bfloat16, device="cuda")
+    act = torch.empty(L.moe_max_slots(M, K, E), 16, F, dtype=torch.bfloat16, device="cuda")
     pairs = torch.empty(M * K, H, device="cuda")
     shared = torch.empty(M, H, device="cuda")
     out = torch.empty(M, H, dtype=torch.bfloat16, device="cuda")
