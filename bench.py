@@ -475,6 +475,14 @@ def bench_step(args, name):
             adaptive = adaptive_prefix(m, heads["dspark_markov (per block row)"]["us"] * k * 1e-6,
                                        heads["_markov_confidence"])
         kern.pop("_markov_confidence", None)
+    elif cfg.name == CONFIGS["config4"].name:
+        # the scheduler over the batch's requests together, on batched step costs
+        heads = time_draft_heads(stream, V, k, requests=B)
+        kern.update(heads)
+        if not args.no_adaptive:
+            draft_s = heads[f"dspark_markov ({B} requests, per block row)"]["us"] * k * 1e-6
+            adaptive = adaptive_prefix(m, draft_s, heads["_markov_confidence"], requests=B)
+        kern.pop("_markov_confidence", None)
     # dominant kernel of the step (launch time; every candidate runs once per layer); the
     # attention counts as its split + merge pair
     per_step = {kk: (1 if kk.startswith("draft_select") else cfg.layers) for kk in kern}
@@ -526,10 +534,11 @@ def bench_step(args, name):
     }
 
 
-def time_draft_heads(stream, V, k, hidden=2048, markov_rank=256):
+def time_draft_heads(stream, V, k, hidden=2048, markov_rank=256, requests=1):
     """The draft-side heads at the config-4 shapes (seeded synthetic weights): the DFlash 2
     selector's hidden projection of k rows (bf16 [256, hidden]) and the DSpark Markov walk over
-    a block of k rows (W1, W2 bf16 [V, rank], with the confidence head), per launch."""
+    a block of k rows (W1, W2 bf16 [V, rank], with the confidence head), per launch; and the
+    head's own confidences over a 15-draft proposal for each of `requests` requests."""
     import torch
     from snowllm_amd.draft_heads import MarkovHead, SelectorHead
     g = torch.Generator(device="cuda").manual_seed(5)
@@ -562,40 +571,61 @@ def time_draft_heads(stream, V, k, hidden=2048, markov_rank=256):
                 "served from the 256 MB Infinity Cache"}
     # the head's own confidences over a 15-draft proposal: the adaptive scheduler's input
     # (snowllm/engine/spec_decode.py:157-166 feeds it the drafter's confidences per request)
-    n = 15
-    rows15 = torch.randn(n, hidden, device="cuda", generator=g).bfloat16()
-    logits15 = torch.randn(n, V, device="cuda", generator=g)
-    path15 = torch.empty(1, n, dtype=torch.int64, device="cuda")
-    conf15 = torch.empty(1, n, device="cuda")
-    mk.propose(rows15, logits15, anchor, path15, conf15)
-    out["_markov_confidence"] = [round(float(c), 4) for c in conf15[0].cpu()]
+    n, b = 15, requests
+    rows15 = torch.randn(b * n, hidden, device="cuda", generator=g).bfloat16()
+    logits15 = torch.randn(b * n, V, device="cuda", generator=g)
+    anchors = torch.randint(0, V, (b,), device="cuda", generator=g)
+    path15 = torch.empty(b, n, dtype=torch.int64, device="cuda")
+    conf15 = torch.empty(b, n, device="cuda")
+    mk.propose(rows15, logits15, anchors, path15, conf15)
+    out["_markov_confidence"] = [[round(float(c), 4) for c in row] for row in conf15.cpu()]
+    if b > 1:
+        # the walk of every request's proposal in one launch, per block row
+        path_b = torch.empty(b, k, dtype=torch.int64, device="cuda")
+        conf_b = torch.empty(b, k, device="cuda")
+        rows_b, logits_b = rows15[:b * k], logits15[:b * k]
+        us = timed_graph(lambda: mk.propose(rows_b, logits_b, anchors, path_b, conf_b), 20,
+                         stream) * 1e3 / k
+        out[f"dspark_markov ({b} requests, per block row)"] = {
+            "us": round(us, 3), "alg_bytes": nb, "gbs": round(nb / (us * 1e-6) / 1e9, 1),
+            "outside_step": True}
     return out
 
 
-def adaptive_prefix(m, draft_s, confidence, rows=tuple(range(1, 17))):
+def adaptive_prefix(m, draft_s, confidence, requests=1):
     """The DSpark prefix scheduler (snowllm/engine/dspark_schedule.py) on step costs measured
-    here: verify steps of 1..16 rows (eager and graph) plus the Markov head's time, and the
-    Markov head's own confidences over a 15-draft proposal (random-init weights, so they say
-    nothing about draft quality; a trained head's would). Every row count of a batch-1 block
-    gets a captured graph, as the reference's profile of its decode shapes
-    (snowllm/engine/spec_decode.py:149-161)."""
+    here: verify steps of `requests` requests and requests x 1..16 rows in all (eager and
+    graph, rows spread evenly over the requests) plus the Markov head's time, and the Markov
+    head's own confidences over each request's 15-draft proposal (random-init weights, so they
+    say nothing about draft quality; a trained head's would). Every profiled row count gets a
+    captured graph, as the reference's profile of its decode shapes
+    (snowllm/engine/spec_decode.py:149-161); the scheduler chooses every request's prefix
+    together (spec_decode.py:157-166)."""
     from snowllm_amd.dspark_schedule import PrefixScheduler, profile_step_costs
-    cost = profile_step_costs(m, rows, draft_seconds=draft_s)
-    conf = [list(confidence)]
-    lengths = PrefixScheduler(16).choose([0], conf, [15], cost)
-    surv, s = [], 1.0
-    for c in conf[0]:
-        s *= c
-        surv.append(s)
+    B = requests
+    rows = tuple(B * t for t in range(1, 17))
+    cost = profile_step_costs(m, rows, requests=B, draft_seconds=draft_s)
+    conf = [list(c) for c in confidence[:B]]
+    lengths = PrefixScheduler(16 * B).choose(list(range(B)), conf, [15] * B, cost)
+    surv = []
+    for c_r in conf:
+        s, row = 1.0, []
+        for c in c_r:
+            s *= c
+            row.append(s)
+        surv.append(row)
 
-    def rate(n):
-        return (1 + sum(surv[:n])) / cost(1 + n)
-    return {"step_us_by_rows": {n: round(cost.graphs[n] * 1e6, 1) for n in rows},
-            "draft_us": round(draft_s * 1e6, 1),
-            "confidence": {"source": "dspark_markov confidence head (15 drafts)",
-                           "values": conf[0]},
-            "chosen_drafts": lengths[0], "expected_tokens_per_s": round(rate(lengths[0]), 1),
-            "fixed_block8_tokens_per_s": round(rate(8), 1)}
+    def rate(ns):
+        return sum(1 + sum(surv[r][:n]) for r, n in enumerate(ns)) / cost(sum(1 + n for n in ns))
+    out = {"requests": B,
+           "step_us_by_rows": {n: round(cost.graphs[n] * 1e6, 1) for n in rows},
+           "draft_us": round(draft_s * 1e6, 1),
+           "confidence": {"source": "dspark_markov confidence head (15 drafts per request)",
+                          "values": conf if B > 1 else conf[0]},
+           "expected_tokens_per_s": round(rate(lengths), 1),
+           "fixed_block8_tokens_per_s": round(rate([8] * B), 1)}
+    out["chosen_drafts"] = lengths if B > 1 else lengths[0]
+    return out
 
 
 def weights_note(cfg):

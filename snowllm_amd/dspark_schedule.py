@@ -145,20 +145,37 @@ def share_weights(source):
     return install
 
 
-def profile_step_costs(source, rows, *, draft_seconds=0.0, seed=0, reps=5, graph_reps=20):
+def even_lengths(total, requests):
+    """Rows per request of a step of `total` rows over `requests` requests, spread as evenly as
+    the reference's profiled decode shapes spread them (snowllm/engine/spec_decode.py:149-156)."""
+    q, rem = divmod(total, requests)
+    return [q + 1] * rem + [q] * (requests - rem)
+
+
+def profile_step_costs(source, rows, *, requests=1, draft_seconds=0.0, seed=0, reps=5,
+                       graph_reps=20):
     """StepCost of this build's verify step (snowllm_amd.verify.VerifyModel.forward) on the
-    weights of the VerifyModel `source`, for one sequence of n query rows at the source's
-    context, for each n in `rows`: the eager time and the time of one replay of the step
-    captured as a HIP graph (the reference's snowllm/engine/dspark_profile.py measures its
-    engine the same two ways)."""
+    weights of the VerifyModel `source`, for `requests` sequences of n query rows in all (spread
+    by even_lengths) at the source's context, for each n in `rows`: the eager time and the time
+    of one replay of the step captured as a HIP graph (the reference's
+    snowllm/engine/dspark_profile.py measures its engine the same two ways, one cost table per
+    request count)."""
     import torch
     from dataclasses import replace
     from .verify import VerifyModel
     eager, graphs = {}, {}
     for n in rows:
-        m = VerifyModel(replace(source.cfg, block=n, tree_parents=()), seed=seed,
-                        weights=share_weights(source))
-        m.set_block(torch.arange(n) * 7 + 1)
+        if n < requests:
+            raise ValueError(f"{n} rows cannot hold {requests} requests")
+        lengths = even_lengths(n, requests)
+        T = max(lengths)
+        m = VerifyModel(replace(source.cfg, block=T, tree_parents=()), seed=seed,
+                        weights=share_weights(source), batch=requests)
+        ids = (torch.arange(requests * T) * 7 + 1).view(requests, T)
+        if requests == 1:
+            m.set_block(ids[0])
+        else:
+            m.set_batch(ids, [source.cfg.context] * requests, lengths)
         m.forward()
         eager[n] = _median_seconds(m.forward, reps)
         stream = torch.cuda.Stream()

@@ -121,3 +121,18 @@ def test_against_brute_force():
             assert lengths[r] <= limits[r]
     assert list(itertools.islice(S.ranked_prefixes([[.5, .5]], [2]), 2)) == [(.5, 0, 0),
                                                                         (.25, 0, 1)]
+
+
+def test_even_lengths_match_the_reference_decode_shapes():
+    """Rows per request of a profiled batch step: the spread of the reference's decode shapes
+    (snowllm/engine/spec_decode.py:149-156: (q + 1,) * rem + (q,) * (n - rem))."""
+    from snowllm_amd.dspark_schedule import even_lengths
+    assert even_lengths(9, 1) == [9]
+    assert even_lengths(36, 4) == [9, 9, 9, 9]
+    assert even_lengths(10, 4) == [3, 3, 2, 2]
+    assert even_lengths(4, 4) == [1, 1, 1, 1]
+    for total in range(3, 80):
+        for n in range(1, min(total, 8) + 1):
+            got = even_lengths(total, n)
+            assert sum(got) == total and len(got) == n and max(got) - min(got) <= 1
+            assert got == sorted(got, reverse=True)
