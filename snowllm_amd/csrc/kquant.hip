@@ -161,7 +161,7 @@ __device__ __forceinline__ floatx4 apply_sb(const DecodedSb<FMT>& d, const half8
   return acc;
 }
 
-template <int FMT, int NW, int MT>
+template <int FMT, int NW, int MT, int NT = 1>
 __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restrict__ quant,
                                                           const u32x4* __restrict__ meta,
                                                           const void* __restrict__ ws,
@@ -169,12 +169,12 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
                                                           int S, int c_bf16, size_t tile_bytes,
                                                           int ldc) {
   constexpr int QV = QLayout<FMT>::kQuantVecs;
-  __shared__ floatx4 part[NW][1][64];
+  __shared__ floatx4 part[NW][NT][64];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kq = lane >> 4, r = lane & 15;
   const int tiles = N / TILE_N;
-  const int tile = blockIdx.x;
+  const int tile0 = blockIdx.x * NT;  // NT column tiles share each row tile's operands
   const int m0 = blockIdx.y * MT;
   const int row_tiles = (M + TILE_M - 1) / TILE_M;
   const int mt = row_tiles - m0 < MT ? row_tiles - m0 : MT;
@@ -190,14 +190,19 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
     vx[m] = r < M - (m0 + m) * TILE_M ? lane * 16 : 0x80000000u;
   }
   const uint32_t Mv = decode_magic<FMT>();
-  floatx4 acc[MT];
+  floatx4 acc[MT][NT];
 #pragma unroll
-  for (int m = 0; m < MT; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[m][t] = floatx4{0.f, 0.f, 0.f, 0.f};
   for (int s = w; s < S; s += NW) {
-    u32x4 q[1][QV], mt4[1];
-    uint32_t dq[1] = {0u};
-    load_sb_w<FMT, 1>(q, mt4, st, s, S, tile, 1);
-    if constexpr (FMT == FMT_Q6_K) load_sb_d<1>(dq, st, s, S, tile, 1);
+    // (a tile past the last reads nothing: its buffer offsets are out of range)
+    u32x4 q[NT][QV], mt4[NT];
+    uint32_t dq[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) dq[t] = 0u;
+    load_sb_w<FMT, NT>(q, mt4, st, s, S, tile0, 1);
+    if constexpr (FMT == FMT_Q6_K) load_sb_d<NT>(dq, st, s, S, tile0, 1);
     // every row tile's operands of this superblock in flight with the weights
     u32x4 x[MT][8];
     float sx0[MT], sx1[MT];
@@ -211,29 +216,33 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
       sx1[m] = bload1(sxr[m], lane * 4, (uint32_t)((s * 2 + 1) * 64 * 4));
       sc[m] = __builtin_bit_cast(floatx4, bload4(scr[m], kq * 16, (uint32_t)(s * 16 * 4)));
     }
-    if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q8_0) {
-      DecodedSb<FMT> d;
-      decode_sb<FMT>(q[0], mt4[0], kq, Mv, d);
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m >= mt) break;  // uniform
-        half8 xa[8];
+    for (int t = 0; t < NT; ++t) {
+      if constexpr (FMT == FMT_Q4_K || FMT == FMT_Q8_0) {
+        DecodedSb<FMT> d;
+        decode_sb<FMT>(q[t], mt4[t], kq, Mv, d);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x[m][j]);
-        const floatx4 sb = apply_sb<FMT>(d, xa, sx0[m], sx1[m]);
-        acc[m] += sb * sc[m];
-      }
-    } else {
-      // Q5_K / Q6_K: the weights loaded once, decoded again for each row tile by the 16-row
-      // kernel's own routine (their decoded operands do not fit the registers of four tiles)
+        for (int m = 0; m < MT; ++m) {
+          if (m >= mt) break;  // uniform
+          half8 xa[8];
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m >= mt) break;  // uniform
-        half8 xa[8];
+          for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x[m][j]);
+          const floatx4 sb = apply_sb<FMT>(d, xa, sx0[m], sx1[m]);
+          acc[m][t] += sb * sc[m];
+        }
+      } else {
+        // Q5_K / Q6_K: the weights loaded once, decoded again for each row tile by the 16-row
+        // kernel's own routine (their decoded operands do not fit the registers of four tiles)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x[m][j]);
-        const floatx4 sb = tile_superblock<FMT>(q[0], mt4[0], dq[0], xa, sx0[m], sx1[m], kq, Mv);
-        acc[m] += sb * sc[m];
+        for (int m = 0; m < MT; ++m) {
+          if (m >= mt) break;  // uniform
+          half8 xa[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x[m][j]);
+          const floatx4 sb =
+              tile_superblock<FMT>(q[t], mt4[t], dq[t], xa, sx0[m], sx1[m], kq, Mv);
+          acc[m][t] += sb * sc[m];
+        }
       }
     }
   }
@@ -241,12 +250,14 @@ __global__ void __launch_bounds__(NW * 64) kquant_gemv_mt(const u32x4* __restric
   for (int m = 0; m < MT; ++m) {
     if (m >= mt) break;  // uniform
     if (m) __syncthreads();
-    combine_waves<1, NW>(part, &acc[m], w, lane);
-    if (threadIdx.x < 64) {
-      const int l = threadIdx.x;
-      floatx4 v = part[0][0][l];
+    combine_waves<NT, NW>(part, acc[m], w, lane);
+    for (int idx = threadIdx.x; idx < NT * 64; idx += NW * 64) {
+      const int t = idx >> 6, l = idx & 63;
+      const int tile = tile0 + t;
+      if (tile >= tiles) continue;
+      floatx4 v = part[0][t][l];
 #pragma unroll
-      for (int ww = 1; ww < NW; ++ww) v += part[ww][0][l];
+      for (int ww = 1; ww < NW; ++ww) v += part[ww][t][l];
       const int n = tile * TILE_N + (l & 15);
       const int rb = (m0 + m) * TILE_M + 4 * (l >> 4);
 #pragma unroll
@@ -266,16 +277,28 @@ int launch_gemv_mt(const void* quant, const void* meta, const void* ws, void* c,
   const int tiles = N / TILE_N;
   const int row_tiles = (M + TILE_M - 1) / TILE_M;
   const size_t tb = xprep_tile_bytes(S);
-  auto go = [&](auto kern, int mt) {
-    hipLaunchKernelGGL(kern, dim3(tiles, (row_tiles + mt - 1) / mt), dim3(NW * 64), 0, s,
-                       (const u32x4*)quant, (const u32x4*)meta, ws, c, M, N, S, c_bf16, tb, ldc);
+  // two column tiles per workgroup halve the row tiles' operand loads (every workgroup reads
+  // all of them) where 160 or more workgroups remain (measured on MI355X at 36 rows:
+  // 5120 x 2048 10.7 -> 7.7 us, 6144 x 4096 18.3 -> 11.8 us; at 128 or 256 tiles one tile per
+  // workgroup stays faster, 2048 x 4096 8.0 against 10.2 us). The same bits either way.
+  const int nt = tiles >= 320 ? 2 : 1;
+  auto go = [&](auto kern, int mt, int ntile) {
+    hipLaunchKernelGGL(kern, dim3((tiles + ntile - 1) / ntile, (row_tiles + mt - 1) / mt),
+                       dim3(NW * 64), 0, s, (const u32x4*)quant, (const u32x4*)meta, ws, c, M,
+                       N, S, c_bf16, tb, ldc);
   };
   if constexpr (FMT == FMT_Q6_K) {
-    go(kquant_gemv_mt<FMT, NW, 2>, 2);  // Q6_K's three tiles of operands spill the registers
+    go(kquant_gemv_mt<FMT, NW, 2>, 2, 1);  // Q6_K's three tiles of operands spill the registers
   } else {
-    if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2>, 2);
-    else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3>, 3);
-    else go(kquant_gemv_mt<FMT, NW, 4>, 4);
+    if (nt == 2) {
+      if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2, 2>, 2, 2);
+      else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3, 2>, 3, 2);
+      else go(kquant_gemv_mt<FMT, NW, 4, 2>, 4, 2);
+    } else {
+      if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2>, 2, 1);
+      else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3>, 3, 1);
+      else go(kquant_gemv_mt<FMT, NW, 4>, 4, 1);
+    }
   }
   SV_CHECK_LAUNCH();
   return SV_OK;
