@@ -1184,9 +1184,12 @@ int launch_dense(const void* w, const void* act, void* c, int M, int N, int S, i
   const int tiles = (N + TILE_N - 1) / TILE_N;
   const int row_tiles = (M + TILE_M - 1) / TILE_M;
   const size_t tb = xprep_tile_bytes(S);
-  if (row_tiles == 1)
-    hipLaunchKernelGGL((dense_gemv<WT, NTILE, NW, 1>), dim3((tiles + NTILE - 1) / NTILE),
-                       dim3(NW * 64), 0, s, (const u32x4*)w, act, c, M, N, S, c_bf16, tb);
+  const int groups = (tiles + NTILE - 1) / NTILE;
+  if (row_tiles == 1 || groups < 64)
+    // one row tile per workgroup: a narrow output (the router's 17 tiles) then still has
+    // workgroups for several CUs (the same sums per row tile)
+    hipLaunchKernelGGL((dense_gemv<WT, NTILE, NW, 1>), dim3(groups, row_tiles), dim3(NW * 64), 0,
+                       s, (const u32x4*)w, act, c, M, N, S, c_bf16, tb);
   else if (row_tiles == 2)
     hipLaunchKernelGGL((dense_gemv<WT, NTILE, NW, 2>), dim3((tiles + NTILE - 1) / NTILE),
                        dim3(NW * 64), 0, s, (const u32x4*)w, act, c, M, N, S, c_bf16, tb);
