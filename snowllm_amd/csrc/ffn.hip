@@ -315,8 +315,8 @@ __global__ void dense_shuffle_kernel(const uint16_t* __restrict__ src, uint16_t*
 // ---------------------------------------------------------------------------------------
 constexpr int MOE_MAX_M = 64;       // block rows per plan
 constexpr int MOE_MAX_PICKS = 512;  // rows * topk per plan
-// routed slots <= unique experts + picks / 16 (an expert of c rows takes <= 1 + c / 16), then
-// the shared expert's ceil(M / 16)
+// routed slots <= unique experts + picks / 16 (an expert of c rows takes <= 1 + c / 16; one
+// slot each up to 16 rows), then the shared expert's ceil(M / 16)
 constexpr int MOE_MAX_SLOTS = 256 + MOE_MAX_PICKS / 16 + MOE_MAX_M / 16;  // 292
 struct MoePlan {
   int32_t n_slots;                         // routed slots + shared slots
@@ -331,7 +331,8 @@ struct MoePlan {
 // Slots a plan of M rows, topk picks each, can take (routed + shared).
 inline int64_t moe_plan_slots(int64_t M, int64_t topk, int64_t E, bool shared) {
   const int64_t picks = M * topk;
-  return std::min(E, picks) + picks / 16 + (shared ? (M + 15) / 16 : 0);
+  // up to 16 rows no expert takes a second slot
+  return std::min(E, picks) + (M > 16 ? picks / 16 : 0) + (shared ? (M + 15) / 16 : 0);
 }
 
 // Plan generation counter: every plan kernel takes the next value (skipping 0) for its plan.
@@ -559,16 +560,34 @@ __device__ __forceinline__ void plan_from_masks(const int32_t* ids_s, int M, int
                                                MoePlan* __restrict__ plan) {
   const int t = threadIdx.x, lane = t & 63;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-  uint64_t mk[4];
-  int base[4];  // first slot of expert lane + 64 i
-  int n_routed = 0;
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint64_t mk[4], bal[4];
+  int cnt[4];
+  bool multi = false;  // some expert routed more than 16 rows (uniform)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     mk[i] = lane + 64 * i < E ? mask[lane + 64 * i] : 0ull;
-    const int v = (__popcll(mk[i]) + 15) >> 4;
-    const int incl = wave_incl_sum(v, lane);
-    base[i] = n_routed + incl - v;
-    n_routed += __builtin_amdgcn_readlane(incl, 63);
+    bal[i] = __ballot(mk[i] != 0ull);
+    cnt[i] = __popcll(bal[i]);
+    if (M > 16) multi |= __ballot(__popcll(mk[i]) > 16) != 0ull;
+  }
+  int base[4];  // first slot of expert lane + 64 i
+  int n_routed = 0;
+  if (!multi) {
+    // one slot per used expert: the slot is the number of used experts below (ballots)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      base[i] = n_routed + __popcll(bal[i] & below);
+      n_routed += cnt[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = (__popcll(mk[i]) + 15) >> 4;
+      const int incl = wave_incl_sum(v, lane);
+      base[i] = n_routed + incl - v;
+      n_routed += __builtin_amdgcn_readlane(incl, 63);
+    }
   }
   const int n_shared = shared ? (M + 15) >> 4 : 0;
   if (w < 4) {
@@ -595,15 +614,25 @@ __device__ __forceinline__ void plan_from_masks(const int32_t* ids_s, int M, int
     // pick p: its row's position among the rows routed to its expert, then that position's slot
     const int p = t - 256;
     const int e = p < M * topk ? ids_s[p] : -1;
-    // every lane takes part in the exchanges; the slot base of expert e from lane e % 64 of
-    // group e / 64
-    const int src = e >= 0 ? (e & 63) : 0;
-    int bg[4];
+    int b = 0;  // the first slot of expert e
+    if (!multi) {
+      if (e >= 0 && e < E) {
+        const int g = e >> 6;
+        const uint64_t bg = g == 0 ? bal[0] : g == 1 ? bal[1] : g == 2 ? bal[2] : bal[3];
+        b = (g > 0 ? cnt[0] : 0) + (g > 1 ? cnt[1] : 0) + (g > 2 ? cnt[2] : 0) +
+            __popcll(bg & ((1ull << (e & 63)) - 1ull));
+      }
+    } else {
+      // every lane takes part in the exchanges: the base from lane e % 64 of group e / 64
+      const int src = e >= 0 ? (e & 63) : 0;
+      int bg[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) bg[i] = __shfl(base[i], src, 64);
+      for (int i = 0; i < 4; ++i) bg[i] = __shfl(base[i], src, 64);
+      const int g = e >= 0 ? e >> 6 : 0;
+      b = g == 0 ? bg[0] : g == 1 ? bg[1] : g == 2 ? bg[2] : bg[3];
+    }
     if (e >= 0 && e < E) {
-      const int g = e >> 6, r = p / topk;
-      const int b = g == 0 ? bg[0] : g == 1 ? bg[1] : g == 2 ? bg[2] : bg[3];
+      const int r = p / topk;
       const int pos = __popcll(mask[e] & ((1ull << r) - 1ull));
       const int sl = b + (pos >> 4);
       plan->row_of[sl][pos & 15] = r;
