@@ -152,6 +152,83 @@ def test_moe_without_norm_and_head(gpu, geometry_of, down_fmt):
         assert torch.equal(logits, want) and torch.equal(logits2, want)
 
 
+def test_moe_of_a_batch(gpu, geometry_of):
+    """snowllm_inference_moe over 36 rows (a batched verify step; one expert routed every row,
+    so it takes three slots) equals the explicit route/plan + experts launches bit for bit,
+    and the oracle's dequantised experts within tolerance."""
+    import numpy as np
+    from oracle import quant as Q
+    from snowllm_amd import layers as L
+    from snowllm_amd import ops
+    from snowllm_amd.verify import VerifyModel
+    cfg = tiny("moe")
+    geometry_of(cfg)
+    print("reference-signature MoE over 36 rows", flush=True)
+    m = VerifyModel(cfg, seed=12, keep_raw=True)
+    E, K, H, F = cfg.experts, cfg.topk, cfg.hidden, cfg.expert_ffn
+    M = 36
+    g = torch.Generator(device="cuda").manual_seed(3)
+    y = torch.randn(M, H, device="cuda", generator=g).bfloat16()
+    lw = m.layers[0]
+    # a router whose expert 2 wins every row: its slots hold 16, 16 and 4 rows
+    router = lw.raw["router"].clone()
+    router[2] = y.float().mean(0).bfloat16() * 50
+    rw = L.dense_shuffle(router)
+    out = torch.empty(M, H, dtype=torch.bfloat16, device="cuda")
+    mws = torch.empty(ops.inference_moe_workspace_bytes(M), dtype=torch.uint8, device="cuda")
+    gate = ops.KQuantExpertWeight(lw.gu[0], lw.gu[1], None, cfg.ffn_fmt)
+    down = ops.KQuantExpertWeight(lw.dn[0], lw.dn[1], None, cfg.ffn_fmt)
+    sh_gate = ops.KQuantProjWeight(lw.sh_gu[0], lw.sh_gu[1], cfg.ffn_fmt)
+    sh_down = ops.KQuantProjWeight(lw.sh_dn[0], lw.sh_dn[1], cfg.ffn_fmt)
+    ops.inference_moe(y, rw, gate, down, sh_gate, sh_down, out, mws)
+    ws = torch.empty(ops.gemm_kquant_a_ws_bytes(M, H), dtype=torch.uint8, device="cuda")
+    ops.gemm_kquant_prepare_a(y, ws)
+    logits = torch.empty(M, E + 1, device="cuda")
+    L.dense_gemv(L.WT_BF16, rw, y, logits, M, E + 1, H)
+    w = torch.empty(M, K, device="cuda")
+    ids = torch.empty(M, K, dtype=torch.int32, device="cuda")
+    sw = torch.empty(M, device="cuda")
+    plan = torch.empty(L.MOE_PLAN_BYTES, dtype=torch.uint8, device="cuda")
+    L.moe_route_plan(logits, E, K, w, ids, sw, plan)
+    act = torch.empty(L.moe_max_slots(M, K, E), 16, F, dtype=torch.bfloat16, device="cuda")
+    pairs = torch.empty(M * K, H, device="cuda")
+    shared = torch.empty(M, H, device="cuda")
+    want = torch.empty_like(out)
+    L.moe_experts(cfg.ffn_fmt, lw.gu, lw.dn, lw.sh_gu, lw.sh_dn, plan, ws, w, sw, act, pairs,
+                  shared, want, M, K, E, H, F)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    p = L.parse_plan(plan)
+    assert list(p["slot_expert"]).count(2) == 3 and list(p["slot_expert"]).count(E) == 3
+    # against the dequantised experts (fp64), rows as the kernels see them (bf16 products)
+    def bf(x):
+        return x.to(torch.bfloat16).double()
+    gub, dnb = lw.gu[2].cpu().numpy(), lw.dn[2].cpu().numpy()
+    gbytes, dbytes = gub.size // E, dnb.size // E
+    xc = y.cpu().double()
+    ref = torch.zeros(M, H, dtype=torch.float64)
+    cache = {}
+
+    def ffn(xr, gw, dw):
+        gg, uu = bf(xr @ gw[:F].T), bf(xr @ gw[F:].T)
+        return bf(bf(gg / (1 + torch.exp(-gg)) * uu) @ dw.T)
+    ids_c, w_c, sw_c = ids.cpu().long(), w.cpu().double(), sw.cpu().double()
+    for r in range(M):
+        for k in range(K):
+            e = int(ids_c[r, k])
+            if e not in cache:
+                cache[e] = (torch.from_numpy(Q.dequant(gub[e * gbytes:(e + 1) * gbytes], 4, 2 * F, H)).double(),
+                            torch.from_numpy(Q.dequant(dnb[e * dbytes:(e + 1) * dbytes], 4, H, F)).double())
+            ref[r] += w_c[r, k] * ffn(xc[r:r + 1], *cache[e])[0]
+    sg = torch.from_numpy(Q.dequant(lw.sh_gu[2].cpu().numpy(), 4, 2 * F, H)).double()
+    sd = torch.from_numpy(Q.dequant(lw.sh_dn[2].cpu().numpy(), 4, H, F)).double()
+    ref += sw_c[:, None] * ffn(xc, sg, sd)
+    err = ((out.cpu().double() - ref).norm() / ref.norm()).item()
+    print(f"  36-row MoE rel L2 {err:.2e}", flush=True)
+    assert err < 5e-3
+    assert np.isfinite(out.float().cpu().numpy()).all()
+
+
 def test_dense_mlp(gpu, geometry_of):
     from snowllm_amd import layers as L
     from snowllm_amd import ops
