@@ -110,3 +110,30 @@ def test_decode_plan_queries():
     lib.snowllm_prefill_q_block_map(lens, 3, m)
     assert list(m) == [0, 0, 1, 0, 1, 16, 2, 0, 2, 16]
     assert lib.snowllm_paged_attention_prepared_bytes(1, 9, 1, 0) == 0
+
+
+def test_moe_plan_layout_and_slot_bound():
+    """The host view of a MoE plan (layers.parse_plan) matches the library's struct, and the slot
+    bound is what the plan can take: one slot per used expert up to 16 rows; above, one per 16
+    rows of an expert and the shared expert's ceil(M / 16); 0 past 64 rows or 512 picks."""
+    from snowllm_amd import layers as L
+    from snowllm_amd._capi import lib
+    S = L.MOE_MAX_SLOTS
+    assert L.MOE_PLAN_BYTES == (2 + 2 * S + 2 * S * 16 + 1) * 4
+    bound = lib.snowverify_moe_max_slots
+    assert bound(9, 8, 256, 1) == 73 and bound(9, 8, 256, 0) == 72
+    assert bound(1, 8, 256, 1) == 9 and bound(16, 16, 256, 1) == 257
+    assert bound(36, 8, 256, 1) == 256 + 288 // 16 + 3
+    assert bound(64, 8, 256, 1) == S and bound(64, 8, 64, 0) == 64 + 32
+    assert bound(65, 8, 256, 1) == 0 and bound(64, 9, 256, 1) == 0 and bound(0, 8, 256, 1) == 0
+    # the bound holds for every routing: experts with c rows take ceil(c / 16) slots
+    import numpy as np
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        M, K, E = int(rng.integers(1, 65)), int(rng.integers(1, 9)), int(rng.integers(8, 257))
+        if M * K > 512 or K > E:
+            continue
+        ids = np.stack([rng.choice(E, K, replace=False) for _ in range(M)])
+        counts = np.bincount(ids.ravel(), minlength=E)
+        slots = int(((counts + 15) // 16).sum()) + (M + 15) // 16
+        assert slots <= bound(M, K, E, 1), (M, K, E)
