@@ -380,8 +380,9 @@ __device__ __forceinline__ void gather_rows(GemvStreams& st, const int32_t* rows
 // ---------------------------------------------------------------------------------------
 // bx: the block's pair group; slot: the plan slot (plan mode) or 0. DEVICE_SCOPE: the
 // activations are stored with device-scope stores (visible to other workgroups of the same
-// launch once the stores complete).
-template <int FMT, int WS, int PPB, bool DEVICE_SCOPE>
+// launch once the stores complete). SC: 0, or the superblock count S when the waves walk them
+// with three weight buffers each (gemv_loop_deep).
+template <int FMT, int WS, int PPB, bool DEVICE_SCOPE, int SC = 0>
 __device__ __forceinline__ void gate_up_body(
     int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
     int64_t gu_qbytes, int64_t gu_mbytes, const uint8_t* __restrict__ sh_quant,
@@ -411,9 +412,15 @@ __device__ __forceinline__ void gate_up_body(
     if (plan) {
       gather_rows(st, plan->row_of[slot], n_rows, lane, ws, S, (M + 15) >> 4,
                   (uint32_t)xprep_tile_bytes(S));
-      gemv_loop<FMT, 2, WS, true>(st, sw, S, pair, half_tiles, kq, Mv, acc);
+      if constexpr (SC > 0)
+        gemv_loop_deep<FMT, 2, SC / WS, true, WS>(st, sw, pair, half_tiles, kq, Mv, acc);
+      else
+        gemv_loop<FMT, 2, WS, true>(st, sw, S, pair, half_tiles, kq, Mv, acc);
     } else {
-      gemv_loop<FMT, 2, WS>(st, sw, S, pair, half_tiles, kq, Mv, acc);
+      if constexpr (SC > 0)
+        gemv_loop_deep<FMT, 2, SC / WS, false, WS>(st, sw, pair, half_tiles, kq, Mv, acc);
+      else
+        gemv_loop<FMT, 2, WS>(st, sw, S, pair, half_tiles, kq, Mv, acc);
     }
   }
   floatx4 g = acc[0], u = acc[1];
@@ -448,14 +455,29 @@ __device__ __forceinline__ void gate_up_body(
   }
 }
 
-template <int FMT, int WS, int PPB>
-__global__ void __launch_bounds__(WS * PPB * 64) gate_up_kernel(
+// The deep form (SC > 0) at two waves per SIMD: with a budget for more waves the compiler moves
+// the later superblocks' loads down to their use.
+template <int FMT, int WS, int PPB, int SC = 0>
+__global__ void __launch_bounds__(WS * PPB * 64)
+    __attribute__((amdgpu_waves_per_eu(SC > 0 ? 2 : 1, SC > 0 ? 2 : 10))) gate_up_kernel(
     const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t gu_qbytes,
     int64_t gu_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
     const MoePlan* __restrict__ plan, int E, const void* __restrict__ ws,
     uint16_t* __restrict__ act_out, int M, int F, int S) {
-  gate_up_body<FMT, WS, PPB, false>(blockIdx.x, blockIdx.y, quant, meta, gu_qbytes, gu_mbytes,
-                                    sh_quant, sh_meta, plan, E, ws, act_out, M, F, S);
+  gate_up_body<FMT, WS, PPB, false, SC>(blockIdx.x, blockIdx.y, quant, meta, gu_qbytes,
+                                        gu_mbytes, sh_quant, sh_meta, plan, E, ws, act_out, M, F,
+                                        S);
+}
+
+// The gate/up loop by superblock count S: at S = 8 or 16 (hidden 2048 or 4096) each of a pair's
+// two waves walks its S / 2 superblocks with the weights of the next two in flight behind the
+// one it multiplies (gemv_loop_deep, unrolled), otherwise gemv_loop's one. The same sums in the
+// same order either way.
+template <class Fn>
+void with_gu_depth(int64_t S, Fn&& fn) {
+  if (S == 8) fn(std::integral_constant<int, 8>{});
+  else if (S == 16) fn(std::integral_constant<int, 16>{});
+  else fn(std::integral_constant<int, 0>{});
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1116,8 +1138,8 @@ constexpr uint32_t MOE_WAIT_POLLS = 1u << 20;  // ~0.1 s: far beyond any gate/up
 
 // Three waves per SIMD when the down items take one superblock per wave (the gate/up items then
 // bound the registers at 168); two otherwise.
-template <int FMT, int DN_FMT, int GU_WS, int GU_PPB, int DN_NTILE, int DN_WS, int DN_GPB,
-          bool ONE_SB, int WAVES = (ONE_SB ? 3 : 2)>
+template <int FMT, int DN_FMT, int GU_WS, int GU_PPB, int GU_SC, int DN_NTILE, int DN_WS,
+          int DN_GPB, bool ONE_SB, int WAVES = (ONE_SB ? 3 : 2)>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) moe_experts_kernel(
     // first the arguments of the plan read and the gate/up weight addresses: the first 56
     // bytes arrive preloaded in SGPRs
@@ -1138,7 +1160,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES,
   if (item < n_gu) {
     const int slot = item / gu_per_slot;
     if (slot >= n_slots) return;
-    gate_up_body<FMT, GU_WS, GU_PPB, true>(item % gu_per_slot, slot, gu_quant, gu_meta,
+    gate_up_body<FMT, GU_WS, GU_PPB, true, GU_SC>(item % gu_per_slot, slot, gu_quant, gu_meta,
                                            gu_qbytes, gu_mbytes, sh_gu_quant, sh_gu_meta, plan,
                                            E, ws, act, M, F, H / QK);
     // every wave waits for its own activation stores to complete (the barrier alone does not
@@ -1358,15 +1380,18 @@ SV_API int snowverify_gate_up_swiglu(int fmt, const void* quant, const void* met
   // 3.266 -> 3.182 ms; eight waves per pair: 26.2 us)
   constexpr int WS = 2, PPB = 2;
   const dim3 grid((unsigned)((F / 16 + PPB - 1) / PPB), 1);
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, dim3(64 * WS * PPB), 0, s, (const uint8_t*)quant,
-                       (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr, 0, ws,
-                       (uint16_t*)act, (int)M, (int)F, S);
-  };
-  if (fmt == 4) go(gate_up_kernel<4, WS, PPB>);
-  else if (fmt == 5) go(gate_up_kernel<5, WS, PPB>);
-  else if (fmt == 6) go(gate_up_kernel<6, WS, PPB>);
-  else go(gate_up_kernel<8, WS, PPB>);
+  with_gu_depth(S, [&](auto sc_c) {
+    constexpr int SC = decltype(sc_c)::value;
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, grid, dim3(64 * WS * PPB), 0, s, (const uint8_t*)quant,
+                         (const uint8_t*)meta, 0, 0, nullptr, nullptr, nullptr, 0, ws,
+                         (uint16_t*)act, (int)M, (int)F, S);
+    };
+    if (fmt == 4) go(gate_up_kernel<4, WS, PPB, SC>);
+    else if (fmt == 5) go(gate_up_kernel<5, WS, PPB, SC>);
+    else if (fmt == 6) go(gate_up_kernel<6, WS, PPB, SC>);
+    else go(gate_up_kernel<8, WS, PPB, SC>);
+  });
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1451,17 +1476,20 @@ SV_API int snowverify_moe_gate_up(int fmt, const void* gu_quant, const void* gu_
       max_slots > MOE_MAX_SLOTS || H % 256 || F % 256)
     return SV_EINVAL;
   const int64_t gu_q = packed_quant(fmt, 2 * F, H), gu_m = packed_meta(fmt, 2 * F, H);
-  const dim3 grid((unsigned)((F / 16 + MOE_GU_PPB - 1) / MOE_GU_PPB), (unsigned)max_slots);
-  auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, dim3(64 * MOE_GU_WS * MOE_GU_PPB), 0, Sx(stream),
-                       (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
-                       (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
-                       (const MoePlan*)plan, (int)E, ws, (uint16_t*)act, (int)M, (int)F,
-                       (int)(H / 256));
-  };
-  if (fmt == 4) go(gate_up_kernel<4, MOE_GU_WS, MOE_GU_PPB>);
-  else if (fmt == 5) go(gate_up_kernel<5, MOE_GU_WS, MOE_GU_PPB>);
-  else go(gate_up_kernel<6, MOE_GU_WS, MOE_GU_PPB>);
+  with_gu_depth(H / 256, [&](auto sc_c) {
+    constexpr int SC = decltype(sc_c)::value;
+    const dim3 grid((unsigned)(F / 16 / MOE_GU_PPB), (unsigned)max_slots);
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, grid, dim3(64 * MOE_GU_WS * MOE_GU_PPB), 0, Sx(stream),
+                         (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
+                         (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
+                         (const MoePlan*)plan, (int)E, ws, (uint16_t*)act, (int)M, (int)F,
+                         (int)(H / 256));
+    };
+    if (fmt == 4) go(gate_up_kernel<4, MOE_GU_WS, MOE_GU_PPB, SC>);
+    else if (fmt == 5) go(gate_up_kernel<5, MOE_GU_WS, MOE_GU_PPB, SC>);
+    else go(gate_up_kernel<6, MOE_GU_WS, MOE_GU_PPB, SC>);
+  });
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -1534,12 +1562,15 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
   auto pick = [&](auto gu, auto dn) {
     constexpr int G = decltype(gu)::value, D = decltype(dn)::value;
     constexpr bool q4 = G == 4 && D == 4;
-    if (F / QK == MOE_DN_WS)
-      launch(moe_experts_kernel<G, D, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
-                                true, q4 ? 3 : 2>);
-    else
-      launch(moe_experts_kernel<G, D, MOE_GU_WS, MOE_GU_PPB, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
-                                false, 2>);
+    with_gu_depth(H / QK, [&](auto sc) {
+      constexpr int SC = decltype(sc)::value;
+      if (F / QK == MOE_DN_WS)
+        launch(moe_experts_kernel<G, D, MOE_GU_WS, MOE_GU_PPB, SC, MOE_DN_NTILE, MOE_DN_WS,
+                                  MOE_DN_GPB, true, q4 ? 3 : 2>);
+      else
+        launch(moe_experts_kernel<G, D, MOE_GU_WS, MOE_GU_PPB, SC, MOE_DN_NTILE, MOE_DN_WS,
+                                  MOE_DN_GPB, false, 2>);
+    });
     return SV_OK;
   };
   using I4 = std::integral_constant<int, 4>;

@@ -588,6 +588,44 @@ __device__ __forceinline__ void gemv_loop(const GemvStreams& st, int w, int S, i
   }
 }
 
+// Wave w of NW walks SC superblocks (w, w + NW, ...) of the tiles tile0 + t * tstride with the
+// weights of the next two in flight while one is multiplied (three weight buffers), and the
+// activation operands, which come from L2, loaded one superblock at a time after the previous
+// superblock's products have read them. Unrolled (SC a compile-time count) so that no load
+// sits under a branch, which would make the compiler wait for every load in flight at the
+// join.
+template <int FMT, int NTILE, int SC, bool GATHER = false, int NW = 1>
+__device__ __forceinline__ void gemv_loop_deep(const GemvStreams& st, int w, int tile0,
+                                               int tstride, int kq, uint32_t Mv, floatx4* acc) {
+  SbOperands<FMT, NTILE> x;  // the activation part
+  u32x4 q[3][NTILE][QLayout<FMT>::kQuantVecs];
+  u32x4 m[3][NTILE];
+  uint32_t dq[3][NTILE];
+  // step i multiplies superblock w + NW i of the SC * NW
+  auto load_w = [&](int b, int i) {
+    load_sb_w<FMT, NTILE>(q[b], m[b], st, w + NW * i, SC * NW, tile0, tstride);
+    if constexpr (FMT == FMT_Q6_K) load_sb_d<NTILE>(dq[b], st, w + NW * i, SC * NW, tile0, tstride);
+  };
+  load_w(0, 0);
+  load_sb_x<FMT, NTILE, GATHER>(x, st, w);
+  if constexpr (SC > 1) load_w(1, 1);
+  if constexpr (SC > 2) load_w(2, 2);
+#pragma unroll
+  for (int s = 0; s < SC; ++s) {
+    const int b = s % 3;
+    half8 xa[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xa[j] = __builtin_bit_cast(half8, x.x[j]);
+#pragma unroll
+    for (int t = 0; t < NTILE; ++t) {
+      floatx4 sb = tile_superblock<FMT>(q[b][t], m[b][t], dq[b][t], xa, x.sx0, x.sx1, kq, Mv);
+      acc[t] += sb * x.scale;
+    }
+    if (s + 1 < SC) load_sb_x<FMT, NTILE, GATHER>(x, st, w + NW * (s + 1));
+    if (s + 3 < SC) load_w(b, s + 3);
+  }
+}
+
 // Variant for bf16 activations read straight from [M, K] (no operand workspace): the raw words
 // of superblock s are loaded with the weights and converted at multiply time (the same
 // per-(row, superblock) power-of-two conversion as the workspace path, so results match it).
