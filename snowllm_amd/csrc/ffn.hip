@@ -381,8 +381,10 @@ __device__ __forceinline__ void gather_rows(GemvStreams& st, const int32_t* rows
 // bx: the block's pair group; slot: the plan slot (plan mode) or 0. DEVICE_SCOPE: the
 // activations are stored with device-scope stores (visible to other workgroups of the same
 // launch once the stores complete). SC: 0, or the superblock count S when the waves walk them
-// with three weight buffers each (gemv_loop_deep).
-template <int FMT, int WS, int PPB, bool DEVICE_SCOPE, int SC = 0>
+// with three weight buffers each (gemv_loop_deep). VW: with WS = 1, the number of waves the
+// one wave stands for (it keeps their partial sums and adds them in their order: VW = 2 gives
+// the bits of WS = 2).
+template <int FMT, int WS, int PPB, bool DEVICE_SCOPE, int SC = 0, int VW = 1>
 __device__ __forceinline__ void gate_up_body(
     int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
     int64_t gu_qbytes, int64_t gu_mbytes, const uint8_t* __restrict__ sh_quant,
@@ -407,23 +409,31 @@ __device__ __forceinline__ void gate_up_body(
   }
   GemvStreams st = make_streams<FMT>(q, m, ws, 2 * half_tiles, S, lane, M);
   const uint32_t Mv = decode_magic<FMT>();
-  floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+  static_assert(VW == 1 || (WS == 1 && SC > 0), "virtual waves: one wave, the deep loop");
+  floatx4 acc[2 * VW];
+#pragma unroll
+  for (int i = 0; i < 2 * VW; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
   if (pair < half_tiles) {
     if (plan) {
       gather_rows(st, plan->row_of[slot], n_rows, lane, ws, S, (M + 15) >> 4,
                   (uint32_t)xprep_tile_bytes(S));
       if constexpr (SC > 0)
-        gemv_loop_deep<FMT, 2, SC / WS, true, WS>(st, sw, pair, half_tiles, kq, Mv, acc);
+        gemv_loop_deep<FMT, 2, SC / WS, true, WS, VW>(st, sw, pair, half_tiles, kq, Mv, acc);
       else
         gemv_loop<FMT, 2, WS, true>(st, sw, S, pair, half_tiles, kq, Mv, acc);
     } else {
       if constexpr (SC > 0)
-        gemv_loop_deep<FMT, 2, SC / WS, false, WS>(st, sw, pair, half_tiles, kq, Mv, acc);
+        gemv_loop_deep<FMT, 2, SC / WS, false, WS, VW>(st, sw, pair, half_tiles, kq, Mv, acc);
       else
         gemv_loop<FMT, 2, WS>(st, sw, S, pair, half_tiles, kq, Mv, acc);
     }
   }
   floatx4 g = acc[0], u = acc[1];
+#pragma unroll
+  for (int v = 1; v < VW; ++v) {  // the virtual waves' partials in the order WS waves add them
+    g += acc[2 * v];
+    u += acc[2 * v + 1];
+  }
   if constexpr (WS > 1) {
     part[pl][sw][0][lane] = acc[0];
     part[pl][sw][1][lane] = acc[1];
@@ -457,16 +467,16 @@ __device__ __forceinline__ void gate_up_body(
 
 // The deep form (SC > 0) at two waves per SIMD: with a budget for more waves the compiler moves
 // the later superblocks' loads down to their use.
-template <int FMT, int WS, int PPB, int SC = 0>
+template <int FMT, int WS, int PPB, int SC = 0, int VW = 1>
 __global__ void __launch_bounds__(WS * PPB * 64)
     __attribute__((amdgpu_waves_per_eu(SC > 0 ? 2 : 1, SC > 0 ? 2 : 10))) gate_up_kernel(
     const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t gu_qbytes,
     int64_t gu_mbytes, const uint8_t* __restrict__ sh_quant, const uint8_t* __restrict__ sh_meta,
     const MoePlan* __restrict__ plan, int E, const void* __restrict__ ws,
     uint16_t* __restrict__ act_out, int M, int F, int S) {
-  gate_up_body<FMT, WS, PPB, false, SC>(blockIdx.x, blockIdx.y, quant, meta, gu_qbytes,
-                                        gu_mbytes, sh_quant, sh_meta, plan, E, ws, act_out, M, F,
-                                        S);
+  gate_up_body<FMT, WS, PPB, false, SC, VW>(blockIdx.x, blockIdx.y, quant, meta, gu_qbytes,
+                                            gu_mbytes, sh_quant, sh_meta, plan, E, ws, act_out,
+                                            M, F, S);
 }
 
 // The gate/up loop by superblock count S: at S = 8 or 16 (hidden 2048 or 4096) each of a pair's
@@ -478,6 +488,24 @@ void with_gu_depth(int64_t S, Fn&& fn) {
   if (S == 8) fn(std::integral_constant<int, 8>{});
   else if (S == 16) fn(std::integral_constant<int, 16>{});
   else fn(std::integral_constant<int, 0>{});
+}
+
+// MoE gate/up item shape: fn(WS, PPB, SC, VW) as integral constants. A launch of 64 or more
+// slots (a block of 8 or more rows) at hidden 2048 runs one wave per pair standing for the two
+// (gemv_loop_deep with VW = 2, the same bits): its 16 or more slots' items fit one round of
+// resident waves, so no gate/up item starts late; fewer slots keep two waves per pair, whose
+// walk is half as long.
+template <class Fn>
+void with_gu_shape(int64_t S, int64_t max_slots, Fn&& fn) {
+  using std::integral_constant;
+  if (S == 8 && max_slots >= 64)
+    fn(integral_constant<int, 1>{}, integral_constant<int, 4>{}, integral_constant<int, 8>{},
+       integral_constant<int, 2>{});
+  else
+    with_gu_depth(S, [&](auto sc) {
+      fn(integral_constant<int, 2>{}, integral_constant<int, 2>{}, sc,
+         integral_constant<int, 1>{});
+    });
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1138,8 +1166,8 @@ constexpr uint32_t MOE_WAIT_POLLS = 1u << 20;  // ~0.1 s: far beyond any gate/up
 
 // Three waves per SIMD when the down items take one superblock per wave (the gate/up items then
 // bound the registers at 168); two otherwise.
-template <int FMT, int DN_FMT, int GU_WS, int GU_PPB, int GU_SC, int DN_NTILE, int DN_WS,
-          int DN_GPB, bool ONE_SB, int WAVES = (ONE_SB ? 3 : 2)>
+template <int FMT, int DN_FMT, int GU_WS, int GU_PPB, int GU_SC, int GU_VW, int DN_NTILE,
+          int DN_WS, int DN_GPB, bool ONE_SB, int WAVES = (ONE_SB ? 3 : 2)>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) moe_experts_kernel(
     // first the arguments of the plan read and the gate/up weight addresses: the first 56
     // bytes arrive preloaded in SGPRs
@@ -1160,7 +1188,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES,
   if (item < n_gu) {
     const int slot = item / gu_per_slot;
     if (slot >= n_slots) return;
-    gate_up_body<FMT, GU_WS, GU_PPB, true, GU_SC>(item % gu_per_slot, slot, gu_quant, gu_meta,
+    gate_up_body<FMT, GU_WS, GU_PPB, true, GU_SC, GU_VW>(item % gu_per_slot, slot, gu_quant, gu_meta,
                                            gu_qbytes, gu_mbytes, sh_gu_quant, sh_gu_meta, plan,
                                            E, ws, act, M, F, H / QK);
     // every wave waits for its own activation stores to complete (the barrier alone does not
@@ -1476,19 +1504,20 @@ SV_API int snowverify_moe_gate_up(int fmt, const void* gu_quant, const void* gu_
       max_slots > MOE_MAX_SLOTS || H % 256 || F % 256)
     return SV_EINVAL;
   const int64_t gu_q = packed_quant(fmt, 2 * F, H), gu_m = packed_meta(fmt, 2 * F, H);
-  with_gu_depth(H / 256, [&](auto sc_c) {
-    constexpr int SC = decltype(sc_c)::value;
-    const dim3 grid((unsigned)(F / 16 / MOE_GU_PPB), (unsigned)max_slots);
+  with_gu_shape(H / 256, max_slots, [&](auto ws_c, auto ppb_c, auto sc_c, auto vw_c) {
+    constexpr int WS = decltype(ws_c)::value, PPB = decltype(ppb_c)::value,
+                  SC = decltype(sc_c)::value, VW = decltype(vw_c)::value;
+    const dim3 grid((unsigned)(F / 16 / PPB), (unsigned)max_slots);
     auto go = [&](auto kern) {
-      hipLaunchKernelGGL(kern, grid, dim3(64 * MOE_GU_WS * MOE_GU_PPB), 0, Sx(stream),
+      hipLaunchKernelGGL(kern, grid, dim3(64 * WS * PPB), 0, Sx(stream),
                          (const uint8_t*)gu_quant, (const uint8_t*)gu_meta, gu_q, gu_m,
                          (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
                          (const MoePlan*)plan, (int)E, ws, (uint16_t*)act, (int)M, (int)F,
                          (int)(H / 256));
     };
-    if (fmt == 4) go(gate_up_kernel<4, MOE_GU_WS, MOE_GU_PPB, SC>);
-    else if (fmt == 5) go(gate_up_kernel<5, MOE_GU_WS, MOE_GU_PPB, SC>);
-    else go(gate_up_kernel<6, MOE_GU_WS, MOE_GU_PPB, SC>);
+    if (fmt == 4) go(gate_up_kernel<4, WS, PPB, SC, VW>);
+    else if (fmt == 5) go(gate_up_kernel<5, WS, PPB, SC, VW>);
+    else go(gate_up_kernel<6, WS, PPB, SC, VW>);
   });
   SV_CHECK_LAUNCH();
   return SV_OK;
@@ -1543,11 +1572,11 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
     return SV_EINVAL;
   const int64_t gu_q = packed_quant(gu_fmt, 2 * F, H), gu_m = packed_meta(gu_fmt, 2 * F, H);
   const int64_t dn_q = packed_quant(dn_fmt, H, F), dn_m = packed_meta(dn_fmt, H, F);
-  const int gu_per_slot = (int)(F / 16 / MOE_GU_PPB);
   const int dn_per_slot = (int)(H / 16 / MOE_DN_NTILE / MOE_DN_GPB);
-  if (gu_per_slot > MOE_MAX_ITEMS || dn_per_slot > MOE_MAX_ITEMS) return SV_ENOTSUP;
-  const int64_t blocks = (int64_t)(gu_per_slot + dn_per_slot) * max_slots;
-  auto launch = [&](auto kern) {
+  if (F / 16 / MOE_GU_PPB > MOE_MAX_ITEMS || dn_per_slot > MOE_MAX_ITEMS) return SV_ENOTSUP;
+  // gu_per_slot: F / 16 pairs over the item shape's pairs per block (at most MOE_GU_PPB's)
+  auto launch = [&](auto kern, int gu_per_slot) {
+    const int64_t blocks = (int64_t)(gu_per_slot + dn_per_slot) * max_slots;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, Sx(stream),
                        (const MoePlan*)plan, (const uint8_t*)gu_quant, (const uint8_t*)gu_meta,
                        gu_q, gu_m, gu_per_slot, dn_per_slot, (int)max_slots, (int)E,
@@ -1562,14 +1591,17 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
   auto pick = [&](auto gu, auto dn) {
     constexpr int G = decltype(gu)::value, D = decltype(dn)::value;
     constexpr bool q4 = G == 4 && D == 4;
-    with_gu_depth(H / QK, [&](auto sc) {
-      constexpr int SC = decltype(sc)::value;
+    with_gu_shape(H / QK, max_slots, [&](auto ws_c, auto ppb_c, auto sc_c, auto vw_c) {
+      constexpr int WS = decltype(ws_c)::value, PPB = decltype(ppb_c)::value,
+                    SC = decltype(sc_c)::value, VW = decltype(vw_c)::value;
       if (F / QK == MOE_DN_WS)
-        launch(moe_experts_kernel<G, D, MOE_GU_WS, MOE_GU_PPB, SC, MOE_DN_NTILE, MOE_DN_WS,
-                                  MOE_DN_GPB, true, q4 ? 3 : 2>);
+        launch(moe_experts_kernel<G, D, WS, PPB, SC, VW, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
+                                  true, q4 ? 3 : 2>,
+               (int)(F / 16 / PPB));
       else
-        launch(moe_experts_kernel<G, D, MOE_GU_WS, MOE_GU_PPB, SC, MOE_DN_NTILE, MOE_DN_WS,
-                                  MOE_DN_GPB, false, 2>);
+        launch(moe_experts_kernel<G, D, WS, PPB, SC, VW, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
+                                  false, 2>,
+               (int)(F / 16 / PPB));
     });
     return SV_OK;
   };

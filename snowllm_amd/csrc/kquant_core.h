@@ -593,8 +593,9 @@ __device__ __forceinline__ void gemv_loop(const GemvStreams& st, int w, int S, i
 // activation operands, which come from L2, loaded one superblock at a time after the previous
 // superblock's products have read them. Unrolled (SC a compile-time count) so that no load
 // sits under a branch, which would make the compiler wait for every load in flight at the
-// join.
-template <int FMT, int NTILE, int SC, bool GATHER = false, int NW = 1>
+// join. VW > 1: step i adds into acc[(i % VW) * NTILE + t], the sums VW waves would keep, so
+// one wave can stand for VW of them with their bits.
+template <int FMT, int NTILE, int SC, bool GATHER = false, int NW = 1, int VW = 1>
 __device__ __forceinline__ void gemv_loop_deep(const GemvStreams& st, int w, int tile0,
                                                int tstride, int kq, uint32_t Mv, floatx4* acc) {
   SbOperands<FMT, NTILE> x;  // the activation part
@@ -619,7 +620,7 @@ __device__ __forceinline__ void gemv_loop_deep(const GemvStreams& st, int w, int
 #pragma unroll
     for (int t = 0; t < NTILE; ++t) {
       floatx4 sb = tile_superblock<FMT>(q[b][t], m[b][t], dq[b][t], xa, x.sx0, x.sx1, kq, Mv);
-      acc[t] += sb * x.scale;
+      acc[(s % VW) * NTILE + t] += sb * x.scale;
     }
     if (s + 1 < SC) load_sb_x<FMT, NTILE, GATHER>(x, st, w + NW * (s + 1));
     if (s + 3 < SC) load_w(b, s + 3);
