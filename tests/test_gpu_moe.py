@@ -102,8 +102,9 @@ def test_gate_up_down_equals_separate_launches(gpu, E, F, gu_f, dn_f):
     # (rows, shared, routing): "spread" puts every row on its own experts (the most slots),
     # "hot" every row on expert 3 (one slot per 16 rows of it)
     cases = ((9, True, ""), (16, True, "spread"), (1, True, ""), (9, False, "spread"),
-             (9, True, "spread"), (36, True, "hot"), (64, True, "spread"), (40, False, "hot"))
-    for M, shared, route in cases if (gu_f, dn_f) == (4, 4) else cases[:2] + cases[5:6]:
+             (9, True, "spread"), (36, True, "hot"), (64, True, "spread"), (40, False, "hot"),
+             (4, True, "spread"))
+    for M, shared, route in cases if (gu_f, dn_f) == (4, 4) else cases[:3] + cases[5:6]:
         print(f"gate_up_down E={E} F={F} fmt={gu_f}/{dn_f} M={M} shared={shared} "
               f"routing={route}", flush=True)
         g = torch.Generator(device="cuda").manual_seed(70 + M)
@@ -124,16 +125,20 @@ def test_gate_up_down_equals_separate_launches(gpu, E, F, gu_f, dn_f):
         ns = L.moe_max_slots(M, K, E, shared)
         sg, sd = (sgu, sdn) if shared else ((None, None), (None, None))
         outs = []
-        for fused in (False, True, True):
-            act = torch.zeros(ns, 16, F, dtype=torch.bfloat16, device="cuda")
+        # the separate launches, the one-launch form twice, and both again with the largest
+        # slot bound: a launch of 64 or more slots runs each gate/up pair on one wave standing
+        # for two, which must give the bits of the two-wave form the smaller bounds take
+        for fused, bound in ((False, ns), (True, ns), (True, ns), (True, L.MOE_MAX_SLOTS),
+                             (False, L.MOE_MAX_SLOTS)):
+            act = torch.zeros(bound, 16, F, dtype=torch.bfloat16, device="cuda")
             pairs = torch.zeros(M * K, H, device="cuda")
             sh_out = torch.zeros(M, H, device="cuda")
             if fused:
                 L.moe_gate_up_down(gu_f | dn_f << 8, gu, dn, sg, sd, plan, ws, w, sw, act, pairs,
-                                   sh_out, M, ns, E, H, F)
+                                   sh_out, M, bound, E, H, F)
             else:
-                L.moe_gate_up(gu_f, gu, sg, plan, ws, act, M, ns, E, H, F)
-                L.moe_down(dn_f, dn, sd, plan, act, w, sw, pairs, sh_out, ns, E, H, F)
+                L.moe_gate_up(gu_f, gu, sg, plan, ws, act, M, bound, E, H, F)
+                L.moe_down(dn_f, dn, sd, plan, act, w, sw, pairs, sh_out, bound, E, H, F)
             torch.cuda.synchronize()
             outs.append((act, pairs, sh_out))
         p = L.parse_plan(plan)
