@@ -492,9 +492,10 @@ void with_gu_depth(int64_t S, Fn&& fn) {
 
 // MoE gate/up item shape: fn(WS, PPB, SC, VW) as integral constants. A launch of 64 or more
 // slots (a block of 8 or more rows) at hidden 2048 runs one wave per pair standing for the two
-// (gemv_loop_deep with VW = 2, the same bits): its 16 or more slots' items fit one round of
-// resident waves, so no gate/up item starts late; fewer slots keep two waves per pair, whose
-// walk is half as long.
+// (gemv_loop_deep with VW = 2, the same bits): 32 gate/up waves per slot instead of 64, so
+// that up to 96 slots' gate/up items are all resident at once (three waves per SIMD) and none
+// starts late. Smaller launches fit either way and keep two waves per pair, whose walk is half
+// as long.
 template <class Fn>
 void with_gu_shape(int64_t S, int64_t max_slots, Fn&& fn) {
   using std::integral_constant;
