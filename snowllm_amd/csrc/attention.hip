@@ -710,8 +710,11 @@ int device_cus() {
 // rounded up to an even count, since the pages go two per step and an odd split's last step
 // costs as much as a full one (measured: 26.1 -> 25.0 us per layer at 8K with 2 KV heads,
 // 5 -> 6 pages; 20.9 -> 20.5 us with 8 KV heads, 17 -> 18). Very short contexts keep at least
-// 6 pages per split (more splits only add merge work).
-int choose_pages_per_split(int64_t batch, int Hkv, int64_t pages) {
+// 6 pages per split (more splits only add merge work), 8 at head size 256, where a split's
+// fixed start and its partials weigh more against its pages than the CUs it leaves idle
+// (2 KV heads over 8K: 65 splits instead of 86, 3.392 -> 3.369 ms per config-4 step; 10 pages:
+// 3.404 ms).
+int choose_pages_per_split(int64_t batch, int Hkv, int64_t pages, int64_t head_size) {
   int64_t pps = g_pages_per_split;
   if (pps <= 0) {
     const int64_t heads = batch * Hkv;
@@ -719,7 +722,8 @@ int choose_pages_per_split(int64_t batch, int Hkv, int64_t pages) {
     const int64_t splits = heads < cus ? cus / heads : 1;
     pps = (pages + splits - 1) / splits;
     pps += pps & 1;
-    if (pps < 6) pps = 6;
+    const int64_t least = head_size >= 256 ? 8 : 6;
+    if (pps < least) pps = least;
   }
   while ((pages + pps - 1) / pps > SPLITS_MAX) ++pps;
   return (int)pps;
@@ -758,8 +762,12 @@ int launch_split_ring(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
 
 template <int D, int DH>
 int launch_split_dh(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
-  if (g_ring == 8) return launch_split_ring<D, DH, 8>(a, nblocks, s);
-  return launch_split_ring<D, DH, 4>(a, nblocks, s);  // measured: as fast, half the LDS
+  // long splits keep more pages in flight: eight-page ring from 32 pages per split (220K
+  // context, 108 pages per split: 7.33 -> 7.22 ms per config-5 step); shorter ones run as
+  // fast on four with half the LDS (config 4: 3.369 against 3.423 ms with eight)
+  if (g_ring == 8 || (g_ring == 0 && a.pages_per_split >= 32))
+    return launch_split_ring<D, DH, 8>(a, nblocks, s);
+  return launch_split_ring<D, DH, 4>(a, nblocks, s);
 }
 
 int g_d_split = 0;  // 0: automatic, 1, 2 or 3 (mixed) forced
@@ -823,7 +831,7 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
   a.G = (int)(num_heads / num_kv_heads);
   a.NRT = n_row_tiles(a.T, a.G);
   a.table_stride = (int)table_stride;
-  a.pages_per_split = choose_pages_per_split(batch, a.Hkv, table_stride);
+  a.pages_per_split = choose_pages_per_split(batch, a.Hkv, table_stride, head_size);
   a.S = (int)((table_stride + a.pages_per_split - 1) / a.pages_per_split);
   a.qk_scale = scale * kLog2e;
   const size_t parts = (size_t)batch * a.Hkv * a.NRT * SPLITS_MAX * 16;
