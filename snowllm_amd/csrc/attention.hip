@@ -774,8 +774,13 @@ int g_d_split = 0;  // 0: automatic, 1, 2 or 3 (mixed) forced
 
 template <int D>
 int launch_split(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
+  // automatic: two waves per tile up to MAX_TILES_DH tiles; five tiles one wave each (config
+  // 4: 3.362 -> 3.351 ms per forward pass against the mixed form; no swap barrier); six and
+  // seven the mixed form (config 5: 7.18 against 7.30 ms with one wave per tile)
   const int dh = g_d_split ? g_d_split
-                           : (a.NRT <= MAX_TILES_DH ? 2 : a.NRT < MAX_TILES ? 3 : 1);
+                           : (a.NRT <= MAX_TILES_DH ? 2
+                              : a.NRT == MAX_TILES_DH + 1 ? 1
+                              : a.NRT < MAX_TILES ? 3 : 1);
   if (dh == 2 && a.NRT <= MAX_TILES_DH) return launch_split_dh<D, 2>(a, nblocks, s);
   if (dh == 3 && a.NRT > MAX_TILES / 2 && a.NRT < MAX_TILES)
     return launch_split_dh<D, 3>(a, nblocks, s);
