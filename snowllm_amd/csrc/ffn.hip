@@ -1123,6 +1123,134 @@ __device__ __forceinline__ void moe_down_body(
   }
 }
 
+// Down item of the one-launch experts kernel with four tiles and all SD superblocks per wave
+// (four waves: sixteen tiles of 16 output columns): each wave's weights, SD times those of a
+// one-superblock item, go out before the wait, so that twice as many down weights stream
+// while the gate/up items run, and the slot's activations are loaded once per workgroup: wave
+// s < SD loads superblock s of the compact rows straight into LDS (device-scope loads) and
+// converts it there, one chunk at a time, with convert_words' arithmetic. The superblocks'
+// products are added in order, s = 0 first: each is an exact product by a power of two, so
+// the sum is the one the two-wave item forms (the same bits). The meta words are loaded one
+// dword per lane and gathered across the column's four lanes at multiply time.
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int DN_WIDE_TILES = 4;  // tiles per wave of a wide down item
+
+template <int FMT, int SD, class Wait>
+__device__ __forceinline__ void moe_down_wide_body(
+    int bx, int slot, const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta,
+    int64_t dn_qbytes, int64_t dn_mbytes, const uint8_t* __restrict__ sh_quant,
+    const uint8_t* __restrict__ sh_meta, const MoePlan* __restrict__ plan, int E,
+    const uint16_t* __restrict__ act, const float* __restrict__ weights,
+    const float* __restrict__ shared_w, float* __restrict__ pairs,
+    float* __restrict__ shared_out, int H, Wait&& wait) {
+  constexpr int DT = DN_WIDE_TILES, F = SD * QK;
+  constexpr int QV = QLayout<FMT>::kQuantVecs;
+  __shared__ u32x4 xs[SD][8][64];  // fp16 A operands of the slot's activation superblocks
+  __shared__ float xs_sum[SD][2][64];
+  __shared__ floatx4 xs_scale[SD][64];
+  __shared__ int32_t ep_dst[16];
+  __shared__ float ep_gate[16];
+  const int lane = threadIdx.x & 63, kq = lane >> 4, r = lane & 15;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (slot >= plan->n_slots) return;
+  const int e = __builtin_amdgcn_readfirstlane(plan->slot_expert[slot]);
+  const int n_rows = __builtin_amdgcn_readfirstlane(plan->slot_rows[slot]);
+  const uint8_t* q = e >= E ? sh_quant : quant + e * dn_qbytes;
+  const uint8_t* m = e >= E ? sh_meta : meta + e * dn_mbytes;
+  const int tiles = H / TILE_N, tile0 = (bx * 4 + wv) * DT;
+  const GemvStreams st = make_streams<FMT>(q, m, nullptr, tiles, SD, lane, 16);
+  u32x4 wq[SD][DT][QV];
+  uint32_t wm[SD][DT];
+  uint32_t wd[SD][DT];
+#pragma unroll
+  for (int s = 0; s < SD; ++s) {
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const uint32_t ts = (uint32_t)((tile0 + t) * SD + s);
+      constexpr uint32_t TB = QLayout<FMT>::kTsBytes;
+      if constexpr (FMT == FMT_Q5_K) {
+        wq[s][t][0] = bload4(st.quant, st.v_quant, ts * TB);
+        wq[s][t][1] = bload4(st.quant, st.v_quant, ts * TB + 1024);
+        const u32x2 h = bload2(st.quant, st.v_quant >> 1, ts * TB + 2048);
+        wq[s][t][2] = u32x4{h.x, h.y, 0u, 0u};
+      } else {
+#pragma unroll
+        for (int i = 0; i < QV; ++i) wq[s][t][i] = bload4(st.quant, st.v_quant, ts * TB + i * 1024);
+      }
+      wm[s][t] = bload1u(st.meta, st.v_meta + kq * 4, ts * 16 * 16);  // dword kq of column r
+    }
+    if constexpr (FMT == FMT_Q6_K) load_sb_d<DT>(wd[s], st, s, SD, tile0, 1);
+  }
+  // the epilogue's destinations and gates of the slot's compact rows
+  if (wv == 1 && lane < 16) {
+    const int32_t* ids = e >= E ? plan->row_of[slot] : plan->pair_of[slot];
+    const float* gsrc = e >= E ? shared_w : weights;
+    const int d = lane < n_rows ? ids[lane] : 0;
+    ep_dst[lane] = d;
+    ep_gate[lane] = lane < n_rows ? gsrc[d] : 0.f;
+  }
+  const bool poisoned = wait();  // ends with a workgroup barrier
+  if (wv < SD) {
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(act + (int64_t)slot * 16 * F), 0, 16 * F * 2, 0x00020000);
+    const uint32_t vo = r < n_rows ? (uint32_t)((r * F + kq * 8) * 2) : 0x80000000u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_void*)&xs[wv][j][0], 16, vo,
+                                               (uint32_t)((wv * QK + j * 32) * 2), 0,
+                                               16 /* sc1: device scope */);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    float sx0, sx1, sc;
+    convert_chunks([&](int j) { return xs[wv][j][lane]; },
+                   [&](int j, u32x4 v) { xs[wv][j][lane] = v; }, lane, sx0, sx1, sc);
+    xs_sum[wv][0][lane] = sx0;
+    xs_sum[wv][1][lane] = sx1;
+    floatx4 rs;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rs[i] = __shfl(sc, 4 * kq + i, 64);  // rows 4 kq + i
+    xs_scale[wv][lane] = rs;
+  }
+  __syncthreads();
+  const uint32_t Mv = decode_magic<FMT>();
+  floatx4 acc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < SD; ++s) {
+    SbOperands<FMT, DT> o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o.x[j] = xs[s][j][lane];
+    o.sx0 = xs_sum[s][0][lane];
+    o.sx1 = xs_sum[s][1][lane];
+    o.scale = xs_scale[s][lane];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int i = 0; i < QV; ++i) o.q[t][i] = wq[s][t][i];
+      o.m[t] = u32x4{(uint32_t)__shfl((int)wm[s][t], r, 64),
+                     (uint32_t)__shfl((int)wm[s][t], r + 16, 64),
+                     (uint32_t)__shfl((int)wm[s][t], r + 32, 64),
+                     (uint32_t)__shfl((int)wm[s][t], r + 48, 64)};
+      o.dq[t] = wd[s][t];
+    }
+    gemv_superblock<FMT, DT>(o, acc, kq, Mv);
+  }
+  float* out = e >= E ? shared_out : pairs;
+  const int rb = 4 * kq;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (rb + i >= n_rows) break;  // compact row
+    const int64_t d = ep_dst[rb + i];
+    const float gt = ep_gate[rb + i];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const int n = (tile0 + t) * TILE_N + (lane & 15);
+      const float y = bf16_to_f32(f32_to_bf16(acc[t][i]));  // expert outputs are bf16 tensors
+      out[d * H + n] = poisoned ? __builtin_nanf("") : y * gt;
+    }
+  }
+}
+
 template <int FMT, int NTILE, int WS, int GPB, bool ONE_SB>
 __global__ void __launch_bounds__(WS * GPB * 64) moe_down_kernel(
     const uint8_t* __restrict__ quant, const uint8_t* __restrict__ meta, int64_t dn_qbytes,
@@ -1168,7 +1296,7 @@ constexpr uint32_t MOE_WAIT_POLLS = 1u << 20;  // ~0.1 s: far beyond any gate/up
 // Three waves per SIMD when the down items take one superblock per wave (the gate/up items then
 // bound the registers at 168); two otherwise.
 template <int FMT, int DN_FMT, int GU_WS, int GU_PPB, int GU_SC, int GU_VW, int DN_NTILE,
-          int DN_WS, int DN_GPB, bool ONE_SB, int WAVES = (ONE_SB ? 3 : 2)>
+          int DN_WS, int DN_GPB, bool ONE_SB, int WAVES = (ONE_SB ? 3 : 2), bool DN_WIDE = false>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) moe_experts_kernel(
     // first the arguments of the plan read and the gate/up weight addresses: the first 56
     // bytes arrive preloaded in SGPRs
@@ -1227,9 +1355,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES,
     __syncthreads();
     return __builtin_amdgcn_readfirstlane(timed_out) != 0u;
   };
-  moe_down_body<DN_FMT, DN_NTILE, DN_WS, DN_GPB, true, ONE_SB>(
-      didx, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
-      plan, E, act, weights, shared_w, pairs, shared_out, H, F, wait);
+  if constexpr (DN_WIDE)
+    moe_down_wide_body<DN_FMT, 2>(didx, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes,
+                                  sh_dn_quant, sh_dn_meta, plan, E, act, weights, shared_w,
+                                  pairs, shared_out, H, wait);
+  else
+    moe_down_body<DN_FMT, DN_NTILE, DN_WS, DN_GPB, true, ONE_SB>(
+        didx, slot, dn_quant, dn_meta, dn_qbytes, dn_mbytes, sh_dn_quant, sh_dn_meta,
+        plan, E, act, weights, shared_w, pairs, shared_out, H, F, wait);
 }
 
 // out[r, n] = bf16(sum_k pairs[r*topk + k, n] + shared_out[r, n]) in a fixed order
@@ -1576,11 +1709,12 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
   const int dn_per_slot = (int)(H / 16 / MOE_DN_NTILE / MOE_DN_GPB);
   if (F / 16 / MOE_GU_PPB > MOE_MAX_ITEMS || dn_per_slot > MOE_MAX_ITEMS) return SV_ENOTSUP;
   // gu_per_slot: F / 16 pairs over the item shape's pairs per block (at most MOE_GU_PPB's)
-  auto launch = [&](auto kern, int gu_per_slot) {
-    const int64_t blocks = (int64_t)(gu_per_slot + dn_per_slot) * max_slots;
+  auto launch = [&](auto kern, int gu_per_slot, int dn_items = -1) {
+    const int dn = dn_items >= 0 ? dn_items : dn_per_slot;
+    const int64_t blocks = (int64_t)(gu_per_slot + dn) * max_slots;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, Sx(stream),
                        (const MoePlan*)plan, (const uint8_t*)gu_quant, (const uint8_t*)gu_meta,
-                       gu_q, gu_m, gu_per_slot, dn_per_slot, (int)max_slots, (int)E,
+                       gu_q, gu_m, gu_per_slot, dn, (int)max_slots, (int)E,
                        (const uint8_t*)sh_gu_quant, (const uint8_t*)sh_gu_meta,
                        (const uint8_t*)dn_quant, (const uint8_t*)dn_meta, dn_q, dn_m,
                        (const uint8_t*)sh_dn_quant, (const uint8_t*)sh_dn_meta, ws,
@@ -1595,6 +1729,17 @@ SV_API int snowverify_moe_gate_up_down(int fmt, const void* gu_quant, const void
     with_gu_shape(H / QK, max_slots, [&](auto ws_c, auto ppb_c, auto sc_c, auto vw_c) {
       constexpr int WS = decltype(ws_c)::value, PPB = decltype(ppb_c)::value,
                     SC = decltype(sc_c)::value, VW = decltype(vw_c)::value;
+      // launches of 128 or more slots (16 or more rows): wide down items, half as many,
+      // twice the down weights in flight while the gate/up items run (measured at 180 slots:
+      // 75.1 -> 70.9 us; at 53-83 slots one-superblock items are ahead by up to 2 us)
+      if constexpr (D != 6) {
+        if (max_slots >= 128 && F / QK == 2 && (H / TILE_N) % (4 * DN_WIDE_TILES) == 0) {
+          launch(moe_experts_kernel<G, D, WS, PPB, SC, VW, DN_WIDE_TILES, 1, 4, true,
+                                    q4 ? 3 : 2, true>,
+                 (int)(F / 16 / PPB), (int)(H / TILE_N / (4 * DN_WIDE_TILES)));
+          return;
+        }
+      }
       if (F / QK == MOE_DN_WS)
         launch(moe_experts_kernel<G, D, WS, PPB, SC, VW, MOE_DN_NTILE, MOE_DN_WS, MOE_DN_GPB,
                                   true, q4 ? 3 : 2>,

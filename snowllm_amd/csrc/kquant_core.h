@@ -69,14 +69,19 @@ struct XOperands {
   float scale;     // 2^e of this lane's row
 };
 
-// Conversion of one lane's 64 bf16 values: raw[j] holds k = 32 j + 8 kq .. + 7 of sub-block
-// j in natural order (two bf16 per dword, low half first).
-__device__ __forceinline__ void convert_words(const u32x4 (&raw)[8], int lane, XOperands& o) {
+// Conversion of one lane's 64 bf16 values: chunk j (get(j)) holds k = 32 j + 8 kq .. + 7 of
+// sub-block j in natural order (two bf16 per dword, low half first); put(j, v) receives the
+// fp16 A operand of sub-block j. get is called twice per chunk (the row maximum, then the
+// conversion), so a source in LDS needs no registers for the whole superblock.
+template <class Get, class Put>
+__device__ __forceinline__ void convert_chunks(Get&& get, Put&& put, int lane, float& sx0,
+                                               float& sx1, float& scale) {
   const int kq = lane >> 4;
   float mx = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+    const u32x4 rj = get(j);
+    const uint32_t w4[4] = {rj.x, rj.y, rj.z, rj.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       mx = fmaxf(mx, __builtin_fabsf(__uint_as_float(w4[i] << 16)));
@@ -91,10 +96,12 @@ __device__ __forceinline__ void convert_words(const u32x4 (&raw)[8], int lane, X
     if (E < -126) E = -126;
     e = E - 14;  // scaled maximum lands in [2^14, 2^15)
   }
-  float part[8];
+  sx0 = 0.0f;
+  sx1 = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+    const u32x4 rj = get(j);
+    const uint32_t w4[4] = {rj.x, rj.y, rj.z, rj.w};
     float f[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -109,19 +116,21 @@ __device__ __forceinline__ void convert_words(const u32x4 (&raw)[8], int lane, X
       h[t] = __builtin_bit_cast(uint16_t, hv);
       sum += (float)hv;
     }
-    part[j] = sum;
-    o.x[j] = u32x4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
-                   h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
+    put(j, u32x4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                 h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)});
+    // the full sub-block sum: the four kq lanes of the row added in a fixed order; lane kq
+    // keeps sub-blocks kq and 4 + kq
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    if (j == kq) sx0 = -sum;
+    if (j == 4 + kq) sx1 = -sum;
   }
-  // full sub-block sums: add the four kq lanes of the row (fixed order)
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    part[j] += __shfl_xor(part[j], 16, 64);
-    part[j] += __shfl_xor(part[j], 32, 64);
-  }
-  o.sx0 = -part[kq];
-  o.sx1 = -part[4 + kq];
-  o.scale = __builtin_ldexpf(1.0f, e);
+  scale = __builtin_ldexpf(1.0f, e);
+}
+
+__device__ __forceinline__ void convert_words(const u32x4 (&raw)[8], int lane, XOperands& o) {
+  convert_chunks([&](int j) { return raw[j]; }, [&](int j, u32x4 v) { o.x[j] = v; }, lane,
+                 o.sx0, o.sx1, o.scale);
 }
 
 __device__ __forceinline__ void convert_superblock(const uint16_t* __restrict__ src,
