@@ -277,29 +277,22 @@ int launch_gemv_mt(const void* quant, const void* meta, const void* ws, void* c,
   const int tiles = N / TILE_N;
   const int row_tiles = (M + TILE_M - 1) / TILE_M;
   const size_t tb = xprep_tile_bytes(S);
-  // two column tiles per workgroup halve the row tiles' operand loads (every workgroup reads
-  // all of them) where 160 or more workgroups remain (measured on MI355X at 36 rows:
-  // 5120 x 2048 10.7 -> 7.7 us, 6144 x 4096 18.3 -> 11.8 us; at 128 or 256 tiles one tile per
-  // workgroup stays faster, 2048 x 4096 8.0 against 10.2 us). The same bits either way.
-  const int nt = tiles >= 320 ? 2 : 1;
+  // One row tile per workgroup (blockIdx.y), two column tiles per workgroup where that still
+  // leaves 192 or more workgroups. Measured on MI355X (prepared operands, the weights from
+  // HBM): decoding a weight superblock once for several row tiles saves less than the
+  // workgroups it takes away. N = 2048, K = 4096 at 36 / 54 / 128 rows: 9.3 / 11.2 / 11.6 us
+  // with three or four row tiles per workgroup against 6.0 / 6.1 / 8.6 us; N = 5120, K = 2048
+  // at 128 rows 20.8 against 11.1 us; N = 14336, K = 4096 at 72 rows 42.8 against 30.4 us.
+  // One column tile only wins at N = 2048 and 18 rows (4.9 against 6.0 us). The same bits
+  // either way (every row gets the 16-row launch's arithmetic).
+  const int nt = (int64_t)(tiles / 2) * row_tiles >= 192 ? 2 : 1;
   auto go = [&](auto kern, int mt, int ntile) {
     hipLaunchKernelGGL(kern, dim3((tiles + ntile - 1) / ntile, (row_tiles + mt - 1) / mt),
                        dim3(NW * 64), 0, s, (const u32x4*)quant, (const u32x4*)meta, ws, c, M,
                        N, S, c_bf16, tb, ldc);
   };
-  if constexpr (FMT == FMT_Q6_K) {
-    go(kquant_gemv_mt<FMT, NW, 2>, 2, 1);  // Q6_K's three tiles of operands spill the registers
-  } else {
-    if (nt == 2) {
-      if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2, 2>, 2, 2);
-      else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3, 2>, 3, 2);
-      else go(kquant_gemv_mt<FMT, NW, 4, 2>, 4, 2);
-    } else {
-      if (row_tiles == 2) go(kquant_gemv_mt<FMT, NW, 2>, 2, 1);
-      else if (row_tiles == 3) go(kquant_gemv_mt<FMT, NW, 3>, 3, 1);
-      else go(kquant_gemv_mt<FMT, NW, 4>, 4, 1);
-    }
-  }
+  if (nt == 2) go(kquant_gemv_mt<FMT, NW, 1, 2>, 1, 2);
+  else go(kquant_gemv_mt<FMT, NW, 1>, 1, 1);
   SV_CHECK_LAUNCH();
   return SV_OK;
 }
@@ -605,8 +598,8 @@ SV_API int snowverify_gemm_kquant_a_prepared_ld(int fmt, const uint8_t* quant,
   const size_t esz = c_is_bf16 ? 2 : 4;
   const int ld = (int)ldc;
   if (mt > 1 && g_gemv_variant == 0) {
-    // wider than one row tile: every weight tile loaded once for up to four row tiles (the
-    // waves split the superblocks as the automatic 16-row launch does: the same bits)
+    // wider than one row tile: one launch over every row tile (the waves split the
+    // superblocks as the automatic 16-row launch does: the same bits)
     return by_format(fmt, [&](auto F) {
       constexpr int FM = decltype(F)::value;
       return S >= 8 ? launch_gemv_mt<FM, 8>(quant, meta, ws, c, (int)M, (int)N, (int)S, c_is_bf16, ld, s)
