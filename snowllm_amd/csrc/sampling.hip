@@ -1391,8 +1391,9 @@ SV_API int snowllm_draft_reject(const float* p, const int64_t* ids, const int64_
 // Workgroup (row, w) takes slice w (FA_SLICE logits, FA_E per thread, coalesced) of a row.
 //   1. slice maxima of x / T;
 //   2. numerators e = exp(x / T - M) with the row maximum M, the slice's fixed-point sum and
-//      the draft token's numerator; the request's last workgroup to finish (a counter)
-//      forms every row's Z and the accepted prefix;
+//      the draft token's numerator, and in one more workgroup per draft row the proposal's
+//      q(d_j); the request's last workgroup to finish (a counter) forms every row's Z and
+//      the accepted prefix, one thread per draft row;
 //   3. one workgroup per 4 * FA_NT-logit sub-chunk of the row where the prefix stops forms
 //      the residual max(p - q, 0) (p at the bonus row) and its fixed-point sums; the
 //      request's last one finds the sub-chunk holding floor(u R) (a wave's prefix scan over
@@ -1418,6 +1419,7 @@ static_assert(FA_SLICE * FA_P_MAX == VOCAB_MAX, "slices cover the vocabulary lim
 __device__ uint32_t g_fa_maxkey[FA_ROWS][FA_P_MAX];
 __device__ uint64_t g_fa_sum[FA_ROWS][FA_P_MAX];
 __device__ uint32_t g_fa_edraft[FA_ROWS];       // a draft token's numerator (f32 bits)
+__device__ uint32_t g_fa_qt[FA_ROWS];           // q(d_j) of a draft row (f32 bits)
 __device__ int32_t g_fa_first[FA_ROWS];         // per request: where the prefix stops
 __device__ uint64_t g_fa_rsub[FA_ROWS][FA_P_MAX][FA_SUBCHUNKS];
 __device__ uint64_t g_fa_psub[FA_ROWS][FA_P_MAX][FA_SUBCHUNKS];
@@ -1540,87 +1542,72 @@ __global__ void __launch_bounds__(FA_NT) fa_sum_kernel(const float* __restrict__
   __shared__ uint64_t red[FA_NT / WAVE];
   __shared__ float red_f[4];
   const int P = a.P, width = a.width, length = width - 1, V = a.V;
-  const int w = blockIdx.x, row = blockIdx.y;  // grid (P, rows)
+  const int w = blockIdx.x, row = blockIdx.y;  // grid (P + 1, rows)
   const int r = row / width, j = row % width;
   const int t = threadIdx.x, lo = w * FA_SLICE;
-  float v[FA_E];
-  fa_load_slice(a.logits + (int64_t)row * V, lo, V, row_temperature(a.temperature, row), v);
-  const float M = fa_row_max(row, P);
   const int64_t dtok = j < length ? a.drafts[(int64_t)r * length + j] : -1;
-  uint64_t sum = 0;
+  if (w < P) {
+    float v[FA_E];
+    fa_load_slice(a.logits + (int64_t)row * V, lo, V, row_temperature(a.temperature, row), v);
+    const float M = fa_row_max(row, P);
+    uint64_t sum = 0;
 #pragma unroll
-  for (int k = 0; k < FA_E; ++k) {
-    const int i = lo + k * FA_NT + t;
-    const float e = canon_exp(__fsub_rn(v[k], M));
-    if (i < V) {
-      sum += canon_fix(e);
-      if (i == dtok) dev_store(&g_fa_edraft[row], __float_as_uint(e));
+    for (int k = 0; k < FA_E; ++k) {
+      const int i = lo + k * FA_NT + t;
+      const float e = canon_exp(__fsub_rn(v[k], M));
+      if (i < V) {
+        sum += canon_fix(e);
+        if (i == dtok) dev_store(&g_fa_edraft[row], __float_as_uint(e));
+      }
     }
-  }
-  sum = block_sum_u64<FA_NT>(sum, red);
-  if (t == 0) dev_store(&g_fa_sum[row][w], sum);
-  if (!fa_last_arrival2(g_fa_cnt1[0][row], P, w == 0, &g_fa_cnt[0][r], width, j == 0)) return;
-  // the request's last workgroup: u_j q(d_j) >= p(d_j) stops the accepted prefix. Every
-  // draft row's sums and numerator are read at once, one per thread.
-  __shared__ uint64_t s_rs[64][FA_P_MAX];
-  __shared__ float s_ed[64];
-  for (int i = t; i < length * P; i += FA_NT)
-    s_rs[i / P][i % P] = dev_load(&g_fa_sum[r * width + i / P][i % P]);
-  for (int jj = t; jj < length; jj += FA_NT)
-    s_ed[jj] = __uint_as_float(dev_load(&g_fa_edraft[r * width + jj]));
-  __syncthreads();
-  const int slot = a.slots[r];
-  const bool valid = a.valid[r] != 0;
-  // q(d_j) of every draft row at once: thread j looks its token up (the direct slot of an
-  // identity list, or a search of a short list); longer non-identity lists are searched by
-  // the whole block below
-  __shared__ float s_qt[64];
-  __shared__ int s_search;
-  if (t == 0) s_search = 0;
-  __syncthreads();
-  if (t < length) {
-    const int64_t token = a.drafts[(int64_t)r * length + t];
+    sum = block_sum_u64<FA_NT>(sum, red);
+    if (t == 0) dev_store(&g_fa_sum[row][w], sum);
+  } else if (j < length) {
+    // workgroup P of a draft row: q(d_j) (1 when the proposal is not valid), while the
+    // slices stream: the direct slot of an identity list, else a search of the list (by one
+    // thread when it is short, by the block otherwise). Every value here is uniform.
     float qt = 1.0f;
-    if (valid) {
-      const int64_t qrow = ((int64_t)slot * length + t) * a.q_width;
+    if (a.valid[r] != 0) {
+      const int64_t qrow = ((int64_t)a.slots[r] * length + j) * a.q_width;
       const float* qr = a.q + qrow;
       const int64_t* cr = a.cand + qrow;
-      if (token >= 0 && token < a.q_width && cr[token] == token) {
-        qt = qr[token];
-      } else if (a.q_width <= Q_STAGE) {
-        qt = row_prob_thread(qr, cr, a.q_width, token);
-      } else {
-        qt = -1.0f;
-        atomicOr(&s_search, 1);
-      }
+      if (dtok >= 0 && dtok < a.q_width && cr[dtok] == dtok)
+        qt = qr[dtok];
+      else if (a.q_width <= Q_STAGE)
+        qt = row_prob_thread(qr, cr, a.q_width, dtok);
+      else
+        qt = row_prob_block(qr, cr, a.q_width, dtok, red_f);
     }
-    s_qt[t] = qt;
+    if (t == 0) dev_store(&g_fa_qt[row], __float_as_uint(qt));
+  }
+  if (!fa_last_arrival2(g_fa_cnt1[0][row], P + 1, w == 0, &g_fa_cnt[0][r], width, j == 0))
+    return;
+  // the request's last workgroup: u_j q(d_j) >= p(d_j) stops the accepted prefix. Every
+  // draft row's sums, numerator and q(d_j) are read at once, one per thread.
+  __shared__ uint64_t s_rs[64][FA_P_MAX];
+  __shared__ float s_ed[64], s_qt[64];
+  for (int i = t; i < length * P; i += FA_NT)
+    s_rs[i / P][i % P] = dev_load(&g_fa_sum[r * width + i / P][i % P]);
+  for (int jj = t; jj < length; jj += FA_NT) {
+    s_ed[jj] = __uint_as_float(dev_load(&g_fa_edraft[r * width + jj]));
+    s_qt[jj] = __uint_as_float(dev_load(&g_fa_qt[r * width + jj]));
   }
   __syncthreads();
-  if (s_search)
-    for (int jj = 0; jj < length; ++jj) {
-      if (s_qt[jj] >= 0.0f) continue;  // (uniform: every thread reads the same value)
-      const int64_t qrow = ((int64_t)slot * length + jj) * a.q_width;
-      const float qt = row_prob_block(a.q + qrow, a.cand + qrow, a.q_width,
-                                      a.drafts[(int64_t)r * length + jj], red_f);
-      if (t == 0) s_qt[jj] = qt;
-      __syncthreads();
-    }
-  if (t == 0) {
-    int first = length;
-    for (int jj = 0; jj < length; ++jj) {
-      const int64_t token = a.drafts[(int64_t)r * length + jj];
+  if (t < WAVE) {
+    // lane jj decides draft row jj (the same sums in the same order as a walk over the rows);
+    // the prefix stops at the first row that rejects
+    bool stop = false;
+    if (t < length) {
+      const int64_t token = a.drafts[(int64_t)r * length + t];
       uint64_t z = 0;
-      for (int i = 0; i < P; ++i) z += s_rs[jj][i];
+      for (int i = 0; i < P; ++i) z += s_rs[t][i];
       const float Zf = canon_unfix(z);
       float pt = 0.0f;
-      if (token >= 0 && token < V) pt = Zf > 0.0f ? canon_div(s_ed[jj], Zf) : 0.0f;
-      if (__fmul_rn(a.uniform[(int64_t)r * width + jj], s_qt[jj]) >= pt) {
-        first = jj;
-        break;
-      }
+      if (token >= 0 && token < V) pt = Zf > 0.0f ? canon_div(s_ed[t], Zf) : 0.0f;
+      stop = __fmul_rn(a.uniform[(int64_t)r * width + t], s_qt[t]) >= pt;
     }
-    g_fa_first[r] = first;
+    const uint64_t b = __ballot(stop);
+    if (t == 0) g_fa_first[r] = b ? (int)__builtin_ctzll(b) : length;
   }
 }
 
@@ -1903,7 +1890,8 @@ SV_API int snowverify_accept_reject(const float* logits, const float* temperatur
   hipLaunchKernelGGL(fa_max_kernel, rows, dim3(FA_NT), 0, S(stream), logits, temperature,
                      (int)vocab, (int)width, P, a);
   SV_CHECK_LAUNCH();
-  hipLaunchKernelGGL(fa_sum_kernel, rows, dim3(FA_NT), 0, S(stream), logits, temperature,
+  hipLaunchKernelGGL(fa_sum_kernel, dim3((unsigned)(P + 1), (unsigned)(b * width)), dim3(FA_NT), 0,
+                     S(stream), logits, temperature,
                      (int)vocab, (int)width, P, a);
   SV_CHECK_LAUNCH();
   hipLaunchKernelGGL(fa_pick_kernel, reqs, dim3(FA_NT), 0, S(stream), logits, temperature,
