@@ -453,7 +453,12 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
     const int64_t block_bytes = page_bytes * a.Hkv;
     const uint8_t* kbase = (const uint8_t*)a.k_pool + h * page_bytes;
     const uint8_t* vbase = (const uint8_t*)a.v_pool + h * page_bytes;
-    // pages past the split reload page p0 into a free slot (keeps the load count uniform)
+    // pages past the split reload page p0 into a free slot (finite data under the masked
+    // second page of an odd last chunk; before the loop the wait for the query row below
+    // counts on every wave's RING - 2 page loads behind it). In the loop a chunk that lies
+    // wholly past the split is not loaded, and a step waits for every load in flight when
+    // fewer than RING - 4 pages are queued behind its own (so the last steps queue nothing
+    // that the workgroup's end would have to wait for).
     auto issue = [&](int pg, int slot_idx) {
       const int pgc = pg < p1 ? pg : p0;
       int64_t blk = pgc - p0 < RING - 2 ? pre[0] : trow[pgc];
@@ -493,14 +498,19 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
       init_state(st);
       int slot = 0;  // first ring slot of the current chunk (even)
       for (int pg = p0; pg < p1; pg += 2) {
-        wait_vmcnt<(RING - 4) * CPW>();  // this wave's loads of pages pg, pg + 1 have landed
+        // this wave's loads of pages pg, pg + 1 have landed (RING - 4 pages queued behind them
+        // while both chunks behind this one are loaded) ...
+        if (RING == 4 || pg + RING - 4 < p1) wait_vmcnt<(RING - 4) * CPW>();
+        else wait_vmcnt<0>();
         block_barrier();                 // ... and every wave's; the previous chunk is free
         if (q_from_lds && pg == p0)
 #pragma unroll
           for (int ds = 0; ds < DS; ++ds) qb[ds] = __builtin_bit_cast(bf16x8, qsh[qpi][ds][lane]);
         const int prev = slot == 0 ? RING - 2 : slot - 2;
-        issue(pg + RING - 2, prev);
-        issue(pg + RING - 1, prev + 1);
+        if (pg + RING - 2 < p1) {  // (uniform) the chunk is one a later step multiplies
+          issue(pg + RING - 2, prev);
+          issue(pg + RING - 1, prev + 1);
+        }
         attend_chunk<D, DHW, MIXED && DHW == 2, MIXED && DHW == 1>(
             st, ring + slot * G::BYTES, pg + 1 < p1, qb, pg, L, ctx,
             anc, a.qk_scale, kq, col, dhalf, xch[MIXED ? w : 0]);
