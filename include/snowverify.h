@@ -287,6 +287,10 @@ int snowverify_attention_d_split(int dh);
 /* Extension, no counterpart in the reference (a tuning knob): pages in the attention split
  * kernel's LDS ring, 4 or 8; 0 = automatic. Returns the previous value. */
 int snowverify_attention_ring(int pages);
+/* Extension, no counterpart in the reference (a tuning knob): row groups of the attention split
+ * kernel's one-wave-per-tile form, 1 or 2 (two workgroups per context split, each with half of
+ * the row tiles, on one XCD); 0 = automatic. Returns the previous value. */
+int snowverify_attention_row_groups(int groups);
 
 /* ---- geometry-driven operator entry points (reference signatures) ---------------------
  * Shapes from the active geometry (see below); weights in the reference's _Weight descriptor

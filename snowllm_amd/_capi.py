@@ -108,6 +108,7 @@ _SIGS = [
     ("snowverify_attention_pages_per_split", c_int, [c_int]),
     ("snowverify_attention_d_split", c_int, [c_int]),
     ("snowverify_attention_ring", c_int, [c_int]),
+    ("snowverify_attention_row_groups", c_int, [c_int]),
     # geometry-driven operator entry points (reference signatures)
     ("snowllm_qkv_proj_scratch_bytes", c_int64, [c_int64]),
     ("snowllm_attn_out_scale_oproj_scratch_bytes", c_int64, [c_int64]),

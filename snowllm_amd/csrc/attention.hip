@@ -59,6 +59,7 @@ struct AttnArgs {
   float* part_o;            // [batch, Hkv, NRT, S, 16, D]
   float* part_ml;           // [batch, Hkv, NRT, S, 16, 2]
   int T, Hq, Hkv, G, NRT, S, pages_per_split, table_stride;
+  int RG;                   // row groups: workgroups that share one (request, head, split)
   float qk_scale;           // softmax scale * log2(e)
   // QK-norm + RoPE + the block's K/V write done here (proj != null): q head hq of block row m
   // at proj + m * proj_stride + hq * q_head_stride, k / v head h at k_off / v_off + h * D;
@@ -300,7 +301,7 @@ template <int D, int CPW, int RING, int DH>
 __global__ void __launch_bounds__(DH == 2 ? MAX_TILES_DH * 2 * 64 : MAX_TILES * 64)
 attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict__ h_lens,
                   int h_S, int h_Hkv, int h_pps, int h_tstride, int h_T, int h_G, int h_NRT,
-                  AttnArgs a) {
+                  int h_RG, AttnArgs a) {
   a.table = h_table, a.lens = h_lens, a.S = h_S, a.Hkv = h_Hkv, a.pages_per_split = h_pps;
   a.table_stride = h_tstride, a.T = h_T, a.G = h_G, a.NRT = h_NRT;
   using G = SlotGeo<D>;
@@ -315,8 +316,10 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
   constexpr bool QSHARE =
       QSH_PAIRS > 0 && RING * G::BYTES + QSH_BYTES + sizeof(xch) <= 150 * 1024;
   __shared__ u32x4 qsh[QSHARE ? QSH_PAIRS : 1][DS][64];
-  const int NW = DH == 3 ? MAX_TILES : h_NRT * DH;  // waves (the launch's; blockDim would be a
-                                                   // kernel-argument load)
+  // waves (the launch's; blockDim would be a kernel-argument load); with two row groups each
+  // workgroup takes half of the row tiles, rounded up
+  const int NW = DH == 3 ? MAX_TILES : (DH == 1 ? (h_RG == 2 ? (h_NRT + 1) >> 1 : h_NRT)
+                                                : h_NRT * DH);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int w, dhalf;  // row tile, output-column part
@@ -332,8 +335,24 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
     dhalf = pair ? (wv - nx) & 1 : 0;
   }
   const int kq = lane >> 4, col = lane & 15;
-  // grid (S, Hkv, batch): the workgroups of a head's splits stay consecutive, and no division
-  const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // grid (S, Hkv, batch): the workgroups of a head's splits stay consecutive, and no division.
+  // Two row groups (one wave per tile): x = 16 * (split / 8) + 8 * group + split % 8, so the
+  // two workgroups of a split are 8 apart in dispatch order and land on the same XCD (the
+  // XCDs take workgroups in turn), where the second one's page loads are served by that
+  // XCD's L2; x past the last split returns at once.
+  int split = blockIdx.x;
+  if constexpr (DH == 1) {
+    if (h_RG == 2) {
+      const int x = blockIdx.x;
+      split = ((x >> 4) << 3) | (x & 7);
+      w += (x & 8) ? NW : 0;
+      if (split >= h_S) return;
+    }
+  }
+  const int h = blockIdx.y, b = blockIdx.z;
+  // a wave past the last row tile (the second group of an odd tile count) loads its share of
+  // the pages and takes part in every barrier, but multiplies and writes nothing
+  const bool idle = DH == 1 && w >= h_NRT;
 
   // this lane's query row (column of S^T / O^T)
   const int r = w * 16 + col;
@@ -511,15 +530,16 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
           issue(pg + RING - 2, prev);
           issue(pg + RING - 1, prev + 1);
         }
-        attend_chunk<D, DHW, MIXED && DHW == 2, MIXED && DHW == 1>(
-            st, ring + slot * G::BYTES, pg + 1 < p1, qb, pg, L, ctx,
-            anc, a.qk_scale, kq, col, dhalf, xch[MIXED ? w : 0]);
+        if (!idle)
+          attend_chunk<D, DHW, MIXED && DHW == 2, MIXED && DHW == 1>(
+              st, ring + slot * G::BYTES, pg + 1 < p1, qb, pg, L, ctx,
+              anc, a.qk_scale, kq, col, dhalf, xch[MIXED ? w : 0]);
         slot = slot == RING - 2 ? 0 : slot + 2;
       }
       wait_vmcnt<0>();  // no load may still target LDS when the workgroup retires
-      write_partials(st);
+      if (!idle) write_partials(st);
     });
-  } else {
+  } else if (!idle) {
     with_state([&](auto& st) {
       init_state(st);
       write_partials(st);
@@ -749,15 +769,17 @@ int g_ring = 0;  // LDS ring pages: 0 automatic, 4 or 8
 template <int D, int DH, int RING>
 int launch_split_ring(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   constexpr int CH = SlotGeo<D>::CHUNKS;
-  const int nw = DH == 3 ? MAX_TILES : a.NRT * DH;  // mixed: eight waves
+  const int rg = DH == 1 ? a.RG : 1;
+  const int nw = DH == 3 ? MAX_TILES : (rg == 2 ? (a.NRT + 1) / 2 : a.NRT * DH);  // mixed: 8
   int cpw = 1;
   while (cpw * nw < CH) cpw *= 2;
   if (RING == 8 && cpw == 16) return launch_split_ring<D, DH, 4>(a, nblocks, s);  // vmcnt range
-  const dim3 grid((unsigned)a.S, (unsigned)a.Hkv, (unsigned)(nblocks / ((int64_t)a.S * a.Hkv))),
+  const unsigned gx = rg == 2 ? (unsigned)(16 * ((a.S + 7) / 8)) : (unsigned)a.S;
+  const dim3 grid(gx, (unsigned)a.Hkv, (unsigned)(nblocks / ((int64_t)a.S * a.Hkv))),
       block((unsigned)(64 * nw));
 #define SV_SPLIT(CPW_, RING_)                                                                   \
   hipLaunchKernelGGL((attn_split_kernel<D, CPW_, RING_, DH>), grid, block, 0, s, a.table, a.lens, \
-                     a.S, a.Hkv, a.pages_per_split, a.table_stride, a.T, a.G, a.NRT, a)
+                     a.S, a.Hkv, a.pages_per_split, a.table_stride, a.T, a.G, a.NRT, rg, a)
   switch (cpw) {
     case 1: SV_SPLIT(1, RING); break;
     case 2: SV_SPLIT(2, RING); break;
@@ -782,15 +804,31 @@ int launch_split_dh(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
 
 int g_d_split = 0;  // 0: automatic, 1, 2 or 3 (mixed) forced
 
+// automatic: two waves per tile up to MAX_TILES_DH tiles; five tiles one wave each (config
+// 4: 3.362 -> 3.351 ms per forward pass against the mixed form; no swap barrier); six and
+// seven the mixed form (config 5: 7.18 against 7.30 ms with one wave per tile)
+int choose_dh(int NRT) {
+  return g_d_split ? g_d_split
+                   : (NRT <= MAX_TILES_DH ? 2 : NRT == MAX_TILES_DH + 1 ? 1 : NRT < MAX_TILES ? 3 : 1);
+}
+
+int g_row_groups = 0;  // 0: automatic, 1 or 2 forced
+
+// Row groups of the one-wave-per-tile form: two workgroups per split, each with half of the
+// row tiles, when that keeps the splits nearly as long -- a short context, whose pages per
+// split sit at the lower bound, so that one group per split leaves CUs idle while each CU
+// runs two tiles on one of its SIMDs. Returns 1 or 2.
+int choose_row_groups(int dh, int NRT, int64_t batch, int Hkv, int64_t pages, int64_t head_size) {
+  if (dh != 1 || NRT < 3) return 1;
+  if (g_row_groups) return g_row_groups;
+  const int64_t one = choose_pages_per_split(batch, Hkv, pages, head_size);
+  const int64_t two = choose_pages_per_split(2 * batch, Hkv, pages, head_size);
+  return two <= one + 2 ? 2 : 1;
+}
+
 template <int D>
 int launch_split(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
-  // automatic: two waves per tile up to MAX_TILES_DH tiles; five tiles one wave each (config
-  // 4: 3.362 -> 3.351 ms per forward pass against the mixed form; no swap barrier); six and
-  // seven the mixed form (config 5: 7.18 against 7.30 ms with one wave per tile)
-  const int dh = g_d_split ? g_d_split
-                           : (a.NRT <= MAX_TILES_DH ? 2
-                              : a.NRT == MAX_TILES_DH + 1 ? 1
-                              : a.NRT < MAX_TILES ? 3 : 1);
+  const int dh = choose_dh(a.NRT);
   if (dh == 2 && a.NRT <= MAX_TILES_DH) return launch_split_dh<D, 2>(a, nblocks, s);
   if (dh == 3 && a.NRT > MAX_TILES / 2 && a.NRT < MAX_TILES)
     return launch_split_dh<D, 3>(a, nblocks, s);
@@ -846,7 +884,15 @@ int paged_attention_impl(AttnArgs a, const void* q, const void* k_pool, const vo
   a.G = (int)(num_heads / num_kv_heads);
   a.NRT = n_row_tiles(a.T, a.G);
   a.table_stride = (int)table_stride;
-  a.pages_per_split = choose_pages_per_split(batch, a.Hkv, table_stride, head_size);
+  {
+    const int dh = choose_dh(a.NRT);
+    // the launch's own test of the form (launch_split): one wave per tile unless two or mixed
+    const int dh_run = (dh == 2 && a.NRT <= MAX_TILES_DH) ? 2
+                       : (dh == 3 && a.NRT > MAX_TILES / 2 && a.NRT < MAX_TILES) ? 3 : 1;
+    a.RG = choose_row_groups(dh_run, a.NRT, batch, a.Hkv, table_stride, head_size);
+  }
+  // a row group counts as a head for the split sizing: RG * batch * Hkv * S <= CUs
+  a.pages_per_split = choose_pages_per_split(batch * a.RG, a.Hkv, table_stride, head_size);
   a.S = (int)((table_stride + a.pages_per_split - 1) / a.pages_per_split);
   a.qk_scale = scale * kLog2e;
   const size_t parts = (size_t)batch * a.Hkv * a.NRT * SPLITS_MAX * 16;
@@ -995,6 +1041,15 @@ SV_API int snowverify_attention_pages_per_split(int pages) {
 SV_API int snowverify_attention_d_split(int dh) {
   const int prev = g_d_split;
   g_d_split = (dh == 1 || dh == 2 || dh == 3) ? dh : 0;
+  return prev;
+}
+
+// Tuning knob (extension, no reference counterpart): row groups of the attention's split
+// kernel in its one-wave-per-tile form (1, or 2: two workgroups per split, each with half of the
+// row tiles; 0 restores the automatic choice). Returns the previous value.
+SV_API int snowverify_attention_row_groups(int groups) {
+  const int prev = g_row_groups;
+  g_row_groups = (groups == 1 || groups == 2) ? groups : 0;
   return prev;
 }
 

@@ -246,8 +246,9 @@ def test_merge_writes_projection_operands(lengths, T, Hq, Hkv, tree):
     ([700 + 7, 333 + 7], 7, 16, 1, 128, False),   # seven tiles of 128-wide heads
 ])
 def test_mixed_tile_waves_equal_one_wave_per_tile(lengths, T, Hq, Hkv, D, tree):
-    """Eight waves with one or two waves per row tile (the pairs split the S products) give the
-    bits of one wave per tile."""
+    """Eight waves with one or two waves per row tile (the pairs split the S products), and one
+    wave per tile in two row groups (two workgroups per split, each with half of the tiles),
+    give the bits of one wave per tile in one workgroup, at the same split length."""
     from snowllm_amd import ops
     from snowllm_amd._capi import lib
     print(f"mixed tile waves lengths={lengths} T={T} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
@@ -273,9 +274,12 @@ def test_mixed_tile_waves_equal_one_wave_per_tile(lengths, T, Hq, Hkv, D, tree):
                           dtype=torch.uint8, device="cuda")
     outs = []
     prev = lib.snowverify_attention_d_split(1)
+    prev_rg = lib.snowverify_attention_row_groups(1)
+    prev_pps = lib.snowverify_attention_pages_per_split(10)
     try:
-        for dh in (1, 3):
+        for dh, rg in ((1, 1), (1, 2), (3, 0)):
             lib.snowverify_attention_d_split(dh)
+            lib.snowverify_attention_row_groups(rg)
             out = torch.empty_like(q)
             ops.paged_attention_explicit(q, kp, vp, out, table.cuda(), lens, D ** -0.5, scratch,
                                          tree=tr)
@@ -283,4 +287,7 @@ def test_mixed_tile_waves_equal_one_wave_per_tile(lengths, T, Hq, Hkv, D, tree):
             outs.append(out)
     finally:
         lib.snowverify_attention_d_split(prev)
+        lib.snowverify_attention_row_groups(prev_rg)
+        lib.snowverify_attention_pages_per_split(prev_pps)
     assert torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[0], outs[2])
