@@ -44,6 +44,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int SPLITS_MAX = 512;
 constexpr int MAX_TILES = 8;     // row tiles per workgroup: T * G <= 128
 constexpr int MAX_TILES_DH = 4;  // up to 4 tiles, each tile's output columns split over 2 waves
+constexpr int RG_WAVES = 8;      // waves of a row-group workgroup (at most MAX_TILES / 2 tiles)
 // The fused QK-norm form rotates at most 128 dims of a head (half <= 64): wider rotations of a
 // 256-wide head would not fit the kernel's registers, and the entry point refuses them.
 constexpr int FUSED_MAX_HS = 2;
@@ -317,9 +318,9 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
       QSH_PAIRS > 0 && RING * G::BYTES + QSH_BYTES + sizeof(xch) <= 150 * 1024;
   __shared__ u32x4 qsh[QSHARE ? QSH_PAIRS : 1][DS][64];
   // waves (the launch's; blockDim would be a kernel-argument load); with two row groups each
-  // workgroup takes half of the row tiles, rounded up
-  const int NW = DH == 3 ? MAX_TILES : (DH == 1 ? (h_RG == 2 ? (h_NRT + 1) >> 1 : h_NRT)
-                                                : h_NRT * DH);
+  // workgroup takes half of the row tiles, rounded up, on four waves (a page's sixteen 1 KiB
+  // loads then split evenly, with no repeated chunk)
+  const int NW = DH == 3 ? MAX_TILES : (DH == 1 ? (h_RG == 2 ? RG_WAVES : h_NRT) : h_NRT * DH);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int w, dhalf;  // row tile, output-column part
@@ -341,22 +342,25 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
   // XCDs take workgroups in turn), where the second one's page loads are served by that
   // XCD's L2; x past the last split returns at once.
   int split = blockIdx.x;
+  bool idle = false;  // wave-uniform
   if constexpr (DH == 1) {
     if (h_RG == 2) {
       const int x = blockIdx.x;
+      const int half = (h_NRT + 1) >> 1;  // tiles of the first group
       split = ((x >> 4) << 3) | (x & 7);
-      w += (x & 8) ? NW : 0;
+      idle = w >= half;
+      w += (x & 8) ? half : 0;
       if (split >= h_S) return;
     }
   }
   const int h = blockIdx.y, b = blockIdx.z;
-  // a wave past the last row tile (the second group of an odd tile count) loads its share of
-  // the pages and takes part in every barrier, but multiplies and writes nothing
-  const bool idle = DH == 1 && w >= h_NRT;
+  // a wave past its group's row tiles loads its share of the pages and takes part in every
+  // barrier, but multiplies and writes nothing
+  idle = idle || (DH == 1 && w >= h_NRT);
 
   // this lane's query row (column of S^T / O^T)
   const int r = w * 16 + col;
-  const bool row_live = r < a.T * a.G;
+  const bool row_live = !idle && r < a.T * a.G;
   const int t = row_live ? r / a.G : 0;
   const int g = row_live ? r % a.G : 0;
   const int hq = h * a.G + g;
@@ -770,7 +774,7 @@ template <int D, int DH, int RING>
 int launch_split_ring(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   constexpr int CH = SlotGeo<D>::CHUNKS;
   const int rg = DH == 1 ? a.RG : 1;
-  const int nw = DH == 3 ? MAX_TILES : (rg == 2 ? (a.NRT + 1) / 2 : a.NRT * DH);  // mixed: 8
+  const int nw = DH == 3 ? MAX_TILES : (rg == 2 ? RG_WAVES : a.NRT * DH);  // mixed: 8
   int cpw = 1;
   while (cpw * nw < CH) cpw *= 2;
   if (RING == 8 && cpw == 16) return launch_split_ring<D, DH, 4>(a, nblocks, s);  // vmcnt range
