@@ -44,7 +44,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int SPLITS_MAX = 512;
 constexpr int MAX_TILES = 8;     // row tiles per workgroup: T * G <= 128
 constexpr int MAX_TILES_DH = 4;  // up to 4 tiles, each tile's output columns split over 2 waves
-constexpr int RG_WAVES = 8;      // waves of a row-group workgroup (at most MAX_TILES / 2 tiles)
+// Waves of a split workgroup: eight for one wave per tile (with or without row groups) and for
+// the mixed form; two per tile, rounded up to a power of two, for two waves per tile. A page's
+// sixteen 1 KiB loads then split evenly over the waves, with no repeated chunk, and waves past
+// the workgroup's row tiles only load pages (more waves issuing the loads: config 4 attention
+// 21.2 -> 20.0 us per launch with four waves per row group, 19.5 with eight).
+__host__ __device__ inline int split_waves(int dh, int nrt) {
+  if (dh != 2) return MAX_TILES;
+  return nrt <= 1 ? 2 : nrt <= 2 ? 4 : 8;
+}
 // The fused QK-norm form rotates at most 128 dims of a head (half <= 64): wider rotations of a
 // 256-wide head would not fit the kernel's registers, and the entry point refuses them.
 constexpr int FUSED_MAX_HS = 2;
@@ -317,10 +325,8 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
   constexpr bool QSHARE =
       QSH_PAIRS > 0 && RING * G::BYTES + QSH_BYTES + sizeof(xch) <= 150 * 1024;
   __shared__ u32x4 qsh[QSHARE ? QSH_PAIRS : 1][DS][64];
-  // waves (the launch's; blockDim would be a kernel-argument load); with two row groups each
-  // workgroup takes half of the row tiles, rounded up, on four waves (a page's sixteen 1 KiB
-  // loads then split evenly, with no repeated chunk)
-  const int NW = DH == 3 ? MAX_TILES : (DH == 1 ? (h_RG == 2 ? RG_WAVES : h_NRT) : h_NRT * DH);
+  // waves (the launch's; blockDim would be a kernel-argument load)
+  const int NW = split_waves(DH, h_NRT);
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int w, dhalf;  // row tile, output-column part
@@ -356,7 +362,7 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
   const int h = blockIdx.y, b = blockIdx.z;
   // a wave past its group's row tiles loads its share of the pages and takes part in every
   // barrier, but multiplies and writes nothing
-  idle = idle || (DH == 1 && w >= h_NRT);
+  idle = idle || w >= h_NRT;
 
   // this lane's query row (column of S^T / O^T)
   const int r = w * 16 + col;
@@ -774,7 +780,7 @@ template <int D, int DH, int RING>
 int launch_split_ring(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
   constexpr int CH = SlotGeo<D>::CHUNKS;
   const int rg = DH == 1 ? a.RG : 1;
-  const int nw = DH == 3 ? MAX_TILES : (rg == 2 ? RG_WAVES : a.NRT * DH);  // mixed: 8
+  const int nw = split_waves(DH, a.NRT);
   int cpw = 1;
   while (cpw * nw < CH) cpw *= 2;
   if (RING == 8 && cpw == 16) return launch_split_ring<D, DH, 4>(a, nblocks, s);  // vmcnt range
