@@ -404,13 +404,16 @@ attn_split_kernel(const int32_t* __restrict__ h_table, const int32_t* __restrict
     constexpr int DT = (int)(sizeof(st.o) / sizeof(st.o[0]));
     // O^T lane holds row col, d = dt*16 + 4*kq + i
     const int64_t pidx = ((((int64_t)b * a.Hkv + h) * a.NRT + w) * a.S + split);
+    // (a padding row's partials are left unwritten: the merges never combine them into an
+    // output)
     float* po = a.part_o + pidx * 16 * D + (int64_t)col * D;
+    if (row_live)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) *(floatx4*)(po + (dhalf * DT + dt) * 16 + 4 * kq) = st.o[dt];
+      for (int dt = 0; dt < DT; ++dt) *(floatx4*)(po + (dhalf * DT + dt) * 16 + 4 * kq) = st.o[dt];
     // row sums: add the four lanes of each row in a fixed order
     float l = st.l + __shfl_xor(st.l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    if (kq == 0 && dhalf == 0) {
+    if (kq == 0 && dhalf == 0 && row_live) {
       float* pml = a.part_ml + (pidx * 16 + col) * 2;
       pml[0] = st.m;
       pml[1] = l;
