@@ -817,12 +817,12 @@ int launch_split_dh(const AttnArgs& a, int64_t nblocks, hipStream_t s) {
 
 int g_d_split = 0;  // 0: automatic, 1, 2 or 3 (mixed) forced
 
-// automatic: two waves per tile up to MAX_TILES_DH tiles; five tiles one wave each (config
-// 4: 3.362 -> 3.351 ms per forward pass against the mixed form; no swap barrier); six and
-// seven the mixed form (config 5: 7.18 against 7.30 ms with one wave per tile)
+// automatic: two waves per tile up to MAX_TILES_DH tiles, one wave per tile above (no swap
+// barrier). Config 4's five tiles: 3.362 -> 3.351 ms per forward pass against the mixed form;
+// config 5's six: 7.21 -> 6.99 ms per step once the one-wave form ran on eight waves (on six,
+// with repeated page chunks, the mixed form had been ahead, 7.18 against 7.30 ms).
 int choose_dh(int NRT) {
-  return g_d_split ? g_d_split
-                   : (NRT <= MAX_TILES_DH ? 2 : NRT == MAX_TILES_DH + 1 ? 1 : NRT < MAX_TILES ? 3 : 1);
+  return g_d_split ? g_d_split : (NRT <= MAX_TILES_DH ? 2 : 1);
 }
 
 int g_row_groups = 0;  // 0: automatic, 1 or 2 forced
